@@ -1,0 +1,252 @@
+#!/usr/bin/env python3
+"""Throughput of the quantized MoE expert-FFN path on one MI355X.
+
+Headline workload (`value`): 512-token prefill of one MoE layer -- d_model 2048, 128 experts, top-8, expert
+intermediate 768, Q4_K gate/up, Q6_K down, router logits biased so tokens per expert follow Zipf(1.1)
+(log p_zipf + Gumbel noise added to the fp32 router GEMV).  One step = router GEMV -> softmax/top-k ->
+bucketing -> Q8_K activations -> grouped int8-MFMA gate/up GEMM (SwiGLU) -> Q8_K hidden -> grouped down GEMM
+-> combine, with every input already in HBM.  Each step uses a fresh (activations, routing) pair and one of
+several independent weight copies, so the 256 MB MALL does not serve the weights.  Steps are replayed from a
+HIP graph (captured once, checked against an eager run first).
+
+Secondary (`decode` object): 1-token decode of the same layer shape in Q4_K/Q4_K: router GEMV -> route ->
+gate/up GEMV -> fused down + combine, cycling 4 layer copies (1.36 GB) and fresh tokens.
+
+`roofline` reports the dominant kernel of the headline step against HBM bandwidth (8 TB/s): algorithmic bytes
+per launch / its average launch duration, measured on its own stream with HIP events over graph replays of
+that kernel.  `cpu_baseline` is the CPU oracle (this repository's restatement of the reference's CPU expert
+path) run on a bounded sample of the same workload on this host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from hyper_amd import moe  # noqa: E402
+from hyper_amd.formats import GType, WORKLOADS, activations, q8_row_bytes, random_layer, row_bytes, vec_dot_type, zipf_logit_bias  # noqa: E402
+
+METRIC = "MoE-layer µs/token decode (HBM GB/s) + prefill tokens/s (MFMA util), 1 GPU"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def graph_time(fn_list, replays: int, stream) -> float:
+    """Capture fn_list (callables enqueueing work) into one HIP graph, replay `replays` times, return ms per replay."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for fn in fn_list:
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(replays):
+        g.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    del g
+    return a.elapsed_time(b) / replays
+
+
+def make_layers(w, copies, dev, seed0):
+    return [random_layer(w.tg, w.td, w.E, w.ff, w.d, seed=seed0 + c, device=dev, d_range=w.d_range) for c in range(copies)]
+
+
+def prefill_bench(args, dev, stream):
+    w = WORKLOADS["q4k_q6k_prefill512"]
+    T, k, E, d, ff = w.rows, w.k, w.E, w.d, w.ff
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234 + 1)
+    layers = make_layers(w, args.copies, dev, 100)
+    devs = [moe.MoeDev(L, torch.arange(E, dtype=torch.int32, device=dev)) for L in layers]
+    W_rs = [torch.randn(E, d, generator=g, device=dev) * 0.02 for _ in range(args.copies)]
+    n_in = args.inputs
+    xs = [activations(T, d, g, dev) for _ in range(n_in)]
+    biases = [zipf_logit_bias(T, E, w.zipf, g, dev) for _ in range(n_in)]
+    runners = [moe.MoeLayerRunner(devs[c], W_rs[c], k, T) for c in range(args.copies)]
+    torch.cuda.synchronize()
+
+    # eager step vs graph replay of the same step (what is timed must compute what eager computes)
+    with torch.cuda.stream(stream):
+        ref = runners[0].prefill(xs[0], biases[0]).clone()
+        torch.cuda.synchronize()
+        gg = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gg, stream=stream):
+            runners[0].prefill(xs[0], biases[0])
+        gg.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(runners[0].out[:T], ref):
+            raise RuntimeError("graph replay of the prefill step differs from the eager step")
+        del gg
+
+    # routing statistics per input (the bytes a step must read)
+    act = []
+    for i in range(n_in):
+        r = runners[i % args.copies]
+        r.prefill(xs[i], biases[i])
+        torch.cuda.synchronize()
+        act.append(int(r.order_n[1].item()))
+    steps = [(i % args.copies, i % n_in) for i in range(args.graph_steps)]
+    fns = [lambda c=c, i=i: runners[c].prefill(xs[i], biases[i]) for c, i in steps]
+
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, args.warmup)):
+            for f in fns:
+                f()
+        torch.cuda.synchronize()
+        reps = max(1, args.steps // len(fns))
+        ms_graph = graph_time(fns, reps, stream)
+    ms_step = ms_graph / len(fns)
+    tok_s = T / (ms_step / 1e3)
+
+    # per-kernel launch durations: each grouped GEMM alone, graph-replayed over the copies/inputs
+    # (inputs of the last prefill of each (copy, input) pair are still in the runners' workspaces)
+    gu_fns, dn_fns = [], []
+    for c, i in steps[: 2 * args.copies]:
+        r = runners[c]
+        gu_fns.append(lambda r=r: moe.moe_gemm_gate_up(r.dev, r.xq, k, r.order, r.order_n, r.egrp, min(E, T * k), r.h))
+        dn_fns.append(lambda r=r: moe.moe_gemm_down(r.dev, r.hq, r.order, r.order_n, r.egrp, min(E, T * k), r.wts, r.y))
+    with torch.cuda.stream(stream):
+        for c in range(args.copies):
+            runners[c].prefill(xs[c % n_in], biases[c % n_in])
+        torch.cuda.synchronize()
+        ms_gu = graph_time(gu_fns, max(1, args.kernel_reps), stream) / len(gu_fns)
+        ms_dn = graph_time(dn_fns, max(1, args.kernel_reps), stream) / len(dn_fns)
+        act_k = [int(runners[c].order_n[1].item()) for c in range(args.copies)]
+    n_act = float(np.mean(act_k))
+    P = T * k
+    L0 = layers[0]
+    gu_bytes = n_act * 2 * L0.gate_bytes + T * q8_row_bytes(vec_dot_type(w.tg), d) + P * ff * 4
+    dn_bytes = n_act * L0.down_bytes + P * q8_row_bytes(vec_dot_type(w.td), ff) + P * d * 4 + P * 4
+    kern = {"gemm_gate_up": {"ms": ms_gu, "bytes": gu_bytes}, "gemm_down": {"ms": ms_dn, "bytes": dn_bytes}}
+    dom = max(kern, key=lambda k_: kern[k_]["ms"])
+    ach = kern[dom]["bytes"] / (kern[dom]["ms"] / 1e3) / 1e9
+    step_bytes = float(np.mean(act)) * L0.expert_bytes() + E * d * 4 + T * d * 4 * 2
+    ops = 2.0 * P * 3 * ff * d
+    res = {
+        "tok_s": tok_s, "ms_step": ms_step, "active_experts_mean": float(np.mean(act)),
+        "step_bytes": step_bytes, "step_hbm_gbs": step_bytes / (ms_step / 1e3) / 1e9,
+        "step_int8_tops": ops / (ms_step / 1e3) / 1e12,
+        "kernels": {k_: {"us": v["ms"] * 1e3, "alg_bytes": v["bytes"], "gbs": v["bytes"] / (v["ms"] / 1e3) / 1e9} for k_, v in kern.items()},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": ach / HBM_PEAK_GBS, "traffic": None},
+    }
+    return res, layers[0], W_rs[0], xs[0], biases[0], runners[0]
+
+
+def decode_bench(args, dev, stream):
+    w = WORKLOADS["q4k_decode"]
+    k, E, d, ff = w.k, w.E, w.d, w.ff
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    layers = make_layers(w, args.decode_copies, dev, 200)
+    devs = [moe.MoeDev(L, torch.arange(E, dtype=torch.int32, device=dev)) for L in layers]
+    W_rs = [torch.randn(E, d, generator=g, device=dev) * 0.02 for _ in layers]
+    xs = activations(64, d, g, dev)
+    runners = [moe.MoeLayerRunner(devs[c], W_rs[c], k, 1) for c in range(len(layers))]
+    fns = [lambda c=c, i=i: runners[c].decode(xs[i:i + 1]) for i, c in zip(range(64), [j % len(layers) for j in range(64)])]
+    with torch.cuda.stream(stream):
+        for f in fns:
+            f()
+        torch.cuda.synchronize()
+        ms = graph_time(fns, max(1, args.decode_reps), stream) / len(fns)
+        gu = [lambda r=r, i=i: moe.moe_gate_up(r.dev, xs[i:i + 1], d, r.ids, k, r.h, 1) for i, r in enumerate(runners)]
+        dn = [lambda r=r: moe.moe_down_reduce(r.dev, r.h, r.ids, r.wts, k, None, None, r.out, 1) for r in runners]
+        ms_gu = graph_time(gu * 8, max(1, args.decode_reps), stream) / (8 * len(gu))
+        ms_dn = graph_time(dn * 8, max(1, args.decode_reps), stream) / (8 * len(dn))
+    L0 = layers[0]
+    tok_bytes = k * L0.expert_bytes() + E * d * 4 + 2 * d * 4
+    us = ms * 1e3
+    return {"workload": "q4k_decode", "us_per_token": us, "hbm_gbs": tok_bytes / (us / 1e6) / 1e9,
+            "hbm_frac": tok_bytes / (us / 1e6) / 1e9 / HBM_PEAK_GBS, "alg_bytes_per_token": tok_bytes,
+            "kernels": {"gate_up_gemv": {"us": ms_gu * 1e3, "gbs": k * 2 * L0.gate_bytes / (ms_gu / 1e3) / 1e9},
+                        "down_reduce": {"us": ms_dn * 1e3, "gbs": k * L0.down_bytes / (ms_dn / 1e3) / 1e9}}}
+
+
+def cpu_baseline(layer, W_r, x, bias, budget_s: float):
+    """The CPU oracle on the first S tokens of the headline step (S grows until about budget_s of work)."""
+    import oracle as orc
+    OL = orc.Layer.from_expert_layer(layer)
+    xh, bh, Wh = x.cpu().numpy(), bias.cpu().numpy(), W_r.cpu().numpy()
+    w = WORKLOADS["q4k_q6k_prefill512"]
+    threads = orc.default_threads()
+    S, spent = 4, 0.0
+    while True:
+        logits = orc.gemv_f32(Wh, xh[:S]) + bh[:S]
+        ids, wts, _ = orc.route(logits.astype(np.float32), w.E, w.k)
+        t0 = time.perf_counter()
+        orc.moe_layer(OL, xh[:S], ids, wts, threads=threads)
+        spent = time.perf_counter() - t0
+        if spent * 2.2 > budget_s or S >= w.rows:
+            break
+        S = min(w.rows, S * 2)
+    return {"value": S / spent, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"first {S} tokens of one 512-token prefill step (same weights, routing and activations), "
+                      f"{spent:.2f} s, oracle/moe_oracle.c with {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64, help="timed prefill steps")
+    ap.add_argument("--warmup", type=int, default=2, help="untimed passes over the step sequence")
+    ap.add_argument("--copies", type=int, default=2, help="independent weight copies cycled by the prefill steps")
+    ap.add_argument("--inputs", type=int, default=4, help="independent (activations, routing) sets")
+    ap.add_argument("--graph-steps", type=int, default=8, help="prefill steps captured per graph")
+    ap.add_argument("--kernel-reps", type=int, default=8)
+    ap.add_argument("--decode-copies", type=int, default=4)
+    ap.add_argument("--decode-reps", type=int, default=8)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-oracle work for cpu_baseline (0: skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    log("prefill: building layers and inputs")
+    pre, L0, W0, x0, b0, _ = prefill_bench(args, dev, stream)
+    log(f"prefill: {pre['tok_s']:.0f} tok/s, {pre['ms_step'] * 1e3:.1f} us/step")
+    dec = None
+    if not args.no_decode:
+        log("decode: building layers")
+        dec = decode_bench(args, dev, stream)
+        log(f"decode: {dec['us_per_token']:.2f} us/token")
+    cpu = None
+    if args.cpu_budget > 0:
+        log("cpu baseline: oracle on a sample of the prefill step")
+        cpu = cpu_baseline(L0, W0, x0, b0, args.cpu_budget)
+    w = WORKLOADS["q4k_q6k_prefill512"]
+    line = {
+        "metric": METRIC, "value": round(pre["tok_s"], 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": max(1, args.steps // args.graph_steps) * args.graph_steps, "warmup": args.warmup,
+        "ms_per_step": round(pre["ms_step"], 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": w.name, "d_model": w.d, "experts": w.E, "top_k": w.k, "ff": w.ff, "rows": w.rows,
+                   "gate_up": w.tg.name, "down": w.td.name, "routing": "zipf(1.1)+gumbel logit bias",
+                   "weight_copies": args.copies, "active_experts_mean": pre["active_experts_mean"]},
+        "roofline": {k_: (round(v, 4) if isinstance(v, float) else v) for k_, v in pre["roofline"].items()},
+        "step": {"alg_bytes": pre["step_bytes"], "hbm_gbs": round(pre["step_hbm_gbs"], 1),
+                 "hbm_frac": round(pre["step_hbm_gbs"] / HBM_PEAK_GBS, 4), "int8_tops": round(pre["step_int8_tops"], 2),
+                 "int8_mfma_frac": round(pre["step_int8_tops"] / INT8_PEAK_TOPS, 4),
+                 "kernels": pre["kernels"]},
+        "decode": dec,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

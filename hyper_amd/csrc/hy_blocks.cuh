@@ -1,0 +1,212 @@
+// Per-type block decoding for the integer dot products.
+//
+// Decode GEMV mapping: a 256-value item of a weight row (one super-block, or eight IQ4_NL blocks) is
+// handled by 8 lanes; lane L loads a 16-byte slice of the quant bytes (coalesced: the group reads the
+// item's quant bytes contiguously) and returns exact integer partial sums (sumi, summ) against the
+// matching Q8 activation bytes; the 8 partials are summed exactly in integers.  Layouts follow the
+// reference's deq8<T> (src/kernels4.cu:421-714).
+#pragma once
+#include "hy_common.cuh"
+
+namespace hy {
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int) a, (int) b, c, false); }
+__device__ __forceinline__ uint32_t byte_of(uint4 v, int i) {   // byte i (0..15) of a 16-byte vector
+    const uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
+    return (w >> (8 * (i & 3))) & 0xff;
+}
+// 6-bit scale and min of sub-block j from the 12 scale bytes held in words s0..s2 (src/kernels4.cu:423-426)
+__device__ __forceinline__ void scale_min_k4(uint32_t s0, uint32_t s1, uint32_t s2, int j, int &sc, int &mn) {
+    const uint4 v = make_uint4(s0, s1, s2, 0);
+    if (j < 4) { sc = byte_of(v, j) & 63; mn = byte_of(v, j + 4) & 63; }
+    else { sc = (byte_of(v, j + 4) & 0xF) | ((byte_of(v, j - 4) >> 6) << 4); mn = (byte_of(v, j + 4) >> 4) | ((byte_of(v, j) >> 6) << 4); }
+}
+// four packed nibble indices (bytes 0..15) -> the IQ4_NL codebook values as packed int8
+__device__ __forceinline__ uint32_t kv4(uint32_t idx) {
+    const uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;
+    // (bytes: -127 -104 -83 -65 | -49 -35 -22 -10 | 1 13 25 38 | 53 69 89 113)
+    const uint32_t sel = idx & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
+    const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
+    return (hi & m) | (lo & ~m);
+}
+// IQ2 signs: 8 sign bits -> two words whose bytes are 0xFF where negated; value = (g ^ M) + (M & 1)
+__device__ __forceinline__ uint32_t spread4(uint32_t b4) { return (b4 * 0x00204081u) & 0x01010101u; }
+__device__ __forceinline__ uint32_t apply_sign(uint32_t g, uint32_t b4) {
+    const uint32_t one = spread4(b4);
+    return (g ^ (one * 0xFFu)) + one;
+}
+// Q6_K: q6 bytes (0..63) -> q6 - 32 as int8
+__device__ __forceinline__ uint32_t q6_signed(uint32_t q) {
+    const uint32_t v = q ^ 0x20202020u, s = v & 0x20202020u;
+    return v | (s << 1) | (s << 2);
+}
+
+// ---------------------------------------------------------------- decode-GEMV items (8 lanes)
+template <int T> struct Item;
+
+// Q4_K (144 B: d, dmin, scales[12], qs[128]).  Lane L: qs bytes 16 L .. 16 L + 15 = values 16 (L & 1) ..
+// of sub-blocks 2 (L >> 1) (low nibbles) and 2 (L >> 1) + 1 (high nibbles).
+template <> struct Item<Q4_K> {
+    uint4 hd, qs;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) { hd = load16_a4(b); qs = load16_a4(b + 16 + 16 * L); }
+    __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
+        const int c = L >> 1, hh = L & 1;
+        int sc0, m0, sc1, m1;
+        scale_min_k4(hd.y, hd.z, hd.w, 2 * c, sc0, m0);
+        scale_min_k4(hd.y, hd.z, hd.w, 2 * c + 1, sc1, m1);
+        const uint32_t *ya = (const uint32_t *) (y + 4 + 64 * c + 16 * hh), *yb = (const uint32_t *) (y + 4 + 64 * c + 32 + 16 * hh);
+        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+        int sa = 0, sb = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { sa = sdot4(q[i] & 0x0F0F0F0Fu, ya[i], sa); sb = sdot4((q[i] >> 4) & 0x0F0F0F0Fu, yb[i], sb); }
+        const int16_t *bs = (const int16_t *) (y + 260);
+        si = sc0 * sa + sc1 * sb;
+        sm = m0 * bs[4 * c + hh] + m1 * bs[4 * c + 2 + hh];
+    }
+    __device__ __forceinline__ float tval(int si, int sm) const {
+        return __builtin_fmaf(h2f(hd.x & 0xffff), (float) si, -(h2f(hd.x >> 16) * (float) sm));
+    }
+};
+// Q5_K (176 B: d, dmin, scales[12], qh[32], qs[128]): as Q4_K, bit j of qh[l] is bit 4 of sub-block j's value l.
+template <> struct Item<Q5_K> {
+    uint4 hd, qh, qs;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+        hd = load16_a4(b); qh = load16_a4(b + 16 + 16 * (L & 1)); qs = load16_a4(b + 48 + 16 * L);
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
+        const int c = L >> 1, hh = L & 1;
+        int sc0, m0, sc1, m1;
+        scale_min_k4(hd.y, hd.z, hd.w, 2 * c, sc0, m0);
+        scale_min_k4(hd.y, hd.z, hd.w, 2 * c + 1, sc1, m1);
+        const uint32_t *ya = (const uint32_t *) (y + 4 + 64 * c + 16 * hh), *yb = (const uint32_t *) (y + 4 + 64 * c + 32 + 16 * hh);
+        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w}, h[4] = {qh.x, qh.y, qh.z, qh.w};
+        int sa = 0, sb = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = (q[i] & 0x0F0F0F0Fu) | (((h[i] >> (2 * c)) & 0x01010101u) << 4);
+            const uint32_t hi = ((q[i] >> 4) & 0x0F0F0F0Fu) | (((h[i] >> (2 * c + 1)) & 0x01010101u) << 4);
+            sa = sdot4(lo, ya[i], sa); sb = sdot4(hi, yb[i], sb);
+        }
+        const int16_t *bs = (const int16_t *) (y + 260);
+        si = sc0 * sa + sc1 * sb;
+        sm = m0 * bs[4 * c + hh] + m1 * bs[4 * c + 2 + hh];
+    }
+    __device__ __forceinline__ float tval(int si, int sm) const {
+        return __builtin_fmaf(h2f(hd.x & 0xffff), (float) si, -(h2f(hd.x >> 16) * (float) sm));
+    }
+};
+// Q6_K (210 B: ql[128], qh[64], scales int8[16], d).  Lane L: ql bytes 64 hf + 32 qt0 + 16 hl .. (+16) with
+// hf = L >> 2, qt0 = (L >> 1) & 1, hl = L & 1: low nibbles are the 16-group g = 8 hf + 2 qt0 + hl, high nibbles
+// group g + 4; bits 2 qt of qh[32 hf + l] are bits 4-5.  (q6 - 32) . y = q6 . y - 32 bsum_g.
+template <> struct Item<Q6_K> {
+    uint4 ql, qh;
+    int sc_lo, sc_hi;
+    uint16_t d;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+        const int hf = L >> 2, qt0 = (L >> 1) & 1, hl = L & 1, g = 8 * hf + 2 * qt0 + hl;
+        ql = load16_a2(b + 64 * hf + 32 * qt0 + 16 * hl);
+        qh = load16_a2(b + 128 + 32 * hf + 16 * hl);
+        sc_lo = (int8_t) b[192 + g]; sc_hi = (int8_t) b[192 + g + 4];
+        d = ld_u16(b + 208);
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
+        const int hf = L >> 2, qt0 = (L >> 1) & 1, hl = L & 1, g = 8 * hf + 2 * qt0 + hl;
+        const uint32_t *ya = (const uint32_t *) (y + 4 + 16 * g), *yb = (const uint32_t *) (y + 4 + 16 * (g + 4));
+        const uint32_t q[4] = {ql.x, ql.y, ql.z, ql.w}, h[4] = {qh.x, qh.y, qh.z, qh.w};
+        int sa = 0, sb = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = (q[i] & 0x0F0F0F0Fu) | (((h[i] >> (2 * qt0)) & 0x03030303u) << 4);
+            const uint32_t hi = ((q[i] >> 4) & 0x0F0F0F0Fu) | (((h[i] >> (2 * qt0 + 4)) & 0x03030303u) << 4);
+            sa = sdot4(lo, ya[i], sa); sb = sdot4(hi, yb[i], sb);
+        }
+        const int16_t *bs = (const int16_t *) (y + 260);
+        si = sc_lo * (sa - 32 * bs[g]) + sc_hi * (sb - 32 * bs[g + 4]);
+        sm = 0;
+    }
+    __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
+};
+// IQ4_XS (136 B: d, scales_h u16, scales_l[4], qs[128]).  Lane L = 32-group L: qs bytes 16 L .. (+16), low
+// nibbles values 0..15, high nibbles 16..31; scale ls - 32 (src/iq3s_dot.h:136-166).
+template <> struct Item<IQ4_XS> {
+    uint4 qs;
+    uint32_t dsh;   // d | scales_h << 16
+    uint32_t sl;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+        qs = load16_a4(b + 8 + 16 * L);
+        dsh = *(const uint32_t *) b;
+        sl = b[4 + (L >> 1)];
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
+        const uint32_t *ya = (const uint32_t *) (y + 4 + 32 * L);
+        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { s = sdot4(kv4(q[i] & 0x0F0F0F0Fu), ya[i], s); s = sdot4(kv4((q[i] >> 4) & 0x0F0F0F0Fu), ya[4 + i], s); }
+        const int ls = ((sl >> (4 * (L & 1))) & 0xF) | ((((dsh >> 16) >> (2 * L)) & 3) << 4);
+        si = (ls - 32) * s;
+        sm = 0;
+    }
+    __device__ __forceinline__ float tval(int si, int) const { return h2f(dsh & 0xffff) * (float) si; }
+};
+// IQ2_XS (74 B: d, qs u16[32], scales[8]).  Lane L = 32-group L: 8-groups l = 0..3 use qs[4 L + l]: grid row
+// q & 511, signs ksigns[q >> 9]; scale nibble l >> 1 of scales[L]; value d (2 sc + 1) / 8 grid sign.
+// `grid`: the codebook rows expanded to 8 bytes each (LDS).
+template <> struct Item<IQ2_XS> {
+    uint16_t q[4];
+    uint16_t d;
+    uint8_t sc;
+    const uint2 *grid;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+#pragma unroll
+        for (int l = 0; l < 4; ++l) q[l] = ld_u16(b + 2 + 2 * (4 * L + l));
+        d = ld_u16(b);
+        sc = b[66 + L];
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
+        const uint32_t *ya = (const uint32_t *) (y + 4 + 32 * L);
+        int s[4];
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint2 g = grid[q[l] & 511];
+            const uint32_t sg = ksign(q[l] >> 9);
+            s[l] = sdot4(apply_sign(g.y, sg >> 4), ya[2 * l + 1], sdot4(apply_sign(g.x, sg & 15), ya[2 * l], 0));
+        }
+        si = (2 * (sc & 15) + 1) * (s[0] + s[1]) + (2 * (sc >> 4) + 1) * (s[2] + s[3]);
+        sm = 0;
+    }
+    __device__ __forceinline__ float tval(int si, int) const { return (h2f(d) * 0.125f) * (float) si; }
+};
+// IQ4_NL (18 B: d, qs[16]) against Q8_0: lane L takes the item's block L (32 values) whole; `y` is that
+// block's Q8_0 data in the padded layout (d at 0, qs at 4).
+template <> struct Item<IQ4_NL> {
+    uint4 qs;
+    uint16_t d;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) { qs = load16_a2(b + 18 * L + 2); d = ld_u16(b + 18 * L); }
+    __device__ __forceinline__ void ints(const uint8_t *y, int, int &si, int &sm) const {
+        const uint32_t *ya = (const uint32_t *) (y + 4);
+        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { s = sdot4(kv4(q[i] & 0x0F0F0F0Fu), ya[i], s); s = sdot4(kv4((q[i] >> 4) & 0x0F0F0F0Fu), ya[4 + i], s); }
+        si = s; sm = 0;
+    }
+    __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
+};
+
+// expand the IQ2_XS codebook (base-3 codes) into 512 x 8 bytes of LDS
+__device__ __forceinline__ void expand_iq2xs_grid(uint2 *grid) {
+    for (int i = threadIdx.x; i < 512; i += blockDim.x) {
+        uint32_t c = c_iq2xs_code[i], lo = 0, hi = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t dgt = c % 3; c /= 3;
+            const uint32_t v = dgt == 0 ? 8u : dgt == 1 ? 25u : 43u;
+            if (j < 4) lo |= v << (8 * j); else hi |= v << (8 * (j - 4));
+        }
+        grid[i] = make_uint2(lo, hi);
+    }
+}
+
+} // namespace hy

@@ -1,0 +1,213 @@
+// The C ABI (include/hymoe.h): argument validation, error state, and the host-side expert upload.
+#include "hy_internal.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace hy {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+int check_launch(const char *what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) { set_error("%s: %s", what, hipGetErrorString(e)); return HY_EHIP; }
+    return HY_OK;
+}
+
+static bool dot_type(int t) { return t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ4_NL; }
+static bool gemm_type(int t) { return t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS; }
+
+// the expert layer descriptor is usable: types, sizes, pointers, row sizes that the kernels assume
+static int check_dev(const hy_moe_dev *m, const char *what, bool need_gate, bool need_down) {
+    if (!m) { set_error("%s: null hy_moe_dev", what); return HY_EINVAL; }
+    if (!m->slot || m->n_expert <= 0) { set_error("%s: slot table missing", what); return HY_EINVAL; }
+    if (m->ff <= 0 || m->n <= 0) { set_error("%s: ff %d, n %d", what, m->ff, m->n); return HY_EBAD_SHAPE; }
+    if (need_gate) {
+        if (!dot_type(m->tg)) { set_error("%s: unsupported gate/up type %d", what, m->tg); return HY_EUNSUPPORTED_TYPE; }
+        if (!m->gate || !m->up) { set_error("%s: null gate/up", what); return HY_EINVAL; }
+        if (m->n % 256) { set_error("%s: n = %d is not a multiple of 256", what, m->n); return HY_EBAD_SHAPE; }
+        const size_t rb = (size_t) (m->n / block_elems(m->tg)) * block_bytes(m->tg);
+        if (m->gate_bytes != rb * (size_t) m->ff) { set_error("%s: gate_bytes %zu != ff * row bytes %zu", what, m->gate_bytes, rb * m->ff); return HY_EBAD_SHAPE; }
+    }
+    if (need_down) {
+        if (!dot_type(m->td)) { set_error("%s: unsupported down type %d", what, m->td); return HY_EUNSUPPORTED_TYPE; }
+        if (!m->down) { set_error("%s: null down", what); return HY_EINVAL; }
+        if (m->ff % 256) { set_error("%s: ff = %d is not a multiple of 256", what, m->ff); return HY_EBAD_SHAPE; }
+        const size_t rb = (size_t) (m->ff / block_elems(m->td)) * block_bytes(m->td);
+        if (m->down_bytes != rb * (size_t) m->n) { set_error("%s: down_bytes %zu != n * row bytes %zu", what, m->down_bytes, rb * m->n); return HY_EBAD_SHAPE; }
+    }
+    return HY_OK;
+}
+static bool aligned16(const void *p) { return ((uintptr_t) p & 15) == 0; }
+
+} // namespace hy
+
+using namespace hy;
+
+extern "C" {
+
+const char *hy_last_error(void) { return g_err; }
+int hy_abi_version(void) { return 1; }
+
+size_t hy_block_bytes(int type) { return (size_t) block_bytes(type); }
+int hy_block_elems(int type) { return block_elems(type); }
+int hy_vec_dot_type(int type) { return dot_type(type) ? vec_dot_type(type) : -1; }
+size_t hy_q8_row_bytes(int vtype, int n) {
+    if (vtype == Q8_K && n % 256 == 0) return (size_t) (n / 256) * Q8K_BYTES;
+    if (vtype == Q8_0 && n % 32 == 0) return (size_t) (n / 32) * Q8_0_BYTES;
+    return 0;
+}
+
+int hy_upload_experts(const hy_expert_tensors *t, const int32_t *slot_host, int32_t ff, int32_t n, float clamp, hy_moe_dev *out) {
+    if (!t || !slot_host || !out || !t->gate || !t->up || !t->down || t->E <= 0) { set_error("hy_upload_experts: null argument"); return HY_EINVAL; }
+    int nl = 0;
+    for (int e = 0; e < t->E; ++e) nl = std::max(nl, slot_host[e] + 1);
+    const size_t n_alloc = std::max(nl, 1);
+    uint8_t *dg = nullptr, *du = nullptr, *dd = nullptr;
+    int32_t *ds = nullptr;
+    hipError_t err = hipMalloc(&dg, t->gb * n_alloc);
+    if (err == hipSuccess) err = hipMalloc(&du, t->gb * n_alloc);
+    if (err == hipSuccess) err = hipMalloc(&dd, t->db * n_alloc);
+    if (err == hipSuccess) err = hipMalloc(&ds, sizeof(int32_t) * t->E);
+    for (int e = 0; err == hipSuccess && e < t->E; ++e) {
+        if (slot_host[e] < 0) continue;
+        const size_t sl = (size_t) slot_host[e];
+        err = hipMemcpy(dg + sl * t->gb, t->gate + (size_t) e * t->gb, t->gb, hipMemcpyHostToDevice);
+        if (err == hipSuccess) err = hipMemcpy(du + sl * t->gb, t->up + (size_t) e * t->gb, t->gb, hipMemcpyHostToDevice);
+        if (err == hipSuccess) err = hipMemcpy(dd + sl * t->db, t->down + (size_t) e * t->db, t->db, hipMemcpyHostToDevice);
+    }
+    if (err == hipSuccess) err = hipMemcpy(ds, slot_host, sizeof(int32_t) * t->E, hipMemcpyHostToDevice);
+    if (err != hipSuccess) {
+        (void) hipFree(dg); (void) hipFree(du); (void) hipFree(dd); (void) hipFree(ds);
+        set_error("hy_upload_experts: %s", hipGetErrorString(err));
+        return HY_EHIP;
+    }
+    hy_moe_dev m;
+    m.gate = dg; m.up = du; m.down = dd;
+    m.tg = t->tg; m.td = t->td;
+    m.gate_bytes = t->gb; m.down_bytes = t->db;
+    m.slot = ds;
+    m.ff = ff; m.n = n; m.clamp = clamp; m.n_expert = t->E;
+    *out = m;
+    return HY_OK;
+}
+int hy_free_experts(hy_moe_dev *m) {
+    if (!m) return HY_EINVAL;
+    (void) hipFree((void *) m->gate); (void) hipFree((void *) m->up); (void) hipFree((void *) m->down); (void) hipFree((void *) m->slot);
+    m->gate = m->up = m->down = nullptr;
+    m->slot = nullptr;
+    return HY_OK;
+}
+
+int hy_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bias_stride,
+                hipStream_t s) {
+    if (!W || !x || !y || rows < 0 || nt < 0) { set_error("hy_gemv_f32: bad argument"); return HY_EINVAL; }
+    if (kdim <= 0 || kdim % 4 || xs % 4 || !aligned16(W) || !aligned16(x)) { set_error("hy_gemv_f32: kdim/xs must be multiples of 4, W/x 16-byte aligned"); return HY_EBAD_SHAPE; }
+    if (rows == 0 || nt == 0) return HY_OK;
+    return launch_gemv_f32(W, rows, kdim, x, xs, y, ys, nt, bias, bias_stride, s);
+}
+
+int hy_moe_route(const float *logits, int ls, int n_expert, int k, int32_t *ids, float *wts, float *sg, int nt, hipStream_t s) {
+    if (!logits || !ids || !wts || nt < 0) { set_error("hy_moe_route: bad argument"); return HY_EINVAL; }
+    if (n_expert <= 0 || n_expert > 1024) { set_error("hy_moe_route: too many experts (%d > 1024)", n_expert); return HY_EBAD_SHAPE; }
+    if (k <= 0 || k > 64 || k > n_expert) { set_error("hy_moe_route: k = %d out of range", k); return HY_EBAD_SHAPE; }
+    if (ls < n_expert || (sg && ls <= n_expert)) { set_error("hy_moe_route: logit stride %d too small", ls); return HY_EBAD_SHAPE; }
+    return launch_route(logits, ls, n_expert, k, ids, wts, sg, nt, s);
+}
+
+int hy_moe_order(const hy_moe_dev *m, const int32_t *ids, int n_pairs, int n_expert, int32_t *order, int32_t *order_n, hipStream_t s,
+                 int32_t *egrp) {
+    if (!m || !m->slot || !ids || !order || !order_n || n_pairs < 0) { set_error("hy_moe_order: bad argument"); return HY_EINVAL; }
+    if (n_expert <= 0 || n_expert > 1024 || n_expert > m->n_expert) { set_error("hy_moe_order: n_expert %d out of range", n_expert); return HY_EBAD_SHAPE; }
+    return launch_order(m->slot, ids, n_pairs, n_expert, order, order_n, egrp, s);
+}
+
+int hy_q8_quantize(int vtype, const float *x, int xs, int n, int nt, void *q, hipStream_t s) {
+    if (!x || !q || nt < 0) { set_error("hy_q8_quantize: bad argument"); return HY_EINVAL; }
+    if (vtype == Q8_K) {
+        if (n <= 0 || n % 256 || xs % 4 || !aligned16(x) || ((uintptr_t) q & 3)) { set_error("hy_q8_quantize: Q8_K needs n %% 256 == 0, xs %% 4 == 0, aligned rows"); return HY_EBAD_SHAPE; }
+    } else if (vtype == Q8_0) {
+        if (n <= 0 || n % 32 || ((uintptr_t) q & 1)) { set_error("hy_q8_quantize: Q8_0 needs n %% 32 == 0"); return HY_EBAD_SHAPE; }
+    } else { set_error("hy_q8_quantize: vtype %d", vtype); return HY_EUNSUPPORTED_TYPE; }
+    return launch_q8(vtype, x, xs, n, nt, q, s);
+}
+
+int hy_moe_gate_up(const hy_moe_dev *m, const float *x, int xs, const int32_t *ids, int k, float *h, int nt, hipStream_t s,
+                   const int32_t *order, const int32_t *order_n) {
+    int rc = check_dev(m, "hy_moe_gate_up", true, false);
+    if (rc) return rc;
+    if (!x || !ids || !h || k <= 0 || nt < 0 || (order && !order_n)) { set_error("hy_moe_gate_up: bad argument"); return HY_EINVAL; }
+    if (xs % 4 || !aligned16(x)) { set_error("hy_moe_gate_up: x rows must be 16-byte aligned"); return HY_EBAD_SHAPE; }
+    return launch_gate_up(*m, x, xs, ids, k, h, nt, s, order, order_n);
+}
+
+int hy_moe_down(const hy_moe_dev *m, const float *h, const int32_t *ids, const float *wts, int k, float *y, int nt, hipStream_t s,
+                const int32_t *order, const int32_t *order_n) {
+    int rc = check_dev(m, "hy_moe_down", false, true);
+    if (rc) return rc;
+    if (!h || !ids || !wts || !y || k <= 0 || nt < 0 || (order && !order_n)) { set_error("hy_moe_down: bad argument"); return HY_EINVAL; }
+    if (m->ff % 4 || !aligned16(h)) { set_error("hy_moe_down: h rows must be 16-byte aligned"); return HY_EBAD_SHAPE; }
+    return launch_down(*m, h, ids, wts, k, y, nt, s, order, order_n);
+}
+
+int hy_moe_gemm_gate_up(const hy_moe_dev *m, const void *xq, int k, const int32_t *order, const int32_t *order_n, const int32_t *egrp,
+                        int max_active, float *h, hipStream_t s) {
+    int rc = check_dev(m, "hy_moe_gemm_gate_up", true, false);
+    if (rc) return rc;
+    if (!gemm_type(m->tg)) { set_error("hy_moe_gemm_gate_up: no grouped GEMM for type %d", m->tg); return HY_EUNSUPPORTED_TYPE; }
+    if (!xq || !order || !order_n || !egrp || !h || k <= 0 || max_active < 0) { set_error("hy_moe_gemm_gate_up: bad argument"); return HY_EINVAL; }
+    if ((uintptr_t) xq & 3) { set_error("hy_moe_gemm_gate_up: xq must be 4-byte aligned"); return HY_EBAD_SHAPE; }
+    return launch_gemm_gate_up(*m, xq, k, order, order_n, egrp, max_active, h, s);
+}
+
+int hy_moe_gemm_down(const hy_moe_dev *m, const void *hq, const int32_t *order, const int32_t *order_n, const int32_t *egrp, int max_active,
+                     const float *wts, float *y, hipStream_t s) {
+    int rc = check_dev(m, "hy_moe_gemm_down", false, true);
+    if (rc) return rc;
+    if (!gemm_type(m->td)) { set_error("hy_moe_gemm_down: no grouped GEMM for type %d", m->td); return HY_EUNSUPPORTED_TYPE; }
+    if (!hq || !order || !order_n || !egrp || !wts || !y || max_active < 0) { set_error("hy_moe_gemm_down: bad argument"); return HY_EINVAL; }
+    if ((uintptr_t) hq & 3) { set_error("hy_moe_gemm_down: hq must be 4-byte aligned"); return HY_EBAD_SHAPE; }
+    return launch_gemm_down(*m, hq, order, order_n, egrp, max_active, wts, y, s);
+}
+
+int hy_moe_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int32_t *ids, hipStream_t s) {
+    if (!y || !out || !ids || k <= 0 || k > 64 || n <= 0 || nt < 0) { set_error("hy_moe_reduce: bad argument"); return HY_EINVAL; }
+    return launch_reduce(shexp, sg, y, k, out, n, nt, ids, s);
+}
+
+int hy_moe_down_reduce(const hy_moe_dev *m, const float *h, const int32_t *ids, const float *wts, int k, const float *shexp, const float *sg,
+                       float *out, int nt, hipStream_t s) {
+    int rc = check_dev(m, "hy_moe_down_reduce", false, true);
+    if (rc) return rc;
+    if (!h || !ids || !wts || !out || k <= 0 || k > 64 || nt < 0) { set_error("hy_moe_down_reduce: bad argument"); return HY_EINVAL; }
+    if (!aligned16(h)) { set_error("hy_moe_down_reduce: h must be 16-byte aligned"); return HY_EBAD_SHAPE; }
+    return launch_down_reduce(*m, h, ids, wts, k, shexp, sg, out, nt, s);
+}
+
+int hy_dequant_row(int type, const uint8_t *row, int n, float *out, hipStream_t s) {
+    if (!row || !out || n < 0) { set_error("hy_dequant_row: bad argument"); return HY_EINVAL; }
+    if (!(dot_type(type) || type == Q8_0 || type == Q8_K)) { set_error("hy_dequant_row: type %d", type); return HY_EUNSUPPORTED_TYPE; }
+    if (n % block_elems(type) || ((uintptr_t) row & 3)) { set_error("hy_dequant_row: n %% block != 0 or row unaligned"); return HY_EBAD_SHAPE; }
+    return launch_dequant_row(type, row, n, out, s);
+}
+
+int hy_block_ints(int type, const uint8_t *rows, size_t row_bytes, int nrows, const void *xq, int n, int32_t *sumi, int32_t *summ,
+                  hipStream_t s) {
+    if (!rows || !xq || !sumi || !summ || nrows < 0) { set_error("hy_block_ints: bad argument"); return HY_EINVAL; }
+    if (!dot_type(type)) { set_error("hy_block_ints: type %d", type); return HY_EUNSUPPORTED_TYPE; }
+    if (n <= 0 || n % 256 || row_bytes % 2 || ((uintptr_t) rows & 15) || ((uintptr_t) xq & 3)) { set_error("hy_block_ints: n %% 256 != 0 or unaligned"); return HY_EBAD_SHAPE; }
+    return launch_block_ints(type, rows, row_bytes, nrows, xq, n, sumi, summ, s);
+}
+
+} // extern "C"

@@ -1,0 +1,191 @@
+// Shared device code of the MoE expert-FFN kernels (gfx950, wave64).
+//
+// Numeric contract (shared with the CPU oracle, which restates src/cpu_moe.cpp:668-1008):
+//  * activations are quantized to ggml's vec_dot partner of the weight type: Q8_K (K-quants, IQ4_XS,
+//    IQ2_XS; src/cpu_moe.cpp:35-78) or Q8_0 (IQ4_NL);
+//  * each weight block against its activation block yields exact integers sumi (and summ for the types
+//    with mins); a row dot product folds block b's integers into t_b with one fp32 formula and
+//    accumulates acc = fmaf(xd_b, t_b, acc) over b = 0, 1, ... in order;
+//  * SwiGLU uses hy_expf below (Cody-Waite reduction + the Cephes degree-5 polynomial);
+//  * the library is compiled with -ffp-contract=off: every product and sum not written as fmaf is
+//    rounded on its own, so results are bit-identical to the oracle's.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace hy {
+
+// GGUF type ids (src/gguf.h:13-18)
+enum GT : int { Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, IQ2_XS = 17, IQ4_NL = 20, IQ4_XS = 23 };
+
+constexpr int Q8K_BYTES = 292;   // float d; int8 qs[256]; int16 bsums[16]
+constexpr int Q8_0_BYTES = 34;   // fp16 d; int8 qs[32]
+
+__host__ __device__ constexpr int block_bytes(int t) {
+    return t == Q4_K ? 144 : t == Q5_K ? 176 : t == Q6_K ? 210 : t == IQ4_XS ? 136 : t == IQ2_XS ? 74
+         : t == IQ4_NL ? 18 : t == Q8_0 ? 34 : t == Q8_K ? 292 : 0;
+}
+__host__ __device__ constexpr int block_elems(int t) {
+    return (t == IQ4_NL || t == Q8_0) ? 32 : (t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == Q8_K) ? 256 : 0;
+}
+__host__ __device__ constexpr int vec_dot_type(int t) { return t == IQ4_NL ? Q8_0 : Q8_K; }
+
+// ------------------------------------------------------------------ scalar helpers
+
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+// exp(x) of the contract: x = n ln2 + r (ln2 = 0.693359375 - 2.12194440e-4, the first part exact in
+// 9 bits), exp(r) by the Cephes expf polynomial (S. L. Moshier), 2^n applied as two exact scalings.
+// Below exp(-87) the result is 0: no subnormal is ever produced.
+__device__ __forceinline__ float hy_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_huge_valf();
+    if (x < -87.0f) return 0.0f;
+    const float n = __builtin_rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(n, -0.693359375f, x);
+    r = __builtin_fmaf(n, 2.12194440e-4f, r);
+    float p = 1.9875691500e-4f;
+    p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+    p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+    p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+    p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+    p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+    const float z = r * r;
+    float y = __builtin_fmaf(p, z, r);
+    y = y + 1.0f;
+    const int ni = (int) n, n1 = ni / 2, n2 = ni - n1;
+    const float s1 = __uint_as_float((uint32_t) (n1 + 127) << 23), s2 = __uint_as_float((uint32_t) (n2 + 127) << 23);
+    return (y * s1) * s2;
+}
+__device__ __forceinline__ float hy_silu(float x) { return x / (1.0f + hy_expf(-x)); }
+// silu(g) * u, with a limit L > 0: silu(min(g, L)) * clamp(u, -L, L) (src/cpu_moe.cpp:891-892)
+__device__ __forceinline__ float hy_swiglu(float g, float u, float L) {
+    if (L > 0.0f) { g = fminf(g, L); u = fminf(fmaxf(u, -L), L); }
+    return hy_silu(g) * u;
+}
+
+// ------------------------------------------------------------------ wave helpers
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+__device__ __forceinline__ float wave_sum_xor(float v) {     // xor butterfly 32, 16, ..., 1 (every lane ends equal)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+template <int W> __device__ __forceinline__ int group_isum(int v) {   // sum over aligned groups of W lanes
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// 16 bytes from a 2-byte aligned address (GGUF blocks of 18, 74, 210 bytes): when the address is 2 mod 4,
+// a halfword, three dwords and a halfword -- exactly the 16 bytes, nothing past them
+__device__ __forceinline__ uint4 load16_a2(const uint8_t *p) {
+    uint4 v;
+    if (((uintptr_t) p & 3) == 0) {
+        const uint32_t *q = (const uint32_t *) p;
+        v.x = q[0]; v.y = q[1]; v.z = q[2]; v.w = q[3];
+        return v;
+    }
+    const uint32_t h0 = *(const uint16_t *) p, h4 = *(const uint16_t *) (p + 14);
+    const uint32_t *q = (const uint32_t *) (p + 2);
+    const uint32_t d1 = q[0], d2 = q[1], d3 = q[2];
+    v.x = h0 | (d1 << 16); v.y = (d1 >> 16) | (d2 << 16); v.z = (d2 >> 16) | (d3 << 16); v.w = (d3 >> 16) | (h4 << 16);
+    return v;
+}
+__device__ __forceinline__ uint4 load16_a4(const uint8_t *p) {   // dword-aligned 16 bytes
+    const uint32_t *q = (const uint32_t *) p;
+    uint4 v; v.x = q[0]; v.y = q[1]; v.z = q[2]; v.w = q[3];
+    return v;
+}
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t *p) { return *(const uint16_t *) p; }
+
+// ------------------------------------------------------------------ codebooks
+
+// IQ4_NL / IQ4_XS values (src/kernels4.cu:546)
+__device__ __constant__ const int8_t c_kv_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+// IQ2_XS codebook rows, base-3 coded (digit i = byte i: 0 -> 8, 1 -> 25, 2 -> 43)
+__device__ __constant__ const uint16_t c_iq2xs_code[512] = {
+#include "iq2xs_grid.inc"
+};
+// the IQ2 sign table: 7 sign bits plus an 8th that makes the count even (src/iq_grids.h:4-13)
+__device__ __forceinline__ uint32_t ksign(uint32_t i) { return i | ((uint32_t) (__builtin_popcount(i) & 1) << 7); }
+
+// ------------------------------------------------------------------ activation quantizers
+
+__device__ __forceinline__ int nearest_int(float f) {   // the 1.5 * 2^23 trick of ggml's nearest_int
+    const float v = f + 12582912.f;
+    return (__float_as_int(v) & 0x007fffff) - 0x00400000;
+}
+
+// one Q8_K block of 256 values by one wave (lane: values 4 lane .. 4 lane + 3): first-occurrence signed
+// max, iscale = -127/max, q = min(127, nearest_int(iscale * x)), int16 sums of 16, d = 1/iscale.
+// An all-zero block writes d = 0, qs = 0, bsums = 0. `out` may be global or LDS (4-byte aligned).
+__device__ __forceinline__ void q8k_block_wave(const float *x, uint8_t *out) {
+    const int lane = lane_id();
+    const float4 v = *(const float4 *) (x + 4 * lane);
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    float am = fabsf(xv[0]);
+    int ix = 0;
+#pragma unroll
+    for (int i = 1; i < 4; ++i) { const float a = fabsf(xv[i]); if (a > am) { am = a; ix = i; } }
+    int gi = 4 * lane + ix;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float oa = __shfl_xor(am, o);
+        const int oi = __shfl_xor(gi, o);
+        if (oa > am || (oa == am && oi < gi)) { am = oa; gi = oi; }
+    }
+    uint32_t packed = 0;
+    int s = 0;
+    float d = 0.0f;
+    if (am > 0.0f) {
+        const int src = gi >> 2, c = gi & 3;
+        const float m0 = __shfl(xv[0], src), m1 = __shfl(xv[1], src), m2 = __shfl(xv[2], src), m3 = __shfl(xv[3], src);
+        const float mx = c == 0 ? m0 : c == 1 ? m1 : c == 2 ? m2 : m3;
+        const float iscale = -127.f / mx;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float pr = iscale * xv[i];
+            int q = nearest_int(pr);
+            q = q < 127 ? q : 127;
+            s += q;
+            packed |= (uint32_t) (q & 0xff) << (8 * i);
+        }
+        d = 1.0f / iscale;
+    }
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    ((uint32_t *) (out + 4))[lane] = packed;
+    if ((lane & 3) == 0) ((int16_t *) (out + 260))[lane >> 2] = (int16_t) s;
+    if (lane == 0) *(float *) out = d;
+}
+
+// two Q8_0 blocks of 32 by one wave (lanes 0-31: the first, 32-63: the second), as ggml's x86 quantize_row_q8_0:
+// d = amax / 127 (stored fp16), id = 127 / amax (0 if amax == 0), q = round-to-nearest-even(x * id).
+// `out` points at the first block; `valid2`: the second block exists.
+__device__ __forceinline__ void q8_0_blocks_wave(const float *x, uint8_t *out, bool valid2) {
+    const int lane = lane_id();
+    const bool on = lane < 32 || valid2;
+    const float v = on ? x[lane] : 0.0f;
+    float am = fabsf(v);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+    const float d = am / 127.f;
+    const float id = am != 0.0f ? 127.f / am : 0.0f;
+    const int q = (int) __builtin_rintf(v * id);
+    if (on) {
+        uint8_t *b = out + (lane >> 5) * Q8_0_BYTES;
+        b[2 + (lane & 31)] = (uint8_t) (int8_t) q;
+        if ((lane & 31) == 0) *(uint16_t *) b = f2h(d);
+    }
+}
+
+} // namespace hy

@@ -1,0 +1,32 @@
+// Internal declarations shared by the HIP translation units of libhymoe.so.
+#pragma once
+#include "../../include/hymoe.h"
+#include "hy_common.cuh"
+
+namespace hy {
+
+void set_error(const char *fmt, ...);
+// after a launch: HY_OK, or HY_EHIP with the launch error recorded under `what`
+int check_launch(const char *what);
+
+int launch_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bs,
+                    hipStream_t s);
+int launch_route(const float *logits, int ls, int ne, int k, int *ids, float *wts, float *sg, int nt, hipStream_t s);
+int launch_order(const int *slot, const int *ids, int P, int ne, int *order, int *order_n, int *egrp, hipStream_t s);
+int launch_q8(int vtype, const float *x, int xs, int n, int nt, void *q, hipStream_t s);
+int launch_gate_up(const hy_moe_dev &m, const float *x, int xs, const int *ids, int k, float *h, int nt, hipStream_t s, const int *order,
+                   const int *order_n);
+int launch_down(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, float *y, int nt, hipStream_t s,
+                const int *order, const int *order_n);
+int launch_down_reduce(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp, const float *sg,
+                       float *out, int nt, hipStream_t s);
+int launch_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int *ids, hipStream_t s);
+int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, const int *order, const int *order_n, const int *egrp, int max_active,
+                        float *h, hipStream_t s);
+int launch_gemm_down(const hy_moe_dev &m, const void *hq, const int *order, const int *order_n, const int *egrp, int max_active,
+                     const float *wts, float *y, hipStream_t s);
+int launch_dequant_row(int type, const uint8_t *row, int n, float *out, hipStream_t s);
+int launch_block_ints(int type, const uint8_t *rows, size_t row_bytes, int nrows, const void *xq, int n, int *sumi, int *summ,
+                      hipStream_t s);
+
+} // namespace hy

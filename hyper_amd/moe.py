@@ -1,0 +1,229 @@
+"""The reference's expert-compute API on torch device tensors, calling libhymoe's C ABI.
+
+Function names, argument order and meaning follow src/kernels4.cuh:45-91 and src/experts.h:26-50
+(moe_route, moe_order, moe_gate_up, moe_down, moe_gemm_gate_up, moe_gemm_down, moe_reduce,
+upload_experts); errors raise HyError where the reference throws std::runtime_error.  Activations for
+the grouped GEMMs are Q8 rows (q8_quantize) instead of the reference's fp16 copies.
+
+MoeLayerRunner strings the calls together the way the reference engine does per MoE layer
+(src/engine4.cu:807-888): router GEMV, route, then gate/up -> down -> combine for decode rows, or
+order -> quantize -> grouped GEMMs -> combine for a prefill chunk.
+"""
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import check, hy_expert_tensors, hy_moe_dev, lib
+from .formats import ExpertLayer, GType, q8_row_bytes, vec_dot_type
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _s(stream) -> ctypes.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+class MoeDev:
+    """Device expert weights + slot table (hy_moe_dev / MoeDev).  Keeps the tensors alive."""
+
+    def __init__(self, layer: ExpertLayer, slot: torch.Tensor):
+        self.layer, self.slot = layer, slot
+        c = hy_moe_dev()
+        c.gate, c.up, c.down = layer.gate.data_ptr(), layer.up.data_ptr(), layer.down.data_ptr()
+        c.tg, c.td = int(layer.tg), int(layer.td)
+        c.gate_bytes, c.down_bytes = layer.gate_bytes, layer.down_bytes
+        c.slot = slot.data_ptr()
+        c.ff, c.n, c.clamp, c.n_expert = layer.ff, layer.n, float(layer.clamp), slot.numel()
+        self.c = c
+        self.ref = ctypes.byref(c)
+
+    @property
+    def tg(self):
+        return self.layer.tg
+
+    @property
+    def td(self):
+        return self.layer.td
+
+
+def upload_experts(layer: ExpertLayer, slot=None, device="cuda") -> MoeDev:
+    """Copy the experts with slot[e] >= 0 to the device at their slots (src/experts.cu:56-74).
+    slot None: every expert at its own index."""
+    E = layer.E
+    slot_list = list(range(E)) if slot is None else [int(s) for s in slot]
+    nl = max(max(slot_list) + 1, 1)
+    shape_g, shape_d = (nl,) + tuple(layer.gate.shape[1:]), (nl,) + tuple(layer.down.shape[1:])
+    g = torch.zeros(shape_g, dtype=torch.uint8, device=device)
+    u = torch.zeros(shape_g, dtype=torch.uint8, device=device)
+    d = torch.zeros(shape_d, dtype=torch.uint8, device=device)
+    for e, s in enumerate(slot_list):
+        if s >= 0:
+            g[s].copy_(layer.gate[e]); u[s].copy_(layer.up[e]); d[s].copy_(layer.down[e])
+    dev_layer = ExpertLayer(layer.tg, layer.td, nl, layer.ff, layer.n, g, u, d, layer.clamp)
+    return MoeDev(dev_layer, torch.tensor(slot_list, dtype=torch.int32, device=device))
+
+
+def upload_experts_c(layer: ExpertLayer, slot) -> hy_moe_dev:
+    """The C ABI's own upload (hipMalloc + copies; release with free_experts)."""
+    t = hy_expert_tensors()
+    g, u, d = (layer.gate.contiguous().cpu(), layer.up.contiguous().cpu(), layer.down.contiguous().cpu())
+    t.gate, t.up, t.down = g.data_ptr(), u.data_ptr(), d.data_ptr()
+    t.gb, t.db, t.E, t.tg, t.td = layer.gate_bytes, layer.down_bytes, layer.E, int(layer.tg), int(layer.td)
+    sl = torch.tensor(list(slot), dtype=torch.int32)
+    out = hy_moe_dev()
+    check(lib().hy_upload_experts(ctypes.byref(t), _p(sl), layer.ff, layer.n, float(layer.clamp), ctypes.byref(out)))
+    return out
+
+
+def free_experts(m: hy_moe_dev) -> None:
+    check(lib().hy_free_experts(ctypes.byref(m)))
+
+
+# ------------------------------------------------------------------ the reference API
+
+def gemv_f32(W, rows, kdim, x, xs, y, ys, nt, stream=None, bias=None, bias_stride=0):
+    check(lib().hy_gemv_f32(_p(W), rows, kdim, _p(x), xs, _p(y), ys, nt, _p(bias), bias_stride, _s(stream)))
+
+
+def moe_route(logits, ls, n_expert, k, ids, wts, sg, nt, stream=None):
+    check(lib().hy_moe_route(_p(logits), ls, n_expert, k, _p(ids), _p(wts), _p(sg), nt, _s(stream)))
+
+
+def moe_order(m: MoeDev, ids, n_pairs, n_expert, order, order_n, stream=None, egrp=None):
+    check(lib().hy_moe_order(m.ref, _p(ids), n_pairs, n_expert, _p(order), _p(order_n), _s(stream), _p(egrp)))
+
+
+def q8_quantize(vtype, x, xs, n, nt, q, stream=None):
+    check(lib().hy_q8_quantize(int(vtype), _p(x), xs, n, nt, _p(q), _s(stream)))
+
+
+def moe_gate_up(m: MoeDev, x, xs, ids, k, h, nt, stream=None, order=None, order_n=None):
+    check(lib().hy_moe_gate_up(m.ref, _p(x), xs, _p(ids), k, _p(h), nt, _s(stream), _p(order), _p(order_n)))
+
+
+def moe_down(m: MoeDev, h, ids, wts, k, y, nt, stream=None, order=None, order_n=None):
+    check(lib().hy_moe_down(m.ref, _p(h), _p(ids), _p(wts), k, _p(y), nt, _s(stream), _p(order), _p(order_n)))
+
+
+def moe_gemm_gate_up(m: MoeDev, xq, k, order, order_n, egrp, max_active, h, stream=None):
+    check(lib().hy_moe_gemm_gate_up(m.ref, _p(xq), k, _p(order), _p(order_n), _p(egrp), max_active, _p(h), _s(stream)))
+
+
+def moe_gemm_down(m: MoeDev, hq, order, order_n, egrp, max_active, wts, y, stream=None):
+    check(lib().hy_moe_gemm_down(m.ref, _p(hq), _p(order), _p(order_n), _p(egrp), max_active, _p(wts), _p(y), _s(stream)))
+
+
+def moe_reduce(shexp, sg, y, k, out, n, nt, ids, stream=None):
+    check(lib().hy_moe_reduce(_p(shexp), _p(sg), _p(y), k, _p(out), n, nt, _p(ids), _s(stream)))
+
+
+def moe_down_reduce(m: MoeDev, h, ids, wts, k, shexp, sg, out, nt, stream=None):
+    check(lib().hy_moe_down_reduce(m.ref, _p(h), _p(ids), _p(wts), k, _p(shexp), _p(sg), _p(out), nt, _s(stream)))
+
+
+def dequant_row(type_, row, n, out, stream=None):
+    check(lib().hy_dequant_row(int(type_), _p(row), n, _p(out), _s(stream)))
+
+
+def block_ints(type_, rows, row_bytes, nrows, xq, n, sumi, summ, stream=None):
+    check(lib().hy_block_ints(int(type_), _p(rows), row_bytes, nrows, _p(xq), n, _p(sumi), _p(summ), _s(stream)))
+
+
+# ------------------------------------------------------------------ one MoE layer, engine-style
+
+class MoeLayerRunner:
+    """Workspace + call sequence for one MoE layer on one GPU.
+
+    decode(x): rows <= decode_rows use gate/up GEMV -> fused down+combine (src/engine4.cu:880-888);
+    prefill(x): bucketing + grouped int8-MFMA GEMMs (src/engine4.cu:851-854, :887).
+    The router is fp32 W_r [E, d] (src/engine4.cu:807); `bias` adds per-token logits (skewed routing).
+    """
+
+    def __init__(self, dev: MoeDev, W_r: torch.Tensor, k: int, max_rows: int, shared: Optional[MoeDev] = None,
+                 sg_logit: bool = False):
+        L = dev.layer
+        self.dev, self.W_r, self.k, self.E, self.d, self.ff = dev, W_r, k, dev.slot.numel(), L.n, L.ff
+        self.shared = shared
+        self.sg_logit = sg_logit
+        device = W_r.device
+        T, P = max_rows, max_rows * k
+        f32, i32 = dict(dtype=torch.float32, device=device), dict(dtype=torch.int32, device=device)
+        self.ls = self.E + (1 if sg_logit else 0)
+        self.logits = torch.empty(T, self.ls, **f32)
+        self.ids = torch.empty(P, **i32)
+        self.wts = torch.empty(P, **f32)
+        self.sg = torch.empty(T, **f32) if sg_logit else None
+        self.order = torch.empty(P, **i32)
+        self.order_n = torch.zeros(2, **i32)
+        self.egrp = torch.empty(3 * self.E, **i32)
+        self.h = torch.empty(P, self.ff, **f32)
+        self.y = torch.empty(P, self.d, **f32)
+        self.out = torch.empty(T, self.d, **f32)
+        self.vg, self.vd = vec_dot_type(L.tg), vec_dot_type(L.td)
+        self.xq = torch.empty(T * q8_row_bytes(self.vg, self.d), dtype=torch.uint8, device=device)
+        self.hq = torch.empty(P * q8_row_bytes(self.vd, self.ff), dtype=torch.uint8, device=device)
+        if shared is not None:
+            S = shared.layer
+            self.sh_ids = torch.zeros(T, **i32)
+            self.sh_ones = torch.ones(T, **f32)
+            self.sh_h = torch.empty(T, S.ff, **f32)
+            self.sh_y = torch.empty(T, self.d, **f32)
+            self.sh_order = torch.arange(T, **i32)
+            self.sh_order_n = torch.tensor([0, 1], **i32)
+            self.sh_egrp = torch.tensor([0, 0, 0], **i32)
+            self.sh_xq = torch.empty(T * q8_row_bytes(vec_dot_type(S.tg), self.d), dtype=torch.uint8, device=device)
+            self.sh_hq = torch.empty(T * q8_row_bytes(vec_dot_type(S.td), S.ff), dtype=torch.uint8, device=device)
+
+    def route(self, x: torch.Tensor, nt: int, bias: Optional[torch.Tensor] = None, stream=None):
+        rows = self.W_r.shape[0]
+        gemv_f32(self.W_r, rows, self.d, x, x.stride(0), self.logits, self.ls, nt, stream,
+                 bias=bias, bias_stride=0 if bias is None else bias.stride(0))
+        moe_route(self.logits, self.ls, self.E, self.k, self.ids, self.wts, self.sg, nt, stream)
+
+    def _shared_decode(self, x, nt, stream):
+        S = self.shared
+        moe_gate_up(S, x, x.stride(0), self.sh_ids, 1, self.sh_h, nt, stream)
+        moe_down(S, self.sh_h, self.sh_ids, self.sh_ones, 1, self.sh_y, nt, stream)
+
+    def _shared_prefill(self, x, nt, stream):
+        S = self.shared
+        # one active "expert" holding every token: (0, 0, nt)
+        self.sh_order_n[0] = nt
+        self.sh_egrp[2] = nt
+        q8_quantize(vec_dot_type(S.tg), x, x.stride(0), self.d, nt, self.sh_xq, stream)
+        moe_gemm_gate_up(S, self.sh_xq, 1, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_h, stream)
+        q8_quantize(vec_dot_type(S.td), self.sh_h, S.layer.ff, S.layer.ff, nt, self.sh_hq, stream)
+        moe_gemm_down(S, self.sh_hq, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_ones, self.sh_y, stream)
+
+    def decode(self, x: torch.Tensor, bias=None, stream=None) -> torch.Tensor:
+        nt = x.shape[0]
+        self.route(x, nt, bias, stream)
+        shexp = None
+        if self.shared is not None:
+            self._shared_decode(x, nt, stream)
+            shexp = self.sh_y
+        moe_gate_up(self.dev, x, x.stride(0), self.ids, self.k, self.h, nt, stream)
+        moe_down_reduce(self.dev, self.h, self.ids, self.wts, self.k, shexp, self.sg, self.out, nt, stream)
+        return self.out[:nt]
+
+    def prefill(self, x: torch.Tensor, bias=None, stream=None, shared_ready=False) -> torch.Tensor:
+        nt, k = x.shape[0], self.k
+        P = nt * k
+        self.route(x, nt, bias, stream)
+        moe_order(self.dev, self.ids, P, self.E, self.order, self.order_n, stream, self.egrp)
+        q8_quantize(self.vg, x, x.stride(0), self.d, nt, self.xq, stream)
+        max_active = min(self.E, P)
+        moe_gemm_gate_up(self.dev, self.xq, k, self.order, self.order_n, self.egrp, max_active, self.h, stream)
+        q8_quantize(self.vd, self.h, self.ff, self.ff, P, self.hq, stream)
+        moe_gemm_down(self.dev, self.hq, self.order, self.order_n, self.egrp, max_active, self.wts, self.y, stream)
+        shexp = None
+        if self.shared is not None:
+            self._shared_prefill(x, nt, stream)
+            shexp = self.sh_y
+        moe_reduce(shexp, self.sg, self.y, k, self.out, self.d, nt, self.ids, stream)
+        return self.out[:nt]

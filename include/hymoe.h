@@ -1,0 +1,144 @@
+/*
+ * hymoe -- C ABI of the MI355X (gfx950) quantized MoE expert-FFN path.
+ *
+ * Every entry point replaces one function of the reference's expert-compute API (hyper, src/kernels4.cuh:45-91,
+ * src/experts.h:26-50, src/cpu_moe.h:31-90); the citation above each declaration names it.  Differences that
+ * apply to all of them:
+ *   - plain C: pointers and sizes, a hipStream_t, an int status instead of a C++ exception
+ *     (HY_OK, or an HY_E* code with a message from hy_last_error(), thread-local);
+ *   - every device pointer is caller-owned (the reference's callers own theirs as well); no entry point
+ *     except hy_upload_experts allocates, and all are stream-ordered and free of host synchronisation;
+ *   - activations reach the expert matrices as Q8 blocks (block_q8_K, 292 B per 256 values, or block_q8_0,
+ *     34 B per 32 values for IQ4_NL weights), the partner types of the reference's CPU path
+ *     (src/cpu_moe.cpp:711-715), and every block dot product is an exact integer.
+ *
+ * Results are bit-identical to the CPU oracle of this repository (oracle/), which restates the reference's
+ * CPU expert path src/cpu_moe.cpp:668-1008.
+ */
+#ifndef HYMOE_H
+#define HYMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    HY_OK = 0,
+    HY_EUNSUPPORTED_TYPE = 1,   /* weight type without kernels (reference: runtime_error, src/kernels4.cu:1970) */
+    HY_EBAD_SHAPE = 2,          /* sizes / strides the kernels do not take (src/kernels4.cu:1926-1927, :2027-2030) */
+    HY_EHIP = 3,                /* a HIP runtime error (reference: CUDA_CHECK, src/cuda_check.h:7-8) */
+    HY_EINVAL = 4               /* null pointer or out-of-range argument */
+};
+
+/* GGUF type ids used by the path (src/gguf.h:13-18) */
+enum {
+    HY_Q8_0 = 8, HY_Q4_K = 12, HY_Q5_K = 13, HY_Q6_K = 14, HY_Q8_K = 15,
+    HY_IQ2_XS = 17, HY_IQ4_NL = 20, HY_IQ4_XS = 23
+};
+
+/* Expert weights of one layer on the device (replaces MoeDev, src/kernels4.cuh:56-63): n_local experts,
+   gate/up [n_local][ff][row bytes of n values] and down [n_local][n][row bytes of ff values] in their GGUF
+   types; slot[e] (device, n_expert entries) = local index of expert e or -1. */
+typedef struct hy_moe_dev {
+    const uint8_t *gate, *up, *down;
+    int32_t tg, td;                 /* gate/up type, down type */
+    size_t gate_bytes, down_bytes;  /* bytes per expert matrix */
+    const int32_t *slot;
+    int32_t ff, n;                  /* expert intermediate size, d_model */
+    float clamp;                    /* SwiGLU limit (0: none) */
+    int32_t n_expert;               /* entries of slot (not in MoeDev: ids outside [0, n_expert) are skipped, as on the CPU,
+                                       src/cpu_moe.cpp:679, instead of indexing slot out of bounds) */
+} hy_moe_dev;
+
+/* Host view of one layer's GGUF expert tensors (replaces ExpertTensors, src/experts.h:20-26). */
+typedef struct hy_expert_tensors {
+    const uint8_t *gate, *up, *down;   /* host, [E] expert matrices back to back */
+    size_t gb, db;                     /* bytes of one expert's gate (= up) / down matrix */
+    int32_t E;
+    int32_t tg, td;
+} hy_expert_tensors;
+
+const char *hy_last_error(void);
+int hy_abi_version(void);
+
+/* bytes per block / values per block / activation partner type of a GGUF type (src/gguf.cpp:43-82;
+   vec_dot_type: src/cpu_moe.cpp:711-715); 0 or -1 for types the path does not take */
+size_t hy_block_bytes(int type);
+int hy_block_elems(int type);
+int hy_vec_dot_type(int type);
+/* bytes of one quantized activation row of n values in partner type vtype */
+size_t hy_q8_row_bytes(int vtype, int n);
+
+/* Upload the experts with slot_host[e] >= 0 to their slots (replaces upload_experts, src/experts.h:50 /
+   src/experts.cu:56-74).  Allocates gate/up/down and the slot table with hipMalloc; hy_free_experts releases. */
+int hy_upload_experts(const hy_expert_tensors *t, const int32_t *slot_host, int32_t ff, int32_t n, float clamp, hy_moe_dev *out);
+int hy_free_experts(hy_moe_dev *m);
+
+/* Router logits y[t][r] = W[r] . x[t] (+ bias[t * bias_stride + r] if bias) for fp32 W [rows][kdim]
+   (replaces gemv_f32, src/kernels4.cuh:35 / src/kernels4.cu:1910-1913).  kdim % 4 == 0, xs % 4 == 0. */
+int hy_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt,
+                const float *bias, int bias_stride, hipStream_t s);
+
+/* Softmax over logits[t][0..n_expert), top-k (ties to the lower index), weights renormalised over the selected;
+   sg[t] = sigmoid(logits[t][n_expert]) when sg is not NULL (needs ls > n_expert)
+   (replaces moe_route, src/kernels4.cuh:48 / src/kernels4.cu:1925-1935).  n_expert <= 1024, k <= 64. */
+int hy_moe_route(const float *logits, int ls, int n_expert, int k, int32_t *ids, float *wts, float *sg, int nt, hipStream_t s);
+
+/* Pairs p < n_pairs whose expert has slot >= 0, grouped by expert in ascending id, stable by pair index:
+   order[], order_n[0] = their count, order_n[1] = active experts, egrp[3 i ..] = (expert, start, count)
+   (replaces moe_order, src/kernels4.cuh:74-75 / src/kernels4.cu:2059-2062).  n_expert <= 1024. */
+int hy_moe_order(const hy_moe_dev *m, const int32_t *ids, int n_pairs, int n_expert, int32_t *order, int32_t *order_n,
+                 hipStream_t s, int32_t *egrp);
+
+/* Activations to Q8 blocks: rows x[t * xs ..][0..n) -> q (nt rows of hy_q8_row_bytes(vtype, n) bytes)
+   (replaces to_half before the grouped GEMMs, src/kernels.cu:2235-2237, and the CPU path's quantizer,
+   src/cpu_moe.cpp:35-78 for Q8_K).  vtype HY_Q8_K (n % 256 == 0) or HY_Q8_0 (n % 32 == 0). */
+int hy_q8_quantize(int vtype, const float *x, int xs, int n, int nt, void *q, hipStream_t s);
+
+/* Decode gate/up: h[p][f] = silu(gate_e[f] . x[t]) * (up_e[f] . x[t]) for pairs p = t*k + j (or the order_n[0]
+   pairs in order) whose expert is local; x is quantized inside (replaces moe_gate_up, src/kernels4.cuh:67-68 /
+   src/kernels4.cu:1973-2006). */
+int hy_moe_gate_up(const hy_moe_dev *m, const float *x, int xs, const int32_t *ids, int k, float *h, int nt, hipStream_t s,
+                   const int32_t *order, const int32_t *order_n);
+
+/* Decode down: y[p][r] = wts[p] * (down_e[r] . q8(h[p])); without order non-local pairs get 0
+   (replaces moe_down, src/kernels4.cuh:70-71 / src/kernels4.cu:2007-2022). */
+int hy_moe_down(const hy_moe_dev *m, const float *h, const int32_t *ids, const float *wts, int k, float *y, int nt, hipStream_t s,
+                const int32_t *order, const int32_t *order_n);
+
+/* Prefill / verify grouped GEMMs over bucketed pairs (replace moe_gemm_gate_up / moe_gemm_down,
+   src/kernels4.cuh:77-80 / src/kernels4.cu:2063-2093).  xq: Q8 rows of the tokens (pair p reads row p / k);
+   h [n_pairs][ff] fp32; hq: Q8 rows of h per pair; y[p][r] = wts[p] * (down_e[r] . hq[p]).
+   grid: max_active >= order_n[1] expert blocks. */
+int hy_moe_gemm_gate_up(const hy_moe_dev *m, const void *xq, int k, const int32_t *order, const int32_t *order_n,
+                        const int32_t *egrp, int max_active, float *h, hipStream_t s);
+int hy_moe_gemm_down(const hy_moe_dev *m, const void *hq, const int32_t *order, const int32_t *order_n, const int32_t *egrp,
+                     int max_active, const float *wts, float *y, hipStream_t s);
+
+/* Combine: out[t][r] = sg[t] * shexp[t][r] (when shexp; sg NULL: 1) + the pairs' y[t*k + j][r] added in ascending
+   expert-id order (without shexp the first pair is the start value); ids with a negative expert are skipped
+   (replaces moe_reduce, src/kernels4.cuh:88-91 / src/kernels4.cu:1182-1206, single device, no CPU owner). */
+int hy_moe_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int32_t *ids,
+                  hipStream_t s);
+
+/* Decode down + combine in one launch: out[t][r] as hy_moe_reduce of hy_moe_down's y, without materialising y
+   (fuses src/kernels4.cu:2007-2022 with :1182-1206; every expert must be local). */
+int hy_moe_down_reduce(const hy_moe_dev *m, const float *h, const int32_t *ids, const float *wts, int k, const float *shexp,
+                       const float *sg, float *out, int nt, hipStream_t s);
+
+/* Test hooks.  One row of n weights dequantized by the kernels' block decoders (replaces deq_row_test,
+   src/kernels4.cuh:181 / src/kernels4.cu:2036-2044); and the exact integers of every block of nrows weight rows
+   (row stride row_bytes) against one Q8 activation row: sumi/summ [nrows][n / block_elems] (summ 0 for types
+   without mins) -- the per-block int32 dot products of the contract. */
+int hy_dequant_row(int type, const uint8_t *row, int n, float *out, hipStream_t s);
+int hy_block_ints(int type, const uint8_t *rows, size_t row_bytes, int nrows, const void *xq, int n, int32_t *sumi, int32_t *summ,
+                  hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,592 @@
+/*
+ * CPU oracle for the quantized MoE expert-FFN path -- TEST INFRASTRUCTURE ONLY (see moe_oracle.h).
+ *
+ * Every function names the reference lines it restates.  The reference's CPU path takes its block dot
+ * products and the Q8_0 quantizer from ggml, which is not vendored (Makefile:4, :15, :33-34); those are
+ * restated here from the block layouts the reference itself decodes (src/kernels4.cu:421-714) and the
+ * integer structure of its own IQ4_XS x Q8_K dot (src/iq3s_dot.h:136-166).
+ */
+#define _GNU_SOURCE
+#include "moe_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ formats / tables */
+
+size_t or_block_bytes(int type) {
+    switch (type) {                      /* src/gguf.cpp:43-82 */
+    case OR_Q8_0: return 34;
+    case OR_Q4_K: return 144;
+    case OR_Q5_K: return 176;
+    case OR_Q6_K: return 210;
+    case OR_Q8_K: return 292;
+    case OR_IQ2_XS: return 74;
+    case OR_IQ4_NL: return 18;
+    case OR_IQ4_XS: return 136;
+    default: return 0;
+    }
+}
+int or_block_elems(int type) {
+    switch (type) {
+    case OR_Q8_0: case OR_IQ4_NL: return 32;
+    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_Q8_K: case OR_IQ2_XS: case OR_IQ4_XS: return 256;
+    default: return 0;
+    }
+}
+/* ggml's vec_dot_type: Q8_0 for IQ4_NL, Q8_K for the K-quants and the 256-block IQ types
+   (the activation quantizer is chosen per weight type: src/cpu_moe.cpp:711-715) */
+int or_vec_dot_type(int type) {
+    switch (type) {
+    case OR_IQ4_NL: return OR_Q8_0;
+    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ4_XS: return OR_Q8_K;
+    default: return -1;
+    }
+}
+
+/* IQ4_NL / IQ4_XS codebook (src/kernels4.cu:546) */
+static const int8_t kv_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* IQ2_XS codebook: 512 rows, base-3 coded; expanded once (values of src/iq_grids.h:80-209) */
+static const uint16_t iq2xs_code[512] = {
+#include "../hyper_amd/csrc/iq2xs_grid.inc"
+};
+static uint8_t iq2xs_rows[512][8];
+static int iq2xs_ready = 0;
+static void iq2xs_init(void) {
+    if (__atomic_load_n(&iq2xs_ready, __ATOMIC_ACQUIRE)) return;
+    static const uint8_t lv[3] = {8, 25, 43};
+    for (int i = 0; i < 512; ++i) {
+        unsigned c = iq2xs_code[i];
+        for (int j = 0; j < 8; ++j) { iq2xs_rows[i][j] = lv[c % 3]; c /= 3; }
+    }
+    __atomic_store_n(&iq2xs_ready, 1, __ATOMIC_RELEASE);
+}
+/* the IQ2 sign table (src/iq_grids.h:4-13): 7 sign bits plus an 8th that makes the count even */
+static inline uint8_t ksign(unsigned i) { return (uint8_t) (i | ((unsigned) __builtin_parity(i) << 7)); }
+
+/* ------------------------------------------------------------------ scalar helpers */
+
+float or_fp16_to_fp32(uint16_t h) {
+    const uint32_t s = (uint32_t) (h & 0x8000) << 16, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+    uint32_t x;
+    if (e == 0) {
+        if (m == 0) x = s;
+        else { float f = (float) m * (1.0f / 16777216.0f); memcpy(&x, &f, 4); x |= s; }
+    } else if (e == 31) x = s | 0x7f800000 | (m << 13);
+    else x = s | ((e + 112) << 23) | (m << 13);
+    float f; memcpy(&f, &x, 4);
+    return f;
+}
+uint16_t or_fp32_to_fp16(float f) {          /* round to nearest even */
+    uint32_t x; memcpy(&x, &f, 4);
+    const uint16_t s = (uint16_t) ((x >> 16) & 0x8000);
+    const uint32_t a = x & 0x7fffffff;
+    if (a >= 0x7f800000) return s | (a > 0x7f800000 ? 0x7e00 : 0x7c00);
+    if (a >= 0x477ff000) return s | 0x7c00;                       /* >= 65520: inf */
+    if (a < 0x38800000) {                                         /* below 2^-14: subnormal half */
+        float v; memcpy(&v, &a, 4);
+        return s | (uint16_t) lrintf(v * 16777216.0f);           /* exact scaling, RNE */
+    }
+    const uint32_t mant = a & 0x7fffff, rem = mant & 0x1fff;
+    uint32_t h = ((((a >> 23) - 112) << 10) | (mant >> 13));
+    if (rem > 0x1000 || (rem == 0x1000 && (h & 1))) ++h;
+    return s | (uint16_t) h;
+}
+
+/* exp(x): Cody-Waite reduction x = n ln2 + r with ln2 = C1 + C2 (C1 exact in 9 bits), exp(r) by the Cephes
+   degree-5 polynomial (S. L. Moshier, Cephes Math Library, expf.c), 2^n applied as two exact power-of-two
+   scalings.  Results below exp(-87) (about 1.6e-38) are flushed to 0, so no subnormal is ever produced. */
+float or_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return INFINITY;
+    if (x < -87.0f) return 0.0f;
+    const float n = rintf(x * 1.44269504088896341f);
+    float r = fmaf(n, -0.693359375f, x);
+    r = fmaf(n, 2.12194440e-4f, r);
+    float p = 1.9875691500e-4f;
+    p = fmaf(p, r, 1.3981999507e-3f);
+    p = fmaf(p, r, 8.3334519073e-3f);
+    p = fmaf(p, r, 4.1665795894e-2f);
+    p = fmaf(p, r, 1.6666665459e-1f);
+    p = fmaf(p, r, 5.0000001201e-1f);
+    const float z = r * r;
+    float y = fmaf(p, z, r);
+    y = y + 1.0f;
+    const int ni = (int) n, n1 = ni / 2, n2 = ni - n1;
+    uint32_t b1 = (uint32_t) (n1 + 127) << 23, b2 = (uint32_t) (n2 + 127) << 23;
+    float s1, s2; memcpy(&s1, &b1, 4); memcpy(&s2, &b2, 4);
+    return (y * s1) * s2;
+}
+/* src/cpu_moe.cpp:29 */
+float or_silu(float x) { return x / (1.0f + or_expf(-x)); }
+
+/* ------------------------------------------------------------------ activation quantizers */
+
+/* Q8_K (src/cpu_moe.cpp:35-78, ggml's quantize_row_q8_K): first-occurrence signed max, iscale = -127/max,
+   products rounded by the 1.5 * 2^23 trick, min(127, v), int16 sums of 16, d = 1/iscale.  An all-zero
+   block gets d = 0, qs = 0 and (unlike the reference, which leaves them) bsums = 0. */
+static inline int nearest_int(float f) {
+    float v = f + 12582912.f;
+    int i; memcpy(&i, &v, 4);
+    return (i & 0x007fffff) - 0x00400000;
+}
+void or_quantize_q8_K(const float *x, void *vy, int n) {
+    uint8_t *y = (uint8_t *) vy;
+    for (int i = 0; i < n / 256; ++i, x += 256, y += 292) {
+        float amax = 0.0f, mx = 0.0f;
+        for (int j = 0; j < 256; ++j) { const float ax = fabsf(x[j]); if (ax > amax) { amax = ax; mx = x[j]; } }
+        int8_t qs[256];
+        int16_t bs[16];
+        float d;
+        if (amax == 0.0f) {
+            d = 0.0f; memset(qs, 0, sizeof qs); memset(bs, 0, sizeof bs);
+        } else {
+            const float iscale = -127.f / mx;
+            for (int j = 0; j < 256; ++j) {
+                const float pr = iscale * x[j];
+                const int v = nearest_int(pr);
+                qs[j] = (int8_t) (v < 127 ? v : 127);
+            }
+            for (int j = 0; j < 16; ++j) { int s = 0; for (int l = 0; l < 16; ++l) s += qs[16 * j + l]; bs[j] = (int16_t) s; }
+            d = 1.0f / iscale;
+        }
+        memcpy(y, &d, 4); memcpy(y + 4, qs, 256); memcpy(y + 260, bs, 32);
+    }
+}
+/* Q8_0 as ggml's x86 (AVX2) quantize_row_q8_0 computes it (the path the reference reaches through
+   from_float for IQ4_NL activations, src/cpu_moe.cpp:711-715): amax over 32, d = amax / 127 stored as fp16,
+   id = 127 / amax (0 for an all-zero block), q = round-to-nearest-even(x * id). */
+void or_quantize_q8_0(const float *x, void *vy, int n) {
+    uint8_t *y = (uint8_t *) vy;
+    for (int i = 0; i < n / 32; ++i, x += 32, y += 34) {
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
+        const float d = amax / 127.f;
+        const uint16_t dh = or_fp32_to_fp16(d);
+        const float id = amax != 0.0f ? 127.f / amax : 0.0f;
+        memcpy(y, &dh, 2);
+        for (int j = 0; j < 32; ++j) y[2 + j] = (uint8_t) (int8_t) (int) rintf(x[j] * id);
+    }
+}
+int or_quantize_row(int vtype, const float *x, void *y, int n) {
+    if (vtype == OR_Q8_K) { if (n % 256) return -1; or_quantize_q8_K(x, y, n); return 0; }
+    if (vtype == OR_Q8_0) { if (n % 32) return -1; or_quantize_q8_0(x, y, n); return 0; }
+    return -1;
+}
+
+/* ------------------------------------------------------------------ block decoding */
+
+static inline float h2f(const uint8_t *p) { uint16_t h; memcpy(&h, p, 2); return or_fp16_to_fp32(h); }
+
+/* src/kernels4.cu:423-426 */
+static inline void scale_min_k4(int j, const uint8_t *q, int *d, int *m) {
+    if (j < 4) { *d = q[j] & 63; *m = q[j + 4] & 63; }
+    else { *d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4); *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4); }
+}
+/* quant value of element e (0..255) of a Q4_K super-block: nibble e % 32 of sub-block e / 32 sits at
+   byte 16 + 32 (j / 2) + l, low nibble for even j (src/kernels4.cu:427-436) */
+static inline int q4k_q(const uint8_t *b, int e) {
+    const int j = e >> 5, l = e & 31;
+    return (b[16 + 32 * (j >> 1) + l] >> (4 * (j & 1))) & 0xF;
+}
+/* Q5_K: as Q4_K with qs at 48 and bit j of qh[l] as bit 4 (src/kernels4.cu:437-448) */
+static inline int q5k_q(const uint8_t *b, int e) {
+    const int j = e >> 5, l = e & 31;
+    return ((b[48 + 32 * (j >> 1) + l] >> (4 * (j & 1))) & 0xF) | (((b[16 + l] >> j) & 1) << 4);
+}
+/* Q6_K: q6 - 32 of element e (src/kernels4.cu:671-681) */
+static inline int q6k_q(const uint8_t *b, int e) {
+    const int hf = e >> 7, qt = (e >> 5) & 3, l = e & 31;
+    const int lo = (b[hf * 64 + (qt & 1) * 32 + l] >> (qt >= 2 ? 4 : 0)) & 0xF;
+    const int hi = (b[128 + hf * 32 + l] >> (2 * qt)) & 3;
+    return (lo | (hi << 4)) - 32;
+}
+/* IQ4_XS 6-bit group scale ls of 32-group ib (src/kernels4.cu:660-670) */
+static inline int iq4xs_ls(const uint8_t *b, int ib) {
+    const unsigned sh = (unsigned) b[2] | ((unsigned) b[3] << 8);
+    return ((b[4 + (ib >> 1)] >> (4 * (ib & 1))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4);
+}
+static inline int iq4xs_q(const uint8_t *b, int e) {    /* codebook value of element e */
+    const int ib = e >> 5, l = e & 31;
+    return kv_iq4nl[(b[8 + 16 * ib + (l & 15)] >> (l >= 16 ? 4 : 0)) & 0xF];
+}
+static inline int iq4nl_q(const uint8_t *b, int e) {    /* element e (0..31) of an 18-byte block */
+    return kv_iq4nl[(b[2 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF];
+}
+/* IQ2_XS signed grid value of element e and the 4-bit scale of its 8-group (src/kernels4.cu:592-601) */
+static inline int iq2xs_q(const uint8_t *b, int e) {
+    const int ib = e >> 5, l = (e >> 3) & 3, j = e & 7;
+    const unsigned q = (unsigned) b[2 + 2 * (4 * ib + l)] | ((unsigned) b[3 + 2 * (4 * ib + l)] << 8);
+    const int g = iq2xs_rows[q & 511][j];
+    return (ksign(q >> 9) >> j) & 1 ? -g : g;
+}
+static inline int iq2xs_sc(const uint8_t *b, int e) {
+    const int ib = e >> 5, l = (e >> 3) & 3;
+    return (b[66 + ib] >> (4 * (l >> 1))) & 0xF;
+}
+
+/* dequantized values: the deq8<T> expressions (src/kernels4.cu:427-714), each product rounded */
+int or_dequant_row(int type, const uint8_t *row, int n, float *out) {
+    const int be = or_block_elems(type);
+    const size_t bb = or_block_bytes(type);
+    if (!be || n % be) return -1;
+    iq2xs_init();
+    for (int ib = 0; ib < n / be; ++ib) {
+        const uint8_t *b = row + ib * bb;
+        float *o = out + (size_t) ib * be;
+        switch (type) {
+        case OR_Q4_K: case OR_Q5_K:
+            for (int e = 0; e < 256; ++e) {
+                int sc, m; scale_min_k4(e >> 5, b + 4, &sc, &m);
+                const float d = h2f(b) * (float) sc, mn = h2f(b + 2) * (float) m;
+                const int q = type == OR_Q4_K ? q4k_q(b, e) : q5k_q(b, e);
+                o[e] = d * (float) q - mn;
+            }
+            break;
+        case OR_Q6_K:
+            for (int e = 0; e < 256; ++e) {
+                const int hf = e >> 7, qt = (e >> 5) & 3, l = e & 31;
+                const float d = h2f(b + 208) * (float) (int8_t) b[192 + hf * 8 + (l >> 4) + 2 * qt];
+                o[e] = d * (float) q6k_q(b, e);
+            }
+            break;
+        case OR_IQ4_XS:
+            for (int e = 0; e < 256; ++e) o[e] = (h2f(b) * (float) (iq4xs_ls(b, e >> 5) - 32)) * (float) iq4xs_q(b, e);
+            break;
+        case OR_IQ4_NL:
+            for (int e = 0; e < 32; ++e) o[e] = (float) iq4nl_q(b, e) * h2f(b);
+            break;
+        case OR_IQ2_XS:
+            for (int e = 0; e < 256; ++e) {
+                const float db = h2f(b) * (0.5f + (float) iq2xs_sc(b, e)) * 0.25f;
+                const int q = iq2xs_q(b, e);
+                o[e] = (db * (float) (q < 0 ? -q : q)) * (q < 0 ? -1.0f : 1.0f);
+            }
+            break;
+        case OR_Q8_0:
+            for (int e = 0; e < 32; ++e) o[e] = h2f(b) * (float) (int8_t) b[2 + e];
+            break;
+        case OR_Q8_K: {
+            float d; memcpy(&d, b, 4);
+            for (int e = 0; e < 256; ++e) o[e] = d * (float) (int8_t) b[4 + e];
+            break;
+        }
+        default: return -1;
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ integer block dots */
+
+/* exact integers of one weight block (type, bytes b) against activation block y (Q8_K: 292 B, Q8_0: 34 B).
+   K-quants: sumi = sum_j sc_j S_j, summ = sum_j m_j (bsums[2j] + bsums[2j+1]) (ggml q4_K/q5_K x q8_K);
+   Q6_K: sumi = sum_g sc_g sum_16 (q6 - 32) y; IQ4_XS: sumi = sum_ib (ls - 32) sum_32 kv y (src/iq3s_dot.h:
+   136-166); IQ2_XS: sumi = sum (2 sc + 1) sum_16 grid sign y; IQ4_NL x Q8_0: sumi = sum_32 kv q8. */
+static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *sumi, int32_t *summ) {
+    int32_t si = 0, sm = 0;
+    const int8_t *q8 = (const int8_t *) (y + (type == OR_IQ4_NL ? 2 : 4));
+    switch (type) {
+    case OR_Q4_K: case OR_Q5_K: {
+        int16_t bs[16]; memcpy(bs, y + 260, 32);
+        for (int j = 0; j < 8; ++j) {
+            int sc, m; scale_min_k4(j, b + 4, &sc, &m);
+            int32_t s = 0;
+            for (int l = 0; l < 32; ++l) s += (type == OR_Q4_K ? q4k_q(b, 32 * j + l) : q5k_q(b, 32 * j + l)) * q8[32 * j + l];
+            si += sc * s;
+            sm += m * (bs[2 * j] + bs[2 * j + 1]);
+        }
+        break;
+    }
+    case OR_Q6_K:
+        for (int g = 0; g < 16; ++g) {
+            int32_t s = 0;
+            for (int l = 0; l < 16; ++l) s += q6k_q(b, 16 * g + l) * q8[16 * g + l];
+            si += (int8_t) b[192 + g] * s;
+        }
+        break;
+    case OR_IQ4_XS:
+        for (int ib = 0; ib < 8; ++ib) {
+            int32_t s = 0;
+            for (int l = 0; l < 32; ++l) s += iq4xs_q(b, 32 * ib + l) * q8[32 * ib + l];
+            si += (iq4xs_ls(b, ib) - 32) * s;
+        }
+        break;
+    case OR_IQ2_XS:
+        for (int g = 0; g < 16; ++g) {
+            int32_t s = 0;
+            for (int l = 0; l < 16; ++l) s += iq2xs_q(b, 16 * g + l) * q8[16 * g + l];
+            si += (2 * iq2xs_sc(b, 16 * g) + 1) * s;
+        }
+        break;
+    case OR_IQ4_NL:
+        for (int l = 0; l < 32; ++l) si += iq4nl_q(b, l) * q8[l];
+        break;
+    default: break;
+    }
+    *sumi = si; *summ = sm;
+}
+static int dot_ok(int type) {
+    return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_IQ4_XS || type == OR_IQ2_XS || type == OR_IQ4_NL;
+}
+int or_block_ints(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ) {
+    if (!dot_ok(type) || n % or_block_elems(type)) return -1;
+    iq2xs_init();
+    const size_t bb = or_block_bytes(type), yb = or_block_bytes(or_vec_dot_type(type));
+    for (int ib = 0; ib < n / or_block_elems(type); ++ib)
+        block_ints(type, row + ib * bb, (const uint8_t *) xq + ib * yb, sumi + ib, summ + ib);
+    return 0;
+}
+/* the contract's per-block fp32 fold, blocks accumulated in order */
+static float row_dot(int type, const uint8_t *row, const uint8_t *xq, int n) {
+    const size_t bb = or_block_bytes(type), yb = or_block_bytes(or_vec_dot_type(type));
+    float acc = 0.0f;
+    for (int ib = 0; ib < n / or_block_elems(type); ++ib) {
+        const uint8_t *b = row + ib * bb, *y = xq + ib * yb;
+        int32_t si, sm;
+        block_ints(type, b, y, &si, &sm);
+        float xd, t;
+        if (type == OR_IQ4_NL) xd = h2f(y); else memcpy(&xd, y, 4);
+        switch (type) {
+        case OR_Q4_K: case OR_Q5_K: t = fmaf(h2f(b), (float) si, -(h2f(b + 2) * (float) sm)); break;
+        case OR_Q6_K: t = h2f(b + 208) * (float) si; break;
+        case OR_IQ2_XS: t = (h2f(b) * 0.125f) * (float) si; break;
+        default: t = h2f(b) * (float) si; break;        /* IQ4_XS, IQ4_NL */
+        }
+        acc = fmaf(xd, t, acc);
+    }
+    return acc;
+}
+float or_row_dot(int type, const uint8_t *row, const void *xq, int n) {
+    if (!dot_ok(type) || n % or_block_elems(type)) return NAN;
+    iq2xs_init();
+    return row_dot(type, row, (const uint8_t *) xq, n);
+}
+
+/* ------------------------------------------------------------------ router */
+
+/* y[t][r] = W[r] . x[t] (the fp32 router GEMV, src/kernels4.cu:163-180) in the contract's order */
+void or_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt) {
+    for (int t = 0; t < nt; ++t)
+        for (int r = 0; r < rows; ++r) {
+            const float *w = W + (size_t) r * kdim, *xv = x + (size_t) t * xs;
+            float acc[64];
+            for (int L = 0; L < 64; ++L) {
+                float a = 0.0f;
+                for (int i = 0; 256 * i + 4 * L < kdim; ++i)
+                    for (int j = 0; j < 4; ++j) {
+                        const int e = 256 * i + 4 * L + j;
+                        if (e < kdim) a = fmaf(w[e], xv[e], a);
+                    }
+                acc[L] = a;
+            }
+            for (int off = 32; off > 0; off >>= 1) {
+                float nx[64];
+                for (int L = 0; L < 64; ++L) nx[L] = acc[L] + acc[L ^ off];
+                memcpy(acc, nx, sizeof acc);
+            }
+            y[(size_t) t * ys + r] = acc[0];
+        }
+}
+/* 64 partial sums (lane L: e = L + 64 i in order), then the xor butterfly */
+static float tree_sum64(const float *v, int n) {
+    float acc[64];
+    for (int L = 0; L < 64; ++L) { float a = 0.0f; for (int e = L; e < n; e += 64) a = a + v[e]; acc[L] = a; }
+    for (int off = 32; off > 0; off >>= 1) {
+        float nx[64];
+        for (int L = 0; L < 64; ++L) nx[L] = acc[L] + acc[L ^ off];
+        memcpy(acc, nx, sizeof acc);
+    }
+    return acc[0];
+}
+/* softmax, top-k by (p descending, index ascending), weights renormalized over the selected in selection
+   order, sg = sigmoid(logit ne) (src/kernels4.cu:297-344; ties: rt_better :295) */
+int or_route(const float *logits, int ls, int ne, int k, int nt, int32_t *ids, float *wts, float *sg) {
+    if (ne <= 0 || k <= 0 || k > ne || (sg && ls <= ne)) return -1;
+    float *v = (float *) malloc(sizeof(float) * ne);
+    unsigned char *used = (unsigned char *) malloc(ne);
+    if (!v || !used) { free(v); free(used); return -1; }
+    for (int t = 0; t < nt; ++t) {
+        const float *l = logits + (size_t) t * ls;
+        float mx = -INFINITY;
+        for (int e = 0; e < ne; ++e) mx = fmaxf(mx, l[e]);
+        for (int e = 0; e < ne; ++e) v[e] = or_expf(l[e] - mx);
+        const float s = tree_sum64(v, ne);
+        for (int e = 0; e < ne; ++e) v[e] = v[e] / s;
+        memset(used, 0, ne);
+        float sel[64];
+        float tot = 0.0f;
+        for (int j = 0; j < k; ++j) {
+            int bi = -1;
+            for (int e = 0; e < ne; ++e)
+                if (!used[e] && (bi < 0 || v[e] > v[bi])) bi = e;   /* strict >: ties keep the lower index */
+            used[bi] = 1;
+            ids[(size_t) t * k + j] = bi;
+            sel[j < 64 ? j : 63] = v[bi];
+            tot = tot + v[bi];
+        }
+        for (int j = 0; j < k; ++j) wts[(size_t) t * k + j] = v[ids[(size_t) t * k + j]] / tot;
+        if (sg) sg[t] = 1.0f / (1.0f + or_expf(-l[ne]));
+        (void) sel;
+    }
+    free(v); free(used);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ bucketing */
+
+int or_order(const int32_t *slot, const int32_t *ids, int n_pairs, int ne, int32_t *order, int32_t *order_n, int32_t *egrp) {
+    int32_t *cnt = (int32_t *) calloc(ne, sizeof(int32_t));
+    if (!cnt) return -1;
+    for (int p = 0; p < n_pairs; ++p) {
+        const int e = ids[p];
+        if (e >= 0 && e < ne && slot[e] >= 0) ++cnt[e];
+    }
+    int s = 0, na = 0;
+    for (int e = 0; e < ne; ++e) {
+        const int c = cnt[e];
+        if (c) { if (egrp) { egrp[3 * na] = e; egrp[3 * na + 1] = s; egrp[3 * na + 2] = c; } ++na; }
+        cnt[e] = s;
+        s += c;
+    }
+    for (int p = 0; p < n_pairs; ++p) {
+        const int e = ids[p];
+        if (e >= 0 && e < ne && slot[e] >= 0) order[cnt[e]++] = p;
+    }
+    order_n[0] = s; order_n[1] = na;
+    free(cnt);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ the layer job */
+
+static float swiglu(float g, float u, float L) {        /* src/cpu_moe.cpp:891-892, :29 */
+    if (L > 0.0f) { g = fminf(g, L); u = fminf(fmaxf(u, -L), L); }
+    return or_silu(g) * u;
+}
+
+typedef struct { int t, e, p; float w; } pair_t;
+static int pair_cmp(const void *a, const void *b) {     /* stable: ties by pair index */
+    const pair_t *x = (const pair_t *) a, *y = (const pair_t *) b;
+    if (x->e != y->e) return x->e < y->e ? -1 : 1;
+    return x->p < y->p ? -1 : x->p > y->p;
+}
+
+/* gate/up + SwiGLU for a list of (token, expert) rows, then h quantized, then down: y_out[i][n] */
+static int ffn_rows(const or_layer *L, int np, const int *tok, const int *exp_, const uint8_t *qx, size_t qx_row,
+                    float *h, float *y, int n_threads) {
+    const int ff = L->ff, n = L->n;
+    const int vg = or_vec_dot_type(L->tg), vd = or_vec_dot_type(L->td);
+    if (vg < 0 || vd < 0 || n % or_block_elems(L->tg) || ff % or_block_elems(L->td)) return -1;
+    const size_t g_row = L->gate_bytes / ff, d_row = L->down_bytes / n;
+    const size_t qh_row = (size_t) (ff / or_block_elems(vd)) * or_block_bytes(vd);
+    uint8_t *qh = (uint8_t *) malloc((size_t) np * qh_row + 1);
+    if (!qh) return -1;
+    const int RC = 16, gchunks = (ff + RC - 1) / RC;
+#pragma omp parallel for schedule(dynamic) num_threads(n_threads)
+    for (int task = 0; task < np * gchunks; ++task) {
+        const int i = task / gchunks, r0 = (task % gchunks) * RC, r1 = r0 + RC < ff ? r0 + RC : ff;
+        const uint8_t *gb = L->gate + (size_t) exp_[i] * L->gate_bytes, *ub = L->up + (size_t) exp_[i] * L->gate_bytes;
+        const uint8_t *xq = qx + (size_t) tok[i] * qx_row;
+        for (int r = r0; r < r1; ++r) {
+            const float g = row_dot(L->tg, gb + r * g_row, xq, n);
+            const float u = row_dot(L->tg, ub + r * g_row, xq, n);
+            h[(size_t) i * ff + r] = swiglu(g, u, L->clamp);
+        }
+    }
+#pragma omp parallel for num_threads(n_threads)
+    for (int i = 0; i < np; ++i) or_quantize_row(vd, h + (size_t) i * ff, qh + i * qh_row, ff);
+    const int RD = 32, dchunks = (n + RD - 1) / RD;
+#pragma omp parallel for schedule(dynamic) num_threads(n_threads)
+    for (int task = 0; task < np * dchunks; ++task) {
+        const int i = task / dchunks, r0 = (task % dchunks) * RD, r1 = r0 + RD < n ? r0 + RD : n;
+        const uint8_t *db = L->down + (size_t) exp_[i] * L->down_bytes;
+        for (int r = r0; r < r1; ++r) y[(size_t) i * n + r] = row_dot(L->td, db + r * d_row, qh + i * qh_row, ff);
+    }
+    free(qh);
+    return 0;
+}
+
+static int quantize_tokens(int vtype, int nt, const float *x, int xs, int n, uint8_t **qx, size_t *qx_row, int n_threads) {
+    *qx_row = (size_t) (n / or_block_elems(vtype)) * or_block_bytes(vtype);
+    *qx = (uint8_t *) malloc((size_t) nt * *qx_row + 1);
+    if (!*qx) return -1;
+#pragma omp parallel for num_threads(n_threads)
+    for (int t = 0; t < nt; ++t) or_quantize_row(vtype, x + (size_t) t * xs, *qx + t * *qx_row, n);
+    return 0;
+}
+
+int or_expert_ffn(const or_layer *L, int e, int nt, const float *x, int xs, float *h, float *y, int n_threads) {
+    iq2xs_init();
+    if (n_threads <= 0) n_threads = 1;
+    uint8_t *qx; size_t qx_row;
+    if (or_vec_dot_type(L->tg) < 0 || L->n % or_block_elems(L->tg)) return -1;
+    if (quantize_tokens(or_vec_dot_type(L->tg), nt, x, xs, L->n, &qx, &qx_row, n_threads)) return -1;
+    int *tok = (int *) malloc(sizeof(int) * (nt + 1)), *ex = (int *) malloc(sizeof(int) * (nt + 1));
+    float *hh = h ? h : (float *) malloc(sizeof(float) * (size_t) nt * L->ff + 1);
+    int rc = -1;
+    if (tok && ex && hh) {
+        for (int t = 0; t < nt; ++t) { tok[t] = t; ex[t] = e; }
+        rc = ffn_rows(L, nt, tok, ex, qx, qx_row, hh, y, n_threads);
+    }
+    if (!h) free(hh);
+    free(tok); free(ex); free(qx);
+    return rc;
+}
+
+/* src/cpu_moe.cpp:668-1008 (CpuMoe::run_layer, every expert owned, any nt): pairs grouped by expert
+   (stable), activations quantized, gate/up dots + SwiGLU, hidden re-quantized, down dots, weighted sum
+   per token in expert-id order.  With a shared expert its term sg * y_sh comes first (src/kernels4.cu:
+   1182-1206 starts moe_reduce's sum from it). */
+int or_moe_layer(const or_layer *L, int nt, const float *x, int xs, const int32_t *ids, const float *wts, int k,
+                 float *out, int os, const or_layer *sh, const float *sg, float *h_out, float *y_out, int n_threads) {
+    iq2xs_init();
+    if (n_threads <= 0) n_threads = 1;
+    const int n = L->n, ff = L->ff, P = nt * k;
+    if (or_vec_dot_type(L->tg) < 0 || or_vec_dot_type(L->td) < 0 || n % or_block_elems(L->tg) || ff % or_block_elems(L->td)) return -1;
+    pair_t *pairs = (pair_t *) malloc(sizeof(pair_t) * (P + 1));
+    int np = 0;
+    for (int t = 0; t < nt; ++t)
+        for (int j = 0; j < k; ++j) {
+            const int e = ids[t * k + j];
+            if (e < 0 || e >= L->E) continue;             /* garbage routing is skipped (src/cpu_moe.cpp:679) */
+            pairs[np].t = t; pairs[np].e = e; pairs[np].p = t * k + j; pairs[np].w = wts[t * k + j];
+            ++np;
+        }
+    qsort(pairs, np, sizeof(pair_t), pair_cmp);
+    uint8_t *qx; size_t qx_row;
+    if (quantize_tokens(or_vec_dot_type(L->tg), nt, x, xs, n, &qx, &qx_row, n_threads)) { free(pairs); return -1; }
+    int *tok = (int *) malloc(sizeof(int) * (np + 1)), *ex = (int *) malloc(sizeof(int) * (np + 1));
+    float *h = (float *) malloc(sizeof(float) * ((size_t) np * ff + 1)), *y = (float *) malloc(sizeof(float) * ((size_t) np * n + 1));
+    float *ysh = sh ? (float *) malloc(sizeof(float) * ((size_t) nt * sh->n + 1)) : NULL;
+    int rc = -1;
+    if (!tok || !ex || !h || !y || (sh && !ysh)) goto done;
+    for (int i = 0; i < np; ++i) { tok[i] = pairs[i].t; ex[i] = pairs[i].e; }
+    if (ffn_rows(L, np, tok, ex, qx, qx_row, h, y, n_threads)) goto done;
+    if (sh && or_expert_ffn(sh, 0, nt, x, xs, NULL, ysh, n_threads)) goto done;
+#pragma omp parallel for num_threads(n_threads)
+    for (int t = 0; t < nt; ++t) {
+        float *o = out + (size_t) t * os;
+        int first = 1;
+        if (sh) {
+            const float g = sg ? sg[t] : 1.0f;
+            for (int r = 0; r < n; ++r) o[r] = g * ysh[(size_t) t * sh->n + r];
+            first = 0;
+        }
+        for (int i = 0; i < np; ++i) {
+            if (pairs[i].t != t) continue;
+            const float w = pairs[i].w, *yy = y + (size_t) i * n;
+            if (first) { for (int r = 0; r < n; ++r) o[r] = w * yy[r]; first = 0; }
+            else for (int r = 0; r < n; ++r) o[r] = o[r] + w * yy[r];
+        }
+        if (first) for (int r = 0; r < n; ++r) o[r] = 0.0f;
+    }
+    if (h_out) for (int i = 0; i < np; ++i) memcpy(h_out + (size_t) pairs[i].p * ff, h + (size_t) i * ff, sizeof(float) * ff);
+    if (y_out) for (int i = 0; i < np; ++i) memcpy(y_out + (size_t) pairs[i].p * n, y + (size_t) i * n, sizeof(float) * n);
+    rc = 0;
+done:
+    free(pairs); free(qx); free(tok); free(ex); free(h); free(y); free(ysh);
+    return rc;
+}

@@ -1,0 +1,75 @@
+"""Shared test utilities: seeded inputs, the oracle's view of a layer, exact comparisons."""
+import numpy as np
+import torch
+
+import oracle as orc
+from hyper_amd.formats import GType, activations, random_layer, zipf_logit_bias
+
+TYPES_256 = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS]
+ALL_TYPES = TYPES_256 + [GType.IQ4_NL]
+D_RANGE = {GType.Q4_K: (1e-4, 4e-3), GType.Q5_K: (1e-4, 4e-3), GType.Q6_K: (1e-4, 4e-3),
+           GType.IQ4_XS: (1e-3, 1e-2), GType.IQ2_XS: (1e-3, 1e-2), GType.IQ4_NL: (1e-3, 1e-2)}
+
+
+def gen(seed: int) -> torch.Generator:
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return g
+
+
+def x_distributions(n: int, seed: int) -> dict:
+    """The activation distributions of the reference's quantizer test (tools/cpumoebench.cu:53-86): normal,
+    heavy-tailed x^3 * 30, values on a 1/8 grid (exact ties), sparse large outliers; plus all-zero and
+    negative-maximum blocks."""
+    rng = np.random.default_rng(seed)
+    z = rng.standard_normal(n).astype(np.float32)
+    d = {
+        "normal": z,
+        "heavy": (z ** 3 * 30).astype(np.float32),
+        "ties": (np.round(z * 8) / 8).astype(np.float32),
+        "sparse": np.where(rng.random(n) < 0.01, z * 1000, z * 0.01).astype(np.float32),
+    }
+    zero = z.copy()
+    zero[:256] = 0
+    d["zero_block"] = zero
+    neg = z.copy()
+    neg[37] = -50.0
+    neg[300] = 50.0     # equal magnitude later in the block: the first occurrence (negative) wins
+    d["neg_max"] = neg
+    return d
+
+
+def layer(tg, td, E, ff, n, seed, clamp=0.0):
+    return random_layer(tg, td, E, ff, n, seed, d_range=D_RANGE[GType(tg)], d_range_down=D_RANGE[GType(td)], clamp=clamp)
+
+
+def oracle_layer(L) -> "orc.Layer":
+    return orc.Layer.from_expert_layer(L)
+
+
+def routing(T, E, k, seed, zipf=None):
+    """ids/wts [T, k] from the oracle's router on seeded logits (Zipf-biased when zipf is set)."""
+    g = gen(seed)
+    logits = torch.randn(T, E, generator=g) * 0.5
+    if zipf:
+        logits = logits + zipf_logit_bias(T, E, zipf, g)
+    ids, wts, _ = orc.route(logits.numpy(), E, k)
+    return ids, wts
+
+
+def assert_bits_equal(a, b, what=""):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.shape == b.shape, f"{what}: shape {a.shape} vs {b.shape}"
+    if a.dtype.kind == "f":
+        ok = (a == b) | (np.isnan(a) & np.isnan(b))
+    else:
+        ok = a == b
+    if not ok.all():
+        idx = np.argwhere(~ok)
+        i = tuple(idx[0])
+        raise AssertionError(f"{what}: {int((~ok).sum())} of {a.size} differ; first at {i}: {a[i]!r} vs {b[i]!r}")
+
+
+def rel_l2(a, b) -> float:
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))

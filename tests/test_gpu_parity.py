@@ -1,0 +1,238 @@
+"""GPU parity: every kernel of the path through the C ABI against the CPU oracle on the same seeded inputs.
+
+Integer and index results (Q8 blocks, block integers, ids, order) must be identical; fp32 results are
+bit-identical under the shared numeric contract (each test also states the north star's 2e-3
+relative-L2 bound, which bit-identity implies).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from hyper_amd import moe
+from hyper_amd.formats import GType, block_bytes, block_elems, q8_row_bytes, random_blocks, vec_dot_type
+from tests.helpers import (ALL_TYPES, D_RANGE, TYPES_256, assert_bits_equal, gen, layer, oracle_layer, rel_l2, routing,
+                           x_distributions)
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3   # north star: final fp32 expert outputs within 2e-3 relative L2 of the CPU path
+
+
+def _sync():
+    torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------ A4: activation quantizers
+
+@pytest.mark.parametrize("vt", [GType.Q8_K, GType.Q8_0])
+def test_q8_quantize_bitexact(cuda, vt):
+    n = 2048
+    for name, x in x_distributions(4 * n, seed=11).items():
+        x2 = x.reshape(4, n)
+        ref = orc.quantize(vt, x2)
+        xd = torch.from_numpy(x2).to(cuda)
+        q = torch.zeros(4 * q8_row_bytes(vt, n), dtype=torch.uint8, device=cuda)
+        moe.q8_quantize(vt, xd, n, n, 4, q)
+        _sync()
+        assert_bits_equal(q.cpu().numpy().reshape(ref.shape), ref, f"{vt.name} {name}")
+
+
+# ------------------------------------------------------------------ A11: block decoding
+
+@pytest.mark.parametrize("t", ALL_TYPES + [GType.Q8_0])
+def test_dequant_row_bitexact(cuda, t):
+    n = 4096
+    nb = n // block_elems(t)
+    blk = random_blocks(t, nb, gen(21 + int(t)), "cpu", D_RANGE.get(t, (1e-3, 1e-2)))
+    row = blk.reshape(-1).numpy()
+    ref = orc.dequant_row(t, row, n)
+    out = torch.zeros(n, dtype=torch.float32, device=cuda)
+    moe.dequant_row(t, blk.reshape(-1).to(cuda), n, out)
+    _sync()
+    assert_bits_equal(out.cpu().numpy(), ref, f"dequant {t.name}")
+
+
+@pytest.mark.parametrize("t", ALL_TYPES)
+def test_block_ints_bitexact(cuda, t):
+    """The per-block int32 dot products (sumi, summ) of the decode kernels' item code."""
+    n, nrows = 2048, 24
+    rb = n // block_elems(t) * block_bytes(t)
+    rows = random_blocks(t, nrows * n // block_elems(t), gen(31 + int(t)), "cpu", D_RANGE[t]).reshape(nrows, rb)
+    vt = vec_dot_type(t)
+    x = x_distributions(n, seed=7)["heavy"]
+    xq = orc.quantize(vt, x)
+    ref_si = np.stack([orc.block_ints(t, rows[i].numpy(), xq, n)[0] for i in range(nrows)])
+    ref_sm = np.stack([orc.block_ints(t, rows[i].numpy(), xq, n)[1] for i in range(nrows)])
+    nb = n // block_elems(t)
+    si = torch.zeros(nrows * nb, dtype=torch.int32, device=cuda)
+    sm = torch.zeros(nrows * nb, dtype=torch.int32, device=cuda)
+    moe.block_ints(t, rows.reshape(-1).to(cuda), rb, nrows, torch.from_numpy(xq).to(cuda), n, si, sm)
+    _sync()
+    assert_bits_equal(si.cpu().numpy().reshape(nrows, nb), ref_si, f"sumi {t.name}")
+    assert_bits_equal(sm.cpu().numpy().reshape(nrows, nb), ref_sm, f"summ {t.name}")
+
+
+# ------------------------------------------------------------------ A1-A3: router and bucketing
+
+@pytest.mark.parametrize("rows,kdim,nt", [(128, 2048, 1), (129, 2048, 3), (288, 4096, 4), (128, 2048, 37)])
+def test_router_gemv_bitexact(cuda, rows, kdim, nt):
+    g = gen(41)
+    W = torch.randn(rows, kdim, generator=g) * 0.02
+    x = torch.randn(nt, kdim, generator=g)
+    bias = torch.randn(nt, rows, generator=g)
+    ref = orc.gemv_f32(W.numpy(), x.numpy())
+    y = torch.zeros(nt, rows, device=cuda)
+    moe.gemv_f32(W.to(cuda), rows, kdim, x.to(cuda), kdim, y, rows, nt)
+    yb = torch.zeros(nt, rows, device=cuda)
+    moe.gemv_f32(W.to(cuda), rows, kdim, x.to(cuda), kdim, yb, rows, nt, bias=bias.to(cuda), bias_stride=rows)
+    _sync()
+    assert_bits_equal(y.cpu().numpy(), ref, "logits")
+    assert_bits_equal(yb.cpu().numpy(), (ref + bias.numpy()).astype(np.float32), "logits + bias")
+
+
+@pytest.mark.parametrize("E,k,nt", [(128, 8, 7), (288, 8, 5), (384, 6, 9), (512, 10, 33), (1000, 14, 3), (64, 64, 2)])
+def test_route_bitexact(cuda, E, k, nt):
+    g = gen(51 + E)
+    logits = torch.randn(nt, E + 1, generator=g) * 2
+    logits[0, :E] = 0.25                  # all equal: ids 0..k-1 (tools/routebench.cu:20 tie test)
+    if nt > 1:
+        logits[1, 5] = logits[1, 9]       # an exact tie between two experts
+    ids_r, wts_r, sg_r = orc.route(logits.numpy(), E, k, with_sg=True)
+    ids = torch.zeros(nt * k, dtype=torch.int32, device=cuda)
+    wts = torch.zeros(nt * k, device=cuda)
+    sg = torch.zeros(nt, device=cuda)
+    moe.moe_route(logits.to(cuda), E + 1, E, k, ids, wts, sg, nt)
+    _sync()
+    assert_bits_equal(ids.cpu().numpy().reshape(nt, k), ids_r, "ids")
+    assert_bits_equal(wts.cpu().numpy().reshape(nt, k), wts_r, "wts")
+    assert_bits_equal(sg.cpu().numpy(), sg_r, "sg")
+    assert list(ids_r[0]) == list(range(k))
+
+
+@pytest.mark.parametrize("E,P,absent", [(128, 4096, 0), (512, 20480, 0), (288, 32, 5), (1024, 3000, 100), (16, 0, 0), (8, 333, 3)])
+def test_order_bitexact(cuda, E, P, absent):
+    rng = np.random.default_rng(E + P)
+    slot = np.arange(E, dtype=np.int32)
+    if absent:
+        slot[rng.choice(E, absent, replace=False)] = -1
+    ids = rng.integers(-2, E + 2, P).astype(np.int32)   # includes out-of-range ids (skipped)
+    o_r, on_r, eg_r = orc.order(slot, ids, E)
+    dev = moe.MoeDev.__new__(moe.MoeDev)
+    from hyper_amd import hy_moe_dev
+    import ctypes
+    sl = torch.from_numpy(slot).to(cuda)
+    c = hy_moe_dev(); c.slot = sl.data_ptr(); c.n_expert = E
+    dev.c, dev.ref, dev.slot = c, ctypes.byref(c), sl
+    order = torch.full((max(P, 1),), -7, dtype=torch.int32, device=cuda)
+    order_n = torch.zeros(2, dtype=torch.int32, device=cuda)
+    egrp = torch.zeros(3 * E, dtype=torch.int32, device=cuda)
+    moe.moe_order(dev, torch.from_numpy(ids).to(cuda) if P else order, P, E, order, order_n, egrp=egrp)
+    _sync()
+    on = order_n.cpu().numpy()
+    assert_bits_equal(on, on_r, "order_n")
+    assert_bits_equal(order.cpu().numpy()[:on[0]], o_r, "order")
+    assert_bits_equal(egrp.cpu().numpy()[:3 * on[1]].reshape(-1, 3), eg_r, "egrp")
+
+
+# ------------------------------------------------------------------ A5/A6/A9: decode GEMVs + combine
+
+DECODE_CASES = [
+    (GType.Q4_K, GType.Q4_K, 2048, 768, 8, 1),
+    (GType.Q4_K, GType.Q6_K, 2048, 768, 8, 3),
+    (GType.Q5_K, GType.Q6_K, 2048, 512, 10, 2),
+    (GType.IQ4_NL, GType.IQ4_NL, 4096, 1536, 8, 1),
+    (GType.IQ4_XS, GType.IQ4_XS, 4096, 1536, 8, 4),
+    (GType.IQ2_XS, GType.IQ2_XS, 7168, 2048, 6, 2),
+]
+
+
+@pytest.mark.parametrize("tg,td,d,ff,k,nt", DECODE_CASES)
+def test_decode_gemv_bitexact(cuda, tg, td, d, ff, k, nt):
+    E = 12
+    L = layer(tg, td, E, ff, d, seed=61 + int(tg), clamp=0.0)
+    OL = oracle_layer(L)
+    ids, wts = routing(nt, E, k, seed=62)
+    x = torch.randn(nt, d, generator=gen(63))
+    out_r, h_r, y_r = orc.moe_layer(OL, x.numpy(), ids, wts, want_hy=True)
+    dev = moe.upload_experts(L, device=cuda)
+    xd, idsd, wtsd = x.to(cuda), torch.from_numpy(ids).reshape(-1).to(cuda), torch.from_numpy(wts).reshape(-1).to(cuda)
+    h = torch.zeros(nt * k, ff, device=cuda)
+    y = torch.zeros(nt * k, d, device=cuda)
+    out = torch.zeros(nt, d, device=cuda)
+    out2 = torch.zeros(nt, d, device=cuda)
+    moe.moe_gate_up(dev, xd, d, idsd, k, h, nt)
+    moe.moe_down(dev, h, idsd, wtsd, k, y, nt)
+    moe.moe_reduce(None, None, y, k, out, d, nt, idsd)
+    moe.moe_down_reduce(dev, h, idsd, wtsd, k, None, None, out2, nt)
+    _sync()
+    assert_bits_equal(h.cpu().numpy(), h_r, "h")
+    assert_bits_equal(y.cpu().numpy(), (wts.reshape(-1, 1) * y_r).astype(np.float32), "y = w * down . q8(h)")
+    assert_bits_equal(out.cpu().numpy(), out_r, "out (reduce)")
+    assert_bits_equal(out2.cpu().numpy(), out_r, "out (fused down + reduce)")
+    assert rel_l2(out.cpu().numpy(), out_r) <= TOL
+
+
+def test_decode_clamp_and_order(cuda):
+    """SwiGLU limit (src/cpu_moe.cpp:891-892) and the ordered pair list (skips non-local experts)."""
+    tg = td = GType.Q4_K
+    E, d, ff, k, nt = 10, 2048, 512, 4, 3
+    L = layer(tg, td, E, ff, d, seed=71, clamp=3.0)
+    OL = oracle_layer(L)
+    ids, wts = routing(nt, E, k, seed=72)
+    x = torch.randn(nt, d, generator=gen(73)) * 3
+    _, h_r, y_r = orc.moe_layer(OL, x.numpy(), ids, wts, want_hy=True)
+    dev = moe.upload_experts(L, device=cuda)
+    idsd, wtsd = torch.from_numpy(ids).reshape(-1).to(cuda), torch.from_numpy(wts).reshape(-1).to(cuda)
+    order = torch.zeros(nt * k, dtype=torch.int32, device=cuda)
+    order_n = torch.zeros(2, dtype=torch.int32, device=cuda)
+    moe.moe_order(dev, idsd, nt * k, E, order, order_n)
+    h = torch.full((nt * k, ff), float("nan"), device=cuda)
+    y = torch.full((nt * k, d), float("nan"), device=cuda)
+    moe.moe_gate_up(dev, x.to(cuda), d, idsd, k, h, nt, order=order, order_n=order_n)
+    moe.moe_down(dev, h, idsd, wtsd, k, y, nt, order=order, order_n=order_n)
+    _sync()
+    assert_bits_equal(h.cpu().numpy(), h_r, "h (clamped)")
+    assert_bits_equal(y.cpu().numpy(), (wts.reshape(-1, 1) * y_r).astype(np.float32), "y")
+
+
+# ------------------------------------------------------------------ A7/A8: grouped GEMMs
+
+GEMM_CASES = [
+    (GType.Q4_K, GType.Q6_K, 2048, 768, 8, 40),
+    (GType.Q4_K, GType.Q4_K, 2048, 768, 8, 70),
+    (GType.Q5_K, GType.Q6_K, 2048, 512, 10, 33),
+    (GType.IQ4_XS, GType.IQ4_XS, 4096, 1536, 8, 4),
+    (GType.IQ2_XS, GType.IQ2_XS, 7168, 2048, 6, 8),
+]
+
+
+@pytest.mark.parametrize("tg,td,d,ff,k,nt", GEMM_CASES)
+def test_grouped_gemm_bitexact(cuda, tg, td, d, ff, k, nt):
+    E = 16
+    L = layer(tg, td, E, ff, d, seed=81 + int(tg))
+    OL = oracle_layer(L)
+    ids, wts = routing(nt, E, k, seed=82, zipf=1.1)
+    x = torch.randn(nt, d, generator=gen(83))
+    out_r, h_r, y_r = orc.moe_layer(OL, x.numpy(), ids, wts, want_hy=True)
+    dev = moe.upload_experts(L, device=cuda)
+    P = nt * k
+    idsd, wtsd = torch.from_numpy(ids).reshape(-1).to(cuda), torch.from_numpy(wts).reshape(-1).to(cuda)
+    order = torch.zeros(P, dtype=torch.int32, device=cuda)
+    order_n = torch.zeros(2, dtype=torch.int32, device=cuda)
+    egrp = torch.zeros(3 * E, dtype=torch.int32, device=cuda)
+    moe.moe_order(dev, idsd, P, E, order, order_n, egrp=egrp)
+    xq = torch.zeros(nt * q8_row_bytes(vec_dot_type(tg), d), dtype=torch.uint8, device=cuda)
+    moe.q8_quantize(vec_dot_type(tg), x.to(cuda), d, d, nt, xq)
+    h = torch.full((P, ff), float("nan"), device=cuda)
+    moe.moe_gemm_gate_up(dev, xq, k, order, order_n, egrp, E, h)
+    hq = torch.zeros(P * q8_row_bytes(vec_dot_type(td), ff), dtype=torch.uint8, device=cuda)
+    moe.q8_quantize(vec_dot_type(td), h, ff, ff, P, hq)
+    y = torch.full((P, d), float("nan"), device=cuda)
+    moe.moe_gemm_down(dev, hq, order, order_n, egrp, E, wtsd, y)
+    out = torch.zeros(nt, d, device=cuda)
+    moe.moe_reduce(None, None, y, k, out, d, nt, idsd)
+    _sync()
+    assert_bits_equal(h.cpu().numpy(), h_r, "h (grouped gate/up)")
+    assert_bits_equal(y.cpu().numpy(), (wts.reshape(-1, 1) * y_r).astype(np.float32), "y (grouped down)")
+    assert_bits_equal(out.cpu().numpy(), out_r, "out")
+    assert rel_l2(out.cpu().numpy(), out_r) <= TOL
