@@ -116,8 +116,8 @@ def prefill_bench(args, dev, stream):
     gu_fns, dn_fns = [], []
     for c, i in steps[: 2 * args.copies]:
         r = runners[c]
-        gu_fns.append(lambda r=r: moe.moe_gemm_gate_up(r.dev, r.xq, k, r.order, r.order_n, r.egrp, min(E, T * k), r.h))
-        dn_fns.append(lambda r=r: moe.moe_gemm_down(r.dev, r.hq, r.order, r.order_n, r.egrp, min(E, T * k), r.wts, r.y))
+        gu_fns.append(lambda r=r: moe.moe_gemm_gate_up(r.dev, r.xq, k, T * k, r.order, r.order_n, r.egrp, min(E, T * k), r.h))
+        dn_fns.append(lambda r=r: moe.moe_gemm_down(r.dev, r.hq, T * k, r.order, r.order_n, r.egrp, min(E, T * k), r.wts, r.y))
     with torch.cuda.stream(stream):
         for c in range(args.copies):
             runners[c].prefill(xs[c % n_in], biases[c % n_in])

@@ -59,8 +59,8 @@ SIGNATURES = {
     "hy_q8_quantize": (_I, [_I, _P, _I, _I, _I, _P, _P]),
     "hy_moe_gate_up": (_I, [_DEV, _P, _I, _P, _I, _P, _I, _P, _P, _P]),
     "hy_moe_down": (_I, [_DEV, _P, _P, _P, _I, _P, _I, _P, _P, _P]),
-    "hy_moe_gemm_gate_up": (_I, [_DEV, _P, _I, _P, _P, _P, _I, _P, _P]),
-    "hy_moe_gemm_down": (_I, [_DEV, _P, _P, _P, _P, _I, _P, _P, _P]),
+    "hy_moe_gemm_gate_up": (_I, [_DEV, _P, _I, _I, _P, _P, _P, _I, _P, _P]),
+    "hy_moe_gemm_down": (_I, [_DEV, _P, _I, _P, _P, _P, _I, _P, _P, _P]),
     "hy_moe_reduce": (_I, [_P, _P, _P, _I, _P, _I, _I, _P, _P]),
     "hy_moe_down_reduce": (_I, [_DEV, _P, _P, _P, _I, _P, _P, _P, _I, _P]),
     "hy_dequant_row": (_I, [_I, _P, _I, _P, _P]),

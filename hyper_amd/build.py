@@ -7,6 +7,7 @@ Flags every HIP source is compiled with:
                                               source calls fmaf (the numeric contract with the CPU oracle)
   -fhip-fp32-correctly-rounded-divide-sqrt    IEEE division (the quantizers' -127/max, 1/iscale, softmax)
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed-fp32 VALU instructions
+  -mllvm -amdgpu-mfma-vgpr-form               MFMA results in VGPRs (the integer scaling reads them next)
 """
 import os
 import shutil
@@ -25,6 +26,7 @@ ARCH = os.environ.get("HYMOE_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-mllvm", "-amdgpu-mfma-vgpr-form",
          "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-I", str(PKG.parent / "include")]
 
 

@@ -36,11 +36,8 @@ __device__ __forceinline__ uint32_t apply_sign(uint32_t g, uint32_t b4) {
     const uint32_t one = spread4(b4);
     return (g ^ (one * 0xFFu)) + one;
 }
-// Q6_K: q6 bytes (0..63) -> q6 - 32 as int8
-__device__ __forceinline__ uint32_t q6_signed(uint32_t q) {
-    const uint32_t v = q ^ 0x20202020u, s = v & 0x20202020u;
-    return v | (s << 1) | (s << 2);
-}
+// Q6_K: q6 bytes (0..63) -> q6 - 32 as int8: per byte (q + 96) ^ 128 = q - 32 mod 256 (q + 96 < 256: no carry)
+__device__ __forceinline__ uint32_t q6_signed(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
 
 // ---------------------------------------------------------------- decode-GEMV items (8 lanes)
 template <int T> struct Item;

@@ -161,24 +161,26 @@ int hy_moe_down(const hy_moe_dev *m, const float *h, const int32_t *ids, const f
     return launch_down(*m, h, ids, wts, k, y, nt, s, order, order_n);
 }
 
-int hy_moe_gemm_gate_up(const hy_moe_dev *m, const void *xq, int k, const int32_t *order, const int32_t *order_n, const int32_t *egrp,
-                        int max_active, float *h, hipStream_t s) {
+int hy_moe_gemm_gate_up(const hy_moe_dev *m, const void *xq, int k, int n_pairs, const int32_t *order, const int32_t *order_n,
+                        const int32_t *egrp, int max_active, float *h, hipStream_t s) {
     int rc = check_dev(m, "hy_moe_gemm_gate_up", true, false);
     if (rc) return rc;
     if (!gemm_type(m->tg)) { set_error("hy_moe_gemm_gate_up: no grouped GEMM for type %d", m->tg); return HY_EUNSUPPORTED_TYPE; }
-    if (!xq || !order || !order_n || !egrp || !h || k <= 0 || max_active < 0) { set_error("hy_moe_gemm_gate_up: bad argument"); return HY_EINVAL; }
+    if (!xq || !order || !order_n || !egrp || !h || k <= 0 || max_active < 0 || n_pairs < 0) { set_error("hy_moe_gemm_gate_up: bad argument"); return HY_EINVAL; }
     if ((uintptr_t) xq & 3) { set_error("hy_moe_gemm_gate_up: xq must be 4-byte aligned"); return HY_EBAD_SHAPE; }
-    return launch_gemm_gate_up(*m, xq, k, order, order_n, egrp, max_active, h, s);
+    if (max_active > 1024 || max_active > m->n_expert) { set_error("hy_moe_gemm_gate_up: max_active %d > experts", max_active); return HY_EBAD_SHAPE; }
+    return launch_gemm_gate_up(*m, xq, k, n_pairs, order, order_n, egrp, max_active, h, s);
 }
 
-int hy_moe_gemm_down(const hy_moe_dev *m, const void *hq, const int32_t *order, const int32_t *order_n, const int32_t *egrp, int max_active,
-                     const float *wts, float *y, hipStream_t s) {
+int hy_moe_gemm_down(const hy_moe_dev *m, const void *hq, int n_pairs, const int32_t *order, const int32_t *order_n, const int32_t *egrp,
+                     int max_active, const float *wts, float *y, hipStream_t s) {
     int rc = check_dev(m, "hy_moe_gemm_down", false, true);
     if (rc) return rc;
     if (!gemm_type(m->td)) { set_error("hy_moe_gemm_down: no grouped GEMM for type %d", m->td); return HY_EUNSUPPORTED_TYPE; }
-    if (!hq || !order || !order_n || !egrp || !wts || !y || max_active < 0) { set_error("hy_moe_gemm_down: bad argument"); return HY_EINVAL; }
+    if (!hq || !order || !order_n || !egrp || !wts || !y || max_active < 0 || n_pairs < 0) { set_error("hy_moe_gemm_down: bad argument"); return HY_EINVAL; }
     if ((uintptr_t) hq & 3) { set_error("hy_moe_gemm_down: hq must be 4-byte aligned"); return HY_EBAD_SHAPE; }
-    return launch_gemm_down(*m, hq, order, order_n, egrp, max_active, wts, y, s);
+    if (max_active > 1024 || max_active > m->n_expert) { set_error("hy_moe_gemm_down: max_active %d > experts", max_active); return HY_EBAD_SHAPE; }
+    return launch_gemm_down(*m, hq, n_pairs, order, order_n, egrp, max_active, wts, y, s);
 }
 
 int hy_moe_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int32_t *ids, hipStream_t s) {

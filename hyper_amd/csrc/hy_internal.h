@@ -21,9 +21,9 @@ int launch_down(const hy_moe_dev &m, const float *h, const int *ids, const float
 int launch_down_reduce(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp, const float *sg,
                        float *out, int nt, hipStream_t s);
 int launch_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int *ids, hipStream_t s);
-int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, const int *order, const int *order_n, const int *egrp, int max_active,
-                        float *h, hipStream_t s);
-int launch_gemm_down(const hy_moe_dev &m, const void *hq, const int *order, const int *order_n, const int *egrp, int max_active,
+int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs, const int *order, const int *order_n, const int *egrp,
+                        int max_active, float *h, hipStream_t s);
+int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int *order, const int *order_n, const int *egrp, int max_active,
                      const float *wts, float *y, hipStream_t s);
 int launch_dequant_row(int type, const uint8_t *row, int n, float *out, hipStream_t s);
 int launch_block_ints(int type, const uint8_t *rows, size_t row_bytes, int nrows, const void *xq, int n, int *sumi, int *summ,

@@ -110,12 +110,12 @@ def moe_down(m: MoeDev, h, ids, wts, k, y, nt, stream=None, order=None, order_n=
     check(lib().hy_moe_down(m.ref, _p(h), _p(ids), _p(wts), k, _p(y), nt, _s(stream), _p(order), _p(order_n)))
 
 
-def moe_gemm_gate_up(m: MoeDev, xq, k, order, order_n, egrp, max_active, h, stream=None):
-    check(lib().hy_moe_gemm_gate_up(m.ref, _p(xq), k, _p(order), _p(order_n), _p(egrp), max_active, _p(h), _s(stream)))
+def moe_gemm_gate_up(m: MoeDev, xq, k, n_pairs, order, order_n, egrp, max_active, h, stream=None):
+    check(lib().hy_moe_gemm_gate_up(m.ref, _p(xq), k, n_pairs, _p(order), _p(order_n), _p(egrp), max_active, _p(h), _s(stream)))
 
 
-def moe_gemm_down(m: MoeDev, hq, order, order_n, egrp, max_active, wts, y, stream=None):
-    check(lib().hy_moe_gemm_down(m.ref, _p(hq), _p(order), _p(order_n), _p(egrp), max_active, _p(wts), _p(y), _s(stream)))
+def moe_gemm_down(m: MoeDev, hq, n_pairs, order, order_n, egrp, max_active, wts, y, stream=None):
+    check(lib().hy_moe_gemm_down(m.ref, _p(hq), n_pairs, _p(order), _p(order_n), _p(egrp), max_active, _p(wts), _p(y), _s(stream)))
 
 
 def moe_reduce(shexp, sg, y, k, out, n, nt, ids, stream=None):
@@ -196,9 +196,9 @@ class MoeLayerRunner:
         self.sh_order_n[0] = nt
         self.sh_egrp[2] = nt
         q8_quantize(vec_dot_type(S.tg), x, x.stride(0), self.d, nt, self.sh_xq, stream)
-        moe_gemm_gate_up(S, self.sh_xq, 1, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_h, stream)
+        moe_gemm_gate_up(S, self.sh_xq, 1, nt, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_h, stream)
         q8_quantize(vec_dot_type(S.td), self.sh_h, S.layer.ff, S.layer.ff, nt, self.sh_hq, stream)
-        moe_gemm_down(S, self.sh_hq, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_ones, self.sh_y, stream)
+        moe_gemm_down(S, self.sh_hq, nt, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_ones, self.sh_y, stream)
 
     def decode(self, x: torch.Tensor, bias=None, stream=None) -> torch.Tensor:
         nt = x.shape[0]
@@ -218,9 +218,9 @@ class MoeLayerRunner:
         moe_order(self.dev, self.ids, P, self.E, self.order, self.order_n, stream, self.egrp)
         q8_quantize(self.vg, x, x.stride(0), self.d, nt, self.xq, stream)
         max_active = min(self.E, P)
-        moe_gemm_gate_up(self.dev, self.xq, k, self.order, self.order_n, self.egrp, max_active, self.h, stream)
+        moe_gemm_gate_up(self.dev, self.xq, k, P, self.order, self.order_n, self.egrp, max_active, self.h, stream)
         q8_quantize(self.vd, self.h, self.ff, self.ff, P, self.hq, stream)
-        moe_gemm_down(self.dev, self.hq, self.order, self.order_n, self.egrp, max_active, self.wts, self.y, stream)
+        moe_gemm_down(self.dev, self.hq, P, self.order, self.order_n, self.egrp, max_active, self.wts, self.y, stream)
         shexp = None
         if self.shared is not None:
             self._shared_prefill(x, nt, stream)

@@ -113,10 +113,11 @@ int hy_moe_down(const hy_moe_dev *m, const float *h, const int32_t *ids, const f
 /* Prefill / verify grouped GEMMs over bucketed pairs (replace moe_gemm_gate_up / moe_gemm_down,
    src/kernels4.cuh:77-80 / src/kernels4.cu:2063-2093).  xq: Q8 rows of the tokens (pair p reads row p / k);
    h [n_pairs][ff] fp32; hq: Q8 rows of h per pair; y[p][r] = wts[p] * (down_e[r] . hq[p]).
-   grid: max_active >= order_n[1] expert blocks. */
-int hy_moe_gemm_gate_up(const hy_moe_dev *m, const void *xq, int k, const int32_t *order, const int32_t *order_n,
+   n_pairs (not in the reference: its grid was one block per active expert) bounds the work items, chunks of
+   up to 32 tokens of one expert; max_active >= order_n[1] (<= 1024). */
+int hy_moe_gemm_gate_up(const hy_moe_dev *m, const void *xq, int k, int n_pairs, const int32_t *order, const int32_t *order_n,
                         const int32_t *egrp, int max_active, float *h, hipStream_t s);
-int hy_moe_gemm_down(const hy_moe_dev *m, const void *hq, const int32_t *order, const int32_t *order_n, const int32_t *egrp,
+int hy_moe_gemm_down(const hy_moe_dev *m, const void *hq, int n_pairs, const int32_t *order, const int32_t *order_n, const int32_t *egrp,
                      int max_active, const float *wts, float *y, hipStream_t s);
 
 /* Combine: out[t][r] = sg[t] * shexp[t][r] (when shexp; sg NULL: 1) + the pairs' y[t*k + j][r] added in ascending

@@ -224,11 +224,11 @@ def test_grouped_gemm_bitexact(cuda, tg, td, d, ff, k, nt):
     xq = torch.zeros(nt * q8_row_bytes(vec_dot_type(tg), d), dtype=torch.uint8, device=cuda)
     moe.q8_quantize(vec_dot_type(tg), x.to(cuda), d, d, nt, xq)
     h = torch.full((P, ff), float("nan"), device=cuda)
-    moe.moe_gemm_gate_up(dev, xq, k, order, order_n, egrp, E, h)
+    moe.moe_gemm_gate_up(dev, xq, k, P, order, order_n, egrp, E, h)
     hq = torch.zeros(P * q8_row_bytes(vec_dot_type(td), ff), dtype=torch.uint8, device=cuda)
     moe.q8_quantize(vec_dot_type(td), h, ff, ff, P, hq)
     y = torch.full((P, d), float("nan"), device=cuda)
-    moe.moe_gemm_down(dev, hq, order, order_n, egrp, E, wtsd, y)
+    moe.moe_gemm_down(dev, hq, P, order, order_n, egrp, E, wtsd, y)
     out = torch.zeros(nt, d, device=cuda)
     moe.moe_reduce(None, None, y, k, out, d, nt, idsd)
     _sync()
