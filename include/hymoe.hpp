@@ -1,0 +1,89 @@
+// C++ face of libhymoe with the reference's expert-compute signatures (hyper src/kernels4.cuh:45-91,
+// src/experts.h:20-50): the same function names, argument order and meaning, std::runtime_error on failure
+// (the reference throws at the same places, src/kernels4.cu:1926-1927, :1970, :2027-2030, :2066, :2081).
+// Header-only over include/hymoe.h; device pointers and the stream are the caller's.
+#pragma once
+#include "hymoe.h"
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace hymoe {
+
+using MoeDev = hy_moe_dev;                 // src/kernels4.cuh:56-63 (+ n_expert)
+
+inline void check(int rc) {
+    if (rc != HY_OK) throw std::runtime_error(std::string("hymoe: ") + hy_last_error());
+}
+
+// src/experts.h:20-26 -- one layer's GGUF expert tensors on the host
+struct ExpertTensors {
+    const uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
+    size_t gb = 0, db = 0;
+    int E = 0;
+    int tg = 0, td = 0;
+};
+// src/experts.h:50 -- the experts with slot[e] >= 0 copied to their device slots
+inline MoeDev upload_experts(const ExpertTensors &t, const std::vector<int> &slot, int ff, int n, float clamp) {
+    if ((int) slot.size() != t.E) throw std::runtime_error("upload_experts: slot table size != E");
+    hy_expert_tensors c{t.gate, t.up, t.down, t.gb, t.db, t.E, t.tg, t.td};
+    MoeDev m{};
+    check(hy_upload_experts(&c, slot.data(), ff, n, clamp, &m));
+    return m;
+}
+inline void free_experts(MoeDev &m) { check(hy_free_experts(&m)); }
+
+// src/kernels4.cuh:35
+inline void gemv_f32(const float *W, int rows, int k, const float *x, int xs, float *y, int ys, int nt, hipStream_t s,
+                     const float *bias = nullptr, int bias_stride = 0) {
+    check(hy_gemv_f32(W, rows, k, x, xs, y, ys, nt, bias, bias_stride, s));
+}
+// src/kernels4.cuh:48
+inline void moe_route(const float *logits, int ls, int n_expert, int k, int *ids, float *wts, float *sg, int nt, hipStream_t s) {
+    check(hy_moe_route(logits, ls, n_expert, k, ids, wts, sg, nt, s));
+}
+// src/kernels4.cuh:67-68
+inline void moe_gate_up(const MoeDev &m, const float *x, int xs, const int *ids, int k, float *h, int nt, hipStream_t s,
+                        const int *order = nullptr, const int *order_n = nullptr) {
+    check(hy_moe_gate_up(&m, x, xs, ids, k, h, nt, s, order, order_n));
+}
+// src/kernels4.cuh:70-71
+inline void moe_down(const MoeDev &m, const float *h, const int *ids, const float *wts, int k, float *y, int nt, hipStream_t s,
+                     const int *order = nullptr, const int *order_n = nullptr) {
+    check(hy_moe_down(&m, h, ids, wts, k, y, nt, s, order, order_n));
+}
+// src/kernels4.cuh:74-75
+inline void moe_order(const MoeDev &m, const int *ids, int n_pairs, int n_expert, int *order, int *order_n, hipStream_t s,
+                      int *egrp = nullptr) {
+    check(hy_moe_order(&m, ids, n_pairs, n_expert, order, order_n, s, egrp));
+}
+// activation quantizer: replaces to_half (src/kernels.cu:2235-2237) ahead of the grouped GEMMs
+inline void q8_quantize(int vtype, const float *x, int xs, int n, int nt, void *q, hipStream_t s) {
+    check(hy_q8_quantize(vtype, x, xs, n, nt, q, s));
+}
+// src/kernels4.cuh:77-80 (Q8 activations instead of fp16, fp32 hidden; n_pairs bounds the work items)
+inline void moe_gemm_gate_up(const MoeDev &m, const void *xq, int k, int n_pairs, const int *order, const int *order_n, const int *egrp,
+                             int max_active, float *h, hipStream_t s) {
+    check(hy_moe_gemm_gate_up(&m, xq, k, n_pairs, order, order_n, egrp, max_active, h, s));
+}
+inline void moe_gemm_down(const MoeDev &m, const void *hq, int n_pairs, const int *order, const int *order_n, const int *egrp,
+                          int max_active, const float *wts, float *y, hipStream_t s) {
+    check(hy_moe_gemm_down(&m, hq, n_pairs, order, order_n, egrp, max_active, wts, y, s));
+}
+// src/kernels4.cuh:88-91 (single device: no owner tables, no CPU hand-off)
+inline void moe_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int *ids,
+                       hipStream_t s) {
+    check(hy_moe_reduce(shexp, sg, y, k, out, n, nt, ids, s));
+}
+inline void moe_down_reduce(const MoeDev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp,
+                            const float *sg, float *out, int nt, hipStream_t s) {
+    check(hy_moe_down_reduce(&m, h, ids, wts, k, shexp, sg, out, nt, s));
+}
+// src/kernels4.cuh:181 test hook
+inline void deq_row_test(int type, const uint8_t *row, int n, float *out, hipStream_t s = nullptr) {
+    check(hy_dequant_row(type, row, n, out, s));
+}
+
+} // namespace hymoe

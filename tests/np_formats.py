@@ -1,0 +1,148 @@
+"""Independent numpy decoders of the GGUF block formats, written from the reference's deq8<T> layouts
+(src/kernels4.cu:421-714) in vectorised numpy -- a second implementation the C oracle is checked against.
+
+Each decoder returns the block's integer structure: quant values q [nb, 256 or 32] as the dot products use
+them (Q6_K: q6 - 32; IQ4: codebook values; IQ2_XS: signed grid values), the per-group integer scales
+(group size 32 or 16) and mins, and the fp16 scale fields as float32.
+"""
+import numpy as np
+
+KV_IQ4NL = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.int64)
+
+
+def f16(b2):
+    return np.ascontiguousarray(b2).view(np.float16).astype(np.float32).reshape(-1)
+
+
+def _scale_min_k4(s):      # s: [nb, 12] -> sc, m [nb, 8] (src/kernels4.cu:423-426)
+    s = s.astype(np.int64)
+    sc, m = np.zeros((s.shape[0], 8), np.int64), np.zeros((s.shape[0], 8), np.int64)
+    sc[:, :4] = s[:, 0:4] & 63
+    m[:, :4] = s[:, 4:8] & 63
+    sc[:, 4:] = (s[:, 8:12] & 0xF) | ((s[:, 0:4] >> 6) << 4)
+    m[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+    return sc, m
+
+
+def q4k(b):
+    b = b.reshape(-1, 144)
+    sc, m = _scale_min_k4(b[:, 4:16])
+    qs = b[:, 16:144].astype(np.int64).reshape(-1, 4, 32)          # 4 pairs of sub-blocks
+    q = np.stack([qs & 0xF, qs >> 4], axis=2).reshape(-1, 256)       # sub-block 2p: low, 2p+1: high
+    return dict(q=q, sc=sc, m=m, gsize=32, d=f16(b[:, 0:2]), dmin=f16(b[:, 2:4]))
+
+
+def q5k(b):
+    b = b.reshape(-1, 176)
+    sc, m = _scale_min_k4(b[:, 4:16])
+    qh = b[:, 16:48].astype(np.int64)                                 # [nb, 32]: bit j -> sub-block j
+    qs = b[:, 48:176].astype(np.int64).reshape(-1, 4, 32)
+    lo = np.stack([qs & 0xF, qs >> 4], axis=2).reshape(-1, 8, 32)
+    hb = np.stack([(qh >> j) & 1 for j in range(8)], axis=1)          # [nb, 8, 32]
+    q = (lo | (hb << 4)).reshape(-1, 256)
+    return dict(q=q, sc=sc, m=m, gsize=32, d=f16(b[:, 0:2]), dmin=f16(b[:, 2:4]))
+
+
+def q6k(b):
+    b = b.reshape(-1, 210)
+    ql = b[:, 0:128].astype(np.int64).reshape(-1, 2, 2, 32)           # [half][qt & 1][l]
+    qh = b[:, 128:192].astype(np.int64).reshape(-1, 2, 32)            # [half][l]
+    q = np.zeros((b.shape[0], 2, 4, 32), np.int64)                    # [half][qt][l]
+    for qt in range(4):
+        lo = (ql[:, :, qt & 1, :] >> (4 if qt >= 2 else 0)) & 0xF
+        q[:, :, qt, :] = lo | (((qh >> (2 * qt)) & 3) << 4)
+    q = q.reshape(-1, 256) - 32
+    sc = b[:, 192:208].view(np.int8).astype(np.int64)                  # group e // 16
+    return dict(q=q, sc=sc, m=None, gsize=16, d=f16(b[:, 208:210]))
+
+
+def iq4xs(b):
+    b = b.reshape(-1, 136)
+    sh = b[:, 2].astype(np.int64) | (b[:, 3].astype(np.int64) << 8)
+    sl = b[:, 4:8].astype(np.int64)
+    ls = np.stack([((sl[:, ib // 2] >> (4 * (ib % 2))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4) for ib in range(8)], axis=1)
+    qs = b[:, 8:136].astype(np.int64).reshape(-1, 8, 16)
+    idx = np.concatenate([qs & 0xF, qs >> 4], axis=2).reshape(-1, 256)
+    return dict(q=KV_IQ4NL[idx], sc=ls - 32, m=None, gsize=32, d=f16(b[:, 0:2]))
+
+
+def iq4nl(b):
+    b = b.reshape(-1, 18)
+    qs = b[:, 2:18].astype(np.int64)
+    idx = np.concatenate([qs & 0xF, qs >> 4], axis=1)
+    return dict(q=KV_IQ4NL[idx], sc=np.ones((b.shape[0], 1), np.int64), m=None, gsize=32, d=f16(b[:, 0:2]))
+
+
+def iq2xs(b, grid_rows, ksigns):
+    """grid_rows: [512, 8] codebook bytes, ksigns: [128] sign bytes."""
+    b = b.reshape(-1, 74)
+    qs = b[:, 2:66].copy().view(np.uint16).astype(np.int64).reshape(-1, 8, 4)     # [ib][l]
+    g = grid_rows[qs & 511].astype(np.int64)                                       # [nb, 8, 4, 8]
+    sgn = ksigns[qs >> 9].astype(np.int64)
+    bits = (sgn[..., None] >> np.arange(8)) & 1
+    q = np.where(bits == 1, -g, g).reshape(-1, 256)
+    s = b[:, 66:74].astype(np.int64)
+    sc = np.stack([s & 0xF, s >> 4], axis=2).reshape(-1, 16)                       # 16-groups
+    return dict(q=q, sc=2 * sc + 1, m=None, gsize=16, d=f16(b[:, 0:2]))
+
+
+def q8k(b):
+    b = b.reshape(-1, 292)
+    return dict(d=b[:, 0:4].copy().view(np.float32).reshape(-1), qs=b[:, 4:260].view(np.int8).astype(np.int64),
+                bsums=b[:, 260:292].copy().view(np.int16).astype(np.int64))
+
+
+def q8_0(b):
+    b = b.reshape(-1, 34)
+    return dict(d=f16(b[:, 0:2]), qs=b[:, 2:34].view(np.int8).astype(np.int64))
+
+
+def decode(t, b, grid_rows=None, ksigns=None):
+    t = int(t)
+    if t == 12: return q4k(b)
+    if t == 13: return q5k(b)
+    if t == 14: return q6k(b)
+    if t == 23: return iq4xs(b)
+    if t == 20: return iq4nl(b)
+    if t == 17: return iq2xs(b, grid_rows, ksigns)
+    raise ValueError(t)
+
+
+def dequant(t, b, grid_rows=None, ksigns=None):
+    """float32 values with the deq8 expression order (each product rounded on its own)."""
+    f = decode(t, b, grid_rows, ksigns)
+    q, gs = f["q"], f["gsize"]
+    n = q.shape[1]
+    sc = np.repeat(f["sc"], gs, axis=1)[:, :n].astype(np.float32)
+    d = f["d"][:, None]
+    t = int(t)
+    if t in (12, 13):
+        m = np.repeat(f["m"], gs, axis=1).astype(np.float32)
+        return ((d * sc) * q.astype(np.float32) - f["dmin"][:, None] * m).astype(np.float32)
+    if t == 14:
+        return ((d * sc) * q.astype(np.float32)).astype(np.float32)
+    if t == 23:
+        return ((d * sc) * q.astype(np.float32)).astype(np.float32)
+    if t == 20:
+        return (q.astype(np.float32) * d).astype(np.float32)
+    if t == 17:
+        db = (d * (np.float32(0.5) + ((sc - 1) / 2).astype(np.float32))) * np.float32(0.25)
+        return ((db * np.abs(q).astype(np.float32)) * np.where(q < 0, np.float32(-1), np.float32(1))).astype(np.float32)
+    raise ValueError(t)
+
+
+def block_ints(t, b, xq, grid_rows=None, ksigns=None):
+    """Brute-force integers per block: sumi = sum over groups of scale * sum(q * y), summ = sum_j m_j * sum(y_j)."""
+    f = decode(t, b, grid_rows, ksigns)
+    q, gs = f["q"], f["gsize"]
+    if int(t) == 20:
+        y = q8_0(xq)["qs"]
+    else:
+        y = q8k(xq)["qs"]
+    prod = (q * y).reshape(q.shape[0], -1, gs).sum(axis=2)            # per group
+    sumi = (prod * f["sc"]).sum(axis=1)
+    if f["m"] is not None:
+        summ = (f["m"] * y.reshape(y.shape[0], 8, 32).sum(axis=2)).sum(axis=1)
+    else:
+        summ = np.zeros_like(sumi)
+    return sumi, summ

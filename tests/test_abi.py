@@ -1,0 +1,71 @@
+"""The C-ABI library without a GPU: it loads, exports every entry point include/hymoe.h declares, the Python
+binding covers them all, answers the host-only queries, rejects bad arguments with the documented codes,
+and the C++ header compiles."""
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import hyper_amd
+from hyper_amd import HyError, check, lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared() -> set:
+    text = (ROOT / "include/hymoe.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(hy_[a-z0-9_]+)\s*\(", text))
+
+
+def test_exports_every_declared_symbol():
+    names = declared()
+    assert len(names) >= 18
+    L = lib()
+    for n in sorted(names):
+        assert hasattr(L, n), f"libhymoe.so does not export {n}"
+    assert names == set(hyper_amd.SIGNATURES), "Python signatures out of step with the header"
+
+
+def test_host_queries():
+    L = lib()
+    assert L.hy_abi_version() == 1
+    sizes = {12: (144, 256), 13: (176, 256), 14: (210, 256), 17: (74, 256), 20: (18, 32), 23: (136, 256), 8: (34, 32), 15: (292, 256)}
+    for t, (bb, be) in sizes.items():          # src/gguf.cpp:43-82
+        assert L.hy_block_bytes(t) == bb and L.hy_block_elems(t) == be
+    assert L.hy_vec_dot_type(20) == 8 and L.hy_vec_dot_type(12) == 15 and L.hy_vec_dot_type(2) == -1
+    assert L.hy_q8_row_bytes(15, 2048) == 8 * 292 and L.hy_q8_row_bytes(8, 4096) == 128 * 34 and L.hy_q8_row_bytes(15, 100) == 0
+
+
+def test_argument_errors_need_no_gpu():
+    """Validation happens before any HIP call: the codes and messages of the reference's throw sites."""
+    from hyper_amd import hy_moe_dev
+    L = lib()
+    p = ctypes.c_void_p(16)
+    assert L.hy_moe_route(None, 129, 128, 8, p, p, None, 1, None) == hyper_amd.HY_EINVAL
+    rc = L.hy_moe_route(p, 2000, 2000, 8, p, p, None, 1, None)
+    assert rc == hyper_amd.HY_EBAD_SHAPE and b"too many experts" in L.hy_last_error()
+    with pytest.raises(HyError):
+        check(L.hy_moe_route(p, 128, 128, 200, p, p, None, 1, None))
+    m = hy_moe_dev()
+    m.gate = m.up = m.down = m.slot = 16
+    m.tg, m.td, m.ff, m.n, m.n_expert = 2, 12, 768, 2048, 128       # Q4_0 gate: no kernels for it
+    rc = L.hy_moe_gate_up(ctypes.byref(m), p, 2048, p, 8, p, 1, None, None, None)
+    assert rc == hyper_amd.HY_EUNSUPPORTED_TYPE
+    m.tg, m.gate_bytes = 12, 1234                                   # wrong bytes per expert matrix
+    assert L.hy_moe_gate_up(ctypes.byref(m), p, 2048, p, 8, p, 1, None, None, None) == hyper_amd.HY_EBAD_SHAPE
+    assert L.hy_q8_quantize(15, p, 2048, 300, 1, p, None) == hyper_amd.HY_EBAD_SHAPE
+
+
+def test_cpp_header_compiles(tmp_path):
+    gxx = shutil.which("g++")
+    if not gxx or not Path("/opt/rocm/include/hip/hip_runtime_api.h").exists():
+        pytest.skip("g++ or the HIP headers are not installed")
+    src = tmp_path / "t.cpp"
+    src.write_text('#include "hymoe.hpp"\nint main() { hymoe::MoeDev m{}; (void) m; return hy_abi_version() == 1 ? 0 : 1; }\n')
+    r = subprocess.run([gxx, "-std=c++17", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}",
+                        "-I/opt/rocm/include", str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

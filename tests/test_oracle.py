@@ -1,0 +1,400 @@
+"""CPU tests that pin the oracle (oracle/moe_oracle.c) without a GPU.
+
+The reference ships no golden vectors for this path and its CPU dot products come from ggml, which is not
+vendored; the oracle is pinned instead by
+  - the reference's codebooks (digests in tests/golden/reference_tables.json, made from the reference sources),
+  - known-answer blocks built by hand from the layouts of the reference's deq8<T> (src/kernels4.cu:421-714),
+  - a second, independent numpy decoder of every format (tests/np_formats.py),
+  - brute-force integer dot products and an fp64 recomputation of the whole layer,
+  - the reference's quantizer-test distributions (tools/cpumoebench.cu:53-86) against numpy restatements of
+    ggml's scalar quantize_row_q8_K and x86 quantize_row_q8_0,
+  - closed forms and properties for exp, routing and bucketing.
+"""
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from hyper_amd.formats import GType, block_bytes, block_elems, random_blocks, row_bytes
+from tests import np_formats as nf
+from tests.helpers import D_RANGE, gen, layer, oracle_layer, routing, x_distributions
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+TABLES = json.loads((GOLDEN / "reference_tables.json").read_text())
+
+
+# ------------------------------------------------------------------ codebooks
+
+def iq2xs_rows() -> np.ndarray:
+    """The IQ2_XS codebook as the kernels and the oracle expand it from iq2xs_grid.inc."""
+    text = (Path(__file__).resolve().parents[1] / "hyper_amd/csrc/iq2xs_grid.inc").read_text()
+    body = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("//"))
+    codes = [int(v) for v in body.replace(",", " ").split() if v.isdigit()]
+    assert len(codes) == 512
+    lv = np.array([8, 25, 43], np.uint8)
+    rows = np.zeros((512, 8), np.uint8)
+    for i, c in enumerate(codes):
+        for j in range(8):
+            rows[i, j] = lv[c % 3]
+            c //= 3
+    return rows
+
+
+def ksigns() -> np.ndarray:
+    return np.array([i | ((bin(i).count("1") & 1) << 7) for i in range(128)], np.uint8)
+
+
+def test_codebooks_match_reference():
+    rows = iq2xs_rows()
+    assert hashlib.sha256(rows.tobytes()).hexdigest() == TABLES["iq2xs_grid_sha256"]
+    assert hashlib.sha256(ksigns().tobytes()).hexdigest() == TABLES["ksigns_sha256"]
+    assert hashlib.sha256(nf.KV_IQ4NL.astype(np.int8).tobytes()).hexdigest() == TABLES["iq4nl_sha256"]
+    assert all(bin(int(s)).count("1") % 2 == 0 for s in ksigns())   # every sign byte has an even bit count
+
+
+# ------------------------------------------------------------------ scalar helpers
+
+def test_expf_accuracy_and_special_values():
+    x = np.concatenate([np.linspace(-87.0, 88.7, 200001, dtype=np.float32),
+                        np.float32([0.0, -0.0, 1e-30, -1e-30, 0.5, -0.5, 1.0, 10.0, -10.0])])
+    got = np.array([orc.expf(v) for v in x[::7]], np.float64)
+    ref = np.exp(x[::7].astype(np.float64))
+    ulp = np.abs(got - ref) / np.spacing(np.float32(ref).astype(np.float32)).astype(np.float64)
+    assert ulp.max() <= 2.0, f"max {ulp.max()} ulp"
+    assert orc.expf(0.0) == 1.0
+    assert orc.expf(-87.5) == 0.0 and orc.expf(-1e30) == 0.0             # below exp(-87): flushed, no subnormals
+    assert np.isinf(orc.expf(88.8)) and np.isnan(orc.expf(float("nan")))
+    assert orc.expf(-87.0) >= np.finfo(np.float32).tiny                  # the smallest non-zero result is normal
+    for v in (-30.0, -1.5, 0.0, 2.0, 40.0):                               # silu(x) = x / (1 + exp(-x))
+        assert orc.silu(v) == np.float32(np.float32(v) / (np.float32(1.0) + np.float32(orc.expf(-v))))
+
+
+def test_fp16_conversions_match_numpy():
+    allh = np.arange(65536, dtype=np.uint16)
+    ref = allh.view(np.float16).astype(np.float32)
+    got = np.array([orc.lib().or_fp16_to_fp32(int(h)) for h in allh[::3]], np.float32)
+    ok = (got == ref[::3]) | (np.isnan(got) & np.isnan(ref[::3]))
+    assert ok.all()
+    rng = np.random.default_rng(3)
+    f = np.concatenate([rng.standard_normal(3000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, 3000),
+                        np.float32([65504.0, 65520.0, 65519.99, 6.1e-5, 5.96e-8, 2.98e-8, 1e-9, -0.0, np.inf])])
+    got = np.array([orc.lib().or_fp32_to_fp16(float(v)) for v in f], np.uint16)
+    with np.errstate(over="ignore"):
+        assert (got == f.astype(np.float16).view(np.uint16)).all()
+
+
+# ------------------------------------------------------------------ activation quantizers
+
+def np_quantize_q8_K(x: np.ndarray) -> np.ndarray:
+    """ggml's quantize_row_q8_K (scalar reference) in float32 numpy: first-occurrence signed max,
+    iscale = -127/max, nearest_int(iscale * x) by the 1.5 * 2^23 trick, min(127, .), int16 sums of 16."""
+    out = np.zeros((x.size // 256, 292), np.uint8)
+    for i, blk in enumerate(x.astype(np.float32).reshape(-1, 256)):
+        ax = np.abs(blk)
+        amax = ax.max()
+        if amax == 0:
+            continue
+        mx = blk[int(np.argmax(ax))]                          # argmax returns the first occurrence
+        iscale = np.float32(-127.0) / mx
+        v = (iscale * blk).astype(np.float32) + np.float32(12582912.0)
+        q = (v.view(np.int32) & 0x007FFFFF) - 0x00400000
+        q = np.minimum(q, 127).astype(np.int8)
+        out[i, 0:4] = np.frombuffer(np.float32(np.float32(1.0) / iscale).tobytes(), np.uint8)
+        out[i, 4:260] = q.view(np.uint8)
+        out[i, 260:292] = q.astype(np.int16).reshape(16, 16).sum(axis=1).astype(np.int16).view(np.uint8)
+    return out
+
+
+def np_quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    """ggml's x86 quantize_row_q8_0 in float32 numpy: d = amax/127 (fp16), id = 127/amax, round-half-even."""
+    out = np.zeros((x.size // 32, 34), np.uint8)
+    for i, blk in enumerate(x.astype(np.float32).reshape(-1, 32)):
+        amax = np.abs(blk).max()
+        d = np.float32(amax / np.float32(127.0))
+        idv = np.float32(np.float32(127.0) / amax) if amax != 0 else np.float32(0.0)
+        out[i, 0:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+        out[i, 2:34] = np.rint((blk * idv).astype(np.float32)).astype(np.int8).view(np.uint8)
+    return out
+
+
+@pytest.mark.parametrize("name", ["normal", "heavy", "ties", "sparse", "zero_block", "neg_max"])
+def test_q8k_matches_ggml_scalar_restatement(name):
+    x = x_distributions(4096, seed=17)[name]
+    got = orc.quantize(GType.Q8_K, x.reshape(2, 2048)).reshape(-1, 292)
+    assert (got == np_quantize_q8_K(x)).all()
+
+
+@pytest.mark.parametrize("name", ["normal", "heavy", "ties", "sparse", "zero_block"])
+def test_q8_0_matches_ggml_x86_restatement(name):
+    x = x_distributions(4096, seed=19)[name]
+    got = orc.quantize(GType.Q8_0, x.reshape(2, 2048)).reshape(-1, 34)
+    assert (got == np_quantize_q8_0(x)).all()
+
+
+def test_q8k_known_answers():
+    x = np.zeros(512, np.float32)
+    # block 0: max -127 at index 3 -> iscale = 1, q = round-half-even(x)
+    x[:8] = [2.5, 3.5, -0.5, -127.0, 1.5, -2.5, 0.49999997, 126.5]
+    # block 1: |x| equal at 10 (positive, first) and 20 (negative): max = +5, iscale = -25.4
+    x[256 + 10], x[256 + 20], x[256 + 30] = 5.0, -5.0, 0.1
+    q = orc.quantize(GType.Q8_K, x).reshape(2, 292)
+    d0, qs0 = q[0, 0:4].view(np.float32)[0], q[0, 4:260].view(np.int8)
+    assert d0 == 1.0
+    assert list(qs0[:8]) == [2, 4, 0, -127, 2, -2, 0, 126]
+    assert (q[0, 260:292].view(np.int16) == qs0.astype(np.int16).reshape(16, 16).sum(1)).all()
+    d1, qs1 = q[1, 0:4].view(np.float32)[0], q[1, 4:260].view(np.int8)
+    assert qs1[10] == -127 and qs1[20] == 127 and qs1[30] == -3      # -25.4 * 0.1 = -2.54 -> -3
+    assert d1 == np.float32(1.0) / (np.float32(-127.0) / np.float32(5.0))
+    z = orc.quantize(GType.Q8_K, np.zeros(256, np.float32))          # all zero: d = 0, qs = 0, bsums = 0
+    assert not z.any()
+
+
+# ------------------------------------------------------------------ block decoding
+
+ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ4_NL]
+
+
+def blocks(t, nb, seed):
+    return random_blocks(t, nb, gen(seed), "cpu", D_RANGE.get(GType(t), (1e-3, 1e-2))).numpy()
+
+
+@pytest.mark.parametrize("t", ALL)
+def test_dequant_matches_numpy_decoder(t):
+    b = blocks(t, 64, 100 + int(t))
+    n = 64 * block_elems(t)
+    got = orc.dequant_row(t, b.reshape(-1), n)
+    ref = nf.dequant(t, b, iq2xs_rows(), ksigns()).reshape(-1)
+    assert (got == ref).all(), f"{int((got != ref).sum())} values differ"
+
+
+def _f16b(v):
+    return list(np.frombuffer(np.float16(v).tobytes(), np.uint8))
+
+
+def test_q4k_known_answer_positions():
+    """d = 1, dmin = 0, every sub-block scale 1: value e must be the nibble placed for element e by the
+    reference's layout (byte 16 + 32 (j/2) + l, low nibble for even sub-block j; src/kernels4.cu:427-436)."""
+    want = np.array([(7 * e + e // 32) % 16 for e in range(256)], np.int64)
+    blk = np.zeros(144, np.uint8)
+    blk[0:2], blk[2:4] = _f16b(1.0), _f16b(0.0)
+    blk[4:16] = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]              # sc = 1, m = 0 for all eight sub-blocks
+    for e in range(256):
+        j, l = divmod(e, 32)
+        blk[16 + 32 * (j // 2) + l] |= want[e] << (4 * (j % 2))
+    assert (orc.dequant_row(GType.Q4_K, blk, 256) == want.astype(np.float32)).all()
+    blk[2:4] = _f16b(0.5)                                          # mins: sub-block 5 gets m = 3
+    blk[4 + 9] = 1 | (3 << 4)                                      # scale byte 9: sc_5 = 1, m_5 = 3 (j >= 4 branch)
+    exp = want.astype(np.float32) - np.where(np.arange(256) // 32 == 5, np.float32(1.5), np.float32(0))
+    assert (orc.dequant_row(GType.Q4_K, blk, 256) == exp).all()
+
+
+def test_q6k_known_answer_positions():
+    """Q6_K element e = 128 hf + 32 qt + l: low 4 bits in ql[64 hf + 32 (qt & 1) + l] (high nibble for qt >= 2),
+    bits 4-5 in qh[32 hf + l] >> 2 qt, int8 scale e // 16, value d * sc * (q6 - 32) (src/kernels4.cu:671-681)."""
+    want = np.array([(11 * e) % 64 for e in range(256)], np.int64)
+    blk = np.zeros(210, np.uint8)
+    for e in range(256):
+        hf, qt, l = e // 128, (e // 32) % 4, e % 32
+        blk[64 * hf + 32 * (qt & 1) + l] |= (want[e] & 15) << (4 if qt >= 2 else 0)
+        blk[128 + 32 * hf + l] |= (want[e] >> 4) << (2 * qt)
+    blk[192:208] = np.arange(1, 17, dtype=np.int8).view(np.uint8) * np.where(np.arange(16) % 2, -1, 1).astype(np.int8).view(np.uint8)
+    blk[208:210] = _f16b(1.0)
+    sc = blk[192:208].view(np.int8).astype(np.float32)
+    exp = (np.repeat(sc, 16) * (want - 32).astype(np.float32)).astype(np.float32)
+    assert (orc.dequant_row(GType.Q6_K, blk, 256) == exp).all()
+
+
+def test_iq2xs_known_answer():
+    """IQ2_XS 8-group l of 32-group ib: grid row qs[4 ib + l] & 511, signs ksigns[qs >> 9], scale nibble (l / 2) of
+    scales[ib]; value d (0.5 + sc) / 4 grid sign (src/kernels4.cu:592-601)."""
+    rows, ks = iq2xs_rows(), ksigns()
+    blk = np.zeros(74, np.uint8)
+    blk[0:2] = _f16b(4.0)
+    qs = np.array([(37 * i) % 512 | (((5 * i) % 128) << 9) for i in range(32)], np.uint16)
+    blk[2:66] = qs.view(np.uint8)
+    blk[66:74] = [0x10, 0x32, 0x54, 0x76, 0x98, 0xBA, 0xDC, 0xFE]
+    got = orc.dequant_row(GType.IQ2_XS, blk, 256)
+    for e in range(256):
+        ib, l, j = e // 32, (e // 8) % 4, e % 8
+        q = int(qs[4 * ib + l])
+        sc = (blk[66 + ib] >> (4 * (l // 2))) & 15
+        v = np.float32(4.0) * (np.float32(0.5) + np.float32(sc)) * np.float32(0.25) * np.float32(rows[q & 511, j])
+        assert got[e] == (-v if (ks[q >> 9] >> j) & 1 else v)
+
+
+# ------------------------------------------------------------------ integer block dots
+
+@pytest.mark.parametrize("t", ALL)
+def test_block_ints_brute_force(t):
+    n = 2048
+    vt = GType.Q8_0 if t == GType.IQ4_NL else GType.Q8_K
+    rows = blocks(t, 6 * n // block_elems(t), 200 + int(t)).reshape(6, -1)
+    for name, x in list(x_distributions(n, seed=23).items())[:4]:
+        xq = orc.quantize(vt, x)
+        for r in range(rows.shape[0]):
+            si, sm = orc.block_ints(t, rows[r], xq, n)
+            bsi, bsm = nf.block_ints(t, rows[r], xq, iq2xs_rows(), ksigns())
+            assert (si == bsi).all() and (sm == bsm).all(), f"{t.name} {name} row {r}"
+
+
+@pytest.mark.parametrize("t", ALL)
+def test_row_dot_equals_fp64_of_dequantized_operands(t):
+    """The block integers and their fp32 fold agree with sum(dequant(w) * dequant(q8(x))) in fp64 up to fp32 rounding."""
+    n = 4096
+    vt = GType.Q8_0 if t == GType.IQ4_NL else GType.Q8_K
+    rows = blocks(t, 8 * n // block_elems(t), 300 + int(t)).reshape(8, -1)
+    x = np.random.default_rng(5).standard_normal(n).astype(np.float32)
+    xq = orc.quantize(vt, x)
+    xd = orc.dequant_row(vt, xq, n).astype(np.float64)
+    for r in range(8):
+        w = nf.dequant(t, rows[r], iq2xs_rows(), ksigns()).reshape(-1).astype(np.float64)
+        ref = float(w @ xd)
+        got = float(orc.row_dot(t, rows[r], xq, n))
+        scale = float(np.abs(w).dot(np.abs(xd)))
+        assert abs(got - ref) <= 1e-6 * scale + 1e-30, (t, r, got, ref)
+
+
+# ------------------------------------------------------------------ router and bucketing
+
+def test_router_gemv_sum_order_and_value():
+    rng = np.random.default_rng(7)
+    W = (rng.standard_normal((9, 2048)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((2, 2048)).astype(np.float32)
+    y = orc.gemv_f32(W, x)
+    ref = x.astype(np.float64) @ W.astype(np.float64).T
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(x).max() * np.abs(W).max() * 2048 ** 0.5
+    # the contract's order, restated: 64 fma chains over e = 256 i + 4 L + j, then the xor butterfly
+    w, xv = W[0], x[0]
+    part = []
+    for L in range(64):
+        a = np.float32(0)
+        for i in range(8):
+            for j in range(4):
+                e = 256 * i + 4 * L + j
+                a = np.float32(np.float64(w[e]) * np.float64(xv[e]) + np.float64(a))   # fma: exact product, one rounding
+        part.append(a)
+    part = np.array(part, np.float32)
+    for off in (32, 16, 8, 4, 2, 1):
+        part = (part + part[np.arange(64) ^ off]).astype(np.float32)
+    assert part[0] == y[0, 0]
+
+
+@pytest.mark.parametrize("E,k", [(128, 8), (288, 8), (384, 6), (512, 10), (1024, 16)])
+def test_route_topk_properties(E, k):
+    rng = np.random.default_rng(E)
+    logits = (rng.standard_normal((20, E + 1)) * 3).astype(np.float32)
+    ids, wts, sg = orc.route(logits, E, k, with_sg=True)
+    for t in range(20):
+        l = logits[t, :E].astype(np.float64)
+        order = np.lexsort((np.arange(E), -l))          # exact selection on logits (softmax is monotonic)
+        gap = l[order[k - 1]] - l[order[k]]
+        if gap > 1e-5:
+            assert list(ids[t]) == list(order[:k])
+        p = np.exp(l[ids[t]] - l.max())
+        assert np.allclose(wts[t], p / p.sum(), rtol=2e-6, atol=1e-12)
+        assert abs(sg[t] - 1.0 / (1.0 + np.exp(-float(logits[t, E])))) <= 2e-7
+    eq = np.full((1, E), 0.3, np.float32)                  # all ties: the lowest indices (tools/routebench.cu:20)
+    ids, wts, _ = orc.route(eq, E, k)
+    assert list(ids[0]) == list(range(k)) and np.all(wts == wts[0, 0])
+
+
+def test_order_matches_stable_sort():
+    rng = np.random.default_rng(9)
+    E, P = 300, 5000
+    slot = np.arange(E, dtype=np.int32)
+    slot[rng.choice(E, 40, replace=False)] = -1
+    ids = rng.integers(-3, E + 3, P).astype(np.int32)
+    order, on, eg = orc.order(slot, ids, E)
+    valid = (ids >= 0) & (ids < E)
+    valid[valid] &= slot[ids[valid]] >= 0
+    p = np.nonzero(valid)[0]
+    ref = p[np.argsort(ids[p], kind="stable")]
+    assert (order == ref).all() and on[0] == ref.size
+    e_act, counts = np.unique(ids[p], return_counts=True)
+    assert on[1] == e_act.size and (eg[:, 0] == e_act).all() and (eg[:, 2] == counts).all()
+    assert (eg[:, 1] == np.concatenate([[0], np.cumsum(counts)[:-1]])).all()
+
+
+# ------------------------------------------------------------------ the layer
+
+@pytest.mark.parametrize("tg,td,d,ff,k", [(GType.Q4_K, GType.Q6_K, 2048, 512, 4), (GType.IQ4_NL, GType.IQ4_NL, 1024, 512, 3),
+                                          (GType.IQ2_XS, GType.Q4_K, 1024, 256, 2), (GType.Q5_K, GType.IQ4_XS, 512, 512, 5)])
+def test_layer_matches_fp64_recomputation(tg, td, d, ff, k):
+    """CpuMoe::run_layer semantics (src/cpu_moe.cpp:668-1008): pairs in expert order, quantized activations,
+    SwiGLU, re-quantized hidden, down, weighted sum -- recomputed in fp64 from the numpy decoders."""
+    E, nt = 6, 3
+    L = layer(tg, td, E, ff, d, seed=400 + int(tg), clamp=0.0)
+    OL = oracle_layer(L)
+    ids, wts = routing(nt, E, k, seed=401)
+    x = torch.randn(nt, d, generator=gen(402)).numpy()
+    out, h, y = orc.moe_layer(OL, x, ids, wts, want_hy=True)
+    vg, vd = (GType.Q8_0 if tg == GType.IQ4_NL else GType.Q8_K), (GType.Q8_0 if td == GType.IQ4_NL else GType.Q8_K)
+    rows_g, ks = iq2xs_rows(), ksigns()
+    ref = np.zeros((nt, d))
+    for t in range(nt):
+        xd = orc.dequant_row(vg, orc.quantize(vg, x[t]), d).astype(np.float64)
+        for j in np.argsort(ids[t], kind="stable"):
+            e = ids[t, j]
+            G = nf.dequant(tg, OL.gate[e], rows_g, ks).reshape(ff, d).astype(np.float64)
+            U = nf.dequant(tg, OL.up[e], rows_g, ks).reshape(ff, d).astype(np.float64)
+            g, u = G @ xd, U @ xd
+            hh = g / (1 + np.exp(-g)) * u
+            p = t * k + j
+            assert np.allclose(hh, h[p], rtol=1e-5, atol=1e-5 * np.abs(hh).max())
+            hd = orc.dequant_row(vd, orc.quantize(vd, h[p]), ff).astype(np.float64)   # the oracle's own h
+            D = nf.dequant(td, OL.down[e], rows_g, ks).reshape(d, ff).astype(np.float64)
+            yy = D @ hd
+            assert np.allclose(yy, y[p], rtol=1e-5, atol=1e-5 * np.abs(yy).max())
+            ref[t] += wts[t, j] * yy
+    assert np.linalg.norm(out - ref) <= 1e-5 * np.linalg.norm(ref)
+    # the weighted sum itself: first pair assigns w*y, later pairs add w*y, in ascending expert id
+    for t in range(nt):
+        acc = None
+        for j in np.argsort(ids[t], kind="stable"):
+            v = (wts[t, j] * y[t * k + j]).astype(np.float32)
+            acc = v if acc is None else (acc + v).astype(np.float32)
+        assert (acc == out[t]).all()
+
+
+def test_layer_close_to_unquantized_math():
+    """Q8 activations cost well under 3 % relative L2 against fp64 math on fp32 activations."""
+    E, d, ff, k, nt = 4, 2048, 512, 2, 2
+    L = layer(GType.Q4_K, GType.Q4_K, E, ff, d, seed=500)
+    OL = oracle_layer(L)
+    ids, wts = routing(nt, E, k, seed=501)
+    x = torch.randn(nt, d, generator=gen(502)).numpy()
+    out = orc.moe_layer(OL, x, ids, wts)
+    ref = np.zeros((nt, d))
+    for t in range(nt):
+        for j in range(k):
+            e = ids[t, j]
+            G = nf.dequant(GType.Q4_K, OL.gate[e]).reshape(ff, d).astype(np.float64)
+            U = nf.dequant(GType.Q4_K, OL.up[e]).reshape(ff, d).astype(np.float64)
+            D = nf.dequant(GType.Q4_K, OL.down[e]).reshape(d, ff).astype(np.float64)
+            g, u = G @ x[t], U @ x[t]
+            ref[t] += wts[t, j] * (D @ (g / (1 + np.exp(-g)) * u))
+    assert np.linalg.norm(out - ref) / np.linalg.norm(ref) < 0.03
+
+
+def test_shared_expert_and_garbage_ids():
+    E, d, ff, k, nt = 5, 512, 256, 2, 3
+    L = layer(GType.Q4_K, GType.Q4_K, E, ff, d, seed=600)
+    S = layer(GType.Q4_K, GType.Q4_K, 1, ff, d, seed=601)
+    OL, OS = oracle_layer(L), oracle_layer(S)
+    ids = np.array([[0, 3], [4, -1], [7, 2]], np.int32)          # -1 and 7 (>= E) are skipped
+    wts = np.full((nt, k), 0.5, np.float32)
+    x = torch.randn(nt, d, generator=gen(602)).numpy()
+    sg = np.float32([0.25, 1.0, 0.75])
+    out = orc.moe_layer(OL, x, ids, wts, shared=OS, sg=sg)
+    _, ysh = orc.expert_ffn(OS, 0, x)
+    _, _, y = orc.moe_layer(OL, x, ids, wts, want_hy=True)
+    for t in range(nt):
+        acc = (sg[t] * ysh[t]).astype(np.float32)
+        for j in np.argsort(ids[t], kind="stable"):
+            if 0 <= ids[t, j] < E:
+                acc = (acc + (wts[t, j] * y[t * k + j]).astype(np.float32)).astype(np.float32)
+        assert (acc == out[t]).all()
