@@ -141,9 +141,9 @@ def prefill_bench(args, dev, stream):
         "step_int8_tops": ops / (ms_step / 1e3) / 1e12,
         "kernels": {k_: {"us": v["ms"] * 1e3, "alg_bytes": v["bytes"], "gbs": v["bytes"] / (v["ms"] / 1e3) / 1e9} for k_, v in kern.items()},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": ach / HBM_PEAK_GBS, "traffic": None},
+                     "frac": ach / HBM_PEAK_GBS, "traffic": traffic_from_profile(dom)},
     }
-    return res, layers[0], W_rs[0], xs[0], biases[0], runners[0]
+    return res, layers[0], W_rs[0], xs, biases
 
 
 def decode_bench(args, dev, stream):
@@ -175,26 +175,60 @@ def decode_bench(args, dev, stream):
                         "down_reduce": {"us": ms_dn * 1e3, "gbs": k * L0.down_bytes / (ms_dn / 1e3) / 1e9}}}
 
 
-def cpu_baseline(layer, W_r, x, bias, budget_s: float):
-    """The CPU oracle on the first S tokens of the headline step (S grows until about budget_s of work)."""
+def cpu_baseline(layer, W_r, xs, biases, budget_s: float):
+    """The CPU oracle on the headline step: the first S tokens of one step, S doubling up to the full 512, then
+    whole steps over the next inputs until about budget_s seconds of oracle work have been timed."""
     import oracle as orc
     OL = orc.Layer.from_expert_layer(layer)
-    xh, bh, Wh = x.cpu().numpy(), bias.cpu().numpy(), W_r.cpu().numpy()
+    Wh = W_r.cpu().numpy()
     w = WORKLOADS["q4k_q6k_prefill512"]
     threads = orc.default_threads()
-    S, spent = 4, 0.0
-    while True:
-        logits = orc.gemv_f32(Wh, xh[:S]) + bh[:S]
-        ids, wts, _ = orc.route(logits.astype(np.float32), w.E, w.k)
+
+    def one(i, S):
+        xh, bh = xs[i % len(xs)][:S].cpu().numpy(), biases[i % len(xs)][:S].cpu().numpy()
+        logits = (orc.gemv_f32(Wh, xh) + bh).astype(np.float32)
         t0 = time.perf_counter()
-        orc.moe_layer(OL, xh[:S], ids, wts, threads=threads)
-        spent = time.perf_counter() - t0
-        if spent * 2.2 > budget_s or S >= w.rows:
-            break
-        S = min(w.rows, S * 2)
-    return {"value": S / spent, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"first {S} tokens of one 512-token prefill step (same weights, routing and activations), "
-                      f"{spent:.2f} s, oracle/moe_oracle.c with {threads} threads"}
+        ids, wts, _ = orc.route(logits, w.E, w.k)
+        orc.moe_layer(OL, xh, ids, wts, threads=threads)
+        return time.perf_counter() - t0
+
+    S = 4
+    while S < w.rows:
+        dt = one(0, S)
+        if dt * (w.rows / S) > budget_s:        # a full step would overrun the budget: report this sample
+            return {"value": S / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+                    "sample": f"first {S} tokens of one {w.rows}-token step, {dt:.2f} s, oracle/moe_oracle.c, {threads} threads"}
+        S *= 2
+    spent, steps = 0.0, 0
+    while spent < budget_s or steps == 0:
+        spent += one(steps, w.rows)
+        steps += 1
+    return {"value": steps * w.rows / spent, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} whole {w.rows}-token steps (routing + expert FFN + combine; same weights, fresh inputs), "
+                      f"{spent:.1f} s, oracle/moe_oracle.c, {threads} threads"}
+
+
+def copy_probe(mib: int, dev):
+    """A plain copy kernel of known size (mib MiB read, mib MiB written), three launches: the yardstick that
+    scales the FETCH_SIZE / WRITE_SIZE counters into bytes."""
+    src = torch.randn(mib * (1 << 18), device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def traffic_from_profile(kernel: str):
+    """HBM bytes per launch of `kernel` measured by counter passes (committed summary), or None."""
+    f = ROOT / "profiles" / "traffic_q4k_q6k_prefill512.txt"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        parts = line.split()
+        if len(parts) >= 3 and parts[0] == "traffic_bytes" and parts[1] == kernel:
+            return float(parts[2])
+    return None
 
 
 def main():
@@ -202,7 +236,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64, help="timed prefill steps")
     ap.add_argument("--warmup", type=int, default=2, help="untimed passes over the step sequence")
-    ap.add_argument("--copies", type=int, default=2, help="independent weight copies cycled by the prefill steps")
+    ap.add_argument("--copies", type=int, default=4, help="independent weight copies cycled by the prefill steps")
     ap.add_argument("--inputs", type=int, default=4, help="independent (activations, routing) sets")
     ap.add_argument("--graph-steps", type=int, default=8, help="prefill steps captured per graph")
     ap.add_argument("--kernel-reps", type=int, default=8)
@@ -210,14 +244,18 @@ def main():
     ap.add_argument("--decode-reps", type=int, default=8)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-oracle work for cpu_baseline (0: skip)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run a plain copy kernel over MIB MiB (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream()
+    if args.copy_probe:
+        copy_probe(args.copy_probe, dev)
     log("prefill: building layers and inputs")
-    pre, L0, W0, x0, b0, _ = prefill_bench(args, dev, stream)
+    pre, L0, W0, xs0, bs0 = prefill_bench(args, dev, stream)
     log(f"prefill: {pre['tok_s']:.0f} tok/s, {pre['ms_step'] * 1e3:.1f} us/step")
     dec = None
     if not args.no_decode:
@@ -227,7 +265,7 @@ def main():
     cpu = None
     if args.cpu_budget > 0:
         log("cpu baseline: oracle on a sample of the prefill step")
-        cpu = cpu_baseline(L0, W0, x0, b0, args.cpu_budget)
+        cpu = cpu_baseline(L0, W0, xs0, bs0, args.cpu_budget)
     w = WORKLOADS["q4k_q6k_prefill512"]
     line = {
         "metric": METRIC, "value": round(pre["tok_s"], 1), "unit": "tokens/s", "n_gpus": 1,

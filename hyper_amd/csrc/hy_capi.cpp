@@ -26,7 +26,7 @@ int check_launch(const char *what) {
 }
 
 static bool dot_type(int t) { return t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ4_NL; }
-static bool gemm_type(int t) { return t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS; }
+static bool gemm_type(int t) { return t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ4_NL; }
 
 // the expert layer descriptor is usable: types, sizes, pointers, row sizes that the kernels assume
 static int check_dev(const hy_moe_dev *m, const char *what, bool need_gate, bool need_down) {

@@ -39,7 +39,7 @@ __device__ __forceinline__ uint2 load8_a2(const uint8_t *p) {   // 8 bytes from 
 template <int T> struct Raw;
 
 template <> struct Raw<Q4_K> {   // 144 B: d, dmin, scales[12], qs[128]; chunk c: nibbles (c & 1) of qs[32 (c / 2) + 8 q ..]
-    static constexpr bool mins = true, g16 = false;
+    static constexpr bool mins = true, g16 = false, per_chunk = false;
     uint4 hd; uint2 qv[4];
     __device__ __forceinline__ void load(const uint8_t *blk, int q) {
         hd = load16_a4(blk);
@@ -57,7 +57,7 @@ template <> struct Raw<Q4_K> {   // 144 B: d, dmin, scales[12], qs[128]; chunk c
     }
 };
 template <> struct Raw<Q5_K> {   // 176 B: + qh[32] @16 (bit c of qh[l] is bit 4 of chunk c's value l), qs @48
-    static constexpr bool mins = true, g16 = false;
+    static constexpr bool mins = true, g16 = false, per_chunk = false;
     uint4 hd; uint2 qv[4], qh;
     __device__ __forceinline__ void load(const uint8_t *blk, int q) {
         hd = load16_a4(blk);
@@ -79,7 +79,7 @@ template <> struct Raw<Q5_K> {   // 176 B: + qh[32] @16 (bit c of qh[l] is bit 4
 // Q6_K (210 B): chunk c = elements 32 c ..: hf = c >> 2, qt = c & 3; lane values l = 8 q .. + 7 from
 // ql[64 hf + 32 (qt & 1) + l] (high nibble when qt >= 2) and bits 2 qt of qh[32 hf + l]; groups 2 c, 2 c + 1.
 template <> struct Raw<Q6_K> {
-    static constexpr bool mins = false, g16 = true;
+    static constexpr bool mins = false, g16 = true, per_chunk = false;
     uint2 ql[4], qh[2]; uint4 scv; uint32_t d;
     __device__ __forceinline__ void load(const uint8_t *blk, int q) {
 #pragma unroll
@@ -102,7 +102,7 @@ template <> struct Raw<Q6_K> {
 };
 // IQ4_XS (136 B): chunk c = 32-group c; lane values 8 q .. + 7 are nibbles (q >> 1) of qs[16 c + 8 (q & 1) ..]
 template <> struct Raw<IQ4_XS> {
-    static constexpr bool mins = false, g16 = false;
+    static constexpr bool mins = false, g16 = false, per_chunk = false;
     uint2 qv[8]; uint32_t dsh, sl;
     __device__ __forceinline__ void load(const uint8_t *blk, int q) {
 #pragma unroll
@@ -122,7 +122,7 @@ template <> struct Raw<IQ4_XS> {
 // IQ2_XS (74 B): chunk c = 32-group c; lane q takes 8-group q (grid row qs[4 c + q], signs); scales
 // 2 (scales[c] & 15) + 1 for k 0..15 (lanes q < 2) and 2 (scales[c] >> 4) + 1 for k 16..31.
 template <> struct Raw<IQ2_XS> {
-    static constexpr bool mins = false, g16 = true;
+    static constexpr bool mins = false, g16 = true, per_chunk = false;
     uint32_t qq[4]; uint2 scv; uint32_t d;
     __device__ __forceinline__ void load(const uint8_t *blk, int q) {
 #pragma unroll
@@ -142,6 +142,27 @@ template <> struct Raw<IQ2_XS> {
         mn = 0;
     }
     __device__ __forceinline__ float fold(int si, int) const { return (h2f(d) * 0.125f) * (float) si; }
+};
+
+// IQ4_NL (8 blocks of 18 B per 256 values, Q8_0 activations): chunk c = block c; lane values 8 q .. + 7 are
+// nibbles (q >> 1) of qs[8 (q & 1) ..]; every block folds on its own: acc = fma(x_d, fp16(d_c) * D, acc).
+template <> struct Raw<IQ4_NL> {
+    static constexpr bool mins = false, g16 = false, per_chunk = true;
+    uint2 qv[8]; uint32_t dd[4];
+    __device__ __forceinline__ void load(const uint8_t *blk, int q) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) qv[c] = load8_a2(blk + 18 * c + 2 + 8 * (q & 1));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dd[i] = (uint32_t) ld_u16(blk + 36 * i) | ((uint32_t) ld_u16(blk + 36 * i + 18) << 16);
+    }
+    __device__ __forceinline__ void chunk(int c, int q, const uint2 *, uint32_t &b0, uint32_t &b1, int &s0, int &s1, int &mn) const {
+        const int s = 4 * (q >> 1);
+        b0 = kv4((qv[c].x >> s) & 0x0F0F0F0Fu);
+        b1 = kv4((qv[c].y >> s) & 0x0F0F0F0Fu);
+        s0 = 1; s1 = 0; mn = 0;
+    }
+    __device__ __forceinline__ float cfold(int c, int d) const { return h2f((dd[c >> 1] >> (16 * (c & 1))) & 0xffff) * (float) d; }
+    __device__ __forceinline__ float fold(int si, int) const { return (float) si; }
 };
 
 constexpr int GM_TOK = 64, GM_TILES = GM_TOK / 16, GM_ROWS = 64, GM_LD = 264;   // LDS row stride of staged activations
@@ -174,6 +195,24 @@ __device__ __forceinline__ void chunk_ints(const Raw<T> &w, int c, int q, const 
     }
 }
 
+// IQ4_NL: one chunk's MFMA per tile folded straight into the fp32 accumulators (Yc: 8 block scales per token)
+template <int T>
+__device__ __forceinline__ void chunk_fold(const Raw<T> &w, int c, int q, const int8_t *As, const float *Yc, int rr, int ntile,
+                                           float (&acc)[GM_TILES][4]) {
+    const v4i z = {0, 0, 0, 0};
+    uint32_t b0, b1;
+    int s0, s1, mn;
+    w.chunk(c, q, nullptr, b0, b1, s0, s1, mn);
+#pragma unroll
+    for (int tile = 0; tile < GM_TILES; ++tile) {
+        if (tile >= ntile) break;
+        const long a = *(const long *) (As + (tile * 16 + rr) * GM_LD + 32 * c + 8 * q);
+        const v4i d0 = mfma16(a, mk_long(b0, b1), z);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[tile][v] = __builtin_fmaf(Yc[(tile * 16 + 4 * q + v) * 8 + c], w.cfold(c, d0[v]), acc[tile][v]);
+    }
+}
+
 // A block walks the work items it, it + gridDim.y, ...; the (item, block) steps form one stream in which the
 // next step's weight and activation bytes are loaded while the current step computes, across item boundaries.
 template <int T, bool GU>
@@ -181,7 +220,8 @@ __global__ __launch_bounds__(256) void k_gemm(hy_moe_dev m, const uint8_t *__res
                                               const int *__restrict__ order_n, const int *__restrict__ egrp, const float *__restrict__ wts,
                                               float *__restrict__ out) {
     __shared__ __align__(16) int8_t As[2][GM_TOK * GM_LD];
-    __shared__ float Yd[2][GM_TOK];
+    constexpr bool NL = T == IQ4_NL;                 // Q8_0 activations, per-block fold
+    __shared__ float Yd[2][GM_TOK * (NL ? 8 : 1)];
     __shared__ int s_scan[1024 + 8];
     __shared__ float s_up[GU ? 32 * GM_TOK : 1];
     __shared__ uint2 grid[T == IQ2_XS ? 512 : 1];
@@ -218,8 +258,9 @@ __global__ __launch_bounds__(256) void k_gemm(hy_moe_dev m, const uint8_t *__res
     const bool row_ok = row < rows;
     const size_t mbytes = GU ? m.gate_bytes : m.down_bytes, rb = mbytes / rows;
     const uint8_t *Wbase = (GU ? (wave < 2 ? m.gate : m.up) : m.down) + (size_t) (row_ok ? row : rows - 1) * rb;
-    const size_t arow = (size_t) nsb * Q8K_BYTES;
-    constexpr int BB = block_bytes(T);
+    constexpr int AB = NL ? 8 * Q8_0_BYTES : Q8K_BYTES;   // activation bytes per 256 values
+    const size_t arow = (size_t) nsb * AB;
+    constexpr int BB = NL ? 8 * block_bytes(T) : block_bytes(T);   // weight bytes per 256 values
     const int st_tok = tid >> 2, st_part = tid & 3;   // staging: 64 bytes of token st_tok per thread
 
     // item -> (first pair in order, tokens, weight pointer); the staging thread's activation row
@@ -239,16 +280,23 @@ __global__ __launch_bounds__(256) void k_gemm(hy_moe_dev m, const uint8_t *__res
         }
         return st;
     };
-    auto load_a = [&](const uint8_t *src, int b, uint4 (&a)[4], float &yd) {
+    auto load_a = [&](const uint8_t *src, int b, uint4 (&a)[4], float (&yd)[2]) {
         if (src) {
-            const uint8_t *s = src + (size_t) b * Q8K_BYTES;
+            const uint8_t *s = src + (size_t) b * AB;
+            if constexpr (NL) {   // Q8_0 blocks 2 st_part, 2 st_part + 1: qs at 68 p + 2 (2 mod 4) and 68 p + 36
+                const uint8_t *p0 = s + 2 * Q8_0_BYTES * st_part;
+                a[0] = load16_a2(p0 + 2); a[1] = load16_a2(p0 + 18);
+                a[2] = load16_a4(p0 + 36); a[3] = load16_a4(p0 + 52);
+                yd[0] = h2f(ld_u16(p0)); yd[1] = h2f(ld_u16(p0 + Q8_0_BYTES));
+            } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = load16_a4(s + 4 + 64 * st_part + 16 * i);
-            yd = *(const float *) s;
+                for (int i = 0; i < 4; ++i) a[i] = load16_a4(s + 4 + 64 * st_part + 16 * i);
+                yd[0] = *(const float *) s; yd[1] = 0.0f;
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) a[i] = make_uint4(0, 0, 0, 0);
-            yd = 0.0f;
+            yd[0] = yd[1] = 0.0f;
         }
     };
 
@@ -256,7 +304,7 @@ __global__ __launch_bounds__(256) void k_gemm(hy_moe_dev m, const uint8_t *__res
     Raw<T> w;
     w.load(cur.W, q);
     uint4 a[4];
-    float yd;
+    float yd[2];
     load_a(cur.src, 0, a, yd);
     float acc[GM_TILES][4];
 #pragma unroll
@@ -269,7 +317,8 @@ __global__ __launch_bounds__(256) void k_gemm(hy_moe_dev m, const uint8_t *__res
             uint4 *dst = (uint4 *) (As[buf] + st_tok * GM_LD + 64 * st_part);
 #pragma unroll
             for (int i = 0; i < 4; ++i) dst[i] = a[i];
-            if (st_part == 0) Yd[buf][st_tok] = yd;
+            if constexpr (NL) { Yd[buf][st_tok * 8 + 2 * st_part] = yd[0]; Yd[buf][st_tok * 8 + 2 * st_part + 1] = yd[1]; }
+            else if (st_part == 0) Yd[buf][st_tok] = yd[0];
         }
         // the next step: block b + 1 of this item, or block 0 of the next item
         const bool last_b = b + 1 == nsb;
@@ -285,22 +334,27 @@ __global__ __launch_bounds__(256) void k_gemm(hy_moe_dev m, const uint8_t *__res
         }
         __syncthreads();
         const int ntile = (cur.ntok + 15) / 16;
-        int si[GM_TILES][4];
-        v4i sm[GM_TILES];
+        if constexpr (NL) {
 #pragma unroll
-        for (int i = 0; i < GM_TILES; ++i) {
+            for (int c = 0; c < 8; ++c) chunk_fold<T>(w, c, q, As[buf], Yd[buf], rr, ntile, acc);
+        } else {
+            int si[GM_TILES][4];
+            v4i sm[GM_TILES];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) si[i][v] = 0;
-            sm[i] = v4i{0, 0, 0, 0};
-        }
+            for (int i = 0; i < GM_TILES; ++i) {
 #pragma unroll
-        for (int c = 0; c < 8; ++c) chunk_ints<T>(w, c, q, grid, As[buf], rr, ntile, si, sm);
+                for (int v = 0; v < 4; ++v) si[i][v] = 0;
+                sm[i] = v4i{0, 0, 0, 0};
+            }
 #pragma unroll
-        for (int tile = 0; tile < GM_TILES; ++tile) {
-            if (tile >= ntile) break;
+            for (int c = 0; c < 8; ++c) chunk_ints<T>(w, c, q, grid, As[buf], rr, ntile, si, sm);
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
-                acc[tile][v] = __builtin_fmaf(Yd[buf][tile * 16 + 4 * q + v], w.fold(si[tile][v], sm[tile][v]), acc[tile][v]);
+            for (int tile = 0; tile < GM_TILES; ++tile) {
+                if (tile >= ntile) break;
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    acc[tile][v] = __builtin_fmaf(Yd[buf][tile * 16 + 4 * q + v], w.fold(si[tile][v], sm[tile][v]), acc[tile][v]);
+            }
         }
         if (last_b) {   // the item's outputs
             if (GU && wave >= 2) {
@@ -346,6 +400,7 @@ __global__ __launch_bounds__(256) void k_gemm(hy_moe_dev m, const uint8_t *__res
     case Q6_K: { constexpr int TT = Q6_K; CALL; }                                                 \
     case IQ4_XS: { constexpr int TT = IQ4_XS; CALL; }                                             \
     case IQ2_XS: { constexpr int TT = IQ2_XS; CALL; }                                             \
+    case IQ4_NL: { constexpr int TT = IQ4_NL; CALL; }                                             \
     default: set_error("grouped GEMM: unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 

@@ -203,6 +203,8 @@ GEMM_CASES = [
     (GType.Q5_K, GType.Q6_K, 2048, 512, 10, 33),
     (GType.IQ4_XS, GType.IQ4_XS, 4096, 1536, 8, 4),
     (GType.IQ2_XS, GType.IQ2_XS, 7168, 2048, 6, 8),
+    (GType.IQ4_NL, GType.IQ4_NL, 4096, 1536, 8, 4),
+    (GType.IQ4_NL, GType.IQ4_NL, 2048, 512, 8, 50),
 ]
 
 
