@@ -156,9 +156,11 @@ static int launch_gemv_t(const hy_moe_dev &m, const float *src, int ss, const in
                          hipStream_t s, const int *order, const int *order_n) {
     const int in_dim = GU ? m.n : m.ff, rows = GU ? m.ff : m.n, ng = in_dim / 256, nmat = GU ? 2 : 1;
     int R = 32 * GEMV_MAXI / (nmat * ng);
+    if (R < 1) { set_error("%s: input dimension %d exceeds %d", GU ? "hy_moe_gate_up" : "hy_moe_down", in_dim, 256 * 32 * GEMV_MAXI / nmat); return HY_EBAD_SHAPE; }
     if (R > rows) R = rows;
     if (R > 128) R = 128;
     const size_t lds = gemv_lds<T, GU>(in_dim, R);
+    if (lds > 64 * 1024) { set_error("%s: %zu bytes of LDS needed", GU ? "hy_moe_gate_up" : "hy_moe_down", lds); return HY_EBAD_SHAPE; }
     dim3 grid(nt * k, (rows + R - 1) / R);
     if (grid.x == 0) return HY_OK;
     hipLaunchKernelGGL((k_gemv<T, GU>), grid, dim3(256), lds, s, m, m.n_expert, src, ss, ids, k, wts, dst, R, order, order_n);
