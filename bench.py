@@ -9,8 +9,8 @@ bucketing -> Q8_K activations -> grouped int8-MFMA gate/up GEMM (SwiGLU) -> Q8_K
 several independent weight copies, so the 256 MB MALL does not serve the weights.  Steps are replayed from a
 HIP graph (captured once, checked against an eager run first).
 
-Secondary (`decode` object): 1-token decode of the same layer shape in Q4_K/Q4_K: router GEMV -> route ->
-gate/up GEMV -> fused down + combine, cycling 4 layer copies (1.36 GB) and fresh tokens.
+Secondary (`decode` object): 1-token decode of the same layer shape in Q4_K/Q4_K, three launches: router GEMV +
+Q8 of x -> routing + gate/up GEMV -> down GEMV + combine, cycling 4 layer copies (1.36 GB) and fresh tokens.
 
 `roofline` reports the dominant kernel of the headline step against HBM bandwidth (8 TB/s): algorithmic bytes
 per launch / its average launch duration, measured on its own stream with HIP events over graph replays of
@@ -162,8 +162,10 @@ def decode_bench(args, dev, stream):
             f()
         torch.cuda.synchronize()
         ms = graph_time(fns, max(1, args.decode_reps), stream) / len(fns)
-        gu = [lambda r=r, i=i: moe.moe_gate_up(r.dev, xs[i:i + 1], d, r.ids, k, r.h, 1) for i, r in enumerate(runners)]
+        rq = [lambda r=r, i=i: moe.moe_router_q8(r.W_r, E, d, xs[i:i + 1], d, r.logits, E, r.vg, r.xq, 1) for i, r in enumerate(runners)]
+        gu = [lambda r=r: moe.moe_route_gate_up(r.dev, r.logits, E, E, k, r.xq, r.ids, r.wts, None, r.h, 1) for r in runners]
         dn = [lambda r=r: moe.moe_down_reduce(r.dev, r.h, r.ids, r.wts, k, None, None, r.out, 1) for r in runners]
+        ms_rq = graph_time(rq * 8, max(1, args.decode_reps), stream) / (8 * len(rq))
         ms_gu = graph_time(gu * 8, max(1, args.decode_reps), stream) / (8 * len(gu))
         ms_dn = graph_time(dn * 8, max(1, args.decode_reps), stream) / (8 * len(dn))
     L0 = layers[0]
@@ -171,7 +173,8 @@ def decode_bench(args, dev, stream):
     us = ms * 1e3
     return {"workload": "q4k_decode", "us_per_token": us, "hbm_gbs": tok_bytes / (us / 1e6) / 1e9,
             "hbm_frac": tok_bytes / (us / 1e6) / 1e9 / HBM_PEAK_GBS, "alg_bytes_per_token": tok_bytes,
-            "kernels": {"gate_up_gemv": {"us": ms_gu * 1e3, "gbs": k * 2 * L0.gate_bytes / (ms_gu / 1e3) / 1e9},
+            "kernels": {"router_q8": {"us": ms_rq * 1e3, "gbs": (E * d * 4 + d * 4) / (ms_rq / 1e3) / 1e9},
+                        "route_gate_up": {"us": ms_gu * 1e3, "gbs": k * 2 * L0.gate_bytes / (ms_gu / 1e3) / 1e9},
                         "down_reduce": {"us": ms_dn * 1e3, "gbs": k * L0.down_bytes / (ms_dn / 1e3) / 1e9}}}
 
 

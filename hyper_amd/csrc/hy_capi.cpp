@@ -194,7 +194,34 @@ int hy_moe_down_reduce(const hy_moe_dev *m, const float *h, const int32_t *ids, 
     if (rc) return rc;
     if (!h || !ids || !wts || !out || k <= 0 || k > 64 || nt < 0) { set_error("hy_moe_down_reduce: bad argument"); return HY_EINVAL; }
     if (!aligned16(h)) { set_error("hy_moe_down_reduce: h must be 16-byte aligned"); return HY_EBAD_SHAPE; }
-    return launch_down_reduce(*m, h, ids, wts, k, shexp, sg, out, nt, s);
+    rc = launch_dec_down(*m, h, ids, wts, k, shexp, sg, out, nt, s);
+    if (rc != HY_EUNSUPPORTED_TYPE) return rc;
+    return launch_down_reduce(*m, h, ids, wts, k, shexp, sg, out, nt, s);   // shapes beyond the fused kernel's LDS budget
+}
+
+int hy_moe_router_q8(const float *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride, float *logits,
+                     int ls, int vtype, void *xq, int nt, hipStream_t s) {
+    if (!W_r || !x || !logits || !xq || rows <= 0 || nt < 0) { set_error("hy_moe_router_q8: bad argument"); return HY_EINVAL; }
+    if (kdim <= 0 || xs % 4 || !aligned16(W_r) || !aligned16(x)) { set_error("hy_moe_router_q8: W_r / x rows must be 16-byte aligned"); return HY_EBAD_SHAPE; }
+    if (vtype == Q8_K) {
+        if (kdim % 256 || ((uintptr_t) xq & 3)) { set_error("hy_moe_router_q8: Q8_K needs kdim %% 256 == 0"); return HY_EBAD_SHAPE; }
+    } else if (vtype == Q8_0) {
+        if (kdim % 32 || ((uintptr_t) xq & 1)) { set_error("hy_moe_router_q8: Q8_0 needs kdim %% 32 == 0"); return HY_EBAD_SHAPE; }
+    } else { set_error("hy_moe_router_q8: vtype %d", vtype); return HY_EUNSUPPORTED_TYPE; }
+    if (rows > ls) { set_error("hy_moe_router_q8: %d rows do not fit the logit stride %d", rows, ls); return HY_EBAD_SHAPE; }
+    return launch_router_q8(W_r, rows, kdim, x, xs, bias, bias_stride, logits, ls, vtype, xq, nt, s);
+}
+
+int hy_moe_route_gate_up(const hy_moe_dev *m, const float *logits, int ls, int n_expert, int k, const void *xq, int32_t *ids, float *wts,
+                         float *sg, float *h, int nt, hipStream_t s) {
+    int rc = check_dev(m, "hy_moe_route_gate_up", true, false);
+    if (rc) return rc;
+    if (!logits || !xq || !ids || !wts || !h || nt < 0) { set_error("hy_moe_route_gate_up: bad argument"); return HY_EINVAL; }
+    if (n_expert <= 0 || n_expert > 1024 || n_expert > m->n_expert) { set_error("hy_moe_route_gate_up: n_expert %d out of range", n_expert); return HY_EBAD_SHAPE; }
+    if (k <= 0 || k > 64 || k > n_expert) { set_error("hy_moe_route_gate_up: k = %d out of range", k); return HY_EBAD_SHAPE; }
+    if (ls < n_expert || (sg && ls <= n_expert)) { set_error("hy_moe_route_gate_up: logit stride %d too small", ls); return HY_EBAD_SHAPE; }
+    if ((uintptr_t) xq & 3) { set_error("hy_moe_route_gate_up: xq must be 4-byte aligned"); return HY_EBAD_SHAPE; }
+    return launch_route_gate_up(*m, logits, ls, n_expert, k, xq, ids, wts, sg, h, nt, s);
 }
 
 int hy_dequant_row(int type, const uint8_t *row, int n, float *out, hipStream_t s) {

@@ -69,15 +69,55 @@ __device__ __forceinline__ float hy_swiglu(float g, float u, float L) {
 // ------------------------------------------------------------------ wave helpers
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
-__device__ __forceinline__ float wave_sum_xor(float v) {     // xor butterfly 32, 16, ..., 1 (every lane ends equal)
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o);
-    return v;
+// DPP lane exchange (GFX9 dpp_ctrl): quad_perm [1,0,3,2] = lane ^ 1, quad_perm [2,3,0,1] = lane ^ 2,
+// row_half_mirror = lane i <-> 7 - i within 8, row_mirror = lane i <-> 15 - i within 16
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+template <int CTRL> __device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+__device__ __forceinline__ float readlane_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+
+// The contract's wave sum: the xor butterfly 1, 2, 4, ..., 32 (lane i adds lane i ^ o), every lane gets the
+// result.  Steps 1 and 2 are exact xor exchanges; after them each quad holds one value, so pairing lane i with
+// 7 - i adds the same two quad values as xor 4 does (and i <-> 15 - i the same two half-rows as xor 8); the
+// row values then meet as (r0 + r1) + (r2 + r3), as xor 16 then xor 32 add them.  fp32 addition is
+// commutative, so every step produces the butterfly's bits.
+__device__ __forceinline__ float wave_sum_xor(float v) {
+    v = v + dpp_f<DPP_XOR1>(v);
+    v = v + dpp_f<DPP_XOR2>(v);
+    v = v + dpp_f<DPP_HALF_MIRROR>(v);
+    v = v + dpp_f<DPP_MIRROR>(v);
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+// exact integer sum over each aligned group of 8 lanes (every lane of the group gets it)
+__device__ __forceinline__ int group8_isum(int v) {
+    v += dpp_i<DPP_XOR1>(v);
+    v += dpp_i<DPP_XOR2>(v);
+    v += dpp_i<DPP_HALF_MIRROR>(v);
     return v;
+}
+// wave-wide best (value, index) under `better` (a strict total order: the result does not depend on how the
+// lanes are paired); every lane gets it (uniform)
+template <class Better>
+__device__ __forceinline__ void wave_best(float &v, int &i, Better better) {
+#define HY_BEST_STEP(CTRL) { const float ov = dpp_f<CTRL>(v); const int oi = dpp_i<CTRL>(i); if (better(ov, oi, v, i)) { v = ov; i = oi; } }
+    HY_BEST_STEP(DPP_XOR1) HY_BEST_STEP(DPP_XOR2) HY_BEST_STEP(DPP_HALF_MIRROR) HY_BEST_STEP(DPP_MIRROR)
+#undef HY_BEST_STEP
+    float bv = readlane_f(v, 0);
+    int bi = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+    for (int r = 16; r < 64; r += 16) {
+        const float ov = readlane_f(v, r);
+        const int oi = __builtin_amdgcn_readlane(i, r);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    v = bv; i = bi;
 }
 template <int W> __device__ __forceinline__ int group_isum(int v) {   // sum over aligned groups of W lanes
 #pragma unroll
@@ -128,28 +168,21 @@ __device__ __forceinline__ int nearest_int(float f) {   // the 1.5 * 2^23 trick 
 // one Q8_K block of 256 values by one wave (lane: values 4 lane .. 4 lane + 3): first-occurrence signed
 // max, iscale = -127/max, q = min(127, nearest_int(iscale * x)), int16 sums of 16, d = 1/iscale.
 // An all-zero block writes d = 0, qs = 0, bsums = 0. `out` may be global or LDS (4-byte aligned).
-__device__ __forceinline__ void q8k_block_wave(const float *x, uint8_t *out) {
+// q8k_block_vals: the block from the lane's four values xv (values 4 lane .. 4 lane + 3)
+__device__ __forceinline__ void q8k_block_vals(const float (&xv)[4], uint8_t *out) {
     const int lane = lane_id();
-    const float4 v = *(const float4 *) (x + 4 * lane);
-    const float xv[4] = {v.x, v.y, v.z, v.w};
     float am = fabsf(xv[0]);
     int ix = 0;
 #pragma unroll
     for (int i = 1; i < 4; ++i) { const float a = fabsf(xv[i]); if (a > am) { am = a; ix = i; } }
     int gi = 4 * lane + ix;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float oa = __shfl_xor(am, o);
-        const int oi = __shfl_xor(gi, o);
-        if (oa > am || (oa == am && oi < gi)) { am = oa; gi = oi; }
-    }
+    wave_best(am, gi, [](float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); });
     uint32_t packed = 0;
     int s = 0;
     float d = 0.0f;
     if (am > 0.0f) {
-        const int src = gi >> 2, c = gi & 3;
-        const float m0 = __shfl(xv[0], src), m1 = __shfl(xv[1], src), m2 = __shfl(xv[2], src), m3 = __shfl(xv[3], src);
-        const float mx = c == 0 ? m0 : c == 1 ? m1 : c == 2 ? m2 : m3;
+        const int src = gi >> 2, c = gi & 3;   // uniform
+        const float mx = readlane_f(c == 0 ? xv[0] : c == 1 ? xv[1] : c == 2 ? xv[2] : xv[3], src);
         const float iscale = -127.f / mx;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -161,31 +194,43 @@ __device__ __forceinline__ void q8k_block_wave(const float *x, uint8_t *out) {
         }
         d = 1.0f / iscale;
     }
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
+    s += dpp_i<DPP_XOR1>(s);
+    s += dpp_i<DPP_XOR2>(s);
     ((uint32_t *) (out + 4))[lane] = packed;
     if ((lane & 3) == 0) ((int16_t *) (out + 260))[lane >> 2] = (int16_t) s;
     if (lane == 0) *(float *) out = d;
 }
+__device__ __forceinline__ void q8k_block_wave(const float *x, uint8_t *out) {
+    const float4 v = *(const float4 *) (x + 4 * lane_id());
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    q8k_block_vals(xv, out);
+}
 
-// two Q8_0 blocks of 32 by one wave (lanes 0-31: the first, 32-63: the second), as ggml's x86 quantize_row_q8_0:
-// d = amax / 127 (stored fp16), id = 127 / amax (0 if amax == 0), q = round-to-nearest-even(x * id).
-// `out` points at the first block; `valid2`: the second block exists.
-__device__ __forceinline__ void q8_0_blocks_wave(const float *x, uint8_t *out, bool valid2) {
+// two Q8_0 blocks (64 values) by one wave into blocks of `stride` bytes with qs at `qoff`, as ggml's x86
+// quantize_row_q8_0: d = amax / 127 (stored fp16), id = 127 / amax (0 if amax == 0), q = rint(x * id)
+// from the lane's value v (value `lane` of the pair; lanes 32-63 ignored when !valid2)
+__device__ __forceinline__ void q8_0_pair_vals(float v, uint8_t *out, bool valid2, int stride, int qoff) {
     const int lane = lane_id();
     const bool on = lane < 32 || valid2;
-    const float v = on ? x[lane] : 0.0f;
+    if (!on) v = 0.0f;
     float am = fabsf(v);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+    am = fmaxf(am, dpp_f<DPP_XOR1>(am));
+    am = fmaxf(am, dpp_f<DPP_XOR2>(am));
+    am = fmaxf(am, dpp_f<DPP_HALF_MIRROR>(am));
+    am = fmaxf(am, dpp_f<DPP_MIRROR>(am));
+    am = lane < 32 ? fmaxf(readlane_f(am, 0), readlane_f(am, 16)) : fmaxf(readlane_f(am, 32), readlane_f(am, 48));
     const float d = am / 127.f;
     const float id = am != 0.0f ? 127.f / am : 0.0f;
     const int q = (int) __builtin_rintf(v * id);
     if (on) {
-        uint8_t *b = out + (lane >> 5) * Q8_0_BYTES;
-        b[2 + (lane & 31)] = (uint8_t) (int8_t) q;
+        uint8_t *b = out + (lane >> 5) * stride;
+        b[qoff + (lane & 31)] = (uint8_t) (int8_t) q;
         if ((lane & 31) == 0) *(uint16_t *) b = f2h(d);
     }
+}
+__device__ __forceinline__ void q8_0_pair_wave(const float *x, uint8_t *out, bool valid2, int stride, int qoff) {
+    const int lane = lane_id();
+    q8_0_pair_vals(lane < 32 || valid2 ? x[lane] : 0.0f, out, valid2, stride, qoff);
 }
 
 } // namespace hy

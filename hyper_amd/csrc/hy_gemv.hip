@@ -10,24 +10,6 @@ namespace hy {
 // the padded Q8_0 layout used in LDS: d at 0, qs at 4 (36 bytes: the qs words stay 4-byte aligned)
 constexpr int Q8_0_LDS = 36;
 
-// two Q8_0 blocks (64 values) by one wave into blocks of `stride` bytes with qs at `qoff`
-__device__ __forceinline__ void q8_0_pair_wave(const float *x, uint8_t *out, bool valid2, int stride, int qoff) {
-    const int lane = lane_id();
-    const bool on = lane < 32 || valid2;
-    const float v = on ? x[lane] : 0.0f;
-    float am = fabsf(v);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
-    const float d = am / 127.f;
-    const float id = am != 0.0f ? 127.f / am : 0.0f;
-    const int q = (int) __builtin_rintf(v * id);
-    if (on) {
-        uint8_t *b = out + (lane >> 5) * stride;
-        b[qoff + (lane & 31)] = (uint8_t) (int8_t) q;
-        if ((lane & 31) == 0) *(uint16_t *) b = f2h(d);
-    }
-}
-
 __global__ __launch_bounds__(256) void k_q8k(const float *__restrict__ x, int xs, int n, uint8_t *__restrict__ q) {
     const int t = blockIdx.y, b = blockIdx.x * 4 + (threadIdx.x >> 6), nb = n / 256;
     if (b >= nb) return;
@@ -121,8 +103,8 @@ __global__ __launch_bounds__(256) void k_gemv(hy_moe_dev m, int n_expert, const 
                 tv[(mat * R + row) * nb + 8 * gi + L] = it[i].tval(si, sm);
             } else {
                 it[i].ints(xq + gi * Q8K_BYTES, L, si, sm);
-                si = group_isum<8>(si);
-                sm = group_isum<8>(sm);
+                si = group8_isum(si);
+                sm = group8_isum(sm);
                 if (L == 0) tv[(mat * R + row) * nb + gi] = it[i].tval(si, sm);
             }
         }
@@ -285,8 +267,8 @@ __global__ __launch_bounds__(256) void k_down_reduce(hy_moe_dev m, int n_expert,
                 tv[(j * R + row) * nb + 8 * gi + L] = it[i].tval(si, sm);
             } else {
                 it[i].ints(xq + j * xq_row + gi * Q8K_BYTES, L, si, sm);
-                si = group_isum<8>(si);
-                sm = group_isum<8>(sm);
+                si = group8_isum(si);
+                sm = group8_isum(sm);
                 if (L == 0) tv[(j * R + row) * nb + gi] = it[i].tval(si, sm);
             }
         }
@@ -429,8 +411,8 @@ __global__ __launch_bounds__(256) void k_block_ints(const uint8_t *__restrict__ 
         summ[row * nb + 8 * gi + L] = 0;
     } else {
         it.ints(xq + gi * Q8K_BYTES, L, si, sm);
-        si = group_isum<8>(si);
-        sm = group_isum<8>(sm);
+        si = group8_isum(si);
+        sm = group8_isum(sm);
         if (L == 0) { sumi[row * nb + gi] = si; summ[row * nb + gi] = sm; }
     }
 }

@@ -6,7 +6,7 @@ namespace hy {
 // ---------------------------------------------------------------- router logits (A1)
 // y[t][r] = W[r] . x[t] (+ bias[t][r]): src/kernels4.cu:163-180 (gemv_f32).  Summation order of the contract:
 // lane L of a wave accumulates elements 256 i + 4 L + j (j = 0..3) with fmaf in index order, then the
-// 64 partial sums meet in an xor butterfly (32, 16, ..., 1).  A wave computes RW rows x TW tokens.
+// 64 partial sums meet in an xor butterfly (1, 2, ..., 32).  A wave computes RW rows x TW tokens.
 template <int RW, int TW>
 __global__ __launch_bounds__(256) void k_gemv_f32(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
                                                   float *__restrict__ y, int ys, int nt, const float *__restrict__ bias, int bs) {
@@ -103,12 +103,7 @@ __global__ __launch_bounds__(64) void k_route(const float *__restrict__ logits, 
     for (int j = 0; j < k; ++j) {
         float bv = v[0];
         int bi = vi[0];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int oi = __shfl_xor(bi, o);
-            if (rt_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-        }
+        wave_best(bv, bi, rt_better);
         if (lane == j) { selw = bv; seli = bi; }
         tot = tot + bv;
         if (vi[0] == bi) {

@@ -126,6 +126,17 @@ def moe_down_reduce(m: MoeDev, h, ids, wts, k, shexp, sg, out, nt, stream=None):
     check(lib().hy_moe_down_reduce(m.ref, _p(h), _p(ids), _p(wts), k, _p(shexp), _p(sg), _p(out), nt, _s(stream)))
 
 
+def moe_router_q8(W_r, rows, kdim, x, xs, logits, ls, vtype, xq, nt, stream=None, bias=None, bias_stride=0):
+    """gemv_f32 and the Q8 rows of x in one launch."""
+    check(lib().hy_moe_router_q8(_p(W_r), rows, kdim, _p(x), xs, _p(bias), bias_stride, _p(logits), ls, int(vtype), _p(xq), nt,
+                                 _s(stream)))
+
+
+def moe_route_gate_up(m: MoeDev, logits, ls, n_expert, k, xq, ids, wts, sg, h, nt, stream=None):
+    """moe_route and moe_gate_up (on Q8 rows) in one launch."""
+    check(lib().hy_moe_route_gate_up(m.ref, _p(logits), ls, n_expert, k, _p(xq), _p(ids), _p(wts), _p(sg), _p(h), nt, _s(stream)))
+
+
 def dequant_row(type_, row, n, out, stream=None):
     check(lib().hy_dequant_row(int(type_), _p(row), n, _p(out), _s(stream)))
 
@@ -188,6 +199,11 @@ class MoeLayerRunner:
     def _shared_decode(self, x, nt, stream):
         S = self.shared
         moe_gate_up(S, x, x.stride(0), self.sh_ids, 1, self.sh_h, nt, stream)
+        moe_down_reduce(S, self.sh_h, self.sh_ids, self.sh_ones, 1, None, None, self.sh_y, nt, stream)
+
+    def _shared_decode_legacy(self, x, nt, stream):
+        S = self.shared
+        moe_gate_up(S, x, x.stride(0), self.sh_ids, 1, self.sh_h, nt, stream)
         moe_down(S, self.sh_h, self.sh_ids, self.sh_ones, 1, self.sh_y, nt, stream)
 
     def _shared_prefill(self, x, nt, stream):
@@ -201,11 +217,25 @@ class MoeLayerRunner:
         moe_gemm_down(S, self.sh_hq, nt, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_ones, self.sh_y, stream)
 
     def decode(self, x: torch.Tensor, bias=None, stream=None) -> torch.Tensor:
+        """Decode / short verify: router + Q8 of x, route + gate/up, down + combine (two more for a shared expert)."""
+        nt = x.shape[0]
+        moe_router_q8(self.W_r, self.W_r.shape[0], self.d, x, x.stride(0), self.logits, self.ls, self.vg, self.xq, nt, stream,
+                      bias=bias, bias_stride=0 if bias is None else bias.stride(0))
+        shexp = None
+        if self.shared is not None:
+            self._shared_decode(x, nt, stream)
+            shexp = self.sh_y
+        moe_route_gate_up(self.dev, self.logits, self.ls, self.E, self.k, self.xq, self.ids, self.wts, self.sg, self.h, nt, stream)
+        moe_down_reduce(self.dev, self.h, self.ids, self.wts, self.k, shexp, self.sg, self.out, nt, stream)
+        return self.out[:nt]
+
+    def decode_legacy(self, x: torch.Tensor, bias=None, stream=None) -> torch.Tensor:
+        """The same step through the reference-signature entry points (fp32 x and h in, quantized inside)."""
         nt = x.shape[0]
         self.route(x, nt, bias, stream)
         shexp = None
         if self.shared is not None:
-            self._shared_decode(x, nt, stream)
+            self._shared_decode_legacy(x, nt, stream)
             shexp = self.sh_y
         moe_gate_up(self.dev, x, x.stride(0), self.ids, self.k, self.h, nt, stream)
         moe_down_reduce(self.dev, self.h, self.ids, self.wts, self.k, shexp, self.sg, self.out, nt, stream)

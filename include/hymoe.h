@@ -114,7 +114,7 @@ int hy_moe_down(const hy_moe_dev *m, const float *h, const int32_t *ids, const f
    src/kernels4.cuh:77-80 / src/kernels4.cu:2063-2093).  xq: Q8 rows of the tokens (pair p reads row p / k);
    h [n_pairs][ff] fp32; hq: Q8 rows of h per pair; y[p][r] = wts[p] * (down_e[r] . hq[p]).
    n_pairs (not in the reference: its grid was one block per active expert) bounds the work items, chunks of
-   up to 32 tokens of one expert; max_active >= order_n[1] (<= 1024). */
+   up to 64 tokens of one expert; max_active >= order_n[1] (<= 1024). */
 int hy_moe_gemm_gate_up(const hy_moe_dev *m, const void *xq, int k, int n_pairs, const int32_t *order, const int32_t *order_n,
                         const int32_t *egrp, int max_active, float *h, hipStream_t s);
 int hy_moe_gemm_down(const hy_moe_dev *m, const void *hq, int n_pairs, const int32_t *order, const int32_t *order_n, const int32_t *egrp,
@@ -126,10 +126,24 @@ int hy_moe_gemm_down(const hy_moe_dev *m, const void *hq, int n_pairs, const int
 int hy_moe_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int32_t *ids,
                   hipStream_t s);
 
-/* Decode down + combine in one launch: out[t][r] as hy_moe_reduce of hy_moe_down's y, without materialising y
-   (fuses src/kernels4.cu:2007-2022 with :1182-1206; every expert must be local). */
+/* Decode down + combine in one launch: out[t][r] as hy_moe_reduce of hy_moe_down's y, without materialising y;
+   pairs whose expert is not local (or whose id is out of range) are left out of the sum
+   (fuses src/kernels4.cu:2007-2022 with :1182-1206). */
 int hy_moe_down_reduce(const hy_moe_dev *m, const float *h, const int32_t *ids, const float *wts, int k, const float *shexp,
                        const float *sg, float *out, int nt, hipStream_t s);
+
+/* Router logits and the Q8 rows of x in one launch: logits as hy_gemv_f32 (rows of W_r, stride ls >= rows) and xq as
+   hy_q8_quantize(vtype, x, xs, kdim, nt) -- fuses gemv_f32 (src/kernels4.cu:1910-1913) with the activation
+   quantization of the expert kernels.  nt > 8 runs the two steps as separate launches. */
+int hy_moe_router_q8(const float *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride, float *logits,
+                     int ls, int vtype, void *xq, int nt, hipStream_t s);
+
+/* Routing + decode gate/up in one launch: each token's softmax / top-k / weights / sg exactly as hy_moe_route
+   (written to ids, wts, sg), then h[t*k + j] as hy_moe_gate_up, from the Q8 rows xq (partner type of the gate
+   type, e.g. from hy_moe_router_q8).  Pairs whose expert is not local leave their h rows unwritten
+   (fuses moe_route and moe_gate_up, src/kernels4.cu:1925-1935 and :1973-2006). */
+int hy_moe_route_gate_up(const hy_moe_dev *m, const float *logits, int ls, int n_expert, int k, const void *xq, int32_t *ids, float *wts,
+                         float *sg, float *h, int nt, hipStream_t s);
 
 /* Test hooks.  One row of n weights dequantized by the kernels' block decoders (replaces deq_row_test,
    src/kernels4.cuh:181 / src/kernels4.cu:2036-2044); and the exact integers of every block of nrows weight rows

@@ -382,7 +382,7 @@ void or_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, flo
                     }
                 acc[L] = a;
             }
-            for (int off = 32; off > 0; off >>= 1) {
+            for (int off = 1; off < 64; off <<= 1) {
                 float nx[64];
                 for (int L = 0; L < 64; ++L) nx[L] = acc[L] + acc[L ^ off];
                 memcpy(acc, nx, sizeof acc);
@@ -390,11 +390,11 @@ void or_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, flo
             y[(size_t) t * ys + r] = acc[0];
         }
 }
-/* 64 partial sums (lane L: e = L + 64 i in order), then the xor butterfly */
+/* 64 partial sums (lane L: e = L + 64 i in order), then the xor butterfly 1, 2, ..., 32 */
 static float tree_sum64(const float *v, int n) {
     float acc[64];
     for (int L = 0; L < 64; ++L) { float a = 0.0f; for (int e = L; e < n; e += 64) a = a + v[e]; acc[L] = a; }
-    for (int off = 32; off > 0; off >>= 1) {
+    for (int off = 1; off < 64; off <<= 1) {
         float nx[64];
         for (int L = 0; L < 64; ++L) nx[L] = acc[L] + acc[L ^ off];
         memcpy(acc, nx, sizeof acc);

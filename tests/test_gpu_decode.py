@@ -1,0 +1,151 @@
+"""GPU parity of the three-launch decode path -- router + Q8 of x, route + gate/up, down + combine -- against the
+CPU oracle, through the C ABI.  Everything is compared bit for bit (the fp32 results share the oracle's
+expression order); the 2e-3 relative-L2 bound of the north star is asserted as well."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from hyper_amd import moe
+from hyper_amd.formats import GType, q8_row_bytes, vec_dot_type
+from tests.helpers import assert_bits_equal, gen, layer, oracle_layer, rel_l2
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+@pytest.mark.parametrize("E,d,nt,vt,with_sg,with_bias", [
+    (128, 2048, 1, GType.Q8_K, False, False),
+    (128, 2048, 8, GType.Q8_K, False, True),
+    (288, 4096, 4, GType.Q8_0, False, False),
+    (384, 7168, 8, GType.Q8_K, True, False),
+    (512, 2048, 3, GType.Q8_K, True, True),
+    (64, 512, 12, GType.Q8_0, True, False),     # more than 8 rows: the separate kernels
+])
+def test_router_q8_bitexact(cuda, E, d, nt, vt, with_sg, with_bias):
+    g = gen(1000 + E + nt)
+    rows = E + (1 if with_sg else 0)
+    W = torch.randn(rows, d, generator=g) * 0.02
+    x = torch.randn(nt, d, generator=g)
+    bias = torch.randn(nt, rows, generator=g) if with_bias else None
+    ref_log = orc.gemv_f32(W.numpy(), x.numpy())
+    if bias is not None:
+        ref_log = (ref_log + bias.numpy()).astype(np.float32)
+    ref_q = orc.quantize(vt, x.numpy())
+    logits = torch.full((nt, rows), float("nan"), device=cuda)
+    xq = torch.zeros(nt * q8_row_bytes(vt, d), dtype=torch.uint8, device=cuda)
+    moe.moe_router_q8(W.to(cuda), rows, d, x.to(cuda), d, logits, rows, vt, xq, nt,
+                      bias=bias.to(cuda) if bias is not None else None, bias_stride=rows if bias is not None else 0)
+    torch.cuda.synchronize()
+    assert_bits_equal(logits.cpu().numpy(), ref_log, "logits")
+    assert_bits_equal(xq.cpu().numpy().reshape(ref_q.shape), ref_q, "xq")
+
+
+ROUTE_GU_CASES = [
+    # tg, td, E, d, ff, k, nt, sg
+    (GType.Q4_K, GType.Q4_K, 128, 2048, 768, 8, 1, False),
+    (GType.Q4_K, GType.Q6_K, 128, 2048, 768, 8, 3, True),
+    (GType.Q5_K, GType.Q6_K, 40, 2048, 512, 10, 2, False),
+    (GType.IQ4_NL, GType.IQ4_NL, 24, 4096, 1536, 8, 1, False),
+    (GType.IQ4_XS, GType.IQ4_XS, 24, 4096, 1536, 8, 4, False),
+    (GType.IQ2_XS, GType.IQ2_XS, 16, 7168, 2048, 6, 2, True),
+    (GType.IQ4_NL, GType.IQ4_NL, 16, 2048, 4096, 8, 2, False),   # k * ff / 32 > 512: down falls back to the R-row kernel
+]
+
+
+def _logits(E, nt, sg, seed):
+    g = gen(seed)
+    return (torch.randn(nt, E + (1 if sg else 0), generator=g) * 1.5).numpy().astype(np.float32)
+
+
+@pytest.mark.parametrize("tg,td,E,d,ff,k,nt,sg", ROUTE_GU_CASES)
+def test_route_gate_up_and_down_bitexact(cuda, tg, td, E, d, ff, k, nt, sg):
+    L = layer(tg, td, E, ff, d, seed=700 + int(tg) + nt)
+    OL = oracle_layer(L)
+    dev = moe.upload_experts(L, device=cuda)
+    vg = vec_dot_type(tg)
+    for rep, rows in enumerate((nt, max(1, nt - 1))):
+        lg = _logits(E, rows, sg, 710 + rep)
+        ls = lg.shape[1]
+        ids_r, wts_r, sg_r = orc.route(lg, E, k, with_sg=sg)
+        x = torch.randn(rows, d, generator=gen(720 + rep))
+        out_r, h_r, _ = orc.moe_layer(OL, x.numpy(), ids_r, wts_r, want_hy=True)
+        xq = torch.from_numpy(orc.quantize(vg, x.numpy())).reshape(-1).to(cuda)
+        ids = torch.full((rows * k,), -5, dtype=torch.int32, device=cuda)
+        wts = torch.zeros(rows * k, device=cuda)
+        sgd = torch.zeros(rows, device=cuda) if sg else None
+        h = torch.full((rows * k, ff), float("nan"), device=cuda)
+        out = torch.full((rows, d), float("nan"), device=cuda)
+        moe.moe_route_gate_up(dev, torch.from_numpy(lg).to(cuda), ls, E, k, xq, ids, wts, sgd, h, rows)
+        moe.moe_down_reduce(dev, h, ids, wts, k, None, None, out, rows)
+        torch.cuda.synchronize()
+        assert_bits_equal(ids.cpu().numpy().reshape(rows, k), ids_r, f"ids rep {rep}")
+        assert_bits_equal(wts.cpu().numpy().reshape(rows, k), wts_r, f"wts rep {rep}")
+        if sg:
+            assert_bits_equal(sgd.cpu().numpy(), sg_r, f"sg rep {rep}")
+        assert_bits_equal(h.cpu().numpy(), h_r, f"h rep {rep}")
+        assert_bits_equal(out.cpu().numpy(), out_r, f"out rep {rep}")
+        assert rel_l2(out.cpu().numpy(), out_r) <= TOL
+
+
+def test_decode_skips_non_local_experts(cuda):
+    """Experts without a slot leave their h rows unwritten and drop out of the sum, as on the CPU."""
+    tg = td = GType.Q4_K
+    E, d, ff, k, nt = 12, 2048, 512, 4, 3
+    L = layer(tg, td, E, ff, d, seed=730)
+    slot = [(-1 if e in (2, 5, 7) else e) for e in range(E)]
+    dev = moe.upload_experts(L, slot=slot, device=cuda)
+    lg = _logits(E, nt, False, 731)
+    ids_r, wts_r, _ = orc.route(lg, E, k)
+    x = torch.randn(nt, d, generator=gen(732))
+    local = np.array([slot[e] >= 0 for e in ids_r.reshape(-1)]).reshape(ids_r.shape)
+    assert not local.all(), "the case must route some pairs to non-local experts"
+    ids_cpu = np.where(local, ids_r, -1).astype(np.int32)
+    out_r, h_r, _ = orc.moe_layer(oracle_layer(L), x.numpy(), ids_cpu, wts_r, want_hy=True)
+    xq = torch.from_numpy(orc.quantize(GType.Q8_K, x.numpy())).reshape(-1).to(cuda)
+    ids = torch.zeros(nt * k, dtype=torch.int32, device=cuda)
+    wts = torch.zeros(nt * k, device=cuda)
+    h = torch.full((nt * k, ff), float("nan"), device=cuda)
+    out = torch.zeros(nt, d, device=cuda)
+    moe.moe_route_gate_up(dev, torch.from_numpy(lg).to(cuda), E, E, k, xq, ids, wts, None, h, nt)
+    moe.moe_down_reduce(dev, h, ids, wts, k, None, None, out, nt)
+    torch.cuda.synchronize()
+    hv = h.cpu().numpy()
+    lv = local.reshape(-1)
+    assert_bits_equal(hv[lv], h_r[lv], "h of local pairs")
+    assert np.isnan(hv[~lv]).all()
+    assert_bits_equal(out.cpu().numpy(), out_r, "out")
+
+
+RUNNER_CASES = [
+    # tg, td, E, d, ff, k, nt, shared (type or None), sg_logit
+    (GType.Q4_K, GType.Q4_K, 128, 2048, 768, 8, 1, None, False),
+    (GType.IQ4_NL, GType.IQ4_NL, 24, 4096, 1536, 8, 4, None, False),
+    (GType.IQ4_XS, GType.IQ4_XS, 24, 4096, 1536, 8, 1, None, False),
+    (GType.IQ2_XS, GType.IQ2_XS, 16, 7168, 2048, 6, 1, GType.Q4_K, True),
+    (GType.IQ2_XS, GType.IQ2_XS, 16, 7168, 2048, 6, 8, GType.Q4_K, True),
+    (GType.Q5_K, GType.Q6_K, 32, 2048, 512, 10, 2, GType.Q5_K, False),
+]
+
+
+@pytest.mark.parametrize("tg,td,E,d,ff,k,nt,sh,sg_logit", RUNNER_CASES)
+def test_runner_decode_matches_oracle(cuda, tg, td, E, d, ff, k, nt, sh, sg_logit):
+    L = layer(tg, td, E, ff, d, seed=600 + E + nt)
+    S = layer(sh, GType.Q6_K if sh == GType.Q5_K else sh, 1, ff, d, seed=601) if sh is not None else None
+    g = gen(602)
+    W_r = torch.randn(E + (1 if sg_logit else 0), d, generator=g) * 0.02
+    x = torch.randn(nt, d, generator=g)
+    logits = orc.gemv_f32(W_r.numpy(), x.numpy())
+    ids, wts, sgv = orc.route(logits, E, k, with_sg=sg_logit)
+    out_r = orc.moe_layer(oracle_layer(L), x.numpy(), ids, wts, shared=oracle_layer(S) if S is not None else None,
+                          sg=sgv if sg_logit else None)
+    dev = moe.upload_experts(L, device=cuda)
+    sdev = moe.upload_experts(S, device=cuda) if S is not None else None
+    r = moe.MoeLayerRunner(dev, W_r.to(cuda), k, max_rows=8, shared=sdev, sg_logit=sg_logit)
+    xd = x.to(cuda)
+    out = r.decode(xd).clone()
+    out_legacy = r.decode_legacy(xd).clone()
+    torch.cuda.synchronize()
+    assert_bits_equal(out.cpu().numpy(), out_r, "runner.decode")
+    assert_bits_equal(out_legacy.cpu().numpy(), out_r, "runner.decode_legacy")
+    assert rel_l2(out.cpu().numpy(), out_r) <= TOL

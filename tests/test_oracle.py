@@ -267,7 +267,7 @@ def test_router_gemv_sum_order_and_value():
     y = orc.gemv_f32(W, x)
     ref = x.astype(np.float64) @ W.astype(np.float64).T
     assert np.abs(y - ref).max() <= 1e-5 * np.abs(x).max() * np.abs(W).max() * 2048 ** 0.5
-    # the contract's order, restated: 64 fma chains over e = 256 i + 4 L + j, then the xor butterfly
+    # the contract's order, restated: 64 fma chains over e = 256 i + 4 L + j, then the xor butterfly 1 .. 32
     w, xv = W[0], x[0]
     part = []
     for L in range(64):
@@ -278,7 +278,7 @@ def test_router_gemv_sum_order_and_value():
                 a = np.float32(np.float64(w[e]) * np.float64(xv[e]) + np.float64(a))   # fma: exact product, one rounding
         part.append(a)
     part = np.array(part, np.float32)
-    for off in (32, 16, 8, 4, 2, 1):
+    for off in (1, 2, 4, 8, 16, 32):
         part = (part + part[np.arange(64) ^ off]).astype(np.float32)
     assert part[0] == y[0, 0]
 
