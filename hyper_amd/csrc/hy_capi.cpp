@@ -71,6 +71,12 @@ size_t hy_q8_row_bytes(int vtype, int n) {
 
 int hy_upload_experts(const hy_expert_tensors *t, const int32_t *slot_host, int32_t ff, int32_t n, float clamp, hy_moe_dev *out) {
     if (!t || !slot_host || !out || !t->gate || !t->up || !t->down || t->E <= 0) { set_error("hy_upload_experts: null argument"); return HY_EINVAL; }
+    if (!dot_type(t->tg) || !dot_type(t->td)) { set_error("hy_upload_experts: unsupported expert type"); return HY_EUNSUPPORTED_TYPE; }
+    if (ff <= 0 || n <= 0 || ff % 256 || n % 256 || t->gb != (size_t) ff * (n / 256) * span_bytes(t->tg) ||
+        t->db != (size_t) n * (ff / 256) * span_bytes(t->td)) {
+        set_error("hy_upload_experts: ff and n must be multiples of 256 and gb/db the matrices' GGUF sizes");
+        return HY_EBAD_SHAPE;
+    }
     int nl = 0;
     for (int e = 0; e < t->E; ++e) nl = std::max(nl, slot_host[e] + 1);
     const size_t n_alloc = std::max(nl, 1);
@@ -80,12 +86,21 @@ int hy_upload_experts(const hy_expert_tensors *t, const int32_t *slot_host, int3
     if (err == hipSuccess) err = hipMalloc(&du, t->gb * n_alloc);
     if (err == hipSuccess) err = hipMalloc(&dd, t->db * n_alloc);
     if (err == hipSuccess) err = hipMalloc(&ds, sizeof(int32_t) * t->E);
+    // GGUF rows -> 16-row tiles (tiled_off), one expert matrix at a time through a host staging buffer
+    std::vector<uint8_t> stage(std::max(t->gb, t->db));
+    auto put = [&](uint8_t *dst, const uint8_t *src, int rows, int in_dim, int type) {
+        const int nspan = in_dim / 256, sb = span_bytes(type);
+        for (int r = 0; r < rows; ++r)
+            for (int sp = 0; sp < nspan; ++sp)
+                std::memcpy(stage.data() + tiled_off(r, sp, nspan, sb), src + ((size_t) r * nspan + sp) * sb, sb);
+        return hipMemcpy(dst, stage.data(), (size_t) rows * nspan * sb, hipMemcpyHostToDevice);
+    };
     for (int e = 0; err == hipSuccess && e < t->E; ++e) {
         if (slot_host[e] < 0) continue;
         const size_t sl = (size_t) slot_host[e];
-        err = hipMemcpy(dg + sl * t->gb, t->gate + (size_t) e * t->gb, t->gb, hipMemcpyHostToDevice);
-        if (err == hipSuccess) err = hipMemcpy(du + sl * t->gb, t->up + (size_t) e * t->gb, t->gb, hipMemcpyHostToDevice);
-        if (err == hipSuccess) err = hipMemcpy(dd + sl * t->db, t->down + (size_t) e * t->db, t->db, hipMemcpyHostToDevice);
+        err = put(dg + sl * t->gb, t->gate + (size_t) e * t->gb, ff, n, t->tg);
+        if (err == hipSuccess) err = put(du + sl * t->gb, t->up + (size_t) e * t->gb, ff, n, t->tg);
+        if (err == hipSuccess) err = put(dd + sl * t->db, t->down + (size_t) e * t->db, n, ff, t->td);
     }
     if (err == hipSuccess) err = hipMemcpy(ds, slot_host, sizeof(int32_t) * t->E, hipMemcpyHostToDevice);
     if (err != hipSuccess) {

@@ -66,6 +66,17 @@ __device__ __forceinline__ float hy_swiglu(float g, float u, float L) {
     return hy_silu(g) * u;
 }
 
+// ------------------------------------------------------------------ weight layout in HBM
+// Expert matrices are stored as 16-row tiles whose 256-value spans lie together: span s of row r at byte
+// ((r / 16) * nspan + s) * 16 * sb + (r % 16) * sb  (sb: bytes per 256 values, nspan = values per row / 256).
+// One K step of 16 rows is then one contiguous run (2304 bytes for Q4_K) instead of 16 pieces a row apart; the
+// GGUF block bytes themselves are unchanged.  hy_upload_experts writes this layout.
+constexpr int HY_TILE = 16;
+__host__ __device__ constexpr size_t tiled_off(int row, int span, int nspan, int sb) {
+    return ((size_t) (row >> 4) * nspan + span) * (size_t) (HY_TILE * sb) + (size_t) (row & 15) * sb;
+}
+__host__ __device__ constexpr int span_bytes(int t) { return block_bytes(t) * (256 / block_elems(t)); }
+
 // ------------------------------------------------------------------ wave helpers
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }

@@ -187,9 +187,8 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     const int ff = m.ff, ng = m.n / 256, nb = m.n / BE, items = 2 * ng;
     const int row = blockIdx.x * DEC_GU_WAVES + wave;
     if (row >= ff) return;  // wave-uniform; no block barrier follows
-    const size_t rb = m.gate_bytes / ff;
-    const uint8_t *Wg = m.gate + (size_t) slot * m.gate_bytes + (size_t) row * rb;
-    const uint8_t *Wu = m.up + (size_t) slot * m.gate_bytes + (size_t) row * rb;
+    const uint8_t *Wg = m.gate + (size_t) slot * m.gate_bytes + tiled_off(row, 0, ng, SPAN_W);
+    const uint8_t *Wu = m.up + (size_t) slot * m.gate_bytes + tiled_off(row, 0, ng, SPAN_W);
     const uint8_t *y = xq + (size_t) t * ng * SPAN_Y;
     Item<T> it[NP];
 #pragma unroll
@@ -197,7 +196,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
         const int i = g + 8 * ps;
         if (i < items) {
             const int mat = i >= ng, gi = i - mat * ng;
-            it[ps].load((mat ? Wu : Wg) + (size_t) gi * SPAN_W, L);
+            it[ps].load((mat ? Wu : Wg) + (size_t) gi * HY_TILE * SPAN_W, L);
         }
     }
     float *tw = tv[wave];
@@ -253,7 +252,6 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     const int n = m.n, ff = m.ff, ng = ff / 256, nb = ff / BE, items = k * ng;
     const int row = blockIdx.x * DEC_DN_WAVES + wave;
     const bool row_ok = row < n;
-    const size_t rb = m.down_bytes / n;
     // lane j < k: pair j's expert and slot (-1: skipped); `okm`: the valid pairs as a wave-uniform bit mask
     const int my_e = lane < k ? ids[t * k + lane] : -1;
     const int my_slot = (my_e >= 0 && my_e < m.n_expert) ? m.slot[my_e] : -1;
@@ -266,7 +264,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
             const int i = base + g + 8 * ps;
             const int j = i / ng, gi = i - j * ng;
             const int sl = __shfl(my_slot, j < 64 ? j : 0);
-            if (i < items && row_ok && sl >= 0) it[ps].load(m.down + (size_t) sl * m.down_bytes + (size_t) row * rb + (size_t) gi * SPAN_W, L);
+            if (i < items && row_ok && sl >= 0) it[ps].load(m.down + (size_t) sl * m.down_bytes + tiled_off(row, gi, ng, SPAN_W), L);
         }
     };
     // the first round of weight bytes goes out before the hidden rows are quantized

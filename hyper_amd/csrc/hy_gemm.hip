@@ -329,8 +329,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm(hy_moe_dev m, const uint8_t *__
     const int rows = GU ? m.ff : m.n, in_dim = GU ? m.n : m.ff, nsb = in_dim / 256;
     const int row = blockIdx.x * (GU ? 32 : GM_ROWS) + (GU ? (wave & 1) : wave) * 16 + rr;
     const bool row_ok = row < rows;
-    const size_t mbytes = GU ? m.gate_bytes : m.down_bytes, rb = mbytes / rows;
-    const uint8_t *Wrow = (GU ? (wave < 2 ? m.gate : m.up) : m.down) + (size_t) (row_ok ? row : rows - 1) * rb;
+    const size_t mbytes = GU ? m.gate_bytes : m.down_bytes;
+    // span b of this lane's row sits at Wrow + b * HY_TILE * BB (tiled weight layout)
+    const uint8_t *Wrow = (GU ? (wave < 2 ? m.gate : m.up) : m.down) + tiled_off(row_ok ? row : rows - 1, 0, nsb, BB);
     const size_t arow = (size_t) nsb * AB;
     const int my_tok = wave * 16 + (lane & 15);   // the token whose row pointer this lane carries (lanes 0..15)
 
@@ -379,7 +380,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(hy_moe_dev m, const uint8_t *__
             }
             if (lane < 16) dma_lds_b32(src_cur + (size_t) b * AB, lds_addr(Ys(stage) + wave * 16));
             __builtin_amdgcn_sched_barrier(0);
-            wr.load(Wrow + (size_t) s_item[it][2] * mbytes + (size_t) b * BB, q);
+            wr.load(Wrow + (size_t) s_item[it][2] * mbytes + (size_t) b * (HY_TILE * BB), q);
             __builtin_amdgcn_sched_barrier(0);
         };
 
@@ -536,8 +537,8 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
     const int orows = GU ? 32 : GM_ROWS;
     const int row = blockIdx.x * orows + (GU ? (wave & 1) : wave) * 16 + rr;
     const bool row_ok = row < rows;
-    const size_t mbytes = GU ? m.gate_bytes : m.down_bytes, rb = mbytes / rows;
-    const uint8_t *Wbase = (GU ? (wave < 2 ? m.gate : m.up) : m.down) + (size_t) (row_ok ? row : rows - 1) * rb;
+    const size_t mbytes = GU ? m.gate_bytes : m.down_bytes;
+    const uint8_t *Wbase = (GU ? (wave < 2 ? m.gate : m.up) : m.down) + tiled_off(row_ok ? row : rows - 1, 0, nsb, span_bytes(T));
     constexpr int AB = NL ? 8 * Q8_0_BYTES : Q8K_BYTES;   // activation bytes per 256 values
     const size_t arow = (size_t) nsb * AB;
     constexpr int BB = NL ? 8 * block_bytes(T) : block_bytes(T);   // weight bytes per 256 values
@@ -609,7 +610,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
         if (more) {
             if (last_b) nxt = locate(nit);
             const int nb = last_b ? 0 : b + 1;
-            nw.load(nxt.W + (size_t) nb * BB, q);
+            nw.load(nxt.W + (size_t) nb * (HY_TILE * BB), q);
             load_a(nxt.src, nb, a, yd);
         }
         __syncthreads();

@@ -65,7 +65,6 @@ __global__ __launch_bounds__(256) void k_gemv(hy_moe_dev m, int n_expert, const 
     const int nb = in_dim / BE, ng = in_dim / 256;
     const int nmat = GU ? 2 : 1;
     const size_t mbytes = GU ? m.gate_bytes : m.down_bytes;
-    const size_t rb = mbytes / rows;
     const uint8_t *W0 = (GU ? m.gate : m.down) + (size_t) slot * mbytes;
     const uint8_t *W1 = GU ? m.up + (size_t) slot * mbytes : nullptr;
     const float *xin = src + (size_t) (GU ? p / k : p) * ss;
@@ -84,7 +83,7 @@ __global__ __launch_bounds__(256) void k_gemv(hy_moe_dev m, int n_expert, const 
         const int id = g + 32 * i;
         if (id < items) {
             const int mat = id / (nr * ng), rem = id % (nr * ng), row = rem / ng, gi = rem % ng;
-            const uint8_t *base = (mat ? W1 : W0) + (size_t) (r0 + row) * rb + (size_t) gi * (256 / BE) * block_bytes(T);
+            const uint8_t *base = (mat ? W1 : W0) + tiled_off(r0 + row, gi, ng, span_bytes(T));
             it[i].load(base, L);
         }
     }
@@ -234,7 +233,6 @@ __global__ __launch_bounds__(256) void k_down_reduce(hy_moe_dev m, int n_expert,
         }
         for (int i = c; i < k; ++i) ord[i] = -1;
     }
-    const size_t rb = m.down_bytes / rows;
     const int g = threadIdx.x >> 3, L = threadIdx.x & 7;
     const int items = k * nr * ng;
     // pairs are indexed by j here (route rank); ord gives the summation order
@@ -247,7 +245,7 @@ __global__ __launch_bounds__(256) void k_down_reduce(hy_moe_dev m, int n_expert,
             const int e = ids[t * k + j];
             const int sl = (e >= 0 && e < n_expert) ? m.slot[e] : -1;
             if (sl >= 0) {
-                const uint8_t *base = m.down + (size_t) sl * m.down_bytes + (size_t) (r0 + row) * rb + (size_t) gi * (256 / BE) * block_bytes(T);
+                const uint8_t *base = m.down + (size_t) sl * m.down_bytes + tiled_off(r0 + row, gi, ng, span_bytes(T));
                 it[i].load(base, L);
             }
         }

@@ -28,10 +28,26 @@ def _s(stream) -> ctypes.c_void_p:
     return ctypes.c_void_p(stream.cuda_stream)
 
 
+def tile_rows(mat: torch.Tensor, in_dim: int) -> torch.Tensor:
+    """GGUF rows [E, rows, row_bytes] -> the kernels' tiled layout, same shape and bytes: 16-row tiles whose 256-value
+    spans lie together (span s of row r at ((r / 16) * nspan + s) * 16 * sb + (r % 16) * sb within an expert)."""
+    E, rows, rb = mat.shape
+    nspan = in_dim // 256
+    if rows % 16 or in_dim % 256 or rb % nspan:
+        raise ValueError(f"tile_rows: rows {rows} must be a multiple of 16 and in_dim {in_dim} of 256")
+    sb = rb // nspan
+    return mat.reshape(E, rows // 16, 16, nspan, sb).permute(0, 1, 3, 2, 4).contiguous().reshape(E, rows, rb)
+
+
 class MoeDev:
-    """Device expert weights + slot table (hy_moe_dev / MoeDev).  Keeps the tensors alive."""
+    """Device expert weights + slot table (hy_moe_dev / MoeDev).  Keeps the tensors alive.
+
+    `layer` holds GGUF rows on the device; they are re-laid into tiles (tile_rows) here, once, as the kernels read
+    them.  The raw layer is not kept."""
 
     def __init__(self, layer: ExpertLayer, slot: torch.Tensor):
+        layer = ExpertLayer(layer.tg, layer.td, layer.E, layer.ff, layer.n, tile_rows(layer.gate, layer.n),
+                            tile_rows(layer.up, layer.n), tile_rows(layer.down, layer.ff), layer.clamp)
         self.layer, self.slot = layer, slot
         c = hy_moe_dev()
         c.gate, c.up, c.down = layer.gate.data_ptr(), layer.up.data_ptr(), layer.down.data_ptr()

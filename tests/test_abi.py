@@ -69,3 +69,21 @@ def test_cpp_header_compiles(tmp_path):
     r = subprocess.run([gxx, "-std=c++17", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}",
                         "-I/opt/rocm/include", str(src)], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_tile_rows_layout():
+    """tile_rows puts span s of row r at ((r // 16) * nspan + s) * 16 * sb + (r % 16) * sb of each expert, and the
+    bytes of every span move whole."""
+    import torch
+    from hyper_amd.moe import tile_rows
+    E, rows, in_dim, sb = 2, 48, 1024, 144
+    nspan = in_dim // 256
+    raw = torch.randint(0, 256, (E, rows, nspan * sb), dtype=torch.uint8)
+    t = tile_rows(raw, in_dim).reshape(E, -1)
+    for e in range(E):
+        for r in (0, 1, 15, 16, 31, 47):
+            for s in range(nspan):
+                off = ((r // 16) * nspan + s) * 16 * sb + (r % 16) * sb
+                assert torch.equal(t[e, off:off + sb], raw[e, r, s * sb:(s + 1) * sb])
+    with pytest.raises(ValueError):
+        tile_rows(raw[:, :40], in_dim)

@@ -1,6 +1,9 @@
 """GPU parity of the three-launch decode path -- router + Q8 of x, route + gate/up, down + combine -- against the
 CPU oracle, through the C ABI.  Everything is compared bit for bit (the fp32 results share the oracle's
 expression order); the 2e-3 relative-L2 bound of the north star is asserted as well."""
+import ctypes
+import types
+
 import numpy as np
 import pytest
 import torch
@@ -149,3 +152,33 @@ def test_runner_decode_matches_oracle(cuda, tg, td, E, d, ff, k, nt, sh, sg_logi
     assert_bits_equal(out.cpu().numpy(), out_r, "runner.decode")
     assert_bits_equal(out_legacy.cpu().numpy(), out_r, "runner.decode_legacy")
     assert rel_l2(out.cpu().numpy(), out_r) <= TOL
+
+
+@pytest.mark.parametrize("tg,td", [(GType.Q4_K, GType.Q6_K), (GType.IQ4_NL, GType.IQ4_NL)])
+def test_c_abi_upload_matches_python_upload(cuda, tg, td):
+    """hy_upload_experts (host-side tiling) and the Python upload (device-side tiling) hand the kernels the same
+    bytes: the decode through either matches the oracle bit for bit."""
+    E, d, ff, k, nt = 12, 2048, 512, 4, 2
+    L = layer(tg, td, E, ff, d, seed=740 + int(tg))
+    slot = [(-1 if e == 3 else (E + 2 - e if e > 3 else e)) for e in range(E)]   # 0 1 2 -1 10 9 ... 3: unique
+    c = moe.upload_experts_c(L, slot)
+    try:
+        py = moe.upload_experts(L, slot=slot, device=cuda)
+        cd = types.SimpleNamespace(c=c, ref=ctypes.byref(c))
+        lg = _logits(E, nt, False, 741)
+        ids_r, wts_r, _ = orc.route(lg, E, k)
+        x = torch.randn(nt, d, generator=gen(742))
+        local = np.array([slot[e] >= 0 for e in ids_r.reshape(-1)]).reshape(ids_r.shape)
+        out_r = orc.moe_layer(oracle_layer(L), x.numpy(), np.where(local, ids_r, -1).astype(np.int32), wts_r)
+        xq = torch.from_numpy(orc.quantize(vec_dot_type(tg), x.numpy())).reshape(-1).to(cuda)
+        for dev in (cd, py):
+            ids = torch.zeros(nt * k, dtype=torch.int32, device=cuda)
+            wts = torch.zeros(nt * k, device=cuda)
+            h = torch.zeros(nt * k, ff, device=cuda)
+            out = torch.full((nt, d), float("nan"), device=cuda)
+            moe.moe_route_gate_up(dev, torch.from_numpy(lg).to(cuda), E, E, k, xq, ids, wts, None, h, nt)
+            moe.moe_down_reduce(dev, h, ids, wts, k, None, None, out, nt)
+            torch.cuda.synchronize()
+            assert_bits_equal(out.cpu().numpy(), out_r, "out")
+    finally:
+        moe.free_experts(c)
