@@ -270,44 +270,165 @@ __device__ __forceinline__ void dma_lds_b128(const void *g, uint32_t lds) {
 }
 __device__ __forceinline__ void store_f32(float *g, float v) { asm volatile("global_store_dword %0, %1, off" ::"v"(g), "v"(v) : "memory"); }
 
-constexpr int GM_STAGES = 3;         // activation stages in LDS, filled by DMA two steps ahead of their use
-constexpr int GM_MAX_ITEMS = 32;     // items per segment: their tables live in LDS (more items: one segment after another)
+// ------------------------------------------------------------------ the grouped GEMM stream
+// A block (8 waves, 512 threads, one per CU) owns 128 weight rows -- gate/up: 64 gate rows (waves 0-3) and the 64
+// up rows of the same outputs (waves 4-7); down: 128 rows -- and the work items blockIdx.y, + gridDim.y, ... (numbered
+// expert by expert, up to 64 tokens each).  Its steps, (item, 256-value span b) in order, form one stream.  Every
+// operand reaches LDS by DMA: a stage holds the 8 waves' 16-row weight tiles of span b (each one contiguous run of
+// the tiled layout) and the item's 64 activation rows of span b.  D stages rotate: step s computes from stage s % D
+// while the DMAs of steps s + 1 .. s + D - 1 are in flight.
+//
+// Waits are explicit.  Each wave issues the same L DMA instructions per step, and loads complete in issue order, so
+// "vmcnt <= (D - 2) L" right before issuing step s + D - 1 means this wave's step-s DMAs have landed; a barrier
+// then makes the whole stage visible and frees stage (s - 1) % D for the next issue.  Nothing in the stream is a
+// compiler-visible global load, so the compiler adds no waits of its own.  The epilogue's stores are not counted:
+// a store still in flight only makes a later wait stricter (loads cannot overtake the loads before them).
+constexpr int G5_WAVES = 8, G5_THREADS = 64 * G5_WAVES, G5_ROWS = 16 * G5_WAVES;
+constexpr int G5_ITEMS = 16;                  // items per segment (their tables live in LDS)
+constexpr int G5_LDS_STAGES = 150 * 1024;     // LDS for the stages (the tables take the rest of the 160 KB)
 
-// A block owns the items blockIdx.y, + gridDim.y, ... (numbered expert by expert, up to 64 tokens each) for its 64
-// weight rows (blockIdx.x).  Its steps -- (item, 256-value block b) in order -- form one stream: step s computes
-// from activation stage s % 3 and weight registers w[s % 3] while the DMA and the weight loads of step s + 2 are in
-// flight.  In every step the activation DMA is issued before the weight loads (a scheduling barrier keeps them
-// apart) and loads complete in order, so once w[s % 3] has landed this wave's stage-s DMA has too; a block
-// barrier then makes every wave's stage-s bytes visible and frees stage (s - 1) % 3 for the DMA of step s + 2.
+template <int T> struct G5 {
+    static constexpr int BB = block_bytes(T);                   // weight bytes per row and 256 values
+    static constexpr int TB = 16 * BB;                          // one wave's 16-row tile of a span
+    static constexpr int WB = G5_WAVES * TB;                    // weights of a stage
+    static constexpr int AB = GM_TOK * 256;                     // activation values of a stage (64 rows of 256)
+    static constexpr int SB = WB + AB + 4 * GM_TOK;             // + the rows' Q8_K d
+    static constexpr int D = 4 * SB <= G5_LDS_STAGES ? 4 : 3;   // stages
+    static constexpr int N4 = TB / 1024, NR = TB - 1024 * N4, N1 = (NR + 255) / 256;   // tile DMAs: 1 KB, then 256 B
+    static constexpr int L = N4 + N1 + 3;                       // DMA instructions per wave and step
+    static_assert(TB % 16 == 0 && NR % 4 == 0 && SB % 16 == 0, "DMA granules");
+    static_assert(D * SB <= G5_LDS_STAGES, "stages fit");
+    static_assert((D - 2) * L <= 63, "vmcnt range");
+};
+
+__device__ __forceinline__ v4i mfma64(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
+typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+// byte `b` of x in both 16-bit halves / in all four bytes
+__device__ __forceinline__ uint32_t bcast16(uint32_t x, int b) { return __builtin_amdgcn_perm(0u, x, 0x0C000C00u | (uint32_t) b | ((uint32_t) b << 16)); }
+__device__ __forceinline__ uint32_t bcast8(uint32_t x, int b) { return __builtin_amdgcn_perm(0u, x, 0x01010101u * (uint32_t) b); }
+// four bytes of q (each < 16) times the small factor f (< 8) held in both 16-bit halves: products < 128 stay in their bytes
+__device__ __forceinline__ int mul_bytes(uint32_t q, uint32_t f) {
+    const v2u16 r = __builtin_bit_cast(v2u16, q) * __builtin_bit_cast(v2u16, f);
+    return (int) __builtin_bit_cast(uint32_t, r);
+}
+
+// Q4_K step on the 16x16x64 MFMA.  MFMA j covers chunks 2j and 2j + 1: lane quarter q holds values 8 q .. + 7 of both
+// (A: two 8-byte pieces of the token row; B: the low and high nibbles of qs[32 j + 8 q ..]).  The 6-bit chunk scale
+// s = 8 a + b (a, b < 8) is applied inside the B operand: D1 = sum_c a_c dot_c and D2 = sum_c b_c dot_c (a q, b q < 128
+// fit int8), so sum_c s_c dot_c = 8 D1 + D2 exactly; a third MFMA against the chunk mins gives sum_c m_c sum(x_c).
+__device__ __forceinline__ void step_q4k(const uint8_t *wl, int q, const int8_t *as, int rr, int ntile, const float *yd,
+                                         float (&acc)[GM_TILES][4]) {
+    const uint4 hd = *(const uint4 *) wl;   // d | dmin, scales[12]
+    const uint32_t s_lo = hd.y & 0x3F3F3F3Fu, m_lo = hd.z & 0x3F3F3F3Fu;   // chunks 0..3, one per byte
+    const uint32_t s_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);         // chunks 4..7
+    const uint32_t m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+    const v4i z = {0, 0, 0, 0};
+    v4i d1[GM_TILES], d2[GM_TILES], dm[GM_TILES];
+#pragma unroll
+    for (int t = 0; t < GM_TILES; ++t) { d1[t] = z; d2[t] = z; dm[t] = z; }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint2 w = *(const uint2 *) (wl + 16 + 32 * j + 8 * q);
+        const uint32_t sp = j < 2 ? s_lo : s_hi, mp = j < 2 ? m_lo : m_hi;
+        const int c0 = (2 * j) & 3;
+        const uint32_t ah = (sp >> 3) & 0x07070707u, bl = sp & 0x07070707u;
+        const uint32_t a0 = bcast16(ah, c0), a1 = bcast16(ah, c0 + 1), b0 = bcast16(bl, c0), b1 = bcast16(bl, c0 + 1);
+        const uint32_t l0 = w.x & 0x0F0F0F0Fu, l1 = w.y & 0x0F0F0F0Fu, h0 = (w.x >> 4) & 0x0F0F0F0Fu, h1 = (w.y >> 4) & 0x0F0F0F0Fu;
+        const v4i B1 = {mul_bytes(l0, a0), mul_bytes(l1, a0), mul_bytes(h0, a1), mul_bytes(h1, a1)};
+        const v4i B2 = {mul_bytes(l0, b0), mul_bytes(l1, b0), mul_bytes(h0, b1), mul_bytes(h1, b1)};
+        const int mm0 = (int) bcast8(mp, c0), mm1 = (int) bcast8(mp, c0 + 1);
+        const v4i Bm = {mm0, mm0, mm1, mm1};
+#pragma unroll
+        for (int t = 0; t < GM_TILES; ++t) {
+            if (t >= ntile) break;
+            const long a_lo = a_frag<true>(as, t, rr, 2 * j, q), a_hi = a_frag<true>(as, t, rr, 2 * j + 1, q);
+            const v4i A = {(int) (uint32_t) a_lo, (int) (uint32_t) ((unsigned long long) a_lo >> 32), (int) (uint32_t) a_hi,
+                           (int) (uint32_t) ((unsigned long long) a_hi >> 32)};
+            d1[t] = mfma64(A, B1, d1[t]);
+            d2[t] = mfma64(A, B2, d2[t]);
+            dm[t] = mfma64(A, Bm, dm[t]);
+        }
+    }
+    const float d = h2f(hd.x & 0xffff), dmin = h2f(hd.x >> 16);
+#pragma unroll
+    for (int t = 0; t < GM_TILES; ++t) {
+        if (t >= ntile) break;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int si = (d1[t][v] << 3) + d2[t][v];
+            acc[t][v] = __builtin_fmaf(yd[t * 16 + 4 * q + v], __builtin_fmaf(d, (float) si, -(dmin * (float) dm[t][v])), acc[t][v]);
+        }
+    }
+}
+
+// One step's integer products and fold for NT token tiles (NT is uniform per item, so the code is straight-line)
+template <int T, int NT>
+__device__ __forceinline__ void step_math(const Raw<T> &wr, int q, const uint2 *grid, const int8_t *as, int rr, const float *yd,
+                                          float (&acc)[GM_TILES][4]) {
+    const v4i z = {0, 0, 0, 0};
+    int si[NT][4];
+    v4i sm[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) si[i][v] = 0;
+        sm[i] = z;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        uint32_t b0, b1;
+        int s0, s1, mn;
+        wr.chunk(c, q, grid, b0, b1, s0, s1, mn);
+        const uint32_t mb = __builtin_amdgcn_perm(0u, (uint32_t) mn, 0u);
+#pragma unroll
+        for (int tile = 0; tile < NT; ++tile) {
+            const long a = a_frag<true>(as, tile, rr, c, q);
+            if constexpr (Raw<T>::g16) {
+                const bool lo = q < 2;
+                const v4i d0 = mfma16(a, mk_long(lo ? b0 : 0u, lo ? b1 : 0u), z);
+                const v4i d1 = mfma16(a, mk_long(lo ? 0u : b0, lo ? 0u : b1), z);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) si[tile][v] += __mul24(s0, d0[v]) + __mul24(s1, d1[v]);
+            } else {
+                const v4i d0 = mfma16(a, mk_long(b0, b1), z);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) si[tile][v] += __mul24(s0, d0[v]);
+                if constexpr (Raw<T>::mins) sm[tile] = mfma16(a, mk_long(mb, mb), sm[tile]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);   // chunk by chunk: keeps the operands of one chunk live at a time
+    }
+#pragma unroll
+    for (int tile = 0; tile < NT; ++tile)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[tile][v] = __builtin_fmaf(yd[tile * 16 + 4 * q + v], wr.fold(si[tile][v], sm[tile][v]), acc[tile][v]);
+}
+
+template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
 template <int T, bool GU>
-__global__ __launch_bounds__(256, 2) void k_gemm(hy_moe_dev m, const uint8_t *__restrict__ aq, int a_div, const int *__restrict__ order,
-                                                 const int *__restrict__ order_n, const int *__restrict__ egrp, const float *__restrict__ wts,
-                                                 float *__restrict__ out) {
+__global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint8_t *__restrict__ aq, int a_div, const int *__restrict__ order,
+                                                        const int *__restrict__ order_n, const int *__restrict__ egrp, const float *__restrict__ wts,
+                                                        float *__restrict__ out) {
     static_assert(T != IQ4_NL, "IQ4_NL runs k_gemm_nl");
-    constexpr int AB = Q8K_BYTES;                                // activation bytes per 256 values (Q8_K)
-    constexpr int BB = block_bytes(T);                           // weight bytes per 256 values
-    // the three stages are separate objects, so that the compiler can tell a stage being read from the stages
-    // the DMA is filling (else it would wait for every outstanding DMA before each LDS read)
-    __shared__ __align__(16) int8_t As0[GM_TOK * 256], As1[GM_TOK * 256], As2[GM_TOK * 256];   // swizzled token rows
-    __shared__ __align__(16) uint32_t Ys0[GM_TOK], Ys1[GM_TOK], Ys2[GM_TOK];   // the Q8_K d (fp32) of each token
-    auto As = [&](int stage) -> int8_t * { return stage == 0 ? As0 : stage == 1 ? As1 : As2; };
-    auto Ys = [&](int stage) -> uint32_t * { return stage == 0 ? Ys0 : stage == 1 ? Ys1 : Ys2; };
+    using C = G5<T>;
+    constexpr int D = C::D, AQ = Q8K_BYTES;
+    __shared__ __align__(16) uint8_t smem[D * C::SB];   // stage s at s * SB: weights [wave][TB], activations [64][256], d [64]
     __shared__ int s_scan[1024 + 8];
-    __shared__ int s_item[GM_MAX_ITEMS][3];                       // first pair in order, tokens, weight slot
-    __shared__ int s_pair[GM_MAX_ITEMS][GM_TOK];                  // pair index of each token of the segment's items
-    __shared__ float s_wt[GU ? 1 : GM_MAX_ITEMS][GM_TOK];         // down: their route weights
-    __shared__ float s_up[GU ? 32 * GM_TOK : 1];
+    __shared__ int s_item[G5_ITEMS][3];                  // first pair in order, tokens, weight slot
+    __shared__ int s_pair[G5_ITEMS][GM_TOK];             // pair index of each token of the segment's items
+    __shared__ float s_wt[GU ? 1 : G5_ITEMS][GM_TOK];    // down: their route weights
     __shared__ uint2 grid[T == IQ2_XS ? 512 : 1];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, rr = lane & 15, q = lane >> 4;
     const int na = order_n[1];
-    // ---- items: expert group g owns ceil(cnt_g / GM_TOK) of them; s_scan = exclusive prefix (block-wide)
+    // ---- items: expert group g owns ceil(cnt_g / 64) of them; s_scan = exclusive prefix (block-wide)
     {
-        int c4[4], loc = 0;
+        int c2[2], loc = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int g = 4 * tid + i;
-            c4[i] = g < na ? (egrp[3 * g + 2] + GM_TOK - 1) / GM_TOK : 0;
-            loc += c4[i];
+        for (int i = 0; i < 2; ++i) {
+            const int g = 2 * tid + i;
+            c2[i] = g < na ? (egrp[3 * g + 2] + GM_TOK - 1) / GM_TOK : 0;
+            loc += c2[i];
         }
         int inc = loc;
 #pragma unroll
@@ -318,27 +439,30 @@ __global__ __launch_bounds__(256, 2) void k_gemm(hy_moe_dev m, const uint8_t *__
         for (int w = 0; w < wave; ++w) base += s_scan[1024 + w];
         int ex = base + inc - loc;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) { s_scan[4 * tid + i] = ex; ex += c4[i]; }
+        for (int i = 0; i < 2; ++i) { s_scan[2 * tid + i] = ex; ex += c2[i]; }
         if (T == IQ2_XS) expand_iq2xs_grid(grid);
         __syncthreads();
     }
-    const int total = s_scan[1024] + s_scan[1025] + s_scan[1026] + s_scan[1027];
+    int total = 0;
+    for (int w = 0; w < G5_WAVES; ++w) total += s_scan[1024 + w];
     const int y0 = blockIdx.y, ys = gridDim.y;
     const int my_items = total > y0 ? (total - 1 - y0) / ys + 1 : 0;
     if (my_items == 0) return;   // uniform over the block
-    const int rows = GU ? m.ff : m.n, in_dim = GU ? m.n : m.ff, nsb = in_dim / 256;
-    const int row = blockIdx.x * (GU ? 32 : GM_ROWS) + (GU ? (wave & 1) : wave) * 16 + rr;
-    const bool row_ok = row < rows;
+    const int in_dim = GU ? m.n : m.ff, nsb = in_dim / 256;
     const size_t mbytes = GU ? m.gate_bytes : m.down_bytes;
-    // span b of this lane's row sits at Wrow + b * HY_TILE * BB (tiled weight layout)
-    const uint8_t *Wrow = (GU ? (wave < 2 ? m.gate : m.up) : m.down) + tiled_off(row_ok ? row : rows - 1, 0, nsb, BB);
-    const size_t arow = (size_t) nsb * AB;
-    const int my_tok = wave * 16 + (lane & 15);   // the token whose row pointer this lane carries (lanes 0..15)
+    // this wave's 16 rows: tile index (rows / 16) in its matrix, and the output row of each lane
+    const int tile_row = GU ? blockIdx.x * 4 + (wave & 3) : blockIdx.x * G5_WAVES + wave;
+    const int row = 16 * tile_row + rr;
+    const uint8_t *Wmat = (GU ? (wave < 4 ? m.gate : m.up) : m.down) + (size_t) tile_row * nsb * C::TB;
+    const size_t arow = (size_t) nsb * AQ;
+    auto stage_w = [&](int s) { return smem + s * C::SB; };
+    auto stage_a = [&](int s) { return (int8_t *) (smem + s * C::SB + C::WB); };
+    auto stage_d = [&](int s) { return (const float *) (smem + s * C::SB + C::WB + C::AB); };
 
-    for (int seg = 0; seg < my_items; seg += GM_MAX_ITEMS) {
-        const int nit = min(GM_MAX_ITEMS, my_items - seg);
-        __syncthreads();   // readers of the previous segment's table are done
-        for (int i = tid; i < nit; i += 256) {
+    for (int seg = 0; seg < my_items; seg += G5_ITEMS) {
+        const int nit = min(G5_ITEMS, my_items - seg);
+        __syncthreads();   // readers of the previous segment's tables are done
+        for (int i = tid; i < nit; i += G5_THREADS) {
             const int item = y0 + (seg + i) * ys;
             int lo = 0, hi = na - 1;   // last group whose prefix <= item
             while (lo < hi) { const int mid = (lo + hi + 1) >> 1; if (s_scan[mid] <= item) lo = mid; else hi = mid - 1; }
@@ -348,8 +472,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(hy_moe_dev m, const uint8_t *__
             s_item[i][2] = m.slot[egrp[3 * lo]];
         }
         __syncthreads();
-        // the segment's pair indices (and down: route weights), with ordinary loads, before its stream starts
-        for (int i = tid; i < nit * GM_TOK; i += 256) {
+        for (int i = tid; i < nit * GM_TOK; i += G5_THREADS) {
             const int it = i / GM_TOK, tk = i - it * GM_TOK;
             const int pr = tk < s_item[it][1] ? order[s_item[it][0] + tk] : -1;
             s_pair[it][tk] = pr;
@@ -357,122 +480,128 @@ __global__ __launch_bounds__(256, 2) void k_gemm(hy_moe_dev m, const uint8_t *__
         }
         __syncthreads();
         const int nsteps = nit * nsb;
-        const uint8_t *src_cur = nullptr;
-        Raw<T> w[3];
-        auto issue = [&](int st, int stage, Raw<T> &wr) {
+
+        // ---- issue: step st's DMAs into stage `stage`.  Activation rows: this wave's tokens 8 wave + 4 i + lane / 16
+        // (lane l fetches 16-byte piece (l % 16) ^ (t % 16) of token t, the conflict-free layout the MFMA reads use)
+        // and, on lanes 0-7, the d of tokens 8 wave + lane; absent tokens re-read the item's first row (their LDS
+        // rows are never stored).
+        const uint8_t *arow_p[2], *drow_p;
+        auto issue = [&](int st, int stage) {
             const int it = st / nsb, b = st - it * nsb;
-            const int ntok = s_item[it][1];
             if (b == 0) {
-                const int pr = my_tok < ntok ? s_pair[it][my_tok] : -1;
-                src_cur = pr >= 0 ? aq + (size_t) (GU ? pr / a_div : pr) * arow : aq;
-            }
-            // activations of step st -> stage: one DMA per token row of this wave, then the scales.  Every step issues
-            // the same instructions (rows of absent tokens point at row 0 of the activations: harmless reads into LDS
-            // rows nobody uses), so the compiler can count the loads in flight and wait for exactly one step.
-            int8_t *as = As(stage);
-            const uint64_t sp = (uint64_t) src_cur;
+                const int ntok = s_item[it][1];
+                const int p0 = s_pair[it][0];
 #pragma unroll
-            for (int i4 = 0; i4 < 4; ++i4) {   // tokens wave*16 + 4 i4 .. + 3: lane l takes piece (l % 16) ^ (t % 16) of token l / 16
-                const int t16 = 4 * i4 + (lane >> 4), tk = wave * 16 + t16;
-                const uint8_t *rowp = (const uint8_t *) __shfl(sp, t16);
-                const int piece = (lane & 15) ^ (tk & 15);
-                dma_lds_b128(rowp + (size_t) b * AB + 4 + 16 * piece, lds_addr(as + (wave * 16 + 4 * i4) * 256));
+                for (int i = 0; i < 2; ++i) {
+                    const int t = 8 * wave + 4 * i + (lane >> 4);
+                    const int pr = t < ntok ? s_pair[it][t] : p0;
+                    arow_p[i] = aq + (size_t) (GU ? pr / a_div : pr) * arow;
+                }
+                const int td = 8 * wave + (lane & 7);
+                const int prd = td < ntok ? s_pair[it][td] : p0;
+                drow_p = aq + (size_t) (GU ? prd / a_div : prd) * arow;
             }
-            if (lane < 16) dma_lds_b32(src_cur + (size_t) b * AB, lds_addr(Ys(stage) + wave * 16));
-            __builtin_amdgcn_sched_barrier(0);
-            wr.load(Wrow + (size_t) s_item[it][2] * mbytes + (size_t) b * (HY_TILE * BB), q);
-            __builtin_amdgcn_sched_barrier(0);
+            const uint8_t *wsrc = Wmat + (size_t) __builtin_amdgcn_readfirstlane(s_item[it][2]) * mbytes + (size_t) b * C::TB;
+            const uint32_t wdst = lds_addr(stage_w(stage) + wave * C::TB);
+#pragma unroll
+            for (int i = 0; i < C::N4; ++i) dma_lds_b128(wsrc + 1024 * i + 16 * lane, wdst + 1024 * i);
+#pragma unroll
+            for (int j = 0; j < C::N1; ++j)
+                if (256 * j + 4 * lane < C::NR) dma_lds_b32(wsrc + 1024 * C::N4 + 256 * j + 4 * lane, wdst + 1024 * C::N4 + 256 * j);
+            int8_t *as = stage_a(stage);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int t = 8 * wave + 4 * i + (lane >> 4);
+                const int piece = (lane & 15) ^ (t & 15);
+                dma_lds_b128(arow_p[i] + (size_t) b * AQ + 4 + 16 * piece, lds_addr(as + (8 * wave + 4 * i) * 256));
+            }
+            if (lane < 8) dma_lds_b32(drow_p + (size_t) b * AQ, lds_addr(stage_d(stage) + 8 * wave));
         };
 
-        // compute side
-        float acc[GM_TILES][4], ep_val[GM_TILES][4];
-        int ep_it = -1;
+        float acc[GM_TILES][4];
 #pragma unroll
         for (int i = 0; i < GM_TILES; ++i)
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[i][v] = 0.0f;
-        auto compute = [&](int st, int stage, const Raw<T> &wr) {
+        auto compute = [&](int st, int stage) {
             const int it = st / nsb, b = st - it * nsb;
-            const int ntok = s_item[it][1], ntile = (ntok + 15) / 16;
-            const int8_t *as = As(stage);
-            {
-                int si[GM_TILES][4];
-                v4i sm[GM_TILES];
+            const int ntok = __builtin_amdgcn_readfirstlane(s_item[it][1]), ntile = (ntok + 15) >> 4;   // uniform
+            const int8_t *as = stage_a(stage);
+            const float *yd = stage_d(stage);
+            if constexpr (T == Q4_K) step_q4k(stage_w(stage) + wave * C::TB + rr * C::BB, q, as, rr, ntile, yd, acc);
+            else {
+            Raw<T> wr;
+            wr.load(stage_w(stage) + wave * C::TB + rr * C::BB, q);
+            int si[GM_TILES][4];
+            v4i sm[GM_TILES];
 #pragma unroll
-                for (int i = 0; i < GM_TILES; ++i) {
+            for (int i = 0; i < GM_TILES; ++i) {
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) si[i][v] = 0;
-                    sm[i] = v4i{0, 0, 0, 0};
-                }
-#pragma unroll
-                for (int c = 0; c < 8; ++c) chunk_ints<T, true>(wr, c, q, grid, as, rr, ntile, si, sm);
-                const float *yd = (const float *) Ys(stage);
-#pragma unroll
-                for (int tile = 0; tile < GM_TILES; ++tile) {
-                    if (tile >= ntile) break;
-#pragma unroll
-                    for (int v = 0; v < 4; ++v)
-                        acc[tile][v] = __builtin_fmaf(yd[tile * 16 + 4 * q + v], wr.fold(si[tile][v], sm[tile][v]), acc[tile][v]);
-                }
+                for (int v = 0; v < 4; ++v) si[i][v] = 0;
+                sm[i] = v4i{0, 0, 0, 0};
             }
-            if (b == nsb - 1) {   // the item's outputs: into ep_val now, to memory at the start of the next step
-                if (GU && wave >= 2) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) chunk_ints<T, true>(wr, c, q, grid, as, rr, ntile, si, sm);
+#pragma unroll
+            for (int tile = 0; tile < GM_TILES; ++tile) {
+                if (tile >= ntile) break;
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    acc[tile][v] = __builtin_fmaf(yd[tile * 16 + 4 * q + v], wr.fold(si[tile][v], sm[tile][v]), acc[tile][v]);
+            }
+            }
+            if (b != nsb - 1) return;
+            // ---- the item's outputs
+            if (GU) {
+                // SwiGLU needs the up rows of waves 4-7 in waves 0-3: exchanged through this stage's activation
+                // area (64 rows x 64 tokens of fp32), once every wave has finished reading it
+                float *s_up = (float *) stage_a(stage);
+                lds_barrier();
+                if (wave >= 4) {
 #pragma unroll
                     for (int tile = 0; tile < GM_TILES; ++tile)
 #pragma unroll
-                        for (int v = 0; v < 4; ++v) s_up[((wave & 1) * 16 + rr) * GM_TOK + tile * 16 + 4 * q + v] = acc[tile][v];
+                        for (int v = 0; v < 4; ++v) s_up[((wave & 3) * 16 + rr) * GM_TOK + tile * 16 + 4 * q + v] = acc[tile][v];
                 }
-                if (GU) lds_barrier();
+                lds_barrier();
+                if (wave < 4) {
+#pragma unroll
+                    for (int tile = 0; tile < GM_TILES; ++tile)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            const int tok = tile * 16 + 4 * q + v;
+                            if (tok < ntok)
+                                store_f32(out + (size_t) s_pair[it][tok] * m.ff + row,
+                                          hy_swiglu(acc[tile][v], s_up[((wave & 3) * 16 + rr) * GM_TOK + tok], m.clamp));
+                        }
+                }
+            } else {
 #pragma unroll
                 for (int tile = 0; tile < GM_TILES; ++tile)
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
                         const int tok = tile * 16 + 4 * q + v;
-                        if (GU) ep_val[tile][v] = wave < 2 && tile < ntile ? hy_swiglu(acc[tile][v], s_up[((wave & 1) * 16 + rr) * GM_TOK + tok], m.clamp) : 0.0f;
-                        else ep_val[tile][v] = tile < ntile ? s_wt[GU ? 0 : it][tok] * acc[tile][v] : 0.0f;
-                        acc[tile][v] = 0.0f;
-                    }
-                ep_it = it;
-            }
-        };
-        // the stored item's outputs (rows of this wave that exist, tokens of the item)
-        auto flush_ep = [&]() {
-            if (ep_it < 0) return;
-            const int ntok = s_item[ep_it][1];
-            if (row_ok && (!GU || wave < 2)) {
-#pragma unroll
-                for (int tile = 0; tile < GM_TILES; ++tile)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const int tok = tile * 16 + 4 * q + v;
-                        if (tok < ntok) store_f32(out + (size_t) s_pair[ep_it][tok] * (GU ? m.ff : m.n) + row, ep_val[tile][v]);
+                        if (tok < ntok) store_f32(out + (size_t) s_pair[it][tok] * m.n + row, s_wt[GU ? 0 : it][tok] * acc[tile][v]);
                     }
             }
-            ep_it = -1;
+#pragma unroll
+            for (int tile = 0; tile < GM_TILES; ++tile)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[tile][v] = 0.0f;
         };
 
-        // the stream: steps 0 and 1 issued ahead, then per step: wait for its bytes, barrier, issue step + 2, compute
-        issue(0, 0, w[0]);
-        issue(min(1, nsteps - 1), 1, w[1]);
-#define HY_GM_STEP(U)                                                                          \
-        {                                                                                      \
-            const int st = s0 + U;                                                             \
-            if (st >= nsteps) break;                                                           \
-            touch_regs(w[U]);                                                                  \
-            lds_barrier();                                                                     \
-            flush_ep();                                                                        \
-            issue(min(st + 2, nsteps - 1), (U + 2) % 3, w[(U + 2) % 3]);   /* past the end: a harmless repeat */ \
-            compute(st, U, w[U]);                                                              \
+        // the stream: steps 0 .. D - 2 issued ahead; past the end, the last step is issued again (into the stage
+        // of step s - 1, which nobody reads any more) so that every wait counts the same instructions
+#pragma unroll
+        for (int s = 0; s < D - 1; ++s) issue(min(s, nsteps - 1), s);
+        for (int st = 0; st < nsteps; ++st) {
+            wait_vm<(D - 2) * C::L>();
+            lds_barrier();
+            issue(min(st + D - 1, nsteps - 1), (st + D - 1) % D);
+            compute(st, st % D);
         }
-        for (int s0 = 0; s0 < nsteps; s0 += 3) {
-            HY_GM_STEP(0)
-            HY_GM_STEP(1)
-            HY_GM_STEP(2)
-        }
-#undef HY_GM_STEP
-        flush_ep();
+        wait_vm<0>();   // no DMA into this block's LDS may outlive the segment
     }
-    __builtin_amdgcn_s_waitcnt(0);   // no DMA into this block's LDS may outlive it
 }
 
 // IQ4_NL: one chunk's MFMA per tile folded straight into the fp32 accumulators (Yc: 8 block scales per token)
@@ -690,7 +819,7 @@ static int max_items(int n_pairs, int max_active) { return (n_pairs + GM_TOK - 1
 static int item_slots(int row_tiles, int n_pairs, int max_active, int per_cu) {
     static int cus = 0;
     if (!cus) { int dev = 0; hipDeviceProp_t pr; if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&pr, dev) == hipSuccess) cus = pr.multiProcessorCount; if (cus <= 0) cus = 256; }
-    const int want = (cus * per_cu + row_tiles - 1) / row_tiles;
+    const int want = cus * per_cu / row_tiles;   // every block resident at once
     return std::max(1, std::min(max_items(n_pairs, max_active), want));
 }
 
@@ -703,8 +832,9 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
         hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
         return check_launch("hy_moe_gemm_gate_up");
     }
-    dim3 grid(rt, item_slots(rt, n_pairs, max_active, 2));
-    HY_GEMM_SWITCH(m.tg, hipLaunchKernelGGL((k_gemm<TT, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp,
+    const int rb = m.ff / 64;
+    dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
+    HY_GEMM_SWITCH(m.tg, hipLaunchKernelGGL((k_gemm<TT, true>), grid, dim3(G5_THREADS), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp,
                                             nullptr, h);
                    return check_launch("hy_moe_gemm_gate_up"));
 }
@@ -717,8 +847,9 @@ int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int
         hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
         return check_launch("hy_moe_gemm_down");
     }
-    dim3 grid(rt, item_slots(rt, n_pairs, max_active, 2));
-    HY_GEMM_SWITCH(m.td, hipLaunchKernelGGL((k_gemm<TT, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp,
+    const int rb = m.n / G5_ROWS;
+    dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
+    HY_GEMM_SWITCH(m.td, hipLaunchKernelGGL((k_gemm<TT, false>), grid, dim3(G5_THREADS), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp,
                                             wts, y);
                    return check_launch("hy_moe_gemm_down"));
 }
