@@ -268,6 +268,24 @@ __device__ __forceinline__ void dma_lds_b128(const void *g, uint32_t lds) {
     asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
                  : "=&s"(keep) : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
+// The same with a wave-uniform base address in SGPRs and a per-lane 32-bit byte offset (no 64-bit address math per lane)
+__device__ __forceinline__ uint64_t sgpr_ptr(const void *p) {   // p is uniform; this makes the compiler keep it in SGPRs
+    const uint64_t v = (uint64_t) p;
+    // readfirstlane returns int: each half goes through uint32_t so that the low half does not sign-extend
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (v >> 32));
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) v);
+    return ((uint64_t) hi << 32) | lo;
+}
+__device__ __forceinline__ void dma_s32(const void *base, uint32_t voff, uint32_t lds) {
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(voff), "s"(sgpr_ptr(base)), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+__device__ __forceinline__ void dma_s128(const void *base, uint32_t voff, uint32_t lds) {
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(voff), "s"(sgpr_ptr(base)), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
 __device__ __forceinline__ void store_f32(float *g, float v) { asm volatile("global_store_dword %0, %1, off" ::"v"(g), "v"(v) : "memory"); }
 
 // ------------------------------------------------------------------ the grouped GEMM stream
@@ -419,7 +437,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
     __shared__ int s_pair[G5_ITEMS][GM_TOK];             // pair index of each token of the segment's items
     __shared__ float s_wt[GU ? 1 : G5_ITEMS][GM_TOK];    // down: their route weights
     __shared__ uint2 grid[T == IQ2_XS ? 512 : 1];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, rr = lane & 15, q = lane >> 4;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, rr = lane & 15, q = lane >> 4;
     const int na = order_n[1];
     // ---- items: expert group g owns ceil(cnt_g / 64) of them; s_scan = exclusive prefix (block-wide)
     {
@@ -481,13 +499,16 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
         __syncthreads();
         const int nsteps = nit * nsb;
 
-        // ---- issue: step st's DMAs into stage `stage`.  Activation rows: this wave's tokens 8 wave + 4 i + lane / 16
-        // (lane l fetches 16-byte piece (l % 16) ^ (t % 16) of token t, the conflict-free layout the MFMA reads use)
-        // and, on lanes 0-7, the d of tokens 8 wave + lane; absent tokens re-read the item's first row (their LDS
-        // rows are never stored).
-        const uint8_t *arow_p[2], *drow_p;
-        auto issue = [&](int st, int stage) {
-            const int it = st / nsb, b = st - it * nsb;
+        // ---- issue: the DMAs of step (iss_it, iss_b) into stage iss_stage, then advance (staying on the last step
+        // once there).  Activation rows: this wave's tokens 8 wave + 4 i + lane / 16 (lane l fetches 16-byte piece
+        // (l % 16) ^ (t % 16) of token t, the conflict-free layout the MFMA reads use) and, on lanes 0-7, the d of
+        // tokens 8 wave + lane; absent tokens re-read the item's first row (their LDS rows are never stored).
+        // Offsets are bytes from aq (the caller's activations stay below 4 GB).
+        uint32_t aoff[2], doff;
+        int iss_it = 0, iss_b = 0, iss_stage = 0, iss_step = 0;
+        const uint32_t lane16 = 16 * lane, lane4 = 4 * lane;
+        auto issue = [&]() {
+            const int it = iss_it, b = iss_b;
             if (b == 0) {
                 const int ntok = s_item[it][1];
                 const int p0 = s_pair[it][0];
@@ -495,27 +516,30 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
                 for (int i = 0; i < 2; ++i) {
                     const int t = 8 * wave + 4 * i + (lane >> 4);
                     const int pr = t < ntok ? s_pair[it][t] : p0;
-                    arow_p[i] = aq + (size_t) (GU ? pr / a_div : pr) * arow;
+                    aoff[i] = (uint32_t) (GU ? pr / a_div : pr) * (uint32_t) arow + 4 + 16 * ((lane & 15) ^ (t & 15));
                 }
                 const int td = 8 * wave + (lane & 7);
                 const int prd = td < ntok ? s_pair[it][td] : p0;
-                drow_p = aq + (size_t) (GU ? prd / a_div : prd) * arow;
+                doff = (uint32_t) (GU ? prd / a_div : prd) * (uint32_t) arow;
             }
+            const int stage = iss_stage;
             const uint8_t *wsrc = Wmat + (size_t) __builtin_amdgcn_readfirstlane(s_item[it][2]) * mbytes + (size_t) b * C::TB;
             const uint32_t wdst = lds_addr(stage_w(stage) + wave * C::TB);
 #pragma unroll
-            for (int i = 0; i < C::N4; ++i) dma_lds_b128(wsrc + 1024 * i + 16 * lane, wdst + 1024 * i);
+            for (int i = 0; i < C::N4; ++i) dma_s128(wsrc + 1024 * i, lane16, wdst + 1024 * i);
 #pragma unroll
             for (int j = 0; j < C::N1; ++j)
-                if (256 * j + 4 * lane < C::NR) dma_lds_b32(wsrc + 1024 * C::N4 + 256 * j + 4 * lane, wdst + 1024 * C::N4 + 256 * j);
-            int8_t *as = stage_a(stage);
+                if (256 * j + 4 * lane < C::NR) dma_s32(wsrc + 1024 * C::N4 + 256 * j, lane4, wdst + 1024 * C::N4 + 256 * j);
+            const uint32_t bo = (uint32_t) b * AQ;
+            const uint32_t adst = lds_addr(stage_a(stage) + 8 * wave * 256);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int t = 8 * wave + 4 * i + (lane >> 4);
-                const int piece = (lane & 15) ^ (t & 15);
-                dma_lds_b128(arow_p[i] + (size_t) b * AQ + 4 + 16 * piece, lds_addr(as + (8 * wave + 4 * i) * 256));
+            for (int i = 0; i < 2; ++i) dma_s128(aq, aoff[i] + bo, adst + 1024 * i);
+            if (lane < 8) dma_s32(aq, doff + bo, lds_addr(stage_d(stage) + 8 * wave));
+            if (iss_step < nsteps - 1) {
+                ++iss_step;
+                if (++iss_b == nsb) { iss_b = 0; ++iss_it; }
             }
-            if (lane < 8) dma_lds_b32(drow_p + (size_t) b * AQ, lds_addr(stage_d(stage) + 8 * wave));
+            iss_stage = iss_stage == D - 1 ? 0 : iss_stage + 1;
         };
 
         float acc[GM_TILES][4];
@@ -523,8 +547,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
         for (int i = 0; i < GM_TILES; ++i)
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[i][v] = 0.0f;
-        auto compute = [&](int st, int stage) {
-            const int it = st / nsb, b = st - it * nsb;
+        auto compute = [&](int it, int b, int stage) {
             const int ntok = __builtin_amdgcn_readfirstlane(s_item[it][1]), ntile = (ntok + 15) >> 4;   // uniform
             const int8_t *as = stage_a(stage);
             const float *yd = stage_d(stage);
@@ -593,12 +616,14 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
         // the stream: steps 0 .. D - 2 issued ahead; past the end, the last step is issued again (into the stage
         // of step s - 1, which nobody reads any more) so that every wait counts the same instructions
 #pragma unroll
-        for (int s = 0; s < D - 1; ++s) issue(min(s, nsteps - 1), s);
-        for (int st = 0; st < nsteps; ++st) {
+        for (int s = 0; s < D - 1; ++s) issue();
+        for (int st = 0, it = 0, b = 0, stage = 0; st < nsteps; ++st) {
             wait_vm<(D - 2) * C::L>();
             lds_barrier();
-            issue(min(st + D - 1, nsteps - 1), (st + D - 1) % D);
-            compute(st, st % D);
+            issue();
+            compute(it, b, stage);
+            if (++b == nsb) { b = 0; ++it; }
+            stage = stage == D - 1 ? 0 : stage + 1;
         }
         wait_vm<0>();   // no DMA into this block's LDS may outlive the segment
     }
@@ -833,6 +858,7 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
         return check_launch("hy_moe_gemm_gate_up");
     }
     const int rb = m.ff / 64;
+    if ((size_t) n_pairs * (m.n / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_gate_up: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
     dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
     HY_GEMM_SWITCH(m.tg, hipLaunchKernelGGL((k_gemm<TT, true>), grid, dim3(G5_THREADS), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp,
                                             nullptr, h);
@@ -848,6 +874,7 @@ int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int
         return check_launch("hy_moe_gemm_down");
     }
     const int rb = m.n / G5_ROWS;
+    if ((size_t) n_pairs * (m.ff / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_down: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
     dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
     HY_GEMM_SWITCH(m.td, hipLaunchKernelGGL((k_gemm<TT, false>), grid, dim3(G5_THREADS), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp,
                                             wts, y);
