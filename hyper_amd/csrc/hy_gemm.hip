@@ -432,39 +432,51 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
     using C = G5<T>;
     constexpr int D = C::D, AQ = Q8K_BYTES;
     __shared__ __align__(16) uint8_t smem[D * C::SB];   // stage s at s * SB: weights [wave][TB], activations [64][256], d [64]
-    __shared__ int s_scan[1024 + 8];
+    __shared__ uint64_t s_scan[1024 + 8];                // per expert group: exclusive prefix of its items per tile class
     __shared__ int s_item[G5_ITEMS][3];                  // first pair in order, tokens, weight slot
     __shared__ int s_pair[G5_ITEMS][GM_TOK];             // pair index of each token of the segment's items
     __shared__ float s_wt[GU ? 1 : G5_ITEMS][GM_TOK];    // down: their route weights
     __shared__ uint2 grid[T == IQ2_XS ? 512 : 1];
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, rr = lane & 15, q = lane >> 4;
     const int na = order_n[1];
-    // ---- items: expert group g owns ceil(cnt_g / 64) of them; s_scan = exclusive prefix (block-wide)
+    // ---- items.  Expert group g (cnt tokens) owns ceil(cnt / 64) items: full ones of 4 token tiles and a last one of
+    // ceil(rem / 16) tiles.  Items are ordered by tile count (class 4: full items and last items of 4 tiles, expert by
+    // expert; then the last items of 3, 2 and 1 tiles) and dealt to the gridDim.y item slots in snake order (slot y
+    // takes positions k S + y for even k and k S + S - 1 - y for odd k), which evens out the slots' work.
+    // s_scan holds each group's exclusive prefix of the four class counts, 16 bits each (item totals stay below 2^16).
     {
-        int c2[2], loc = 0;
+        uint64_t c2[2], loc = 0;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int g = 2 * tid + i;
-            c2[i] = g < na ? (egrp[3 * g + 2] + GM_TOK - 1) / GM_TOK : 0;
-            loc += c2[i];
+            uint64_t c = 0;
+            if (g < na) {
+                const int cnt = egrp[3 * g + 2], n = (cnt + GM_TOK - 1) / GM_TOK, cl = (cnt - GM_TOK * (n - 1) + 15) >> 4;
+                c = (uint64_t) (n - 1 + (cl == 4)) | ((uint64_t) (cl == 3) << 16) | ((uint64_t) (cl == 2) << 32) | ((uint64_t) (cl == 1) << 48);
+            }
+            c2[i] = c;
+            loc += c;
         }
-        int inc = loc;
+        uint64_t inc = loc;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) { const int t = __shfl_up(inc, o); if (lane >= o) inc += t; }
+        for (int o = 1; o < 64; o <<= 1) { const uint64_t t = __shfl_up(inc, o); if (lane >= o) inc += t; }
         if (lane == 63) s_scan[1024 + wave] = inc;
         __syncthreads();
-        int base = 0;
+        uint64_t base = 0;
         for (int w = 0; w < wave; ++w) base += s_scan[1024 + w];
-        int ex = base + inc - loc;
+        uint64_t ex = base + inc - loc;
 #pragma unroll
         for (int i = 0; i < 2; ++i) { s_scan[2 * tid + i] = ex; ex += c2[i]; }
         if (T == IQ2_XS) expand_iq2xs_grid(grid);
         __syncthreads();
     }
-    int total = 0;
-    for (int w = 0; w < G5_WAVES; ++w) total += s_scan[1024 + w];
+    uint64_t tot = 0;
+    for (int w = 0; w < G5_WAVES; ++w) tot += s_scan[1024 + w];
+    const int n4 = (int) (tot & 0xffff), n3 = (int) ((tot >> 16) & 0xffff), n2 = (int) ((tot >> 32) & 0xffff), n1 = (int) (tot >> 48);
+    const int total = n4 + n3 + n2 + n1;
     const int y0 = blockIdx.y, ys = gridDim.y;
-    const int my_items = total > y0 ? (total - 1 - y0) / ys + 1 : 0;
+    const int rounds = total / ys, rem_items = total - rounds * ys;
+    const int my_items = rounds + (((rounds & 1) ? ys - 1 - y0 : y0) < rem_items ? 1 : 0);
     if (my_items == 0) return;   // uniform over the block
     const int in_dim = GU ? m.n : m.ff, nsb = in_dim / 256;
     const size_t mbytes = GU ? m.gate_bytes : m.down_bytes;
@@ -481,12 +493,20 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
         const int nit = min(G5_ITEMS, my_items - seg);
         __syncthreads();   // readers of the previous segment's tables are done
         for (int i = tid; i < nit; i += G5_THREADS) {
-            const int item = y0 + (seg + i) * ys;
-            int lo = 0, hi = na - 1;   // last group whose prefix <= item
-            while (lo < hi) { const int mid = (lo + hi + 1) >> 1; if (s_scan[mid] <= item) lo = mid; else hi = mid - 1; }
-            const int tok0 = (item - s_scan[lo]) * GM_TOK;
+            const int k = seg + i;
+            int pos = k * ys + ((k & 1) ? ys - 1 - y0 : y0);   // position in the class order
+            int cls = 0;                                        // field of s_scan: 0 = 4 tiles, 1 = 3, 2 = 2, 3 = 1
+            if (pos >= n4) { pos -= n4; cls = 1; if (pos >= n3) { pos -= n3; cls = 2; if (pos >= n2) { pos -= n2; cls = 3; } } }
+            int lo = 0, hi = na - 1;   // last group whose prefix in the class <= pos: the group that owns the item
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if ((int) ((s_scan[mid] >> (16 * cls)) & 0xffff) <= pos) lo = mid; else hi = mid - 1;
+            }
+            const int cnt = egrp[3 * lo + 2];
+            const int chunk = cls == 0 ? pos - (int) (s_scan[lo] & 0xffff) : (cnt - 1) / GM_TOK;
+            const int tok0 = chunk * GM_TOK;
             s_item[i][0] = egrp[3 * lo + 1] + tok0;
-            s_item[i][1] = min(GM_TOK, egrp[3 * lo + 2] - tok0);
+            s_item[i][1] = min(GM_TOK, cnt - tok0);
             s_item[i][2] = m.slot[egrp[3 * lo]];
         }
         __syncthreads();
@@ -502,15 +522,17 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
         // ---- issue: the DMAs of step (iss_it, iss_b) into stage iss_stage, then advance (staying on the last step
         // once there).  Activation rows: this wave's tokens 8 wave + 4 i + lane / 16 (lane l fetches 16-byte piece
         // (l % 16) ^ (t % 16) of token t, the conflict-free layout the MFMA reads use) and, on lanes 0-7, the d of
-        // tokens 8 wave + lane; absent tokens re-read the item's first row (their LDS rows are never stored).
+        // tokens 8 wave + lane.  Absent tokens are not fetched (their LDS rows keep stale bytes, whose MFMA columns
+        // are never stored); lane 0 of an instruction fetches from the item's first row when its token is absent.
         // Offsets are bytes from aq (the caller's activations stay below 4 GB).
         uint32_t aoff[2], doff;
-        int iss_it = 0, iss_b = 0, iss_stage = 0, iss_step = 0;
+        int iss_it = 0, iss_b = 0, iss_stage = 0, iss_step = 0, iss_ntok = 0;
         const uint32_t lane16 = 16 * lane, lane4 = 4 * lane;
         auto issue = [&]() {
             const int it = iss_it, b = iss_b;
             if (b == 0) {
                 const int ntok = s_item[it][1];
+                iss_ntok = ntok;
                 const int p0 = s_pair[it][0];
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
@@ -532,9 +554,11 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
                 if (256 * j + 4 * lane < C::NR) dma_s32(wsrc + 1024 * C::N4 + 256 * j, lane4, wdst + 1024 * C::N4 + 256 * j);
             const uint32_t bo = (uint32_t) b * AQ;
             const uint32_t adst = lds_addr(stage_a(stage) + 8 * wave * 256);
+            // lanes of absent tokens sit out, except lane 0, so that every instruction issues (the waits count them)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) dma_s128(aq, aoff[i] + bo, adst + 1024 * i);
-            if (lane < 8) dma_s32(aq, doff + bo, lds_addr(stage_d(stage) + 8 * wave));
+            for (int i = 0; i < 2; ++i)
+                if (8 * wave + 4 * i + (lane >> 4) < iss_ntok || lane == 0) dma_s128(aq, aoff[i] + bo, adst + 1024 * i);
+            if (lane < 8 && (8 * wave + lane < iss_ntok || lane == 0)) dma_s32(aq, doff + bo, lds_addr(stage_d(stage) + 8 * wave));
             if (iss_step < nsteps - 1) {
                 ++iss_step;
                 if (++iss_b == nsb) { iss_b = 0; ++iss_it; }
