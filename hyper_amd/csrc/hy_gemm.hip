@@ -301,7 +301,14 @@ __device__ __forceinline__ void store_f32(float *g, float v) { asm volatile("glo
 // then makes the whole stage visible and frees stage (s - 1) % D for the next issue.  Nothing in the stream is a
 // compiler-visible global load, so the compiler adds no waits of its own.  The epilogue's stores are not counted:
 // a store still in flight only makes a later wait stricter (loads cannot overtake the loads before them).
-constexpr int G5_WAVES = 8, G5_THREADS = 64 * G5_WAVES, G5_ROWS = 16 * G5_WAVES;
+#ifndef HY_G5_WAVES
+#define HY_G5_WAVES 8
+#endif
+constexpr int G5_WAVES = HY_G5_WAVES, G5_THREADS = 64 * G5_WAVES, G5_ROWS = 16 * G5_WAVES;
+constexpr int G5_HALF = G5_WAVES / 2;         // gate/up: waves 0 .. HALF - 1 in gate, the rest in up
+constexpr int G5_TPW = GM_TOK / G5_WAVES;     // activation rows each wave fetches per step
+constexpr int G5_NA = G5_TPW / 4;             // their 1 KB DMA instructions
+constexpr int G5_PER = 1024 / G5_THREADS;     // expert groups per thread in the item scan
 constexpr int G5_ITEMS = 16;                  // items per segment (their tables live in LDS)
 constexpr int G5_LDS_STAGES = 150 * 1024;     // LDS for the stages (the tables take the rest of the 160 KB)
 
@@ -311,9 +318,9 @@ template <int T> struct G5 {
     static constexpr int WB = G5_WAVES * TB;                    // weights of a stage
     static constexpr int AB = GM_TOK * 256;                     // activation values of a stage (64 rows of 256)
     static constexpr int SB = WB + AB + 4 * GM_TOK;             // + the rows' Q8_K d
-    static constexpr int D = 4 * SB <= G5_LDS_STAGES ? 4 : 3;   // stages
+    static constexpr int D = 4 * SB <= G5_LDS_STAGES ? 4 : 3 * SB <= G5_LDS_STAGES ? 3 : 2;   // stages
     static constexpr int N4 = TB / 1024, NR = TB - 1024 * N4, N1 = (NR + 255) / 256;   // tile DMAs: 1 KB, then 256 B
-    static constexpr int L = N4 + N1 + 3;                       // DMA instructions per wave and step
+    static constexpr int L = N4 + N1 + G5_NA + 1;               // DMA instructions per wave and step
     static_assert(TB % 16 == 0 && NR % 4 == 0 && SB % 16 == 0, "DMA granules");
     static_assert(D * SB <= G5_LDS_STAGES, "stages fit");
     static_assert((D - 2) * L <= 63, "vmcnt range");
@@ -432,7 +439,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
     using C = G5<T>;
     constexpr int D = C::D, AQ = Q8K_BYTES;
     __shared__ __align__(16) uint8_t smem[D * C::SB];   // stage s at s * SB: weights [wave][TB], activations [64][256], d [64]
-    __shared__ uint64_t s_scan[1024 + 8];                // per expert group: exclusive prefix of its items per tile class
+    __shared__ uint64_t s_scan[1024 + G5_WAVES];                // per expert group: exclusive prefix of its items per tile class
     __shared__ int s_item[G5_ITEMS][3];                  // first pair in order, tokens, weight slot
     __shared__ int s_pair[G5_ITEMS][GM_TOK];             // pair index of each token of the segment's items
     __shared__ float s_wt[GU ? 1 : G5_ITEMS][GM_TOK];    // down: their route weights
@@ -445,10 +452,10 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
     // takes positions k S + y for even k and k S + S - 1 - y for odd k), which evens out the slots' work.
     // s_scan holds each group's exclusive prefix of the four class counts, 16 bits each (item totals stay below 2^16).
     {
-        uint64_t c2[2], loc = 0;
+        uint64_t c2[G5_PER], loc = 0;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int g = 2 * tid + i;
+        for (int i = 0; i < G5_PER; ++i) {
+            const int g = G5_PER * tid + i;
             uint64_t c = 0;
             if (g < na) {
                 const int cnt = egrp[3 * g + 2], n = (cnt + GM_TOK - 1) / GM_TOK, cl = (cnt - GM_TOK * (n - 1) + 15) >> 4;
@@ -466,7 +473,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
         for (int w = 0; w < wave; ++w) base += s_scan[1024 + w];
         uint64_t ex = base + inc - loc;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) { s_scan[2 * tid + i] = ex; ex += c2[i]; }
+        for (int i = 0; i < G5_PER; ++i) { s_scan[G5_PER * tid + i] = ex; ex += c2[i]; }
         if (T == IQ2_XS) expand_iq2xs_grid(grid);
         __syncthreads();
     }
@@ -481,9 +488,9 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
     const int in_dim = GU ? m.n : m.ff, nsb = in_dim / 256;
     const size_t mbytes = GU ? m.gate_bytes : m.down_bytes;
     // this wave's 16 rows: tile index (rows / 16) in its matrix, and the output row of each lane
-    const int tile_row = GU ? blockIdx.x * 4 + (wave & 3) : blockIdx.x * G5_WAVES + wave;
+    const int tile_row = GU ? blockIdx.x * G5_HALF + wave % G5_HALF : blockIdx.x * G5_WAVES + wave;
     const int row = 16 * tile_row + rr;
-    const uint8_t *Wmat = (GU ? (wave < 4 ? m.gate : m.up) : m.down) + (size_t) tile_row * nsb * C::TB;
+    const uint8_t *Wmat = (GU ? (wave < G5_HALF ? m.gate : m.up) : m.down) + (size_t) tile_row * nsb * C::TB;
     const size_t arow = (size_t) nsb * AQ;
     auto stage_w = [&](int s) { return smem + s * C::SB; };
     auto stage_a = [&](int s) { return (int8_t *) (smem + s * C::SB + C::WB); };
@@ -525,7 +532,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
         // tokens 8 wave + lane.  Absent tokens are not fetched (their LDS rows keep stale bytes, whose MFMA columns
         // are never stored); lane 0 of an instruction fetches from the item's first row when its token is absent.
         // Offsets are bytes from aq (the caller's activations stay below 4 GB).
-        uint32_t aoff[2], doff;
+        uint32_t aoff[G5_NA], doff;
         int iss_it = 0, iss_b = 0, iss_stage = 0, iss_step = 0, iss_ntok = 0;
         const uint32_t lane16 = 16 * lane, lane4 = 4 * lane;
         auto issue = [&]() {
@@ -535,12 +542,12 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
                 iss_ntok = ntok;
                 const int p0 = s_pair[it][0];
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const int t = 8 * wave + 4 * i + (lane >> 4);
+                for (int i = 0; i < G5_NA; ++i) {
+                    const int t = G5_TPW * wave + 4 * i + (lane >> 4);
                     const int pr = t < ntok ? s_pair[it][t] : p0;
                     aoff[i] = (uint32_t) (GU ? pr / a_div : pr) * (uint32_t) arow + 4 + 16 * ((lane & 15) ^ (t & 15));
                 }
-                const int td = 8 * wave + (lane & 7);
+                const int td = G5_TPW * wave + (lane & (G5_TPW - 1));
                 const int prd = td < ntok ? s_pair[it][td] : p0;
                 doff = (uint32_t) (GU ? prd / a_div : prd) * (uint32_t) arow;
             }
@@ -553,12 +560,12 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
             for (int j = 0; j < C::N1; ++j)
                 if (256 * j + 4 * lane < C::NR) dma_s32(wsrc + 1024 * C::N4 + 256 * j, lane4, wdst + 1024 * C::N4 + 256 * j);
             const uint32_t bo = (uint32_t) b * AQ;
-            const uint32_t adst = lds_addr(stage_a(stage) + 8 * wave * 256);
+            const uint32_t adst = lds_addr(stage_a(stage) + G5_TPW * wave * 256);
             // lanes of absent tokens sit out, except lane 0, so that every instruction issues (the waits count them)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                if (8 * wave + 4 * i + (lane >> 4) < iss_ntok || lane == 0) dma_s128(aq, aoff[i] + bo, adst + 1024 * i);
-            if (lane < 8 && (8 * wave + lane < iss_ntok || lane == 0)) dma_s32(aq, doff + bo, lds_addr(stage_d(stage) + 8 * wave));
+            for (int i = 0; i < G5_NA; ++i)
+                if (G5_TPW * wave + 4 * i + (lane >> 4) < iss_ntok || lane == 0) dma_s128(aq, aoff[i] + bo, adst + 1024 * i);
+            if (lane < G5_TPW && (G5_TPW * wave + lane < iss_ntok || lane == 0)) dma_s32(aq, doff + bo, lds_addr(stage_d(stage) + G5_TPW * wave));
             if (iss_step < nsteps - 1) {
                 ++iss_step;
                 if (++iss_b == nsb) { iss_b = 0; ++iss_it; }
@@ -600,18 +607,19 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
             if (b != nsb - 1) return;
             // ---- the item's outputs
             if (GU) {
-                // SwiGLU needs the up rows of waves 4-7 in waves 0-3: exchanged through this stage's activation
-                // area (64 rows x 64 tokens of fp32), once every wave has finished reading it
-                float *s_up = (float *) stage_a(stage);
+                // SwiGLU needs the up rows of the upper half of the waves in the lower half: exchanged through this
+                // stage (its weights and activations, once every wave has finished reading them)
+                static_assert(G5_HALF * 16 * GM_TOK * 4 <= C::WB + C::AB, "the exchange fits in a stage");
+                float *s_up = (float *) stage_w(stage);
                 lds_barrier();
-                if (wave >= 4) {
+                if (wave >= G5_HALF) {
 #pragma unroll
                     for (int tile = 0; tile < GM_TILES; ++tile)
 #pragma unroll
-                        for (int v = 0; v < 4; ++v) s_up[((wave & 3) * 16 + rr) * GM_TOK + tile * 16 + 4 * q + v] = acc[tile][v];
+                        for (int v = 0; v < 4; ++v) s_up[((wave % G5_HALF) * 16 + rr) * GM_TOK + tile * 16 + 4 * q + v] = acc[tile][v];
                 }
                 lds_barrier();
-                if (wave < 4) {
+                if (wave < G5_HALF) {
 #pragma unroll
                     for (int tile = 0; tile < GM_TILES; ++tile)
 #pragma unroll
@@ -619,7 +627,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
                             const int tok = tile * 16 + 4 * q + v;
                             if (tok < ntok)
                                 store_f32(out + (size_t) s_pair[it][tok] * m.ff + row,
-                                          hy_swiglu(acc[tile][v], s_up[((wave & 3) * 16 + rr) * GM_TOK + tok], m.clamp));
+                                          hy_swiglu(acc[tile][v], s_up[((wave % G5_HALF) * 16 + rr) * GM_TOK + tok], m.clamp));
                         }
                 }
             } else {
@@ -881,7 +889,7 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
         hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
         return check_launch("hy_moe_gemm_gate_up");
     }
-    const int rb = m.ff / 64;
+    const int rb = m.ff / (16 * G5_HALF);
     if ((size_t) n_pairs * (m.n / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_gate_up: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
     dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
     HY_GEMM_SWITCH(m.tg, hipLaunchKernelGGL((k_gemm<TT, true>), grid, dim3(G5_THREADS), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp,

@@ -170,36 +170,56 @@ int launch_down(const hy_moe_dev &m, const float *h, const int *ids, const float
 
 // ---------------------------------------------------------------- combine (A9)
 // out[t][r] = sg * shexp (if shexp) then + y of the token's pairs in ascending expert id (src/cpu_moe.cpp:863-874
-// order; the first pair is the start value when there is no shared expert); negative ids are skipped.
+// order; the first pair is the start value when there is no shared expert); negative ids are skipped.  One block
+// per token: wave 0 ranks the token's pairs (rank = valid pairs with a smaller id, ties by position), then every
+// thread sums VW consecutive columns per pass (VW = 4: 16-byte loads when n and the rows allow it).
+template <int VW>
 __global__ __launch_bounds__(256) void k_reduce(const float *__restrict__ shexp, const float *__restrict__ sg, const float *__restrict__ y,
                                                 int k, float *__restrict__ out, int n, const int *__restrict__ ids) {
     __shared__ int ord[64];
-    const int t = blockIdx.y, r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (threadIdx.x == 0) {
-        int c = 0;
-        for (int j = 0; j < k; ++j) {
-            const int e = ids[t * k + j];
-            if (e < 0) continue;
-            int i = c++;
-            while (i > 0 && ids[t * k + ord[i - 1]] > e) { ord[i] = ord[i - 1]; --i; }
-            ord[i] = j;
+    __shared__ int s_cnt;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    if (tid < 64) {
+        const int e = tid < k ? ids[(size_t) t * k + tid] : -1;
+        int rank = 0;
+        for (int i = 0; i < k; ++i) {
+            const int o = __shfl(e, i);
+            rank += (o >= 0 && (o < e || (o == e && i < tid))) ? 1 : 0;
         }
-        for (int i = c; i < 64; ++i) ord[i] = -1;
+        if (e >= 0) ord[rank] = tid;
+        const int c = __popcll(__ballot(e >= 0));
+        if (tid == 0) s_cnt = c;
     }
     __syncthreads();
-    if (r >= n) return;
-    float acc = 0.0f;
-    bool first = true;
-    if (shexp) { acc = (sg ? sg[t] : 1.0f) * shexp[(size_t) t * n + r]; first = false; }
-    for (int i = 0; i < k && ord[i] >= 0; ++i) {
-        const float v = y[((size_t) t * k + ord[i]) * n + r];
-        if (first) { acc = v; first = false; } else acc = acc + v;
+    const int c = s_cnt;
+    const float g = shexp ? (sg ? sg[t] : 1.0f) : 0.0f;
+    for (int r = VW * tid; r < n; r += VW * 256) {
+        float acc[VW] = {}, v[VW];   // a token with no shared expert and no valid pair gets zeros
+        bool first = true;
+        if (shexp) {
+            if constexpr (VW == 4) { const float4 x = *(const float4 *) (shexp + (size_t) t * n + r); v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w; }
+            else v[0] = shexp[(size_t) t * n + r];
+#pragma unroll
+            for (int j = 0; j < VW; ++j) acc[j] = g * v[j];
+            first = false;
+        }
+        for (int i = 0; i < c; ++i) {
+            const float *yp = y + ((size_t) t * k + ord[i]) * n + r;
+            if constexpr (VW == 4) { const float4 x = *(const float4 *) yp; v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w; }
+            else v[0] = *yp;
+#pragma unroll
+            for (int j = 0; j < VW; ++j) acc[j] = first ? v[j] : acc[j] + v[j];
+            first = false;
+        }
+        if constexpr (VW == 4) *(float4 *) (out + (size_t) t * n + r) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        else out[(size_t) t * n + r] = acc[0];
     }
-    out[(size_t) t * n + r] = acc;
 }
 int launch_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int *ids, hipStream_t s) {
     if (nt == 0) return HY_OK;
-    hipLaunchKernelGGL(k_reduce, dim3((n + 255) / 256, nt), dim3(256), 0, s, shexp, sg, y, k, out, n, ids);
+    const bool vec = n % 4 == 0 && ((uintptr_t) y & 15) == 0 && ((uintptr_t) out & 15) == 0 && ((uintptr_t) shexp & 15) == 0;
+    if (vec) hipLaunchKernelGGL(k_reduce<4>, dim3(nt), dim3(256), 0, s, shexp, sg, y, k, out, n, ids);
+    else hipLaunchKernelGGL(k_reduce<1>, dim3(nt), dim3(256), 0, s, shexp, sg, y, k, out, n, ids);
     return check_launch("hy_moe_reduce");
 }
 

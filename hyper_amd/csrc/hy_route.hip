@@ -129,16 +129,17 @@ int launch_route(const float *logits, int ls, int ne, int k, int *ids, float *wt
 }
 
 // ---------------------------------------------------------------- bucketing (A3)
-// One block of 8 waves.  Pairs p with slot[ids[p]] >= 0, grouped by expert, stable by pair index
+// One block of 16 waves.  Pairs p with slot[ids[p]] >= 0, grouped by expert, stable by pair index
 // (src/cpu_moe.cpp:672-687 order; the GPU reference src/kernels4.cu:1275-1295 is unordered within an
 // expert).  Wave w owns a contiguous segment of pairs: (1) per-wave histograms, (2) prefix over experts
-// and waves, egrp/order_n, (3) each wave ranks 64-pair chunks with an in-register bitonic sort of
-// (expert, lane) keys and places them after its running per-expert counters.
-constexpr int ORD_WAVES = 8;
+// and waves, egrp/order_n, (3) each wave walks its segment 64 pairs at a time: a lane finds the lanes that hold its
+// expert from ten ballots (one per bit of the id, ids < 1024), its rank is the number of those below it, and the
+// highest of them advances the wave's running counter for the expert.
+constexpr int ORD_WAVES = 16;
 __global__ __launch_bounds__(64 * ORD_WAVES) void k_order(const int *__restrict__ slot, const int *__restrict__ ids, int P, int ne,
                                                           int *__restrict__ order, int *__restrict__ order_n, int *__restrict__ egrp) {
     __shared__ int c[ORD_WAVES * 1024];
-    __shared__ int tot[1024], act[1024];
+    __shared__ int tot[1024];
     __shared__ int wsum[2][ORD_WAVES];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int seg = ((P + ORD_WAVES - 1) / ORD_WAVES + 63) / 64 * 64;
@@ -150,19 +151,15 @@ __global__ __launch_bounds__(64 * ORD_WAVES) void k_order(const int *__restrict_
         if (e >= 0 && e < ne && slot[e] >= 0) atomicAdd(&c[w * ne + e], 1);
     }
     __syncthreads();
-    for (int e = tid; e < ne; e += blockDim.x) {
-        int s = 0;
-        for (int ww = 0; ww < ORD_WAVES; ++ww) { const int v = c[ww * ne + e]; c[ww * ne + e] = s; s += v; }
-        tot[e] = s;
-        act[e] = s > 0;
-    }
-    __syncthreads();
-    // exclusive scans of tot and act over ne <= 1024 entries: each thread two consecutive entries
+    // per expert e (thread e): the waves' counts become offsets within the expert; then exclusive scans over the
+    // experts of the pair totals and of the active flags (ne <= 1024 = one entry per thread)
     {
-        const int e0 = 2 * tid, e1 = 2 * tid + 1;
-        const int a0 = e0 < ne ? tot[e0] : 0, a1 = e1 < ne ? tot[e1] : 0;
-        const int b0 = e0 < ne ? act[e0] : 0, b1 = e1 < ne ? act[e1] : 0;
-        int sa = a0 + a1, sb = b0 + b1;
+        const int e = tid;
+        int a = 0;
+        if (e < ne)
+            for (int ww = 0; ww < ORD_WAVES; ++ww) { const int v = c[ww * ne + e]; c[ww * ne + e] = a; a += v; }
+        const int b = a > 0;
+        int sa = a, sb = b;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const int ta = __shfl_up(sa, o), tb = __shfl_up(sb, o);
@@ -172,10 +169,11 @@ __global__ __launch_bounds__(64 * ORD_WAVES) void k_order(const int *__restrict_
         __syncthreads();
         int oa = 0, ob = 0;
         for (int ww = 0; ww < w; ++ww) { oa += wsum[0][ww]; ob += wsum[1][ww]; }
-        const int ea = oa + sa - (a0 + a1), eb = ob + sb - (b0 + b1);   // exclusive prefix before e0
-        __syncthreads();
-        if (e0 < ne) { tot[e0] = ea; act[e0] = b0 ? eb : -1; if (b0) { if (egrp) { egrp[3 * eb] = e0; egrp[3 * eb + 1] = ea; egrp[3 * eb + 2] = a0; } } }
-        if (e1 < ne) { tot[e1] = ea + a0; act[e1] = b1 ? eb + b0 : -1; if (b1) { if (egrp) { egrp[3 * (eb + b0)] = e1; egrp[3 * (eb + b0) + 1] = ea + a0; egrp[3 * (eb + b0) + 2] = a1; } } }
+        const int ea = oa + sa - a, eb = ob + sb - b;   // exclusive prefixes before e
+        if (e < ne) {
+            tot[e] = ea;
+            if (b && egrp) { egrp[3 * eb] = e; egrp[3 * eb + 1] = ea; egrp[3 * eb + 2] = a; }
+        }
         if (tid == blockDim.x - 1) {
             int ta = 0, tb = 0;
             for (int ww = 0; ww < ORD_WAVES; ++ww) { ta += wsum[0][ww]; tb += wsum[1][ww]; }
@@ -186,32 +184,23 @@ __global__ __launch_bounds__(64 * ORD_WAVES) void k_order(const int *__restrict_
     for (int i = tid; i < ORD_WAVES * ne; i += blockDim.x) c[i] += tot[i % ne];
     __syncthreads();
     int *cw = c + w * ne;
+    const unsigned long long below = (1ull << lane) - 1;
     for (int q0 = p0; q0 < p1; q0 += 64) {
         const int p = q0 + lane;
-        int e = p < p1 ? ids[p] : -1;
+        const int e = p < p1 ? ids[p] : -1;
         const bool valid = e >= 0 && e < ne && slot[e] >= 0;
-        int key = valid ? (e << 6) | lane : (0x7ffffc0 | lane);
+        unsigned long long same = __ballot(valid);
 #pragma unroll
-        for (int size = 2; size <= 64; size <<= 1)
-#pragma unroll
-            for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                const int other = __shfl_xor(key, stride);
-                const bool up = (lane & size) == 0, lower = (lane & stride) == 0;
-                key = (lower == up) ? min(key, other) : max(key, other);
-            }
-        const int se = key >> 6, sl = key & 63;
-        const bool sv = key < 0x7ffffc0;
-        const int prev = __shfl_up(se, 1), next = __shfl_down(se, 1);
-        const bool head = lane == 0 || se != prev, tail = lane == 63 || se != next;
-        const unsigned long long heads = __ballot(head);
-        const unsigned long long upto = lane == 63 ? ~0ull : ((2ull << lane) - 1);
-        const int first = 63 - __builtin_clzll(heads & upto);
-        const int rank = lane - first;
-        int base = 0;
-        if (sv) base = cw[se];
-        if (sv) order[base + rank] = q0 + sl;
-        __builtin_amdgcn_wave_barrier();
-        if (sv && tail) cw[se] = base + rank + 1;
+        for (int bit = 0; bit < 10; ++bit) {
+            const unsigned long long ones = __ballot((e >> bit) & 1);
+            same &= ((e >> bit) & 1) ? ones : ~ones;
+        }
+        if (valid) {
+            const int rank = __popcll(same & below);
+            const int base = cw[e];
+            order[base + rank] = p;
+            if (rank == __popcll(same) - 1) cw[e] = base + rank + 1;   // the group's highest lane
+        }
         __builtin_amdgcn_wave_barrier();
     }
 }

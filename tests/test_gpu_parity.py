@@ -238,3 +238,47 @@ def test_grouped_gemm_bitexact(cuda, tg, td, d, ff, k, nt):
     assert_bits_equal(y.cpu().numpy(), (wts.reshape(-1, 1) * y_r).astype(np.float32), "y (grouped down)")
     assert_bits_equal(out.cpu().numpy(), out_r, "out")
     assert rel_l2(out.cpu().numpy(), out_r) <= TOL
+
+
+@pytest.mark.parametrize("tg,td,E,d,ff,k,nt,sh,sg_logit", [
+    (GType.Q4_K, GType.Q6_K, 32, 2048, 768, 8, 40, GType.Q4_K, True),
+    (GType.IQ4_XS, GType.IQ4_XS, 24, 4096, 1536, 8, 24, GType.IQ4_XS, False),
+])
+def test_runner_prefill_shared_matches_oracle(cuda, tg, td, E, d, ff, k, nt, sh, sg_logit):
+    """Prefill through the runner with an always-on shared expert (and its sigmoid gate): the combine's shared
+    term and the pairs' order against the oracle's layer."""
+    L = layer(tg, td, E, ff, d, seed=900 + nt)
+    S = layer(sh, td, 1, ff, d, seed=901)
+    g = gen(902)
+    W_r = torch.randn(E + (1 if sg_logit else 0), d, generator=g) * 0.02
+    x = torch.randn(nt, d, generator=g)
+    logits = orc.gemv_f32(W_r.numpy(), x.numpy())
+    ids, wts, sgv = orc.route(logits, E, k, with_sg=sg_logit)
+    out_r = orc.moe_layer(oracle_layer(L), x.numpy(), ids, wts, shared=oracle_layer(S), sg=sgv if sg_logit else None)
+    r = moe.MoeLayerRunner(moe.upload_experts(L, device=cuda), W_r.to(cuda), k, max_rows=nt,
+                           shared=moe.upload_experts(S, device=cuda), sg_logit=sg_logit)
+    out = r.prefill(x.to(cuda)).clone()
+    _sync()
+    assert_bits_equal(out.cpu().numpy(), out_r, "runner.prefill")
+
+
+def test_reduce_unaligned_rows(cuda):
+    """The combine with rows that are not a multiple of 4 (the scalar path): sg * shexp, then the valid pairs in
+    ascending expert id, ties by position; ids < 0 are skipped and a token without pairs keeps sg * shexp."""
+    nt, k, n = 5, 6, 257
+    g = gen(910)
+    y = torch.randn(nt * k, n, generator=g)
+    shexp = torch.randn(nt, n, generator=g)
+    sg = torch.rand(nt, generator=g)
+    ids = torch.tensor([[5, 1, -1, 9, 3, 2], [0, 0, 4, -1, -1, 7], [-1] * 6, [12, 11, 10, 9, 8, 7], [3, -1, 3, 1, 2, 0]],
+                       dtype=torch.int32)
+    want = np.zeros((nt, n), dtype=np.float32)
+    for t in range(nt):
+        acc = (np.float32(sg[t]) * shexp[t].numpy()).astype(np.float32)
+        for j in sorted((j for j in range(k) if ids[t, j] >= 0), key=lambda j: (int(ids[t, j]), j)):
+            acc = (acc + y[t * k + j].numpy()).astype(np.float32)
+        want[t] = acc
+    out = torch.full((nt, n), float("nan"), device=cuda)
+    moe.moe_reduce(shexp.to(cuda), sg.to(cuda), y.to(cuda), k, out, n, nt, ids.reshape(-1).to(cuda))
+    _sync()
+    assert_bits_equal(out.cpu().numpy(), want, "out")
