@@ -38,8 +38,9 @@ __device__ __forceinline__ uint2 load8_a2(const uint8_t *p) {   // 8 bytes from 
 // the loads in flight): whole dwords from the aligned-down address, joined with v_alignbyte.
 __device__ __forceinline__ uint32_t join_b(uint32_t hi, uint32_t lo, uint32_t sb) { return __builtin_amdgcn_alignbyte(hi, lo, sb); }
 // 8 bytes at p (2-byte aligned); reads the dwords at p & ~3 .. + 11, all of which must lie in the buffer
+// (the aligned-down pointer is formed by pointer arithmetic on p, so that an LDS pointer stays an LDS pointer)
 __device__ __forceinline__ uint2 ld8_2a(const uint8_t *p) {
-    const uint32_t *w = (const uint32_t *) ((uintptr_t) p & ~(uintptr_t) 3);
+    const uint32_t *w = (const uint32_t *) (p - ((uintptr_t) p & 3));
     const uint32_t sb = (uint32_t) ((uintptr_t) p & 3);
     const uint32_t d0 = w[0], d1 = w[1], d2 = w[2];
     return make_uint2(join_b(d1, d0, sb), join_b(d2, d1, sb));
@@ -47,7 +48,7 @@ __device__ __forceinline__ uint2 ld8_2a(const uint8_t *p) {
 // 16 bytes at p (2-byte aligned), with p + 18 the end of the block: the fifth dword is read only when p is
 // misaligned (else the fourth is read again), so nothing past p + 18 is touched
 __device__ __forceinline__ uint4 ld16_2a_tail(const uint8_t *p) {
-    const uint32_t *w = (const uint32_t *) ((uintptr_t) p & ~(uintptr_t) 3);
+    const uint32_t *w = (const uint32_t *) (p - ((uintptr_t) p & 3));
     const uint32_t sb = (uint32_t) ((uintptr_t) p & 3);
     const uint32_t d0 = w[0], d1 = w[1], d2 = w[2], d3 = w[3], d4 = w[sb ? 4 : 3];
     return make_uint4(join_b(d1, d0, sb), join_b(d2, d1, sb), join_b(d3, d2, sb), join_b(d4, d3, sb));
