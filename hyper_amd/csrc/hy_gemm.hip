@@ -606,8 +606,37 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
             }
             }
             if (b != nsb - 1) return;
-            // ---- the item's outputs
-            if (GU) {
+            // ---- the item's outputs.  Where two token-major copies fit in a stage (every wave has finished reading
+            // this one after a barrier), the waves' accumulators go there -- rows padded by one float against bank
+            // conflicts -- and wave w finishes tokens w, w + WAVES, ...: one output row per lane (SwiGLU of the gate
+            // and up values, or the route weight times the down value), stored as whole rows.
+            constexpr int OR = GU ? 16 * G5_HALF : G5_ROWS;   // output rows of the block
+            constexpr int LD = OR + 1;                         // floats per token in LDS
+            constexpr bool XCH = (GU ? 2 : 1) * GM_TOK * LD * 4 <= C::WB + C::AB;
+            if constexpr (XCH) {
+                float *s_o = (float *) stage_w(stage);         // gate (or down) values
+                float *s_u = s_o + GM_TOK * LD;                // up values
+                lds_barrier();
+                {
+                    float *dst = GU && wave >= G5_HALF ? s_u : s_o;
+                    const int orow = (GU ? wave % G5_HALF : wave) * 16 + rr;
+#pragma unroll
+                    for (int tile = 0; tile < GM_TILES; ++tile) {
+                        if (tile >= ntile) break;
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) dst[(tile * 16 + 4 * q + v) * LD + orow] = acc[tile][v];
+                    }
+                }
+                lds_barrier();
+                const int row0 = blockIdx.x * OR;
+                for (int tok = wave; tok < ntok; tok += G5_WAVES) {
+                    float *o = out + (size_t) s_pair[it][tok] * (GU ? m.ff : m.n) + row0;
+                    const float wt = GU ? 0.0f : s_wt[GU ? 0 : it][tok];
+#pragma unroll
+                    for (int r = lane; r < OR; r += 64)
+                        store_f32(o + r, GU ? hy_swiglu(s_o[tok * LD + r], s_u[tok * LD + r], m.clamp) : wt * s_o[tok * LD + r]);
+                }
+            } else if (GU) {
                 // SwiGLU needs the up rows of the upper half of the waves in the lower half: exchanged through this
                 // stage (its weights and activations, once every wave has finished reading them)
                 static_assert(G5_HALF * 16 * GM_TOK * 4 <= C::WB + C::AB, "the exchange fits in a stage");
