@@ -302,30 +302,31 @@ __device__ __forceinline__ void store_f32(float *g, float v) { asm volatile("glo
 // then makes the whole stage visible and frees stage (s - 1) % D for the next issue.  Nothing in the stream is a
 // compiler-visible global load, so the compiler adds no waits of its own.  The epilogue's stores are not counted:
 // a store still in flight only makes a later wait stricter (loads cannot overtake the loads before them).
-#ifndef HY_G5_WAVES
-#define HY_G5_WAVES 8
-#endif
-constexpr int G5_WAVES = HY_G5_WAVES, G5_THREADS = 64 * G5_WAVES, G5_ROWS = 16 * G5_WAVES;
-constexpr int G5_HALF = G5_WAVES / 2;         // gate/up: waves 0 .. HALF - 1 in gate, the rest in up
-constexpr int G5_TPW = GM_TOK / G5_WAVES;     // activation rows each wave fetches per step
-constexpr int G5_NA = G5_TPW / 4;             // their 1 KB DMA instructions
-constexpr int G5_PER = 1024 / G5_THREADS;     // expert groups per thread in the item scan
 constexpr int G5_ITEMS = 16;                  // items per segment (their tables live in LDS)
 constexpr int G5_LDS_STAGES = 150 * 1024;     // LDS for the stages (the tables take the rest of the 160 KB)
 
-template <int T> struct G5 {
+// Geometry of the stream kernel for weight type T and W waves (8 or 16) per block.
+template <int T, int W> struct G5 {
+    static constexpr int WAVES = W, THREADS = 64 * W, ROWS = 16 * W;   // a wave owns 16 weight rows
+    static constexpr int HALF = W / 2;                          // gate/up: waves 0 .. HALF - 1 in gate, the rest in up
+    static constexpr int TPW = GM_TOK / W;                      // activation rows each wave fetches per step
+    static constexpr int NA = TPW / 4;                          // their 1 KB DMA instructions
+    static constexpr int PER = 1024 / THREADS;                  // expert groups per thread in the item scan
     static constexpr int BB = block_bytes(T);                   // weight bytes per row and 256 values
     static constexpr int TB = 16 * BB;                          // one wave's 16-row tile of a span
-    static constexpr int WB = G5_WAVES * TB;                    // weights of a stage
+    static constexpr int WB = W * TB;                           // weights of a stage
     static constexpr int AB = GM_TOK * 256;                     // activation values of a stage (64 rows of 256)
     static constexpr int SB = WB + AB + 4 * GM_TOK;             // + the rows' Q8_K d
     static constexpr int D = 4 * SB <= G5_LDS_STAGES ? 4 : 3 * SB <= G5_LDS_STAGES ? 3 : 2;   // stages
     static constexpr int N4 = TB / 1024, NR = TB - 1024 * N4, N1 = (NR + 255) / 256;   // tile DMAs: 1 KB, then 256 B
-    static constexpr int L = N4 + N1 + G5_NA + 1;               // DMA instructions per wave and step
+    static constexpr int L = N4 + N1 + NA + 1;                  // DMA instructions per wave and step
+    static_assert(W == 8 || W == 16, "8 or 16 waves");
     static_assert(TB % 16 == 0 && NR % 4 == 0 && SB % 16 == 0, "DMA granules");
     static_assert(D * SB <= G5_LDS_STAGES, "stages fit");
     static_assert((D - 2) * L <= 63, "vmcnt range");
 };
+// waves per block: 16 (four per SIMD) where the type's step fits 128 registers, else 8
+template <int T, bool GU> constexpr int g5_waves() { return GU && (T == Q4_K || T == IQ4_XS) ? 16 : 8; }
 
 __device__ __forceinline__ v4i mfma64(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
@@ -387,60 +388,17 @@ __device__ __forceinline__ void step_q4k(const uint8_t *wl, int q, const int8_t 
     }
 }
 
-// One step's integer products and fold for NT token tiles (NT is uniform per item, so the code is straight-line)
-template <int T, int NT>
-__device__ __forceinline__ void step_math(const Raw<T> &wr, int q, const uint2 *grid, const int8_t *as, int rr, const float *yd,
-                                          float (&acc)[GM_TILES][4]) {
-    const v4i z = {0, 0, 0, 0};
-    int si[NT][4];
-    v4i sm[NT];
-#pragma unroll
-    for (int i = 0; i < NT; ++i) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) si[i][v] = 0;
-        sm[i] = z;
-    }
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        uint32_t b0, b1;
-        int s0, s1, mn;
-        wr.chunk(c, q, grid, b0, b1, s0, s1, mn);
-        const uint32_t mb = __builtin_amdgcn_perm(0u, (uint32_t) mn, 0u);
-#pragma unroll
-        for (int tile = 0; tile < NT; ++tile) {
-            const long a = a_frag<true>(as, tile, rr, c, q);
-            if constexpr (Raw<T>::g16) {
-                const bool lo = q < 2;
-                const v4i d0 = mfma16(a, mk_long(lo ? b0 : 0u, lo ? b1 : 0u), z);
-                const v4i d1 = mfma16(a, mk_long(lo ? 0u : b0, lo ? 0u : b1), z);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) si[tile][v] += __mul24(s0, d0[v]) + __mul24(s1, d1[v]);
-            } else {
-                const v4i d0 = mfma16(a, mk_long(b0, b1), z);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) si[tile][v] += __mul24(s0, d0[v]);
-                if constexpr (Raw<T>::mins) sm[tile] = mfma16(a, mk_long(mb, mb), sm[tile]);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);   // chunk by chunk: keeps the operands of one chunk live at a time
-    }
-#pragma unroll
-    for (int tile = 0; tile < NT; ++tile)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[tile][v] = __builtin_fmaf(yd[tile * 16 + 4 * q + v], wr.fold(si[tile][v], sm[tile][v]), acc[tile][v]);
-}
-
 template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
-template <int T, bool GU>
-__global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint8_t *__restrict__ aq, int a_div, const int *__restrict__ order,
+template <int T, bool GU, int W>
+__global__ __launch_bounds__(64 * W, 1) void k_gemm(hy_moe_dev m, const uint8_t *__restrict__ aq, int a_div, const int *__restrict__ order,
                                                         const int *__restrict__ order_n, const int *__restrict__ egrp, const float *__restrict__ wts,
                                                         float *__restrict__ out) {
     static_assert(T != IQ4_NL, "IQ4_NL runs k_gemm_nl");
-    using C = G5<T>;
+    using C = G5<T, W>;
     constexpr int D = C::D, AQ = Q8K_BYTES;
     __shared__ __align__(16) uint8_t smem[D * C::SB];   // stage s at s * SB: weights [wave][TB], activations [64][256], d [64]
-    __shared__ uint64_t s_scan[1024 + G5_WAVES];                // per expert group: exclusive prefix of its items per tile class
+    __shared__ uint64_t s_scan[1024 + C::WAVES];                // per expert group: exclusive prefix of its items per tile class
     __shared__ int s_item[G5_ITEMS][3];                  // first pair in order, tokens, weight slot
     __shared__ int s_pair[G5_ITEMS][GM_TOK];             // pair index of each token of the segment's items
     __shared__ float s_wt[GU ? 1 : G5_ITEMS][GM_TOK];    // down: their route weights
@@ -453,10 +411,10 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
     // takes positions k S + y for even k and k S + S - 1 - y for odd k), which evens out the slots' work.
     // s_scan holds each group's exclusive prefix of the four class counts, 16 bits each (item totals stay below 2^16).
     {
-        uint64_t c2[G5_PER], loc = 0;
+        uint64_t c2[C::PER], loc = 0;
 #pragma unroll
-        for (int i = 0; i < G5_PER; ++i) {
-            const int g = G5_PER * tid + i;
+        for (int i = 0; i < C::PER; ++i) {
+            const int g = C::PER * tid + i;
             uint64_t c = 0;
             if (g < na) {
                 const int cnt = egrp[3 * g + 2], n = (cnt + GM_TOK - 1) / GM_TOK, cl = (cnt - GM_TOK * (n - 1) + 15) >> 4;
@@ -474,12 +432,12 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
         for (int w = 0; w < wave; ++w) base += s_scan[1024 + w];
         uint64_t ex = base + inc - loc;
 #pragma unroll
-        for (int i = 0; i < G5_PER; ++i) { s_scan[G5_PER * tid + i] = ex; ex += c2[i]; }
+        for (int i = 0; i < C::PER; ++i) { s_scan[C::PER * tid + i] = ex; ex += c2[i]; }
         if (T == IQ2_XS) expand_iq2xs_grid(grid);
         __syncthreads();
     }
     uint64_t tot = 0;
-    for (int w = 0; w < G5_WAVES; ++w) tot += s_scan[1024 + w];
+    for (int w = 0; w < C::WAVES; ++w) tot += s_scan[1024 + w];
     const int n4 = (int) (tot & 0xffff), n3 = (int) ((tot >> 16) & 0xffff), n2 = (int) ((tot >> 32) & 0xffff), n1 = (int) (tot >> 48);
     const int total = n4 + n3 + n2 + n1;
     const int y0 = blockIdx.y, ys = gridDim.y;
@@ -489,9 +447,9 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
     const int in_dim = GU ? m.n : m.ff, nsb = in_dim / 256;
     const size_t mbytes = GU ? m.gate_bytes : m.down_bytes;
     // this wave's 16 rows: tile index (rows / 16) in its matrix, and the output row of each lane
-    const int tile_row = GU ? blockIdx.x * G5_HALF + wave % G5_HALF : blockIdx.x * G5_WAVES + wave;
+    const int tile_row = GU ? blockIdx.x * C::HALF + wave % C::HALF : blockIdx.x * C::WAVES + wave;
     const int row = 16 * tile_row + rr;
-    const uint8_t *Wmat = (GU ? (wave < G5_HALF ? m.gate : m.up) : m.down) + (size_t) tile_row * nsb * C::TB;
+    const uint8_t *Wmat = (GU ? (wave < C::HALF ? m.gate : m.up) : m.down) + (size_t) tile_row * nsb * C::TB;
     const size_t arow = (size_t) nsb * AQ;
     auto stage_w = [&](int s) { return smem + s * C::SB; };
     auto stage_a = [&](int s) { return (int8_t *) (smem + s * C::SB + C::WB); };
@@ -500,7 +458,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
     for (int seg = 0; seg < my_items; seg += G5_ITEMS) {
         const int nit = min(G5_ITEMS, my_items - seg);
         __syncthreads();   // readers of the previous segment's tables are done
-        for (int i = tid; i < nit; i += G5_THREADS) {
+        for (int i = tid; i < nit; i += C::THREADS) {
             const int k = seg + i;
             int pos = k * ys + ((k & 1) ? ys - 1 - y0 : y0);   // position in the class order
             int cls = 0;                                        // field of s_scan: 0 = 4 tiles, 1 = 3, 2 = 2, 3 = 1
@@ -518,7 +476,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
             s_item[i][2] = m.slot[egrp[3 * lo]];
         }
         __syncthreads();
-        for (int i = tid; i < nit * GM_TOK; i += G5_THREADS) {
+        for (int i = tid; i < nit * GM_TOK; i += C::THREADS) {
             const int it = i / GM_TOK, tk = i - it * GM_TOK;
             const int pr = tk < s_item[it][1] ? order[s_item[it][0] + tk] : -1;
             s_pair[it][tk] = pr;
@@ -533,7 +491,7 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
         // tokens 8 wave + lane.  Absent tokens are not fetched (their LDS rows keep stale bytes, whose MFMA columns
         // are never stored); lane 0 of an instruction fetches from the item's first row when its token is absent.
         // Offsets are bytes from aq (the caller's activations stay below 4 GB).
-        uint32_t aoff[G5_NA], doff;
+        uint32_t aoff[C::NA], doff;
         int iss_it = 0, iss_b = 0, iss_stage = 0, iss_step = 0, iss_ntok = 0;
         const uint32_t lane16 = 16 * lane, lane4 = 4 * lane;
         auto issue = [&]() {
@@ -543,12 +501,12 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
                 iss_ntok = ntok;
                 const int p0 = s_pair[it][0];
 #pragma unroll
-                for (int i = 0; i < G5_NA; ++i) {
-                    const int t = G5_TPW * wave + 4 * i + (lane >> 4);
+                for (int i = 0; i < C::NA; ++i) {
+                    const int t = C::TPW * wave + 4 * i + (lane >> 4);
                     const int pr = t < ntok ? s_pair[it][t] : p0;
                     aoff[i] = (uint32_t) (GU ? pr / a_div : pr) * (uint32_t) arow + 4 + 16 * ((lane & 15) ^ (t & 15));
                 }
-                const int td = G5_TPW * wave + (lane & (G5_TPW - 1));
+                const int td = C::TPW * wave + (lane & (C::TPW - 1));
                 const int prd = td < ntok ? s_pair[it][td] : p0;
                 doff = (uint32_t) (GU ? prd / a_div : prd) * (uint32_t) arow;
             }
@@ -561,12 +519,12 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
             for (int j = 0; j < C::N1; ++j)
                 if (256 * j + 4 * lane < C::NR) dma_s32(wsrc + 1024 * C::N4 + 256 * j, lane4, wdst + 1024 * C::N4 + 256 * j);
             const uint32_t bo = (uint32_t) b * AQ;
-            const uint32_t adst = lds_addr(stage_a(stage) + G5_TPW * wave * 256);
+            const uint32_t adst = lds_addr(stage_a(stage) + C::TPW * wave * 256);
             // lanes of absent tokens sit out, except lane 0, so that every instruction issues (the waits count them)
 #pragma unroll
-            for (int i = 0; i < G5_NA; ++i)
-                if (G5_TPW * wave + 4 * i + (lane >> 4) < iss_ntok || lane == 0) dma_s128(aq, aoff[i] + bo, adst + 1024 * i);
-            if (lane < G5_TPW && (G5_TPW * wave + lane < iss_ntok || lane == 0)) dma_s32(aq, doff + bo, lds_addr(stage_d(stage) + G5_TPW * wave));
+            for (int i = 0; i < C::NA; ++i)
+                if (C::TPW * wave + 4 * i + (lane >> 4) < iss_ntok || lane == 0) dma_s128(aq, aoff[i] + bo, adst + 1024 * i);
+            if (lane < C::TPW && (C::TPW * wave + lane < iss_ntok || lane == 0)) dma_s32(aq, doff + bo, lds_addr(stage_d(stage) + C::TPW * wave));
             if (iss_step < nsteps - 1) {
                 ++iss_step;
                 if (++iss_b == nsb) { iss_b = 0; ++iss_it; }
@@ -606,68 +564,39 @@ __global__ __launch_bounds__(G5_THREADS, 1) void k_gemm(hy_moe_dev m, const uint
             }
             }
             if (b != nsb - 1) return;
-            // ---- the item's outputs.  Where two token-major copies fit in a stage (every wave has finished reading
-            // this one after a barrier), the waves' accumulators go there -- rows padded by one float against bank
-            // conflicts -- and wave w finishes tokens w, w + WAVES, ...: one output row per lane (SwiGLU of the gate
-            // and up values, or the route weight times the down value), stored as whole rows.
-            constexpr int OR = GU ? 16 * G5_HALF : G5_ROWS;   // output rows of the block
+            // ---- the item's outputs, through this stage (every wave has finished reading it after a barrier), TOKP
+            // tokens a pass: the waves' accumulators go there token-major -- rows padded by one float against bank
+            // conflicts -- and wave w finishes tokens w, w + WAVES, ... of the pass: one output row per lane (SwiGLU
+            // of the gate and up values, or the route weight times the down value), stored as whole rows.
+            constexpr int OR = GU ? 16 * C::HALF : C::ROWS;   // output rows of the block
             constexpr int LD = OR + 1;                         // floats per token in LDS
-            constexpr bool XCH = (GU ? 2 : 1) * GM_TOK * LD * 4 <= C::WB + C::AB;
-            if constexpr (XCH) {
-                float *s_o = (float *) stage_w(stage);         // gate (or down) values
-                float *s_u = s_o + GM_TOK * LD;                // up values
-                lds_barrier();
+            constexpr int NCOPY = GU ? 2 : 1;
+            constexpr int TOKP = NCOPY * 64 * LD * 4 <= C::WB + C::AB ? 64 : NCOPY * 32 * LD * 4 <= C::WB + C::AB ? 32 : 16;
+            static_assert(NCOPY * TOKP * LD * 4 <= C::WB + C::AB, "the exchange fits in a stage");
+            float *s_o = (float *) stage_w(stage);             // gate (or down) values
+            float *s_u = s_o + TOKP * LD;                      // up values
+            const int row0 = blockIdx.x * OR;
+            for (int p0 = 0; p0 < ntok; p0 += TOKP) {
+                lds_barrier();   // the stage (or the previous pass) is no longer read
                 {
-                    float *dst = GU && wave >= G5_HALF ? s_u : s_o;
-                    const int orow = (GU ? wave % G5_HALF : wave) * 16 + rr;
+                    float *dst = GU && wave >= C::HALF ? s_u : s_o;
+                    const int orow = (GU ? wave % C::HALF : wave) * 16 + rr;
 #pragma unroll
                     for (int tile = 0; tile < GM_TILES; ++tile) {
                         if (tile >= ntile) break;
+                        if (tile * 16 < p0 || tile * 16 >= p0 + TOKP) continue;
 #pragma unroll
-                        for (int v = 0; v < 4; ++v) dst[(tile * 16 + 4 * q + v) * LD + orow] = acc[tile][v];
+                        for (int v = 0; v < 4; ++v) dst[(tile * 16 - p0 + 4 * q + v) * LD + orow] = acc[tile][v];
                     }
                 }
                 lds_barrier();
-                const int row0 = blockIdx.x * OR;
-                for (int tok = wave; tok < ntok; tok += G5_WAVES) {
+                for (int tok = p0 + wave; tok < min(ntok, p0 + TOKP); tok += C::WAVES) {
                     float *o = out + (size_t) s_pair[it][tok] * (GU ? m.ff : m.n) + row0;
                     const float wt = GU ? 0.0f : s_wt[GU ? 0 : it][tok];
+                    const float *so = s_o + (tok - p0) * LD, *su = s_u + (tok - p0) * LD;
 #pragma unroll
-                    for (int r = lane; r < OR; r += 64)
-                        store_f32(o + r, GU ? hy_swiglu(s_o[tok * LD + r], s_u[tok * LD + r], m.clamp) : wt * s_o[tok * LD + r]);
+                    for (int r = lane; r < OR; r += 64) store_f32(o + r, GU ? hy_swiglu(so[r], su[r], m.clamp) : wt * so[r]);
                 }
-            } else if (GU) {
-                // SwiGLU needs the up rows of the upper half of the waves in the lower half: exchanged through this
-                // stage (its weights and activations, once every wave has finished reading them)
-                static_assert(G5_HALF * 16 * GM_TOK * 4 <= C::WB + C::AB, "the exchange fits in a stage");
-                float *s_up = (float *) stage_w(stage);
-                lds_barrier();
-                if (wave >= G5_HALF) {
-#pragma unroll
-                    for (int tile = 0; tile < GM_TILES; ++tile)
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) s_up[((wave % G5_HALF) * 16 + rr) * GM_TOK + tile * 16 + 4 * q + v] = acc[tile][v];
-                }
-                lds_barrier();
-                if (wave < G5_HALF) {
-#pragma unroll
-                    for (int tile = 0; tile < GM_TILES; ++tile)
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) {
-                            const int tok = tile * 16 + 4 * q + v;
-                            if (tok < ntok)
-                                store_f32(out + (size_t) s_pair[it][tok] * m.ff + row,
-                                          hy_swiglu(acc[tile][v], s_up[((wave % G5_HALF) * 16 + rr) * GM_TOK + tok], m.clamp));
-                        }
-                }
-            } else {
-#pragma unroll
-                for (int tile = 0; tile < GM_TILES; ++tile)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const int tok = tile * 16 + 4 * q + v;
-                        if (tok < ntok) store_f32(out + (size_t) s_pair[it][tok] * m.n + row, s_wt[GU ? 0 : it][tok] * acc[tile][v]);
-                    }
             }
 #pragma unroll
             for (int tile = 0; tile < GM_TILES; ++tile)
@@ -890,13 +819,13 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
     }
 }
 
-#define HY_GEMM_SWITCH(T, CALL)                                                                    \
+#define HY_GEMM_SWITCH(T, ...)                                                                    \
     switch (T) {                                                                                   \
-    case Q4_K: { constexpr int TT = Q4_K; CALL; }                                                 \
-    case Q5_K: { constexpr int TT = Q5_K; CALL; }                                                 \
-    case Q6_K: { constexpr int TT = Q6_K; CALL; }                                                 \
-    case IQ4_XS: { constexpr int TT = IQ4_XS; CALL; }                                             \
-    case IQ2_XS: { constexpr int TT = IQ2_XS; CALL; }                                             \
+    case Q4_K: { constexpr int TT = Q4_K; __VA_ARGS__; }                                                 \
+    case Q5_K: { constexpr int TT = Q5_K; __VA_ARGS__; }                                                 \
+    case Q6_K: { constexpr int TT = Q6_K; __VA_ARGS__; }                                                 \
+    case IQ4_XS: { constexpr int TT = IQ4_XS; __VA_ARGS__; }                                             \
+    case IQ2_XS: { constexpr int TT = IQ2_XS; __VA_ARGS__; }                                             \
     default: set_error("grouped GEMM: unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 
@@ -919,12 +848,14 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
         hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
         return check_launch("hy_moe_gemm_gate_up");
     }
-    const int rb = m.ff / (16 * G5_HALF);
     if ((size_t) n_pairs * (m.n / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_gate_up: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
-    dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
-    HY_GEMM_SWITCH(m.tg, hipLaunchKernelGGL((k_gemm<TT, true>), grid, dim3(G5_THREADS), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp,
-                                            nullptr, h);
-                   return check_launch("hy_moe_gemm_gate_up"));
+    HY_GEMM_SWITCH(m.tg, {
+        constexpr int W = g5_waves<TT, true>();
+        const int rb = m.ff / (8 * W);   // 8 W output rows a block
+        dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
+        hipLaunchKernelGGL((k_gemm<TT, true, W>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
+        return check_launch("hy_moe_gemm_gate_up");
+    });
 }
 int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int *order, const int *order_n, const int *egrp, int max_active,
                      const float *wts, float *y, hipStream_t s) {
@@ -935,12 +866,14 @@ int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int
         hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
         return check_launch("hy_moe_gemm_down");
     }
-    const int rb = m.n / G5_ROWS;
     if ((size_t) n_pairs * (m.ff / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_down: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
-    dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
-    HY_GEMM_SWITCH(m.td, hipLaunchKernelGGL((k_gemm<TT, false>), grid, dim3(G5_THREADS), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp,
-                                            wts, y);
-                   return check_launch("hy_moe_gemm_down"));
+    HY_GEMM_SWITCH(m.td, {
+        constexpr int W = g5_waves<TT, false>();
+        const int rb = m.n / (16 * W);   // 16 W output rows a block
+        dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
+        hipLaunchKernelGGL((k_gemm<TT, false, W>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
+        return check_launch("hy_moe_gemm_down");
+    });
 }
 
 } // namespace hy
