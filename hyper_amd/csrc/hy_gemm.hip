@@ -302,31 +302,32 @@ __device__ __forceinline__ void store_f32(float *g, float v) { asm volatile("glo
 // then makes the whole stage visible and frees stage (s - 1) % D for the next issue.  Nothing in the stream is a
 // compiler-visible global load, so the compiler adds no waits of its own.  The epilogue's stores are not counted:
 // a store still in flight only makes a later wait stricter (loads cannot overtake the loads before them).
-constexpr int G5_ITEMS = 16;                  // items per segment (their tables live in LDS)
-constexpr int G5_LDS_STAGES = 150 * 1024;     // LDS for the stages (the tables take the rest of the 160 KB)
-
-// Geometry of the stream kernel for weight type T and W waves (8 or 16) per block.
-template <int T, int W> struct G5 {
+// Geometry of the stream kernel for weight type T, W waves (8 or 16) per block and B blocks per CU (1 or 2): the
+// stages get what is left of the CU's 160 KB LDS after the item tables.
+template <int T, int W, int B> struct G5 {
     static constexpr int WAVES = W, THREADS = 64 * W, ROWS = 16 * W;   // a wave owns 16 weight rows
     static constexpr int HALF = W / 2;                          // gate/up: waves 0 .. HALF - 1 in gate, the rest in up
     static constexpr int TPW = GM_TOK / W;                      // activation rows each wave fetches per step
     static constexpr int NA = TPW / 4;                          // their 1 KB DMA instructions
     static constexpr int PER = 1024 / THREADS;                  // expert groups per thread in the item scan
+    static constexpr int ITEMS = B == 1 ? 16 : 8;               // items per segment (their tables live in LDS)
+    static constexpr int LDS_STAGES = B == 1 ? 150 * 1024 : 72 * 1024;
     static constexpr int BB = block_bytes(T);                   // weight bytes per row and 256 values
     static constexpr int TB = 16 * BB;                          // one wave's 16-row tile of a span
     static constexpr int WB = W * TB;                           // weights of a stage
     static constexpr int AB = GM_TOK * 256;                     // activation values of a stage (64 rows of 256)
     static constexpr int SB = WB + AB + 4 * GM_TOK;             // + the rows' Q8_K d
-    static constexpr int D = 4 * SB <= G5_LDS_STAGES ? 4 : 3 * SB <= G5_LDS_STAGES ? 3 : 2;   // stages
+    static constexpr int D = 4 * SB <= LDS_STAGES ? 4 : 3 * SB <= LDS_STAGES ? 3 : 2;   // stages
     static constexpr int N4 = TB / 1024, NR = TB - 1024 * N4, N1 = (NR + 255) / 256;   // tile DMAs: 1 KB, then 256 B
     static constexpr int L = N4 + N1 + NA + 1;                  // DMA instructions per wave and step
     static_assert(W == 8 || W == 16, "8 or 16 waves");
     static_assert(TB % 16 == 0 && NR % 4 == 0 && SB % 16 == 0, "DMA granules");
-    static_assert(D * SB <= G5_LDS_STAGES, "stages fit");
+    static_assert(D * SB <= LDS_STAGES, "stages fit");
     static_assert((D - 2) * L <= 63, "vmcnt range");
 };
-// waves per block: 16 (four per SIMD) where the type's step fits 128 registers, else 8
-template <int T, bool GU> constexpr int g5_waves() { return GU && (T == Q4_K || T == IQ4_XS) ? 16 : 8; }
+// Q4_K and IQ4_XS gate/up (whose step fits 128 registers): two blocks of 8 waves per CU, each block's stream
+// running independently of the other's; the rest: one block of 8 waves (up to 256 registers, deeper rings)
+template <int T, bool GU> constexpr int g5_blocks() { return GU && (T == Q4_K || T == IQ4_XS) ? 2 : 1; }
 
 __device__ __forceinline__ v4i mfma64(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
@@ -349,10 +350,9 @@ __device__ __forceinline__ void step_q4k(const uint8_t *wl, int q, const int8_t 
     const uint32_t s_lo = hd.y & 0x3F3F3F3Fu, m_lo = hd.z & 0x3F3F3F3Fu;   // chunks 0..3, one per byte
     const uint32_t s_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);         // chunks 4..7
     const uint32_t m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+    // accumulators: the first MFMA of a tile starts from zero, so tiles past ntile never need a value
     const v4i z = {0, 0, 0, 0};
     v4i d1[GM_TILES], d2[GM_TILES], dm[GM_TILES];
-#pragma unroll
-    for (int t = 0; t < GM_TILES; ++t) { d1[t] = z; d2[t] = z; dm[t] = z; }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint2 w = *(const uint2 *) (wl + 16 + 32 * j + 8 * q);
@@ -371,9 +371,9 @@ __device__ __forceinline__ void step_q4k(const uint8_t *wl, int q, const int8_t 
             const long a_lo = a_frag<true>(as, t, rr, 2 * j, q), a_hi = a_frag<true>(as, t, rr, 2 * j + 1, q);
             const v4i A = {(int) (uint32_t) a_lo, (int) (uint32_t) ((unsigned long long) a_lo >> 32), (int) (uint32_t) a_hi,
                            (int) (uint32_t) ((unsigned long long) a_hi >> 32)};
-            d1[t] = mfma64(A, B1, d1[t]);
-            d2[t] = mfma64(A, B2, d2[t]);
-            dm[t] = mfma64(A, Bm, dm[t]);
+            d1[t] = mfma64(A, B1, j ? d1[t] : z);
+            d2[t] = mfma64(A, B2, j ? d2[t] : z);
+            dm[t] = mfma64(A, Bm, j ? dm[t] : z);
         }
     }
     const float d = h2f(hd.x & 0xffff), dmin = h2f(hd.x >> 16);
@@ -390,18 +390,18 @@ __device__ __forceinline__ void step_q4k(const uint8_t *wl, int q, const int8_t 
 
 template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
-template <int T, bool GU, int W>
-__global__ __launch_bounds__(64 * W, 1) void k_gemm(hy_moe_dev m, const uint8_t *__restrict__ aq, int a_div, const int *__restrict__ order,
+template <int T, bool GU, int W, int B>
+__global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const uint8_t *__restrict__ aq, int a_div, const int *__restrict__ order,
                                                         const int *__restrict__ order_n, const int *__restrict__ egrp, const float *__restrict__ wts,
                                                         float *__restrict__ out) {
     static_assert(T != IQ4_NL, "IQ4_NL runs k_gemm_nl");
-    using C = G5<T, W>;
+    using C = G5<T, W, B>;
     constexpr int D = C::D, AQ = Q8K_BYTES;
     __shared__ __align__(16) uint8_t smem[D * C::SB];   // stage s at s * SB: weights [wave][TB], activations [64][256], d [64]
     __shared__ uint64_t s_scan[1024 + C::WAVES];                // per expert group: exclusive prefix of its items per tile class
-    __shared__ int s_item[G5_ITEMS][3];                  // first pair in order, tokens, weight slot
-    __shared__ int s_pair[G5_ITEMS][GM_TOK];             // pair index of each token of the segment's items
-    __shared__ float s_wt[GU ? 1 : G5_ITEMS][GM_TOK];    // down: their route weights
+    __shared__ int s_item[C::ITEMS][3];                  // first pair in order, tokens, weight slot
+    __shared__ int s_pair[C::ITEMS][GM_TOK];             // pair index of each token of the segment's items
+    __shared__ float s_wt[GU ? 1 : C::ITEMS][GM_TOK];    // down: their route weights
     __shared__ uint2 grid[T == IQ2_XS ? 512 : 1];
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, rr = lane & 15, q = lane >> 4;
     const int na = order_n[1];
@@ -455,8 +455,8 @@ __global__ __launch_bounds__(64 * W, 1) void k_gemm(hy_moe_dev m, const uint8_t 
     auto stage_a = [&](int s) { return (int8_t *) (smem + s * C::SB + C::WB); };
     auto stage_d = [&](int s) { return (const float *) (smem + s * C::SB + C::WB + C::AB); };
 
-    for (int seg = 0; seg < my_items; seg += G5_ITEMS) {
-        const int nit = min(G5_ITEMS, my_items - seg);
+    for (int seg = 0; seg < my_items; seg += C::ITEMS) {
+        const int nit = min(C::ITEMS, my_items - seg);
         __syncthreads();   // readers of the previous segment's tables are done
         for (int i = tid; i < nit; i += C::THREADS) {
             const int k = seg + i;
@@ -850,10 +850,10 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
     }
     if ((size_t) n_pairs * (m.n / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_gate_up: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
     HY_GEMM_SWITCH(m.tg, {
-        constexpr int W = g5_waves<TT, true>();
+        constexpr int W = 8, B = g5_blocks<TT, true>();
         const int rb = m.ff / (8 * W);   // 8 W output rows a block
-        dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
-        hipLaunchKernelGGL((k_gemm<TT, true, W>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
+        dim3 grid(rb, item_slots(rb, n_pairs, max_active, B));
+        hipLaunchKernelGGL((k_gemm<TT, true, W, B>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
         return check_launch("hy_moe_gemm_gate_up");
     });
 }
@@ -868,10 +868,10 @@ int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int
     }
     if ((size_t) n_pairs * (m.ff / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_down: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
     HY_GEMM_SWITCH(m.td, {
-        constexpr int W = g5_waves<TT, false>();
+        constexpr int W = 8, B = g5_blocks<TT, false>();
         const int rb = m.n / (16 * W);   // 16 W output rows a block
-        dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
-        hipLaunchKernelGGL((k_gemm<TT, false, W>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
+        dim3 grid(rb, item_slots(rb, n_pairs, max_active, B));
+        hipLaunchKernelGGL((k_gemm<TT, false, W, B>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
         return check_launch("hy_moe_gemm_down");
     });
 }
