@@ -41,8 +41,11 @@ enum {
 };
 
 /* Expert weights of one layer on the device (replaces MoeDev, src/kernels4.cuh:56-63): n_local experts,
-   gate/up [n_local][ff][row bytes of n values] and down [n_local][n][row bytes of ff values] in their GGUF
-   types; slot[e] (device, n_expert entries) = local index of expert e or -1. */
+   gate/up [n_local][ff rows of n values] and down [n_local][n rows of ff values] in their GGUF types, each expert
+   matrix in the tiled order the kernels read: 16-row tiles whose 256-value spans lie together -- span s (sb bytes,
+   the GGUF blocks of 256 values) of row r at byte ((r / 16) * nspan + s) * 16 * sb + (r % 16) * sb, nspan = values
+   per row / 256.  The block bytes themselves are GGUF's; hy_upload_experts writes this order from GGUF rows.
+   slot[e] (device, n_expert entries) = local index of expert e or -1. */
 typedef struct hy_moe_dev {
     const uint8_t *gate, *up, *down;
     int32_t tg, td;                 /* gate/up type, down type */
@@ -74,7 +77,8 @@ int hy_vec_dot_type(int type);
 size_t hy_q8_row_bytes(int vtype, int n);
 
 /* Upload the experts with slot_host[e] >= 0 to their slots (replaces upload_experts, src/experts.h:50 /
-   src/experts.cu:56-74).  Allocates gate/up/down and the slot table with hipMalloc; hy_free_experts releases. */
+   src/experts.cu:56-74), re-laid from GGUF rows into the tiled order above (ff and n multiples of 256, gb / db the
+   matrices' GGUF sizes).  Allocates gate/up/down and the slot table with hipMalloc; hy_free_experts releases. */
 int hy_upload_experts(const hy_expert_tensors *t, const int32_t *slot_host, int32_t ff, int32_t n, float clamp, hy_moe_dev *out);
 int hy_free_experts(hy_moe_dev *m);
 
