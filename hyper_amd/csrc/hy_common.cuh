@@ -130,6 +130,16 @@ __device__ __forceinline__ void wave_best(float &v, int &i, Better better) {
     }
     v = bv; i = bi;
 }
+// Block barrier for LDS hand-offs that leaves global loads in flight: waits for this wave's LDS operations only
+// (s_waitcnt lgkmcnt(0); vmcnt and expcnt left at their maxima), no memory fence -- __syncthreads() would also
+// wait for every outstanding global load, which would drain every prefetch in flight.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 template <int W> __device__ __forceinline__ int group_isum(int v) {   // sum over aligned groups of W lanes
 #pragma unroll
     for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -187,7 +197,7 @@ __device__ __forceinline__ void q8k_block_vals(const float (&xv)[4], uint8_t *ou
 #pragma unroll
     for (int i = 1; i < 4; ++i) { const float a = fabsf(xv[i]); if (a > am) { am = a; ix = i; } }
     int gi = 4 * lane + ix;
-    wave_best(am, gi, [](float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); });
+    wave_best(am, gi, [](float a, int ia, float b, int ib) { return (a > b) | ((a == b) & (ia < ib)); });
     uint32_t packed = 0;
     int s = 0;
     float d = 0.0f;
@@ -210,6 +220,46 @@ __device__ __forceinline__ void q8k_block_vals(const float (&xv)[4], uint8_t *ou
     ((uint32_t *) (out + 4))[lane] = packed;
     if ((lane & 3) == 0) ((int16_t *) (out + 260))[lane >> 2] = (int16_t) s;
     if (lane == 0) *(float *) out = d;
+}
+// The same Q8_K block by 16 lanes (an aligned DPP row; row lane l holds values 16 l .. 16 l + 15): each lane's
+// values are one int16 sum, and the signed max travels with the (|x|, index) winner of the row.
+__device__ __forceinline__ void q8k_block16(const float (&xv)[16], uint8_t *out) {
+    const int l = lane_id() & 15;
+    float am = fabsf(xv[0]), sv = xv[0];
+    int gi = 16 * l;
+#pragma unroll
+    for (int i = 1; i < 16; ++i) {
+        const float a = fabsf(xv[i]);
+        if (a > am) { am = a; sv = xv[i]; gi = 16 * l + i; }
+    }
+#define HY_B16_STEP(CTRL)                                                                                      \
+    {                                                                                                          \
+        const float oa = dpp_f<CTRL>(am), os = dpp_f<CTRL>(sv);                                                \
+        const int oi = dpp_i<CTRL>(gi);                                                                        \
+        if ((oa > am) | ((oa == am) & (oi < gi))) { am = oa; sv = os; gi = oi; }                                   \
+    }
+    HY_B16_STEP(DPP_XOR1) HY_B16_STEP(DPP_XOR2) HY_B16_STEP(DPP_HALF_MIRROR) HY_B16_STEP(DPP_MIRROR)
+#undef HY_B16_STEP
+    uint32_t pk[4] = {0u, 0u, 0u, 0u};
+    int s = 0;
+    float d = 0.0f;
+    if (am > 0.0f) {   // uniform over the row
+        const float iscale = -127.f / sv;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float pr = iscale * xv[i];
+            int q = nearest_int(pr);
+            q = q < 127 ? q : 127;
+            s += q;
+            pk[i >> 2] |= (uint32_t) (q & 0xff) << (8 * (i & 3));
+        }
+        d = 1.0f / iscale;
+    }
+    uint32_t *qs = (uint32_t *) (out + 4 + 16 * l);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qs[i] = pk[i];
+    ((int16_t *) (out + 260))[l] = (int16_t) s;
+    if (l == 0) *(float *) out = d;
 }
 __device__ __forceinline__ void q8k_block_wave(const float *x, uint8_t *out) {
     const float4 v = *(const float4 *) (x + 4 * lane_id());

@@ -1,14 +1,18 @@
 // Decode / short-verify path in three launches per MoE layer, with no hand-off between blocks of a launch
 // (device-scope fences and contended atomics cost more than a launch boundary on MI355X):
-//   k_router_q8      router GEMV, a wave per logit row, plus the Q8 blocks of x (gemv_f32, src/kernels4.cu:163-180);
-//   k_route_gate_up  every block routes its own token from the logits (one wave: softmax / top-k / renormalise /
-//                    shared gate, src/kernels4.cu:297-344), then a wave per ff row of its pair computes gate and up
-//                    against the Q8 x and SwiGLU (moe_gate_up, src/kernels4.cu:1973-2006);
-//   k_dec_down       each block quantizes the k hidden rows of its token into LDS once, then a wave per output row
-//                    computes the down dots of all k pairs and the combine in ascending expert id (moe_down +
-//                    moe_reduce, src/kernels4.cu:2007-2022, :1182-1206).
+//   k_router_q8      router GEMV, a wave per logit row with its loads in flight together, and separate waves for the
+//                    Q8 blocks of x (gemv_f32, src/kernels4.cu:163-180);
+//   k_route_gate_up  every block routes its own token from the logits (softmax / top-k / renormalise / shared gate,
+//                    src/kernels4.cu:297-344: up to 128 experts ranked by all eight waves at once, more by one wave),
+//                    then each wave takes rw ff rows of its pair, gate and up against the Q8 x, and one wave folds
+//                    and applies SwiGLU for the block's rows (moe_gate_up, src/kernels4.cu:1973-2006);
+//   k_dec_down       each block brings in its token's pairs, the slot table and the k hidden rows at once, quantizes
+//                    the rows into LDS (16 lanes per Q8_K block) while the down weights travel, then a wave per
+//                    output row computes the down dots of all k pairs and the combine in ascending expert id
+//                    (moe_down + moe_reduce, src/kernels4.cu:2007-2022, :1182-1206).
 // Inside a wave the 8-lane groups take 256-value items (Item<T>, exact integers), the group's integers are summed
-// with DPP, and each row's blocks are folded in block order by one lane: the same contract as the oracle.
+// with DPP, and each row's blocks are folded in block order: the same contract as the oracle.  Block barriers are
+// LDS-only (lds_barrier), so global loads stay in flight across them.
 #include "hy_internal.h"
 #include "hy_blocks.cuh"
 
@@ -19,24 +23,34 @@ namespace hy {
 constexpr int DEC_MAXP = 8;        // passes of 8 items per wave: up to 64 items (256-value spans) per wave
 constexpr int DEC_ROUTE_NT = 8;    // tokens the fused router takes (more: the separate kernels)
 
+__device__ __forceinline__ void wave_lds_sync() {   // a wave's own LDS writes, visible to its other lanes
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ---------------------------------------------------------------- k_router
 
-__device__ __forceinline__ bool rt_better2(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
+__device__ __forceinline__ bool rt_better2(float a, int ia, float b, int ib) { return (a > b) | ((a == b) & (ia < ib)); }   // no short circuit: no branches
 
-// softmax / top-k of one token by one wave (expert e in lane e % 64, slot e / 64), the contract of k_route
+// one token's logits in a wave: expert e in lane e % 64, slot e / 64; -inf / index 0x7fffffff past ne
 template <int V>
-__device__ void route_wave(const float *l, int ne, int k, int *ids, float *wts, float *sg) {
+__device__ __forceinline__ void route_load(const float *l, int ne, float (&v)[V], int (&vi)[V]) {
     const int lane = threadIdx.x & 63;
-    float v[V];
-    int vi[V];
-    float mx = -__builtin_huge_valf();
 #pragma unroll
     for (int i = 0; i < V; ++i) {
         const int e = lane + 64 * i;
         v[i] = e < ne ? l[e] : -__builtin_huge_valf();
         vi[i] = e < ne ? e : 0x7fffffff;
-        mx = fmaxf(mx, v[i]);
     }
+}
+// the logits -> probabilities of k_route: max, exp, the contract's sum (slot order, then the xor butterfly),
+// p = v / s; -1 for the empty slots
+template <int V>
+__device__ __forceinline__ void route_probs(float (&v)[V], const int (&vi)[V], int ne) {
+    float mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int i = 0; i < V; ++i) mx = fmaxf(mx, v[i]);
     mx = wave_max(mx);
     float acc = 0.0f;
 #pragma unroll
@@ -45,6 +59,17 @@ __device__ void route_wave(const float *l, int ne, int k, int *ids, float *wts, 
     const float s = wave_sum_xor(acc);
 #pragma unroll
     for (int i = 0; i < V; ++i) v[i] = vi[i] < ne ? v[i] / s : -1.0f;
+}
+
+// softmax / top-k of one token by one wave, the contract of k_route: k rounds of wave argmax over the lanes'
+// sorted candidates
+template <int V>
+__device__ void route_wave(const float *l, int ne, int k, int *ids, float *wts, float *sg) {
+    const int lane = threadIdx.x & 63;
+    float v[V];
+    int vi[V];
+    route_load<V>(l, ne, v, vi);
+    route_probs<V>(v, vi, ne);
 #pragma unroll
     for (int i = 1; i < V; ++i)
 #pragma unroll
@@ -77,35 +102,58 @@ __global__ __launch_bounds__(256) void k_router_q8(const float *__restrict__ W, 
                                                    uint8_t *__restrict__ xq, int nt) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int gw = blockIdx.x * 4 + wave, r = gw;
-    // Q8 of x: global wave gw quantizes Q8_K block gw (token gw / nb) or the Q8_0 pair 2 gw ..
-    if (VT == Q8_K) {
-        const int nb = kdim / 256;
-        if (gw < nt * nb) {
-            const int t = gw / nb, b = gw % nb;
-            q8k_block_wave(x + (size_t) t * xs + 256 * b, xq + ((size_t) t * nb + b) * Q8K_BYTES);
+    // waves [0, rows): a logit row each; waves [rows, rows + units): the Q8 of x, a Q8_K block (token q / nb) or a
+    // Q8_0 pair of blocks each -- no wave does both, so neither waits for the other
+    if (r >= rows) {
+        const int q = gw - rows;
+        if (VT == Q8_K) {
+            const int nb = kdim / 256;
+            if (q < nt * nb) {
+                const int t = q / nb, b = q % nb;
+                q8k_block_wave(x + (size_t) t * xs + 256 * b, xq + ((size_t) t * nb + b) * Q8K_BYTES);
+            }
+        } else {
+            const int nb = kdim / 32, npair = (nb + 1) / 2;
+            if (q < nt * npair) {
+                const int t = q / npair, b = 2 * (q % npair);
+                q8_0_pair_wave(x + (size_t) t * xs + 32 * b, xq + ((size_t) t * nb + b) * Q8_0_BYTES, b + 1 < nb, Q8_0_BYTES, 2);
+            }
         }
-    } else {
-        const int nb = kdim / 32, npair = (nb + 1) / 2;
-        if (gw < nt * npair) {
-            const int t = gw / npair, b = 2 * (gw % npair);
-            q8_0_pair_wave(x + (size_t) t * xs + 32 * b, xq + ((size_t) t * nb + b) * Q8_0_BYTES, b + 1 < nb, Q8_0_BYTES, 2);
-        }
+        return;
     }
-    // logits of row r for every token: lane L sums elements 256 i + 4 L + j with fmaf, then the butterfly
-    if (r >= rows) return;
+    // logits of row r for every token: lane L sums elements 256 i + 4 L + j with fmaf, then the butterfly.  The
+    // row's loads go out RB float4 at a time (one memory round trip per 256 RB values), then the fma chains.
+    constexpr int RB = 8;
+    const float *wr = W + (size_t) r * kdim;
     float acc[DEC_ROUTE_NT];
 #pragma unroll
     for (int t = 0; t < DEC_ROUTE_NT; ++t) acc[t] = 0.0f;
-    for (int e = 4 * lane; e < kdim; e += 256) {
-        const float4 w = *(const float4 *) (W + (size_t) r * kdim + e);
+    for (int e0 = 0; e0 < kdim; e0 += 256 * RB) {
+        float4 w[RB], xv[RB];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            const int e = e0 + 256 * i + 4 * lane;
+            w[i] = e < kdim ? *(const float4 *) (wr + e) : make_float4(0, 0, 0, 0);
+            xv[i] = e < kdim ? *(const float4 *) (x + e) : make_float4(0, 0, 0, 0);
+        }
 #pragma unroll
         for (int t = 0; t < DEC_ROUTE_NT; ++t) {
-            if (t < nt) {
-                const float4 xv = *(const float4 *) (x + (size_t) t * xs + e);
-                acc[t] = __builtin_fmaf(w.x, xv.x, acc[t]);
-                acc[t] = __builtin_fmaf(w.y, xv.y, acc[t]);
-                acc[t] = __builtin_fmaf(w.z, xv.z, acc[t]);
-                acc[t] = __builtin_fmaf(w.w, xv.w, acc[t]);
+            if (t >= nt) break;
+            if (t > 0) {
+#pragma unroll
+                for (int i = 0; i < RB; ++i) {
+                    const int e = e0 + 256 * i + 4 * lane;
+                    xv[i] = e < kdim ? *(const float4 *) (x + (size_t) t * xs + e) : make_float4(0, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < RB; ++i) {
+                if (e0 + 256 * i + 4 * lane < kdim) {
+                    acc[t] = __builtin_fmaf(w[i].x, xv[i].x, acc[t]);
+                    acc[t] = __builtin_fmaf(w[i].y, xv[i].y, acc[t]);
+                    acc[t] = __builtin_fmaf(w[i].z, xv[i].z, acc[t]);
+                    acc[t] = __builtin_fmaf(w[i].w, xv[i].w, acc[t]);
+                }
             }
         }
     }
@@ -155,12 +203,17 @@ template <int VT> __device__ __forceinline__ float q8_scale(const uint8_t *y, in
 // ---------------------------------------------------------------- k_dec_gate_up
 
 constexpr int DEC_GU_TV = 2 * 256;   // fold inputs per wave: 2 matrices x up to 256 blocks (IQ4_NL, n <= 8192)
-constexpr int DEC_GU_WAVES = 8;      // ff rows per block (a wave each)
+constexpr int DEC_GU_WAVES = 8;      // waves per block, rw ff rows each
+#ifndef HY_DEC_GU_BLOCKS
+#define HY_DEC_GU_BLOCKS 768
+#endif
+constexpr int DEC_GU_BLOCKS = HY_DEC_GU_BLOCKS;   // grid size the rows per wave aim below
 
 template <int T, int V, int NP>
 __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev m, const float *__restrict__ logits, int ls, int ne, int k,
                                                                    const uint8_t *__restrict__ xq, int *__restrict__ ids,
-                                                                   float *__restrict__ wts, float *__restrict__ sg, float *__restrict__ h) {
+                                                                   float *__restrict__ wts, float *__restrict__ sg, float *__restrict__ h,
+                                                                   int rw) {
     constexpr int VT = vec_dot_type(T), BE = block_elems(T);
     constexpr int SPAN_W = 256 / BE * block_bytes(T);
     constexpr int SPAN_Y = VT == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
@@ -169,59 +222,151 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     __shared__ float s_wts[64], s_sg;
     __shared__ int s_slot[64 * V];
     __shared__ uint2 grid[T == IQ2_XS ? 512 : 1];
+    __shared__ float s_xd[DEC_GU_TV / 2];   // activation scales of the token's Q8 row, one per weight block
+    __shared__ __align__(16) float s_l[DEC_GU_WAVES][V <= 2 ? 64 * V : 4];   // each wave's copy of the logits
+    __shared__ __align__(16) float s_p[V <= 2 ? 64 * V : 4];
+    __shared__ int s_sel[2][65];   // experts by logit rank (0..k), by probability rank
     const int p = blockIdx.y, t = p / k, j = p - t * k;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
-    // the slot table comes in alongside the logits; the token's routing (every block of the token computes the
-    // same bits); the first block of each token publishes it for the down projection
-    for (int e = (int) threadIdx.x; e < ne; e += 64 * DEC_GU_WAVES) s_slot[e] = m.slot[e];
-    if (wave == 0) route_wave<V>(logits + (size_t) t * ls, ne, k, s_ids, s_wts, sg ? &s_sg : nullptr);
-    if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
-    __syncthreads();
-    if (blockIdx.x == 0 && j == 0 && wave == 0) {
-        if (lane < k) { ids[(size_t) t * k + lane] = s_ids[lane]; wts[(size_t) t * k + lane] = s_wts[lane]; }
-        if (lane == 0 && sg) sg[t] = s_sg;
+    const int ff = m.ff, ng = m.n / 256, nb = m.n / BE;
+    const uint8_t *y = xq + (size_t) t * ng * SPAN_Y;
+    const float *lg = logits + (size_t) t * ls;
+    // the token's routing: every block of the token computes the same bits
+    int e_sel;   // the expert of pair j
+    if constexpr (V <= 2) {
+        // Up to 128 experts.  p = softmax(l) is monotone in l, so the order of k_route (p descending, then the
+        // lower index) is the order of the logits unless two probabilities round to the same value.  Every wave
+        // ranks 8 V experts by logit (4 / V lanes per expert, each against 16 V^2 experts, the counts summed with
+        // DPP) while wave 0 computes the probabilities; after one barrier every wave reads the k + 1 best by logit
+        // and, if their probabilities fall strictly (the usual case), the logit order is the contract's.  Else
+        // the ranking is redone on the probabilities (block-uniform branch).
+        static_assert(DEC_GU_WAVES == 8, "eight rank chunks");
+        constexpr int CH = 8 * V, LPE = 64 / CH, VPL = 64 * V / LPE;   // experts per wave, lanes per expert, values per lane
+        const int tid = (int) threadIdx.x;
+        float lv[V];
+        int li[V];
+        route_load<V>(lg, ne, lv, li);
+        const float lsg = (wave == 0 && sg) ? lg[ne] : 0.0f;
+        const int sl = tid < ne ? m.slot[tid] : -1;
+        const float xd = tid < nb ? q8_scale<VT>(y, tid) : 0.0f;
+        float *my_l = s_l[wave];
+#pragma unroll
+        for (int i = 0; i < V; ++i) my_l[lane + 64 * i] = lv[i];
+        wave_lds_sync();
+        const int c = lane / LPE, q = lane % LPE, e = wave * CH + c;
+        // rank of expert e under `vals` (index convention of route_load: past ne -> 0x7fffffff)
+        auto rank_of = [&](const float *vals) {
+            const float ve = vals[e];
+            const int ie = e < ne ? e : 0x7fffffff;
+            float w[VPL];
+#pragma unroll
+            for (int u = 0; u < VPL; u += 4) {
+                const float4 f4 = *(const float4 *) (vals + q * VPL + u);
+                w[u] = f4.x; w[u + 1] = f4.y; w[u + 2] = f4.z; w[u + 3] = f4.w;
+            }
+            int cnt = 0;
+#pragma unroll
+            for (int u = 0; u < VPL; ++u) {
+                const int iu = q * VPL + u < ne ? q * VPL + u : 0x7fffffff;
+                cnt += rt_better2(w[u], iu, ve, ie) ? 1 : 0;
+            }
+            cnt += dpp_i<DPP_XOR1>(cnt);
+            cnt += dpp_i<DPP_XOR2>(cnt);
+            if constexpr (LPE == 8) cnt += dpp_i<DPP_HALF_MIRROR>(cnt);
+            return cnt;
+        };
+        const int rl = rank_of(my_l);
+        if (q == 0 && e < ne && rl <= k) s_sel[0][rl] = e;
+        if (wave == 0) {
+            float v[V];
+#pragma unroll
+            for (int i = 0; i < V; ++i) v[i] = lv[i];
+            route_probs<V>(v, li, ne);
+#pragma unroll
+            for (int i = 0; i < V; ++i) s_p[lane + 64 * i] = v[i];
+        }
+        if (tid < ne) s_slot[tid] = sl;
+        if (tid < nb) s_xd[tid] = xd;
+        if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
+        lds_barrier();
+        // lane r <= k: the expert of logit rank r (ranks stop at ne - 1; a stale entry, possible only with NaN
+        // logits, is clamped to a valid index)
+        int er = lane <= k && lane < ne ? s_sel[0][lane] : 0;
+        er = (unsigned) er < (unsigned) ne ? er : 0;
+        float pr = lane <= k && lane < ne ? s_p[er] : 0.0f;
+        const float pn = __shfl_down(pr, 1);
+        const bool tie = k < 64 ? (lane < k && lane + 1 < ne && !(pr > pn)) : true;
+        if (__ballot(tie)) {   // block-uniform: every wave read the same LDS
+            const int rp = rank_of(s_p);
+            if (q == 0 && e < ne && rp < k) s_sel[1][rp] = e;
+            lds_barrier();
+            er = lane < k ? s_sel[1][lane] : 0;
+            er = (unsigned) er < (unsigned) ne ? er : 0;
+            pr = lane < k ? s_p[er] : 0.0f;
+        }
+        float tot = 0.0f;
+        for (int r = 0; r < k; ++r) tot = tot + readlane_f(pr, r);   // selection order
+        e_sel = __builtin_amdgcn_readlane(er, j);
+        if (blockIdx.x == 0 && j == 0 && wave == 0) {   // the first block of each token publishes the routing
+            if (lane < k) { ids[(size_t) t * k + lane] = er; wts[(size_t) t * k + lane] = pr / tot; }
+            if (lane == 0 && sg) sg[t] = 1.0f / (1.0f + hy_expf(-lsg));
+        }
+    } else {
+        // wave 0 routes the token while the other waves bring in the slot table and the activation scales
+        if (wave == 0) {
+            route_wave<V>(lg, ne, k, s_ids, s_wts, sg ? &s_sg : nullptr);
+        } else {
+            const int i0 = (int) threadIdx.x - 64, stride = 64 * (DEC_GU_WAVES - 1);
+            for (int ex = i0; ex < ne; ex += stride) s_slot[ex] = m.slot[ex];
+            for (int b = i0; b < nb; b += stride) s_xd[b] = q8_scale<VT>(y, b);
+        }
+        if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
+        lds_barrier();
+        if (blockIdx.x == 0 && j == 0 && wave == 0) {   // the first block of each token publishes the routing
+            if (lane < k) { ids[(size_t) t * k + lane] = s_ids[lane]; wts[(size_t) t * k + lane] = s_wts[lane]; }
+            if (lane == 0 && sg) sg[t] = s_sg;
+        }
+        e_sel = s_ids[j];
     }
-    const int e = s_ids[j];
+    const int e = e_sel;
     const int slot = (e >= 0 && e < ne) ? s_slot[e] : -1;
     if (slot < 0) return;   // uniform over the block: the pair's h rows are not written
-    const int ff = m.ff, ng = m.n / 256, nb = m.n / BE, items = 2 * ng;
-    const int row = blockIdx.x * DEC_GU_WAVES + wave;
-    if (row >= ff) return;  // wave-uniform; no block barrier follows
-    const uint8_t *Wg = m.gate + (size_t) slot * m.gate_bytes + tiled_off(row, 0, ng, SPAN_W);
-    const uint8_t *Wu = m.up + (size_t) slot * m.gate_bytes + tiled_off(row, 0, ng, SPAN_W);
-    const uint8_t *y = xq + (size_t) t * ng * SPAN_Y;
+    // the wave's rows row0 .. row0 + rw - 1, each 2 ng items (gate spans, then up spans); rows past ff sit out
+    const int per_row = 2 * ng, nwi = rw * per_row, row0 = (blockIdx.x * DEC_GU_WAVES + wave) * rw;
+    const uint8_t *Wg = m.gate + (size_t) slot * m.gate_bytes, *Wu = m.up + (size_t) slot * m.gate_bytes;
     Item<T> it[NP];
 #pragma unroll
     for (int ps = 0; ps < NP; ++ps) {
-        const int i = g + 8 * ps;
-        if (i < items) {
-            const int mat = i >= ng, gi = i - mat * ng;
-            it[ps].load((mat ? Wu : Wg) + (size_t) gi * HY_TILE * SPAN_W, L);
-        }
+        const int i = g + 8 * ps, r = i / per_row, ii = i - r * per_row, mat = ii >= ng, gi = ii - mat * ng;
+        if (i < nwi && row0 + r < ff) it[ps].load((mat ? Wu : Wg) + tiled_off(row0 + r, gi, ng, SPAN_W), L);
     }
     float *tw = tv[wave];
 #pragma unroll
     for (int ps = 0; ps < NP; ++ps) {
-        const int i = g + 8 * ps;
-        if (8 * ps >= items) break;   // wave-uniform
-        const bool valid = i < items;
-        const int mat = i >= ng, gi = i - mat * ng;
+        if (8 * ps >= nwi) break;   // wave-uniform
+        const int i = g + 8 * ps, r = i / per_row, ii = i - r * per_row, mat = ii >= ng, gi = ii - mat * ng;
+        const bool valid = i < nwi && row0 + r < ff;
         if constexpr (T == IQ2_XS) it[ps].grid = grid;
-        item_t<T>(it[ps], y, gi, L, valid, tw, mat * nb + (T == IQ4_NL ? 8 * gi : gi));
+        item_t<T>(it[ps], y, gi, L, valid, tw, r * 2 * nb + mat * nb + (T == IQ4_NL ? 8 * gi : gi));
     }
-    // the wave's own LDS writes, read back by its lane 0 (LDS operations of a wave complete in order)
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane == 0) {
-        float ag = 0.0f, au = 0.0f;
-        for (int b = 0; b < nb; ++b) {
-            const float xd = q8_scale<VT>(y, b);
-            ag = __builtin_fmaf(xd, tw[b], ag);
-            au = __builtin_fmaf(xd, tw[nb + b], au);
-        }
-        h[(size_t) p * ff + row] = hy_swiglu(ag, au, m.clamp);
+    lds_barrier();
+    // the folds, in block order, by wave 0: lane l takes the block's row l (wave l / rw, its row l % rw); eight
+    // blocks' inputs per LDS round trip, then the fma chain
+    if (wave != 0 || lane >= DEC_GU_WAVES * rw) return;
+    const int row = blockIdx.x * DEC_GU_WAVES * rw + lane;
+    if (row >= ff) return;
+    const float *tg = tv[lane / rw] + (lane % rw) * 2 * nb;
+    float ag = 0.0f, au = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += 8) {
+        float xa[8], ga[8], ua[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (b0 + u < nb) { xa[u] = s_xd[b0 + u]; ga[u] = tg[b0 + u]; ua[u] = tg[nb + b0 + u]; }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (b0 + u < nb) { ag = __builtin_fmaf(xa[u], ga[u], ag); au = __builtin_fmaf(xa[u], ua[u], au); }
     }
+    h[(size_t) p * ff + row] = hy_swiglu(ag, au, m.clamp);
 }
 
 // ---------------------------------------------------------------- k_dec_down
@@ -229,12 +374,6 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
 constexpr int DEC_DN_WAVES = 8;       // output rows per block (a wave each)
 constexpr int DEC_DN_TV = 512;        // fold inputs per wave: k pairs x blocks of ff (k * nb <= 512)
 constexpr int DEC_DN_HQ = 32768;      // LDS bytes for the token's k quantized hidden rows
-
-__device__ __forceinline__ void wave_lds_sync() {   // a wave's own LDS writes, visible to its other lanes
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 template <int T, int NP>
 __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, const float *__restrict__ h, const int *__restrict__ ids,
@@ -245,16 +384,61 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     constexpr int SPAN_Y = VT == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
     __shared__ __align__(16) uint8_t hq[DEC_DN_HQ];
     __shared__ float tv[DEC_DN_WAVES][DEC_DN_TV];
-    __shared__ float fo[DEC_DN_WAVES][64];
-    __shared__ int ordw[DEC_DN_WAVES][64];
+    __shared__ int s_slot[2 * 64 * DEC_DN_WAVES];   // n_expert <= 1024
+    __shared__ int s_ord[DEC_DN_WAVES][64];
     __shared__ uint2 grid[T == IQ2_XS ? 512 : 1];
     const int t = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
     const int n = m.n, ff = m.ff, ng = ff / 256, nb = ff / BE, items = k * ng;
     const int row = blockIdx.x * DEC_DN_WAVES + wave;
     const bool row_ok = row < n;
-    // lane j < k: pair j's expert and slot (-1: skipped); `okm`: the valid pairs as a wave-uniform bit mask
+    const float *hp = h + (size_t) t * k * ff;
+    // Everything the block reads first goes out together: lane j < k's pair (expert, weight), the slot table and
+    // the first batch of hidden rows (all k pairs' rows; those of skipped pairs are read but never used).
     const int my_e = lane < k ? ids[t * k + lane] : -1;
-    const int my_slot = (my_e >= 0 && my_e < m.n_expert) ? m.slot[my_e] : -1;
+    const float my_w = lane < k ? wts[t * k + lane] : 0.0f;
+    const int tid = (int) threadIdx.x;
+    const int sl0 = tid < m.n_expert ? m.slot[tid] : -1;
+    const int sl1 = tid + 64 * DEC_DN_WAVES < m.n_expert ? m.slot[tid + 64 * DEC_DN_WAVES] : -1;
+    float sh_x = 0.0f, sh_g = 1.0f;   // the shared expert's value and gate of this output, used at the end
+    if (shexp && row_ok) {
+        sh_x = shexp[(size_t) t * n + row];
+        if (sg) sh_g = sg[t];
+    }
+    // Hidden-row units: Q8_K a 256-value block per 16-lane row (4 per wave), Q8_0 a pair of 32-value blocks per
+    // wave (QU per wave); a batch is UB units.
+    constexpr int QU = 4;
+    constexpr int UB = (VT == Q8_K ? 4 : QU) * DEC_DN_WAVES;
+    const int npair = (nb + 1) / 2, units = VT == Q8_K ? k * ng : k * npair;
+    float xv[16];
+    auto hload = [&](int ub) {
+        if constexpr (VT == Q8_K) {
+            const int u = ub + 4 * wave + (lane >> 4);
+            if (u < units) {
+                const float4 *src = (const float4 *) (hp + (size_t) u * 256 + 16 * (lane & 15));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float4 v = src[i];
+                    xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < QU; ++q) {
+                const int u = ub + wave + q * DEC_DN_WAVES;
+                xv[q] = 0.0f;
+                if (u < units) {
+                    const int j = u / npair, b = 2 * (u - j * npair);
+                    if (lane < 32 || b + 1 < nb) xv[q] = hp[(size_t) j * ff + 32 * b + lane];
+                }
+            }
+        }
+    };
+    hload(0);
+    s_slot[tid] = sl0;
+    s_slot[tid + 64 * DEC_DN_WAVES] = sl1;
+    lds_barrier();
+    // lane j < k: pair j's slot (-1: skipped); `okm`: the valid pairs as a wave-uniform bit mask
+    const int my_slot = (my_e >= 0 && my_e < m.n_expert) ? s_slot[my_e] : -1;
     const uint64_t okm = __ballot(my_slot >= 0);
     auto pair_ok = [&](int j) { return (okm >> j) & 1; };
     Item<T> it[NP];
@@ -267,57 +451,38 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
             if (i < items && row_ok && sl >= 0) it[ps].load(m.down + (size_t) sl * m.down_bytes + tiled_off(row, gi, ng, SPAN_W), L);
         }
     };
-    // the first round of weight bytes goes out before the hidden rows are quantized
+    // the first round of weight bytes goes out before the hidden rows are quantized (wave-uniform branches below)
     load_round(0);
-    {
-        const float *hp = h + (size_t) t * k * ff;
-        // a wave's units: all their loads first, then the quantization (one memory round trip)
-        constexpr int QU = 4;   // units per wave per batch
+    // while they travel: each valid pair's rank by (expert id, j) is its place in the combine; `ordl` (lane r) is
+    // the lane of rank r
+    int rank = 0;
+    for (int i = 0; i < k; ++i) {   // uniform trip count; the other lanes' experts by lane read
+        const int ei = __builtin_amdgcn_readlane(my_e, i);
+        if (pair_ok(i) && (ei < my_e || (ei == my_e && i < lane))) ++rank;
+    }
+    const bool mine = lane < k && pair_ok(lane);
+    if (mine) s_ord[wave][rank] = lane;
+    wave_lds_sync();
+    const int ordl = s_ord[wave][lane];
+    auto hquant = [&](int ub) {
         if constexpr (VT == Q8_K) {
-            const int units = k * ng;
-            for (int u0 = wave; u0 < units; u0 += QU * DEC_DN_WAVES) {
-                float xv[QU][4];
-#pragma unroll
-                for (int q = 0; q < QU; ++q) {
-                    const int u = u0 + q * DEC_DN_WAVES;
-                    if (u < units && pair_ok(u / ng)) {
-                        const float4 v = *(const float4 *) (hp + (size_t) u * 256 + 4 * lane);
-                        xv[q][0] = v.x; xv[q][1] = v.y; xv[q][2] = v.z; xv[q][3] = v.w;
-                    }
-                }
-#pragma unroll
-                for (int q = 0; q < QU; ++q) {
-                    const int u = u0 + q * DEC_DN_WAVES;
-                    if (u < units && pair_ok(u / ng)) q8k_block_vals(xv[q], hq + (size_t) u * Q8K_BYTES);   // wave-uniform
-                }
-            }
+            const int u = ub + 4 * wave + (lane >> 4);
+            if (u < units && pair_ok(u / ng)) q8k_block16(xv, hq + (size_t) u * Q8K_BYTES);   // uniform over the row
         } else {
-            const int npair = (nb + 1) / 2, units = k * npair;
-            for (int u0 = wave; u0 < units; u0 += QU * DEC_DN_WAVES) {
-                float xv[QU];
 #pragma unroll
-                for (int q = 0; q < QU; ++q) {
-                    const int u = u0 + q * DEC_DN_WAVES;
-                    xv[q] = 0.0f;
-                    if (u < units) {
-                        const int j = u / npair, b = 2 * (u - j * npair);
-                        if (pair_ok(j) && (lane < 32 || b + 1 < nb)) xv[q] = hp[(size_t) j * ff + 32 * b + lane];
-                    }
-                }
-#pragma unroll
-                for (int q = 0; q < QU; ++q) {
-                    const int u = u0 + q * DEC_DN_WAVES;
-                    if (u < units) {
-                        const int j = u / npair, b = 2 * (u - j * npair);
-                        if (pair_ok(j))   // wave-uniform
-                            q8_0_pair_vals(xv[q], hq + (size_t) j * ng * SPAN_Y + (size_t) b * Q8_0_BYTES, b + 1 < nb, Q8_0_BYTES, 2);
-                    }
+            for (int q = 0; q < QU; ++q) {
+                const int u = ub + wave + q * DEC_DN_WAVES;
+                if (u < units) {
+                    const int j = u / npair, b = 2 * (u - j * npair);
+                    if (pair_ok(j)) q8_0_pair_vals(xv[q], hq + (size_t) j * ng * SPAN_Y + (size_t) b * Q8_0_BYTES, b + 1 < nb, Q8_0_BYTES, 2);
                 }
             }
         }
-    }
+    };
+    hquant(0);
+    for (int ub = UB; ub < units; ub += UB) { hload(ub); hquant(ub); }
     if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
-    __syncthreads();
+    lds_barrier();
     if (!row_ok) return;   // wave-uniform; no block barrier follows
     float *tw = tv[wave];
     for (int base = 0; base < items; base += 8 * NP) {   // wave-uniform rounds of up to 8 NP items
@@ -333,31 +498,33 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
         }
     }
     wave_lds_sync();
-    // lane j folds pair j in block order; its rank among the valid pairs by (expert id, j) is its place in the sum
-    int rank = 0;
-    for (int i = 0; i < k; ++i) {   // uniform trip count; the other lanes' experts by lane read
-        const int ei = __shfl(my_e, i);
-        if (pair_ok(i) && (ei < my_e || (ei == my_e && i < lane))) ++rank;
-    }
-    if (lane < k && pair_ok(lane)) {
+    // lane j folds pair j in block order
+    float fo = 0.0f;
+    if (mine) {   // LDS reads four blocks at a time, then the fma chain
         const uint8_t *yj = hq + (size_t) lane * ng * SPAN_Y;
+        const float *tj = tw + lane * nb;
         float acc = 0.0f;
-        for (int b = 0; b < nb; ++b) acc = __builtin_fmaf(q8_scale<VT>(yj, b), tw[lane * nb + b], acc);
-        fo[wave][lane] = wts[t * k + lane] * acc;
-        ordw[wave][rank] = lane;
-    }
-    wave_lds_sync();
-    if (lane == 0) {
-        const int nv = __builtin_popcountll(okm);
-        float acc = 0.0f;
-        bool first = true;
-        if (shexp) { acc = (sg ? sg[t] : 1.0f) * shexp[(size_t) t * n + row]; first = false; }
-        for (int r = 0; r < nv; ++r) {
-            const float v = fo[wave][ordw[wave][r]];
-            if (first) { acc = v; first = false; } else acc = acc + v;
+        for (int b0 = 0; b0 < nb; b0 += 4) {
+            float sc[4], tq[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (b0 + u < nb) { sc[u] = q8_scale<VT>(yj, b0 + u); tq[u] = tj[b0 + u]; }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (b0 + u < nb) acc = __builtin_fmaf(sc[u], tq[u], acc);
         }
-        out[(size_t) t * n + row] = acc;
+        fo = my_w * acc;
     }
+    // the combine in rank order, each value read from the lane that holds it
+    const int nv = __builtin_popcountll(okm);
+    float acc = 0.0f;
+    bool first = true;
+    if (shexp) { acc = sh_g * sh_x; first = false; }
+    for (int r = 0; r < nv; ++r) {
+        const float v = readlane_f(fo, __builtin_amdgcn_readlane(ordl, r));
+        if (first) { acc = v; first = false; } else acc = acc + v;
+    }
+    if (lane == 0) out[(size_t) t * n + row] = acc;
 }
 
 // ---------------------------------------------------------------- launchers
@@ -382,7 +549,7 @@ int launch_router_q8(const float *W, int rows, int kdim, const float *x, int xs,
         return rc;
     }
     const int qwaves = vtype == Q8_K ? nt * (kdim / 256) : nt * ((kdim / 32 + 1) / 2);
-    const int blocks = (std::max(rows, qwaves) + 3) / 4;
+    const int blocks = (rows + qwaves + 3) / 4;
     if (vtype == Q8_K)
         hipLaunchKernelGGL((k_router_q8<Q8_K>), dim3(blocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, (uint8_t *) xq, nt);
     else
@@ -395,10 +562,15 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
     const int ng = m.n / 256, nb = m.n / block_elems(m.tg);
     if (2 * ng > 8 * DEC_MAXP || 2 * nb > DEC_GU_TV) { set_error("hy_moe_route_gate_up: n = %d exceeds %d", m.n, 256 * 4 * DEC_MAXP); return HY_EBAD_SHAPE; }
     if (nt == 0) return HY_OK;
-    dim3 grid((m.ff + DEC_GU_WAVES - 1) / DEC_GU_WAVES, nt * k);
+    // rows per wave: every block routes its token again, so the grid is kept near DEC_GU_BLOCKS blocks, within the
+    // item registers (rw 2 ng <= 8 DEC_MAXP) and the fold inputs (rw 2 nb <= DEC_GU_TV)
+    int rw = 1;
+    auto nblocks = [&](int r) { return (long) ((m.ff + DEC_GU_WAVES * r - 1) / (DEC_GU_WAVES * r)) * nt * k; };
+    while (rw < 8 && nblocks(rw) > DEC_GU_BLOCKS && (rw + 1) * 2 * ng <= 8 * DEC_MAXP && (rw + 1) * 2 * nb <= DEC_GU_TV) ++rw;
+    dim3 grid((m.ff + DEC_GU_WAVES * rw - 1) / (DEC_GU_WAVES * rw), nt * k);
     const int V = (ne + 63) / 64;
-    const int np = (2 * ng + 7) / 8;   // passes of 8 items
-#define HY_RGU(VV, NN) hipLaunchKernelGGL((k_route_gate_up<TT, VV, NN>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h)
+    const int np = (rw * 2 * ng + 7) / 8;   // passes of 8 items
+#define HY_RGU(VV, NN) hipLaunchKernelGGL((k_route_gate_up<TT, VV, NN>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, rw)
 #define HY_RGU_V(NN) if (V <= 1) HY_RGU(1, NN); else if (V <= 2) HY_RGU(2, NN); else if (V <= 4) HY_RGU(4, NN); else if (V <= 8) HY_RGU(8, NN); else HY_RGU(16, NN);
     HY_DEC_SWITCH(m.tg, {
         if (np <= 2) { HY_RGU_V(2) } else if (np <= 4) { HY_RGU_V(4) } else { HY_RGU_V(8) }
@@ -413,7 +585,8 @@ int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const f
                     float *out, int nt, hipStream_t s) {
     const int vt = vec_dot_type(m.td), ng = m.ff / 256, nb = m.ff / block_elems(m.td);
     const int span_y = vt == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
-    if (k > 64 || k * nb > DEC_DN_TV || (size_t) k * ng * span_y > (size_t) DEC_DN_HQ) return HY_EUNSUPPORTED_TYPE;
+    if (k > 64 || k * nb > DEC_DN_TV || (size_t) k * ng * span_y > (size_t) DEC_DN_HQ || m.n_expert > 2 * 64 * DEC_DN_WAVES)
+        return HY_EUNSUPPORTED_TYPE;
     if (nt == 0) return HY_OK;
     dim3 grid((m.n + DEC_DN_WAVES - 1) / DEC_DN_WAVES, nt);
     const int np = (k * ng + 7) / 8;   // passes of 8 items (more than 8: rounds)

@@ -243,16 +243,6 @@ template <class R> __device__ __forceinline__ void touch_regs(const R &r) {
     for (int i = 0; i < (int) (sizeof(R) / 4); ++i) asm volatile("" ::"v"(w[i]));
 }
 
-// Block barrier for LDS hand-offs that leaves global loads in flight: waits for this wave's LDS operations only
-// (s_waitcnt lgkmcnt(0); vmcnt and expcnt left at their maxima), no memory fence -- __syncthreads() would also
-// wait for every outstanding global load, which would drain the prefetch stream at every step.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
 // Direct global -> LDS loads and the epilogue's stores, issued from inline asm so that the compiler's wait
 // bookkeeping sees only the weight loads of the stream.  (Its bookkeeping treats LDS loads, register loads and
 // stores as possibly completing out of order and would then wait for all of them at every step.)  Vector memory

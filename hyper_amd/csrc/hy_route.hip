@@ -61,7 +61,7 @@ int launch_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, 
 }
 
 // ---------------------------------------------------------------- routing (A2)
-__device__ __forceinline__ bool rt_better(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
+__device__ __forceinline__ bool rt_better(float a, int ia, float b, int ib) { return (a > b) | ((a == b) & (ia < ib)); }   // no short circuit: no branches
 
 // a wave per token, expert e in lane e % 64 slot e / 64 (V slots): max, exp, the contract's sum (lane L adds
 // its experts in slot order, then the xor butterfly), p = v / s; each lane sorts its V candidates

@@ -91,6 +91,45 @@ def test_route_gate_up_and_down_bitexact(cuda, tg, td, E, d, ff, k, nt, sg):
         assert rel_l2(out.cpu().numpy(), out_r) <= TOL
 
 
+def _tie_logits(E, seed):
+    """Three tokens whose routing leans on the tie rules: equal top logits, top logits a few ulps apart (their
+    probabilities can round to one value), and all logits equal (the selection is the k lowest ids)."""
+    rng = np.random.default_rng(seed)
+    lg = (rng.standard_normal((3, E)) * 0.5).astype(np.float32)
+    top = rng.permutation(E)[:6]
+    lg[0, top] = 2.0
+    lg[1] -= 2.0
+    lg[1, top] = np.float32(0.25) - np.arange(6, dtype=np.float32) * np.float32(2.0 ** -26)   # one ulp apart
+    lg[2, :] = 0.25
+    return lg
+
+
+@pytest.mark.parametrize("E,k", [(40, 8), (128, 8), (8, 8), (64, 64)])
+def test_route_gate_up_tie_rules(cuda, E, k):
+    """The fused routing (logit ranks, checked against the probabilities, else ranks of the probabilities)
+    selects, orders and weights the experts exactly as the oracle's router on ties."""
+    tg = td = GType.Q4_K
+    d, ff = 2048, 256
+    L = layer(tg, td, E, ff, d, seed=760 + E)
+    OL = oracle_layer(L)
+    dev = moe.upload_experts(L, device=cuda)
+    lg = _tie_logits(E, 761 + k)
+    nt = lg.shape[0]
+    ids_r, wts_r, _ = orc.route(lg, E, k)
+    x = torch.randn(nt, d, generator=gen(762))
+    _, h_r, _ = orc.moe_layer(OL, x.numpy(), ids_r, wts_r, want_hy=True)
+    xq = torch.from_numpy(orc.quantize(GType.Q8_K, x.numpy())).reshape(-1).to(cuda)
+    ids = torch.full((nt * k,), -5, dtype=torch.int32, device=cuda)
+    wts = torch.zeros(nt * k, device=cuda)
+    h = torch.full((nt * k, ff), float("nan"), device=cuda)
+    moe.moe_route_gate_up(dev, torch.from_numpy(lg).to(cuda), E, E, k, xq, ids, wts, None, h, nt)
+    torch.cuda.synchronize()
+    assert_bits_equal(ids.cpu().numpy().reshape(nt, k), ids_r, "ids")
+    assert_bits_equal(wts.cpu().numpy().reshape(nt, k), wts_r, "wts")
+    assert_bits_equal(h.cpu().numpy(), h_r, "h")
+    assert list(ids_r[2]) == list(range(k)), "all-equal logits select the k lowest ids"
+
+
 def test_decode_skips_non_local_experts(cuda):
     """Experts without a slot leave their h rows unwritten and drop out of the sum, as on the CPU."""
     tg = td = GType.Q4_K
