@@ -261,6 +261,17 @@ __device__ __forceinline__ void q8k_block16(const float (&xv)[16], uint8_t *out)
     ((int16_t *) (out + 260))[l] = (int16_t) s;
     if (l == 0) *(float *) out = d;
 }
+// q8k_block16 from memory: the row's lane l loads values 16 l .. 16 l + 15 of the block at x (16-byte aligned)
+__device__ __forceinline__ void q8k_block16_load(const float *x, uint8_t *out) {
+    const float4 *src = (const float4 *) (x + 16 * (lane_id() & 15));
+    float xv[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 v = src[i];
+        xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+    }
+    q8k_block16(xv, out);
+}
 __device__ __forceinline__ void q8k_block_wave(const float *x, uint8_t *out) {
     const float4 v = *(const float4 *) (x + 4 * lane_id());
     const float xv[4] = {v.x, v.y, v.z, v.w};

@@ -125,6 +125,7 @@ __global__ __launch_bounds__(256) void k_router_q8(const float *__restrict__ W, 
     // row's loads go out RB float4 at a time (one memory round trip per 256 RB values), then the fma chains.
     constexpr int RB = 8;
     const float *wr = W + (size_t) r * kdim;
+    const float bv = bias && lane < nt ? bias[(size_t) lane * bs + r] : 0.0f;   // token lane's bias, added after the butterfly
     float acc[DEC_ROUTE_NT];
 #pragma unroll
     for (int t = 0; t < DEC_ROUTE_NT; ++t) acc[t] = 0.0f;
@@ -161,7 +162,7 @@ __global__ __launch_bounds__(256) void k_router_q8(const float *__restrict__ W, 
     for (int t = 0; t < DEC_ROUTE_NT; ++t) {
         if (t < nt) {
             float v = wave_sum_xor(acc[t]);
-            if (bias) v = v + bias[(size_t) t * bs + r];
+            if (bias) v = v + readlane_f(bv, t);
             if (lane == 0) logits[(size_t) t * ls + r] = v;
         }
     }
@@ -543,11 +544,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
 int launch_router_q8(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
                      int vtype, void *xq, int nt, hipStream_t s) {
     if (nt == 0) return HY_OK;
-    if (nt > DEC_ROUTE_NT) {   // batched rows: the separate kernels
-        int rc = launch_q8(vtype, x, xs, kdim, nt, xq, s);
-        if (!rc) rc = launch_gemv_f32(W, rows, kdim, x, xs, logits, ls, nt, bias, bs, s);
-        return rc;
-    }
+    if (nt > DEC_ROUTE_NT) return launch_router_pre(W, rows, kdim, x, xs, bias, bs, logits, ls, vtype, xq, nt, s);   // batched rows
     const int qwaves = vtype == Q8_K ? nt * (kdim / 256) : nt * ((kdim / 32 + 1) / 2);
     const int blocks = (rows + qwaves + 3) / 4;
     if (vtype == Q8_K)

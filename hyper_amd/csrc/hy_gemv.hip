@@ -10,10 +10,12 @@ namespace hy {
 // the padded Q8_0 layout used in LDS: d at 0, qs at 4 (36 bytes: the qs words stay 4-byte aligned)
 constexpr int Q8_0_LDS = 36;
 
-__global__ __launch_bounds__(256) void k_q8k(const float *__restrict__ x, int xs, int n, uint8_t *__restrict__ q) {
-    const int t = blockIdx.y, b = blockIdx.x * 4 + (threadIdx.x >> 6), nb = n / 256;
-    if (b >= nb) return;
-    q8k_block_wave(x + (size_t) t * xs + 256 * b, q + ((size_t) t * nb + b) * Q8K_BYTES);
+// Q8_K: 16 blocks of 256 values per block of 256 threads, 16 lanes each (block u = token u / nb, block u % nb)
+__global__ __launch_bounds__(256) void k_q8k(const float *__restrict__ x, int xs, int n, int nt, uint8_t *__restrict__ q) {
+    const int nb = n / 256, u = blockIdx.x * 16 + (threadIdx.x >> 4);
+    if (u >= nt * nb) return;   // uniform over the 16-lane row
+    const int t = u / nb, b = u - t * nb;
+    q8k_block16_load(x + (size_t) t * xs + 256 * b, q + ((size_t) t * nb + b) * Q8K_BYTES);
 }
 __global__ __launch_bounds__(256) void k_q8_0(const float *__restrict__ x, int xs, int n, uint8_t *__restrict__ q) {
     const int t = blockIdx.y, b = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 2, nb = n / 32;
@@ -22,7 +24,7 @@ __global__ __launch_bounds__(256) void k_q8_0(const float *__restrict__ x, int x
 }
 int launch_q8(int vtype, const float *x, int xs, int n, int nt, void *q, hipStream_t s) {
     if (nt == 0) return HY_OK;
-    if (vtype == Q8_K) hipLaunchKernelGGL(k_q8k, dim3((n / 256 + 3) / 4, nt), dim3(256), 0, s, x, xs, n, (uint8_t *) q);
+    if (vtype == Q8_K) hipLaunchKernelGGL(k_q8k, dim3((nt * (n / 256) + 15) / 16), dim3(256), 0, s, x, xs, n, nt, (uint8_t *) q);
     else hipLaunchKernelGGL(k_q8_0, dim3((n / 32 + 7) / 8, nt), dim3(256), 0, s, x, xs, n, (uint8_t *) q);
     return check_launch("hy_q8_quantize");
 }

@@ -14,6 +14,8 @@ int launch_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, 
 int launch_route(const float *logits, int ls, int ne, int k, int *ids, float *wts, float *sg, int nt, hipStream_t s);
 int launch_order(const int *slot, const int *ids, int P, int ne, int *order, int *order_n, int *egrp, hipStream_t s);
 int launch_q8(int vtype, const float *x, int xs, int n, int nt, void *q, hipStream_t s);
+int launch_router_pre(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
+                      int vtype, void *xq, int nt, hipStream_t s);
 int launch_gate_up(const hy_moe_dev &m, const float *x, int xs, const int *ids, int k, float *h, int nt, hipStream_t s, const int *order,
                    const int *order_n);
 int launch_down(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, float *y, int nt, hipStream_t s,

@@ -6,58 +6,145 @@ namespace hy {
 // ---------------------------------------------------------------- router logits (A1)
 // y[t][r] = W[r] . x[t] (+ bias[t][r]): src/kernels4.cu:163-180 (gemv_f32).  Summation order of the contract:
 // lane L of a wave accumulates elements 256 i + 4 L + j (j = 0..3) with fmaf in index order, then the
-// 64 partial sums meet in an xor butterfly (1, 2, ..., 32).  A wave computes RW rows x TW tokens.
+// 64 partial sums meet in an xor butterfly (1, 2, ..., 32).  A wave computes RW rows x TW tokens; its loads for
+// step i + 1 are in flight while step i's fmas run (two register sets, a uniform trip count: past the row's end a
+// lane re-reads its first element and skips the fmas).
 template <int RW, int TW>
-__global__ __launch_bounds__(256) void k_gemv_f32(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
-                                                  float *__restrict__ y, int ys, int nt, const float *__restrict__ bias, int bs) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r0 = (blockIdx.x * 4 + wave) * RW, t0 = blockIdx.y * TW;
+__device__ __forceinline__ void gemv_tile(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+                                          float *__restrict__ y, int ys, int nt, const float *__restrict__ bias, int bs, int r0, int t0) {
+    const int lane = threadIdx.x & 63;
     if (r0 >= rows) return;
     float acc[RW][TW];
 #pragma unroll
     for (int a = 0; a < RW; ++a)
 #pragma unroll
         for (int b = 0; b < TW; ++b) acc[a][b] = 0.0f;
-    for (int e = 4 * lane; e < kdim; e += 256) {
-        float4 w[RW], xv[TW];
+    const float *wr[RW], *xr[TW];
 #pragma unroll
-        for (int a = 0; a < RW; ++a) w[a] = r0 + a < rows ? *(const float4 *) (W + (size_t) (r0 + a) * kdim + e) : make_float4(0, 0, 0, 0);
+    for (int a = 0; a < RW; ++a) wr[a] = W + (size_t) (r0 + a < rows ? r0 + a : r0) * kdim;
 #pragma unroll
-        for (int b = 0; b < TW; ++b) xv[b] = t0 + b < nt ? *(const float4 *) (x + (size_t) (t0 + b) * xs + e) : make_float4(0, 0, 0, 0);
+    for (int b = 0; b < TW; ++b) xr[b] = x + (size_t) (t0 + b < nt ? t0 + b : t0) * xs;
+    const int niter = (kdim + 255) / 256;
+    // the tile's biases, lane a TW + b holding (row r0 + a, token t0 + b): loaded now, added after the butterfly
+    static_assert(RW * TW <= 64, "one bias per lane");
+    float bv = 0.0f;
+    if (bias && lane < RW * TW && r0 + lane / TW < rows && t0 + lane % TW < nt) bv = bias[(size_t) (t0 + lane % TW) * bs + r0 + lane / TW];
+    float4 wa[RW], xa[TW], wb[RW], xb[TW];
+    auto ld = [&](int i, float4 (&wd)[RW], float4 (&xd)[TW]) {
+        const int e = 256 * i + 4 * lane < kdim ? 256 * i + 4 * lane : 4 * lane < kdim ? 4 * lane : 0;
+#pragma unroll
+        for (int a = 0; a < RW; ++a) wd[a] = *(const float4 *) (wr[a] + e);
+#pragma unroll
+        for (int b = 0; b < TW; ++b) xd[b] = *(const float4 *) (xr[b] + e);
+    };
+    auto fma_step = [&](int i, const float4 (&wd)[RW], const float4 (&xd)[TW]) {
+        if (i >= niter || 256 * i + 4 * lane >= kdim) return;
 #pragma unroll
         for (int a = 0; a < RW; ++a)
 #pragma unroll
             for (int b = 0; b < TW; ++b) {
                 float s = acc[a][b];
-                s = __builtin_fmaf(w[a].x, xv[b].x, s);
-                s = __builtin_fmaf(w[a].y, xv[b].y, s);
-                s = __builtin_fmaf(w[a].z, xv[b].z, s);
-                s = __builtin_fmaf(w[a].w, xv[b].w, s);
+                s = __builtin_fmaf(wd[a].x, xd[b].x, s);
+                s = __builtin_fmaf(wd[a].y, xd[b].y, s);
+                s = __builtin_fmaf(wd[a].z, xd[b].z, s);
+                s = __builtin_fmaf(wd[a].w, xd[b].w, s);
                 acc[a][b] = s;
             }
+    };
+    ld(0, wa, xa);
+    for (int i = 0; i < niter; i += 2) {
+        ld(i + 1, wb, xb);
+        fma_step(i, wa, xa);
+        ld(i + 2, wa, xa);
+        fma_step(i + 1, wb, xb);
     }
 #pragma unroll
     for (int a = 0; a < RW; ++a)
 #pragma unroll
         for (int b = 0; b < TW; ++b) {
             float s = wave_sum_xor(acc[a][b]);
-            if (lane == 0 && r0 + a < rows && t0 + b < nt) {
-                if (bias) s = s + bias[(size_t) (t0 + b) * bs + r0 + a];
-                y[(size_t) (t0 + b) * ys + r0 + a] = s;
-            }
+            if (bias) s = s + readlane_f(bv, a * TW + b);
+            if (lane == 0 && r0 + a < rows && t0 + b < nt) y[(size_t) (t0 + b) * ys + r0 + a] = s;
         }
+}
+
+// Block bid of a gx x gy grid of (row group, token group) tiles.  Workgroups go to the 8 XCDs round robin (bid % 8)
+// and each XCD has its own L2, so when gy % 8 == 0 every token group's gx row groups run on one XCD: each XCD then
+// streams 1/8 of the tokens (and all of W) instead of all of them.
+__device__ __forceinline__ void gemv_tile_of(int bid, int gx, int gy, int &bx, int &by) {
+    if (gy % 8 == 0) {
+        const int slot = bid >> 3;
+        bx = slot % gx;
+        by = (bid & 7) + 8 * (slot / gx);
+    } else {
+        bx = bid % gx;
+        by = bid / gx;
+    }
+}
+
+template <int RW, int TW>
+__global__ __launch_bounds__(256) void k_gemv_f32(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+                                                  float *__restrict__ y, int ys, int nt, const float *__restrict__ bias, int bs, int gx,
+                                                  int gy) {
+    int bx, by;
+    gemv_tile_of(blockIdx.x, gx, gy, bx, by);
+    gemv_tile<RW, TW>(W, rows, kdim, x, xs, y, ys, nt, bias, bs, (bx * 4 + (threadIdx.x >> 6)) * RW, by * TW);
 }
 
 int launch_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bs,
                     hipStream_t s) {
     if (nt <= 4) {
-        dim3 g((rows + 3) / 4, nt);
-        hipLaunchKernelGGL((k_gemv_f32<1, 1>), g, dim3(256), 0, s, W, rows, kdim, x, xs, y, ys, nt, bias, bs);
+        const int gx = (rows + 3) / 4, gy = nt;
+        hipLaunchKernelGGL((k_gemv_f32<1, 1>), dim3(gx * gy), dim3(256), 0, s, W, rows, kdim, x, xs, y, ys, nt, bias, bs, gx, gy);
     } else {
-        dim3 g((rows + 15) / 16, (nt + 7) / 8);
-        hipLaunchKernelGGL((k_gemv_f32<4, 8>), g, dim3(256), 0, s, W, rows, kdim, x, xs, y, ys, nt, bias, bs);
+        const int gx = (rows + 15) / 16, gy = (nt + 7) / 8;
+        hipLaunchKernelGGL((k_gemv_f32<4, 8>), dim3(gx * gy), dim3(256), 0, s, W, rows, kdim, x, xs, y, ys, nt, bias, bs, gx, gy);
     }
     return check_launch("hy_gemv_f32");
+}
+
+// Router logits of many tokens and the Q8 rows of x in one launch: blocks [0, gemv_blocks) are k_gemv_f32<4, 8>'s
+// grid (gx blocks of 16 rows per 8 tokens), the rest quantize x -- Q8_K: 16 blocks of 256 values per block,
+// 16 lanes each; Q8_0: 4 pairs of 32-value blocks per block, a wave each.
+template <int VT>
+__global__ __launch_bounds__(256) void k_router_pre(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+                                                    const float *__restrict__ bias, int bs, float *__restrict__ y, int ys, int nt,
+                                                    uint8_t *__restrict__ xq, int gx, int gemv_blocks) {
+    const int bid = blockIdx.x;
+    if (bid < gemv_blocks) {
+        int bx, by;
+        gemv_tile_of(bid, gx, gemv_blocks / gx, bx, by);
+        gemv_tile<4, 8>(W, rows, kdim, x, xs, y, ys, nt, bias, bs, (bx * 4 + (threadIdx.x >> 6)) * 4, by * 8);
+        return;
+    }
+    const int qb = bid - gemv_blocks;
+    if constexpr (VT == Q8_K) {
+        const int nb = kdim / 256, u = qb * 16 + (threadIdx.x >> 4);
+        if (u >= nt * nb) return;   // uniform over the 16-lane row
+        const int t = u / nb, b = u - t * nb;
+        q8k_block16_load(x + (size_t) t * xs + 256 * b, xq + ((size_t) t * nb + b) * Q8K_BYTES);
+    } else {
+        const int nb = kdim / 32, npair = (nb + 1) / 2, u = qb * 4 + (threadIdx.x >> 6);
+        if (u >= nt * npair) return;   // wave-uniform
+        const int t = u / npair, b = 2 * (u - t * npair);
+        q8_0_pair_wave(x + (size_t) t * xs + 32 * b, xq + ((size_t) t * nb + b) * Q8_0_BYTES, b + 1 < nb, Q8_0_BYTES, 2);
+    }
+}
+
+int launch_router_pre(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
+                      int vtype, void *xq, int nt, hipStream_t s) {
+    if (nt == 0) return HY_OK;
+    const int gx = (rows + 15) / 16, gemv_blocks = gx * ((nt + 7) / 8);
+    if (vtype == Q8_K) {
+        const int qblocks = (nt * (kdim / 256) + 15) / 16;
+        hipLaunchKernelGGL(k_router_pre<Q8_K>, dim3(gemv_blocks + qblocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, nt,
+                           (uint8_t *) xq, gx, gemv_blocks);
+    } else {
+        const int qblocks = (nt * ((kdim / 32 + 1) / 2) + 3) / 4;
+        hipLaunchKernelGGL(k_router_pre<Q8_0>, dim3(gemv_blocks + qblocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, nt,
+                           (uint8_t *) xq, gx, gemv_blocks);
+    }
+    return check_launch("hy_moe_router_q8");
 }
 
 // ---------------------------------------------------------------- routing (A2)

@@ -260,9 +260,10 @@ class MoeLayerRunner:
     def prefill(self, x: torch.Tensor, bias=None, stream=None, shared_ready=False) -> torch.Tensor:
         nt, k = x.shape[0], self.k
         P = nt * k
-        self.route(x, nt, bias, stream)
+        moe_router_q8(self.W_r, self.W_r.shape[0], self.d, x, x.stride(0), self.logits, self.ls, self.vg, self.xq, nt, stream,
+                      bias=bias, bias_stride=0 if bias is None else bias.stride(0))
+        moe_route(self.logits, self.ls, self.E, self.k, self.ids, self.wts, self.sg, nt, stream)
         moe_order(self.dev, self.ids, P, self.E, self.order, self.order_n, stream, self.egrp)
-        q8_quantize(self.vg, x, x.stride(0), self.d, nt, self.xq, stream)
         max_active = min(self.E, P)
         moe_gemm_gate_up(self.dev, self.xq, k, P, self.order, self.order_n, self.egrp, max_active, self.h, stream)
         q8_quantize(self.vd, self.h, self.ff, self.ff, P, self.hq, stream)
