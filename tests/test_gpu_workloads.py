@@ -1,0 +1,58 @@
+"""Every configured workload at its real shapes (expert count, d_model, ff, k, rows, types, shared expert, Zipf routing
+and log-normal token norms) through MoeLayerRunner on the GPU: decode / verify rows through the three-launch decode,
+longer batches through the prefill path.  The layers are generated on the device at full size; the oracle checks a
+sample of the tokens on a sub-layer holding only the experts they route to (ids remapped in ascending order, so the
+combine order is unchanged).  Logits, routing and outputs are compared bit for bit; the 2e-3 relative-L2 bound of the
+north star is asserted as well."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from hyper_amd import moe
+from hyper_amd.formats import WORKLOADS, activations, random_layer, zipf_logit_bias
+from tests.helpers import assert_bits_equal, rel_l2
+
+pytestmark = pytest.mark.gpu
+SAMPLE = 24   # tokens checked against the oracle in batches longer than that
+
+
+def _sub_layer(L, used):
+    """oracle layer of the experts `used` (ascending) of the device layer L"""
+    idx = torch.as_tensor(used, dtype=torch.long, device=L.gate.device)
+    return orc.Layer(L.tg, L.td, L.gate[idx].cpu().numpy(), L.up[idx].cpu().numpy(), L.down[idx].cpu().numpy(), L.ff, L.n, L.clamp)
+
+
+@pytest.mark.parametrize("name", list(WORKLOADS))
+def test_workload_full_size(cuda, name):
+    w = WORKLOADS[name]
+    seed = 900 + sum(map(ord, name))
+    L = random_layer(w.tg, w.td, w.E, w.ff, w.d, seed=seed, device=cuda, d_range=w.d_range, d_range_down=w.d_range_down)
+    S = random_layer(w.shared[0], w.shared[1], 1, w.ff, w.d, seed=seed + 1, device=cuda, d_range=w.d_range) if w.shared else None
+    g = torch.Generator(device=cuda)
+    g.manual_seed(seed + 2)
+    W_r = torch.randn(w.E, w.d, generator=g, device=cuda) * 0.02
+    x = activations(w.rows, w.d, g, cuda, lognormal=w.norm_lognormal)
+    bias = zipf_logit_bias(w.rows, w.E, w.zipf, g, cuda) if w.zipf else None
+    dev = moe.MoeDev(L, torch.arange(w.E, dtype=torch.int32, device=cuda))
+    sdev = moe.MoeDev(S, torch.zeros(1, dtype=torch.int32, device=cuda)) if S is not None else None
+    r = moe.MoeLayerRunner(dev, W_r, w.k, max_rows=w.rows, shared=sdev)
+    out = (r.decode(x, bias=bias) if w.rows <= 8 else r.prefill(x, bias=bias)).clone()
+    torch.cuda.synchronize()
+
+    rng = np.random.default_rng(seed)
+    tok = np.arange(w.rows) if w.rows <= SAMPLE else np.sort(rng.choice(w.rows, SAMPLE, replace=False))
+    xs = x.cpu().numpy()[tok]
+    logits = orc.gemv_f32(W_r.cpu().numpy(), xs)
+    if bias is not None:
+        logits = (logits + bias.cpu().numpy()[tok]).astype(np.float32)
+    assert_bits_equal(r.logits.cpu().numpy()[tok], logits, "logits")
+    ids, wts, _ = orc.route(logits, w.E, w.k)
+    assert_bits_equal(r.ids.cpu().numpy().reshape(-1, w.k)[tok], ids, "ids")
+    assert_bits_equal(r.wts.cpu().numpy().reshape(-1, w.k)[tok], wts, "wts")
+    used = np.unique(ids)
+    ids_sub = np.searchsorted(used, ids).astype(np.int32)
+    ref = orc.moe_layer(_sub_layer(L, used), xs, ids_sub, wts, shared=orc.Layer.from_expert_layer(S) if S is not None else None)
+    got = out.cpu().numpy()[tok]
+    assert_bits_equal(got, ref, "out")
+    assert rel_l2(got, ref) <= 2e-3
