@@ -12,6 +12,11 @@ HIP graph (captured once, checked against an eager run first).
 Secondary (`decode` object): 1-token decode of the same layer shape in Q4_K/Q4_K, three launches: router GEMV +
 Q8 of x -> routing + gate/up GEMV -> down GEMV + combine, cycling 4 layer copies (1.36 GB) and fresh tokens.
 
+Secondary (`workloads` object): the other configured workloads at their full shapes -- IQ4_NL / IQ4_XS (d_model
+4096, 288 experts) at 1 and 4 rows, IQ2_XS (d_model 7168, 384 experts, top-6) with a shared Q4_K expert at 1 and 8
+rows, and one 2048-token chunk of Q5_K/Q6_K (512 experts, top-10, shared expert) -- µs per step and the HBM rate of
+the expert bytes each step touches.
+
 `roofline` reports the dominant kernel of the headline step against HBM bandwidth (8 TB/s): algorithmic bytes
 per launch / its average launch duration, measured on its own stream with HIP events over graph replays of
 that kernel.  `cpu_baseline` is the CPU oracle (this repository's restatement of the reference's CPU expert
@@ -178,6 +183,54 @@ def decode_bench(args, dev, stream):
                         "down_reduce": {"us": ms_dn * 1e3, "gbs": k * L0.down_bytes / (ms_dn / 1e3) / 1e9}}}
 
 
+def workloads_bench(args, dev, stream):
+    """The other configured workloads at their full shapes (C3-C5: IQ4_NL / IQ4_XS decode and 4-row verify, IQ2_XS with
+    a shared Q4_K expert at 1 and 8 rows, the 2048-token Q5_K/Q6_K chunk): µs per step from graph replays over
+    `workload_copies` weight copies and fresh inputs.  Bytes per step: the distinct experts its rows route to, the
+    shared expert, the router weights and the activations in and out."""
+    res = {}
+    for name, w in WORKLOADS.items():
+        if name in ("q4k_decode", "q4k_q6k_prefill512"):
+            continue
+        copies, n_in, nsteps = args.workload_copies, 4, 8
+        g = torch.Generator(device=dev)
+        g.manual_seed(4321)
+        layers = [random_layer(w.tg, w.td, w.E, w.ff, w.d, seed=500 + c, device=dev, d_range=w.d_range, d_range_down=w.d_range_down)
+                  for c in range(copies)]
+        S = random_layer(w.shared[0], w.shared[1], 1, w.ff, w.d, seed=550, device=dev, d_range=w.d_range) if w.shared else None
+        sdev = moe.MoeDev(S, torch.zeros(1, dtype=torch.int32, device=dev)) if S is not None else None
+        runners = [moe.MoeLayerRunner(moe.MoeDev(L, torch.arange(w.E, dtype=torch.int32, device=dev)),
+                                      torch.randn(w.E, w.d, generator=g, device=dev) * 0.02, w.k, w.rows, shared=sdev) for L in layers]
+        xs = [activations(w.rows, w.d, g, dev, lognormal=w.norm_lognormal) for _ in range(n_in)]
+        bs = [zipf_logit_bias(w.rows, w.E, w.zipf, g, dev) if w.zipf else None for _ in range(n_in)]
+        decode = w.rows <= 8
+
+        def step(r, x, b):
+            return r.decode(x, bias=b) if decode else r.prefill(x, bias=b)
+
+        touched = []
+        for i in range(n_in):
+            step(runners[0], xs[i], bs[i])
+            torch.cuda.synchronize()
+            touched.append(int(torch.unique(runners[0].ids[: w.rows * w.k]).numel()))
+        fns = [lambda c=i % copies, i=i: step(runners[c], xs[i % n_in], bs[i % n_in]) for i in range(nsteps)]
+        with torch.cuda.stream(stream):
+            for f in fns:
+                f()
+            torch.cuda.synchronize()
+            ms = graph_time(fns, max(1, args.decode_reps), stream) / nsteps
+        L0 = layers[0]
+        step_bytes = float(np.mean(touched)) * L0.expert_bytes() + (S.expert_bytes() if S is not None else 0) + w.E * w.d * 4 + 2 * w.rows * w.d * 4
+        gbs = step_bytes / (ms / 1e3) / 1e9
+        res[name] = {"rows": w.rows, "us_per_step": round(ms * 1e3, 2), "tok_s": round(w.rows / (ms / 1e3), 1),
+                     "experts_touched": float(np.mean(touched)), "alg_bytes": step_bytes, "hbm_gbs": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "path": "decode" if decode else "prefill"}
+        log(f"workload {name}: {ms * 1e3:.2f} us/step, {gbs:.0f} GB/s")
+        del runners, layers, sdev, S
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(layer, W_r, xs, biases, budget_s: float):
     """The CPU oracle on the headline step: the first S tokens of one step, S doubling up to the full 512, then
     whole steps over the next inputs until about budget_s seconds of oracle work have been timed."""
@@ -246,6 +299,8 @@ def main():
     ap.add_argument("--decode-copies", type=int, default=4)
     ap.add_argument("--decode-reps", type=int, default=8)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--workload-copies", type=int, default=2, help="weight copies per workload in the `workloads` object")
+    ap.add_argument("--no-workloads", action="store_true", help="skip the `workloads` object (the other configured workloads)")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-oracle work for cpu_baseline (0: skip)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain copy kernel over MIB MiB (counter calibration under rocprofv3 --pmc)")
@@ -265,6 +320,10 @@ def main():
         log("decode: building layers")
         dec = decode_bench(args, dev, stream)
         log(f"decode: {dec['us_per_token']:.2f} us/token")
+    wl = None
+    if not args.no_workloads:
+        log("workloads: the other configured shapes")
+        wl = workloads_bench(args, dev, stream)
     cpu = None
     if args.cpu_budget > 0:
         log("cpu baseline: oracle on a sample of the prefill step")
@@ -284,6 +343,7 @@ def main():
                  "int8_mfma_frac": round(pre["step_int8_tops"] / INT8_PEAK_TOPS, 4),
                  "kernels": pre["kernels"]},
         "decode": dec,
+        "workloads": wl,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

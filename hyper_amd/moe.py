@@ -203,6 +203,7 @@ class MoeLayerRunner:
             self.sh_order = torch.arange(T, **i32)
             self.sh_order_n = torch.tensor([0, 1], **i32)
             self.sh_egrp = torch.tensor([0, 0, 0], **i32)
+            self._sh_nt = 0
             self.sh_xq = torch.empty(T * q8_row_bytes(vec_dot_type(S.tg), self.d), dtype=torch.uint8, device=device)
             self.sh_hq = torch.empty(T * q8_row_bytes(vec_dot_type(S.td), S.ff), dtype=torch.uint8, device=device)
 
@@ -224,9 +225,12 @@ class MoeLayerRunner:
 
     def _shared_prefill(self, x, nt, stream):
         S = self.shared
-        # one active "expert" holding every token: (0, 0, nt)
-        self.sh_order_n[0] = nt
-        self.sh_egrp[2] = nt
+        # one active "expert" holding every token: (0, 0, nt); rewritten (a device fill, which a graph may record) only
+        # when nt changes
+        if nt != self._sh_nt:
+            self.sh_order_n[0:1].fill_(nt)
+            self.sh_egrp[2:3].fill_(nt)
+            self._sh_nt = nt
         q8_quantize(vec_dot_type(S.tg), x, x.stride(0), self.d, nt, self.sh_xq, stream)
         moe_gemm_gate_up(S, self.sh_xq, 1, nt, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_h, stream)
         q8_quantize(vec_dot_type(S.td), self.sh_h, S.layer.ff, S.layer.ff, nt, self.sh_hq, stream)
