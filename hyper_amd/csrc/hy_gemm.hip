@@ -378,6 +378,8 @@ __device__ __forceinline__ void step_q4k(const uint8_t *wl, int q, const int8_t 
     }
 }
 
+__host__ __device__ constexpr int xcd_gcd8(int n) { return (n & 7) == 0 ? 8 : (n & 3) == 0 ? 4 : (n & 1) == 0 ? 2 : 1; }
+
 template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
 template <int T, bool GU, int W, int B>
@@ -430,7 +432,12 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
     for (int w = 0; w < C::WAVES; ++w) tot += s_scan[1024 + w];
     const int n4 = (int) (tot & 0xffff), n3 = (int) ((tot >> 16) & 0xffff), n2 = (int) ((tot >> 32) & 0xffff), n1 = (int) (tot >> 48);
     const int total = n4 + n3 + n2 + n1;
-    const int y0 = blockIdx.y, ys = gridDim.y;
+    // Block (x, y) runs on XCD (x + gridDim.x y) % 8, and each XCD has its own L2.  Consecutive item positions are
+    // mostly items of one expert (the same weights), so they go to logical slots l, l + 1, ... placed P = 8 /
+    // gcd(gridDim.x, 8) physical slots apart: the same XCD for every row block, where the second reader of a weight
+    // tile finds it in L2.  (The host makes gridDim.y a multiple of P when it has P slots or more; else P = 1.)
+    const int ys = gridDim.y, P0 = 8 / xcd_gcd8((int) gridDim.x), P = ys % P0 == 0 ? P0 : 1;
+    const int y0 = ((int) blockIdx.y % P) * (ys / P) + (int) blockIdx.y / P;   // this block's logical slot
     const int rounds = total / ys, rem_items = total - rounds * ys;
     const int my_items = rounds + (((rounds & 1) ? ys - 1 - y0 : y0) < rem_items ? 1 : 0);
     if (my_items == 0) return;   // uniform over the block
@@ -826,7 +833,9 @@ static int item_slots(int row_tiles, int n_pairs, int max_active, int per_cu) {
     static int cus = 0;
     if (!cus) { int dev = 0; hipDeviceProp_t pr; if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&pr, dev) == hipSuccess) cus = pr.multiProcessorCount; if (cus <= 0) cus = 256; }
     const int want = cus * per_cu / row_tiles;   // every block resident at once
-    return std::max(1, std::min(max_items(n_pairs, max_active), want));
+    const int n = std::max(1, std::min(max_items(n_pairs, max_active), want));
+    const int P = 8 / xcd_gcd8(row_tiles);       // k_gemm places consecutive items P slots apart: a multiple of P
+    return n >= P ? n / P * P : n;
 }
 
 int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs, const int *order, const int *order_n, const int *egrp,
