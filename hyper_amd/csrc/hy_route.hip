@@ -1,5 +1,6 @@
 // Router GEMV, softmax/top-k routing and token->expert bucketing.
 #include "hy_internal.h"
+#include "hy_routing.cuh"
 
 namespace hy {
 
@@ -148,67 +149,33 @@ int launch_router_pre(const float *W, int rows, int kdim, const float *x, int xs
 }
 
 // ---------------------------------------------------------------- routing (A2)
-__device__ __forceinline__ bool rt_better(float a, int ia, float b, int ib) { return (a > b) | ((a == b) & (ia < ib)); }   // no short circuit: no branches
-
-// a wave per token, expert e in lane e % 64 slot e / 64 (V slots): max, exp, the contract's sum (lane L adds
-// its experts in slot order, then the xor butterfly), p = v / s; each lane sorts its V candidates
-// (descending, ties to the lower index), then k rounds of wave argmax; weights p_j / sum of the selected
-// (summed in selection order); sg = sigmoid(logit ne).  src/kernels4.cu:297-344.
+// A token per block: up to 128 experts by eight waves (route_rank8), more by one wave (route_wave); both give the
+// bits of src/kernels4.cu:297-344's contract (hy_routing.cuh).
+template <int V>
+__global__ __launch_bounds__(512) void k_route8(const float *__restrict__ logits, int ls, int ne, int k, int *__restrict__ ids,
+                                                float *__restrict__ wts, float *__restrict__ sg) {
+    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int er;
+    float pr, tot, lsg;
+    route_rank8<V>(logits + (size_t) t * ls, ne, k, sg != nullptr, er, pr, tot, lsg, [] {});
+    if (wave == 0) {
+        if (lane < k) { ids[(size_t) t * k + lane] = er; wts[(size_t) t * k + lane] = pr / tot; }
+        if (lane == 0 && sg) sg[t] = 1.0f / (1.0f + hy_expf(-lsg));
+    }
+}
 template <int V>
 __global__ __launch_bounds__(64) void k_route(const float *__restrict__ logits, int ls, int ne, int k, int *__restrict__ ids,
                                               float *__restrict__ wts, float *__restrict__ sg) {
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const float *l = logits + (size_t) t * ls;
-    float v[V];
-    int vi[V];
-    float mx = -__builtin_huge_valf();
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-        const int e = lane + 64 * i;
-        v[i] = e < ne ? l[e] : -__builtin_huge_valf();
-        vi[i] = e < ne ? e : 0x7fffffff;
-        mx = fmaxf(mx, v[i]);
-    }
-    mx = wave_max(mx);
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < V; ++i)
-        if (vi[i] < ne) { v[i] = hy_expf(v[i] - mx); acc = acc + v[i]; }
-    const float s = wave_sum_xor(acc);
-#pragma unroll
-    for (int i = 0; i < V; ++i) v[i] = vi[i] < ne ? v[i] / s : -1.0f;
-#pragma unroll
-    for (int i = 1; i < V; ++i)
-#pragma unroll
-        for (int j = i; j > 0; --j)
-            if (rt_better(v[j], vi[j], v[j - 1], vi[j - 1])) {
-                const float tv = v[j]; v[j] = v[j - 1]; v[j - 1] = tv;
-                const int ti = vi[j]; vi[j] = vi[j - 1]; vi[j - 1] = ti;
-            }
-    float selw = 0.0f, tot = 0.0f;
-    int seli = 0;
-    for (int j = 0; j < k; ++j) {
-        float bv = v[0];
-        int bi = vi[0];
-        wave_best(bv, bi, rt_better);
-        if (lane == j) { selw = bv; seli = bi; }
-        tot = tot + bv;
-        if (vi[0] == bi) {
-#pragma unroll
-            for (int i = 0; i < V - 1; ++i) { v[i] = v[i + 1]; vi[i] = vi[i + 1]; }
-            v[V - 1] = -1.0f; vi[V - 1] = 0x7fffffff;
-        }
-    }
-    if (lane < k) { ids[(size_t) t * k + lane] = seli; wts[(size_t) t * k + lane] = selw / tot; }
-    if (lane == 0 && sg) sg[t] = 1.0f / (1.0f + hy_expf(-l[ne]));
+    const int t = blockIdx.x;
+    route_wave<V>(logits + (size_t) t * ls, ne, k, ids + (size_t) t * k, wts + (size_t) t * k, sg ? sg + t : nullptr);
 }
 
 int launch_route(const float *logits, int ls, int ne, int k, int *ids, float *wts, float *sg, int nt, hipStream_t s) {
     if (nt == 0) return HY_OK;
     const int V = (ne + 63) / 64;
     dim3 g(nt);
-    if (V <= 1) hipLaunchKernelGGL((k_route<1>), g, dim3(64), 0, s, logits, ls, ne, k, ids, wts, sg);
-    else if (V <= 2) hipLaunchKernelGGL((k_route<2>), g, dim3(64), 0, s, logits, ls, ne, k, ids, wts, sg);
+    if (V <= 1) hipLaunchKernelGGL((k_route8<1>), g, dim3(512), 0, s, logits, ls, ne, k, ids, wts, sg);
+    else if (V <= 2) hipLaunchKernelGGL((k_route8<2>), g, dim3(512), 0, s, logits, ls, ne, k, ids, wts, sg);
     else if (V <= 4) hipLaunchKernelGGL((k_route<4>), g, dim3(64), 0, s, logits, ls, ne, k, ids, wts, sg);
     else if (V <= 8) hipLaunchKernelGGL((k_route<8>), g, dim3(64), 0, s, logits, ls, ne, k, ids, wts, sg);
     else hipLaunchKernelGGL((k_route<16>), g, dim3(64), 0, s, logits, ls, ne, k, ids, wts, sg);
@@ -223,19 +190,37 @@ int launch_route(const float *logits, int ls, int ne, int k, int *ids, float *wt
 // expert from ten ballots (one per bit of the id, ids < 1024), its rank is the number of those below it, and the
 // highest of them advances the wave's running counter for the expert.
 constexpr int ORD_WAVES = 16;
+constexpr int ORD_B = 8;   // 64-pair rows of a wave's segment whose ids are loaded together
 __global__ __launch_bounds__(64 * ORD_WAVES) void k_order(const int *__restrict__ slot, const int *__restrict__ ids, int P, int ne,
                                                           int *__restrict__ order, int *__restrict__ order_n, int *__restrict__ egrp) {
     __shared__ int c[ORD_WAVES * 1024];
     __shared__ int tot[1024];
+    __shared__ int s_slot[1024];
     __shared__ int wsum[2][ORD_WAVES];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int seg = ((P + ORD_WAVES - 1) / ORD_WAVES + 63) / 64 * 64;
     const int p0 = w * seg, p1 = min(P, p0 + seg);
+    // the ids of a batch (ORD_B rows of 64 pairs) in flight together; the slot table goes to LDS alongside the first
+    int idv[ORD_B];
+    auto load_ids = [&](int q0) {
+#pragma unroll
+        for (int r = 0; r < ORD_B; ++r) {
+            const int p = q0 + 64 * r + lane;
+            idv[r] = p < p1 ? ids[p] : -1;
+        }
+    };
+    auto valid_e = [&](int e) { return e >= 0 && e < ne && s_slot[e] >= 0; };
+    const bool one_batch = p1 - p0 <= 64 * ORD_B;   // wave-uniform: the ids stay in registers for the second pass
+    load_ids(p0);
+    const int sl = tid < ne ? slot[tid] : -1;
     for (int i = tid; i < ORD_WAVES * ne; i += blockDim.x) c[i] = 0;
+    if (tid < ne) s_slot[tid] = sl;
     __syncthreads();
-    for (int p = p0 + lane; p < p1; p += 64) {
-        const int e = ids[p];
-        if (e >= 0 && e < ne && slot[e] >= 0) atomicAdd(&c[w * ne + e], 1);
+    for (int q0 = p0; q0 < p1; q0 += 64 * ORD_B) {
+        if (q0 != p0) load_ids(q0);
+#pragma unroll
+        for (int r = 0; r < ORD_B; ++r)
+            if (valid_e(idv[r])) atomicAdd(&c[w * ne + idv[r]], 1);
     }
     __syncthreads();
     // per expert e (thread e): the waves' counts become offsets within the expert; then exclusive scans over the
@@ -272,23 +257,28 @@ __global__ __launch_bounds__(64 * ORD_WAVES) void k_order(const int *__restrict_
     __syncthreads();
     int *cw = c + w * ne;
     const unsigned long long below = (1ull << lane) - 1;
-    for (int q0 = p0; q0 < p1; q0 += 64) {
-        const int p = q0 + lane;
-        const int e = p < p1 ? ids[p] : -1;
-        const bool valid = e >= 0 && e < ne && slot[e] >= 0;
-        unsigned long long same = __ballot(valid);
+    for (int q0 = p0; q0 < p1; q0 += 64 * ORD_B) {
+        if (!one_batch) load_ids(q0);
 #pragma unroll
-        for (int bit = 0; bit < 10; ++bit) {
-            const unsigned long long ones = __ballot((e >> bit) & 1);
-            same &= ((e >> bit) & 1) ? ones : ~ones;
+        for (int r = 0; r < ORD_B; ++r) {
+            if (q0 + 64 * r >= p1) break;   // wave-uniform
+            const int p = q0 + 64 * r + lane;
+            const int e = idv[r];
+            const bool valid = valid_e(e);
+            unsigned long long same = __ballot(valid);
+#pragma unroll
+            for (int bit = 0; bit < 10; ++bit) {
+                const unsigned long long ones = __ballot((e >> bit) & 1);
+                same &= ((e >> bit) & 1) ? ones : ~ones;
+            }
+            if (valid) {
+                const int rank = __popcll(same & below);
+                const int base = cw[e];
+                order[base + rank] = p;
+                if (rank == __popcll(same) - 1) cw[e] = base + rank + 1;   // the group's highest lane
+            }
+            __builtin_amdgcn_wave_barrier();
         }
-        if (valid) {
-            const int rank = __popcll(same & below);
-            const int base = cw[e];
-            order[base + rank] = p;
-            if (rank == __popcll(same) - 1) cw[e] = base + rank + 1;   // the group's highest lane
-        }
-        __builtin_amdgcn_wave_barrier();
     }
 }
 
