@@ -209,7 +209,7 @@ __device__ __forceinline__ long a_frag(const int8_t *As, int tile, int rr, int c
 
 template <int T, bool SWZ = false>
 __device__ __forceinline__ void chunk_ints(const Raw<T> &w, int c, int q, const uint2 *grid, const int8_t *As, int rr, int ntile,
-                                           int (&si)[GM_TILES][4], v4i (&sm)[GM_TILES]) {
+                                           int (&si)[GM_TILES][4], v4i (&sm)[GM_TILES], const long (*af)[8] = nullptr) {
     const v4i z = {0, 0, 0, 0};
     uint32_t b0, b1;
     int s0, s1, mn;
@@ -218,7 +218,7 @@ __device__ __forceinline__ void chunk_ints(const Raw<T> &w, int c, int q, const 
 #pragma unroll
     for (int tile = 0; tile < GM_TILES; ++tile) {
         if (tile >= ntile) break;
-        const long a = a_frag<SWZ>(As, tile, rr, c, q);
+        const long a = af ? af[tile][c] : a_frag<SWZ>(As, tile, rr, c, q);   // af: read up front by the caller
         if constexpr (Raw<T>::g16) {
             const bool lo = q < 2;
             const v4i d0 = mfma16(a, mk_long(lo ? b0 : 0u, lo ? b1 : 0u), z);
@@ -550,8 +550,22 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
                 for (int v = 0; v < 4; ++v) si[i][v] = 0;
                 sm[i] = v4i{0, 0, 0, 0};
             }
+            if constexpr (B == 1) {
+                // the step's activation fragments (tile, chunk) read from LDS up front: one LDS round trip a step
+                // instead of one per chunk and tile (the register budget of one block per CU has room for them)
+                long af[GM_TILES][8];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) chunk_ints<T, true>(wr, c, q, grid, as, rr, ntile, si, sm);
+                for (int tile = 0; tile < GM_TILES; ++tile) {
+                    if (tile >= ntile) break;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) af[tile][c] = a_frag<true>(as, tile, rr, c, q);
+                }
+#pragma unroll
+                for (int c = 0; c < 8; ++c) chunk_ints<T, true>(wr, c, q, grid, as, rr, ntile, si, sm, af);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 8; ++c) chunk_ints<T, true>(wr, c, q, grid, as, rr, ntile, si, sm);
+            }
 #pragma unroll
             for (int tile = 0; tile < GM_TILES; ++tile) {
                 if (tile >= ntile) break;
