@@ -494,7 +494,7 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
         auto issue = [&]() {
             const int it = iss_it, b = iss_b;
             if (b == 0) {
-                const int ntok = s_item[it][1];
+                const int ntok = __builtin_amdgcn_readfirstlane(s_item[it][1]);   // uniform: a scalar register
                 iss_ntok = ntok;
                 const int p0 = s_pair[it][0];
 #pragma unroll
