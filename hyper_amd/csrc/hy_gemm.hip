@@ -21,6 +21,7 @@
 #include "hy_blocks.cuh"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace hy {
 
@@ -207,7 +208,8 @@ __device__ __forceinline__ long a_frag(const int8_t *As, int tile, int rr, int c
     else return *(const long *) (As + (tile * 16 + rr) * GM_LD + 32 * c + 8 * q);
 }
 
-template <int T, bool SWZ = false>
+// (NT: a compile-time bound on the tiles; ntile, the run-time count, is NT itself where the caller specializes)
+template <int T, bool SWZ = false, int NT = GM_TILES>
 __device__ __forceinline__ void chunk_ints(const Raw<T> &w, int c, int q, const uint2 *grid, const int8_t *As, int rr, int ntile,
                                            int (&si)[GM_TILES][4], v4i (&sm)[GM_TILES], const long (*af)[8] = nullptr) {
     const v4i z = {0, 0, 0, 0};
@@ -216,7 +218,7 @@ __device__ __forceinline__ void chunk_ints(const Raw<T> &w, int c, int q, const 
     w.chunk(c, q, grid, b0, b1, s0, s1, mn);
     const uint32_t mb = __builtin_amdgcn_perm(0u, (uint32_t) mn, 0u);   // the min in all four bytes (selector 0-3: bytes of the 2nd operand)
 #pragma unroll
-    for (int tile = 0; tile < GM_TILES; ++tile) {
+    for (int tile = 0; tile < NT; ++tile) {
         if (tile >= ntile) break;
         const long a = af ? af[tile][c] : a_frag<SWZ>(As, tile, rr, c, q);   // af: read up front by the caller
         if constexpr (Raw<T>::g16) {
@@ -330,52 +332,139 @@ __device__ __forceinline__ int mul_bytes(uint32_t q, uint32_t f) {
     return (int) __builtin_bit_cast(uint32_t, r);
 }
 
-// Q4_K step on the 16x16x64 MFMA.  MFMA j covers chunks 2j and 2j + 1: lane quarter q holds values 8 q .. + 7 of both
-// (A: two 8-byte pieces of the token row; B: the low and high nibbles of qs[32 j + 8 q ..]).  The 6-bit chunk scale
-// s = 8 a + b (a, b < 8) is applied inside the B operand: D1 = sum_c a_c dot_c and D2 = sum_c b_c dot_c (a q, b q < 128
-// fit int8), so sum_c s_c dot_c = 8 D1 + D2 exactly; a third MFMA against the chunk mins gives sum_c m_c sum(x_c).
-__device__ __forceinline__ void step_q4k(const uint8_t *wl, int q, const int8_t *as, int rr, int ntile, const float *yd,
-                                         float (&acc)[GM_TILES][4]) {
+// Q4_K step on the 16x16x64 MFMA.  The dot products are exact integers, so the K order inside an MFMA is free: in MFMA
+// j (values 64 j .. 64 j + 63 of the span) lane quarter q holds values 64 j + 16 q .. + 15, one contiguous 16-byte
+// piece of the token row (A: a single LDS read straight into the operand registers) and, for B, the same values of the
+// weight row: the low nibbles of qs[32 j + 16 q ..] (chunk 2j) for q < 2, the high nibbles of qs[32 j + 16 (q - 2) ..]
+// (chunk 2j + 1) for q >= 2.  Every lane's 16 values lie in one chunk, so its 6-bit scale s = 8 a + b (a, b < 8) is
+// applied inside B: D1 = sum a_c dot_c and D2 = sum b_c dot_c (a q, b q < 128 fit int8), sum_c s_c dot_c = 8 D1 + D2
+// exactly; a third MFMA against the chunk mins gives sum_c m_c sum(x_c).
+// Token tiles T0 .. T0 + NT - 1 (compile-time: straight-line code, accumulators only for the tiles present)
+// The lane's constants (quarter, row, offsets, selectors) are derived in the step from a lane id the compiler cannot
+// hoist: recomputing them costs a few instructions, keeping them live across the stream would cost registers.
+__device__ __forceinline__ int lane_id_here() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+template <int NT, int T0>
+__device__ __forceinline__ void step_q4k(const uint8_t *wl0, const int8_t *as, const float *yd, float (&acc)[GM_TILES][4]) {
+    const int lid = lane_id_here(), q = lid >> 4, rr = lid & 15;
+    const uint8_t *wl = wl0 + rr * block_bytes(Q4_K);
     const uint4 hd = *(const uint4 *) wl;   // d | dmin, scales[12]
     const uint32_t s_lo = hd.y & 0x3F3F3F3Fu, m_lo = hd.z & 0x3F3F3F3Fu;   // chunks 0..3, one per byte
     const uint32_t s_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);         // chunks 4..7
     const uint32_t m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
-    // accumulators: the first MFMA of a tile starts from zero, so tiles past ntile never need a value
+    const int hs = q >> 1;                   // 1: this lane takes the odd chunk of each pair (the high nibbles)
+    const uint32_t nsh = 4u * (uint32_t) hs;
+    const int8_t *arow = as + rr * 256;      // token row rr of tile 0; piece p of row t sits at p ^ (t % 16)
     const v4i z = {0, 0, 0, 0};
-    v4i d1[GM_TILES], d2[GM_TILES], dm[GM_TILES];
+    v4i d1[NT], d2[NT], dm[NT];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint2 w = *(const uint2 *) (wl + 16 + 32 * j + 8 * q);
+        const uint4 w = *(const uint4 *) (wl + 16 + 32 * j + 16 * (q & 1));
         const uint32_t sp = j < 2 ? s_lo : s_hi, mp = j < 2 ? m_lo : m_hi;
-        const int c0 = (2 * j) & 3;
-        const uint32_t ah = (sp >> 3) & 0x07070707u, bl = sp & 0x07070707u;
-        const uint32_t a0 = bcast16(ah, c0), a1 = bcast16(ah, c0 + 1), b0 = bcast16(bl, c0), b1 = bcast16(bl, c0 + 1);
-        const uint32_t l0 = w.x & 0x0F0F0F0Fu, l1 = w.y & 0x0F0F0F0Fu, h0 = (w.x >> 4) & 0x0F0F0F0Fu, h1 = (w.y >> 4) & 0x0F0F0F0Fu;
-        const v4i B1 = {mul_bytes(l0, a0), mul_bytes(l1, a0), mul_bytes(h0, a1), mul_bytes(h1, a1)};
-        const v4i B2 = {mul_bytes(l0, b0), mul_bytes(l1, b0), mul_bytes(h0, b1), mul_bytes(h1, b1)};
-        const int mm0 = (int) bcast8(mp, c0), mm1 = (int) bcast8(mp, c0 + 1);
-        const v4i Bm = {mm0, mm0, mm1, mm1};
+        const int c = ((2 * j) & 3) + hs;    // this lane's chunk, as a byte of sp / mp
+        const uint32_t a = bcast16((sp >> 3) & 0x07070707u, c), b = bcast16(sp & 0x07070707u, c);
+        const uint32_t n0 = (w.x >> nsh) & 0x0F0F0F0Fu, n1 = (w.y >> nsh) & 0x0F0F0F0Fu;
+        const uint32_t n2 = (w.z >> nsh) & 0x0F0F0F0Fu, n3 = (w.w >> nsh) & 0x0F0F0F0Fu;
+        const v4i B1 = {mul_bytes(n0, a), mul_bytes(n1, a), mul_bytes(n2, a), mul_bytes(n3, a)};
+        const v4i B2 = {mul_bytes(n0, b), mul_bytes(n1, b), mul_bytes(n2, b), mul_bytes(n3, b)};
+        const int mm = (int) bcast8(mp, c);
+        const v4i Bm = {mm, mm, mm, mm};
+        const int po = 16 * ((4 * j + q) ^ rr);
 #pragma unroll
-        for (int t = 0; t < GM_TILES; ++t) {
-            if (t >= ntile) break;
-            const long a_lo = a_frag<true>(as, t, rr, 2 * j, q), a_hi = a_frag<true>(as, t, rr, 2 * j + 1, q);
-            const v4i A = {(int) (uint32_t) a_lo, (int) (uint32_t) ((unsigned long long) a_lo >> 32), (int) (uint32_t) a_hi,
-                           (int) (uint32_t) ((unsigned long long) a_hi >> 32)};
+        for (int t = 0; t < NT; ++t) {
+            const v4i A = *(const v4i *) (arow + (T0 + t) * 16 * 256 + po);
             d1[t] = mfma64(A, B1, j ? d1[t] : z);
             d2[t] = mfma64(A, B2, j ? d2[t] : z);
             dm[t] = mfma64(A, Bm, j ? dm[t] : z);
+            asm volatile("");   // a scheduling-region boundary: operands are not hoisted across tiles (register pressure)
         }
     }
     const float d = h2f(hd.x & 0xffff), dmin = h2f(hd.x >> 16);
 #pragma unroll
-    for (int t = 0; t < GM_TILES; ++t) {
-        if (t >= ntile) break;
+    for (int t = 0; t < NT; ++t) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int si = (d1[t][v] << 3) + d2[t][v];
-            acc[t][v] = __builtin_fmaf(yd[t * 16 + 4 * q + v], __builtin_fmaf(d, (float) si, -(dmin * (float) dm[t][v])), acc[t][v]);
+            acc[T0 + t][v] = __builtin_fmaf(yd[(T0 + t) * 16 + 4 * q + v], __builtin_fmaf(d, (float) si, -(dmin * (float) dm[t][v])), acc[T0 + t][v]);
         }
     }
+}
+
+// 16 bytes at p, which is 2-byte aligned (sb = p & 3 is 0 or 2, the same for every call of a lane): five dwords from
+// p - sb, joined; reads at most p + 18
+__device__ __forceinline__ uint4 ld16_u2(const uint8_t *p, uint32_t sb) {
+    const uint32_t *w = (const uint32_t *) (p - sb);
+    const uint32_t d0 = w[0], d1 = w[1], d2 = w[2], d3 = w[3], d4 = w[4];
+    return make_uint4(__builtin_amdgcn_alignbyte(d1, d0, sb), __builtin_amdgcn_alignbyte(d2, d1, sb),
+                      __builtin_amdgcn_alignbyte(d3, d2, sb), __builtin_amdgcn_alignbyte(d4, d3, sb));
+}
+typedef short v2i16 __attribute__((ext_vector_type(2)));
+
+// Q6_K step on the 16x16x64 MFMA.  In MFMA j (values 64 j .. + 63 of the span) lane quarter q holds values
+// 64 j + 16 q .. + 15, which are exactly scale group g = 4 j + q: A is one contiguous 16-byte piece of the token row,
+// B carries the group's scale, B = sc_g (q6 - 32) in [-4064, 4096], as two int8 planes B = 64 H + L (H = B >> 6 in
+// [-64, 64], L = B & 63): D_H = X.H and D_L = X.L give sum_g sc_g dot_g = 64 D_H + D_L exactly.  The lane's values sit
+// in ql[64 (j / 2) + 16 q ..] (nibble j % 2) and qh[32 (j / 2) + 16 (q % 2) ..] (bits 4 (j % 2) + 2 (q / 2)); rows of
+// the 210-byte blocks are 2-byte aligned in LDS, so 16-byte reads go through ld16_u2.
+template <int NT, int T0>
+__device__ __forceinline__ void step_q6k(const uint8_t *wt0, const int8_t *as, const float *yd, float (&acc)[GM_TILES][4]) {
+    const int lid = lane_id_here(), q = lid >> 4, rr = lid & 15;
+    const uint8_t *blk = wt0 + rr * block_bytes(Q6_K);
+    const uint32_t sb = 2u * (uint32_t) (rr & 1);   // the tile starts dword-aligned; a 210-byte row shifts by 2
+    const uint4 scq = ld16_u2(blk + 192, sb);       // the 16 group scales (int8)
+    const float d = h2f(ld_u16(blk + 208));
+    const int8_t *arow = as + rr * 256;
+    const v4i z = {0, 0, 0, 0};
+    v4i dh[NT], dl[NT];
+    uint4 ql, qh;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if ((j & 1) == 0) {
+            ql = ld16_u2(blk + 64 * (j >> 1) + 16 * q, sb);
+            qh = ld16_u2(blk + 128 + 32 * (j >> 1) + 16 * (q & 1), sb);
+        }
+        const uint32_t scw = j == 0 ? scq.x : j == 1 ? scq.y : j == 2 ? scq.z : scq.w;
+        const int sc = __builtin_amdgcn_sbfe((int) scw, 8 * q, 8);   // scale of group 4 j + q
+        const uint32_t sc16 = ((uint32_t) sc & 0xffffu) * 0x10001u, off16 = ((uint32_t) (-32 * sc) & 0xffffu) * 0x10001u;
+        const uint32_t hsh = 4u * (uint32_t) (j & 1) + 2u * (uint32_t) (q >> 1);
+        const uint32_t qlw[4] = {ql.x, ql.y, ql.z, ql.w}, qhw[4] = {qh.x, qh.y, qh.z, qh.w};
+        int H[4], L[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t nib = ((j & 1) ? qlw[i] >> 4 : qlw[i]) & 0x0F0F0F0Fu;
+            const uint32_t qv = nib | (((qhw[i] >> hsh) & 0x03030303u) << 4);   // four 6-bit values, one per byte
+            // values 0, 1 and 2, 3 in 16-bit lanes: B = q sc - 32 sc, exact in 16 bits
+            const v2u16 e = __builtin_bit_cast(v2u16, __builtin_amdgcn_perm(0u, qv, 0x0C010C00u));
+            const v2u16 o = __builtin_bit_cast(v2u16, __builtin_amdgcn_perm(0u, qv, 0x0C030C02u));
+            const v2u16 s2 = __builtin_bit_cast(v2u16, sc16), c2 = __builtin_bit_cast(v2u16, off16);
+            const v2u16 be = e * s2 + c2, bo = o * s2 + c2;
+            const uint32_t ube = __builtin_bit_cast(uint32_t, be), ubo = __builtin_bit_cast(uint32_t, bo);
+            L[i] = (int) (__builtin_amdgcn_perm(ubo, ube, 0x06040200u) & 0x3F3F3F3Fu);
+            const v2i16 he = __builtin_bit_cast(v2i16, be) >> (short) 6, ho = __builtin_bit_cast(v2i16, bo) >> (short) 6;
+            H[i] = (int) __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, ho), __builtin_bit_cast(uint32_t, he), 0x06040200u);
+        }
+        const v4i Bh = {H[0], H[1], H[2], H[3]}, Bl = {L[0], L[1], L[2], L[3]};
+        const int po = 16 * ((4 * j + q) ^ rr);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const v4i A = *(const v4i *) (arow + (T0 + t) * 16 * 256 + po);
+            dh[t] = mfma64(A, Bh, j ? dh[t] : z);
+            dl[t] = mfma64(A, Bl, j ? dl[t] : z);
+            asm volatile("");   // a scheduling-region boundary: operands are not hoisted across tiles (register pressure)
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int si = (dh[t][v] << 6) + dl[t][v];
+            acc[T0 + t][v] = __builtin_fmaf(yd[(T0 + t) * 16 + 4 * q + v], d * (float) si, acc[T0 + t][v]);
+        }
+    }
+    asm volatile("");   // keeps the tile-count variants from being merged (which moved the accumulators to memory)
 }
 
 __host__ __device__ constexpr int xcd_gcd8(int n) { return (n & 7) == 0 ? 8 : (n & 3) == 0 ? 4 : (n & 1) == 0 ? 2 : 1; }
@@ -527,6 +616,11 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
                 if (++iss_b == nsb) { iss_b = 0; ++iss_it; }
             }
             iss_stage = iss_stage == D - 1 ? 0 : iss_stage + 1;
+            // uniform counters: kept in scalar registers (the compiler cannot prove them uniform by itself)
+            iss_it = __builtin_amdgcn_readfirstlane(iss_it);
+            iss_b = __builtin_amdgcn_readfirstlane(iss_b);
+            iss_step = __builtin_amdgcn_readfirstlane(iss_step);
+            iss_stage = __builtin_amdgcn_readfirstlane(iss_stage);
         };
 
         float acc[GM_TILES][4];
@@ -538,8 +632,25 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
             const int ntok = __builtin_amdgcn_readfirstlane(s_item[it][1]), ntile = (ntok + 15) >> 4;   // uniform
             const int8_t *as = stage_a(stage);
             const float *yd = stage_d(stage);
-            if constexpr (T == Q4_K) step_q4k(stage_w(stage) + wave * C::TB + rr * C::BB, q, as, rr, ntile, yd, acc);
-            else {
+            if constexpr (T == Q4_K) {
+                // straight-line code per tile count
+                const uint8_t *wt = stage_w(stage) + wave * C::TB;
+                static_assert(GM_TILES == 4, "one case per tile count");
+                switch (ntile) {
+                case 1: step_q4k<1, 0>(wt, as, yd, acc); break;
+                case 2: step_q4k<2, 0>(wt, as, yd, acc); break;
+                case 3: step_q4k<3, 0>(wt, as, yd, acc); break;
+                default: step_q4k<4, 0>(wt, as, yd, acc); break;
+                }
+            } else if constexpr (T == Q6_K) {
+                const uint8_t *wt = stage_w(stage) + wave * C::TB;
+                switch (ntile) {
+                case 1: step_q6k<1, 0>(wt, as, yd, acc); break;
+                case 2: step_q6k<2, 0>(wt, as, yd, acc); break;
+                case 3: step_q6k<3, 0>(wt, as, yd, acc); break;
+                default: step_q6k<4, 0>(wt, as, yd, acc); break;
+                }
+            } else {
             Raw<T> wr;
             wr.load(stage_w(stage) + wave * C::TB + rr * C::BB, q);
             int si[GM_TILES][4];
@@ -881,7 +992,7 @@ int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int
     }
     if ((size_t) n_pairs * (m.ff / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_down: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
     HY_GEMM_SWITCH(m.td, {
-        constexpr int W = 8, B = g5_blocks<TT, false>();
+        constexpr int W = TT == Q6_K ? 16 : 8, B = g5_blocks<TT, false>();   // Q6_K: 16 waves (fits 128 registers)
         const int rb = m.n / (16 * W);   // 16 W output rows a block
         dim3 grid(rb, item_slots(rb, n_pairs, max_active, B));
         hipLaunchKernelGGL((k_gemm<TT, false, W, B>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
