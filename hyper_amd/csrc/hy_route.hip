@@ -104,28 +104,98 @@ int launch_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, 
     return check_launch("hy_gemv_f32");
 }
 
-// Router logits of many tokens and the Q8 rows of x in one launch: blocks [0, gemv_blocks) are k_gemv_f32<4, 8>'s
-// grid (gx blocks of 16 rows per 8 tokens), the rest quantize x -- Q8_K: 16 blocks of 256 values per block,
-// 16 lanes each; Q8_0: 4 pairs of 32-value blocks per block, a wave each.
+// The same contract for a block tile of 16 rows x 16 tokens (kdim a multiple of 256), 8 waves: each 256-value step
+// of the 16 W rows and 16 x rows goes through LDS once (32 KB, one global read per block instead of one per wave),
+// and wave w computes rows 4 (w % 4) .. + 3 of tokens 8 (w / 4) .. + 7 from it.  Lane L reads the float4 at 4 L of
+// each row, so every lane's partial sums see the elements of gemv_tile in the same order.  The next step's 32 KB are
+// loaded into registers while this step's fmas run.
+constexpr int GL_R = 16, GL_T = 16, GL_THREADS = 512;
+typedef float f4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void gemv_block_lds(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+                                               float *__restrict__ y, int ys, int nt, const float *__restrict__ bias, int bs, int r0,
+                                               int t0, f4v *st) {   // st: LDS, (GL_R + GL_T) rows of 64 float4
+    constexpr int RW = 4, TW = 8, NS = (GL_R + GL_T) * 64 / GL_THREADS;   // float4 staged by each thread per step
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr0 = r0 + RW * (wave & 3), wt0 = t0 + TW * (wave >> 2);   // this wave's rows and tokens
+    // the NS float4 this thread stages per step: tile row (tid + 512 k) / 64 (W rows, then x rows), column tid % 64
+    const float *src[NS];
+#pragma clang loop unroll(full)
+    for (int k = 0; k < NS; ++k) {
+        const int row = (tid >> 6) + (GL_THREADS / 64) * k;
+        if (row < GL_R) { const int r = r0 + row; src[k] = W + (size_t) (r < rows ? r : rows - 1) * kdim + 4 * lane; }
+        else { const int t = t0 + row - GL_R; src[k] = x + (size_t) (t < nt ? t : nt - 1) * xs + 4 * lane; }
+    }
+    float bv = 0.0f;   // lane a TW + b: the bias of (row wr0 + a, token wt0 + b), added after the butterfly
+    if (bias && lane < RW * TW && wr0 + lane / TW < rows && wt0 + lane % TW < nt) bv = bias[(size_t) (wt0 + lane % TW) * bs + wr0 + lane / TW];
+    float acc[RW][TW];
+#pragma unroll
+    for (int a = 0; a < RW; ++a)
+#pragma unroll
+        for (int b = 0; b < TW; ++b) acc[a][b] = 0.0f;
+    f4v pre[NS];
+#pragma clang loop unroll(full)
+    for (int k = 0; k < NS; ++k) pre[k] = *(const f4v *) src[k];
+    const int niter = kdim / 256;
+    for (int i = 0; i < niter; ++i) {
+        __syncthreads();   // the previous step's reads of st are done
+#pragma clang loop unroll(full)
+        for (int k = 0; k < NS; ++k) st[tid + GL_THREADS * k] = pre[k];
+        __syncthreads();
+        if (i + 1 < niter) {
+#pragma clang loop unroll(full)
+            for (int k = 0; k < NS; ++k) pre[k] = *(const f4v *) (src[k] + 256 * (i + 1));
+        }
+        f4v xv[TW];
+#pragma unroll
+        for (int b = 0; b < TW; ++b) xv[b] = st[(GL_R + TW * (wave >> 2) + b) * 64 + lane];
+#pragma unroll
+        for (int a = 0; a < RW; ++a) {
+            const f4v wv = st[(RW * (wave & 3) + a) * 64 + lane];
+#pragma unroll
+            for (int b = 0; b < TW; ++b) {
+                float s = acc[a][b];
+                s = __builtin_fmaf(wv.x, xv[b].x, s);
+                s = __builtin_fmaf(wv.y, xv[b].y, s);
+                s = __builtin_fmaf(wv.z, xv[b].z, s);
+                s = __builtin_fmaf(wv.w, xv[b].w, s);
+                acc[a][b] = s;
+            }
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < RW; ++a)
+#pragma unroll
+        for (int b = 0; b < TW; ++b) {
+            float s = wave_sum_xor(acc[a][b]);
+            if (bias) s = s + readlane_f(bv, a * TW + b);
+            if (lane == 0 && wr0 + a < rows && wt0 + b < nt) y[(size_t) (wt0 + b) * ys + wr0 + a] = s;
+        }
+}
+
+// Router logits of many tokens and the Q8 rows of x in one launch: blocks [0, gemv_blocks) compute the logits (gx
+// blocks of 16 rows per 16 tokens through gemv_block_lds, or per 8 tokens through gemv_tile), the rest quantize x --
+// Q8_K: 32 blocks of 256 values per block, 16 lanes each; Q8_0: 8 pairs of 32-value blocks per block, a wave each.
 template <int VT>
-__global__ __launch_bounds__(256) void k_router_pre(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+__global__ __launch_bounds__(GL_THREADS) void k_router_pre(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
                                                     const float *__restrict__ bias, int bs, float *__restrict__ y, int ys, int nt,
                                                     uint8_t *__restrict__ xq, int gx, int gemv_blocks) {
+    __shared__ f4v st[(GL_R + GL_T) * 64];
     const int bid = blockIdx.x;
     if (bid < gemv_blocks) {
         int bx, by;
         gemv_tile_of(bid, gx, gemv_blocks / gx, bx, by);
-        gemv_tile<4, 8>(W, rows, kdim, x, xs, y, ys, nt, bias, bs, (bx * 4 + (threadIdx.x >> 6)) * 4, by * 8);
+        if (kdim % 256 == 0) gemv_block_lds(W, rows, kdim, x, xs, y, ys, nt, bias, bs, bx * GL_R, by * GL_T, st);
+        else if (threadIdx.x < 256) gemv_tile<4, 8>(W, rows, kdim, x, xs, y, ys, nt, bias, bs, (bx * 4 + (threadIdx.x >> 6)) * 4, by * 8);
         return;
     }
     const int qb = bid - gemv_blocks;
     if constexpr (VT == Q8_K) {
-        const int nb = kdim / 256, u = qb * 16 + (threadIdx.x >> 4);
+        const int nb = kdim / 256, u = qb * (GL_THREADS / 16) + (threadIdx.x >> 4);
         if (u >= nt * nb) return;   // uniform over the 16-lane row
         const int t = u / nb, b = u - t * nb;
         q8k_block16_load(x + (size_t) t * xs + 256 * b, xq + ((size_t) t * nb + b) * Q8K_BYTES);
     } else {
-        const int nb = kdim / 32, npair = (nb + 1) / 2, u = qb * 4 + (threadIdx.x >> 6);
+        const int nb = kdim / 32, npair = (nb + 1) / 2, u = qb * (GL_THREADS / 64) + (threadIdx.x >> 6);
         if (u >= nt * npair) return;   // wave-uniform
         const int t = u / npair, b = 2 * (u - t * npair);
         q8_0_pair_wave(x + (size_t) t * xs + 32 * b, xq + ((size_t) t * nb + b) * Q8_0_BYTES, b + 1 < nb, Q8_0_BYTES, 2);
@@ -135,14 +205,15 @@ __global__ __launch_bounds__(256) void k_router_pre(const float *__restrict__ W,
 int launch_router_pre(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
                       int vtype, void *xq, int nt, hipStream_t s) {
     if (nt == 0) return HY_OK;
-    const int gx = (rows + 15) / 16, gemv_blocks = gx * ((nt + 7) / 8);
+    // kdim % 256 == 0: 16 x 16 tiles through LDS (gemv_block_lds); else 16 rows x 8 tokens a block (gemv_tile)
+    const int gx = (rows + 15) / 16, gemv_blocks = gx * (kdim % 256 == 0 ? (nt + GL_T - 1) / GL_T : (nt + 7) / 8);
     if (vtype == Q8_K) {
-        const int qblocks = (nt * (kdim / 256) + 15) / 16;
-        hipLaunchKernelGGL(k_router_pre<Q8_K>, dim3(gemv_blocks + qblocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, nt,
+        const int qblocks = (nt * (kdim / 256) + GL_THREADS / 16 - 1) / (GL_THREADS / 16);
+        hipLaunchKernelGGL(k_router_pre<Q8_K>, dim3(gemv_blocks + qblocks), dim3(GL_THREADS), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, nt,
                            (uint8_t *) xq, gx, gemv_blocks);
     } else {
-        const int qblocks = (nt * ((kdim / 32 + 1) / 2) + 3) / 4;
-        hipLaunchKernelGGL(k_router_pre<Q8_0>, dim3(gemv_blocks + qblocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, nt,
+        const int qblocks = (nt * ((kdim / 32 + 1) / 2) + GL_THREADS / 64 - 1) / (GL_THREADS / 64);
+        hipLaunchKernelGGL(k_router_pre<Q8_0>, dim3(gemv_blocks + qblocks), dim3(GL_THREADS), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, nt,
                            (uint8_t *) xq, gx, gemv_blocks);
     }
     return check_launch("hy_moe_router_q8");
