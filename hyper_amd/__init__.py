@@ -38,6 +38,12 @@ class hy_expert_tensors(ctypes.Structure):
                 ("tg", ctypes.c_int32), ("td", ctypes.c_int32)]
 
 
+class hy_gguf_tensor_info(ctypes.Structure):
+    """C layout of hy_gguf_tensor_info (include/hymoe.h; replaces GTensor, src/gguf.h:22-32)."""
+    _fields_ = [("name", ctypes.c_char_p), ("data", ctypes.c_void_p), ("nbytes", ctypes.c_size_t),
+                ("type", ctypes.c_int32), ("n_dims", ctypes.c_int32), ("ne", ctypes.c_int64 * 4)]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
@@ -53,6 +59,19 @@ SIGNATURES = {
     "hy_q8_row_bytes": (ctypes.c_size_t, [_I, _I]),
     "hy_upload_experts": (_I, [ctypes.POINTER(hy_expert_tensors), _P, ctypes.c_int32, ctypes.c_int32, _F, _DEV]),
     "hy_free_experts": (_I, [_DEV]),
+    "hy_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]),
+    "hy_gguf_close": (_I, [_P]),
+    "hy_gguf_arch": (ctypes.c_char_p, [_P]),
+    "hy_gguf_has": (_I, [_P, ctypes.c_char_p]),
+    "hy_gguf_get_int": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+    "hy_gguf_get_float": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    "hy_gguf_get_str": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)]),
+    "hy_gguf_get_int_arr": (_I, [_P, ctypes.c_char_p, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]),
+    "hy_gguf_get_float_arr": (_I, [_P, ctypes.c_char_p, _P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]),
+    "hy_gguf_n_tensors": (_I, [_P]),
+    "hy_gguf_tensor_at": (_I, [_P, _I, ctypes.POINTER(hy_gguf_tensor_info)]),
+    "hy_gguf_tensor": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(hy_gguf_tensor_info)]),
+    "hy_gguf_expert_tensors": (_I, [_P, _I, _I, ctypes.POINTER(hy_expert_tensors)]),
     "hy_gemv_f32": (_I, [_P, _I, _I, _P, _I, _P, _I, _I, _P, _I, _P]),
     "hy_moe_route": (_I, [_P, _I, _I, _I, _P, _P, _P, _I, _P]),
     "hy_moe_order": (_I, [_DEV, _P, _I, _I, _P, _P, _P, _P]),

@@ -68,6 +68,41 @@ typedef struct hy_expert_tensors {
 const char *hy_last_error(void);
 int hy_abi_version(void);
 
+/* ---- GGUF expert loading (replaces class GGUF, src/gguf.h:38-70 / src/gguf.cpp:84-285, and expert_tensors,
+   src/experts.h:26 / src/experts.cu:12-22).  A read-only view of a GGUF v2/v3 file, memory-mapped; path may name the
+   first shard of a split model (<name>-00001-of-0000N.gguf): every shard is mapped and the metadata comes from the
+   first.  Opening fails (HY_EINVAL with a message) on a bad magic, a truncated header, a tensor outside its file or
+   named twice, or a missing general.architecture; HY_EUNSUPPORTED_TYPE on a tensor type outside the reader's table
+   (src/gguf.cpp:43-82).  Tensor data pointers stay valid until hy_gguf_close. */
+typedef struct hy_gguf hy_gguf;
+typedef struct hy_gguf_tensor_info {    /* GTensor, src/gguf.h:22-32 */
+    const char *name;
+    const uint8_t *data;           /* host, inside the mapping */
+    size_t nbytes;
+    int32_t type;                  /* GGUF type id */
+    int32_t n_dims;
+    int64_t ne[4];                 /* ggml order: ne[0] is the row length; unused dimensions are 1 */
+} hy_gguf_tensor_info;
+int hy_gguf_open(const char *path, hy_gguf **out);
+int hy_gguf_close(hy_gguf *g);
+const char *hy_gguf_arch(const hy_gguf *g);                   /* general.architecture (GGUF::arch) */
+int hy_gguf_has(const hy_gguf *g, const char *key);           /* 1 if the key is present (GGUF::has) */
+/* metadata (GGUF::get_int / get_float / get_str / get_int_arr / get_float_arr): HY_EINVAL if the key is missing or of
+   another kind; an int reads as a float, a scalar as a one-element array; arrays copy min(cap, length) elements and
+   set *n to the length; strings stay valid until hy_gguf_close */
+int hy_gguf_get_int(const hy_gguf *g, const char *key, int64_t *out);
+int hy_gguf_get_float(const hy_gguf *g, const char *key, double *out);
+int hy_gguf_get_str(const hy_gguf *g, const char *key, const char **out);
+int hy_gguf_get_int_arr(const hy_gguf *g, const char *key, int64_t *out, size_t cap, size_t *n);
+int hy_gguf_get_float_arr(const hy_gguf *g, const char *key, double *out, size_t cap, size_t *n);
+/* the tensor table (GGUF::tensors / tensor / need): by position in file order, or by name (HY_EINVAL if missing) */
+int hy_gguf_n_tensors(const hy_gguf *g);
+int hy_gguf_tensor_at(const hy_gguf *g, int i, hy_gguf_tensor_info *out);
+int hy_gguf_tensor(const hy_gguf *g, const char *name, hy_gguf_tensor_info *out);
+/* blk.<il>.ffn_{gate,up,down}_exps.weight of E experts: host pointers, bytes per expert matrix, types (gate and up
+   alike, else HY_EBAD_SHAPE) -- ready for hy_upload_experts */
+int hy_gguf_expert_tensors(const hy_gguf *g, int il, int E, hy_expert_tensors *out);
+
 /* bytes per block / values per block / activation partner type of a GGUF type (src/gguf.cpp:43-82;
    vec_dot_type: src/cpu_moe.cpp:711-715); 0 or -1 for types the path does not take */
 size_t hy_block_bytes(int type);

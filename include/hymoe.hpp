@@ -35,6 +35,65 @@ inline MoeDev upload_experts(const ExpertTensors &t, const std::vector<int> &slo
 }
 inline void free_experts(MoeDev &m) { check(hy_free_experts(&m)); }
 
+// src/gguf.h:22-32 -- a tensor of a GGUF file (host data inside the mapping)
+struct GTensor {
+    std::string name;
+    int type = 0;
+    std::vector<int64_t> ne;
+    const uint8_t *data = nullptr;
+    size_t nbytes = 0;
+};
+// src/gguf.h:38-70 -- a read-only GGUF file (or the shards of a split model), memory-mapped while the object lives
+class GGUF {
+public:
+    explicit GGUF(const std::string &path) { check(hy_gguf_open(path.c_str(), &g_)); }
+    ~GGUF() { hy_gguf_close(g_); }
+    GGUF(const GGUF &) = delete;
+    GGUF &operator=(const GGUF &) = delete;
+    bool has(const std::string &key) const { return hy_gguf_has(g_, key.c_str()) != 0; }
+    int64_t get_int(const std::string &key) const { int64_t v = 0; check(hy_gguf_get_int(g_, key.c_str(), &v)); return v; }
+    int64_t get_int(const std::string &key, int64_t def) const { return has(key) ? get_int(key) : def; }
+    double get_float(const std::string &key) const { double v = 0; check(hy_gguf_get_float(g_, key.c_str(), &v)); return v; }
+    double get_float(const std::string &key, double def) const { return has(key) ? get_float(key) : def; }
+    std::string get_str(const std::string &key) const { const char *v = nullptr; check(hy_gguf_get_str(g_, key.c_str(), &v)); return v; }
+    std::vector<int64_t> get_int_arr(const std::string &key) const {
+        size_t n = 0;
+        check(hy_gguf_get_int_arr(g_, key.c_str(), nullptr, 0, &n));
+        std::vector<int64_t> v(n);
+        check(hy_gguf_get_int_arr(g_, key.c_str(), v.data(), n, &n));
+        return v;
+    }
+    std::vector<double> get_float_arr(const std::string &key) const {
+        size_t n = 0;
+        check(hy_gguf_get_float_arr(g_, key.c_str(), nullptr, 0, &n));
+        std::vector<double> v(n);
+        check(hy_gguf_get_float_arr(g_, key.c_str(), v.data(), n, &n));
+        return v;
+    }
+    std::string arch() const { return hy_gguf_arch(g_); }
+    bool tensor(const std::string &name, GTensor &out) const {   // false if missing (GGUF::tensor returns nullptr)
+        hy_gguf_tensor_info t;
+        if (hy_gguf_tensor(g_, name.c_str(), &t) != HY_OK) return false;
+        out = {t.name, t.type, std::vector<int64_t>(t.ne, t.ne + t.n_dims), t.data, t.nbytes};
+        return true;
+    }
+    GTensor need(const std::string &name) const {
+        GTensor t;
+        if (!tensor(name, t)) throw std::runtime_error("gguf: missing tensor " + name);
+        return t;
+    }
+    const hy_gguf *handle() const { return g_; }
+
+private:
+    hy_gguf *g_ = nullptr;
+};
+// src/experts.h:26 / src/experts.cu:12-22 -- blk.<il>.ffn_{gate,up,down}_exps.weight of E experts
+inline ExpertTensors expert_tensors(const GGUF &g, int il, int E) {
+    hy_expert_tensors c{};
+    check(hy_gguf_expert_tensors(g.handle(), il, E, &c));
+    return {c.gate, c.up, c.down, c.gb, c.db, c.E, c.tg, c.td};
+}
+
 // src/kernels4.cuh:35
 inline void gemv_f32(const float *W, int rows, int k, const float *x, int xs, float *y, int ys, int nt, hipStream_t s,
                      const float *bias = nullptr, int bias_stride = 0) {
