@@ -74,6 +74,8 @@ SIGNATURES = {
     "hy_gguf_expert_tensors": (_I, [_P, _I, _I, ctypes.POINTER(hy_expert_tensors)]),
     "hy_gemv_f32": (_I, [_P, _I, _I, _P, _I, _P, _I, _I, _P, _I, _P]),
     "hy_moe_route": (_I, [_P, _I, _I, _I, _P, _P, _P, _I, _P]),
+    "hy_moe_route_sig": (_I, [_P, _I, _P, _I, _I, _F, _P, _P, _P, _I, _P]),
+    "hy_moe_route_sqrtsp": (_I, [_P, _I, _P, _I, _I, _F, _P, _P, _I, _P]),
     "hy_moe_order": (_I, [_DEV, _P, _I, _I, _P, _P, _P, _P]),
     "hy_q8_quantize": (_I, [_I, _P, _I, _I, _I, _P, _P]),
     "hy_moe_gate_up": (_I, [_DEV, _P, _I, _P, _I, _P, _I, _P, _P, _P]),

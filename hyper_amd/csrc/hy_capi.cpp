@@ -141,6 +141,25 @@ int hy_moe_route(const float *logits, int ls, int n_expert, int k, int32_t *ids,
     return launch_route(logits, ls, n_expert, k, ids, wts, sg, nt, s);
 }
 
+static int route_bias_args(const char *what, const float *logits, int ls, const float *bias, int n_expert, int k, const int32_t *ids,
+                           const float *wts, int nt) {
+    if (!logits || !bias || !ids || !wts || nt < 0) { set_error("%s: bad argument", what); return HY_EINVAL; }
+    if (n_expert <= 0 || n_expert > 1024) { set_error("%s: n_expert %d out of range (1..1024)", what, n_expert); return HY_EBAD_SHAPE; }
+    if (k <= 0 || k > 16 || k > n_expert) { set_error("%s: k = %d out of range (1..16)", what, k); return HY_EBAD_SHAPE; }
+    if (ls < n_expert) { set_error("%s: logit stride %d too small", what, ls); return HY_EBAD_SHAPE; }
+    return HY_OK;
+}
+int hy_moe_route_sig(const float *logits, int ls, const float *bias, int n_expert, int k, float scale, int32_t *ids, float *wts, float *sg,
+                     int nt, hipStream_t s) {
+    const int rc = route_bias_args("hy_moe_route_sig", logits, ls, bias, n_expert, k, ids, wts, nt);
+    return rc != HY_OK ? rc : launch_route_bias(0, logits, ls, bias, n_expert, k, scale, ids, wts, sg, nt, s);
+}
+int hy_moe_route_sqrtsp(const float *logits, int ls, const float *bias, int n_expert, int k, float scale, int32_t *ids, float *wts, int nt,
+                        hipStream_t s) {
+    const int rc = route_bias_args("hy_moe_route_sqrtsp", logits, ls, bias, n_expert, k, ids, wts, nt);
+    return rc != HY_OK ? rc : launch_route_bias(1, logits, ls, bias, n_expert, k, scale, ids, wts, nullptr, nt, s);
+}
+
 int hy_moe_order(const hy_moe_dev *m, const int32_t *ids, int n_pairs, int n_expert, int32_t *order, int32_t *order_n, hipStream_t s,
                  int32_t *egrp) {
     if (!m || !m->slot || !ids || !order || !order_n || n_pairs < 0) { set_error("hy_moe_order: bad argument"); return HY_EINVAL; }

@@ -60,6 +60,47 @@ __device__ __forceinline__ float hy_expf(float x) {
     return (y * s1) * s2;
 }
 __device__ __forceinline__ float hy_silu(float x) { return x / (1.0f + hy_expf(-x)); }
+// log(x), x > 0: x = 2^e m with m in [sqrt(1/2), sqrt(2)), log(m) by the Cephes single-precision polynomial in
+// f = m - 1 (S. L. Moshier, Cephes Math Library, logf.c) with fmaf, e ln2 added as e C2 + e C1 (C1 = 0.693359375);
+// subnormal x scaled by 2^23 first.  The same operations as the oracle's or_logf.
+__device__ __forceinline__ float hy_logf(float x) {
+    if (x != x || x < 0.0f) return __builtin_nanf("");
+    if (x == 0.0f) return -__builtin_huge_valf();
+    if (x == __builtin_huge_valf()) return x;
+    int e = 0;
+    if (x < 1.17549435e-38f) { x = x * 8388608.0f; e = -23; }
+    const uint32_t b = __float_as_uint(x);
+    e += (int) ((b >> 23) & 0xffu) - 126;
+    const float m = __uint_as_float((b & 0x007fffffu) | 0x3f000000u);
+    float f;
+    if (m < 0.70710678118654752f) { e -= 1; f = m + m - 1.0f; } else { f = m - 1.0f; }
+    const float z = f * f;
+    float y = 7.0376836292e-2f;
+    y = __builtin_fmaf(y, f, -1.1514610310e-1f);
+    y = __builtin_fmaf(y, f, 1.1676998740e-1f);
+    y = __builtin_fmaf(y, f, -1.2420140846e-1f);
+    y = __builtin_fmaf(y, f, 1.4249322787e-1f);
+    y = __builtin_fmaf(y, f, -1.6668057665e-1f);
+    y = __builtin_fmaf(y, f, 2.0000714765e-1f);
+    y = __builtin_fmaf(y, f, -2.4999993993e-1f);
+    y = __builtin_fmaf(y, f, 3.3333331174e-1f);
+    y = (y * f) * z;
+    const float fe = (float) e;
+    y = __builtin_fmaf(fe, -2.12194440e-4f, y);
+    y = __builtin_fmaf(-0.5f, z, y);
+    return __builtin_fmaf(fe, 0.693359375f, f + y);
+}
+// log(1 + x), x >= -1: log(u) x / (u - 1) with u = 1 + x rounded (D. Goldberg, 1991, theorem 4); x when u == 1
+__device__ __forceinline__ float hy_log1pf(float x) {
+    if (x != x) return x;
+    const float u = 1.0f + x;
+    if (u == 1.0f) return x;
+    if (u == __builtin_huge_valf()) return u;
+    return hy_logf(u) * (x / (u - 1.0f));
+}
+// the routers' scores: sigmoid (src/kernels5.cu:35) and sqrt(softplus) (src/kernels7.cu:823-826)
+__device__ __forceinline__ float hy_sigmoid(float l) { return 1.0f / (1.0f + hy_expf(-l)); }
+__device__ __forceinline__ float hy_sqrt_softplus(float l) { return sqrtf(l > 20.0f ? l : hy_log1pf(hy_expf(l))); }
 // silu(g) * u, with a limit L > 0: silu(min(g, L)) * clamp(u, -L, L) (src/cpu_moe.cpp:891-892)
 __device__ __forceinline__ float hy_swiglu(float g, float u, float L) {
     if (L > 0.0f) { g = fminf(g, L); u = fminf(fmaxf(u, -L), L); }

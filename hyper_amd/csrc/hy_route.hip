@@ -253,6 +253,74 @@ int launch_route(const float *logits, int ls, int ne, int k, int *ids, float *wt
     return check_launch("hy_moe_route");
 }
 
+// Routers with a selection bias (one wave per token): score s_e from the logit -- MODE 0: sigmoid, the contract of
+// k_moe_route_sig (src/kernels5.cu:1090-1122); MODE 1: sqrt(softplus), the contract of k_route7 (src/kernels7.cu:
+// 816-865) -- then the top k of s_e + bias[e] (ties to the lower index) by k rounds of wave argmax over each lane's
+// sorted candidates, as route_wave; the weights use the scores alone, summed in selection order:
+// MODE 0: s scale / max(sum, 2^-14) (and sg = 1); MODE 1: s / (sum + 1e-20) scale.
+template <int V, int MODE>
+__global__ __launch_bounds__(64) void k_route_bias(const float *__restrict__ logits, int ls, const float *__restrict__ bias, int ne, int k,
+                                                   float scale, int *__restrict__ ids, float *__restrict__ wts, float *__restrict__ sg) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const float *l = logits + (size_t) t * ls;
+    float key[V], val[V];
+    int vi[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int e = lane + 64 * i;
+        if (e < ne) {
+            const float x = l[e];
+            val[i] = MODE == 0 ? hy_sigmoid(x) : hy_sqrt_softplus(x);
+            key[i] = val[i] + bias[e];
+            vi[i] = e;
+        } else {
+            key[i] = -__builtin_huge_valf();
+            val[i] = 0.0f;
+            vi[i] = 0x7fffffff;
+        }
+    }
+#pragma unroll
+    for (int i = 1; i < V; ++i)
+#pragma unroll
+        for (int j = i; j > 0; --j)
+            if (rt_better2(key[j], vi[j], key[j - 1], vi[j - 1])) {
+                const float tk = key[j]; key[j] = key[j - 1]; key[j - 1] = tk;
+                const float tv = val[j]; val[j] = val[j - 1]; val[j - 1] = tv;
+                const int ti = vi[j]; vi[j] = vi[j - 1]; vi[j - 1] = ti;
+            }
+    float tot = 0.0f, selv = 0.0f;
+    int seli = 0;
+    for (int j = 0; j < k; ++j) {
+        float bk = key[0];
+        int bi = vi[0];
+        wave_best(bk, bi, rt_better2);
+        const float bv = readlane_f(val[0], bi & 63);   // the winner heads its lane's (sorted) list
+        tot = tot + bv;
+        if (lane == j) { selv = bv; seli = bi; }
+        if (vi[0] == bi) {
+#pragma unroll
+            for (int i = 0; i < V - 1; ++i) { key[i] = key[i + 1]; val[i] = val[i + 1]; vi[i] = vi[i + 1]; }
+            key[V - 1] = -__builtin_huge_valf(); val[V - 1] = 0.0f; vi[V - 1] = 0x7fffffff;
+        }
+    }
+    if (lane < k) {
+        ids[(size_t) t * k + lane] = seli;
+        wts[(size_t) t * k + lane] = MODE == 0 ? selv * (scale / fmaxf(tot, 6.103515625e-5f)) : selv / (tot + 1e-20f) * scale;
+    }
+    if (MODE == 0 && sg && lane == 0) sg[t] = 1.0f;
+}
+
+int launch_route_bias(int mode, const float *logits, int ls, const float *bias, int ne, int k, float scale, int *ids, float *wts,
+                      float *sg, int nt, hipStream_t s) {
+    if (nt == 0) return HY_OK;
+    const int V = (ne + 63) / 64;
+#define HY_RB(VV) { if (mode == 0) hipLaunchKernelGGL((k_route_bias<VV, 0>), dim3(nt), dim3(64), 0, s, logits, ls, bias, ne, k, scale, ids, wts, sg); \
+                    else hipLaunchKernelGGL((k_route_bias<VV, 1>), dim3(nt), dim3(64), 0, s, logits, ls, bias, ne, k, scale, ids, wts, sg); }
+    if (V <= 1) HY_RB(1) else if (V <= 2) HY_RB(2) else if (V <= 4) HY_RB(4) else if (V <= 8) HY_RB(8) else HY_RB(16)
+#undef HY_RB
+    return check_launch(mode == 0 ? "hy_moe_route_sig" : "hy_moe_route_sqrtsp");
+}
+
 // ---------------------------------------------------------------- bucketing (A3)
 // One block of 16 waves.  Pairs p with slot[ids[p]] >= 0, grouped by expert, stable by pair index
 // (src/cpu_moe.cpp:672-687 order; the GPU reference src/kernels4.cu:1275-1295 is unordered within an

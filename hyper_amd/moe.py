@@ -110,6 +110,16 @@ def moe_route(logits, ls, n_expert, k, ids, wts, sg, nt, stream=None):
     check(lib().hy_moe_route(_p(logits), ls, n_expert, k, _p(ids), _p(wts), _p(sg), nt, _s(stream)))
 
 
+def moe_route_sig(logits, ls, bias, n_expert, k, scale, ids, wts, sg, nt, stream=None):
+    """Sigmoid router with selection bias (moe_route_sig, src/kernels5.cuh:74)."""
+    check(lib().hy_moe_route_sig(_p(logits), ls, _p(bias), n_expert, k, float(scale), _p(ids), _p(wts), _p(sg), nt, _s(stream)))
+
+
+def moe_route_sqrtsp(logits, ls, bias, n_expert, k, scale, ids, wts, nt, stream=None):
+    """sqrt-softplus router with selection bias (route7, src/kernels7.cuh:75)."""
+    check(lib().hy_moe_route_sqrtsp(_p(logits), ls, _p(bias), n_expert, k, float(scale), _p(ids), _p(wts), nt, _s(stream)))
+
+
 def moe_order(m: MoeDev, ids, n_pairs, n_expert, order, order_n, stream=None, egrp=None):
     check(lib().hy_moe_order(m.ref, _p(ids), n_pairs, n_expert, _p(order), _p(order_n), _s(stream), _p(egrp)))
 
@@ -169,10 +179,19 @@ class MoeLayerRunner:
     decode(x): rows <= decode_rows use gate/up GEMV -> fused down+combine (src/engine4.cu:880-888);
     prefill(x): bucketing + grouped int8-MFMA GEMMs (src/engine4.cu:851-854, :887).
     The router is fp32 W_r [E, d] (src/engine4.cu:807); `bias` adds per-token logits (skewed routing).
+    `router` picks the routing on the logits: "softmax" (moe_route, src/kernels4.cu:297-344), or, with `router_bias`
+    (E floats, selection only) and `router_scale`: "sigmoid" (moe_route_sig, src/kernels5.cu:1090-1122; sg = 1) or
+    "sqrt_softplus" (route7, src/kernels7.cu:816-865).
     """
 
     def __init__(self, dev: MoeDev, W_r: torch.Tensor, k: int, max_rows: int, shared: Optional[MoeDev] = None,
-                 sg_logit: bool = False):
+                 sg_logit: bool = False, router: str = "softmax", router_bias: Optional[torch.Tensor] = None,
+                 router_scale: float = 1.0):
+        if router not in ("softmax", "sigmoid", "sqrt_softplus"):
+            raise ValueError(f"unknown router {router!r}")
+        if router != "softmax" and (router_bias is None or sg_logit):
+            raise ValueError(f"the {router} router takes router_bias and no shared-gate logit")
+        self.router, self.router_bias, self.router_scale = router, router_bias, float(router_scale)
         L = dev.layer
         self.dev, self.W_r, self.k, self.E, self.d, self.ff = dev, W_r, k, dev.slot.numel(), L.n, L.ff
         self.shared = shared
@@ -184,7 +203,7 @@ class MoeLayerRunner:
         self.logits = torch.empty(T, self.ls, **f32)
         self.ids = torch.empty(P, **i32)
         self.wts = torch.empty(P, **f32)
-        self.sg = torch.empty(T, **f32) if sg_logit else None
+        self.sg = torch.empty(T, **f32) if sg_logit or router == "sigmoid" else None
         self.order = torch.empty(P, **i32)
         self.order_n = torch.zeros(2, **i32)
         self.egrp = torch.empty(3 * self.E, **i32)
@@ -207,11 +226,21 @@ class MoeLayerRunner:
             self.sh_xq = torch.empty(T * q8_row_bytes(vec_dot_type(S.tg), self.d), dtype=torch.uint8, device=device)
             self.sh_hq = torch.empty(T * q8_row_bytes(vec_dot_type(S.td), S.ff), dtype=torch.uint8, device=device)
 
+    def _route_logits(self, nt: int, stream=None):
+        if self.router == "softmax":
+            moe_route(self.logits, self.ls, self.E, self.k, self.ids, self.wts, self.sg, nt, stream)
+        elif self.router == "sigmoid":
+            moe_route_sig(self.logits, self.ls, self.router_bias, self.E, self.k, self.router_scale, self.ids, self.wts, self.sg,
+                          nt, stream)
+        else:
+            moe_route_sqrtsp(self.logits, self.ls, self.router_bias, self.E, self.k, self.router_scale, self.ids, self.wts, nt,
+                             stream)
+
     def route(self, x: torch.Tensor, nt: int, bias: Optional[torch.Tensor] = None, stream=None):
         rows = self.W_r.shape[0]
         gemv_f32(self.W_r, rows, self.d, x, x.stride(0), self.logits, self.ls, nt, stream,
                  bias=bias, bias_stride=0 if bias is None else bias.stride(0))
-        moe_route(self.logits, self.ls, self.E, self.k, self.ids, self.wts, self.sg, nt, stream)
+        self._route_logits(nt, stream)
 
     def _shared_decode(self, x, nt, stream):
         S = self.shared
@@ -245,7 +274,11 @@ class MoeLayerRunner:
         if self.shared is not None:
             self._shared_decode(x, nt, stream)
             shexp = self.sh_y
-        moe_route_gate_up(self.dev, self.logits, self.ls, self.E, self.k, self.xq, self.ids, self.wts, self.sg, self.h, nt, stream)
+        if self.router == "softmax":
+            moe_route_gate_up(self.dev, self.logits, self.ls, self.E, self.k, self.xq, self.ids, self.wts, self.sg, self.h, nt, stream)
+        else:   # the fused route + gate/up kernel routes by softmax: route first, then the gate/up GEMV by ids
+            self._route_logits(nt, stream)
+            moe_gate_up(self.dev, x, x.stride(0), self.ids, self.k, self.h, nt, stream)
         moe_down_reduce(self.dev, self.h, self.ids, self.wts, self.k, shexp, self.sg, self.out, nt, stream)
         return self.out[:nt]
 
@@ -266,7 +299,7 @@ class MoeLayerRunner:
         P = nt * k
         moe_router_q8(self.W_r, self.W_r.shape[0], self.d, x, x.stride(0), self.logits, self.ls, self.vg, self.xq, nt, stream,
                       bias=bias, bias_stride=0 if bias is None else bias.stride(0))
-        moe_route(self.logits, self.ls, self.E, self.k, self.ids, self.wts, self.sg, nt, stream)
+        self._route_logits(nt, stream)
         moe_order(self.dev, self.ids, P, self.E, self.order, self.order_n, stream, self.egrp)
         max_active = min(self.E, P)
         moe_gemm_gate_up(self.dev, self.xq, k, P, self.order, self.order_n, self.egrp, max_active, self.h, stream)

@@ -127,6 +127,18 @@ int hy_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, floa
    (replaces moe_route, src/kernels4.cuh:48 / src/kernels4.cu:1925-1935).  n_expert <= 1024, k <= 64. */
 int hy_moe_route(const float *logits, int ls, int n_expert, int k, int32_t *ids, float *wts, float *sg, int nt, hipStream_t s);
 
+/* Sigmoid router with a selection bias (replaces moe_route_sig, src/kernels5.cuh:74 / src/kernels5.cu:1090-1122,
+   :1291-1295): p = 1 / (1 + exp(-logits[t][e])), the k experts with the largest p + bias[e] (ties to the lower index),
+   weights p scale / max(the selected p summed in selection order, 2^-14); sg[t] = 1 when sg is not NULL.
+   bias: n_expert floats on the device.  n_expert <= 1024, k <= 16. */
+int hy_moe_route_sig(const float *logits, int ls, const float *bias, int n_expert, int k, float scale, int32_t *ids, float *wts, float *sg,
+                     int nt, hipStream_t s);
+/* sqrt-softplus router (replaces route7, src/kernels7.cuh:75 / src/kernels7.cu:816-865, :987-990):
+   s = sqrt(softplus(logits[t][e])) with softplus(l) = l above 20, else log1p(exp(l)); the top k of s + bias[e] (ties
+   to the lower index); weights s / (the selected s summed in selection order + 1e-20) scale.  Limits as above. */
+int hy_moe_route_sqrtsp(const float *logits, int ls, const float *bias, int n_expert, int k, float scale, int32_t *ids, float *wts, int nt,
+                        hipStream_t s);
+
 /* Pairs p < n_pairs whose expert has slot >= 0, grouped by expert in ascending id, stable by pair index:
    order[], order_n[0] = their count, order_n[1] = active experts, egrp[3 i ..] = (expert, start, count)
    (replaces moe_order, src/kernels4.cuh:74-75 / src/kernels4.cu:2059-2062).  n_expert <= 1024. */

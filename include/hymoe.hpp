@@ -103,6 +103,15 @@ inline void gemv_f32(const float *W, int rows, int k, const float *x, int xs, fl
 inline void moe_route(const float *logits, int ls, int n_expert, int k, int *ids, float *wts, float *sg, int nt, hipStream_t s) {
     check(hy_moe_route(logits, ls, n_expert, k, ids, wts, sg, nt, s));
 }
+// src/kernels5.cuh:74 -- sigmoid router with a selection bias
+inline void moe_route_sig(const float *logits, int ls, const float *bias, int n_expert, int k, float scale, int *ids, float *wts,
+                          float *sg, int nt, hipStream_t s) {
+    check(hy_moe_route_sig(logits, ls, bias, n_expert, k, scale, ids, wts, sg, nt, s));
+}
+// src/kernels7.cuh:75 -- sqrt-softplus router with a selection bias
+inline void route7(const float *logits, int ls, const float *bias, int n, int k, float scale, int *ids, float *wts, int nt, hipStream_t s) {
+    check(hy_moe_route_sqrtsp(logits, ls, bias, n, k, scale, ids, wts, nt, s));
+}
 // src/kernels4.cuh:67-68
 inline void moe_gate_up(const MoeDev &m, const float *x, int xs, const int *ids, int k, float *h, int nt, hipStream_t s,
                         const int *order = nullptr, const int *order_n = nullptr) {

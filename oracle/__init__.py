@@ -60,6 +60,9 @@ def lib():
             "or_block_ints": (I, [I, P, P, I, P, P]), "or_row_dot": (F, [I, P, P, I]),
             "or_gemv_f32": (None, [P, I, I, P, I, P, I, I]),
             "or_route": (I, [P, I, I, I, I, P, P, P]),
+            "or_logf": (F, [F]), "or_log1pf": (F, [F]), "or_sigmoid": (F, [F]), "or_sqrt_softplus": (F, [F]),
+            "or_route_sig": (I, [P, I, P, I, I, F, I, P, P, P]),
+            "or_route_sqrtsp": (I, [P, I, P, I, I, F, I, P, P]),
             "or_order": (I, [P, P, I, I, P, P, P]),
             "or_moe_layer": (I, [ctypes.POINTER(or_layer), I, P, I, P, P, I, P, I, ctypes.POINTER(or_layer), P, P, P, I]),
             "or_expert_ffn": (I, [ctypes.POINTER(or_layer), I, I, P, I, P, P, I]),
@@ -150,6 +153,28 @@ def route(logits, ne, k, with_sg=False):
     if lib().or_route(_p(logits), ls, ne, k, nt, _p(ids), _p(wts), _p(sg)):
         raise ValueError("or_route failed")
     return ids, wts, sg
+
+
+def route_sig(logits, bias, ne, k, scale):
+    """sigmoid router with selection bias (src/kernels5.cu:1090-1122): ids, wts, sg (all ones)"""
+    logits = _c(np.atleast_2d(logits), np.float32)
+    bias = _c(bias, np.float32)
+    nt, ls = logits.shape
+    ids, wts, sg = np.zeros((nt, k), np.int32), np.zeros((nt, k), np.float32), np.zeros(nt, np.float32)
+    if lib().or_route_sig(_p(logits), ls, _p(bias), ne, k, float(scale), nt, _p(ids), _p(wts), _p(sg)):
+        raise ValueError("or_route_sig failed")
+    return ids, wts, sg
+
+
+def route_sqrtsp(logits, bias, ne, k, scale):
+    """sqrt-softplus router (src/kernels7.cu:816-865): ids, wts"""
+    logits = _c(np.atleast_2d(logits), np.float32)
+    bias = _c(bias, np.float32)
+    nt, ls = logits.shape
+    ids, wts = np.zeros((nt, k), np.int32), np.zeros((nt, k), np.float32)
+    if lib().or_route_sqrtsp(_p(logits), ls, _p(bias), ne, k, float(scale), nt, _p(ids), _p(wts)):
+        raise ValueError("or_route_sqrtsp failed")
+    return ids, wts
 
 
 def order(slot, ids, ne):

@@ -435,6 +435,104 @@ int or_route(const float *logits, int ls, int ne, int k, int nt, int32_t *ids, f
     return 0;
 }
 
+/* log(x) for x > 0: x = 2^e m with m in [sqrt(1/2), sqrt(2)), log(m) by the Cephes single-precision polynomial in
+   f = m - 1 (S. L. Moshier, Cephes Math Library, logf.c) evaluated with fmaf, e ln2 added as e C2 + e C1 with
+   C1 = 0.693359375 exact in 9 bits (the same split as or_expf).  Subnormal x is scaled by 2^23 first. */
+float or_logf(float x) {
+    if (x != x || x < 0.0f) return NAN;
+    if (x == 0.0f) return -INFINITY;
+    if (isinf(x)) return x;
+    int e = 0;
+    if (x < 1.17549435e-38f) { x = x * 8388608.0f; e = -23; }
+    uint32_t b;
+    memcpy(&b, &x, 4);
+    e += (int) ((b >> 23) & 0xffu) - 126;   /* x = 2^e m, m in [0.5, 1) */
+    const uint32_t mb = (b & 0x007fffffu) | 0x3f000000u;
+    float m;
+    memcpy(&m, &mb, 4);
+    float f;
+    if (m < 0.70710678118654752f) { e -= 1; f = m + m - 1.0f; } else { f = m - 1.0f; }
+    const float z = f * f;
+    float y = 7.0376836292e-2f;
+    y = fmaf(y, f, -1.1514610310e-1f);
+    y = fmaf(y, f, 1.1676998740e-1f);
+    y = fmaf(y, f, -1.2420140846e-1f);
+    y = fmaf(y, f, 1.4249322787e-1f);
+    y = fmaf(y, f, -1.6668057665e-1f);
+    y = fmaf(y, f, 2.0000714765e-1f);
+    y = fmaf(y, f, -2.4999993993e-1f);
+    y = fmaf(y, f, 3.3333331174e-1f);
+    y = (y * f) * z;
+    const float fe = (float) e;
+    y = fmaf(fe, -2.12194440e-4f, y);
+    y = fmaf(-0.5f, z, y);
+    return fmaf(fe, 0.693359375f, f + y);
+}
+/* log(1 + x), x >= -1: u = 1 + x rounded, then log(u) x / (u - 1) (D. Goldberg, "What every computer scientist should
+   know about floating-point arithmetic", 1991, theorem 4), which cancels the rounding of u; x itself when u == 1 */
+float or_log1pf(float x) {
+    if (x != x) return x;
+    const float u = 1.0f + x;
+    if (u == 1.0f) return x;
+    if (isinf(u)) return u;
+    return or_logf(u) * (x / (u - 1.0f));
+}
+/* the routers' scores: sigmoid 1 / (1 + exp(-l)) (src/kernels5.cu:35) and sqrt(softplus(l)) with softplus(l) = l
+   above 20, else log1p(exp(l)) (src/kernels7.cu:823-826) */
+float or_sigmoid(float l) { return 1.0f / (1.0f + or_expf(-l)); }
+float or_sqrt_softplus(float l) { return sqrtf(l > 20.0f ? l : or_log1pf(or_expf(l))); }
+
+/* top k of key (descending, ties to the lower index) -> ids; val of the selected summed in selection order */
+static float topk_by_key(const float *key, const float *val, int ne, int k, unsigned char *used, int32_t *ids) {
+    memset(used, 0, (size_t) ne);
+    float tot = 0.0f;
+    for (int j = 0; j < k; ++j) {
+        int bi = -1;
+        for (int e = 0; e < ne; ++e)
+            if (!used[e] && (bi < 0 || key[e] > key[bi])) bi = e;   /* strict >: ties keep the lower index */
+        used[bi] = 1;
+        ids[j] = bi;
+        tot = tot + val[bi];
+    }
+    return tot;
+}
+/* the sigmoid router with a selection bias (src/kernels5.cu:1090-1122): p = sigmoid(l), the top k of p + bias[e],
+   weights p scale / max(sum of the selected p, 2^-14), sg = 1 */
+int or_route_sig(const float *logits, int ls, const float *bias, int ne, int k, float scale, int nt, int32_t *ids, float *wts, float *sg) {
+    if (ne <= 0 || k <= 0 || k > ne || ls < ne) return -1;
+    float *p = (float *) malloc(sizeof(float) * ne), *key = (float *) malloc(sizeof(float) * ne);
+    unsigned char *used = (unsigned char *) malloc((size_t) ne);
+    if (!p || !key || !used) { free(p); free(key); free(used); return -1; }
+    for (int t = 0; t < nt; ++t) {
+        const float *l = logits + (size_t) t * ls;
+        for (int e = 0; e < ne; ++e) { p[e] = or_sigmoid(l[e]); key[e] = p[e] + bias[e]; }
+        int32_t *id = ids + (size_t) t * k;
+        const float tot = topk_by_key(key, p, ne, k, used, id);
+        const float inv = scale / fmaxf(tot, 6.103515625e-5f);
+        for (int j = 0; j < k; ++j) wts[(size_t) t * k + j] = p[id[j]] * inv;
+        if (sg) sg[t] = 1.0f;
+    }
+    free(p); free(key); free(used);
+    return 0;
+}
+/* the sqrt-softplus router (src/kernels7.cu:816-865): s = sqrt(softplus(l)), the top k of s + bias[e], weights
+   s / (sum of the selected s + 1e-20) scale */
+int or_route_sqrtsp(const float *logits, int ls, const float *bias, int ne, int k, float scale, int nt, int32_t *ids, float *wts) {
+    if (ne <= 0 || k <= 0 || k > ne || ls < ne) return -1;
+    float *sc = (float *) malloc(sizeof(float) * ne), *key = (float *) malloc(sizeof(float) * ne);
+    unsigned char *used = (unsigned char *) malloc((size_t) ne);
+    if (!sc || !key || !used) { free(sc); free(key); free(used); return -1; }
+    for (int t = 0; t < nt; ++t) {
+        const float *l = logits + (size_t) t * ls;
+        for (int e = 0; e < ne; ++e) { sc[e] = or_sqrt_softplus(l[e]); key[e] = sc[e] + bias[e]; }
+        int32_t *id = ids + (size_t) t * k;
+        const float tot = topk_by_key(key, sc, ne, k, used, id);
+        for (int j = 0; j < k; ++j) wts[(size_t) t * k + j] = sc[id[j]] / (tot + 1e-20f) * scale;
+    }
+    free(sc); free(key); free(used);
+    return 0;
+}
+
 /* ------------------------------------------------------------------ bucketing */
 
 int or_order(const int32_t *slot, const int32_t *ids, int n_pairs, int ne, int32_t *order, int32_t *order_n, int32_t *egrp) {

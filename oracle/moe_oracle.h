@@ -72,6 +72,15 @@ float or_row_dot(int type, const uint8_t *row, const void *xq, int n);
 void or_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt);
 /* softmax top-k routing (src/kernels4.cu:297-344): ids/wts [nt][k]; sg[t] = sigmoid(logits[t][ne]) if sg */
 int or_route(const float *logits, int ls, int ne, int k, int nt, int32_t *ids, float *wts, float *sg);
+/* log and log1p (Cephes logf polynomial; Goldberg's log1p correction), the routers' scores */
+float or_logf(float x);
+float or_log1pf(float x);
+float or_sigmoid(float l);
+float or_sqrt_softplus(float l);
+/* sigmoid router with selection bias (src/kernels5.cu:1090-1122) and sqrt-softplus router (src/kernels7.cu:816-865):
+   top k of score + bias[e] (ties to the lower index); weights from the scores alone */
+int or_route_sig(const float *logits, int ls, const float *bias, int ne, int k, float scale, int nt, int32_t *ids, float *wts, float *sg);
+int or_route_sqrtsp(const float *logits, int ls, const float *bias, int ne, int k, float scale, int nt, int32_t *ids, float *wts);
 /* bucketing: pairs with slot[ids[p]] >= 0 grouped by expert, stable by pair index
    (src/kernels4.cu:1275-1295, src/cpu_moe.cpp:672-687); egrp may be NULL */
 int or_order(const int32_t *slot, const int32_t *ids, int n_pairs, int ne, int32_t *order, int32_t *order_n, int32_t *egrp);
