@@ -83,7 +83,9 @@ SIGNATURES = {
     "hy_moe_gemm_gate_up": (_I, [_DEV, _P, _I, _I, _P, _P, _P, _I, _P, _P]),
     "hy_moe_gemm_down": (_I, [_DEV, _P, _I, _P, _P, _P, _I, _P, _P, _P]),
     "hy_moe_reduce": (_I, [_P, _P, _P, _I, _P, _I, _I, _P, _P]),
+    "hy_moe_reduce_residual": (_I, [_P, _P, _P, _I, _P, _I, _I, _P, _P]),
     "hy_moe_down_reduce": (_I, [_DEV, _P, _P, _P, _I, _P, _P, _P, _I, _P]),
+    "hy_moe_down_reduce_residual": (_I, [_DEV, _P, _P, _P, _I, _P, _P, _P, _I, _P]),
     "hy_moe_router_q8": (_I, [_P, _I, _I, _P, _I, _P, _I, _P, _I, _I, _P, _I, _P]),
     "hy_moe_route_gate_up": (_I, [_DEV, _P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
     "hy_dequant_row": (_I, [_I, _P, _I, _P, _P]),

@@ -221,6 +221,11 @@ int hy_moe_reduce(const float *shexp, const float *sg, const float *y, int k, fl
     if (!y || !out || !ids || k <= 0 || k > 64 || n <= 0 || nt < 0) { set_error("hy_moe_reduce: bad argument"); return HY_EINVAL; }
     return launch_reduce(shexp, sg, y, k, out, n, nt, ids, s);
 }
+int hy_moe_reduce_residual(const float *shexp, const float *sg, const float *y, int k, float *resid, int n, int nt, const int32_t *ids,
+                           hipStream_t s) {
+    if (!y || !resid || !ids || k <= 0 || k > 64 || n <= 0 || nt < 0) { set_error("hy_moe_reduce_residual: bad argument"); return HY_EINVAL; }
+    return launch_reduce(shexp, sg, y, k, resid, n, nt, ids, s, 1);
+}
 
 int hy_moe_down_reduce(const hy_moe_dev *m, const float *h, const int32_t *ids, const float *wts, int k, const float *shexp, const float *sg,
                        float *out, int nt, hipStream_t s) {
@@ -231,6 +236,16 @@ int hy_moe_down_reduce(const hy_moe_dev *m, const float *h, const int32_t *ids, 
     rc = launch_dec_down(*m, h, ids, wts, k, shexp, sg, out, nt, s);
     if (rc != HY_EUNSUPPORTED_TYPE) return rc;
     return launch_down_reduce(*m, h, ids, wts, k, shexp, sg, out, nt, s);   // shapes beyond the fused kernel's LDS budget
+}
+int hy_moe_down_reduce_residual(const hy_moe_dev *m, const float *h, const int32_t *ids, const float *wts, int k, const float *shexp,
+                                const float *sg, float *resid, int nt, hipStream_t s) {
+    int rc = check_dev(m, "hy_moe_down_reduce_residual", false, true);
+    if (rc) return rc;
+    if (!h || !ids || !wts || !resid || k <= 0 || k > 64 || nt < 0) { set_error("hy_moe_down_reduce_residual: bad argument"); return HY_EINVAL; }
+    if (!aligned16(h)) { set_error("hy_moe_down_reduce_residual: h must be 16-byte aligned"); return HY_EBAD_SHAPE; }
+    rc = launch_dec_down(*m, h, ids, wts, k, shexp, sg, resid, nt, s, 1);
+    if (rc != HY_EUNSUPPORTED_TYPE) return rc;
+    return launch_down_reduce(*m, h, ids, wts, k, shexp, sg, resid, nt, s, 1);
 }
 
 int hy_moe_router_q8(const float *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride, float *logits,

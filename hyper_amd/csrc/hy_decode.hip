@@ -245,7 +245,7 @@ constexpr int DEC_DN_HQ = 32768;      // LDS bytes for the token's k quantized h
 template <int T, int NP>
 __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, const float *__restrict__ h, const int *__restrict__ ids,
                                                                const float *__restrict__ wts, int k, const float *__restrict__ shexp,
-                                                               const float *__restrict__ sg, float *__restrict__ out) {
+                                                               const float *__restrict__ sg, float *__restrict__ out, int res) {
     constexpr int VT = vec_dot_type(T), BE = block_elems(T);
     constexpr int SPAN_W = 256 / BE * block_bytes(T);
     constexpr int SPAN_Y = VT == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
@@ -391,7 +391,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
         const float v = readlane_f(fo, __builtin_amdgcn_readlane(ordl, r));
         if (first) { acc = v; first = false; } else acc = acc + v;
     }
-    if (lane == 0) out[(size_t) t * n + row] = acc;
+    if (lane == 0) out[(size_t) t * n + row] = res ? out[(size_t) t * n + row] + acc : acc;   // res: the residual add
 }
 
 // ---------------------------------------------------------------- launchers
@@ -445,7 +445,7 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
 
 // the fused decode down + combine; shapes beyond its LDS budget return HY_EUNSUPPORTED_TYPE (caller falls back)
 int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp, const float *sg,
-                    float *out, int nt, hipStream_t s) {
+                    float *out, int nt, hipStream_t s, int res) {
     const int vt = vec_dot_type(m.td), ng = m.ff / 256, nb = m.ff / block_elems(m.td);
     const int span_y = vt == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
     if (k > 64 || k * nb > DEC_DN_TV || (size_t) k * ng * span_y > (size_t) DEC_DN_HQ || m.n_expert > 2 * 64 * DEC_DN_WAVES)
@@ -453,7 +453,7 @@ int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const f
     if (nt == 0) return HY_OK;
     dim3 grid((m.n + DEC_DN_WAVES - 1) / DEC_DN_WAVES, nt);
     const int np = (k * ng + 7) / 8;   // passes of 8 items (more than 8: rounds)
-#define HY_DN(NN) hipLaunchKernelGGL((k_dec_down<TT, NN>), grid, dim3(64 * DEC_DN_WAVES), 0, s, m, h, ids, wts, k, shexp, sg, out)
+#define HY_DN(NN) hipLaunchKernelGGL((k_dec_down<TT, NN>), grid, dim3(64 * DEC_DN_WAVES), 0, s, m, h, ids, wts, k, shexp, sg, out, res)
     HY_DEC_SWITCH(m.td, {
         if (np <= 2) HY_DN(2); else if (np <= 4) HY_DN(4); else HY_DN(8);
         return check_launch("hy_moe_down_reduce");

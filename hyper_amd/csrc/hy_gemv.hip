@@ -177,7 +177,7 @@ int launch_down(const hy_moe_dev &m, const float *h, const int *ids, const float
 // thread sums VW consecutive columns per pass (VW = 4: 16-byte loads when n and the rows allow it).
 template <int VW>
 __global__ __launch_bounds__(256) void k_reduce(const float *__restrict__ shexp, const float *__restrict__ sg, const float *__restrict__ y,
-                                                int k, float *__restrict__ out, int n, const int *__restrict__ ids) {
+                                                int k, float *__restrict__ out, int n, const int *__restrict__ ids, int res) {
     __shared__ int ord[64];
     __shared__ int s_cnt;
     const int t = blockIdx.x, tid = threadIdx.x;
@@ -213,15 +213,19 @@ __global__ __launch_bounds__(256) void k_reduce(const float *__restrict__ shexp,
             for (int j = 0; j < VW; ++j) acc[j] = first ? v[j] : acc[j] + v[j];
             first = false;
         }
+        if (res) {   // the residual add: out (the residual) + the part, as a separate rounding
+            if constexpr (VW == 4) { const float4 o = *(const float4 *) (out + (size_t) t * n + r); acc[0] = o.x + acc[0]; acc[1] = o.y + acc[1]; acc[2] = o.z + acc[2]; acc[3] = o.w + acc[3]; }
+            else acc[0] = out[(size_t) t * n + r] + acc[0];
+        }
         if constexpr (VW == 4) *(float4 *) (out + (size_t) t * n + r) = make_float4(acc[0], acc[1], acc[2], acc[3]);
         else out[(size_t) t * n + r] = acc[0];
     }
 }
-int launch_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int *ids, hipStream_t s) {
+int launch_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int *ids, hipStream_t s, int res) {
     if (nt == 0) return HY_OK;
     const bool vec = n % 4 == 0 && ((uintptr_t) y & 15) == 0 && ((uintptr_t) out & 15) == 0 && ((uintptr_t) shexp & 15) == 0;
-    if (vec) hipLaunchKernelGGL(k_reduce<4>, dim3(nt), dim3(256), 0, s, shexp, sg, y, k, out, n, ids);
-    else hipLaunchKernelGGL(k_reduce<1>, dim3(nt), dim3(256), 0, s, shexp, sg, y, k, out, n, ids);
+    if (vec) hipLaunchKernelGGL(k_reduce<4>, dim3(nt), dim3(256), 0, s, shexp, sg, y, k, out, n, ids, res);
+    else hipLaunchKernelGGL(k_reduce<1>, dim3(nt), dim3(256), 0, s, shexp, sg, y, k, out, n, ids, res);
     return check_launch("hy_moe_reduce");
 }
 
@@ -231,7 +235,7 @@ int launch_reduce(const float *shexp, const float *sg, const float *y, int k, fl
 template <int T>
 __global__ __launch_bounds__(256) void k_down_reduce(hy_moe_dev m, int n_expert, const float *__restrict__ h, const int *__restrict__ ids,
                                                      int k, const float *__restrict__ wts, const float *__restrict__ shexp,
-                                                     const float *__restrict__ sg, float *__restrict__ out, int R) {
+                                                     const float *__restrict__ sg, float *__restrict__ out, int R, int res) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int VT = vec_dot_type(T), BE = block_elems(T);
     const int t = blockIdx.x, in_dim = m.ff, rows = m.n;
@@ -315,13 +319,13 @@ __global__ __launch_bounds__(256) void k_down_reduce(hy_moe_dev m, int n_expert,
             const float v = wts[t * k + j] * fo[j * R + f];
             if (first) { acc = v; first = false; } else acc = acc + v;
         }
-        out[(size_t) t * rows + r0 + f] = acc;
+        out[(size_t) t * rows + r0 + f] = res ? out[(size_t) t * rows + r0 + f] + acc : acc;
     }
 }
 
 template <int T>
 static int launch_down_reduce_t(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp,
-                                const float *sg, float *out, int nt, hipStream_t s) {
+                                const float *sg, float *out, int nt, hipStream_t s, int res) {
     constexpr int VT = vec_dot_type(T), BE = block_elems(T);
     const int in_dim = m.ff, rows = m.n, ng = in_dim / 256, nb = in_dim / BE;
     int R = 32 * GEMV_MAXI / (k * ng);
@@ -332,12 +336,12 @@ static int launch_down_reduce_t(const hy_moe_dev &m, const float *h, const int *
     if (lds > 64 * 1024) { set_error("hy_moe_down_reduce: %zu bytes of LDS needed", lds); return HY_EBAD_SHAPE; }
     if (nt == 0) return HY_OK;
     dim3 grid(nt, (rows + R - 1) / R);
-    hipLaunchKernelGGL((k_down_reduce<T>), grid, dim3(256), lds, s, m, m.n_expert, h, ids, k, wts, shexp, sg, out, R);
+    hipLaunchKernelGGL((k_down_reduce<T>), grid, dim3(256), lds, s, m, m.n_expert, h, ids, k, wts, shexp, sg, out, R, res);
     return check_launch("hy_moe_down_reduce");
 }
 int launch_down_reduce(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp, const float *sg,
-                       float *out, int nt, hipStream_t s) {
-    HY_TYPE_SWITCH(m.td, return (launch_down_reduce_t<TT>(m, h, ids, wts, k, shexp, sg, out, nt, s)));
+                       float *out, int nt, hipStream_t s, int res) {
+    HY_TYPE_SWITCH(m.td, return (launch_down_reduce_t<TT>(m, h, ids, wts, k, shexp, sg, out, nt, s, res)));
 }
 
 // ---------------------------------------------------------------- test hooks

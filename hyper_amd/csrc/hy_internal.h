@@ -23,8 +23,9 @@ int launch_gate_up(const hy_moe_dev &m, const float *x, int xs, const int *ids, 
 int launch_down(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, float *y, int nt, hipStream_t s,
                 const int *order, const int *order_n);
 int launch_down_reduce(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp, const float *sg,
-                       float *out, int nt, hipStream_t s);
-int launch_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int *ids, hipStream_t s);
+                       float *out, int nt, hipStream_t s, int res = 0);
+int launch_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int *ids, hipStream_t s,
+                  int res = 0);
 int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs, const int *order, const int *order_n, const int *egrp,
                         int max_active, float *h, hipStream_t s);
 int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int *order, const int *order_n, const int *egrp, int max_active,
@@ -34,7 +35,7 @@ int launch_router_q8(const float *W, int rows, int kdim, const float *x, int xs,
 int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int ne, int k, const void *xq, int *ids, float *wts, float *sg,
                          float *h, int nt, hipStream_t s);
 int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp, const float *sg,
-                    float *out, int nt, hipStream_t s);
+                    float *out, int nt, hipStream_t s, int res = 0);
 int launch_dequant_row(int type, const uint8_t *row, int n, float *out, hipStream_t s);
 int launch_block_ints(int type, const uint8_t *rows, size_t row_bytes, int nrows, const void *xq, int n, int *sumi, int *summ,
                       hipStream_t s);

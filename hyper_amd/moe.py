@@ -152,6 +152,15 @@ def moe_down_reduce(m: MoeDev, h, ids, wts, k, shexp, sg, out, nt, stream=None):
     check(lib().hy_moe_down_reduce(m.ref, _p(h), _p(ids), _p(wts), k, _p(shexp), _p(sg), _p(out), nt, _s(stream)))
 
 
+def moe_reduce_residual(shexp, sg, y, k, resid, n, nt, ids, stream=None):
+    """The combine added into the residual in place (resid += sg shexp + the token's y rows)."""
+    check(lib().hy_moe_reduce_residual(_p(shexp), _p(sg), _p(y), k, _p(resid), n, nt, _p(ids), _s(stream)))
+
+
+def moe_down_reduce_residual(m: MoeDev, h, ids, wts, k, shexp, sg, resid, nt, stream=None):
+    check(lib().hy_moe_down_reduce_residual(m.ref, _p(h), _p(ids), _p(wts), k, _p(shexp), _p(sg), _p(resid), nt, _s(stream)))
+
+
 def moe_router_q8(W_r, rows, kdim, x, xs, logits, ls, vtype, xq, nt, stream=None, bias=None, bias_stride=0):
     """gemv_f32 and the Q8 rows of x in one launch."""
     check(lib().hy_moe_router_q8(_p(W_r), rows, kdim, _p(x), xs, _p(bias), bias_stride, _p(logits), ls, int(vtype), _p(xq), nt,
@@ -265,8 +274,9 @@ class MoeLayerRunner:
         q8_quantize(vec_dot_type(S.td), self.sh_h, S.layer.ff, S.layer.ff, nt, self.sh_hq, stream)
         moe_gemm_down(S, self.sh_hq, nt, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_ones, self.sh_y, stream)
 
-    def decode(self, x: torch.Tensor, bias=None, stream=None) -> torch.Tensor:
-        """Decode / short verify: router + Q8 of x, route + gate/up, down + combine (two more for a shared expert)."""
+    def decode(self, x: torch.Tensor, bias=None, stream=None, resid: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Decode / short verify: router + Q8 of x, route + gate/up, down + combine (two more for a shared expert).
+        With `resid` ([nt, d] fp32) the combine is added into it in place and resid is returned."""
         nt = x.shape[0]
         moe_router_q8(self.W_r, self.W_r.shape[0], self.d, x, x.stride(0), self.logits, self.ls, self.vg, self.xq, nt, stream,
                       bias=bias, bias_stride=0 if bias is None else bias.stride(0))
@@ -279,6 +289,9 @@ class MoeLayerRunner:
         else:   # the fused route + gate/up kernel routes by softmax: route first, then the gate/up GEMV by ids
             self._route_logits(nt, stream)
             moe_gate_up(self.dev, x, x.stride(0), self.ids, self.k, self.h, nt, stream)
+        if resid is not None:
+            moe_down_reduce_residual(self.dev, self.h, self.ids, self.wts, self.k, shexp, self.sg, resid, nt, stream)
+            return resid[:nt]
         moe_down_reduce(self.dev, self.h, self.ids, self.wts, self.k, shexp, self.sg, self.out, nt, stream)
         return self.out[:nt]
 
@@ -294,7 +307,8 @@ class MoeLayerRunner:
         moe_down_reduce(self.dev, self.h, self.ids, self.wts, self.k, shexp, self.sg, self.out, nt, stream)
         return self.out[:nt]
 
-    def prefill(self, x: torch.Tensor, bias=None, stream=None, shared_ready=False) -> torch.Tensor:
+    def prefill(self, x: torch.Tensor, bias=None, stream=None, shared_ready=False, resid: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Prefill: the grouped GEMM path.  With `resid` ([nt, d] fp32) the combine is added into it in place."""
         nt, k = x.shape[0], self.k
         P = nt * k
         moe_router_q8(self.W_r, self.W_r.shape[0], self.d, x, x.stride(0), self.logits, self.ls, self.vg, self.xq, nt, stream,
@@ -309,5 +323,8 @@ class MoeLayerRunner:
         if self.shared is not None:
             self._shared_prefill(x, nt, stream)
             shexp = self.sh_y
+        if resid is not None:
+            moe_reduce_residual(shexp, self.sg, self.y, k, resid, self.d, nt, self.ids, stream)
+            return resid[:nt]
         moe_reduce(shexp, self.sg, self.y, k, self.out, self.d, nt, self.ids, stream)
         return self.out[:nt]

@@ -176,12 +176,20 @@ int hy_moe_gemm_down(const hy_moe_dev *m, const void *hq, int n_pairs, const int
    (replaces moe_reduce, src/kernels4.cuh:88-91 / src/kernels4.cu:1182-1206, single device, no CPU owner). */
 int hy_moe_reduce(const float *shexp, const float *sg, const float *y, int k, float *out, int n, int nt, const int32_t *ids,
                   hipStream_t s);
+/* The combine written straight into the residual (the next row after moe_reduce, src/kernels4.cu:1182-1206: on one GPU
+   the engine adds the reduced part to the residual, src/engine4.cu:887-895): resid[t][r] = resid[t][r] + part, part
+   formed exactly as hy_moe_reduce forms out, then one fp32 addition. */
+int hy_moe_reduce_residual(const float *shexp, const float *sg, const float *y, int k, float *resid, int n, int nt, const int32_t *ids,
+                           hipStream_t s);
 
 /* Decode down + combine in one launch: out[t][r] as hy_moe_reduce of hy_moe_down's y, without materialising y;
    pairs whose expert is not local (or whose id is out of range) are left out of the sum
    (fuses src/kernels4.cu:2007-2022 with :1182-1206). */
 int hy_moe_down_reduce(const hy_moe_dev *m, const float *h, const int32_t *ids, const float *wts, int k, const float *shexp,
                        const float *sg, float *out, int nt, hipStream_t s);
+/* Decode: hy_moe_down_reduce with the result added into the residual (resid[t][r] = resid[t][r] + out[t][r]), one launch. */
+int hy_moe_down_reduce_residual(const hy_moe_dev *m, const float *h, const int32_t *ids, const float *wts, int k, const float *shexp,
+                                const float *sg, float *resid, int nt, hipStream_t s);
 
 /* Router logits and the Q8 rows of x in one launch: logits as hy_gemv_f32 (rows of W_r, stride ls >= rows) and xq as
    hy_q8_quantize(vtype, x, xs, kdim, nt) -- fuses gemv_f32 (src/kernels4.cu:1910-1913) with the activation

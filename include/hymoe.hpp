@@ -145,6 +145,15 @@ inline void moe_reduce(const float *shexp, const float *sg, const float *y, int 
                        hipStream_t s) {
     check(hy_moe_reduce(shexp, sg, y, k, out, n, nt, ids, s));
 }
+// the combine added into the residual in place (moe_reduce, then the engine's residual add, src/engine4.cu:887-895)
+inline void moe_reduce_residual(const float *shexp, const float *sg, const float *y, int k, float *resid, int n, int nt, const int *ids,
+                                hipStream_t s) {
+    check(hy_moe_reduce_residual(shexp, sg, y, k, resid, n, nt, ids, s));
+}
+inline void moe_down_reduce_residual(const MoeDev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp,
+                                     const float *sg, float *resid, int nt, hipStream_t s) {
+    check(hy_moe_down_reduce_residual(&m, h, ids, wts, k, shexp, sg, resid, nt, s));
+}
 inline void moe_down_reduce(const MoeDev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp,
                             const float *sg, float *out, int nt, hipStream_t s) {
     check(hy_moe_down_reduce(&m, h, ids, wts, k, shexp, sg, out, nt, s));
