@@ -471,8 +471,13 @@ __host__ __device__ constexpr int xcd_gcd8(int n) { return (n & 7) == 0 ? 8 : (n
 
 template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
+// floor(p / a) as a multiply-high, with a_mul = ceil(2^32 / a): exact while p * (a_mul * a - 2^32) < 2^32, which
+// p * a < 2^32 guarantees (the launchers check it)
+__device__ __forceinline__ uint32_t div_by_mul(uint32_t p, uint64_t a_mul) { return (uint32_t) (((uint64_t) p * a_mul) >> 32); }
+static inline uint64_t div_mul_of(int a) { return ((1ull << 32) + (uint64_t) a - 1) / (uint64_t) a; }
+
 template <int T, bool GU, int W, int B>
-__global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const uint8_t *__restrict__ aq, int a_div, const int *__restrict__ order,
+__global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const uint8_t *__restrict__ aq, uint64_t a_mul, const int *__restrict__ order,
                                                         const int *__restrict__ order_n, const int *__restrict__ egrp, const float *__restrict__ wts,
                                                         float *__restrict__ out) {
     static_assert(T != IQ4_NL, "IQ4_NL runs k_gemm_nl");
@@ -590,11 +595,11 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
                 for (int i = 0; i < C::NA; ++i) {
                     const int t = C::TPW * wave + 4 * i + (lane >> 4);
                     const int pr = t < ntok ? s_pair[it][t] : p0;
-                    aoff[i] = (uint32_t) (GU ? pr / a_div : pr) * (uint32_t) arow + 4 + 16 * ((lane & 15) ^ (t & 15));
+                    aoff[i] = (GU ? div_by_mul((uint32_t) pr, a_mul) : (uint32_t) pr) * (uint32_t) arow + 4 + 16 * ((lane & 15) ^ (t & 15));
                 }
                 const int td = C::TPW * wave + (lane & (C::TPW - 1));
                 const int prd = td < ntok ? s_pair[it][td] : p0;
-                doff = (uint32_t) (GU ? prd / a_div : prd) * (uint32_t) arow;
+                doff = (GU ? div_by_mul((uint32_t) prd, a_mul) : (uint32_t) prd) * (uint32_t) arow;
             }
             const int stage = iss_stage;
             const uint8_t *wsrc = Wmat + (size_t) __builtin_amdgcn_readfirstlane(s_item[it][2]) * mbytes + (size_t) b * C::TB;
@@ -973,11 +978,12 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
         return check_launch("hy_moe_gemm_gate_up");
     }
     if ((size_t) n_pairs * (m.n / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_gate_up: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
+    if (k <= 0 || (uint64_t) n_pairs * (uint64_t) k >= (1ull << 32)) { set_error("hy_moe_gemm_gate_up: k out of range for the pair count"); return HY_EBAD_SHAPE; }
     HY_GEMM_SWITCH(m.tg, {
         constexpr int W = 8, B = g5_blocks<TT, true>();
         const int rb = m.ff / (8 * W);   // 8 W output rows a block
         dim3 grid(rb, item_slots(rb, n_pairs, max_active, B));
-        hipLaunchKernelGGL((k_gemm<TT, true, W, B>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
+        hipLaunchKernelGGL((k_gemm<TT, true, W, B>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) xq, div_mul_of(k), order, order_n, egrp, nullptr, h);
         return check_launch("hy_moe_gemm_gate_up");
     });
 }
@@ -995,7 +1001,7 @@ int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int
         constexpr int W = TT == Q6_K ? 16 : 8, B = g5_blocks<TT, false>();   // Q6_K: 16 waves (fits 128 registers)
         const int rb = m.n / (16 * W);   // 16 W output rows a block
         dim3 grid(rb, item_slots(rb, n_pairs, max_active, B));
-        hipLaunchKernelGGL((k_gemm<TT, false, W, B>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
+        hipLaunchKernelGGL((k_gemm<TT, false, W, B>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) hq, div_mul_of(1), order, order_n, egrp, wts, y);
         return check_launch("hy_moe_gemm_down");
     });
 }
