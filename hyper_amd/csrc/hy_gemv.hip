@@ -195,7 +195,7 @@ __global__ __launch_bounds__(256) void k_reduce(const float *__restrict__ shexp,
     __syncthreads();
     const int c = s_cnt;
     const float g = shexp ? (sg ? sg[t] : 1.0f) : 0.0f;
-    for (int r = VW * tid; r < n; r += VW * 256) {
+    for (int r = VW * tid; r < n; r += VW * (int) blockDim.x) {
         float acc[VW] = {}, v[VW];   // a token with no shared expert and no valid pair gets zeros
         bool first = true;
         if (shexp) {
@@ -205,13 +205,24 @@ __global__ __launch_bounds__(256) void k_reduce(const float *__restrict__ shexp,
             for (int j = 0; j < VW; ++j) acc[j] = g * v[j];
             first = false;
         }
-        for (int i = 0; i < c; ++i) {
-            const float *yp = y + ((size_t) t * k + ord[i]) * n + r;
-            if constexpr (VW == 4) { const float4 x = *(const float4 *) yp; v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w; }
-            else v[0] = *yp;
+        // the pairs' rows in batches of 8 whose loads are all in flight before the first add; the adds keep the
+        // ascending expert-id order
+        for (int i0 = 0; i0 < c; i0 += 8) {
+            float b[8][VW];
 #pragma unroll
-            for (int j = 0; j < VW; ++j) acc[j] = first ? v[j] : acc[j] + v[j];
-            first = false;
+            for (int u = 0; u < 8; ++u)
+                if (i0 + u < c) {
+                    const float *yp = y + ((size_t) t * k + ord[i0 + u]) * n + r;
+                    if constexpr (VW == 4) { const float4 x = *(const float4 *) yp; b[u][0] = x.x; b[u][1] = x.y; b[u][2] = x.z; b[u][3] = x.w; }
+                    else b[u][0] = *yp;
+                }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (i0 + u < c) {
+#pragma unroll
+                    for (int j = 0; j < VW; ++j) acc[j] = first ? b[u][j] : acc[j] + b[u][j];
+                    first = false;
+                }
         }
         if (res) {   // the residual add: out (the residual) + the part, as a separate rounding
             if constexpr (VW == 4) { const float4 o = *(const float4 *) (out + (size_t) t * n + r); acc[0] = o.x + acc[0]; acc[1] = o.y + acc[1]; acc[2] = o.z + acc[2]; acc[3] = o.w + acc[3]; }
