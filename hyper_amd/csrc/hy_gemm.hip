@@ -960,8 +960,9 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
 static int max_items(int n_pairs, int max_active) { return (n_pairs + GM_TOK - 1) / GM_TOK + max_active; }
 // item slots per row tile: enough blocks for about `per_cu` resident blocks on every CU
 static int item_slots(int row_tiles, int n_pairs, int max_active, int per_cu) {
-    static int cus = 0;
-    if (!cus) { int dev = 0; hipDeviceProp_t pr; if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&pr, dev) == hipSuccess) cus = pr.multiProcessorCount; if (cus <= 0) cus = 256; }
+    // the current device's CU count (an attribute query: cheap, thread-safe, and right for each device)
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     const int want = cus * per_cu / row_tiles;   // every block resident at once
     const int n = std::max(1, std::min(max_items(n_pairs, max_active), want));
     const int P = 8 / xcd_gcd8(row_tiles);       // k_gemm places consecutive items P slots apart: a multiple of P

@@ -109,12 +109,16 @@ int launch_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, 
 // and wave w computes rows 4 (w % 4) .. + 3 of tokens 8 (w / 4) .. + 7 from it.  Lane L reads the float4 at 4 L of
 // each row, so every lane's partial sums see the elements of gemv_tile in the same order.  The next step's 32 KB are
 // loaded into registers while this step's fmas run.
-constexpr int GL_R = 16, GL_T = 16, GL_THREADS = 512;
+constexpr int GL_R = 16, GL_THREADS = 512;
 typedef float f4v __attribute__((ext_vector_type(4)));
+// GT tokens a block (16, or 8 when 16-token tiles would leave CUs with fewer than two blocks); the waves are 4 row
+// groups x 2 token groups whatever GT, and lane l always takes columns 4 l .. 4 l + 3 of each 256-column step
+template <int GT>
 __device__ __forceinline__ void gemv_block_lds(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
                                                float *__restrict__ y, int ys, int nt, const float *__restrict__ bias, int bs, int r0,
-                                               int t0, f4v *st) {   // st: LDS, (GL_R + GL_T) rows of 64 float4
-    constexpr int RW = 4, TW = 8, NS = (GL_R + GL_T) * 64 / GL_THREADS;   // float4 staged by each thread per step
+                                               int t0, f4v *st) {   // st: LDS, (GL_R + GT) rows of 64 float4
+    constexpr int RW = 4, TW = GT / 2, NS = (GL_R + GT) * 64 / GL_THREADS;   // float4 staged by each thread per step
+    static_assert((GL_R + GT) * 64 % GL_THREADS == 0, "whole float4 per thread");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr0 = r0 + RW * (wave & 3), wt0 = t0 + TW * (wave >> 2);   // this wave's rows and tokens
     // the NS float4 this thread stages per step: tile row (tid + 512 k) / 64 (W rows, then x rows), column tid % 64
@@ -173,18 +177,19 @@ __device__ __forceinline__ void gemv_block_lds(const float *__restrict__ W, int 
 }
 
 // Router logits of many tokens and the Q8 rows of x in one launch: blocks [0, gemv_blocks) compute the logits (gx
-// blocks of 16 rows per 16 tokens through gemv_block_lds, or per 8 tokens through gemv_tile), the rest quantize x --
-// Q8_K: 32 blocks of 256 values per block, 16 lanes each; Q8_0: 8 pairs of 32-value blocks per block, a wave each.
-template <int VT>
-__global__ __launch_bounds__(GL_THREADS) void k_router_pre(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+// blocks of 16 rows per GT tokens through gemv_block_lds when kdim % 256 == 0 (GT 8 or 16), else per 8 tokens
+// through gemv_tile (GT 0)), the rest quantize x -- Q8_K: 32 blocks of 256 values per block, 16 lanes each; Q8_0: 8
+// pairs of 32-value blocks per block, a wave each.  The LDS variants fit two blocks a CU.
+template <int VT, int GT>
+__global__ __launch_bounds__(GL_THREADS, GT ? 4 : 2) void k_router_pre(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
                                                     const float *__restrict__ bias, int bs, float *__restrict__ y, int ys, int nt,
                                                     uint8_t *__restrict__ xq, int gx, int gemv_blocks) {
-    __shared__ f4v st[(GL_R + GL_T) * 64];
+    __shared__ f4v st[GT ? (GL_R + GT) * 64 : 1];
     const int bid = blockIdx.x;
     if (bid < gemv_blocks) {
         int bx, by;
         gemv_tile_of(bid, gx, gemv_blocks / gx, bx, by);
-        if (kdim % 256 == 0) gemv_block_lds(W, rows, kdim, x, xs, y, ys, nt, bias, bs, bx * GL_R, by * GL_T, st);
+        if constexpr (GT != 0) gemv_block_lds<GT>(W, rows, kdim, x, xs, y, ys, nt, bias, bs, bx * GL_R, by * GT, st);
         else if (threadIdx.x < 256) gemv_tile<4, 8>(W, rows, kdim, x, xs, y, ys, nt, bias, bs, (bx * 4 + (threadIdx.x >> 6)) * 4, by * 8);
         return;
     }
@@ -205,17 +210,23 @@ __global__ __launch_bounds__(GL_THREADS) void k_router_pre(const float *__restri
 int launch_router_pre(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
                       int vtype, void *xq, int nt, hipStream_t s) {
     if (nt == 0) return HY_OK;
-    // kdim % 256 == 0: 16 x 16 tiles through LDS (gemv_block_lds); else 16 rows x 8 tokens a block (gemv_tile)
-    const int gx = (rows + 15) / 16, gemv_blocks = gx * (kdim % 256 == 0 ? (nt + GL_T - 1) / GL_T : (nt + 7) / 8);
+    // kdim % 256 == 0: 16 x GT tiles through LDS (gemv_block_lds), GT = 16, or 8 when 16-token tiles number fewer
+    // than two per CU (more blocks to hide the steps' barriers); else 16 rows x 8 tokens a block (gemv_tile, GT 0)
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    const int gx = (rows + 15) / 16;
+    const int gt = kdim % 256 != 0 ? 0 : gx * ((nt + 15) / 16) < 2 * cus ? 8 : 16;
+    const int gemv_blocks = gx * ((nt + (gt ? gt : 8) - 1) / (gt ? gt : 8));
+#define HY_RP(VV, GG) hipLaunchKernelGGL((k_router_pre<VV, GG>), dim3(gemv_blocks + qblocks), dim3(GL_THREADS), 0, s, W, rows, kdim, x, xs, bias, bs, \
+                                         logits, ls, nt, (uint8_t *) xq, gx, gemv_blocks)
     if (vtype == Q8_K) {
         const int qblocks = (nt * (kdim / 256) + GL_THREADS / 16 - 1) / (GL_THREADS / 16);
-        hipLaunchKernelGGL(k_router_pre<Q8_K>, dim3(gemv_blocks + qblocks), dim3(GL_THREADS), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, nt,
-                           (uint8_t *) xq, gx, gemv_blocks);
+        if (gt == 8) HY_RP(Q8_K, 8); else if (gt == 16) HY_RP(Q8_K, 16); else HY_RP(Q8_K, 0);
     } else {
         const int qblocks = (nt * ((kdim / 32 + 1) / 2) + GL_THREADS / 64 - 1) / (GL_THREADS / 64);
-        hipLaunchKernelGGL(k_router_pre<Q8_0>, dim3(gemv_blocks + qblocks), dim3(GL_THREADS), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, nt,
-                           (uint8_t *) xq, gx, gemv_blocks);
+        if (gt == 8) HY_RP(Q8_0, 8); else if (gt == 16) HY_RP(Q8_0, 16); else HY_RP(Q8_0, 0);
     }
+#undef HY_RP
     return check_launch("hy_moe_router_q8");
 }
 

@@ -23,7 +23,9 @@ TOL = 2e-3
     (288, 4096, 4, GType.Q8_0, False, False),
     (384, 7168, 8, GType.Q8_K, True, False),
     (512, 2048, 3, GType.Q8_K, True, True),
-    (64, 512, 12, GType.Q8_0, True, False),     # more than 8 rows: the separate kernels
+    (64, 512, 12, GType.Q8_0, True, False),     # more than 8 rows: the separate kernels (8-token LDS tiles)
+    (512, 512, 256, GType.Q8_K, True, True),    # 33 x 16 16-token tiles: two a CU or more, 16-token LDS tiles
+    (64, 544, 40, GType.Q8_0, False, True),     # d % 256 != 0: the register-tile path, an odd Q8_0 block count
 ])
 def test_router_q8_bitexact(cuda, E, d, nt, vt, with_sg, with_bias):
     g = gen(1000 + E + nt)
