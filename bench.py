@@ -306,7 +306,7 @@ def main():
                     help="first run a plain copy kernel over MIB MiB (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
+        print(f"bench.py measures one GPU: hyper_amd runs the expert path on one GPU and has no multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream()

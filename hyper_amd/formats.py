@@ -119,7 +119,7 @@ def random_layer(tg, td, E: int, ff: int, n: int, seed: int, device="cpu", d_ran
     return ExpertLayer(tg, td, E, ff, n, gate, up, down, clamp)
 
 
-# ------------------------------------------------------------------ the workloads (BASELINE configurations)
+# ------------------------------------------------------------------ the workloads (the benchmarked configurations)
 
 @dataclass
 class Workload:

@@ -25,7 +25,7 @@
  *  - weighted sum per token in expert-id order: the first pair assigns w*y,
  *    later pairs add w*y (src/cpu_moe.cpp:863-874, :994-1006).
  *
- * Parity status per function is listed in the test files and DESIGN.md.
+ * Parity status per function: each function's pinning tests are named in the test files.
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off -fopenmp).
  */
 #ifndef HY_MOE_ORACLE_H

@@ -1,6 +1,6 @@
 """GPU parity of the three-launch decode path -- router + Q8 of x, route + gate/up, down + combine -- against the
 CPU oracle, through the C ABI.  Everything is compared bit for bit (the fp32 results share the oracle's
-expression order); the 2e-3 relative-L2 bound of the north star is asserted as well."""
+expression order); the 2e-3 relative-L2 bound on fp32 expert outputs is asserted as well."""
 import ctypes
 import types
 

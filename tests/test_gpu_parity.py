@@ -1,8 +1,8 @@
 """GPU parity: every kernel of the path through the C ABI against the CPU oracle on the same seeded inputs.
 
 Integer and index results (Q8 blocks, block integers, ids, order) must be identical; fp32 results are
-bit-identical under the shared numeric contract (each test also states the north star's 2e-3
-relative-L2 bound, which bit-identity implies).
+bit-identical under the shared numeric contract (each test also states the 2e-3 relative-L2
+bound on fp32 expert outputs, which bit-identity implies).
 """
 import numpy as np
 import pytest
@@ -15,7 +15,7 @@ from tests.helpers import (ALL_TYPES, D_RANGE, TYPES_256, assert_bits_equal, gen
                            x_distributions)
 
 pytestmark = pytest.mark.gpu
-TOL = 2e-3   # north star: final fp32 expert outputs within 2e-3 relative L2 of the CPU path
+TOL = 2e-3   # final fp32 expert outputs within 2e-3 relative L2 of the CPU path
 
 
 def _sync():

@@ -2,8 +2,8 @@
 and log-normal token norms) through MoeLayerRunner on the GPU: decode / verify rows through the three-launch decode,
 longer batches through the prefill path.  The layers are generated on the device at full size; the oracle checks a
 sample of the tokens on a sub-layer holding only the experts they route to (ids remapped in ascending order, so the
-combine order is unchanged).  Logits, routing and outputs are compared bit for bit; the 2e-3 relative-L2 bound of the
-north star is asserted as well."""
+combine order is unchanged).  Logits, routing and outputs are compared bit for bit; the 2e-3 relative-L2 bound on
+fp32 expert outputs is asserted as well."""
 import numpy as np
 import pytest
 import torch
