@@ -205,6 +205,9 @@ GEMM_CASES = [
     (GType.IQ2_XS, GType.IQ2_XS, 7168, 2048, 6, 8),
     (GType.IQ4_NL, GType.IQ4_NL, 4096, 1536, 8, 4),
     (GType.IQ4_NL, GType.IQ4_NL, 2048, 512, 8, 50),
+    (GType.Q4_K, GType.Q6_K, 2048, 768, 1, 100),    # k = 1: the pair is the token (reciprocal 2^32)
+    (GType.Q4_K, GType.Q6_K, 1024, 512, 3, 90),     # odd k: the pair-to-token multiply-high
+    (GType.Q4_K, GType.Q6_K, 1024, 256, 16, 12),    # k = E: every expert active, every token in each
 ]
 
 
