@@ -265,6 +265,42 @@ def test_runner_prefill_shared_matches_oracle(cuda, tg, td, E, d, ff, k, nt, sh,
     assert_bits_equal(out.cpu().numpy(), out_r, "runner.prefill")
 
 
+def test_runner_prefill_shared_graph_replays(cuda):
+    """The prefill step with a shared expert (and its sigmoid gate) captured into a HIP graph: every replay, with
+    eager work and synchronizations between them, equals the eager step and the oracle, for two inputs in turn."""
+    tg, td, E, d, ff, k, nt = GType.Q4_K, GType.Q6_K, 32, 2048, 768, 8, 48
+    L = layer(tg, td, E, ff, d, seed=920)
+    S = layer(GType.Q4_K, td, 1, ff, d, seed=921)
+    g = gen(922)
+    W_r = torch.randn(E + 1, d, generator=g) * 0.02
+    xs = [torch.randn(nt, d, generator=g) for _ in range(2)]
+    refs = []
+    for x in xs:
+        logits = orc.gemv_f32(W_r.numpy(), x.numpy())
+        ids, wts, sgv = orc.route(logits, E, k, with_sg=True)
+        refs.append(orc.moe_layer(oracle_layer(L), x.numpy(), ids, wts, shared=oracle_layer(S), sg=sgv))
+    r = moe.MoeLayerRunner(moe.upload_experts(L, device=cuda), W_r.to(cuda), k, max_rows=nt,
+                           shared=moe.upload_experts(S, device=cuda), sg_logit=True)
+    xin = torch.empty(nt, d, device=cuda)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        xin.copy_(xs[0])
+        eager = r.prefill(xin).clone()   # also the warm-up before capture
+        torch.cuda.synchronize()
+        assert_bits_equal(eager.cpu().numpy(), refs[0], "eager prefill")
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = r.prefill(xin)
+    for rep in range(4):
+        i = rep % 2
+        xin.copy_(xs[i].to(cuda))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_bits_equal(out.cpu().numpy(), refs[i], f"graph replay {rep}")
+        r.prefill(xin.clone())   # eager work between replays
+        torch.cuda.synchronize()
+
 def test_reduce_unaligned_rows(cuda):
     """The combine with rows that are not a multiple of 4 (the scalar path): sg * shexp, then the valid pairs in
     ascending expert id, ties by position; ids < 0 are skipped and a token without pairs keeps sg * shexp."""
