@@ -33,17 +33,18 @@ static int check_dev(const hy_moe_dev *m, const char *what, bool need_gate, bool
     if (!m) { set_error("%s: null hy_moe_dev", what); return HY_EINVAL; }
     if (!m->slot || m->n_expert <= 0) { set_error("%s: slot table missing", what); return HY_EINVAL; }
     if (m->ff <= 0 || m->n <= 0) { set_error("%s: ff %d, n %d", what, m->ff, m->n); return HY_EBAD_SHAPE; }
+    // every kernel's grid covers ff and n in whole 256-row / 256-value units (the tiled layout's 16-row tiles, the
+    // GEMMs' 64- and 128-row blocks): both are checked whichever matrices the entry point reads
+    if (m->n % 256 || m->ff % 256) { set_error("%s: n = %d and ff = %d must be multiples of 256", what, m->n, m->ff); return HY_EBAD_SHAPE; }
     if (need_gate) {
         if (!dot_type(m->tg)) { set_error("%s: unsupported gate/up type %d", what, m->tg); return HY_EUNSUPPORTED_TYPE; }
         if (!m->gate || !m->up) { set_error("%s: null gate/up", what); return HY_EINVAL; }
-        if (m->n % 256) { set_error("%s: n = %d is not a multiple of 256", what, m->n); return HY_EBAD_SHAPE; }
         const size_t rb = (size_t) (m->n / block_elems(m->tg)) * block_bytes(m->tg);
         if (m->gate_bytes != rb * (size_t) m->ff) { set_error("%s: gate_bytes %zu != ff * row bytes %zu", what, m->gate_bytes, rb * m->ff); return HY_EBAD_SHAPE; }
     }
     if (need_down) {
         if (!dot_type(m->td)) { set_error("%s: unsupported down type %d", what, m->td); return HY_EUNSUPPORTED_TYPE; }
         if (!m->down) { set_error("%s: null down", what); return HY_EINVAL; }
-        if (m->ff % 256) { set_error("%s: ff = %d is not a multiple of 256", what, m->ff); return HY_EBAD_SHAPE; }
         const size_t rb = (size_t) (m->ff / block_elems(m->td)) * block_bytes(m->td);
         if (m->down_bytes != rb * (size_t) m->n) { set_error("%s: down_bytes %zu != n * row bytes %zu", what, m->down_bytes, rb * m->n); return HY_EBAD_SHAPE; }
     }
@@ -77,8 +78,18 @@ int hy_upload_experts(const hy_expert_tensors *t, const int32_t *slot_host, int3
         set_error("hy_upload_experts: ff and n must be multiples of 256 and gb/db the matrices' GGUF sizes");
         return HY_EBAD_SHAPE;
     }
+    // slots: -1 (absent) or a local index below E, each used once -- two experts on one slot would overwrite each
+    // other, and one stray large value would size the allocation
     int nl = 0;
-    for (int e = 0; e < t->E; ++e) nl = std::max(nl, slot_host[e] + 1);
+    std::vector<uint8_t> used(t->E, 0);
+    for (int e = 0; e < t->E; ++e) {
+        const int sl = slot_host[e];
+        if (sl < -1 || sl >= t->E) { set_error("hy_upload_experts: slot[%d] = %d outside [-1, %d)", e, sl, t->E); return HY_EINVAL; }
+        if (sl < 0) continue;
+        if (used[sl]) { set_error("hy_upload_experts: slot %d given to two experts (second: %d)", sl, e); return HY_EINVAL; }
+        used[sl] = 1;
+        nl = std::max(nl, sl + 1);
+    }
     const size_t n_alloc = std::max(nl, 1);
     uint8_t *dg = nullptr, *du = nullptr, *dd = nullptr;
     int32_t *ds = nullptr;

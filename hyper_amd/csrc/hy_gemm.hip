@@ -956,6 +956,9 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
     default: set_error("grouped GEMM: unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 
+// k_gemm keeps each expert group's item prefix per tile class in a 16-bit field of s_scan: the item total of a launch
+// must stay below 2^16 (checked against the upper bound below, from the host)
+constexpr int GM_MAX_ITEMS = 1 << 16;
 // upper bound of the work items: sum over active experts of ceil(cnt / GM_TOK) <= ceil(P / GM_TOK) + active
 static int max_items(int n_pairs, int max_active) { return (n_pairs + GM_TOK - 1) / GM_TOK + max_active; }
 // item slots per row tile: enough blocks for about `per_cu` resident blocks on every CU
@@ -980,6 +983,7 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
     }
     if ((size_t) n_pairs * (m.n / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_gate_up: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
     if (k <= 0 || (uint64_t) n_pairs * (uint64_t) k >= (1ull << 32)) { set_error("hy_moe_gemm_gate_up: k out of range for the pair count"); return HY_EBAD_SHAPE; }
+    if (max_items(n_pairs, max_active) >= GM_MAX_ITEMS) { set_error("hy_moe_gemm_gate_up: %d pairs make more than %d work items", n_pairs, GM_MAX_ITEMS - 1); return HY_EBAD_SHAPE; }
     HY_GEMM_SWITCH(m.tg, {
         constexpr int W = 8, B = g5_blocks<TT, true>();
         const int rb = m.ff / (8 * W);   // 8 W output rows a block
@@ -998,6 +1002,7 @@ int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int
         return check_launch("hy_moe_gemm_down");
     }
     if ((size_t) n_pairs * (m.ff / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_down: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
+    if (max_items(n_pairs, max_active) >= GM_MAX_ITEMS) { set_error("hy_moe_gemm_down: %d pairs make more than %d work items", n_pairs, GM_MAX_ITEMS - 1); return HY_EBAD_SHAPE; }
     HY_GEMM_SWITCH(m.td, {
         constexpr int W = TT == Q6_K ? 16 : 8, B = g5_blocks<TT, false>();   // Q6_K: 16 waves (fits 128 registers)
         const int rb = m.n / (16 * W);   // 16 W output rows a block

@@ -147,6 +147,10 @@ WORKLOADS = {
                                    notes="512 tokens, Zipf(1.1) routing, Q4_K gate/up, Q6_K down"),
     "iq4nl_decode": Workload("iq4nl_decode", 4096, 288, 8, 1536, GType.IQ4_NL, GType.IQ4_NL, 1, d_range=(1e-3, 1e-2),
                              notes="d 4096, 288 experts, top-8, ff 1536, IQ4_NL"),
+    "iq4nl_verify4": Workload("iq4nl_verify4", 4096, 288, 8, 1536, GType.IQ4_NL, GType.IQ4_NL, 4, d_range=(1e-3, 1e-2),
+                              notes="4-row verify batch, IQ4_NL"),
+    "iq4xs_decode": Workload("iq4xs_decode", 4096, 288, 8, 1536, GType.IQ4_XS, GType.IQ4_XS, 1, d_range=(1e-3, 1e-2),
+                             notes="d 4096, 288 experts, top-8, ff 1536, IQ4_XS"),
     "iq4xs_verify4": Workload("iq4xs_verify4", 4096, 288, 8, 1536, GType.IQ4_XS, GType.IQ4_XS, 4, d_range=(1e-3, 1e-2),
                               notes="4-row verify batch, IQ4_XS"),
     "iq2xs_decode": Workload("iq2xs_decode", 7168, 384, 6, 2048, GType.IQ2_XS, GType.IQ2_XS, 1, d_range=(1e-3, 1e-2),

@@ -206,6 +206,7 @@ class MoeLayerRunner:
         self.shared = shared
         self.sg_logit = sg_logit
         device = W_r.device
+        self.device, self.max_rows = device, int(max_rows)
         T, P = max_rows, max_rows * k
         f32, i32 = dict(dtype=torch.float32, device=device), dict(dtype=torch.int32, device=device)
         self.ls = self.E + (1 if sg_logit else 0)
@@ -229,9 +230,9 @@ class MoeLayerRunner:
             self.sh_h = torch.empty(T, S.ff, **f32)
             self.sh_y = torch.empty(T, self.d, **f32)
             self.sh_order = torch.arange(T, **i32)
-            self.sh_order_n = torch.tensor([0, 1], **i32)
-            self.sh_egrp = torch.tensor([0, 0, 0], **i32)
-            self._sh_nt = 0
+            # order_n = (nt, 1) and egrp = (expert 0, start 0, nt) in one buffer, so one strided fill writes both counts
+            self.sh_cnt = torch.tensor([0, 1, 0, 0, 0], **i32)
+            self.sh_order_n, self.sh_egrp = self.sh_cnt[0:2], self.sh_cnt[2:5]
             self.sh_xq = torch.empty(T * q8_row_bytes(vec_dot_type(S.tg), self.d), dtype=torch.uint8, device=device)
             self.sh_hq = torch.empty(T * q8_row_bytes(vec_dot_type(S.td), S.ff), dtype=torch.uint8, device=device)
 
@@ -263,21 +264,43 @@ class MoeLayerRunner:
 
     def _shared_prefill(self, x, nt, stream):
         S = self.shared
-        # one active "expert" holding every token: (0, 0, nt); rewritten (a device fill, which a graph may record) only
-        # when nt changes
-        if nt != self._sh_nt:
-            self.sh_order_n[0:1].fill_(nt)
-            self.sh_egrp[2:3].fill_(nt)
-            self._sh_nt = nt
+        # one active "expert" holding every token: (0, 0, nt).  The count is written on `stream` at every step (a fill
+        # kernel, which a captured graph records with this step's nt), so an eager step or another capture of a
+        # different nt in between never leaves a stale count behind.
+        with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
+            self.sh_cnt[0::4].fill_(nt)
         q8_quantize(vec_dot_type(S.tg), x, x.stride(0), self.d, nt, self.sh_xq, stream)
         moe_gemm_gate_up(S, self.sh_xq, 1, nt, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_h, stream)
         q8_quantize(vec_dot_type(S.td), self.sh_h, S.layer.ff, S.layer.ff, nt, self.sh_hq, stream)
         moe_gemm_down(S, self.sh_hq, nt, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_ones, self.sh_y, stream)
 
+    def _check_rows(self, x: torch.Tensor, bias=None, resid: Optional[torch.Tensor] = None) -> int:
+        """The kernels index every workspace buffer by token: x must fit the rows the runner was built for, and be
+        float32 rows of d contiguous values on the runner's device (as must bias and resid)."""
+        if x.dim() != 2 or x.shape[1] != self.d:
+            raise ValueError(f"x must be [nt, {self.d}], got {tuple(x.shape)}")
+        nt = x.shape[0]
+        if nt > self.max_rows:
+            raise ValueError(f"{nt} rows exceed the runner's max_rows {self.max_rows}")
+        for name, t in (("x", x), ("bias", bias), ("resid", resid)):
+            if t is None:
+                continue
+            if t.dtype != torch.float32 or t.device != self.device:
+                raise ValueError(f"{name} must be float32 on {self.device}, got {t.dtype} on {t.device}")
+            if t.dim() != 2 or t.shape[0] < nt or t.stride(1) != 1:
+                raise ValueError(f"{name} must be 2-D with contiguous rows and at least {nt} of them")
+            if name != "bias" and (t.stride(0) % 4 or t.data_ptr() % 16):
+                raise ValueError(f"{name} rows must be 16-byte aligned")
+        if bias is not None and bias.shape[1] < self.W_r.shape[0]:
+            raise ValueError(f"bias rows must hold {self.W_r.shape[0]} logits")
+        if resid is not None and resid.shape[1] != self.d:
+            raise ValueError(f"resid must be [nt, {self.d}]")
+        return nt
+
     def decode(self, x: torch.Tensor, bias=None, stream=None, resid: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Decode / short verify: router + Q8 of x, route + gate/up, down + combine (two more for a shared expert).
         With `resid` ([nt, d] fp32) the combine is added into it in place and resid is returned."""
-        nt = x.shape[0]
+        nt = self._check_rows(x, bias, resid)
         moe_router_q8(self.W_r, self.W_r.shape[0], self.d, x, x.stride(0), self.logits, self.ls, self.vg, self.xq, nt, stream,
                       bias=bias, bias_stride=0 if bias is None else bias.stride(0))
         shexp = None
@@ -297,7 +320,7 @@ class MoeLayerRunner:
 
     def decode_legacy(self, x: torch.Tensor, bias=None, stream=None) -> torch.Tensor:
         """The same step through the reference-signature entry points (fp32 x and h in, quantized inside)."""
-        nt = x.shape[0]
+        nt = self._check_rows(x, bias)
         self.route(x, nt, bias, stream)
         shexp = None
         if self.shared is not None:
@@ -309,7 +332,7 @@ class MoeLayerRunner:
 
     def prefill(self, x: torch.Tensor, bias=None, stream=None, shared_ready=False, resid: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Prefill: the grouped GEMM path.  With `resid` ([nt, d] fp32) the combine is added into it in place."""
-        nt, k = x.shape[0], self.k
+        nt, k = self._check_rows(x, bias, resid), self.k
         P = nt * k
         moe_router_q8(self.W_r, self.W_r.shape[0], self.d, x, x.stride(0), self.logits, self.ls, self.vg, self.xq, nt, stream,
                       bias=bias, bias_stride=0 if bias is None else bias.stride(0))

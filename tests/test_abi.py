@@ -87,3 +87,59 @@ def test_tile_rows_layout():
                 assert torch.equal(t[e, off:off + sb], raw[e, r, s * sb:(s + 1) * sb])
     with pytest.raises(ValueError):
         tile_rows(raw[:, :40], in_dim)
+
+
+def _dev(tg=12, td=14, ff=768, n=2048, E=128):
+    from hyper_amd import hy_moe_dev
+    m = hy_moe_dev()
+    m.gate = m.up = m.down = m.slot = 16
+    m.tg, m.td, m.ff, m.n, m.n_expert = tg, td, ff, n, E
+    m.gate_bytes = ff * (n // 256) * {12: 144, 13: 176, 14: 210}[tg]
+    m.down_bytes = n * (ff // 256) * {12: 144, 13: 176, 14: 210}[td]
+    return m
+
+
+def test_descriptor_rows_checked_for_every_entry():
+    """Every entry point that reads a hy_moe_dev checks both ff and n against the kernels' 256-row units, also the
+    matrices it does not read: a gate/up-only descriptor with ff = 800 or a down-only one with n = 2100 is rejected."""
+    L = lib()
+    p = ctypes.c_void_p(16)
+    m = _dev(ff=800)
+    m.gate_bytes = 800 * 8 * 144
+    assert L.hy_moe_gate_up(ctypes.byref(m), p, 2048, p, 8, p, 1, None, None, None) == hyper_amd.HY_EBAD_SHAPE
+    assert b"multiples of 256" in L.hy_last_error()
+    m = _dev(n=2100)
+    m.down_bytes = 2100 * 3 * 210
+    assert L.hy_moe_down_reduce(ctypes.byref(m), p, p, p, 8, None, None, p, 1, None) == hyper_amd.HY_EBAD_SHAPE
+    assert L.hy_moe_gemm_down(ctypes.byref(m), p, 64, p, p, p, 8, p, p, None) == hyper_amd.HY_EBAD_SHAPE
+
+
+def test_grouped_gemm_rejects_more_work_items_than_its_fields_hold():
+    """k_gemm keeps per-class item prefixes in 16-bit fields: a launch whose item bound reaches 2^16 is refused on the
+    host (ff 768 down: 4.2 M pairs stay below the 4 GB activation limit but make 65,536 + items)."""
+    L = lib()
+    p = ctypes.c_void_p(16)
+    m = _dev()
+    rc = L.hy_moe_gemm_down(ctypes.byref(m), p, 64 * 65536, p, p, p, 128, p, p, None)
+    assert rc == hyper_amd.HY_EBAD_SHAPE and b"work items" in L.hy_last_error()
+    rc = L.hy_moe_gemm_gate_up(ctypes.byref(m), p, 1, 64 * 65536, p, p, p, 128, p, None)
+    assert rc == hyper_amd.HY_EBAD_SHAPE
+
+
+def test_upload_rejects_bad_slots():
+    """hy_upload_experts validates the slot table before it allocates: -1 or a local index below E, each used once."""
+    from hyper_amd import hy_expert_tensors, hy_moe_dev
+    import numpy as np
+    L = lib()
+    E, ff, n = 4, 256, 256
+    gb, db = ff * 144, n * 144
+    buf = np.zeros(E * max(gb, db), np.uint8)
+    t = hy_expert_tensors()
+    t.gate = t.up = t.down = buf.ctypes.data
+    t.gb, t.db, t.E, t.tg, t.td = gb, db, E, 12, 12
+    out = hy_moe_dev()
+    for bad in ([0, 1, 1, 2], [0, 1, 2, 4], [0, -2, 1, 2], [0, 1, 2, 1 << 30]):
+        sl = np.array(bad, np.int32)
+        rc = L.hy_upload_experts(ctypes.byref(t), sl.ctypes.data_as(ctypes.c_void_p), ff, n, 0.0, ctypes.byref(out))
+        assert rc == hyper_amd.HY_EINVAL, bad
+        assert b"slot" in L.hy_last_error()

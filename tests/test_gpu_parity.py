@@ -267,7 +267,9 @@ def test_runner_prefill_shared_matches_oracle(cuda, tg, td, E, d, ff, k, nt, sh,
 
 def test_runner_prefill_shared_graph_replays(cuda):
     """The prefill step with a shared expert (and its sigmoid gate) captured into a HIP graph: every replay, with
-    eager work and synchronizations between them, equals the eager step and the oracle, for two inputs in turn."""
+    eager work and synchronizations between them, equals the eager step and the oracle, for two inputs in turn.  The
+    eager steps in between take fewer rows than the captured one, so a shared-expert count left behind by them would
+    show in the next replay."""
     tg, td, E, d, ff, k, nt = GType.Q4_K, GType.Q6_K, 32, 2048, 768, 8, 48
     L = layer(tg, td, E, ff, d, seed=920)
     S = layer(GType.Q4_K, td, 1, ff, d, seed=921)
@@ -298,8 +300,14 @@ def test_runner_prefill_shared_graph_replays(cuda):
         graph.replay()
         torch.cuda.synchronize()
         assert_bits_equal(out.cpu().numpy(), refs[i], f"graph replay {rep}")
-        r.prefill(xin.clone())   # eager work between replays
+        nt2 = nt - 8 * (rep + 1)
+        small = r.prefill(xin[:nt2].clone()).clone()   # eager work of another row count between replays
         torch.cuda.synchronize()
+        if rep == 0:
+            x2 = xs[i][:nt2].numpy()
+            ids2, wts2, sg2 = orc.route(orc.gemv_f32(W_r.numpy(), x2), E, k, with_sg=True)
+            ref2 = orc.moe_layer(oracle_layer(L), x2, ids2, wts2, shared=oracle_layer(S), sg=sg2)
+            assert_bits_equal(small.cpu().numpy(), ref2, "eager prefill of fewer rows")
 
 def test_reduce_unaligned_rows(cuda):
     """The combine with rows that are not a multiple of 4 (the scalar path): sg * shexp, then the valid pairs in

@@ -135,6 +135,85 @@ def test_q8_0_matches_ggml_x86_restatement(name):
     assert (got == np_quantize_q8_0(x)).all()
 
 
+def test_q8_0_known_answers_round_half_even():
+    """Q8_0 at exact .5 ties.  The reference links ggml built for its AVX2 host (Makefile:1 names the
+    Threadripper/AVX2 target, Makefile:6 compiles with -march=native, and llama.cpp's own build defaults to the
+    native ISA), so from_float for IQ4_NL activations is ggml's AVX2 quantize_row_q8_0, whose
+    _mm256_round_ps(_MM_ROUND_NEAREST) rounds half to even; the scalar fallback's roundf would give the
+    away-from-zero column below instead.  amax = 127 makes id = 127/amax = 1 exactly and d = 1 (fp16 0x3C00),
+    so every q is the rounding of x itself."""
+    x = np.zeros(64, np.float32)
+    ties = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, -3.5, 126.5, -126.5, 0.25, -0.75]
+    x[0:len(ties)] = ties
+    x[31] = -127.0                                                   # amax of block 0
+    even = [0, 2, 2, 0, -2, -2, 4, -4, 126, -126, 0, -1]
+    away = [1, 2, 3, -1, -2, -3, 4, -4, 127, -127, 0, -1]
+    x[32:40] = [63.5, -63.5, 0.5, 127.0, 1.5, 64.5, -0.5, 2.5]      # block 1: amax 127 again
+    got = orc.quantize(GType.Q8_0, x).reshape(2, 34)
+    assert bytes(got[0, 0:2]) == b"\x00\x3c" and bytes(got[1, 0:2]) == b"\x00\x3c"   # d = 1.0 in fp16
+    q0 = got[0, 2:34].view(np.int8)
+    assert list(q0[:len(ties)]) == even and list(q0[:len(ties)]) != away
+    assert q0[31] == -127 and not q0[len(ties):31].any()
+    assert list(got[1, 2:10].view(np.int8)) == [64, -64, 0, 127, 2, 64, 0, 2]
+
+
+def test_q5k_known_answer_positions():
+    """Q5_K element e of sub-block j = e / 32, l = e % 32: low 4 bits in qs[32 (j / 2) + l] at byte 48 (high nibble
+    for odd j), bit 4 = bit j of qh[l] at byte 16; value (d sc_j) q5 - dmin m_j (src/kernels4.cu:437-448)."""
+    want = np.array([(7 * e + 3 * (e // 32) + e // 64) % 32 for e in range(256)], np.int64)
+    assert len(set(want[0:32])) == 32 and (want >= 16).sum() > 100      # every sub-block uses the fifth bit
+    blk = np.zeros(176, np.uint8)
+    blk[0:2], blk[2:4] = _f16b(1.0), _f16b(0.0)
+    blk[4:16] = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]                  # sc = 1, m = 0 for all eight sub-blocks
+    for e in range(256):
+        j, l = divmod(e, 32)
+        blk[48 + 32 * (j // 2) + l] |= (want[e] & 15) << (4 * (j % 2))
+        blk[16 + l] |= (want[e] >> 4) << j
+    assert (orc.dequant_row(GType.Q5_K, blk, 256) == want.astype(np.float32)).all()
+    # scales and mins through the j >= 4 branch: sub-block 6 gets sc = 37 (low 4 bits 5 in byte 10, high 2 bits 2
+    # in byte 2's top bits), m = 3 (byte 10's high nibble)
+    blk[2:4] = _f16b(0.5)
+    blk[4 + 10] = 5 | (3 << 4)
+    blk[4 + 2] = 1 | (2 << 6)
+    j6 = np.arange(256) // 32 == 6
+    exp = np.where(j6, np.float32(37) * want.astype(np.float32) - np.float32(1.5), want.astype(np.float32)).astype(np.float32)
+    assert (orc.dequant_row(GType.Q5_K, blk, 256) == exp).all()
+
+
+def test_iq4xs_known_answer_positions():
+    """IQ4_XS 32-group ib: 6-bit scale ls = nibble (ib & 1) of scales_l[ib / 2] | bits 2 ib of scales_h << 4; element
+    l < 16 is the low nibble of qs[16 ib + l], l >= 16 the high nibble of qs[16 ib + l - 16]; value
+    (d (ls - 32)) kv[nibble] (src/kernels4.cu:660-670)."""
+    kv = nf.KV_IQ4NL
+    ls = np.array([33, 40, 1, 63, 17, 37, 50, 9], np.int64)             # every value of the two high bits occurs
+    idx = np.array([(5 * e + e // 32 + 3 * ((e // 16) % 2)) % 16 for e in range(256)], np.int64)
+    blk = np.zeros(136, np.uint8)
+    blk[0:2] = _f16b(1.0)
+    sh = 0
+    for ib in range(8):
+        blk[4 + ib // 2] |= (ls[ib] & 15) << (4 * (ib % 2))
+        sh |= int(ls[ib] >> 4) << (2 * ib)
+    blk[2:4] = np.frombuffer(np.uint16(sh).tobytes(), np.uint8)
+    for e in range(256):
+        ib, l = divmod(e, 32)
+        blk[8 + 16 * ib + (l % 16)] |= idx[e] << (4 if l >= 16 else 0)
+    want = ((ls[np.arange(256) // 32] - 32) * kv[idx]).astype(np.float32)
+    assert (orc.dequant_row(GType.IQ4_XS, blk, 256) == want).all()
+
+
+def test_iq4nl_known_answer_positions():
+    """IQ4_NL block of 32: value j < 16 is kv[qs[j] & 15] d, value 16 + j is kv[qs[j] >> 4] d (src/kernels4.cu:629-636)."""
+    kv = nf.KV_IQ4NL
+    idx = np.array([[(3 * j + 7 * b + (j >= 16)) % 16 for j in range(32)] for b in range(2)], np.int64)
+    blk = np.zeros((2, 18), np.uint8)
+    for b, dv in enumerate((2.0, -0.5)):
+        blk[b, 0:2] = _f16b(dv)
+        for j in range(32):
+            blk[b, 2 + (j % 16)] |= idx[b, j] << (4 if j >= 16 else 0)
+    want = np.concatenate([kv[idx[0]] * 2.0, kv[idx[1]] * -0.5]).astype(np.float32)
+    assert (orc.dequant_row(GType.IQ4_NL, blk.reshape(-1), 64) == want).all()
+
+
 def test_q8k_known_answers():
     x = np.zeros(512, np.float32)
     # block 0: max -127 at index 3 -> iscale = 1, q = round-half-even(x)
