@@ -21,7 +21,7 @@ CSRC = PKG / "csrc"
 OUT = PKG / "libhymoe.so"
 BUILD = PKG / "_build"
 
-SOURCES = ["hy_route.hip", "hy_gemv.hip", "hy_gemm.hip", "hy_decode.hip", "hy_capi.cpp", "hy_gguf.cpp"]
+SOURCES = ["hy_route.hip", "hy_gemv.hip", "hy_gemm.hip", "hy_decode.hip", "hy_capi.cpp", "hy_step.cpp", "hy_gguf.cpp"]
 ARCH = os.environ.get("HYMOE_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

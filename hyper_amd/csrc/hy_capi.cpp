@@ -51,6 +51,12 @@ static int check_dev(const hy_moe_dev *m, const char *what, bool need_gate, bool
     return HY_OK;
 }
 static bool aligned16(const void *p) { return ((uintptr_t) p & 15) == 0; }
+// the layer (and the shared expert's) descriptors for a whole decode step: gate/up and down read
+int check_dev_decode(const hy_moe_dev *m, const hy_moe_dev *shared, const char *what) {
+    int rc = check_dev(m, what, true, true);
+    if (rc == HY_OK && shared) rc = check_dev(shared, what, true, true);
+    return rc;
+}
 
 } // namespace hy
 

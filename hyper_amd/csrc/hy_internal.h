@@ -8,6 +8,8 @@ namespace hy {
 void set_error(const char *fmt, ...);
 // after a launch: HY_OK, or HY_EHIP with the launch error recorded under `what`
 int check_launch(const char *what);
+// checks of the layer descriptors a whole decode step reads (gate/up and down of the layer and of the shared expert)
+int check_dev_decode(const hy_moe_dev *m, const hy_moe_dev *shared, const char *what);
 
 int launch_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bs,
                     hipStream_t s);

@@ -204,6 +204,19 @@ int hy_moe_router_q8(const float *W_r, int rows, int kdim, const float *x, int x
 int hy_moe_route_gate_up(const hy_moe_dev *m, const float *logits, int ls, int n_expert, int k, const void *xq, int32_t *ids, float *wts,
                          float *sg, float *h, int nt, hipStream_t s);
 
+/* One MoE layer's decode step (nt <= 64 rows) in one call: the reference engine's per-layer sequence
+   (src/engine4.cu:807-890 -- gemv_f32, moe_route, moe_gate_up, moe_down, moe_reduce -- and the shared expert of
+   src/engine4.cu:795-804) on the decode launches above: hy_moe_router_q8, hy_moe_route_gate_up (softmax routing),
+   hy_moe_down_reduce.  W_r: fp32 [rows][n] with rows = n_expert, or n_expert + 1 whose last row is the shared-expert
+   gate logit (sg = sigmoid of it; without that row the shared expert's gate is 1); bias as in hy_gemv_f32 (NULL:
+   none).  shared: the always-on expert (NULL: none; its slot 0 holds it).  out [nt][n] fp32, or with residual != 0
+   the step is added into it.  The intermediates (logits, ids, wts, sg, Q8 rows of x, h, the shared expert's h and
+   output) live in the caller's workspace `ws` of at least hy_moe_decode_ws_bytes(...) bytes, 256-byte aligned; the
+   routing (ids, wts) is left there.  Results are bit-identical to the separate entry points. */
+size_t hy_moe_decode_ws_bytes(const hy_moe_dev *m, int rows, int k, const hy_moe_dev *shared, int nt);
+int hy_moe_decode(const hy_moe_dev *m, const float *W_r, int rows, const float *x, int xs, const float *bias, int bias_stride, int k,
+                  const hy_moe_dev *shared, float *out, int residual, int nt, void *ws, size_t ws_bytes, hipStream_t s);
+
 /* Test hooks.  One row of n weights dequantized by the kernels' block decoders (replaces deq_row_test,
    src/kernels4.cuh:181 / src/kernels4.cu:2036-2044); and the exact integers of every block of nrows weight rows
    (row stride row_bytes) against one Q8 activation row: sumi/summ [nrows][n / block_elems] (summ 0 for types
