@@ -109,6 +109,31 @@ int run_decode(const hy_moe_dev &m, const float *W_r, int rows, const float *x, 
 
 size_t decode_ws_bytes(const hy_moe_dev &m, int rows, int k, const hy_moe_dev *S, int nt) { return decode_layout(m, rows, k, S, nt).total; }
 
+// ---- the decode step without a workspace argument: its intermediates in `scratch`, a file-scope device array that
+// every device running the library holds until the process ends (1 MiB: e.g. 8 rows of a d_model 7168, top-6, ff 2048
+// layer with a shared expert need 0.75 MiB).  In host code `scratch` names a host-side stand-in, not device memory:
+// kernels get the per-device address that hipGetSymbolAddress returns, taken once per device with that device current.
+constexpr size_t DECODE_SCRATCH_BYTES = 1u << 20;
+__device__ __align__(256) uint8_t scratch[DECODE_SCRATCH_BYTES];
+
+static uint8_t *g_scratch[MAX_DEVICES];
+static std::once_flag g_scratch_once[MAX_DEVICES];
+static int g_scratch_rc[MAX_DEVICES];
+
+static int scratch_ptr(uint8_t *&out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) { set_error("hy_moe_decode_noalloc: no current device"); return HY_EHIP; }
+    std::call_once(g_scratch_once[dev], [dev] {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_rc[dev] = e == hipSuccess && p ? HY_OK : HY_EHIP;
+        if (g_scratch_rc[dev] == HY_OK) g_scratch[dev] = (uint8_t *) p;
+    });
+    if (g_scratch_rc[dev] != HY_OK) { set_error("hy_moe_decode_noalloc: hipGetSymbolAddress of the scratch array failed on device %d", dev); return HY_EHIP; }
+    out = g_scratch[dev];
+    return HY_OK;
+}
+
 } // namespace hy
 
 using namespace hy;
@@ -131,6 +156,21 @@ int hy_moe_decode(const hy_moe_dev *m, const float *W_r, int rows, const float *
         return HY_EINVAL;
     }
     return run_decode(*m, W_r, rows, x, xs, bias, bias_stride, k, shared, out, residual, nt, (uint8_t *) ws, s);
+}
+
+int hy_moe_decode_noalloc(const hy_moe_dev *m, const float *W_r, int rows, const float *x, int xs, const float *bias, int bias_stride, int k,
+                          const hy_moe_dev *shared, float *out, int residual, int nt, hipStream_t s) {
+    int rc = decode_args("hy_moe_decode_noalloc", m, W_r, rows, x, xs, k, shared, out, nt);
+    if (rc) return rc;
+    if ((rc = check_dev_decode(m, shared, "hy_moe_decode_noalloc"))) return rc;
+    const size_t need = decode_ws_bytes(*m, rows, k, shared, nt);
+    if (need > DECODE_SCRATCH_BYTES) {
+        set_error("hy_moe_decode_noalloc: %d rows of this layer need %zu bytes of scratch, more than its %zu", nt, need, DECODE_SCRATCH_BYTES);
+        return HY_EBAD_SHAPE;
+    }
+    uint8_t *ws = nullptr;
+    if ((rc = scratch_ptr(ws))) return rc;
+    return run_decode(*m, W_r, rows, x, xs, bias, bias_stride, k, shared, out, residual, nt, ws, s);
 }
 
 } // extern "C"

@@ -216,6 +216,14 @@ int hy_moe_route_gate_up(const hy_moe_dev *m, const float *logits, int ls, int n
 size_t hy_moe_decode_ws_bytes(const hy_moe_dev *m, int rows, int k, const hy_moe_dev *shared, int nt);
 int hy_moe_decode(const hy_moe_dev *m, const float *W_r, int rows, const float *x, int xs, const float *bias, int bias_stride, int k,
                   const hy_moe_dev *shared, float *out, int residual, int nt, void *ws, size_t ws_bytes, hipStream_t s);
+/* hy_moe_decode without a workspace argument.  No counterpart in the reference: it is for callers that cannot
+   allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+   allocates nothing: the intermediates live in a file-scope device array of 1 MiB that each GPU running the library
+   holds until the process ends (hy_moe_decode_ws_bytes must not exceed it, else HY_EBAD_SHAPE).  Every call on one
+   GPU shares that GPU's array and nothing in it needs to start at zero; calls that overlap on one GPU (other streams,
+   other threads) race on it and must be ordered by the caller. */
+int hy_moe_decode_noalloc(const hy_moe_dev *m, const float *W_r, int rows, const float *x, int xs, const float *bias, int bias_stride,
+                          int k, const hy_moe_dev *shared, float *out, int residual, int nt, hipStream_t s);
 
 /* Test hooks.  One row of n weights dequantized by the kernels' block decoders (replaces deq_row_test,
    src/kernels4.cuh:181 / src/kernels4.cu:2036-2044); and the exact integers of every block of nrows weight rows

@@ -143,3 +143,14 @@ def test_upload_rejects_bad_slots():
         rc = L.hy_upload_experts(ctypes.byref(t), sl.ctypes.data_as(ctypes.c_void_p), ff, n, 0.0, ctypes.byref(out))
         assert rc == hyper_amd.HY_EINVAL, bad
         assert b"slot" in L.hy_last_error()
+
+
+def test_noalloc_decode_rejects_what_its_scratch_cannot_hold():
+    """hy_moe_decode_noalloc refuses, before any device call, a step whose intermediates exceed its 1 MiB scratch array
+    (64 rows of a d_model 7168, top-6, ff 2048 layer need several MiB)."""
+    L = lib()
+    p = ctypes.c_void_p(256)
+    m = _dev(tg=12, td=12, ff=2048, n=7168, E=384)
+    assert L.hy_moe_decode_ws_bytes(ctypes.byref(m), 384, 6, None, 64) > (1 << 20)
+    rc = L.hy_moe_decode_noalloc(ctypes.byref(m), p, 384, p, 7168, None, 0, 6, None, p, 0, 64, None)
+    assert rc == hyper_amd.HY_EBAD_SHAPE and b"scratch" in L.hy_last_error()
