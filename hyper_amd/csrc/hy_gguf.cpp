@@ -7,7 +7,7 @@
 // u32 type, u64 offset); then, from the header's end rounded up to general.alignment (32 by default), the tensor
 // data, each tensor at its offset.  A string is a u64 length and its bytes; an array a u32 element type, a u64 count
 // and the elements.
-#include "hy_internal.h"
+#include "hy_error.h"
 
 #include <fcntl.h>
 #include <sys/mman.h>

@@ -2,10 +2,10 @@
 #pragma once
 #include "../../include/hymoe.h"
 #include "hy_common.cuh"
+#include "hy_error.h"
 
 namespace hy {
 
-void set_error(const char *fmt, ...);
 // after a launch: HY_OK, or HY_EHIP with the launch error recorded under `what`
 int check_launch(const char *what);
 // checks of the layer descriptors a whole decode step reads (gate/up and down of the layer and of the shared expert)

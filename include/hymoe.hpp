@@ -158,6 +158,35 @@ inline void moe_down_reduce(const MoeDev &m, const float *h, const int *ids, con
                             const float *sg, float *out, int nt, hipStream_t s) {
     check(hy_moe_down_reduce(&m, h, ids, wts, k, shexp, sg, out, nt, s));
 }
+// decode: gemv_f32 and the experts' Q8 rows of x in one launch (src/kernels4.cu:1910-1913 + the activation quantizer)
+inline void moe_router_q8(const float *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride, float *logits,
+                          int ls, int vtype, void *xq, int nt, hipStream_t s) {
+    check(hy_moe_router_q8(W_r, rows, kdim, x, xs, bias, bias_stride, logits, ls, vtype, xq, nt, s));
+}
+// decode: moe_route and moe_gate_up (on the Q8 rows) in one launch
+inline void moe_route_gate_up(const MoeDev &m, const float *logits, int ls, int n_expert, int k, const void *xq, int *ids, float *wts,
+                              float *sg, float *h, int nt, hipStream_t s) {
+    check(hy_moe_route_gate_up(&m, logits, ls, n_expert, k, xq, ids, wts, sg, h, nt, s));
+}
+// one layer's decode step (src/engine4.cu:795-890) on a caller workspace of moe_decode_ws_bytes(...) bytes
+inline size_t moe_decode_ws_bytes(const MoeDev &m, int rows, int k, const MoeDev *shared, int nt) {
+    return hy_moe_decode_ws_bytes(&m, rows, k, shared, nt);
+}
+inline void moe_decode(const MoeDev &m, const float *W_r, int rows, const float *x, int xs, const float *bias, int bias_stride, int k,
+                       const MoeDev *shared, float *out, bool residual, int nt, void *ws, size_t ws_bytes, hipStream_t s) {
+    check(hy_moe_decode(&m, W_r, rows, x, xs, bias, bias_stride, k, shared, out, residual ? 1 : 0, nt, ws, ws_bytes, s));
+}
+// the same step with no workspace and no allocation (the library's per-GPU scratch array; overlapping calls race)
+inline void moe_decode_noalloc(const MoeDev &m, const float *W_r, int rows, const float *x, int xs, const float *bias, int bias_stride,
+                               int k, const MoeDev *shared, float *out, bool residual, int nt, hipStream_t s) {
+    check(hy_moe_decode_noalloc(&m, W_r, rows, x, xs, bias, bias_stride, k, shared, out, residual ? 1 : 0, nt, s));
+}
+// src/cpu_moe.h:46 q8k_test_quantize(x, y, k): the expert path's Q8_K activation quantizer, here on device memory
+// (the quantizer the kernels use; bit-identical to the reference's CPU quantizer, src/cpu_moe.cpp:35-78)
+inline void q8k_test_quantize(const float *x, void *y, int64_t k, hipStream_t s = nullptr) {
+    if (k % 256) throw std::runtime_error("q8k_test_quantize: k must be a multiple of 256");
+    check(hy_q8_quantize(HY_Q8_K, x, (int) k, (int) k, 1, y, s));
+}
 // src/kernels4.cuh:181 test hook
 inline void deq_row_test(int type, const uint8_t *row, int n, float *out, hipStream_t s = nullptr) {
     check(hy_dequant_row(type, row, n, out, s));
