@@ -176,11 +176,11 @@ def decode_bench(args, dev, stream):
     L0 = layers[0]
     tok_bytes = k * L0.expert_bytes() + E * d * 4 + 2 * d * 4
     us = ms * 1e3
-    return {"workload": "q4k_decode", "us_per_token": us, "hbm_gbs": tok_bytes / (us / 1e6) / 1e9,
+    return ({"workload": "q4k_decode", "us_per_token": us, "hbm_gbs": tok_bytes / (us / 1e6) / 1e9,
             "hbm_frac": tok_bytes / (us / 1e6) / 1e9 / HBM_PEAK_GBS, "alg_bytes_per_token": tok_bytes,
             "kernels": {"router_q8": {"us": ms_rq * 1e3, "gbs": (E * d * 4 + d * 4) / (ms_rq / 1e3) / 1e9},
                         "route_gate_up": {"us": ms_gu * 1e3, "gbs": k * 2 * L0.gate_bytes / (ms_gu / 1e3) / 1e9},
-                        "down_reduce": {"us": ms_dn * 1e3, "gbs": k * L0.down_bytes / (ms_dn / 1e3) / 1e9}}}
+                        "down_reduce": {"us": ms_dn * 1e3, "gbs": k * L0.down_bytes / (ms_dn / 1e3) / 1e9}}}, layers)
 
 
 def workloads_bench(args, dev, stream):
@@ -231,37 +231,85 @@ def workloads_bench(args, dev, stream):
     return res
 
 
-def cpu_baseline(layer, W_r, xs, biases, budget_s: float):
-    """The CPU oracle on the headline step: the first S tokens of one step, S doubling up to the full 512, then
-    whole steps over the next inputs until about budget_s seconds of oracle work have been timed."""
+def cpu_info() -> dict:
+    """CPU model, physical cores and hardware threads of this host (from /proc/cpuinfo), and the CPUs this process
+    may run on."""
+    model, cores, hw = "unknown", set(), 0
+    try:
+        phys = core = None
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "processor":
+                hw += 1
+            elif k == "model name" and model == "unknown":
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+                cores.add((phys, core))
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return {"model": model, "physical_cores": len(cores) or None, "hw_threads": hw or None, "cpus_available": avail}
+
+
+def cpu_baseline(layer, W_r, xs, biases, budget_s: float, dec_layers=None):
+    """The CPU oracle (AVX2 integer block dots, OpenMP rows) on the headline step, on this host.
+    value: whole 512-token steps on `threads` threads (the CPU share of one GPU on this machine, at most 16) until
+    about 0.6 budget_s; threads_1: the first 64 tokens of a step on one thread.  decode_gbs: the 1-token Q4_K decode
+    (8 experts of 2.65 MB, cycling the decode layer copies so DRAM, not the caches, serves them) as expert bytes per
+    second, on one thread and on `threads` -- the quantity the reference reports for its CPU expert path."""
     import oracle as orc
     OL = orc.Layer.from_expert_layer(layer)
     Wh = W_r.cpu().numpy()
     w = WORKLOADS["q4k_q6k_prefill512"]
     threads = orc.default_threads()
 
-    def one(i, S):
+    def routed(i, S):
         xh, bh = xs[i % len(xs)][:S].cpu().numpy(), biases[i % len(xs)][:S].cpu().numpy()
         logits = (orc.gemv_f32(Wh, xh) + bh).astype(np.float32)
-        t0 = time.perf_counter()
         ids, wts, _ = orc.route(logits, w.E, w.k)
-        orc.moe_layer(OL, xh, ids, wts, threads=threads)
+        return xh, ids, wts
+
+    def one(i, S, th):
+        xh, ids, wts = routed(i, S)
+        t0 = time.perf_counter()
+        orc.moe_layer(OL, xh, ids, wts, threads=th)
         return time.perf_counter() - t0
 
-    S = 4
-    while S < w.rows:
-        dt = one(0, S)
-        if dt * (w.rows / S) > budget_s:        # a full step would overrun the budget: report this sample
-            return {"value": S / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-                    "sample": f"first {S} tokens of one {w.rows}-token step, {dt:.2f} s, oracle/moe_oracle.c, {threads} threads"}
-        S *= 2
     spent, steps = 0.0, 0
-    while spent < budget_s or steps == 0:
-        spent += one(steps, w.rows)
+    while spent < 0.6 * budget_s or steps == 0:
+        spent += one(steps, w.rows, threads)
         steps += 1
-    return {"value": steps * w.rows / spent, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{steps} whole {w.rows}-token steps (routing + expert FFN + combine; same weights, fresh inputs), "
-                      f"{spent:.1f} s, oracle/moe_oracle.c, {threads} threads"}
+    res = {"value": steps * w.rows / spent, "unit": "tokens/s", "cores": threads, "kind": "port",
+           "sample": f"{steps} whole {w.rows}-token steps (routing + expert FFN + combine; same weights, fresh inputs), "
+                     f"{spent:.1f} s, oracle/moe_oracle.c (AVX2 integer block dots), {threads} threads",
+           "threads_1": round(64 / one(0, 64, 1), 1), "cpu": cpu_info()}
+    if dec_layers:
+        wd = WORKLOADS["q4k_decode"]
+        OLs = [orc.Layer.from_expert_layer(L) for L in dec_layers]
+        g = np.random.default_rng(7)
+        tok_bytes = wd.k * dec_layers[0].expert_bytes()
+        for th, key in ((1, "decode_gbs_1"), (threads, "decode_gbs")):
+            n_tok, t_all = 0, 0.0
+            while t_all < 0.1 * budget_s or n_tok < 8:
+                Lc = OLs[n_tok % len(OLs)]
+                x = g.standard_normal((1, wd.d)).astype(np.float32)
+                ids = g.choice(wd.E, size=(1, wd.k), replace=False).astype(np.int32)
+                wts = np.full((1, wd.k), 1.0 / wd.k, np.float32)
+                t0 = time.perf_counter()
+                orc.moe_layer(Lc, x, ids, wts, threads=th)
+                t_all += time.perf_counter() - t0
+                n_tok += 1
+            res[key] = round(n_tok * tok_bytes / t_all / 1e9, 2)
+        res["decode_sample"] = (f"1-token Q4_K decode, 8 experts ({tok_bytes / 1e6:.1f} MB), cycling {len(OLs)} layer copies "
+                                f"({len(OLs) * dec_layers[0].expert_bytes() * wd.E / 1e9:.2f} GB)")
+    return res
 
 
 def copy_probe(mib: int, dev):
@@ -315,10 +363,10 @@ def main():
     log("prefill: building layers and inputs")
     pre, L0, W0, xs0, bs0 = prefill_bench(args, dev, stream)
     log(f"prefill: {pre['tok_s']:.0f} tok/s, {pre['ms_step'] * 1e3:.1f} us/step")
-    dec = None
+    dec, dec_layers = None, None
     if not args.no_decode:
         log("decode: building layers")
-        dec = decode_bench(args, dev, stream)
+        dec, dec_layers = decode_bench(args, dev, stream)
         log(f"decode: {dec['us_per_token']:.2f} us/token")
     wl = None
     if not args.no_workloads:
@@ -327,7 +375,7 @@ def main():
     cpu = None
     if args.cpu_budget > 0:
         log("cpu baseline: oracle on a sample of the prefill step")
-        cpu = cpu_baseline(L0, W0, xs0, bs0, args.cpu_budget)
+        cpu = cpu_baseline(L0, W0, xs0, bs0, args.cpu_budget, [L.to("cpu") for L in dec_layers] if dec_layers else None)
     w = WORKLOADS["q4k_q6k_prefill512"]
     line = {
         "metric": METRIC, "value": round(pre["tok_s"], 1), "unit": "tokens/s", "n_gpus": 1,

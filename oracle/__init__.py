@@ -57,7 +57,7 @@ def lib():
             "or_fp16_to_fp32": (F, [ctypes.c_uint16]), "or_fp32_to_fp16": (ctypes.c_uint16, [F]),
             "or_quantize_q8_K": (None, [P, P, I]), "or_quantize_q8_0": (None, [P, P, I]),
             "or_quantize_row": (I, [I, P, P, I]), "or_dequant_row": (I, [I, P, I, P]),
-            "or_block_ints": (I, [I, P, P, I, P, P]), "or_row_dot": (F, [I, P, P, I]),
+            "or_block_ints": (I, [I, P, P, I, P, P]), "or_block_ints_scalar": (I, [I, P, P, I, P, P]), "or_row_dot": (F, [I, P, P, I]),
             "or_gemv_f32": (None, [P, I, I, P, I, P, I, I]),
             "or_route": (I, [P, I, I, I, I, P, P, P]),
             "or_logf": (F, [F]), "or_log1pf": (F, [F]), "or_sigmoid": (F, [F]), "or_sqrt_softplus": (F, [F]),
@@ -75,9 +75,12 @@ def lib():
 
 
 def default_threads() -> int:
-    """Oracle worker threads: ORACLE_THREADS, else the CPUs available to this process, at most 16."""
+    """Oracle worker threads: ORACLE_THREADS, else OMP_NUM_THREADS, else the CPUs available to this process; at most
+    16 without ORACLE_THREADS, the CPU share one GPU gets on the benchmark hosts (whatever the host's core count)."""
     if os.environ.get("ORACLE_THREADS"):
         return int(os.environ["ORACLE_THREADS"])
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        return max(1, min(16, int(os.environ["OMP_NUM_THREADS"])))
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -122,11 +125,13 @@ def dequant_row(t, row, n) -> np.ndarray:
     return out
 
 
-def block_ints(t, row, xq, n):
+def block_ints(t, row, xq, n, scalar=False):
+    """The exact integers of every block of one weight row; scalar=True: the element-by-element restatement only."""
     row, xq = _c(row, np.uint8), _c(xq, np.uint8)
     nb = n // block_elems(t)
     si, sm = np.zeros(nb, np.int32), np.zeros(nb, np.int32)
-    if lib().or_block_ints(int(t), _p(row), _p(xq), n, _p(si), _p(sm)):
+    fn = lib().or_block_ints_scalar if scalar else lib().or_block_ints
+    if fn(int(t), _p(row), _p(xq), n, _p(si), _p(sm)):
         raise ValueError("or_block_ints failed")
     return si, sm
 

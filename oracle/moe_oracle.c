@@ -285,7 +285,7 @@ int or_dequant_row(int type, const uint8_t *row, int n, float *out) {
    K-quants: sumi = sum_j sc_j S_j, summ = sum_j m_j (bsums[2j] + bsums[2j+1]) (ggml q4_K/q5_K x q8_K);
    Q6_K: sumi = sum_g sc_g sum_16 (q6 - 32) y; IQ4_XS: sumi = sum_ib (ls - 32) sum_32 kv y (src/iq3s_dot.h:
    136-166); IQ2_XS: sumi = sum (2 sc + 1) sum_16 grid sign y; IQ4_NL x Q8_0: sumi = sum_32 kv q8. */
-static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *sumi, int32_t *summ) {
+static void block_ints_scalar(int type, const uint8_t *b, const uint8_t *y, int32_t *sumi, int32_t *summ) {
     int32_t si = 0, sm = 0;
     const int8_t *q8 = (const int8_t *) (y + (type == OR_IQ4_NL ? 2 : 4));
     switch (type) {
@@ -328,6 +328,77 @@ static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *su
     }
     *sumi = si; *summ = sm;
 }
+#if defined(__AVX2__)
+#include <immintrin.h>
+/* The same integers with AVX2 for the K-quants (the CPU baseline's speed; the scalar restatement above stays the
+   definition, and tests/test_oracle.py checks the two against each other).  Integer sums do not depend on their
+   order: maddubs forms exact int16 pair sums (|q y + q y| <= 63 * 127 * 2 < 2^15), madd with the broadcast scale
+   exact int32 products, and everything stays far below 2^31. */
+static inline int32_t hsum8_epi32(__m256i v) {
+    __m128i s = _mm_add_epi32(_mm256_castsi256_si128(v), _mm256_extracti128_si256(v, 1));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0x4E));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0xB1));
+    return _mm_cvtsi128_si32(s);
+}
+/* Q4_K / Q5_K: sub-block j's 32 values are the low (even j) or high (odd j) nibbles of qs[32 (j / 2) ..], plus bit j
+   of qh[l] as bit 4 for Q5_K; sumi = sum_j sc_j S_j, summ = sum_j m_j (bsums[2j] + bsums[2j+1]) */
+static void block_ints_q45k_avx2(int type, const uint8_t *b, const uint8_t *y, int32_t *sumi, int32_t *summ) {
+    const __m256i m4 = _mm256_set1_epi8(0x0F), one = _mm256_set1_epi8(1);
+    const int8_t *q8 = (const int8_t *) (y + 4);
+    int16_t bs[16]; memcpy(bs, y + 260, 32);
+    const uint8_t *qs = b + (type == OR_Q4_K ? 16 : 48);
+    const __m256i qh = type == OR_Q5_K ? _mm256_loadu_si256((const __m256i *) (b + 16)) : _mm256_setzero_si256();
+    __m256i acc = _mm256_setzero_si256();
+    int32_t sm = 0;
+    for (int j2 = 0; j2 < 4; ++j2) {
+        const __m256i raw = _mm256_loadu_si256((const __m256i *) (qs + 32 * j2));
+        __m256i v[2] = {_mm256_and_si256(raw, m4), _mm256_and_si256(_mm256_srli_epi16(raw, 4), m4)};
+        for (int h = 0; h < 2; ++h) {
+            const int j = 2 * j2 + h;
+            if (type == OR_Q5_K) v[h] = _mm256_or_si256(v[h], _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(qh, j), one), 4));
+            int sc, m; scale_min_k4(j, b + 4, &sc, &m);
+            const __m256i p16 = _mm256_maddubs_epi16(v[h], _mm256_loadu_si256((const __m256i *) (q8 + 32 * j)));
+            acc = _mm256_add_epi32(acc, _mm256_madd_epi16(p16, _mm256_set1_epi16((short) sc)));
+            sm += m * (bs[2 * j] + bs[2 * j + 1]);
+        }
+    }
+    *sumi = hsum8_epi32(acc); *summ = sm;
+}
+/* Q6_K: value e = 128 hf + 32 qt + l is nibble (qt >= 2) of ql[64 hf + 32 (qt & 1) + l] | bits 2 qt of qh[32 hf + l] << 4;
+   sum_g sc_g sum_16 (q6 - 32) y = sum_g sc_g sum_16 q6 y - 32 sum_g sc_g bsums[g] */
+static void block_ints_q6k_avx2(const uint8_t *b, const uint8_t *y, int32_t *sumi) {
+    const __m256i m4 = _mm256_set1_epi8(0x0F), m2 = _mm256_set1_epi8(0x03);
+    const int8_t *q8 = (const int8_t *) (y + 4), *sc = (const int8_t *) (b + 192);
+    int16_t bs[16]; memcpy(bs, y + 260, 32);
+    __m256i acc = _mm256_setzero_si256();
+    for (int hf = 0; hf < 2; ++hf) {
+        const __m256i l0 = _mm256_loadu_si256((const __m256i *) (b + 64 * hf)), l1 = _mm256_loadu_si256((const __m256i *) (b + 64 * hf + 32));
+        const __m256i h = _mm256_loadu_si256((const __m256i *) (b + 128 + 32 * hf));
+        for (int qt = 0; qt < 4; ++qt) {
+            const __m256i src = (qt & 1) ? l1 : l0;
+            const __m256i nib = qt >= 2 ? _mm256_and_si256(_mm256_srli_epi16(src, 4), m4) : _mm256_and_si256(src, m4);
+            const __m256i hb = _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(h, 2 * qt), m2), 4);
+            const __m256i q = _mm256_or_si256(nib, hb);
+            const __m256i p16 = _mm256_maddubs_epi16(q, _mm256_loadu_si256((const __m256i *) (q8 + 128 * hf + 32 * qt)));
+            const int g = 8 * hf + 2 * qt;
+            const __m256i s16 = _mm256_set_m128i(_mm_set1_epi16(sc[g + 1]), _mm_set1_epi16(sc[g]));
+            acc = _mm256_add_epi32(acc, _mm256_madd_epi16(p16, s16));
+        }
+    }
+    int32_t off = 0;
+    for (int g = 0; g < 16; ++g) off += sc[g] * bs[g];
+    *sumi = hsum8_epi32(acc) - 32 * off;
+}
+#endif
+
+static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *sumi, int32_t *summ) {
+#if defined(__AVX2__)
+    if (type == OR_Q4_K || type == OR_Q5_K) { block_ints_q45k_avx2(type, b, y, sumi, summ); return; }
+    if (type == OR_Q6_K) { block_ints_q6k_avx2(b, y, sumi); *summ = 0; return; }
+#endif
+    block_ints_scalar(type, b, y, sumi, summ);
+}
+
 static int dot_ok(int type) {
     return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_IQ4_XS || type == OR_IQ2_XS || type == OR_IQ4_NL;
 }
@@ -337,6 +408,14 @@ int or_block_ints(int type, const uint8_t *row, const void *xq, int n, int32_t *
     const size_t bb = or_block_bytes(type), yb = or_block_bytes(or_vec_dot_type(type));
     for (int ib = 0; ib < n / or_block_elems(type); ++ib)
         block_ints(type, row + ib * bb, (const uint8_t *) xq + ib * yb, sumi + ib, summ + ib);
+    return 0;
+}
+int or_block_ints_scalar(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ) {
+    if (!dot_ok(type) || n % or_block_elems(type)) return -1;
+    iq2xs_init();
+    const size_t bb = or_block_bytes(type), yb = or_block_bytes(or_vec_dot_type(type));
+    for (int ib = 0; ib < n / or_block_elems(type); ++ib)
+        block_ints_scalar(type, row + ib * bb, (const uint8_t *) xq + ib * yb, sumi + ib, summ + ib);
     return 0;
 }
 /* the contract's per-block fp32 fold, blocks accumulated in order */

@@ -64,6 +64,8 @@ int or_dequant_row(int type, const uint8_t *row, int n, float *out);
 /* exact integers of every block of one weight row against a quantized activation row:
    sumi[b], summ[b] (summ is 0 for types without mins) */
 int or_block_ints(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ);
+/* the same integers by the element-by-element restatement only (the K-quants' AVX2 path is checked against it) */
+int or_block_ints_scalar(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ);
 /* the contract's row dot product */
 float or_row_dot(int type, const uint8_t *row, const void *xq, int n);
 

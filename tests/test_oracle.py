@@ -320,6 +320,23 @@ def test_block_ints_brute_force(t):
             assert (si == bsi).all() and (sm == bsm).all(), f"{t.name} {name} row {r}"
 
 
+@pytest.mark.parametrize("t", [GType.Q4_K, GType.Q5_K, GType.Q6_K])
+def test_vector_block_ints_equal_scalar_restatement(t):
+    """The K-quants' AVX2 integers (the CPU baseline's path) equal the element-by-element restatement on every block,
+    for all the quantizer-test activation distributions, including blocks with extreme scales."""
+    n = 4096
+    rows = blocks(t, 16 * n // 256, 400 + int(t)).reshape(16, -1)
+    rows[0, :] = 0xFF            # every quant, scale and min at its maximum (the fp16 fields become NaN: ints only)
+    if t == GType.Q6_K:
+        rows[1].reshape(-1, 210)[:, 192:208] = 0x80   # int8 scales at -128
+    for name, x in x_distributions(n, seed=29).items():
+        xq = orc.quantize(GType.Q8_K, x)
+        for r in range(rows.shape[0]):
+            a = orc.block_ints(t, rows[r], xq, n)
+            b = orc.block_ints(t, rows[r], xq, n, scalar=True)
+            assert (a[0] == b[0]).all() and (a[1] == b[1]).all(), f"{t.name} {name} row {r}"
+
+
 @pytest.mark.parametrize("t", ALL)
 def test_row_dot_equals_fp64_of_dequantized_operands(t):
     """The block integers and their fp32 fold agree with sum(dequant(w) * dequant(q8(x))) in fp64 up to fp32 rounding."""
