@@ -190,7 +190,7 @@ def workloads_bench(args, dev, stream):
     shared expert, the router weights and the activations in and out."""
     res = {}
     for name, w in WORKLOADS.items():
-        if name in ("q4k_decode", "q4k_q6k_prefill512"):
+        if name in ("q4k_decode", "q4k_q6k_prefill512") or (args.workload and name not in args.workload):
             continue
         copies, n_in, nsteps = args.workload_copies, 4, 8
         g = torch.Generator(device=dev)
@@ -349,6 +349,10 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--workload-copies", type=int, default=2, help="weight copies per workload in the `workloads` object")
     ap.add_argument("--no-workloads", action="store_true", help="skip the `workloads` object (the other configured workloads)")
+    ap.add_argument("--workload", action="append", default=None, metavar="NAME",
+                    help="time only these workloads in the `workloads` object (repeatable; profiling runs)")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the headline prefill (profiling runs of decode / workloads only; prints no headline line)")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-oracle work for cpu_baseline (0: skip)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain copy kernel over MIB MiB (counter calibration under rocprofv3 --pmc)")
@@ -360,9 +364,11 @@ def main():
     stream = torch.cuda.Stream()
     if args.copy_probe:
         copy_probe(args.copy_probe, dev)
-    log("prefill: building layers and inputs")
-    pre, L0, W0, xs0, bs0 = prefill_bench(args, dev, stream)
-    log(f"prefill: {pre['tok_s']:.0f} tok/s, {pre['ms_step'] * 1e3:.1f} us/step")
+    pre = None
+    if not args.no_prefill:
+        log("prefill: building layers and inputs")
+        pre, L0, W0, xs0, bs0 = prefill_bench(args, dev, stream)
+        log(f"prefill: {pre['tok_s']:.0f} tok/s, {pre['ms_step'] * 1e3:.1f} us/step")
     dec, dec_layers = None, None
     if not args.no_decode:
         log("decode: building layers")
@@ -372,6 +378,9 @@ def main():
     if not args.no_workloads:
         log("workloads: the other configured shapes")
         wl = workloads_bench(args, dev, stream)
+    if pre is None:   # a profiling run: the parts it timed, no headline line
+        print(json.dumps({"decode": dec, "workloads": wl}), flush=True)
+        return
     cpu = None
     if args.cpu_budget > 0:
         log("cpu baseline: oracle on a sample of the prefill step")

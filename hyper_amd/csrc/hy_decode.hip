@@ -23,6 +23,24 @@ namespace hy {
 
 constexpr int DEC_MAXP = 8;        // passes of 8 items per wave: up to 64 items (256-value spans) per wave
 constexpr int DEC_ROUTE_NT = 8;    // tokens the fused router takes (more: the separate kernels)
+constexpr int DEC_Y_BYTES = 9344;  // LDS for one Q8 activation row: 32 Q8_K blocks (n <= 8192), or 256 Q8_0 blocks (8704 B)
+
+// Position of the items g, g + 8, g + 16, ... of a wave's flat item list, a list of units (a matrix row, or a pair's
+// row) of `per` 256-value spans each, without a division per item: advancing by 8 items moves q8 = 8 / per units and
+// r8 = 8 % per spans (both from the host), plus one unit when the span wraps.
+struct Cursor {
+    int u, s;   // unit, span in the unit
+    __device__ __forceinline__ void start(int g, int per) {
+        u = 0; s = g;
+        while (s >= per) { s -= per; ++u; }
+    }
+    __device__ __forceinline__ void next(int per, int q8, int r8) {
+        s += r8;
+        const int c = s >= per ? 1 : 0;
+        s -= c * per;
+        u += q8 + c;
+    }
+};
 
 // ---------------------------------------------------------------- k_router
 
@@ -98,10 +116,10 @@ __global__ __launch_bounds__(256) void k_router_q8(const float *__restrict__ W, 
     }
 }
 
-// ---------------------------------------------------------------- item dots against global Q8 rows
+// ---------------------------------------------------------------- item dots against Q8 rows in LDS
 
-// the integers of item `it` (256 values, span gi of a row) against the Q8 row `y` (global); K-quants: summed
-// over the 8 lanes (every lane of the group gets them)
+// the integers of item `it` (256 values, span gi of a row) against the Q8 row `y` (LDS); K-quants: summed over the
+// 8 lanes (every lane of the group gets them)
 template <int T>
 __device__ __forceinline__ float item_t(const Item<T> &it, const uint8_t *y, int gi, int L, bool valid, float *tv_out, int tv_idx) {
     if constexpr (T == IQ4_NL) {
@@ -144,7 +162,7 @@ template <int T, int V, int NP>
 __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev m, const float *__restrict__ logits, int ls, int ne, int k,
                                                                    const uint8_t *__restrict__ xq, int *__restrict__ ids,
                                                                    float *__restrict__ wts, float *__restrict__ sg, float *__restrict__ h,
-                                                                   int rw) {
+                                                                   int rw, int q8, int r8) {
     constexpr int VT = vec_dot_type(T), BE = block_elems(T);
     constexpr int SPAN_W = 256 / BE * block_bytes(T);
     constexpr int SPAN_Y = VT == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
@@ -154,10 +172,17 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     __shared__ int s_slot[64 * V];
     __shared__ uint2 grid[T == IQ2_XS ? 512 : 1];
     __shared__ float s_xd[DEC_GU_TV / 2];   // activation scales of the token's Q8 row, one per weight block
+    __shared__ __align__(16) uint8_t s_y[DEC_Y_BYTES];   // the token's Q8 row (every item reads its 256-value span here)
     const int p = blockIdx.y, t = p / k, j = p - t * k;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
     const int ff = m.ff, ng = m.n / 256, nb = m.n / BE;
     const uint8_t *y = xq + (size_t) t * ng * SPAN_Y;
+    // the Q8 row to LDS, a dword a thread per pass (row bytes ng SPAN_Y are a multiple of 4: 292 and 272 are)
+    auto stage_y = [&](int i0, int stride) {
+        const uint32_t *src = (const uint32_t *) y;
+        uint32_t *dst = (uint32_t *) s_y;
+        for (int i = i0; i < ng * SPAN_Y / 4; i += stride) dst[i] = src[i];
+    };
     const float *lg = logits + (size_t) t * ls;
     // the token's routing: every block of the token computes the same bits
     int e_sel;   // the expert of pair j
@@ -168,9 +193,10 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
         const float xd = tid < nb ? q8_scale<VT>(y, tid) : 0.0f;
         int er;
         float pr, tot, lsg;
-        route_rank8<V>(lg, ne, k, sg != nullptr, er, pr, tot, lsg, [&] {   // the slot table and scales share its barrier
+        route_rank8<V>(lg, ne, k, sg != nullptr, er, pr, tot, lsg, [&] {   // the slot table, scales and Q8 row share its barrier
             if (tid < ne) s_slot[tid] = sl;
             if (tid < nb) s_xd[tid] = xd;
+            stage_y(tid, 64 * DEC_GU_WAVES);
             if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
         });
         e_sel = __builtin_amdgcn_readlane(er, j);
@@ -186,6 +212,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
             const int i0 = (int) threadIdx.x - 64, stride = 64 * (DEC_GU_WAVES - 1);
             for (int ex = i0; ex < ne; ex += stride) s_slot[ex] = m.slot[ex];
             for (int b = i0; b < nb; b += stride) s_xd[b] = q8_scale<VT>(y, b);
+            stage_y(i0, stride);
         }
         if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
         lds_barrier();
@@ -198,23 +225,30 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     const int e = e_sel;
     const int slot = (e >= 0 && e < ne) ? s_slot[e] : -1;
     if (slot < 0) return;   // uniform over the block: the pair's h rows are not written
-    // the wave's rows row0 .. row0 + rw - 1, each 2 ng items (gate spans, then up spans); rows past ff sit out
-    const int per_row = 2 * ng, nwi = rw * per_row, row0 = (blockIdx.x * DEC_GU_WAVES + wave) * rw;
+    // the wave's rows row0 .. row0 + rw - 1, each 2 ng items (gate spans, then up spans): unit u = 2 r + matrix; lane
+    // group g takes items g, g + 8, ... (a cursor over units and spans); rows past ff sit out
+    const int nunits = 2 * rw, nwi = nunits * ng, row0 = (blockIdx.x * DEC_GU_WAVES + wave) * rw;
     const uint8_t *Wg = m.gate + (size_t) slot * m.gate_bytes, *Wu = m.up + (size_t) slot * m.gate_bytes;
     Item<T> it[NP];
+    Cursor lc;
+    lc.start(g, ng);
 #pragma unroll
     for (int ps = 0; ps < NP; ++ps) {
-        const int i = g + 8 * ps, r = i / per_row, ii = i - r * per_row, mat = ii >= ng, gi = ii - mat * ng;
-        if (i < nwi && row0 + r < ff) it[ps].load((mat ? Wu : Wg) + tiled_off(row0 + r, gi, ng, SPAN_W), L);
+        const int r = lc.u >> 1;
+        if (lc.u < nunits && row0 + r < ff) it[ps].load(((lc.u & 1) ? Wu : Wg) + tiled_off(row0 + r, lc.s, ng, SPAN_W), L);
+        lc.next(ng, q8, r8);
     }
     float *tw = tv[wave];
+    Cursor cc;
+    cc.start(g, ng);
 #pragma unroll
     for (int ps = 0; ps < NP; ++ps) {
         if (8 * ps >= nwi) break;   // wave-uniform
-        const int i = g + 8 * ps, r = i / per_row, ii = i - r * per_row, mat = ii >= ng, gi = ii - mat * ng;
-        const bool valid = i < nwi && row0 + r < ff;
+        const int r = cc.u >> 1, mat = cc.u & 1, gi = cc.s;
+        const bool valid = cc.u < nunits && row0 + r < ff;
         if constexpr (T == IQ2_XS) it[ps].grid = grid;
-        item_t<T>(it[ps], y, gi, L, valid, tw, r * 2 * nb + mat * nb + (T == IQ4_NL ? 8 * gi : gi));
+        item_t<T>(it[ps], s_y, gi, L, valid, tw, r * 2 * nb + mat * nb + (T == IQ4_NL ? 8 * gi : gi));
+        cc.next(ng, q8, r8);
     }
     lds_barrier();
     // the folds, in block order, by wave 0: lane l takes the block's row l (wave l / rw, its row l % rw); eight
@@ -245,7 +279,7 @@ constexpr int DEC_DN_HQ = 32768;      // LDS bytes for the token's k quantized h
 template <int T, int NP>
 __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, const float *__restrict__ h, const int *__restrict__ ids,
                                                                const float *__restrict__ wts, int k, const float *__restrict__ shexp,
-                                                               const float *__restrict__ sg, float *__restrict__ out, int res) {
+                                                               const float *__restrict__ sg, float *__restrict__ out, int res, int q8, int r8) {
     constexpr int VT = vec_dot_type(T), BE = block_elems(T);
     constexpr int SPAN_W = 256 / BE * block_bytes(T);
     constexpr int SPAN_Y = VT == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
@@ -309,13 +343,18 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     const uint64_t okm = __ballot(my_slot >= 0);
     auto pair_ok = [&](int j) { return (okm >> j) & 1; };
     Item<T> it[NP];
+    // item i = pair j's span gi; lane group g takes items g, g + 8, ... (cursors over pairs and spans: one for the loads,
+    // one for the dots, each moving 8 items a pass)
+    Cursor lc, cc;
+    lc.start(g, ng);
+    cc.start(g, ng);
     auto load_round = [&](int base) {
 #pragma unroll
         for (int ps = 0; ps < NP; ++ps) {
-            const int i = base + g + 8 * ps;
-            const int j = i / ng, gi = i - j * ng;
+            const int i = base + g + 8 * ps, j = lc.u, gi = lc.s;
             const int sl = __shfl(my_slot, j < 64 ? j : 0);
             if (i < items && row_ok && sl >= 0) it[ps].load(m.down + (size_t) sl * m.down_bytes + tiled_off(row, gi, ng, SPAN_W), L);
+            lc.next(ng, q8, r8);
         }
     };
     // the first round of weight bytes goes out before the hidden rows are quantized (wave-uniform branches below)
@@ -358,10 +397,11 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
         for (int ps = 0; ps < NP; ++ps) {
             const int i = base + g + 8 * ps;
             if (base + 8 * ps >= items) break;   // wave-uniform
-            const int j = i / ng, gi = i - j * ng;
+            const int j = cc.u, gi = cc.s;
             const bool valid = i < items && pair_ok(j);
             if constexpr (T == IQ2_XS) it[ps].grid = grid;
             item_t<T>(it[ps], hq + (size_t) j * ng * SPAN_Y, gi, L, valid, tw, j * nb + (T == IQ4_NL ? 8 * gi : gi));
+            cc.next(ng, q8, r8);
         }
     }
     wave_lds_sync();
@@ -433,7 +473,8 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
     dim3 grid((m.ff + DEC_GU_WAVES * rw - 1) / (DEC_GU_WAVES * rw), nt * k);
     const int V = (ne + 63) / 64;
     const int np = (rw * 2 * ng + 7) / 8;   // passes of 8 items
-#define HY_RGU(VV, NN) hipLaunchKernelGGL((k_route_gate_up<TT, VV, NN>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, rw)
+    const int q8 = 8 / ng, r8 = 8 % ng;   // the item cursor's step
+#define HY_RGU(VV, NN) hipLaunchKernelGGL((k_route_gate_up<TT, VV, NN>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, rw, q8, r8)
 #define HY_RGU_V(NN) if (V <= 1) HY_RGU(1, NN); else if (V <= 2) HY_RGU(2, NN); else if (V <= 4) HY_RGU(4, NN); else if (V <= 8) HY_RGU(8, NN); else HY_RGU(16, NN);
     HY_DEC_SWITCH(m.tg, {
         if (np <= 2) { HY_RGU_V(2) } else if (np <= 4) { HY_RGU_V(4) } else { HY_RGU_V(8) }
@@ -453,7 +494,8 @@ int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const f
     if (nt == 0) return HY_OK;
     dim3 grid((m.n + DEC_DN_WAVES - 1) / DEC_DN_WAVES, nt);
     const int np = (k * ng + 7) / 8;   // passes of 8 items (more than 8: rounds)
-#define HY_DN(NN) hipLaunchKernelGGL((k_dec_down<TT, NN>), grid, dim3(64 * DEC_DN_WAVES), 0, s, m, h, ids, wts, k, shexp, sg, out, res)
+    const int q8 = 8 / ng, r8 = 8 % ng;   // the item cursors' step
+#define HY_DN(NN) hipLaunchKernelGGL((k_dec_down<TT, NN>), grid, dim3(64 * DEC_DN_WAVES), 0, s, m, h, ids, wts, k, shexp, sg, out, res, q8, r8)
     HY_DEC_SWITCH(m.td, {
         if (np <= 2) HY_DN(2); else if (np <= 4) HY_DN(4); else HY_DN(8);
         return check_launch("hy_moe_down_reduce");
