@@ -290,6 +290,28 @@ int hy_moe_route_gate_up(const hy_moe_dev *m, const float *logits, int ls, int n
     return launch_route_gate_up(*m, logits, ls, n_expert, k, xq, ids, wts, sg, h, nt, s);
 }
 
+int hy_moe_route_gate_up_q8(const hy_moe_dev *m, const float *logits, int ls, int n_expert, int k, const void *xq, int32_t *ids,
+                            float *wts, float *sg, float *h, void *hq, int nt, hipStream_t s) {
+    if (!hq) { set_error("hy_moe_route_gate_up_q8: bad argument"); return HY_EINVAL; }
+    int rc = check_dev(m, "hy_moe_route_gate_up_q8", true, false);
+    if (rc) return rc;
+    if (!logits || !xq || !ids || !wts || !h || nt < 0) { set_error("hy_moe_route_gate_up_q8: bad argument"); return HY_EINVAL; }
+    if (n_expert <= 0 || n_expert > 1024 || n_expert > m->n_expert) { set_error("hy_moe_route_gate_up_q8: n_expert %d out of range", n_expert); return HY_EBAD_SHAPE; }
+    if (k <= 0 || k > 64 || k > n_expert) { set_error("hy_moe_route_gate_up_q8: k = %d out of range", k); return HY_EBAD_SHAPE; }
+    if (ls < n_expert || (sg && ls <= n_expert)) { set_error("hy_moe_route_gate_up_q8: logit stride %d too small", ls); return HY_EBAD_SHAPE; }
+    if ((uintptr_t) xq & 3) { set_error("hy_moe_route_gate_up_q8: xq must be 4-byte aligned"); return HY_EBAD_SHAPE; }
+    return launch_route_gate_up(*m, logits, ls, n_expert, k, xq, ids, wts, sg, h, nt, s, (uint8_t *) hq);
+}
+
+int hy_moe_down_reduce_q8(const hy_moe_dev *m, const void *hq, const int32_t *ids, const float *wts, int k, const float *shexp,
+                          const float *sg, float *out, int residual, int nt, hipStream_t s) {
+    int rc = check_dev(m, "hy_moe_down_reduce_q8", false, true);
+    if (rc) return rc;
+    if (!hq || !ids || !wts || !out || k <= 0 || k > 64 || nt < 0) { set_error("hy_moe_down_reduce_q8: bad argument"); return HY_EINVAL; }
+    if (!aligned16(hq)) { set_error("hy_moe_down_reduce_q8: hq must be 16-byte aligned"); return HY_EBAD_SHAPE; }
+    return launch_dec_down(*m, nullptr, ids, wts, k, shexp, sg, out, nt, s, residual ? 1 : 0, (const uint8_t *) hq);
+}
+
 int hy_dequant_row(int type, const uint8_t *row, int n, float *out, hipStream_t s) {
     if (!row || !out || n < 0) { set_error("hy_dequant_row: bad argument"); return HY_EINVAL; }
     if (!(dot_type(type) || type == Q8_0 || type == Q8_K)) { set_error("hy_dequant_row: type %d", type); return HY_EUNSUPPORTED_TYPE; }

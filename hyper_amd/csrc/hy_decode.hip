@@ -158,15 +158,18 @@ constexpr int DEC_GU_WAVES = 8;      // waves per block, rw ff rows each
 #endif
 constexpr int DEC_GU_BLOCKS = HY_DEC_GU_BLOCKS;   // grid size the rows per wave aim below
 
-template <int T, int V, int NP>
+// HQ: the block's 8 rw = 32 rows form one Q8_0 block of every pair's hidden row, and the fold also writes it to hq
+// (the down kernel then reads the hidden quantized instead of quantizing it in every block)
+template <int T, int V, int NP, bool HQ = false>
 __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev m, const float *__restrict__ logits, int ls, int ne, int k,
                                                                    const uint8_t *__restrict__ xq, int *__restrict__ ids,
                                                                    float *__restrict__ wts, float *__restrict__ sg, float *__restrict__ h,
-                                                                   int rw, int q8, int r8) {
+                                                                   int rw, int q8, int r8, uint8_t *__restrict__ hq) {
     constexpr int VT = vec_dot_type(T), BE = block_elems(T);
     constexpr int SPAN_W = 256 / BE * block_bytes(T);
     constexpr int SPAN_Y = VT == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
-    __shared__ float tv[DEC_GU_WAVES][DEC_GU_TV];
+    constexpr int TVN = HQ ? 2 * DEC_GU_TV : DEC_GU_TV;   // fold inputs per wave (HQ: 4 rows)
+    __shared__ float tv[DEC_GU_WAVES][TVN];
     __shared__ int s_ids[64];
     __shared__ float s_wts[64], s_sg;
     __shared__ int s_slot[64 * V];
@@ -230,44 +233,51 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     const int nunits = 2 * rw, nwi = nunits * ng, row0 = (blockIdx.x * DEC_GU_WAVES + wave) * rw;
     const uint8_t *Wg = m.gate + (size_t) slot * m.gate_bytes, *Wu = m.up + (size_t) slot * m.gate_bytes;
     Item<T> it[NP];
-    Cursor lc;
-    lc.start(g, ng);
-#pragma unroll
-    for (int ps = 0; ps < NP; ++ps) {
-        const int r = lc.u >> 1;
-        if (lc.u < nunits && row0 + r < ff) it[ps].load(((lc.u & 1) ? Wu : Wg) + tiled_off(row0 + r, lc.s, ng, SPAN_W), L);
-        lc.next(ng, q8, r8);
-    }
     float *tw = tv[wave];
-    Cursor cc;
+    Cursor lc, cc;
+    lc.start(g, ng);
     cc.start(g, ng);
+    for (int base = 0; base < nwi; base += 8 * NP) {   // wave-uniform rounds of up to 8 NP items (HQ: two)
 #pragma unroll
-    for (int ps = 0; ps < NP; ++ps) {
-        if (8 * ps >= nwi) break;   // wave-uniform
-        const int r = cc.u >> 1, mat = cc.u & 1, gi = cc.s;
-        const bool valid = cc.u < nunits && row0 + r < ff;
-        if constexpr (T == IQ2_XS) it[ps].grid = grid;
-        item_t<T>(it[ps], s_y, gi, L, valid, tw, r * 2 * nb + mat * nb + (T == IQ4_NL ? 8 * gi : gi));
-        cc.next(ng, q8, r8);
+        for (int ps = 0; ps < NP; ++ps) {
+            const int r = lc.u >> 1;
+            if (lc.u < nunits && row0 + r < ff) it[ps].load(((lc.u & 1) ? Wu : Wg) + tiled_off(row0 + r, lc.s, ng, SPAN_W), L);
+            lc.next(ng, q8, r8);
+        }
+#pragma unroll
+        for (int ps = 0; ps < NP; ++ps) {
+            if (base + 8 * ps >= nwi) break;   // wave-uniform
+            const int r = cc.u >> 1, mat = cc.u & 1, gi = cc.s;
+            const bool valid = cc.u < nunits && row0 + r < ff;
+            if constexpr (T == IQ2_XS) it[ps].grid = grid;
+            item_t<T>(it[ps], s_y, gi, L, valid, tw, r * 2 * nb + mat * nb + (T == IQ4_NL ? 8 * gi : gi));
+            cc.next(ng, q8, r8);
+        }
     }
     lds_barrier();
     // the folds, in block order, by wave 0: lane l takes the block's row l (wave l / rw, its row l % rw); eight
     // blocks' inputs per LDS round trip, then the fma chain
-    if (wave != 0 || lane >= DEC_GU_WAVES * rw) return;
+    if (wave != 0 || (!HQ && lane >= DEC_GU_WAVES * rw)) return;
     const int row = blockIdx.x * DEC_GU_WAVES * rw + lane;
-    if (row >= ff) return;
-    const float *tg = tv[lane / rw] + (lane % rw) * 2 * nb;
-    float ag = 0.0f, au = 0.0f;
-    for (int b0 = 0; b0 < nb; b0 += 8) {
-        float xa[8], ga[8], ua[8];
+    if (!HQ && row >= ff) return;
+    float hv = 0.0f;
+    if (lane < DEC_GU_WAVES * rw) {   // (HQ: lanes 32-63 stay for the quantizer's cross-lane max)
+        const float *tg = tv[lane / rw] + (lane % rw) * 2 * nb;
+        float ag = 0.0f, au = 0.0f;
+        for (int b0 = 0; b0 < nb; b0 += 8) {
+            float xa[8], ga[8], ua[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (b0 + u < nb) { xa[u] = s_xd[b0 + u]; ga[u] = tg[b0 + u]; ua[u] = tg[nb + b0 + u]; }
+            for (int u = 0; u < 8; ++u)
+                if (b0 + u < nb) { xa[u] = s_xd[b0 + u]; ga[u] = tg[b0 + u]; ua[u] = tg[nb + b0 + u]; }
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (b0 + u < nb) { ag = __builtin_fmaf(xa[u], ga[u], ag); au = __builtin_fmaf(xa[u], ua[u], au); }
+            for (int u = 0; u < 8; ++u)
+                if (b0 + u < nb) { ag = __builtin_fmaf(xa[u], ga[u], ag); au = __builtin_fmaf(xa[u], ua[u], au); }
+        }
+        hv = hy_swiglu(ag, au, m.clamp);
+        h[(size_t) p * ff + row] = hv;
     }
-    h[(size_t) p * ff + row] = hy_swiglu(ag, au, m.clamp);
+    if constexpr (HQ)   // lanes 0-31: the 32 values of Q8_0 block blockIdx.x of pair p's hidden row
+        q8_0_pair_vals(hv, hq + ((size_t) p * (ff / 32) + blockIdx.x) * Q8_0_BYTES, false, Q8_0_BYTES, 2);
 }
 
 // ---------------------------------------------------------------- k_dec_down
@@ -279,7 +289,8 @@ constexpr int DEC_DN_HQ = 32768;      // LDS bytes for the token's k quantized h
 template <int T, int NP>
 __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, const float *__restrict__ h, const int *__restrict__ ids,
                                                                const float *__restrict__ wts, int k, const float *__restrict__ shexp,
-                                                               const float *__restrict__ sg, float *__restrict__ out, int res, int q8, int r8) {
+                                                               const float *__restrict__ sg, float *__restrict__ out, int res, int q8, int r8,
+                                                               const uint8_t *__restrict__ hqg) {
     constexpr int VT = vec_dot_type(T), BE = block_elems(T);
     constexpr int SPAN_W = 256 / BE * block_bytes(T);
     constexpr int SPAN_Y = VT == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
@@ -334,7 +345,19 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
             }
         }
     };
-    hload(0);
+    // hqg (Q8_0 partner types): the token's k hidden rows already quantized (rows of nb Q8_0 blocks, consecutive for
+    // the token's pairs, a multiple of 272 bytes each): brought in as 16-byte pieces instead of loaded and quantized
+    constexpr int HQV = DEC_DN_HQ / (16 * 64 * DEC_DN_WAVES);
+    uint4 hv16[HQV];
+    const int n16 = VT == Q8_0 && hqg ? k * nb * Q8_0_BYTES / 16 : 0;
+    if (n16) {
+        const uint4 *src = (const uint4 *) (hqg + (size_t) t * k * nb * Q8_0_BYTES);
+#pragma unroll
+        for (int i = 0; i < HQV; ++i)
+            if (tid + i * 64 * DEC_DN_WAVES < n16) hv16[i] = src[tid + i * 64 * DEC_DN_WAVES];
+    } else {
+        hload(0);
+    }
     s_slot[tid] = sl0;
     s_slot[tid + 64 * DEC_DN_WAVES] = sl1;
     lds_barrier();
@@ -385,8 +408,14 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
             }
         }
     };
-    hquant(0);
-    for (int ub = UB; ub < units; ub += UB) { hload(ub); hquant(ub); }
+    if (n16) {
+#pragma unroll
+        for (int i = 0; i < HQV; ++i)
+            if (tid + i * 64 * DEC_DN_WAVES < n16) ((uint4 *) hq)[tid + i * 64 * DEC_DN_WAVES] = hv16[i];
+    } else {
+        hquant(0);
+        for (int ub = UB; ub < units; ub += UB) { hload(ub); hquant(ub); }
+    }
     if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
     lds_barrier();
     if (!row_ok) return;   // wave-uniform; no block barrier follows
@@ -461,9 +490,22 @@ int launch_router_q8(const float *W, int rows, int kdim, const float *x, int xs,
 }
 
 int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int ne, int k, const void *xq, int *ids, float *wts, float *sg,
-                         float *h, int nt, hipStream_t s) {
+                         float *h, int nt, hipStream_t s, uint8_t *hq) {
     const int ng = m.n / 256, nb = m.n / block_elems(m.tg);
     if (2 * ng > 8 * DEC_MAXP || 2 * nb > DEC_GU_TV) { set_error("hy_moe_route_gate_up: n = %d exceeds %d", m.n, 256 * 4 * DEC_MAXP); return HY_EBAD_SHAPE; }
+    if (hq) {   // the Q8_0 hidden as well: 32-row blocks (rw 4), items and fold inputs within the HQ instantiation's limits
+        if (m.tg != IQ4_NL || m.td != IQ4_NL || 4 * 2 * nb > 2 * DEC_GU_TV) {
+            set_error("hy_moe_route_gate_up_q8: needs IQ4_NL gate/up and down weights and n <= 4096 (types %d/%d, n %d)", m.tg, m.td, m.n);
+            return HY_EUNSUPPORTED_TYPE;
+        }
+        if (nt == 0) return HY_OK;
+        const int V = (ne + 63) / 64, q8 = 8 / ng, r8 = 8 % ng;
+        dim3 grid(m.ff / 32, nt * k);
+#define HY_RGUQ(VV) hipLaunchKernelGGL((k_route_gate_up<IQ4_NL, VV, 8, true>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, 4, q8, r8, hq)
+        if (V <= 1) HY_RGUQ(1); else if (V <= 2) HY_RGUQ(2); else if (V <= 4) HY_RGUQ(4); else if (V <= 8) HY_RGUQ(8); else HY_RGUQ(16);
+#undef HY_RGUQ
+        return check_launch("hy_moe_route_gate_up_q8");
+    }
     if (nt == 0) return HY_OK;
     // rows per wave: every block routes its token again, so the grid is kept near DEC_GU_BLOCKS blocks, within the
     // item registers (rw 2 ng <= 8 DEC_MAXP) and the fold inputs (rw 2 nb <= DEC_GU_TV)
@@ -474,7 +516,7 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
     const int V = (ne + 63) / 64;
     const int np = (rw * 2 * ng + 7) / 8;   // passes of 8 items
     const int q8 = 8 / ng, r8 = 8 % ng;   // the item cursor's step
-#define HY_RGU(VV, NN) hipLaunchKernelGGL((k_route_gate_up<TT, VV, NN>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, rw, q8, r8)
+#define HY_RGU(VV, NN) hipLaunchKernelGGL((k_route_gate_up<TT, VV, NN>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, rw, q8, r8, nullptr)
 #define HY_RGU_V(NN) if (V <= 1) HY_RGU(1, NN); else if (V <= 2) HY_RGU(2, NN); else if (V <= 4) HY_RGU(4, NN); else if (V <= 8) HY_RGU(8, NN); else HY_RGU(16, NN);
     HY_DEC_SWITCH(m.tg, {
         if (np <= 2) { HY_RGU_V(2) } else if (np <= 4) { HY_RGU_V(4) } else { HY_RGU_V(8) }
@@ -484,18 +526,27 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
 #undef HY_RGU
 }
 
-// the fused decode down + combine; shapes beyond its LDS budget return HY_EUNSUPPORTED_TYPE (caller falls back)
-int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp, const float *sg,
-                    float *out, int nt, hipStream_t s, int res) {
+static bool dec_down_fits(const hy_moe_dev &m, int k) {
     const int vt = vec_dot_type(m.td), ng = m.ff / 256, nb = m.ff / block_elems(m.td);
     const int span_y = vt == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
-    if (k > 64 || k * nb > DEC_DN_TV || (size_t) k * ng * span_y > (size_t) DEC_DN_HQ || m.n_expert > 2 * 64 * DEC_DN_WAVES)
+    return k <= 64 && k * nb <= DEC_DN_TV && (size_t) k * ng * span_y <= (size_t) DEC_DN_HQ && m.n_expert <= 2 * 64 * DEC_DN_WAVES;
+}
+bool dec_down_takes_q8(const hy_moe_dev &m, int k) { return vec_dot_type(m.td) == Q8_0 && dec_down_fits(m, k); }
+
+// the fused decode down + combine; shapes beyond its LDS budget return HY_EUNSUPPORTED_TYPE (caller falls back)
+int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp, const float *sg,
+                    float *out, int nt, hipStream_t s, int res, const uint8_t *hq) {
+    const int vt = vec_dot_type(m.td), ng = m.ff / 256;
+    if (hq && vt != Q8_0) { set_error("hy_moe_down_reduce_q8: down type %d does not take Q8_0 rows", m.td); return HY_EUNSUPPORTED_TYPE; }
+    if (!dec_down_fits(m, k)) {
+        if (hq) set_error("hy_moe_down_reduce_q8: k * ff = %d * %d exceeds the kernel's hidden-row budget", k, m.ff);
         return HY_EUNSUPPORTED_TYPE;
+    }
     if (nt == 0) return HY_OK;
     dim3 grid((m.n + DEC_DN_WAVES - 1) / DEC_DN_WAVES, nt);
     const int np = (k * ng + 7) / 8;   // passes of 8 items (more than 8: rounds)
     const int q8 = 8 / ng, r8 = 8 % ng;   // the item cursors' step
-#define HY_DN(NN) hipLaunchKernelGGL((k_dec_down<TT, NN>), grid, dim3(64 * DEC_DN_WAVES), 0, s, m, h, ids, wts, k, shexp, sg, out, res, q8, r8)
+#define HY_DN(NN) hipLaunchKernelGGL((k_dec_down<TT, NN>), grid, dim3(64 * DEC_DN_WAVES), 0, s, m, h, ids, wts, k, shexp, sg, out, res, q8, r8, hq)
     HY_DEC_SWITCH(m.td, {
         if (np <= 2) HY_DN(2); else if (np <= 4) HY_DN(4); else HY_DN(8);
         return check_launch("hy_moe_down_reduce");

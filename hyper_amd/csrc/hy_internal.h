@@ -34,10 +34,14 @@ int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int
                      const float *wts, float *y, hipStream_t s);
 int launch_router_q8(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
                      int vtype, void *xq, int nt, hipStream_t s);
+// hq: also write the Q8_0 rows of h (down types whose partner is Q8_0); HY_EUNSUPPORTED_TYPE where that does not apply
 int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int ne, int k, const void *xq, int *ids, float *wts, float *sg,
-                         float *h, int nt, hipStream_t s);
+                         float *h, int nt, hipStream_t s, uint8_t *hq = nullptr);
+// whether launch_dec_down runs its fused kernel (not HY_EUNSUPPORTED_TYPE) for this layer and k
+bool dec_down_takes_q8(const hy_moe_dev &m, int k);
+// hq: the hidden as Q8_0 rows (from launch_route_gate_up) instead of h
 int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, int k, const float *shexp, const float *sg,
-                    float *out, int nt, hipStream_t s, int res = 0);
+                    float *out, int nt, hipStream_t s, int res = 0, const uint8_t *hq = nullptr);
 int launch_dequant_row(int type, const uint8_t *row, int n, float *out, hipStream_t s);
 int launch_block_ints(int type, const uint8_t *rows, size_t row_bytes, int nrows, const void *xq, int n, int *sumi, int *summ,
                       hipStream_t s);

@@ -42,7 +42,7 @@ static int shared_tables(SharedTables &out) {
 
 // workspace layout: each piece 256-byte aligned
 struct DecodeLayout {
-    size_t logits, ids, wts, sg, xq, h, sh_h, sh_y, total;
+    size_t logits, ids, wts, sg, xq, h, hq, sh_h, sh_y, total;
 };
 static size_t up256(size_t v) { return (v + 255) & ~(size_t) 255; }
 static DecodeLayout decode_layout(const hy_moe_dev &m, int rows, int k, const hy_moe_dev *S, int nt) {
@@ -57,6 +57,7 @@ static DecodeLayout decode_layout(const hy_moe_dev &m, int rows, int k, const hy
     L.sg = take((size_t) nt * 4);
     L.xq = take((size_t) nt * xq_row);
     L.h = take((size_t) nt * k * m.ff * 4);
+    L.hq = vec_dot_type(m.td) == Q8_0 ? take((size_t) nt * k * (m.ff / 32) * Q8_0_BYTES) : 0;   // the hidden as Q8_0 rows
     L.sh_h = S ? take((size_t) nt * S->ff * 4) : 0;
     L.sh_y = S ? take((size_t) nt * m.n * 4) : 0;
     L.total = o;
@@ -100,9 +101,17 @@ int run_decode(const hy_moe_dev &m, const float *W_r, int rows, const float *x, 
         if (rc == HY_EUNSUPPORTED_TYPE) rc = launch_down_reduce(*S, sh_h, T.ids, T.wts, 1, nullptr, nullptr, shexp, nt, s);
         if (rc) return rc;
     }
-    if ((rc = launch_route_gate_up(m, logits, rows, E, k, xq, ids, wts, gate_logit ? sg : nullptr, h, nt, s))) return rc;
+    // down types with a Q8_0 partner: gate/up also writes the hidden as Q8_0 rows, which the down kernel reads (shapes
+    // beyond either kernel's limits take the fp32 hidden)
+    uint8_t *hq = m.tg == IQ4_NL && dec_down_takes_q8(m, k) ? ws + L.hq : nullptr;
+    rc = launch_route_gate_up(m, logits, rows, E, k, xq, ids, wts, gate_logit ? sg : nullptr, h, nt, s, hq);
+    if (rc == HY_EUNSUPPORTED_TYPE && hq) {
+        hq = nullptr;
+        rc = launch_route_gate_up(m, logits, rows, E, k, xq, ids, wts, gate_logit ? sg : nullptr, h, nt, s);
+    }
+    if (rc) return rc;
     const float *g = gate_logit ? sg : nullptr;
-    rc = launch_dec_down(m, h, ids, wts, k, shexp, g, out, nt, s, residual ? 1 : 0);
+    rc = launch_dec_down(m, h, ids, wts, k, shexp, g, out, nt, s, residual ? 1 : 0, hq);
     if (rc == HY_EUNSUPPORTED_TYPE) rc = launch_down_reduce(m, h, ids, wts, k, shexp, g, out, nt, s, residual ? 1 : 0);
     return rc;
 }

@@ -172,6 +172,18 @@ def moe_route_gate_up(m: MoeDev, logits, ls, n_expert, k, xq, ids, wts, sg, h, n
     check(lib().hy_moe_route_gate_up(m.ref, _p(logits), ls, n_expert, k, _p(xq), _p(ids), _p(wts), _p(sg), _p(h), nt, _s(stream)))
 
 
+def moe_route_gate_up_q8(m: MoeDev, logits, ls, n_expert, k, xq, ids, wts, sg, h, hq, nt, stream=None):
+    """moe_route_gate_up that also writes the hidden rows as Q8_0 blocks (down types with a Q8_0 partner)."""
+    check(lib().hy_moe_route_gate_up_q8(m.ref, _p(logits), ls, n_expert, k, _p(xq), _p(ids), _p(wts), _p(sg), _p(h), _p(hq), nt,
+                                        _s(stream)))
+
+
+def moe_down_reduce_q8(m: MoeDev, hq, ids, wts, k, shexp, sg, out, residual, nt, stream=None):
+    """moe_down_reduce (or its residual form) from the Q8_0 hidden rows of moe_route_gate_up_q8."""
+    check(lib().hy_moe_down_reduce_q8(m.ref, _p(hq), _p(ids), _p(wts), k, _p(shexp), _p(sg), _p(out), int(bool(residual)), nt,
+                                      _s(stream)))
+
+
 def dequant_row(type_, row, n, out, stream=None):
     check(lib().hy_dequant_row(int(type_), _p(row), n, _p(out), _s(stream)))
 
@@ -223,6 +235,11 @@ class MoeLayerRunner:
         self.vg, self.vd = vec_dot_type(L.tg), vec_dot_type(L.td)
         self.xq = torch.empty(T * q8_row_bytes(self.vg, self.d), dtype=torch.uint8, device=device)
         self.hq = torch.empty(P * q8_row_bytes(self.vd, self.ff), dtype=torch.uint8, device=device)
+        # decode hands the hidden over as Q8_0 rows where the down type's partner is Q8_0, within the kernels' limits
+        # (n <= 4096; k * ff / 32 <= 512 blocks and k * ff / 32 * 34 bytes <= 32 KiB per token)
+        nbh = self.ff // 32
+        self.dec_hq = (router == "softmax" and L.tg == GType.IQ4_NL and L.td == GType.IQ4_NL and self.d <= 4096 and self.k * nbh <= 512
+                       and self.k * nbh * 34 <= 32768 and self.E <= 1024)
         if shared is not None:
             S = shared.layer
             self.sh_ids = torch.zeros(T, **i32)
@@ -307,6 +324,12 @@ class MoeLayerRunner:
         if self.shared is not None:
             self._shared_decode(x, nt, stream)
             shexp = self.sh_y
+        if self.dec_hq:
+            moe_route_gate_up_q8(self.dev, self.logits, self.ls, self.E, self.k, self.xq, self.ids, self.wts, self.sg, self.h, self.hq,
+                                 nt, stream)
+            out = self.out if resid is None else resid
+            moe_down_reduce_q8(self.dev, self.hq, self.ids, self.wts, self.k, shexp, self.sg, out, resid is not None, nt, stream)
+            return out[:nt]
         if self.router == "softmax":
             moe_route_gate_up(self.dev, self.logits, self.ls, self.E, self.k, self.xq, self.ids, self.wts, self.sg, self.h, nt, stream)
         else:   # the fused route + gate/up kernel routes by softmax: route first, then the gate/up GEMV by ids

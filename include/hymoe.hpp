@@ -168,6 +168,16 @@ inline void moe_route_gate_up(const MoeDev &m, const float *logits, int ls, int 
                               float *sg, float *h, int nt, hipStream_t s) {
     check(hy_moe_route_gate_up(&m, logits, ls, n_expert, k, xq, ids, wts, sg, h, nt, s));
 }
+// moe_route_gate_up that also writes the hidden rows as Q8_0 blocks, and the down + combine that reads them (down types
+// whose partner is Q8_0)
+inline void moe_route_gate_up_q8(const MoeDev &m, const float *logits, int ls, int n_expert, int k, const void *xq, int *ids, float *wts,
+                                 float *sg, float *h, void *hq, int nt, hipStream_t s) {
+    check(hy_moe_route_gate_up_q8(&m, logits, ls, n_expert, k, xq, ids, wts, sg, h, hq, nt, s));
+}
+inline void moe_down_reduce_q8(const MoeDev &m, const void *hq, const int *ids, const float *wts, int k, const float *shexp,
+                               const float *sg, float *out, int residual, int nt, hipStream_t s) {
+    check(hy_moe_down_reduce_q8(&m, hq, ids, wts, k, shexp, sg, out, residual, nt, s));
+}
 // one layer's decode step (src/engine4.cu:795-890) on a caller workspace of moe_decode_ws_bytes(...) bytes
 inline size_t moe_decode_ws_bytes(const MoeDev &m, int rows, int k, const MoeDev *shared, int nt) {
     return hy_moe_decode_ws_bytes(&m, rows, k, shared, nt);
