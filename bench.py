@@ -162,6 +162,7 @@ def decode_bench(args, dev, stream):
     xs = activations(64, d, g, dev)
     runners = [moe.MoeLayerRunner(devs[c], W_rs[c], k, 1) for c in range(len(layers))]
     fns = [lambda c=c, i=i: runners[c].decode(xs[i:i + 1]) for i, c in zip(range(64), [j % len(layers) for j in range(64)])]
+    torch.cuda.synchronize()   # the weights, slot tables and inputs come from the default stream
     with torch.cuda.stream(stream):
         for f in fns:
             f()

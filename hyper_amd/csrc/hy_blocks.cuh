@@ -36,6 +36,10 @@ __device__ __forceinline__ uint32_t apply_sign(uint32_t g, uint32_t b4) {
     const uint32_t one = spread4(b4);
     return (g ^ (one * 0xFFu)) + one;
 }
+// the same with the byte mask given (0xFF per negated byte): -g = ~g + 1 per byte, no carry (codebook bytes are not 0)
+__device__ __forceinline__ uint32_t apply_mask(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
+// LDS entries of an expanded IQ2_XS codebook: 512 rows, then 128 sign masks
+constexpr int IQ2XS_LDS = 512 + 128;
 // Q6_K: q6 bytes (0..63) -> q6 - 32 as int8: per byte (q + 96) ^ 128 = q - 32 mod 256 (q + 96 < 256: no carry)
 __device__ __forceinline__ uint32_t q6_signed(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
 
@@ -149,7 +153,7 @@ template <> struct Item<IQ4_XS> {
 };
 // IQ2_XS (74 B: d, qs u16[32], scales[8]).  Lane L = 32-group L: 8-groups l = 0..3 use qs[4 L + l]: grid row
 // q & 511, signs ksigns[q >> 9]; scale nibble l >> 1 of scales[L]; value d (2 sc + 1) / 8 grid sign.
-// `grid`: the codebook rows expanded to 8 bytes each (LDS).
+// `grid`: the codebook rows expanded to 8 bytes each and the sign masks (LDS, expand_iq2xs_grid).
 template <> struct Item<IQ2_XS> {
     uint16_t q[4];
     uint16_t d;
@@ -166,9 +170,8 @@ template <> struct Item<IQ2_XS> {
         int s[4];
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            const uint2 g = grid[q[l] & 511];
-            const uint32_t sg = ksign(q[l] >> 9);
-            s[l] = sdot4(apply_sign(g.y, sg >> 4), ya[2 * l + 1], sdot4(apply_sign(g.x, sg & 15), ya[2 * l], 0));
+            const uint2 g = grid[q[l] & 511], sm = grid[512 + (q[l] >> 9)];
+            s[l] = sdot4(apply_mask(g.y, sm.y), ya[2 * l + 1], sdot4(apply_mask(g.x, sm.x), ya[2 * l], 0));
         }
         si = (2 * (sc & 15) + 1) * (s[0] + s[1]) + (2 * (sc >> 4) + 1) * (s[2] + s[3]);
         sm = 0;
@@ -192,9 +195,15 @@ template <> struct Item<IQ4_NL> {
     __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
 };
 
-// expand the IQ2_XS codebook (base-3 codes) into 512 x 8 bytes of LDS
+// expand the IQ2_XS codebook (base-3 codes) into 512 x 8 bytes of LDS, followed by the 128 sign patterns as byte
+// masks (entry 512 + i: byte j = 0xFF where bit j of ksign(i) is set, the parity bit giving byte 7)
 __device__ __forceinline__ void expand_iq2xs_grid(uint2 *grid) {
-    for (int i = threadIdx.x; i < 512; i += blockDim.x) {
+    for (int i = threadIdx.x; i < IQ2XS_LDS; i += blockDim.x) {
+        if (i >= 512) {
+            const uint32_t ks = ksign((uint32_t) i - 512);
+            grid[i] = make_uint2(spread4(ks & 15) * 0xFFu, spread4(ks >> 4) * 0xFFu);
+            continue;
+        }
         uint32_t c = c_iq2xs_code[i], lo = 0, hi = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {

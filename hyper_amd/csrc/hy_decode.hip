@@ -173,7 +173,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     __shared__ int s_ids[64];
     __shared__ float s_wts[64], s_sg;
     __shared__ int s_slot[64 * V];
-    __shared__ uint2 grid[T == IQ2_XS ? 512 : 1];
+    __shared__ uint2 grid[T == IQ2_XS ? IQ2XS_LDS : 1];
     __shared__ float s_xd[DEC_GU_TV / 2];   // activation scales of the token's Q8 row, one per weight block
     __shared__ __align__(16) uint8_t s_y[DEC_Y_BYTES];   // the token's Q8 row (every item reads its 256-value span here)
     const int p = blockIdx.y, t = p / k, j = p - t * k;
@@ -298,7 +298,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     __shared__ float tv[DEC_DN_WAVES][DEC_DN_TV];
     __shared__ int s_slot[2 * 64 * DEC_DN_WAVES];   // n_expert <= 1024
     __shared__ int s_ord[DEC_DN_WAVES][64];
-    __shared__ uint2 grid[T == IQ2_XS ? 512 : 1];
+    __shared__ uint2 grid[T == IQ2_XS ? IQ2XS_LDS : 1];
     const int t = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
     const int n = m.n, ff = m.ff, ng = ff / 256, nb = ff / BE, items = k * ng;
     const int row = blockIdx.x * DEC_DN_WAVES + wave;
@@ -508,10 +508,10 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
     }
     if (nt == 0) return HY_OK;
     // rows per wave: every block routes its token again, so the grid is kept near DEC_GU_BLOCKS blocks, within the
-    // item registers (rw 2 ng <= 8 DEC_MAXP) and the fold inputs (rw 2 nb <= DEC_GU_TV)
+    // fold inputs (rw 2 nb <= DEC_GU_TV); a wave's rw 2 ng items run in rounds of up to 8 DEC_MAXP
     int rw = 1;
     auto nblocks = [&](int r) { return (long) ((m.ff + DEC_GU_WAVES * r - 1) / (DEC_GU_WAVES * r)) * nt * k; };
-    while (rw < 8 && nblocks(rw) > DEC_GU_BLOCKS && (rw + 1) * 2 * ng <= 8 * DEC_MAXP && (rw + 1) * 2 * nb <= DEC_GU_TV) ++rw;
+    while (rw < 8 && nblocks(rw) > DEC_GU_BLOCKS && (rw + 1) * 2 * nb <= DEC_GU_TV) ++rw;
     dim3 grid((m.ff + DEC_GU_WAVES * rw - 1) / (DEC_GU_WAVES * rw), nt * k);
     const int V = (ne + 63) / 64;
     const int np = (rw * 2 * ng + 7) / 8;   // passes of 8 items

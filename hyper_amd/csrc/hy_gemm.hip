@@ -154,10 +154,9 @@ template <> struct Raw<IQ2_XS> {
     }
     __device__ __forceinline__ void chunk(int c, int, const uint2 *grid, uint32_t &b0, uint32_t &b1, int &s0, int &s1, int &mn) const {
         const uint32_t qv = (qq[c >> 1] >> (16 * (c & 1))) & 0xffff;
-        const uint2 g = grid[qv & 511];
-        const uint32_t sg = ksign(qv >> 9);
-        b0 = apply_sign(g.x, sg & 15);
-        b1 = apply_sign(g.y, sg >> 4);
+        const uint2 g = grid[qv & 511], sm = grid[512 + (qv >> 9)];
+        b0 = apply_mask(g.x, sm.x);
+        b1 = apply_mask(g.y, sm.y);
         const uint32_t s = ((c < 4 ? scv.x : scv.y) >> (8 * (c & 3))) & 0xff;
         s0 = 2 * (int) (s & 15) + 1;
         s1 = 2 * (int) (s >> 4) + 1;
@@ -488,7 +487,7 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
     __shared__ int s_item[C::ITEMS][3];                  // first pair in order, tokens, weight slot
     __shared__ int s_pair[C::ITEMS][GM_TOK];             // pair index of each token of the segment's items
     __shared__ float s_wt[GU ? 1 : C::ITEMS][GM_TOK];    // down: their route weights
-    __shared__ uint2 grid[T == IQ2_XS ? 512 : 1];
+    __shared__ uint2 grid[T == IQ2_XS ? IQ2XS_LDS : 1];
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, rr = lane & 15, q = lane >> 4;
     const int na = order_n[1];
     // ---- items.  Expert group g (cnt tokens) owns ceil(cnt / 64) items: full ones of 4 token tiles and a last one of
@@ -777,7 +776,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
     __shared__ float Yd[2][GM_TOK * (NL ? 8 : 1)];
     __shared__ int s_scan[1024 + 8];
     __shared__ float s_up[GU ? 32 * GM_TOK : 1];
-    __shared__ uint2 grid[T == IQ2_XS ? 512 : 1];
+    __shared__ uint2 grid[T == IQ2_XS ? IQ2XS_LDS : 1];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, rr = lane & 15, q = lane >> 4;
     const int na = order_n[1];
     // ---- items: expert group g owns ceil(cnt_g / GM_TOK) of them; s_scan = exclusive prefix (block-wide)

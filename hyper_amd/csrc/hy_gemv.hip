@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void k_gemv(hy_moe_dev m, int n_expert, const 
 template <int T, bool GU> static size_t gemv_lds(int in_dim, int R) {
     constexpr int VT = vec_dot_type(T), BE = block_elems(T);
     const int nb = in_dim / BE, ng = in_dim / 256, nmat = GU ? 2 : 1;
-    return lds16(VT == Q8_K ? ng * Q8K_BYTES : nb * Q8_0_LDS) + lds16(4 * nmat * R * nb) + lds16(4 * 2 * R) + (T == IQ2_XS ? 512 * 8 : 0);
+    return lds16(VT == Q8_K ? ng * Q8K_BYTES : nb * Q8_0_LDS) + lds16(4 * nmat * R * nb) + lds16(4 * 2 * R) + (T == IQ2_XS ? IQ2XS_LDS * 8 : 0);
 }
 
 template <int T, bool GU>
@@ -343,7 +343,7 @@ static int launch_down_reduce_t(const hy_moe_dev &m, const float *h, const int *
     if (R < 1) { set_error("hy_moe_down_reduce: k * ff / 256 = %d exceeds %d", k * ng, 32 * GEMV_MAXI); return HY_EBAD_SHAPE; }
     if (R > rows) R = rows;
     const int xq_row = VT == Q8_K ? ng * Q8K_BYTES : nb * Q8_0_LDS;
-    const size_t lds = lds16(k * xq_row) + lds16(4 * k * R * nb) + lds16(4 * k * R) + lds16(4 * k) + (T == IQ2_XS ? 512 * 8 : 0);
+    const size_t lds = lds16(k * xq_row) + lds16(4 * k * R * nb) + lds16(4 * k * R) + lds16(4 * k) + (T == IQ2_XS ? IQ2XS_LDS * 8 : 0);
     if (lds > 64 * 1024) { set_error("hy_moe_down_reduce: %zu bytes of LDS needed", lds); return HY_EBAD_SHAPE; }
     if (nt == 0) return HY_OK;
     dim3 grid(nt, (rows + R - 1) / R);
@@ -358,7 +358,7 @@ int launch_down_reduce(const hy_moe_dev &m, const float *h, const int *ids, cons
 // ---------------------------------------------------------------- test hooks
 // one row dequantized with the deq8 expressions (src/kernels4.cu:421-714): thread per value
 __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, float *__restrict__ out) {
-    __shared__ uint2 grid[512];
+    __shared__ uint2 grid[IQ2XS_LDS];
     if (type == IQ2_XS) expand_iq2xs_grid(grid);
     __syncthreads();
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -420,7 +420,7 @@ int launch_dequant_row(int type, const uint8_t *row, int n, float *out, hipStrea
 template <int T>
 __global__ __launch_bounds__(256) void k_block_ints(const uint8_t *__restrict__ rows, size_t row_bytes, int nrows, const uint8_t *__restrict__ xq,
                                                     int n, int *__restrict__ sumi, int *__restrict__ summ) {
-    __shared__ uint2 grid[512];
+    __shared__ uint2 grid[IQ2XS_LDS];
     __shared__ __align__(16) uint8_t y0[8 * Q8_0_LDS * 32];
     constexpr int BE = block_elems(T), VT = vec_dot_type(T);
     const int ng = n / 256, nb = n / BE;

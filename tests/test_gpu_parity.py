@@ -284,6 +284,7 @@ def test_runner_prefill_shared_graph_replays(cuda):
     r = moe.MoeLayerRunner(moe.upload_experts(L, device=cuda), W_r.to(cuda), k, max_rows=nt,
                            shared=moe.upload_experts(S, device=cuda), sg_logit=True)
     xin = torch.empty(nt, d, device=cuda)
+    torch.cuda.synchronize()   # the uploads ran on the default stream; the step runs on another
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         xin.copy_(xs[0])
