@@ -116,6 +116,10 @@ constexpr int HY_TILE = 16;
 __host__ __device__ constexpr size_t tiled_off(int row, int span, int nspan, int sb) {
     return ((size_t) (row >> 4) * nspan + span) * (size_t) (HY_TILE * sb) + (size_t) (row & 15) * sb;
 }
+// the same within one expert matrix of under 4 GiB (the launchers check), as a 32-bit offset
+__device__ __forceinline__ uint32_t tiled_off32(int row, int span, int nspan, int sb) {
+    return ((uint32_t) (row >> 4) * (uint32_t) nspan + (uint32_t) span) * (uint32_t) (HY_TILE * sb) + (uint32_t) (row & 15) * (uint32_t) sb;
+}
 __host__ __device__ constexpr int span_bytes(int t) { return block_bytes(t) * (256 / block_elems(t)); }
 
 // ------------------------------------------------------------------ wave helpers

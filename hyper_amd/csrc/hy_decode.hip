@@ -157,10 +157,15 @@ constexpr int DEC_GU_WAVES = 8;      // waves per block, rw ff rows each
 #define HY_DEC_GU_BLOCKS 768
 #endif
 constexpr int DEC_GU_BLOCKS = HY_DEC_GU_BLOCKS;   // grid size the rows per wave aim below
+#ifndef HY_DEC_PIPE_NP
+#define HY_DEC_PIPE_NP 2
+#endif
+constexpr int DEC_PIPE_NP = HY_DEC_PIPE_NP;        // passes per round when a wave's positions take several rounds
 
 // HQ: the block's 8 rw = 32 rows form one Q8_0 block of every pair's hidden row, and the fold also writes it to hq
-// (the down kernel then reads the hidden quantized instead of quantizing it in every block)
-template <int T, int V, int NP, bool HQ = false>
+// (the down kernel then reads the hidden quantized instead of quantizing it in every block).  PIPE: for waves with
+// several rounds of items, each round's loads go out before the previous round's dots.
+template <int T, int V, int NP, bool HQ = false, bool PIPE = false>
 __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev m, const float *__restrict__ logits, int ls, int ne, int k,
                                                                    const uint8_t *__restrict__ xq, int *__restrict__ ids,
                                                                    float *__restrict__ wts, float *__restrict__ sg, float *__restrict__ h,
@@ -226,32 +231,51 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
         e_sel = s_ids[j];
     }
     const int e = e_sel;
-    const int slot = (e >= 0 && e < ne) ? s_slot[e] : -1;
+    const int slot = __builtin_amdgcn_readfirstlane((e >= 0 && e < ne) ? s_slot[e] : -1);   // block-uniform
     if (slot < 0) return;   // uniform over the block: the pair's h rows are not written
-    // the wave's rows row0 .. row0 + rw - 1, each 2 ng items (gate spans, then up spans): unit u = 2 r + matrix; lane
-    // group g takes items g, g + 8, ... (a cursor over units and spans); rows past ff sit out
-    const int nunits = 2 * rw, nwi = nunits * ng, row0 = (blockIdx.x * DEC_GU_WAVES + wave) * rw;
+    // the wave's rows row0 .. row0 + rw - 1: position (r, s) = row r's span s, one gate item and one up item at the
+    // same offset; lane group g takes positions g, g + 8, ... (a cursor over rows and spans); rows past ff sit out
+    const int npos = rw * ng, row0 = (blockIdx.x * DEC_GU_WAVES + wave) * rw;
     const uint8_t *Wg = m.gate + (size_t) slot * m.gate_bytes, *Wu = m.up + (size_t) slot * m.gate_bytes;
-    Item<T> it[NP];
     float *tw = tv[wave];
     Cursor lc, cc;
     lc.start(g, ng);
     cc.start(g, ng);
-    for (int base = 0; base < nwi; base += 8 * NP) {   // wave-uniform rounds of up to 8 NP items (HQ: two)
+    // a round: up to 8 NP positions loaded into (bg, bu) (the load cursor moves on), then their dots (the dot cursor)
+    auto load_r = [&](Item<T> (&bg)[NP], Item<T> (&bu)[NP]) {
 #pragma unroll
         for (int ps = 0; ps < NP; ++ps) {
-            const int r = lc.u >> 1;
-            if (lc.u < nunits && row0 + r < ff) it[ps].load(((lc.u & 1) ? Wu : Wg) + tiled_off(row0 + r, lc.s, ng, SPAN_W), L);
+            if (lc.u < rw && row0 + lc.u < ff) {
+                const uint32_t off = tiled_off32(row0 + lc.u, lc.s, ng, SPAN_W);
+                bg[ps].load(Wg + off, L);
+                bu[ps].load(Wu + off, L);
+            }
             lc.next(ng, q8, r8);
         }
+    };
+    auto dots_r = [&](Item<T> (&bg)[NP], Item<T> (&bu)[NP], int base) {
 #pragma unroll
         for (int ps = 0; ps < NP; ++ps) {
-            if (base + 8 * ps >= nwi) break;   // wave-uniform
-            const int r = cc.u >> 1, mat = cc.u & 1, gi = cc.s;
-            const bool valid = cc.u < nunits && row0 + r < ff;
-            if constexpr (T == IQ2_XS) it[ps].grid = grid;
-            item_t<T>(it[ps], s_y, gi, L, valid, tw, r * 2 * nb + mat * nb + (T == IQ4_NL ? 8 * gi : gi));
+            if (base + 8 * ps >= npos) break;   // wave-uniform
+            const int r = cc.u, gi = cc.s, blk = T == IQ4_NL ? 8 * gi : gi;
+            const bool valid = r < rw && row0 + r < ff;
+            if constexpr (T == IQ2_XS) { bg[ps].grid = grid; bu[ps].grid = grid; }
+            item_t<T>(bg[ps], s_y, gi, L, valid, tw, r * 2 * nb + blk);
+            item_t<T>(bu[ps], s_y, gi, L, valid, tw, r * 2 * nb + nb + blk);
             cc.next(ng, q8, r8);
+        }
+    };
+    Item<T> ig[NP], iu[NP];
+    if constexpr (!PIPE) {
+        for (int base = 0; base < npos; base += 8 * NP) { load_r(ig, iu); dots_r(ig, iu, base); }   // wave-uniform rounds
+    } else {   // two sets of item registers: the next round's bytes travel while this round's dots run
+        Item<T> ig2[NP], iu2[NP];
+        load_r(ig, iu);
+        for (int base = 0; base < npos; base += 16 * NP) {
+            if (base + 8 * NP < npos) load_r(ig2, iu2);
+            dots_r(ig, iu, base);
+            if (base + 16 * NP < npos) load_r(ig, iu);
+            if (base + 8 * NP < npos) dots_r(ig2, iu2, base + 8 * NP);
         }
     }
     lds_barrier();
@@ -493,6 +517,7 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
                          float *h, int nt, hipStream_t s, uint8_t *hq) {
     const int ng = m.n / 256, nb = m.n / block_elems(m.tg);
     if (2 * ng > 8 * DEC_MAXP || 2 * nb > DEC_GU_TV) { set_error("hy_moe_route_gate_up: n = %d exceeds %d", m.n, 256 * 4 * DEC_MAXP); return HY_EBAD_SHAPE; }
+    if (m.gate_bytes >= ((size_t) 1 << 32)) { set_error("hy_moe_route_gate_up: an expert matrix of %zu bytes (4 GiB or more)", m.gate_bytes); return HY_EBAD_SHAPE; }
     if (hq) {   // the Q8_0 hidden as well: 32-row blocks (rw 4), items and fold inputs within the HQ instantiation's limits
         if (m.tg != IQ4_NL || m.td != IQ4_NL || 4 * 2 * nb > 2 * DEC_GU_TV) {
             set_error("hy_moe_route_gate_up_q8: needs IQ4_NL gate/up and down weights and n <= 4096 (types %d/%d, n %d)", m.tg, m.td, m.n);
@@ -501,25 +526,25 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
         if (nt == 0) return HY_OK;
         const int V = (ne + 63) / 64, q8 = 8 / ng, r8 = 8 % ng;
         dim3 grid(m.ff / 32, nt * k);
-#define HY_RGUQ(VV) hipLaunchKernelGGL((k_route_gate_up<IQ4_NL, VV, 8, true>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, 4, q8, r8, hq)
+#define HY_RGUQ(VV) hipLaunchKernelGGL((k_route_gate_up<IQ4_NL, VV, DEC_PIPE_NP, true, true>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, 4, q8, r8, hq)
         if (V <= 1) HY_RGUQ(1); else if (V <= 2) HY_RGUQ(2); else if (V <= 4) HY_RGUQ(4); else if (V <= 8) HY_RGUQ(8); else HY_RGUQ(16);
 #undef HY_RGUQ
         return check_launch("hy_moe_route_gate_up_q8");
     }
     if (nt == 0) return HY_OK;
     // rows per wave: every block routes its token again, so the grid is kept near DEC_GU_BLOCKS blocks, within the
-    // fold inputs (rw 2 nb <= DEC_GU_TV); a wave's rw 2 ng items run in rounds of up to 8 DEC_MAXP
+    // fold inputs (rw 2 nb <= DEC_GU_TV); a wave's rw ng positions run in rounds of up to 8 NP
     int rw = 1;
     auto nblocks = [&](int r) { return (long) ((m.ff + DEC_GU_WAVES * r - 1) / (DEC_GU_WAVES * r)) * nt * k; };
     while (rw < 8 && nblocks(rw) > DEC_GU_BLOCKS && (rw + 1) * 2 * nb <= DEC_GU_TV) ++rw;
     dim3 grid((m.ff + DEC_GU_WAVES * rw - 1) / (DEC_GU_WAVES * rw), nt * k);
     const int V = (ne + 63) / 64;
-    const int np = (rw * 2 * ng + 7) / 8;   // passes of 8 items
-    const int q8 = 8 / ng, r8 = 8 % ng;   // the item cursor's step
-#define HY_RGU(VV, NN) hipLaunchKernelGGL((k_route_gate_up<TT, VV, NN>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, rw, q8, r8, nullptr)
-#define HY_RGU_V(NN) if (V <= 1) HY_RGU(1, NN); else if (V <= 2) HY_RGU(2, NN); else if (V <= 4) HY_RGU(4, NN); else if (V <= 8) HY_RGU(8, NN); else HY_RGU(16, NN);
+    const int np = (rw * ng + 7) / 8;   // passes of 8 positions (a gate and an up item each)
+    const int q8 = 8 / ng, r8 = 8 % ng;   // the position cursor's step
+#define HY_RGU(VV, NN, PP) hipLaunchKernelGGL((k_route_gate_up<TT, VV, NN, false, PP>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, rw, q8, r8, nullptr)
+#define HY_RGU_V(NN, PP) if (V <= 1) HY_RGU(1, NN, PP); else if (V <= 2) HY_RGU(2, NN, PP); else if (V <= 4) HY_RGU(4, NN, PP); else if (V <= 8) HY_RGU(8, NN, PP); else HY_RGU(16, NN, PP);
     HY_DEC_SWITCH(m.tg, {
-        if (np <= 2) { HY_RGU_V(2) } else if (np <= 4) { HY_RGU_V(4) } else { HY_RGU_V(8) }
+        if (np <= 1) { HY_RGU_V(1, false) } else if (np <= 2) { HY_RGU_V(2, false) } else if (np <= 4) { HY_RGU_V(4, false) } else { HY_RGU_V(DEC_PIPE_NP, true) }
         return check_launch("hy_moe_route_gate_up");
     });
 #undef HY_RGU_V
