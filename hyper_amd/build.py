@@ -1,6 +1,8 @@
 """Build libhymoe.so (the HIP kernels and the C ABI) in-tree for gfx950.
 
     python -m hyper_amd.build            # compile every source, link hyper_amd/libhymoe.so
+    python -m hyper_amd.build --stamps   # the same with -DHY_STAMPS: hyper_amd/libhymoe_stamps.so, whose decode
+                                         # kernels record per-block phase times (python -m hyper_amd.stamps)
 
 Flags every HIP source is compiled with:
   -ffp-contract=off                           every fp32 product/sum is rounded on its own unless the
@@ -19,6 +21,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OUT = PKG / "libhymoe.so"
+OUT_STAMPS = PKG / "libhymoe_stamps.so"
 BUILD = PKG / "_build"
 
 SOURCES = ["hy_route.hip", "hy_gemv.hip", "hy_gemm.hip", "hy_decode.hip", "hy_capi.cpp", "hy_step.cpp", "hy_gguf.cpp"]
@@ -30,9 +33,9 @@ FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=
          "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-I", str(PKG.parent / "include")]
 
 
-def _compile(src: str) -> Path:
-    obj = BUILD / (Path(src).stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+def _compile(src: str, stamps: bool = False) -> Path:
+    obj = BUILD / (Path(src).stem + ("_stamps.o" if stamps else ".o"))
+    cmd = [HIPCC, *FLAGS, *(["-DHY_STAMPS"] if stamps else []), "-c", str(CSRC / src), "-o", str(obj)]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -45,20 +48,21 @@ def _compile(src: str) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
+def build(verbose: bool = False, stamps: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
+    out = OUT_STAMPS if stamps else OUT
     with ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = OUT.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile(src, stamps), SOURCES))
+    tmp = out.with_suffix(".so.tmp")
     r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)],
                        capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {OUT}")
-    return OUT
+        print(f"built {out}")
+    return out
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, stamps="--stamps" in sys.argv[1:])

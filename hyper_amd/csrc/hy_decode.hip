@@ -16,10 +16,22 @@
 #include "hy_internal.h"
 #include "hy_blocks.cuh"
 #include "hy_routing.cuh"
+#include "hy_stamps.cuh"
 
 #include <algorithm>
 
 namespace hy {
+
+#ifdef HY_STAMPS
+__device__ unsigned long long g_stamps[STAMP_CAP];
+extern "C" int hy_stamps_read(void *dst, size_t bytes) {
+    return (int) hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_stamps), bytes < sizeof(g_stamps) ? bytes : sizeof(g_stamps), 0, hipMemcpyDeviceToHost);
+}
+extern "C" int hy_stamps_clear() {
+    static unsigned long long zero[STAMP_CAP];
+    return (int) hipMemcpyToSymbol(HIP_SYMBOL(g_stamps), zero, sizeof(zero), 0, hipMemcpyHostToDevice);
+}
+#endif
 
 constexpr int DEC_MAXP = 8;        // passes of 8 items per wave: up to 64 items (256-value spans) per wave
 constexpr int DEC_ROUTE_NT = 8;    // tokens the fused router takes (more: the separate kernels)
@@ -48,6 +60,8 @@ template <int VT>
 __global__ __launch_bounds__(256) void k_router_q8(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
                                                    const float *__restrict__ bias, int bs, float *__restrict__ logits, int ls,
                                                    uint8_t *__restrict__ xq, int nt) {
+    HY_STAMP_VARS(3);
+    HY_STAMP(0);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int gw = blockIdx.x * 4 + wave, r = gw;
     // waves [0, rows): a logit row each; waves [rows, rows + units): the Q8 of x, a Q8_K block (token q / nb) or a
@@ -67,6 +81,9 @@ __global__ __launch_bounds__(256) void k_router_q8(const float *__restrict__ W, 
                 q8_0_pair_wave(x + (size_t) t * xs + 32 * b, xq + ((size_t) t * nb + b) * Q8_0_BYTES, b + 1 < nb, Q8_0_BYTES, 2);
             }
         }
+        HY_STAMP(1);
+        HY_STAMP_SET(2, 2);
+        HY_STAMP_SAVE(4 * gw, 3, lane == 0 && gw < 4094, false);
         return;
     }
     // logits of row r for every token: lane L sums elements 256 i + 4 L + j with fmaf, then the butterfly.  The
@@ -114,6 +131,9 @@ __global__ __launch_bounds__(256) void k_router_q8(const float *__restrict__ W, 
             if (lane == 0) logits[(size_t) t * ls + r] = v;
         }
     }
+    HY_STAMP(1);
+    HY_STAMP_SET(2, 1);
+    HY_STAMP_SAVE(4 * gw, 3, lane == 0 && gw < 4094, false);
 }
 
 // ---------------------------------------------------------------- item dots against Q8 rows in LDS
@@ -181,6 +201,8 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     __shared__ uint2 grid[T == IQ2_XS ? IQ2XS_LDS : 1];
     __shared__ float s_xd[DEC_GU_TV / 2];   // activation scales of the token's Q8 row, one per weight block
     __shared__ __align__(16) uint8_t s_y[DEC_Y_BYTES];   // the token's Q8 row (every item reads its 256-value span here)
+    HY_STAMP_VARS(5);
+    HY_STAMP(0);
     const int p = blockIdx.y, t = p / k, j = p - t * k;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
     const int ff = m.ff, ng = m.n / 256, nb = m.n / BE;
@@ -232,6 +254,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     }
     const int e = e_sel;
     const int slot = __builtin_amdgcn_readfirstlane((e >= 0 && e < ne) ? s_slot[e] : -1);   // block-uniform
+    HY_STAMP(1);
     if (slot < 0) return;   // uniform over the block: the pair's h rows are not written
     // the wave's rows row0 .. row0 + rw - 1: position (r, s) = row r's span s, one gate item and one up item at the
     // same offset; lane group g takes positions g, g + 8, ... (a cursor over rows and spans); rows past ff sit out
@@ -267,10 +290,15 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     };
     Item<T> ig[NP], iu[NP];
     if constexpr (!PIPE) {
-        for (int base = 0; base < npos; base += 8 * NP) { load_r(ig, iu); dots_r(ig, iu, base); }   // wave-uniform rounds
+        for (int base = 0; base < npos; base += 8 * NP) {   // wave-uniform rounds
+            load_r(ig, iu);
+            if (base == 0) HY_STAMP_WAIT(2);
+            dots_r(ig, iu, base);
+        }
     } else {   // two sets of item registers: the next round's bytes travel while this round's dots run
         Item<T> ig2[NP], iu2[NP];
         load_r(ig, iu);
+        HY_STAMP_WAIT(2);
         for (int base = 0; base < npos; base += 16 * NP) {
             if (base + 8 * NP < npos) load_r(ig2, iu2);
             dots_r(ig, iu, base);
@@ -279,6 +307,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
         }
     }
     lds_barrier();
+    HY_STAMP(3);
     // the folds, in block order, by wave 0: lane l takes the block's row l (wave l / rw, its row l % rw); eight
     // blocks' inputs per LDS round trip, then the fma chain
     if (wave != 0 || (!HQ && lane >= DEC_GU_WAVES * rw)) return;
@@ -300,6 +329,8 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
         hv = hy_swiglu(ag, au, m.clamp);
         h[(size_t) p * ff + row] = hv;
     }
+    HY_STAMP(4);
+    HY_STAMP_SAVE(16384 + 8 * (int) (blockIdx.y * gridDim.x + blockIdx.x), 5, lane == 0 && blockIdx.y * gridDim.x + blockIdx.x < 2047, true);
     if constexpr (HQ)   // lanes 0-31: the 32 values of Q8_0 block blockIdx.x of pair p's hidden row
         q8_0_pair_vals(hv, hq + ((size_t) p * (ff / 32) + blockIdx.x) * Q8_0_BYTES, false, Q8_0_BYTES, 2);
 }
@@ -323,6 +354,8 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     __shared__ int s_slot[2 * 64 * DEC_DN_WAVES];   // n_expert <= 1024
     __shared__ int s_ord[DEC_DN_WAVES][64];
     __shared__ uint2 grid[T == IQ2_XS ? IQ2XS_LDS : 1];
+    HY_STAMP_VARS(6);
+    HY_STAMP(0);
     const int t = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
     const int n = m.n, ff = m.ff, ng = ff / 256, nb = ff / BE, items = k * ng;
     const int row = blockIdx.x * DEC_DN_WAVES + wave;
@@ -370,21 +403,24 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
         }
     };
     // hqg (Q8_0 partner types): the token's k hidden rows already quantized (rows of nb Q8_0 blocks, consecutive for
-    // the token's pairs, a multiple of 272 bytes each): brought in as 16-byte pieces instead of loaded and quantized
+    // the token's pairs, a multiple of 272 bytes each): copied into LDS as 16-byte pieces, ahead of the first barrier,
+    // instead of loaded and quantized
     constexpr int HQV = DEC_DN_HQ / (16 * 64 * DEC_DN_WAVES);
-    uint4 hv16[HQV];
     const int n16 = VT == Q8_0 && hqg ? k * nb * Q8_0_BYTES / 16 : 0;
     if (n16) {
         const uint4 *src = (const uint4 *) (hqg + (size_t) t * k * nb * Q8_0_BYTES);
 #pragma unroll
-        for (int i = 0; i < HQV; ++i)
-            if (tid + i * 64 * DEC_DN_WAVES < n16) hv16[i] = src[tid + i * 64 * DEC_DN_WAVES];
+        for (int i = 0; i < HQV; ++i) {
+            const int o = tid + i * 64 * DEC_DN_WAVES;
+            if (o < n16) ((uint4 *) hq)[o] = src[o];
+        }
     } else {
         hload(0);
     }
     s_slot[tid] = sl0;
     s_slot[tid + 64 * DEC_DN_WAVES] = sl1;
     lds_barrier();
+    HY_STAMP(1);
     // lane j < k: pair j's slot (-1: skipped); `okm`: the valid pairs as a wave-uniform bit mask
     const int my_slot = (my_e >= 0 && my_e < m.n_expert) ? s_slot[my_e] : -1;
     const uint64_t okm = __ballot(my_slot >= 0);
@@ -432,16 +468,14 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
             }
         }
     };
-    if (n16) {
-#pragma unroll
-        for (int i = 0; i < HQV; ++i)
-            if (tid + i * 64 * DEC_DN_WAVES < n16) ((uint4 *) hq)[tid + i * 64 * DEC_DN_WAVES] = hv16[i];
-    } else {
+    if (!n16) {
         hquant(0);
         for (int ub = UB; ub < units; ub += UB) { hload(ub); hquant(ub); }
     }
     if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
     lds_barrier();
+    HY_STAMP(2);
+    HY_STAMP_WAIT(3);
     if (!row_ok) return;   // wave-uniform; no block barrier follows
     float *tw = tv[wave];
     for (int base = 0; base < items; base += 8 * NP) {   // wave-uniform rounds of up to 8 NP items
@@ -458,6 +492,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
         }
     }
     wave_lds_sync();
+    HY_STAMP(4);
     // lane j folds pair j in block order
     float fo = 0.0f;
     if (mine) {   // LDS reads four blocks at a time, then the fma chain
@@ -485,6 +520,8 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
         if (first) { acc = v; first = false; } else acc = acc + v;
     }
     if (lane == 0) out[(size_t) t * n + row] = res ? out[(size_t) t * n + row] + acc : acc;   // res: the residual add
+    HY_STAMP(5);
+    HY_STAMP_SAVE(32768 + 8 * (int) (blockIdx.y * gridDim.x + blockIdx.x), 6, wave == 0 && lane == 0 && blockIdx.y * gridDim.x + blockIdx.x < 4095, true);
 }
 
 // ---------------------------------------------------------------- launchers
@@ -573,7 +610,8 @@ int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const f
     const int q8 = 8 / ng, r8 = 8 % ng;   // the item cursors' step
 #define HY_DN(NN) hipLaunchKernelGGL((k_dec_down<TT, NN>), grid, dim3(64 * DEC_DN_WAVES), 0, s, m, h, ids, wts, k, shexp, sg, out, res, q8, r8, hq)
     HY_DEC_SWITCH(m.td, {
-        if (np <= 2) HY_DN(2); else if (np <= 4) HY_DN(4); else HY_DN(8);
+        // 8 passes a round only for IQ2_XS (same occupancy as 4); the others take more rounds at a higher occupancy
+        if (np <= 2) HY_DN(2); else if (np <= 4 || TT != IQ2_XS) HY_DN(4); else HY_DN(8);
         return check_launch("hy_moe_down_reduce");
     });
 #undef HY_DN
