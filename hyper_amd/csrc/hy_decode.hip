@@ -194,7 +194,9 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     constexpr int SPAN_W = 256 / BE * block_bytes(T);
     constexpr int SPAN_Y = VT == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
     constexpr int TVN = HQ ? 2 * DEC_GU_TV : DEC_GU_TV;   // fold inputs per wave (HQ: 4 rows)
-    __shared__ float tv[DEC_GU_WAVES][TVN];
+    // fold inputs of the block's rows, row l at l (2 nb + 1): an odd stride puts the rows' entries in distinct LDS
+    // banks when the fold lanes (one row each) read entry b together
+    __shared__ float tv[DEC_GU_WAVES * TVN + 64];
     __shared__ int s_ids[64];
     __shared__ float s_wts[64], s_sg;
     __shared__ int s_slot[64 * V];
@@ -260,7 +262,8 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     // same offset; lane group g takes positions g, g + 8, ... (a cursor over rows and spans); rows past ff sit out
     const int npos = rw * ng, row0 = (blockIdx.x * DEC_GU_WAVES + wave) * rw;
     const uint8_t *Wg = m.gate + (size_t) slot * m.gate_bytes, *Wu = m.up + (size_t) slot * m.gate_bytes;
-    float *tw = tv[wave];
+    const int rs = 2 * nb + 1;
+    float *tw = tv + wave * rw * rs;
     Cursor lc, cc;
     lc.start(g, ng);
     cc.start(g, ng);
@@ -283,8 +286,8 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
             const int r = cc.u, gi = cc.s, blk = T == IQ4_NL ? 8 * gi : gi;
             const bool valid = r < rw && row0 + r < ff;
             if constexpr (T == IQ2_XS) { bg[ps].grid = grid; bu[ps].grid = grid; }
-            item_t<T>(bg[ps], s_y, gi, L, valid, tw, r * 2 * nb + blk);
-            item_t<T>(bu[ps], s_y, gi, L, valid, tw, r * 2 * nb + nb + blk);
+            item_t<T>(bg[ps], s_y, gi, L, valid, tw, r * rs + blk);
+            item_t<T>(bu[ps], s_y, gi, L, valid, tw, r * rs + nb + blk);
             cc.next(ng, q8, r8);
         }
     };
@@ -315,7 +318,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     if (!HQ && row >= ff) return;
     float hv = 0.0f;
     if (lane < DEC_GU_WAVES * rw) {   // (HQ: lanes 32-63 stay for the quantizer's cross-lane max)
-        const float *tg = tv[lane / rw] + (lane % rw) * 2 * nb;
+        const float *tg = tv + lane * rs;
         float ag = 0.0f, au = 0.0f;
         for (int b0 = 0; b0 < nb; b0 += 8) {
             float xa[8], ga[8], ua[8];
@@ -350,7 +353,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     constexpr int SPAN_W = 256 / BE * block_bytes(T);
     constexpr int SPAN_Y = VT == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
     __shared__ __align__(16) uint8_t hq[DEC_DN_HQ];
-    __shared__ float tv[DEC_DN_WAVES][DEC_DN_TV];
+    __shared__ float tv[DEC_DN_WAVES][DEC_DN_TV + 64];   // pair j's inputs at j (nb | 1): an odd stride, distinct banks
     __shared__ int s_slot[2 * 64 * DEC_DN_WAVES];   // n_expert <= 1024
     __shared__ int s_ord[DEC_DN_WAVES][64];
     __shared__ uint2 grid[T == IQ2_XS ? IQ2XS_LDS : 1];
@@ -487,7 +490,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
             const int j = cc.u, gi = cc.s;
             const bool valid = i < items && pair_ok(j);
             if constexpr (T == IQ2_XS) it[ps].grid = grid;
-            item_t<T>(it[ps], hq + (size_t) j * ng * SPAN_Y, gi, L, valid, tw, j * nb + (T == IQ4_NL ? 8 * gi : gi));
+            item_t<T>(it[ps], hq + (size_t) j * ng * SPAN_Y, gi, L, valid, tw, j * (nb | 1) + (T == IQ4_NL ? 8 * gi : gi));
             cc.next(ng, q8, r8);
         }
     }
@@ -497,7 +500,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     float fo = 0.0f;
     if (mine) {   // LDS reads four blocks at a time, then the fma chain
         const uint8_t *yj = hq + (size_t) lane * ng * SPAN_Y;
-        const float *tj = tw + lane * nb;
+        const float *tj = tw + lane * (nb | 1);
         float acc = 0.0f;
         for (int b0 = 0; b0 < nb; b0 += 4) {
             float sc[4], tq[4];
