@@ -326,9 +326,9 @@ __device__ __forceinline__ void q8k_block_wave(const float *x, uint8_t *out) {
 // two Q8_0 blocks (64 values) by one wave into blocks of `stride` bytes with qs at `qoff`, as ggml's x86
 // quantize_row_q8_0: d = amax / 127 (stored fp16), id = 127 / amax (0 if amax == 0), q = rint(x * id)
 // from the lane's value v (value `lane` of the pair; lanes 32-63 ignored when !valid2)
-__device__ __forceinline__ void q8_0_pair_vals(float v, uint8_t *out, bool valid2, int stride, int qoff) {
+// (the arithmetic: the lane's q and its block's d)
+__device__ __forceinline__ int q8_0_pair_q(float v, bool on, float &d) {
     const int lane = lane_id();
-    const bool on = lane < 32 || valid2;
     if (!on) v = 0.0f;
     float am = fabsf(v);
     am = fmaxf(am, dpp_f<DPP_XOR1>(am));
@@ -336,13 +336,30 @@ __device__ __forceinline__ void q8_0_pair_vals(float v, uint8_t *out, bool valid
     am = fmaxf(am, dpp_f<DPP_HALF_MIRROR>(am));
     am = fmaxf(am, dpp_f<DPP_MIRROR>(am));
     am = lane < 32 ? fmaxf(readlane_f(am, 0), readlane_f(am, 16)) : fmaxf(readlane_f(am, 32), readlane_f(am, 48));
-    const float d = am / 127.f;
+    d = am / 127.f;
     const float id = am != 0.0f ? 127.f / am : 0.0f;
-    const int q = (int) __builtin_rintf(v * id);
+    return (int) __builtin_rintf(v * id);
+}
+__device__ __forceinline__ void q8_0_pair_vals(float v, uint8_t *out, bool valid2, int stride, int qoff) {
+    const int lane = lane_id();
+    const bool on = lane < 32 || valid2;
+    float d;
+    const int q = q8_0_pair_q(v, on, d);
     if (on) {
         uint8_t *b = out + (lane >> 5) * stride;
         b[qoff + (lane & 31)] = (uint8_t) (int8_t) q;
         if ((lane & 31) == 0) *(uint16_t *) b = f2h(d);
+    }
+}
+// the same pair into split storage: the blocks' qs at qs + 32 i, their fp16 d at dq[i]
+__device__ __forceinline__ void q8_0_pair_split(float v, uint8_t *qs, uint16_t *dq, bool valid2) {
+    const int lane = lane_id();
+    const bool on = lane < 32 || valid2;
+    float d;
+    const int q = q8_0_pair_q(v, on, d);
+    if (on) {
+        qs[32 * (lane >> 5) + (lane & 31)] = (uint8_t) (int8_t) q;
+        if ((lane & 31) == 0) dq[lane >> 5] = f2h(d);
     }
 }
 __device__ __forceinline__ void q8_0_pair_wave(const float *x, uint8_t *out, bool valid2, int stride, int qoff) {

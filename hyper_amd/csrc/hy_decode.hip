@@ -139,15 +139,16 @@ __global__ __launch_bounds__(256) void k_router_q8(const float *__restrict__ W, 
 // ---------------------------------------------------------------- item dots against Q8 rows in LDS
 
 // the integers of item `it` (256 values, span gi of a row) against the Q8 row `y` (LDS); K-quants: summed over the
-// 8 lanes (every lane of the group gets them)
+// 8 lanes (every lane of the group gets them).  Q8_0 rows in LDS are split: the blocks' qs, 32 bytes each (16-byte
+// aligned), with the scales kept apart.
 template <int T>
 __device__ __forceinline__ float item_t(const Item<T> &it, const uint8_t *y, int gi, int L, bool valid, float *tv_out, int tv_idx) {
     if constexpr (T == IQ4_NL) {
-        // lane L takes block 8 gi + L whole: Q8_0 qs at 34 b + 2
-        const uint8_t *yb = y + (size_t) (8 * gi + L) * Q8_0_BYTES;
+        // lane L takes block 8 gi + L whole
+        const uint8_t *yb = y + (size_t) (8 * gi + L) * 32;
         int s = 0;
         if (valid) {
-            const uint4 y0 = load16_a2(yb + 2), y1 = load16_a2(yb + 18);
+            const uint4 y0 = *(const uint4 *) yb, y1 = *(const uint4 *) (yb + 16);
             const uint32_t q[4] = {it.qs.x, it.qs.y, it.qs.z, it.qs.w}, ya[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) { s = sdot4(kv4(q[i] & 0x0F0F0F0Fu), ya[i], s); s = sdot4(kv4((q[i] >> 4) & 0x0F0F0F0Fu), ya[4 + i], s); }
@@ -209,11 +210,19 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
     const int ff = m.ff, ng = m.n / 256, nb = m.n / BE;
     const uint8_t *y = xq + (size_t) t * ng * SPAN_Y;
-    // the Q8 row to LDS, a dword a thread per pass (row bytes ng SPAN_Y are a multiple of 4: 292 and 272 are)
+    // the Q8 row to LDS, a dword a thread per pass: Q8_K rows as they are (292 bytes a block); Q8_0 rows as the qs of
+    // their blocks, 32 bytes each (the scales go to s_xd)
     auto stage_y = [&](int i0, int stride) {
-        const uint32_t *src = (const uint32_t *) y;
         uint32_t *dst = (uint32_t *) s_y;
-        for (int i = i0; i < ng * SPAN_Y / 4; i += stride) dst[i] = src[i];
+        if constexpr (VT == Q8_K) {
+            const uint32_t *src = (const uint32_t *) y;
+            for (int i = i0; i < ng * SPAN_Y / 4; i += stride) dst[i] = src[i];
+        } else {
+            for (int i = i0; i < nb * 8; i += stride) {   // qs dword i & 7 of block i >> 3: 2-byte aligned in the row
+                const uint8_t *p = y + (size_t) (i >> 3) * Q8_0_BYTES + 2 + 4 * (i & 7);
+                dst[i] = (uint32_t) ld_u16(p) | ((uint32_t) ld_u16(p + 2) << 16);
+            }
+        }
     };
     const float *lg = logits + (size_t) t * ls;
     // the token's routing: every block of the token computes the same bits
@@ -351,7 +360,9 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
                                                                const uint8_t *__restrict__ hqg) {
     constexpr int VT = vec_dot_type(T), BE = block_elems(T);
     constexpr int SPAN_W = 256 / BE * block_bytes(T);
-    constexpr int SPAN_Y = VT == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
+    // the token's k hidden rows in LDS: Q8_K blocks as they are (SPAN_L = 292 bytes a span); Q8_0 split into the
+    // blocks' qs (32 bytes each, SPAN_L = 256 a span) followed by their fp16 scales (hdq, k nb of them)
+    constexpr int SPAN_L = VT == Q8_K ? Q8K_BYTES : 256;
     __shared__ __align__(16) uint8_t hq[DEC_DN_HQ];
     __shared__ float tv[DEC_DN_WAVES][DEC_DN_TV + 64];   // pair j's inputs at j (nb | 1): an odd stride, distinct banks
     __shared__ int s_slot[2 * 64 * DEC_DN_WAVES];   // n_expert <= 1024
@@ -361,6 +372,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     HY_STAMP(0);
     const int t = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
     const int n = m.n, ff = m.ff, ng = ff / 256, nb = ff / BE, items = k * ng;
+    uint16_t *hdq = (uint16_t *) (hq + (VT == Q8_K ? 0 : k * nb * 32));
     const int row = blockIdx.x * DEC_DN_WAVES + wave;
     const bool row_ok = row < n;
     const float *hp = h + (size_t) t * k * ff;
@@ -406,17 +418,15 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
         }
     };
     // hqg (Q8_0 partner types): the token's k hidden rows already quantized (rows of nb Q8_0 blocks, consecutive for
-    // the token's pairs, a multiple of 272 bytes each): copied into LDS as 16-byte pieces, ahead of the first barrier,
-    // instead of loaded and quantized
-    constexpr int HQV = DEC_DN_HQ / (16 * 64 * DEC_DN_WAVES);
-    const int n16 = VT == Q8_0 && hqg ? k * nb * Q8_0_BYTES / 16 : 0;
-    if (n16) {
-        const uint4 *src = (const uint4 *) (hqg + (size_t) t * k * nb * Q8_0_BYTES);
-#pragma unroll
-        for (int i = 0; i < HQV; ++i) {
-            const int o = tid + i * 64 * DEC_DN_WAVES;
-            if (o < n16) ((uint4 *) hq)[o] = src[o];
+    // the token's pairs): copied into the split LDS layout ahead of the first barrier, instead of loaded and quantized
+    const bool hcopy = VT == Q8_0 && hqg;
+    if (hcopy) {
+        const uint8_t *src = hqg + (size_t) t * k * nb * Q8_0_BYTES;
+        for (int i = tid; i < k * nb * 8; i += 64 * DEC_DN_WAVES) {   // qs dword i & 7 of block i >> 3 (2-byte aligned)
+            const uint8_t *p = src + (size_t) (i >> 3) * Q8_0_BYTES + 2 + 4 * (i & 7);
+            ((uint32_t *) hq)[i] = (uint32_t) ld_u16(p) | ((uint32_t) ld_u16(p + 2) << 16);
         }
+        for (int i = tid; i < k * nb; i += 64 * DEC_DN_WAVES) hdq[i] = ld_u16(src + (size_t) i * Q8_0_BYTES);
     } else {
         hload(0);
     }
@@ -466,12 +476,12 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
                 const int u = ub + wave + q * DEC_DN_WAVES;
                 if (u < units) {
                     const int j = u / npair, b = 2 * (u - j * npair);
-                    if (pair_ok(j)) q8_0_pair_vals(xv[q], hq + (size_t) j * ng * SPAN_Y + (size_t) b * Q8_0_BYTES, b + 1 < nb, Q8_0_BYTES, 2);
+                    if (pair_ok(j)) q8_0_pair_split(xv[q], hq + ((size_t) j * nb + b) * 32, hdq + j * nb + b, b + 1 < nb);
                 }
             }
         }
     };
-    if (!n16) {
+    if (!hcopy) {
         hquant(0);
         for (int ub = UB; ub < units; ub += UB) { hload(ub); hquant(ub); }
     }
@@ -490,7 +500,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
             const int j = cc.u, gi = cc.s;
             const bool valid = i < items && pair_ok(j);
             if constexpr (T == IQ2_XS) it[ps].grid = grid;
-            item_t<T>(it[ps], hq + (size_t) j * ng * SPAN_Y, gi, L, valid, tw, j * (nb | 1) + (T == IQ4_NL ? 8 * gi : gi));
+            item_t<T>(it[ps], hq + (size_t) j * ng * SPAN_L, gi, L, valid, tw, j * (nb | 1) + (T == IQ4_NL ? 8 * gi : gi));
             cc.next(ng, q8, r8);
         }
     }
@@ -499,14 +509,14 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     // lane j folds pair j in block order
     float fo = 0.0f;
     if (mine) {   // LDS reads four blocks at a time, then the fma chain
-        const uint8_t *yj = hq + (size_t) lane * ng * SPAN_Y;
+        const uint8_t *yj = hq + (size_t) lane * ng * SPAN_L;
         const float *tj = tw + lane * (nb | 1);
         float acc = 0.0f;
         for (int b0 = 0; b0 < nb; b0 += 4) {
             float sc[4], tq[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                if (b0 + u < nb) { sc[u] = q8_scale<VT>(yj, b0 + u); tq[u] = tj[b0 + u]; }
+                if (b0 + u < nb) { sc[u] = VT == Q8_K ? q8_scale<VT>(yj, b0 + u) : h2f(hdq[lane * nb + b0 + u]); tq[u] = tj[b0 + u]; }
 #pragma unroll
             for (int u = 0; u < 4; ++u)
                 if (b0 + u < nb) acc = __builtin_fmaf(sc[u], tq[u], acc);
