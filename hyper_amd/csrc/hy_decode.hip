@@ -210,52 +210,59 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
     const int ff = m.ff, ng = m.n / 256, nb = m.n / BE;
     const uint8_t *y = xq + (size_t) t * ng * SPAN_Y;
-    // the Q8 row to LDS, a dword a thread per pass: Q8_K rows as they are (292 bytes a block); Q8_0 rows as the qs of
-    // their blocks, 32 bytes each (the scales go to s_xd)
-    auto stage_y = [&](int i0, int stride) {
-        uint32_t *dst = (uint32_t *) s_y;
-        if constexpr (VT == Q8_K) {
-            const uint32_t *src = (const uint32_t *) y;
-            for (int i = i0; i < ng * SPAN_Y / 4; i += stride) dst[i] = src[i];
-        } else {
-            for (int i = i0; i < nb * 8; i += stride) {   // qs dword i & 7 of block i >> 3: 2-byte aligned in the row
-                const uint8_t *p = y + (size_t) (i >> 3) * Q8_0_BYTES + 2 + 4 * (i & 7);
-                dst[i] = (uint32_t) ld_u16(p) | ((uint32_t) ld_u16(p + 2) << 16);
+    // Everything the block stages goes out at once, into registers: the token's Q8 row (Q8_K rows as they are, 292
+    // bytes a block; Q8_0 rows as the qs of their blocks, 32 bytes each), the slot table and the activation scales;
+    // `stage` stores them to LDS ahead of the routing barrier.
+    constexpr int SY = (DEC_Y_BYTES / 4 + 64 * DEC_GU_WAVES - 1) / (64 * DEC_GU_WAVES);
+    const int tid = (int) threadIdx.x, ny = VT == Q8_K ? ng * (Q8K_BYTES / 4) : nb * 8;
+    uint32_t yv[SY];
+#pragma unroll
+    for (int u = 0; u < SY; ++u) {
+        const int i = tid + u * 64 * DEC_GU_WAVES;
+        yv[u] = 0;
+        if (i < ny) {
+            if constexpr (VT == Q8_K) {
+                yv[u] = ((const uint32_t *) y)[i];
+            } else {   // qs dword i & 7 of block i >> 3: 2-byte aligned in the row
+                const uint8_t *q = y + (size_t) (i >> 3) * Q8_0_BYTES + 2 + 4 * (i & 7);
+                yv[u] = (uint32_t) ld_u16(q) | ((uint32_t) ld_u16(q + 2) << 16);
             }
         }
+    }
+    constexpr int NS = 64 * V;   // slot-table entries held (n_expert <= NS)
+    const int sl0 = tid < ne ? m.slot[tid] : -1;
+    const int sl1 = NS > 64 * DEC_GU_WAVES && tid + 64 * DEC_GU_WAVES < ne ? m.slot[tid + 64 * DEC_GU_WAVES] : -1;
+    const float xd = tid < nb ? q8_scale<VT>(y, tid) : 0.0f;
+    auto stage = [&] {
+#pragma unroll
+        for (int u = 0; u < SY; ++u) {
+            const int i = tid + u * 64 * DEC_GU_WAVES;
+            if (i < ny) ((uint32_t *) s_y)[i] = yv[u];
+        }
+        if (tid < ne) s_slot[tid] = sl0;
+        if constexpr (NS > 64 * DEC_GU_WAVES) {
+            if (tid + 64 * DEC_GU_WAVES < ne) s_slot[tid + 64 * DEC_GU_WAVES] = sl1;
+        }
+        if (tid < nb) s_xd[tid] = xd;
+        if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
     };
     const float *lg = logits + (size_t) t * ls;
     // the token's routing: every block of the token computes the same bits
     int e_sel;   // the expert of pair j
     if constexpr (V <= 2) {
         static_assert(DEC_GU_WAVES == 8, "route_rank8 takes eight waves");
-        const int tid = (int) threadIdx.x;
-        const int sl = tid < ne ? m.slot[tid] : -1;
-        const float xd = tid < nb ? q8_scale<VT>(y, tid) : 0.0f;
         int er;
         float pr, tot, lsg;
-        route_rank8<V>(lg, ne, k, sg != nullptr, er, pr, tot, lsg, [&] {   // the slot table, scales and Q8 row share its barrier
-            if (tid < ne) s_slot[tid] = sl;
-            if (tid < nb) s_xd[tid] = xd;
-            stage_y(tid, 64 * DEC_GU_WAVES);
-            if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
-        });
+        route_rank8<V>(lg, ne, k, sg != nullptr, er, pr, tot, lsg, stage);   // the staged data shares its barrier
         e_sel = __builtin_amdgcn_readlane(er, j);
         if (blockIdx.x == 0 && j == 0 && wave == 0) {   // the first block of each token publishes the routing
             if (lane < k) { ids[(size_t) t * k + lane] = er; wts[(size_t) t * k + lane] = pr / tot; }
             if (lane == 0 && sg) sg[t] = 1.0f / (1.0f + hy_expf(-lsg));
         }
     } else {
-        // wave 0 routes the token while the other waves bring in the slot table and the activation scales
-        if (wave == 0) {
-            route_wave<V>(lg, ne, k, s_ids, s_wts, sg ? &s_sg : nullptr);
-        } else {
-            const int i0 = (int) threadIdx.x - 64, stride = 64 * (DEC_GU_WAVES - 1);
-            for (int ex = i0; ex < ne; ex += stride) s_slot[ex] = m.slot[ex];
-            for (int b = i0; b < nb; b += stride) s_xd[b] = q8_scale<VT>(y, b);
-            stage_y(i0, stride);
-        }
-        if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
+        // wave 0 routes the token (one wave for more than 128 experts); every wave then stores its staged share
+        if (wave == 0) route_wave<V>(lg, ne, k, s_ids, s_wts, sg ? &s_sg : nullptr);
+        stage();
         lds_barrier();
         if (blockIdx.x == 0 && j == 0 && wave == 0) {   // the first block of each token publishes the routing
             if (lane < k) { ids[(size_t) t * k + lane] = s_ids[lane]; wts[(size_t) t * k + lane] = s_wts[lane]; }
@@ -343,8 +350,11 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     }
     HY_STAMP(4);
     HY_STAMP_SAVE(16384 + 8 * (int) (blockIdx.y * gridDim.x + blockIdx.x), 5, lane == 0 && blockIdx.y * gridDim.x + blockIdx.x < 2047, true);
-    if constexpr (HQ)   // lanes 0-31: the 32 values of Q8_0 block blockIdx.x of pair p's hidden row
-        q8_0_pair_vals(hv, hq + ((size_t) p * (ff / 32) + blockIdx.x) * Q8_0_BYTES, false, Q8_0_BYTES, 2);
+    if constexpr (HQ) {   // lanes 0-31: the 32 values of Q8_0 block blockIdx.x of pair p's hidden row (split layout)
+        const int nbh = ff / 32;
+        uint8_t *tok = hq + (size_t) t * k * nbh * Q8_0_BYTES;
+        q8_0_pair_split(hv, tok + ((size_t) j * nbh + blockIdx.x) * 32, (uint16_t *) (tok + (size_t) k * nbh * 32) + j * nbh + blockIdx.x, false);
+    }
 }
 
 // ---------------------------------------------------------------- k_dec_down
@@ -417,16 +427,19 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
             }
         }
     };
-    // hqg (Q8_0 partner types): the token's k hidden rows already quantized (rows of nb Q8_0 blocks, consecutive for
-    // the token's pairs): copied into the split LDS layout ahead of the first barrier, instead of loaded and quantized
+    // hqg (Q8_0 partner types): the token's k hidden rows already quantized, in the split layout of LDS (the k nb
+    // blocks' qs, then their scales: k nb 34 bytes, a multiple of 16): copied as 16-byte pieces ahead of the first
+    // barrier, instead of loaded and quantized
     const bool hcopy = VT == Q8_0 && hqg;
     if (hcopy) {
-        const uint8_t *src = hqg + (size_t) t * k * nb * Q8_0_BYTES;
-        for (int i = tid; i < k * nb * 8; i += 64 * DEC_DN_WAVES) {   // qs dword i & 7 of block i >> 3 (2-byte aligned)
-            const uint8_t *p = src + (size_t) (i >> 3) * Q8_0_BYTES + 2 + 4 * (i & 7);
-            ((uint32_t *) hq)[i] = (uint32_t) ld_u16(p) | ((uint32_t) ld_u16(p + 2) << 16);
+        constexpr int HQV = DEC_DN_HQ / (16 * 64 * DEC_DN_WAVES);
+        const int n16 = k * nb * Q8_0_BYTES / 16;
+        const uint4 *src = (const uint4 *) (hqg + (size_t) t * k * nb * Q8_0_BYTES);
+#pragma unroll
+        for (int i = 0; i < HQV; ++i) {
+            const int o = tid + i * 64 * DEC_DN_WAVES;
+            if (o < n16) ((uint4 *) hq)[o] = src[o];
         }
-        for (int i = tid; i < k * nb; i += 64 * DEC_DN_WAVES) hdq[i] = ld_u16(src + (size_t) i * Q8_0_BYTES);
     } else {
         hload(0);
     }

@@ -204,14 +204,16 @@ int hy_moe_router_q8(const float *W_r, int rows, int kdim, const float *x, int x
 int hy_moe_route_gate_up(const hy_moe_dev *m, const float *logits, int ls, int n_expert, int k, const void *xq, int32_t *ids, float *wts,
                          float *sg, float *h, int nt, hipStream_t s);
 
-/* hy_moe_route_gate_up that also writes hq: each pair's hidden row as Q8_0 blocks (row p = t*k + j at p * (ff/32) * 34
-   bytes, the bytes hy_q8_quantize(Q8_0, h row) gives), so the down step reads it instead of quantizing it in every
-   block -- the down kernels' activation quantization (src/kernels4.cu:2007-2022 quantizes h per launch) moved into
-   the producer.  For IQ4_NL gate/up and down weights and n <= 4096, else HY_EUNSUPPORTED_TYPE. */
+/* hy_moe_route_gate_up that also writes hq: the pairs' hidden rows as Q8_0 blocks (the values and scales
+   hy_q8_quantize(Q8_0, h row) gives), so the down step reads them instead of quantizing h in every block -- the down
+   kernels' activation quantization (src/kernels4.cu:2007-2022 quantizes h per launch) moved into the producer.
+   Layout, per token t at t * k * nbh * 34 bytes (nbh = ff / 32): the 32 int8 values of block b of pair j at
+   (j * nbh + b) * 32, then the fp16 scales, block b of pair j at k * nbh * 32 + 2 * (j * nbh + b).  For IQ4_NL
+   gate/up and down weights and n <= 4096, else HY_EUNSUPPORTED_TYPE. */
 int hy_moe_route_gate_up_q8(const hy_moe_dev *m, const float *logits, int ls, int n_expert, int k, const void *xq, int32_t *ids,
                             float *wts, float *sg, float *h, void *hq, int nt, hipStream_t s);
-/* hy_moe_down_reduce (residual == 0) or hy_moe_down_reduce_residual (residual != 0) from those Q8_0 rows (16-byte
-   aligned); bit-identical to them on the h the rows came from.  HY_EUNSUPPORTED_TYPE for other down types. */
+/* hy_moe_down_reduce (residual == 0) or hy_moe_down_reduce_residual (residual != 0) from those Q8_0 blocks (hq
+   16-byte aligned); bit-identical to them on the h the blocks came from.  HY_EUNSUPPORTED_TYPE for other down types. */
 int hy_moe_down_reduce_q8(const hy_moe_dev *m, const void *hq, const int32_t *ids, const float *wts, int k, const float *shexp,
                           const float *sg, float *out, int residual, int nt, hipStream_t s);
 

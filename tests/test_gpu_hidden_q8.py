@@ -43,7 +43,10 @@ def test_hidden_q8_handover_bitexact(cuda, E, d, ff, k, nt, absent):
         ids_cpu = np.where(local, ids_r, -1).astype(np.int32)
         x = torch.randn(rows, d, generator=gen(742 + rep))
         out_r, h_r, _ = orc.moe_layer(OL, x.numpy(), ids_cpu, wts_r, want_hy=True)
-        hq_r = orc.quantize(GType.Q8_0, h_r).reshape(rows * k, row_q)
+        # the oracle's Q8_0 blocks of h, in the hand-over's layout: per token, the k rows' block values, then scales
+        nbh = ff // 32
+        raw = orc.quantize(GType.Q8_0, h_r).reshape(rows, k, nbh, 34)
+        hq_r = np.concatenate([raw[..., 2:].reshape(rows, -1), raw[..., :2].reshape(rows, -1)], axis=1).reshape(-1)
         xq = torch.from_numpy(orc.quantize(GType.Q8_0, x.numpy())).reshape(-1).to(cuda)
         ids = torch.full((rows * k,), -5, dtype=torch.int32, device=cuda)
         wts = torch.zeros(rows * k, device=cuda)
@@ -59,11 +62,20 @@ def test_hidden_q8_handover_bitexact(cuda, E, d, ff, k, nt, absent):
         lv = local.reshape(-1)
         assert_bits_equal(ids.cpu().numpy().reshape(rows, k), ids_r, f"ids rep {rep}")
         assert_bits_equal(wts.cpu().numpy().reshape(rows, k), wts_r, f"wts rep {rep}")
-        hv, hqv = h.cpu().numpy(), hq.cpu().numpy().reshape(rows * k, row_q)
+        hv, hqv = h.cpu().numpy(), hq.cpu().numpy()
         assert_bits_equal(hv[lv], h_r[lv], f"h of local pairs rep {rep}")
         assert np.isnan(hv[~lv]).all(), "non-local pairs leave h unwritten"
-        assert_bits_equal(hqv[lv], hq_r[lv], f"Q8_0 rows of h rep {rep}")
-        assert (hqv[~lv] == 0xAB).all(), "non-local pairs leave their Q8_0 rows unwritten"
+        # byte masks of each pair's values and scales in the layout
+        pair = np.arange(rows * k).reshape(rows, k)
+        sel = np.zeros((rows * k, rows * k * nbh * 34), dtype=bool)
+        for t_ in range(rows):
+            base = t_ * k * nbh * 34
+            for j_ in range(k):
+                sel[pair[t_, j_], base + j_ * nbh * 32: base + (j_ + 1) * nbh * 32] = True
+                sel[pair[t_, j_], base + k * nbh * 32 + j_ * nbh * 2: base + k * nbh * 32 + (j_ + 1) * nbh * 2] = True
+        mine = sel[lv].any(axis=0)
+        assert_bits_equal(hqv[mine], hq_r[mine], f"Q8_0 blocks of h rep {rep}")
+        assert (hqv[sel[~lv].any(axis=0)] == 0xAB).all(), "non-local pairs leave their Q8_0 blocks unwritten"
         assert_bits_equal(out.cpu().numpy(), out_r, f"out rep {rep}")
         assert_bits_equal(resid.cpu().numpy(), (resid0.numpy() + out_r).astype(np.float32), f"resid + out rep {rep}")
         assert rel_l2(out.cpu().numpy(), out_r) <= TOL
