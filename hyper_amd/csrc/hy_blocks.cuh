@@ -27,7 +27,8 @@ __device__ __forceinline__ uint32_t kv4(uint32_t idx) {
     // (bytes: -127 -104 -83 -65 | -49 -35 -22 -10 | 1 13 25 38 | 53 69 89 113)
     const uint32_t sel = idx & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
-    const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
+    // 0xFF in the bytes whose index is 8..15: selector idx >> 1 picks a byte of 0xFFFFFFFF (4..7) or of 0 (0..3)
+    const uint32_t m = __builtin_amdgcn_perm(0xFFFFFFFFu, 0u, (idx >> 1) & 0x07070707u);
     return (hi & m) | (lo & ~m);
 }
 // IQ2 signs: 8 sign bits -> two words whose bytes are 0xFF where negated; value = (g ^ M) + (M & 1)
@@ -106,8 +107,8 @@ template <> struct Item<Q6_K> {
     uint16_t d;
     __device__ __forceinline__ void load(const uint8_t *b, int L) {
         const int hf = L >> 2, qt0 = (L >> 1) & 1, hl = L & 1, g = 8 * hf + 2 * qt0 + hl;
-        ql = load16_a2(b + 64 * hf + 32 * qt0 + 16 * hl);
-        qh = load16_a2(b + 128 + 32 * hf + 16 * hl);
+        ql = load16_a2_nb(b + 64 * hf + 32 * qt0 + 16 * hl);   // (both end well inside the 210-byte block)
+        qh = load16_a2_nb(b + 128 + 32 * hf + 16 * hl);
         sc_lo = (int8_t) b[192 + g]; sc_hi = (int8_t) b[192 + g + 4];
         d = ld_u16(b + 208);
     }
@@ -183,7 +184,9 @@ template <> struct Item<IQ2_XS> {
 template <> struct Item<IQ4_NL> {
     uint4 qs;
     uint16_t d;
-    __device__ __forceinline__ void load(const uint8_t *b, int L) { qs = load16_a2(b + 18 * L + 2); d = ld_u16(b + 18 * L); }
+    // qs of block L: 2 mod 4 for even L (spans are 16-byte aligned), where the 2 bytes read past them are the next
+    // block's d (L < 7)
+    __device__ __forceinline__ void load(const uint8_t *b, int L) { qs = load16_a2_nb(b + 18 * L + 2); d = ld_u16(b + 18 * L); }
     __device__ __forceinline__ void ints(const uint8_t *y, int, int &si, int &sm) const {
         const uint32_t *ya = (const uint32_t *) (y + 4);
         const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};

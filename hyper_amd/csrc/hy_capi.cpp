@@ -36,6 +36,9 @@ static int check_dev(const hy_moe_dev *m, const char *what, bool need_gate, bool
     // every kernel's grid covers ff and n in whole 256-row / 256-value units (the tiled layout's 16-row tiles, the
     // GEMMs' 64- and 128-row blocks): both are checked whichever matrices the entry point reads
     if (m->n % 256 || m->ff % 256) { set_error("%s: n = %d and ff = %d must be multiples of 256", what, m->n, m->ff); return HY_EBAD_SHAPE; }
+    // the kernels read weight bytes in 16-byte pieces and rely on the tiles (16 rows of a span: a multiple of 16
+    // bytes, as every expert matrix is) starting 16-byte aligned, so the matrices themselves must
+    if (((uintptr_t) m->gate | (uintptr_t) m->up | (uintptr_t) m->down) & 15) { set_error("%s: weight matrices must be 16-byte aligned", what); return HY_EBAD_SHAPE; }
     if (need_gate) {
         if (!dot_type(m->tg)) { set_error("%s: unsupported gate/up type %d", what, m->tg); return HY_EUNSUPPORTED_TYPE; }
         if (!m->gate || !m->up) { set_error("%s: null gate/up", what); return HY_EINVAL; }

@@ -206,6 +206,16 @@ __device__ __forceinline__ uint4 load16_a2(const uint8_t *p) {
     v.x = h0 | (d1 << 16); v.y = (d1 >> 16) | (d2 << 16); v.z = (d2 >> 16) | (d3 << 16); v.w = (d3 >> 16) | (h4 << 16);
     return v;
 }
+// the same without a branch, for lanes whose alignments differ: four dwords from p & ~3 and a fifth when p is 2 mod 4
+// (else the fourth again), joined with v_alignbyte; reads at most p + 17, so the 2 bytes after the 16 must exist
+// whenever p is 2 mod 4
+__device__ __forceinline__ uint4 load16_a2_nb(const uint8_t *p) {
+    const uint32_t sb = (uint32_t) ((uintptr_t) p & 3);
+    const uint32_t *w = (const uint32_t *) (p - sb);
+    const uint32_t d0 = w[0], d1 = w[1], d2 = w[2], d3 = w[3], d4 = w[sb ? 4 : 3];
+    return make_uint4(__builtin_amdgcn_alignbyte(d1, d0, sb), __builtin_amdgcn_alignbyte(d2, d1, sb),
+                      __builtin_amdgcn_alignbyte(d3, d2, sb), __builtin_amdgcn_alignbyte(d4, d3, sb));
+}
 __device__ __forceinline__ uint4 load16_a4(const uint8_t *p) {   // dword-aligned 16 bytes
     const uint32_t *q = (const uint32_t *) p;
     uint4 v; v.x = q[0]; v.y = q[1]; v.z = q[2]; v.w = q[3];

@@ -45,6 +45,7 @@ enum {
    matrix in the tiled order the kernels read: 16-row tiles whose 256-value spans lie together -- span s (sb bytes,
    the GGUF blocks of 256 values) of row r at byte ((r / 16) * nspan + s) * 16 * sb + (r % 16) * sb, nspan = values
    per row / 256.  The block bytes themselves are GGUF's; hy_upload_experts writes this order from GGUF rows.
+   gate, up and down start 16-byte aligned (checked: HY_EBAD_SHAPE).
    slot[e] (device, n_expert entries) = local index of expert e or -1. */
 typedef struct hy_moe_dev {
     const uint8_t *gate, *up, *down;

@@ -154,3 +154,15 @@ def test_noalloc_decode_rejects_what_its_scratch_cannot_hold():
     assert L.hy_moe_decode_ws_bytes(ctypes.byref(m), 384, 6, None, 64) > (1 << 20)
     rc = L.hy_moe_decode_noalloc(ctypes.byref(m), p, 384, p, 7168, None, 0, 6, None, p, 0, 64, None)
     assert rc == hyper_amd.HY_EBAD_SHAPE and b"scratch" in L.hy_last_error()
+
+
+def test_descriptor_weights_16_byte_aligned():
+    """The kernels read weight bytes in 16-byte pieces from tiles that start 16-byte aligned: a gate, up or down
+    matrix that does not start on 16 bytes is rejected before any device work."""
+    L = lib()
+    p = ctypes.c_void_p(16)
+    for field in ("gate", "up", "down"):
+        m = _dev()
+        setattr(m, field, 16 + 2)
+        assert L.hy_moe_gate_up(ctypes.byref(m), p, 2048, p, 8, p, 1, None, None, None) == hyper_amd.HY_EBAD_SHAPE
+        assert b"16-byte aligned" in L.hy_last_error()
