@@ -293,6 +293,14 @@ int hy_moe_route_gate_up(const hy_moe_dev *m, const float *logits, int ls, int n
     return launch_route_gate_up(*m, logits, ls, n_expert, k, xq, ids, wts, sg, h, nt, s);
 }
 
+int hy_moe_shared_gate_up(const hy_moe_dev *m, const void *xq, float *h, int nt, hipStream_t s) {
+    int rc = check_dev(m, "hy_moe_shared_gate_up", true, false);
+    if (rc) return rc;
+    if (!xq || !h || nt < 0) { set_error("hy_moe_shared_gate_up: bad argument"); return HY_EINVAL; }
+    if ((uintptr_t) xq & 3) { set_error("hy_moe_shared_gate_up: xq must be 4-byte aligned"); return HY_EBAD_SHAPE; }
+    return launch_fixed_gate_up(*m, xq, h, nt, s);
+}
+
 int hy_moe_route_gate_up_q8(const hy_moe_dev *m, const float *logits, int ls, int n_expert, int k, const void *xq, int32_t *ids,
                             float *wts, float *sg, float *h, void *hq, int nt, hipStream_t s) {
     if (!hq) { set_error("hy_moe_route_gate_up_q8: bad argument"); return HY_EINVAL; }

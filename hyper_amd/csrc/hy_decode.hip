@@ -183,6 +183,7 @@ constexpr int DEC_GU_BLOCKS = HY_DEC_GU_BLOCKS;   // grid size the rows per wave
 #endif
 constexpr int DEC_PIPE_NP = HY_DEC_PIPE_NP;        // passes per round when a wave's positions take several rounds
 
+// V = 0: no routing, the pairs are the tokens and their expert the descriptor's local expert 0 (a shared expert).
 // HQ: the block's 8 rw = 32 rows form one Q8_0 block of every pair's hidden row, and the fold also writes it to hq
 // (the down kernel then reads the hidden quantized instead of quantizing it in every block).  PIPE: for waves with
 // several rounds of items, each round's loads go out before the previous round's dots.
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     __shared__ float tv[DEC_GU_WAVES * TVN + 64];
     __shared__ int s_ids[64];
     __shared__ float s_wts[64], s_sg;
-    __shared__ int s_slot[64 * V];
+    __shared__ int s_slot[V ? 64 * V : 1];
     __shared__ uint2 grid[T == IQ2_XS ? IQ2XS_LDS : 1];
     __shared__ float s_xd[DEC_GU_TV / 2];   // activation scales of the token's Q8 row, one per weight block
     __shared__ __align__(16) uint8_t s_y[DEC_Y_BYTES];   // the token's Q8 row (every item reads its 256-value span here)
@@ -249,7 +250,11 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     const float *lg = logits + (size_t) t * ls;
     // the token's routing: every block of the token computes the same bits
     int e_sel;   // the expert of pair j
-    if constexpr (V <= 2) {
+    if constexpr (V == 0) {   // no routing: every pair is local expert 0 (the always-on shared expert, k = 1)
+        stage();
+        lds_barrier();
+        e_sel = 0;
+    } else if constexpr (V <= 2) {
         static_assert(DEC_GU_WAVES == 8, "route_rank8 takes eight waves");
         int er;
         float pr, tot, lsg;
@@ -612,6 +617,25 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
     });
 #undef HY_RGU_V
 #undef HY_RGU
+}
+
+// the gate/up of local expert 0 for every token (a shared expert) from the Q8 rows: k_route_gate_up without routing
+int launch_fixed_gate_up(const hy_moe_dev &m, const void *xq, float *h, int nt, hipStream_t s) {
+    const int ng = m.n / 256, nb = m.n / block_elems(m.tg);
+    if (2 * ng > 8 * DEC_MAXP || 2 * nb > DEC_GU_TV) { set_error("hy_moe_shared_gate_up: n = %d exceeds %d", m.n, 256 * 4 * DEC_MAXP); return HY_EBAD_SHAPE; }
+    if (m.gate_bytes >= ((size_t) 1 << 32)) { set_error("hy_moe_shared_gate_up: an expert matrix of %zu bytes (4 GiB or more)", m.gate_bytes); return HY_EBAD_SHAPE; }
+    if (nt == 0) return HY_OK;
+    int rw = 1;   // rows per wave, as in launch_route_gate_up
+    auto nblocks = [&](int r) { return (long) ((m.ff + DEC_GU_WAVES * r - 1) / (DEC_GU_WAVES * r)) * nt; };
+    while (rw < 8 && nblocks(rw) > DEC_GU_BLOCKS && (rw + 1) * 2 * nb <= DEC_GU_TV) ++rw;
+    dim3 grid((m.ff + DEC_GU_WAVES * rw - 1) / (DEC_GU_WAVES * rw), nt);
+    const int np = (rw * ng + 7) / 8, q8 = 8 / ng, r8 = 8 % ng;
+#define HY_FGU(NN, PP) hipLaunchKernelGGL((k_route_gate_up<TT, 0, NN, false, PP>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, nullptr, 0, 1, 1, (const uint8_t *) xq, nullptr, nullptr, nullptr, h, rw, q8, r8, nullptr)
+    HY_DEC_SWITCH(m.tg, {
+        if (np <= 1) { HY_FGU(1, false); } else if (np <= 2) { HY_FGU(2, false); } else if (np <= 4) { HY_FGU(4, false); } else { HY_FGU(DEC_PIPE_NP, true); }
+        return check_launch("hy_moe_shared_gate_up");
+    });
+#undef HY_FGU
 }
 
 static bool dec_down_fits(const hy_moe_dev &m, int k) {

@@ -37,6 +37,8 @@ int launch_router_q8(const float *W, int rows, int kdim, const float *x, int xs,
 // hq: also write the Q8_0 rows of h (down types whose partner is Q8_0); HY_EUNSUPPORTED_TYPE where that does not apply
 int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int ne, int k, const void *xq, int *ids, float *wts, float *sg,
                          float *h, int nt, hipStream_t s, uint8_t *hq = nullptr);
+// SwiGLU(gate, up) of the descriptor's local expert 0 for nt Q8 rows (a shared expert's decode gate/up, no routing)
+int launch_fixed_gate_up(const hy_moe_dev &m, const void *xq, float *h, int nt, hipStream_t s);
 // whether launch_dec_down runs its fused kernel (not HY_EUNSUPPORTED_TYPE) for this layer and k
 bool dec_down_takes_q8(const hy_moe_dev &m, int k);
 // hq: the hidden as Q8_0 rows (from launch_route_gate_up) instead of h

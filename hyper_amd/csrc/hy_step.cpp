@@ -96,7 +96,10 @@ int run_decode(const hy_moe_dev &m, const float *W_r, int rows, const float *x, 
         if ((rc = shared_tables(T))) return rc;
         float *sh_h = (float *) (ws + L.sh_h);
         shexp = (float *) (ws + L.sh_y);
-        if ((rc = launch_gate_up(*S, x, xs, T.ids, 1, sh_h, nt, s, nullptr, nullptr))) return rc;
+        // from the Q8 rows of x when the shared expert's gate type takes the same activation type, else from x
+        if (vec_dot_type(S->tg) == vec_dot_type(m.tg)) rc = launch_fixed_gate_up(*S, xq, sh_h, nt, s);
+        else rc = launch_gate_up(*S, x, xs, T.ids, 1, sh_h, nt, s, nullptr, nullptr);
+        if (rc) return rc;
         rc = launch_dec_down(*S, sh_h, T.ids, T.wts, 1, nullptr, nullptr, shexp, nt, s);
         if (rc == HY_EUNSUPPORTED_TYPE) rc = launch_down_reduce(*S, sh_h, T.ids, T.wts, 1, nullptr, nullptr, shexp, nt, s);
         if (rc) return rc;

@@ -172,6 +172,11 @@ def moe_route_gate_up(m: MoeDev, logits, ls, n_expert, k, xq, ids, wts, sg, h, n
     check(lib().hy_moe_route_gate_up(m.ref, _p(logits), ls, n_expert, k, _p(xq), _p(ids), _p(wts), _p(sg), _p(h), nt, _s(stream)))
 
 
+def moe_shared_gate_up(m: MoeDev, xq, h, nt, stream=None):
+    """The shared expert's decode gate/up (local expert 0, k = 1) from the Q8 rows of x."""
+    check(lib().hy_moe_shared_gate_up(m.ref, _p(xq), _p(h), nt, _s(stream)))
+
+
 def moe_route_gate_up_q8(m: MoeDev, logits, ls, n_expert, k, xq, ids, wts, sg, h, hq, nt, stream=None):
     """moe_route_gate_up that also writes the hidden rows as Q8_0 blocks (down types with a Q8_0 partner)."""
     check(lib().hy_moe_route_gate_up_q8(m.ref, _p(logits), ls, n_expert, k, _p(xq), _p(ids), _p(wts), _p(sg), _p(h), _p(hq), nt,
@@ -240,6 +245,10 @@ class MoeLayerRunner:
         nbh = self.ff // 32
         self.dec_hq = (router == "softmax" and L.tg == GType.IQ4_NL and L.td == GType.IQ4_NL and self.d <= 4096 and self.k * nbh <= 512
                        and self.k * nbh * 34 <= 32768 and self.E <= 1024)
+        self._side = None   # the shared expert's decode stream, made on first use
+        # decode's shared expert on a second stream: None = from 4 rows on (a one-token step is shorter in order, its
+        # launches then do not compete with the routed gate/up for CUs), True / False = always / never
+        self.shared_stream: Optional[bool] = None
         if shared is not None:
             S = shared.layer
             self.sh_ids = torch.zeros(T, **i32)
@@ -271,7 +280,10 @@ class MoeLayerRunner:
 
     def _shared_decode(self, x, nt, stream):
         S = self.shared
-        moe_gate_up(S, x, x.stride(0), self.sh_ids, 1, self.sh_h, nt, stream)
+        if vec_dot_type(S.layer.tg) == self.vg:   # the routed gate's Q8 rows of x serve the shared expert too
+            moe_shared_gate_up(S, self.xq, self.sh_h, nt, stream)
+        else:
+            moe_gate_up(S, x, x.stride(0), self.sh_ids, 1, self.sh_h, nt, stream)
         moe_down_reduce(S, self.sh_h, self.sh_ids, self.sh_ones, 1, None, None, self.sh_y, nt, stream)
 
     def _shared_decode_legacy(self, x, nt, stream):
@@ -320,14 +332,29 @@ class MoeLayerRunner:
         nt = self._check_rows(x, bias, resid)
         moe_router_q8(self.W_r, self.W_r.shape[0], self.d, x, x.stride(0), self.logits, self.ls, self.vg, self.xq, nt, stream,
                       bias=bias, bias_stride=0 if bias is None else bias.stride(0))
-        shexp = None
-        if self.shared is not None:
+        shexp, joined = None, None
+        side = self.shared_stream if self.shared_stream is not None else nt >= 4
+        if self.shared is not None and not side:
             self._shared_decode(x, nt, stream)
             shexp = self.sh_y
+        elif self.shared is not None:
+            # the shared expert does not depend on the routing: its two launches run on a second stream (default
+            # priority), forked after the Q8 rows of x and joined before the combine
+            main = stream if stream is not None else torch.cuda.current_stream()
+            if self._side is None:
+                self._side = torch.cuda.Stream(device=self.device)
+                self._fork, self._join = torch.cuda.Event(), torch.cuda.Event()
+            self._fork.record(main)
+            self._side.wait_event(self._fork)
+            self._shared_decode(x, nt, self._side)
+            self._join.record(self._side)
+            shexp, joined = self.sh_y, main
         if self.dec_hq:
             moe_route_gate_up_q8(self.dev, self.logits, self.ls, self.E, self.k, self.xq, self.ids, self.wts, self.sg, self.h, self.hq,
                                  nt, stream)
             out = self.out if resid is None else resid
+            if joined is not None:
+                joined.wait_event(self._join)
             moe_down_reduce_q8(self.dev, self.hq, self.ids, self.wts, self.k, shexp, self.sg, out, resid is not None, nt, stream)
             return out[:nt]
         if self.router == "softmax":
@@ -335,6 +362,8 @@ class MoeLayerRunner:
         else:   # the fused route + gate/up kernel routes by softmax: route first, then the gate/up GEMV by ids
             self._route_logits(nt, stream)
             moe_gate_up(self.dev, x, x.stride(0), self.ids, self.k, self.h, nt, stream)
+        if joined is not None:
+            joined.wait_event(self._join)
         if resid is not None:
             moe_down_reduce_residual(self.dev, self.h, self.ids, self.wts, self.k, shexp, self.sg, resid, nt, stream)
             return resid[:nt]

@@ -205,6 +205,11 @@ int hy_moe_router_q8(const float *W_r, int rows, int kdim, const float *x, int x
 int hy_moe_route_gate_up(const hy_moe_dev *m, const float *logits, int ls, int n_expert, int k, const void *xq, int32_t *ids, float *wts,
                          float *sg, float *h, int nt, hipStream_t s);
 
+/* Decode gate/up of the always-on (shared) expert: h[t] = SwiGLU(gate . x_t, up . x_t) of the descriptor's local
+   expert 0 for nt tokens, from their Q8 rows xq (partner type of the gate type), as hy_moe_gate_up with every id 0
+   and k = 1 computes it from x (the reference's shared-expert call of moe_gate_up, src/engine4.cu:795-804). */
+int hy_moe_shared_gate_up(const hy_moe_dev *m, const void *xq, float *h, int nt, hipStream_t s);
+
 /* hy_moe_route_gate_up that also writes hq: the pairs' hidden rows as Q8_0 blocks (the values and scales
    hy_q8_quantize(Q8_0, h row) gives), so the down step reads them instead of quantizing h in every block -- the down
    kernels' activation quantization (src/kernels4.cu:2007-2022 quantizes h per launch) moved into the producer.

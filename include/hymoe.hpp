@@ -168,6 +168,10 @@ inline void moe_route_gate_up(const MoeDev &m, const float *logits, int ls, int 
                               float *sg, float *h, int nt, hipStream_t s) {
     check(hy_moe_route_gate_up(&m, logits, ls, n_expert, k, xq, ids, wts, sg, h, nt, s));
 }
+// the shared expert's decode gate/up from the Q8 rows of x (moe_gate_up with every id 0, k = 1)
+inline void moe_shared_gate_up(const MoeDev &m, const void *xq, float *h, int nt, hipStream_t s) {
+    check(hy_moe_shared_gate_up(&m, xq, h, nt, s));
+}
 // moe_route_gate_up that also writes the hidden rows as Q8_0 blocks, and the down + combine that reads them (down types
 // whose partner is Q8_0)
 inline void moe_route_gate_up_q8(const MoeDev &m, const float *logits, int ls, int n_expert, int k, const void *xq, int *ids, float *wts,

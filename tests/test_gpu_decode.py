@@ -223,3 +223,65 @@ def test_c_abi_upload_matches_python_upload(cuda, tg, td):
             assert_bits_equal(out.cpu().numpy(), out_r, "out")
     finally:
         moe.free_experts(c)
+
+
+@pytest.mark.parametrize("side", [True, False])
+def test_runner_decode_shared_graph_replays(cuda, side):
+    """Decode with a shared expert (its launches on a second stream forked and joined inside the step, or in order)
+    captured into a HIP graph: every replay, with eager steps (fewer rows) and synchronizations in between, equals the
+    oracle."""
+    tg, td, E, d, ff, k, nt = GType.Q4_K, GType.Q6_K, 32, 2048, 512, 6, 3
+    L = layer(tg, td, E, ff, d, seed=940)
+    S = layer(GType.Q4_K, GType.Q6_K, 1, ff, d, seed=941)
+    g = gen(942)
+    W_r = torch.randn(E + 1, d, generator=g) * 0.02
+    xs = [torch.randn(nt, d, generator=g) for _ in range(2)]
+
+    def ref(x):
+        logits = orc.gemv_f32(W_r.numpy(), x.numpy())
+        ids, wts, sgv = orc.route(logits, E, k, with_sg=True)
+        return orc.moe_layer(oracle_layer(L), x.numpy(), ids, wts, shared=oracle_layer(S), sg=sgv)
+
+    refs = [ref(x) for x in xs]
+    r = moe.MoeLayerRunner(moe.upload_experts(L, device=cuda), W_r.to(cuda), k, max_rows=nt,
+                           shared=moe.upload_experts(S, device=cuda), sg_logit=True)
+    r.shared_stream = side
+    xin = torch.empty(nt, d, device=cuda)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        xin.copy_(xs[0])
+        eager = r.decode(xin).clone()
+        torch.cuda.synchronize()
+        assert_bits_equal(eager.cpu().numpy(), refs[0], "eager decode")
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = r.decode(xin)
+    for rep in range(4):
+        i = rep % 2
+        xin.copy_(xs[i].to(cuda))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_bits_equal(out.cpu().numpy(), refs[i], f"replay {rep}")
+        one = r.decode(xs[1 - i][:1].to(cuda)).clone()   # an eager step of one row in between
+        torch.cuda.synchronize()
+        assert_bits_equal(one.cpu().numpy(), ref(xs[1 - i][:1]), f"eager one-row step {rep}")
+
+
+@pytest.mark.parametrize("tg,d,ff,nt", [(GType.Q4_K, 7168, 2048, 1), (GType.Q5_K, 2048, 512, 5), (GType.IQ2_XS, 7168, 2048, 8),
+                                        (GType.IQ4_NL, 4096, 1536, 2)])
+def test_shared_gate_up_bitexact(cuda, tg, d, ff, nt):
+    """hy_moe_shared_gate_up: local expert 0 for every token from the Q8 rows of x, bit for bit the oracle's h with
+    every id 0 and k = 1 (the shared expert's gate/up)."""
+    L = layer(tg, GType.Q6_K if tg != GType.IQ4_NL else GType.IQ4_NL, 1, ff, d, seed=960 + int(tg))
+    x = torch.randn(nt, d, generator=gen(961))
+    ids = np.zeros((nt, 1), dtype=np.int32)
+    wts = np.ones((nt, 1), dtype=np.float32)
+    _, h_r, _ = orc.moe_layer(oracle_layer(L), x.numpy(), ids, wts, want_hy=True)
+    dev = moe.upload_experts(L, device=cuda)
+    xq = torch.from_numpy(orc.quantize(vec_dot_type(tg), x.numpy())).reshape(-1).to(cuda)
+    h = torch.full((nt, ff), float("nan"), device=cuda)
+    moe.moe_shared_gate_up(dev, xq, h, nt)
+    torch.cuda.synchronize()
+    assert_bits_equal(h.cpu().numpy(), h_r, "h")
