@@ -367,12 +367,16 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
 constexpr int DEC_DN_WAVES = 8;       // output rows per block (a wave each)
 constexpr int DEC_DN_TV = 512;        // fold inputs per wave: k pairs x blocks of ff (k * nb <= 512)
 constexpr int DEC_DN_HQ = 32768;      // LDS bytes for the token's k quantized hidden rows
+#ifndef HY_DEC_DN_BLOCKS
+#define HY_DEC_DN_BLOCKS 512
+#endif
+constexpr int DEC_DN_BLOCKS = HY_DEC_DN_BLOCKS;   // grid size the rows per wave aim below
 
 template <int T, int NP>
 __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, const float *__restrict__ h, const int *__restrict__ ids,
                                                                const float *__restrict__ wts, int k, const float *__restrict__ shexp,
                                                                const float *__restrict__ sg, float *__restrict__ out, int res, int q8, int r8,
-                                                               const uint8_t *__restrict__ hqg) {
+                                                               const uint8_t *__restrict__ hqg, int rpw) {
     constexpr int VT = vec_dot_type(T), BE = block_elems(T);
     constexpr int SPAN_W = 256 / BE * block_bytes(T);
     // the token's k hidden rows in LDS: Q8_K blocks as they are (SPAN_L = 292 bytes a span); Q8_0 split into the
@@ -388,8 +392,9 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     const int t = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
     const int n = m.n, ff = m.ff, ng = ff / 256, nb = ff / BE, items = k * ng;
     uint16_t *hdq = (uint16_t *) (hq + (VT == Q8_K ? 0 : k * nb * 32));
-    const int row = blockIdx.x * DEC_DN_WAVES + wave;
-    const bool row_ok = row < n;
+    // the wave's output rows: rpw consecutive rows, one after the other (the block's hidden rows serve them all)
+    int row = (blockIdx.x * DEC_DN_WAVES + wave) * rpw;
+    bool row_ok = row < n;
     const float *hp = h + (size_t) t * k * ff;
     // Everything the block reads first goes out together: lane j < k's pair (expert, weight), the slot table and
     // the first batch of hidden rows (all k pairs' rows; those of skipped pairs are read but never used).
@@ -509,48 +514,57 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     HY_STAMP_WAIT(3);
     if (!row_ok) return;   // wave-uniform; no block barrier follows
     float *tw = tv[wave];
-    for (int base = 0; base < items; base += 8 * NP) {   // wave-uniform rounds of up to 8 NP items
-        if (base) load_round(base);
+    for (int rr = 0;;) {
+        for (int base = 0; base < items; base += 8 * NP) {   // wave-uniform rounds of up to 8 NP items
+            if (base) load_round(base);
 #pragma unroll
-        for (int ps = 0; ps < NP; ++ps) {
-            const int i = base + g + 8 * ps;
-            if (base + 8 * ps >= items) break;   // wave-uniform
-            const int j = cc.u, gi = cc.s;
-            const bool valid = i < items && pair_ok(j);
-            if constexpr (T == IQ2_XS) it[ps].grid = grid;
-            item_t<T>(it[ps], hq + (size_t) j * ng * SPAN_L, gi, L, valid, tw, j * (nb | 1) + (T == IQ4_NL ? 8 * gi : gi));
-            cc.next(ng, q8, r8);
+            for (int ps = 0; ps < NP; ++ps) {
+                const int i = base + g + 8 * ps;
+                if (base + 8 * ps >= items) break;   // wave-uniform
+                const int j = cc.u, gi = cc.s;
+                const bool valid = i < items && pair_ok(j);
+                if constexpr (T == IQ2_XS) it[ps].grid = grid;
+                item_t<T>(it[ps], hq + (size_t) j * ng * SPAN_L, gi, L, valid, tw, j * (nb | 1) + (T == IQ4_NL ? 8 * gi : gi));
+                cc.next(ng, q8, r8);
+            }
         }
-    }
-    wave_lds_sync();
-    HY_STAMP(4);
-    // lane j folds pair j in block order
-    float fo = 0.0f;
-    if (mine) {   // LDS reads four blocks at a time, then the fma chain
-        const uint8_t *yj = hq + (size_t) lane * ng * SPAN_L;
-        const float *tj = tw + lane * (nb | 1);
+        wave_lds_sync();
+        HY_STAMP(4);
+        // lane j folds pair j in block order
+        float fo = 0.0f;
+        if (mine) {   // LDS reads four blocks at a time, then the fma chain
+            const uint8_t *yj = hq + (size_t) lane * ng * SPAN_L;
+            const float *tj = tw + lane * (nb | 1);
+            float acc = 0.0f;
+            for (int b0 = 0; b0 < nb; b0 += 4) {
+                float sc[4], tq[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (b0 + u < nb) { sc[u] = VT == Q8_K ? q8_scale<VT>(yj, b0 + u) : h2f(hdq[lane * nb + b0 + u]); tq[u] = tj[b0 + u]; }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (b0 + u < nb) acc = __builtin_fmaf(sc[u], tq[u], acc);
+            }
+            fo = my_w * acc;
+        }
+        // the combine in rank order, each value read from the lane that holds it
+        const int nv = __builtin_popcountll(okm);
         float acc = 0.0f;
-        for (int b0 = 0; b0 < nb; b0 += 4) {
-            float sc[4], tq[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (b0 + u < nb) { sc[u] = VT == Q8_K ? q8_scale<VT>(yj, b0 + u) : h2f(hdq[lane * nb + b0 + u]); tq[u] = tj[b0 + u]; }
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (b0 + u < nb) acc = __builtin_fmaf(sc[u], tq[u], acc);
+        bool first = true;
+        if (shexp) { acc = sh_g * sh_x; first = false; }
+        for (int r = 0; r < nv; ++r) {
+            const float v = readlane_f(fo, __builtin_amdgcn_readlane(ordl, r));
+            if (first) { acc = v; first = false; } else acc = acc + v;
         }
-        fo = my_w * acc;
+        if (lane == 0) out[(size_t) t * n + row] = res ? out[(size_t) t * n + row] + acc : acc;   // res: the residual add
+        if (++rr == rpw || ++row >= n) break;   // wave-uniform
+        // the next row: its shared-expert value, fresh cursors, the first round of its weight bytes
+        if (shexp) sh_x = shexp[(size_t) t * n + row];
+        lc.start(g, ng);
+        cc.start(g, ng);
+        wave_lds_sync();   // this row's fold inputs are read before the next row's dots write them
+        load_round(0);
     }
-    // the combine in rank order, each value read from the lane that holds it
-    const int nv = __builtin_popcountll(okm);
-    float acc = 0.0f;
-    bool first = true;
-    if (shexp) { acc = sh_g * sh_x; first = false; }
-    for (int r = 0; r < nv; ++r) {
-        const float v = readlane_f(fo, __builtin_amdgcn_readlane(ordl, r));
-        if (first) { acc = v; first = false; } else acc = acc + v;
-    }
-    if (lane == 0) out[(size_t) t * n + row] = res ? out[(size_t) t * n + row] + acc : acc;   // res: the residual add
     HY_STAMP(5);
     HY_STAMP_SAVE(32768 + 8 * (int) (blockIdx.y * gridDim.x + blockIdx.x), 6, wave == 0 && lane == 0 && blockIdx.y * gridDim.x + blockIdx.x < 4095, true);
 }
@@ -655,10 +669,14 @@ int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const f
         return HY_EUNSUPPORTED_TYPE;
     }
     if (nt == 0) return HY_OK;
-    dim3 grid((m.n + DEC_DN_WAVES - 1) / DEC_DN_WAVES, nt);
+    // rows per wave: more than one when one row a wave would take more blocks than the CUs hold at once (about two
+    // blocks a CU), so that the blocks run in one round and each block quantizes its hidden rows once for them all
+    int rpw = 1;
+    while (rpw < 4 && (long) ((m.n + DEC_DN_WAVES * rpw - 1) / (DEC_DN_WAVES * rpw)) * nt > DEC_DN_BLOCKS) ++rpw;
+    dim3 grid((m.n + DEC_DN_WAVES * rpw - 1) / (DEC_DN_WAVES * rpw), nt);
     const int np = (k * ng + 7) / 8;   // passes of 8 items (more than 8: rounds)
     const int q8 = 8 / ng, r8 = 8 % ng;   // the item cursors' step
-#define HY_DN(NN) hipLaunchKernelGGL((k_dec_down<TT, NN>), grid, dim3(64 * DEC_DN_WAVES), 0, s, m, h, ids, wts, k, shexp, sg, out, res, q8, r8, hq)
+#define HY_DN(NN) hipLaunchKernelGGL((k_dec_down<TT, NN>), grid, dim3(64 * DEC_DN_WAVES), 0, s, m, h, ids, wts, k, shexp, sg, out, res, q8, r8, hq, rpw)
     HY_DEC_SWITCH(m.td, {
         // 8 passes a round only for IQ2_XS (same occupancy as 4); the others take more rounds at a higher occupancy
         if (np <= 2) HY_DN(2); else if (np <= 4 || TT != IQ2_XS) HY_DN(4); else HY_DN(8);

@@ -55,6 +55,7 @@ ROUTE_GU_CASES = [
     (GType.IQ4_XS, GType.IQ4_XS, 24, 4096, 1536, 8, 4, False),
     (GType.IQ2_XS, GType.IQ2_XS, 16, 7168, 2048, 6, 2, True),
     (GType.IQ4_NL, GType.IQ4_NL, 16, 2048, 4096, 8, 2, False),   # k * ff / 32 > 512: down falls back to the R-row kernel
+    (GType.Q4_K, GType.Q6_K, 64, 2560, 512, 8, 4, False),         # down: 3 rows a wave, the last block's rows past n
 ]
 
 
