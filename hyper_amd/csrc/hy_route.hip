@@ -129,8 +129,6 @@ __device__ __forceinline__ void gemv_block_lds(const float *__restrict__ W, int 
         if (row < GL_R) { const int r = r0 + row; src[k] = W + (size_t) (r < rows ? r : rows - 1) * kdim + 4 * lane; }
         else { const int t = t0 + row - GL_R; src[k] = x + (size_t) (t < nt ? t : nt - 1) * xs + 4 * lane; }
     }
-    float bv = 0.0f;   // lane a TW + b: the bias of (row wr0 + a, token wt0 + b), added after the butterfly
-    if (bias && lane < RW * TW && wr0 + lane / TW < rows && wt0 + lane % TW < nt) bv = bias[(size_t) (wt0 + lane % TW) * bs + wr0 + lane / TW];
     float acc[RW][TW];
 #pragma unroll
     for (int a = 0; a < RW; ++a)
@@ -166,14 +164,42 @@ __device__ __forceinline__ void gemv_block_lds(const float *__restrict__ W, int 
             }
         }
     }
+    // The butterfly sums through LDS (the stage is free once every wave is past the last step's reads).  A pass
+    // takes P outputs of the wave: each lane writes its P partial sums, then LPO = 64 / P lanes sum one output's 64
+    // partials -- lane q of them the pairwise tree over partials q (64 / LPO) .. , the butterfly's subtree over those
+    // lanes -- and combine their subtrees with DPP in the butterfly's order: the same tree, far fewer instructions
+    // than a butterfly per output.
+    constexpr int NOUT = RW * TW, P = GT == 16 ? 16 : 8, LPO = 64 / P, SUB = 64 / LPO;
+    static_assert(NOUT % P == 0 && 8 * 64 * P * 4 <= (GL_R + GT) * 64 * 16, "the passes fit the stage");
+    float *red = (float *) st + wave * 64 * P;
+    __syncthreads();
+    const int o = lane / LPO, q = lane % LPO;
 #pragma unroll
-    for (int a = 0; a < RW; ++a)
+    for (int p0 = 0; p0 < NOUT; p0 += P) {
 #pragma unroll
-        for (int b = 0; b < TW; ++b) {
-            float s = wave_sum_xor(acc[a][b]);
-            if (bias) s = s + readlane_f(bv, a * TW + b);
-            if (lane == 0 && wr0 + a < rows && wt0 + b < nt) y[(size_t) (wt0 + b) * ys + wr0 + a] = s;
+        for (int u = 0; u < P; ++u) red[u * 64 + lane] = acc[(p0 + u) / TW][(p0 + u) % TW];
+        wave_lds_sync();
+        float v[SUB];
+#pragma unroll
+        for (int u = 0; u < SUB; u += 4) {
+            const f4v w4 = *(const f4v *) (red + o * 64 + q * SUB + u);
+            v[u] = w4.x; v[u + 1] = w4.y; v[u + 2] = w4.z; v[u + 3] = w4.w;
         }
+#pragma unroll
+        for (int h = 1; h < SUB; h <<= 1)   // pairwise tree, natural order
+#pragma unroll
+            for (int u = 0; u < SUB; u += 2 * h) v[u] = v[u] + v[u + h];
+        float sum = v[0];
+        sum = sum + dpp_f<DPP_XOR1>(sum);                         // lanes q, q ^ 1 (the next two levels up)
+        sum = sum + dpp_f<DPP_XOR2>(sum);
+        if constexpr (LPO == 8) sum = sum + dpp_f<DPP_HALF_MIRROR>(sum);   // quads 0-3 with 4-7
+        const int idx = p0 + o, a = idx / TW, b = idx % TW;
+        if (q == 0 && wr0 + a < rows && wt0 + b < nt) {
+            if (bias) sum = sum + bias[(size_t) (wt0 + b) * bs + wr0 + a];
+            y[(size_t) (wt0 + b) * ys + wr0 + a] = sum;
+        }
+        wave_lds_sync();   // this pass's reads are done before the next pass writes
+    }
 }
 
 // Router logits of many tokens and the Q8 rows of x in one launch: blocks [0, gemv_blocks) compute the logits (gx
