@@ -14,8 +14,9 @@ Q8 of x -> routing + gate/up GEMV -> down GEMV + combine, cycling 4 layer copies
 
 Secondary (`workloads` object): the other configured workloads at their full shapes -- IQ4_NL / IQ4_XS (d_model
 4096, 288 experts) at 1 and 4 rows, IQ2_XS (d_model 7168, 384 experts, top-6) with a shared Q4_K expert at 1 and 8
-rows, and one 2048-token chunk of Q5_K/Q6_K (512 experts, top-10, shared expert) -- µs per step and the HBM rate of
-the expert bytes each step touches.
+rows, one 2048-token chunk of Q5_K/Q6_K (512 experts, top-10, shared expert) and the whole 16384-token prompt as 8
+such chunks (routing drawn per chunk, outputs added into the residual) -- µs per step and the HBM rate of the expert
+bytes each step touches; verify batches also through the grouped GEMM path.
 
 `roofline` reports the dominant kernel of the headline step against HBM bandwidth (8 TB/s): algorithmic bytes
 per launch / its average launch duration, measured on its own stream with HIP events over graph replays of
@@ -185,15 +186,18 @@ def decode_bench(args, dev, stream):
 
 
 def workloads_bench(args, dev, stream):
-    """The other configured workloads at their full shapes (C3-C5: IQ4_NL / IQ4_XS decode and 4-row verify, IQ2_XS with
-    a shared Q4_K expert at 1 and 8 rows, the 2048-token Q5_K/Q6_K chunk): µs per step from graph replays over
-    `workload_copies` weight copies and fresh inputs.  Bytes per step: the distinct experts its rows route to, the
-    shared expert, the router weights and the activations in and out."""
+    """The other configured workloads at their full shapes (IQ4_NL / IQ4_XS decode and 4-row verify, IQ2_XS with a
+    shared Q4_K expert at 1 and 8 rows, one 2048-token Q5_K/Q6_K chunk and the whole 16384-token prompt as 8 such
+    chunks): µs per step from graph replays over `workload_copies` weight copies and fresh inputs.  Bytes per step, per
+    layer call: the distinct experts its rows route to, the shared expert and the router weights; plus the activations
+    in and out.  Verify batches are also timed through the grouped GEMM path (`us_per_step_grouped`)."""
     res = {}
     for name, w in WORKLOADS.items():
         if name in ("q4k_decode", "q4k_q6k_prefill512") or (args.workload and name not in args.workload):
             continue
-        copies, n_in, nsteps = args.workload_copies, 4, 8
+        C = w.chunk or w.rows   # rows per layer call
+        nch = w.rows // C
+        copies, n_in, nsteps = args.workload_copies, 4, 8 if nch == 1 else 2
         g = torch.Generator(device=dev)
         g.manual_seed(4321)
         layers = [random_layer(w.tg, w.td, w.E, w.ff, w.d, seed=500 + c, device=dev, d_range=w.d_range, d_range_down=w.d_range_down)
@@ -201,32 +205,51 @@ def workloads_bench(args, dev, stream):
         S = random_layer(w.shared[0], w.shared[1], 1, w.ff, w.d, seed=550, device=dev, d_range=w.d_range) if w.shared else None
         sdev = moe.MoeDev(S, torch.zeros(1, dtype=torch.int32, device=dev)) if S is not None else None
         runners = [moe.MoeLayerRunner(moe.MoeDev(L, torch.arange(w.E, dtype=torch.int32, device=dev)),
-                                      torch.randn(w.E, w.d, generator=g, device=dev) * 0.02, w.k, w.rows, shared=sdev) for L in layers]
+                                      torch.randn(w.E, w.d, generator=g, device=dev) * 0.02, w.k, C, shared=sdev) for L in layers]
         xs = [activations(w.rows, w.d, g, dev, lognormal=w.norm_lognormal) for _ in range(n_in)]
-        bs = [zipf_logit_bias(w.rows, w.E, w.zipf, g, dev) if w.zipf else None for _ in range(n_in)]
+        # a chunked prompt draws its routing skew per chunk
+        bs = [[zipf_logit_bias(C, w.E, w.zipf, g, dev) if w.zipf else None for _ in range(nch)] for _ in range(n_in)]
+        resid = torch.zeros(w.rows, w.d, device=dev) if nch > 1 else None
         decode = w.rows <= 8
 
-        def step(r, x, b):
-            return r.decode(x, bias=b) if decode else r.prefill(x, bias=b)
+        def step(r, x, b, grouped=False):
+            if nch > 1:   # the prompt's chunks in order, each chunk's output added into its residual rows
+                for j in range(nch):
+                    r.prefill(x[j * C:(j + 1) * C], bias=b[j], resid=resid[j * C:(j + 1) * C])
+                return resid
+            return r.decode(x, bias=b[0]) if decode and not grouped else r.prefill(x, bias=b[0])
 
         touched = []
         for i in range(n_in):
-            step(runners[0], xs[i], bs[i])
-            torch.cuda.synchronize()
-            touched.append(int(torch.unique(runners[0].ids[: w.rows * w.k]).numel()))
-        fns = [lambda c=i % copies, i=i: step(runners[c], xs[i % n_in], bs[i % n_in]) for i in range(nsteps)]
-        with torch.cuda.stream(stream):
-            for f in fns:
-                f()
-            torch.cuda.synchronize()
-            ms = graph_time(fns, max(1, args.decode_reps), stream) / nsteps
+            for j in range(nch):
+                runners[0].prefill(xs[i][j * C:(j + 1) * C], bias=bs[i][j]) if nch > 1 else step(runners[0], xs[i], bs[i])
+                torch.cuda.synchronize()
+                touched.append(int(torch.unique(runners[0].ids[: C * w.k]).numel()))
+
+        def timed(grouped=False):
+            fns = [lambda c=i % copies, i=i: step(runners[c], xs[i % n_in], bs[i % n_in], grouped) for i in range(nsteps)]
+            with torch.cuda.stream(stream):
+                for f in fns:
+                    f()
+                torch.cuda.synchronize()
+                return graph_time(fns, max(1, args.decode_reps), stream) / nsteps
+
+        ms = timed()
         L0 = layers[0]
-        step_bytes = float(np.mean(touched)) * L0.expert_bytes() + (S.expert_bytes() if S is not None else 0) + w.E * w.d * 4 + 2 * w.rows * w.d * 4
+        # per layer call: the distinct experts its rows route to, the shared expert, the router, activations in and out
+        step_bytes = nch * (float(np.mean(touched)) * L0.expert_bytes() + (S.expert_bytes() if S is not None else 0) + w.E * w.d * 4) \
+            + 2 * w.rows * w.d * 4
         gbs = step_bytes / (ms / 1e3) / 1e9
         res[name] = {"rows": w.rows, "us_per_step": round(ms * 1e3, 2), "tok_s": round(w.rows / (ms / 1e3), 1),
                      "experts_touched": float(np.mean(touched)), "alg_bytes": step_bytes, "hbm_gbs": round(gbs, 1),
                      "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "path": "decode" if decode else "prefill"}
-        log(f"workload {name}: {ms * 1e3:.2f} us/step, {gbs:.0f} GB/s")
+        if nch > 1:
+            res[name].update(chunks=nch, chunk_rows=C)
+        if decode and w.rows > 1:
+            # the same verify batch through the grouped GEMM path (bucketing + grouped GEMMs + combine), for the choice
+            res[name]["us_per_step_grouped"] = round(timed(grouped=True) * 1e3, 2)
+        log(f"workload {name}: {ms * 1e3:.2f} us/step, {gbs:.0f} GB/s"
+            + (f" (grouped GEMM path {res[name]['us_per_step_grouped']:.2f} us)" if "us_per_step_grouped" in res[name] else ""))
         del runners, layers, sdev, S
         torch.cuda.empty_cache()
     return res

@@ -665,9 +665,9 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
                 for (int v = 0; v < 4; ++v) si[i][v] = 0;
                 sm[i] = v4i{0, 0, 0, 0};
             }
-            if constexpr (B == 1) {
+            if constexpr (B == 1 && W == 8) {
                 // the step's activation fragments (tile, chunk) read from LDS up front: one LDS round trip a step
-                // instead of one per chunk and tile (the register budget of one block per CU has room for them)
+                // instead of one per chunk and tile (the register budget of one 8-wave block per CU has room for them)
                 long af[GM_TILES][8];
 #pragma unroll
                 for (int tile = 0; tile < GM_TILES; ++tile) {
@@ -679,7 +679,12 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
                 for (int c = 0; c < 8; ++c) chunk_ints<T, true>(wr, c, q, grid, as, rr, ntile, si, sm, af);
             } else {
 #pragma unroll
-                for (int c = 0; c < 8; ++c) chunk_ints<T, true>(wr, c, q, grid, as, rr, ntile, si, sm);
+                for (int c = 0; c < 8; ++c) {
+                    chunk_ints<T, true>(wr, c, q, grid, as, rr, ntile, si, sm);
+                    // 16 waves (128 registers): a scheduling-region boundary per chunk, so that the next chunks'
+                    // operand reads are not hoisted into this one (which spilled)
+                    if constexpr (W == 16) asm volatile("");
+                }
             }
 #pragma unroll
             for (int tile = 0; tile < GM_TILES; ++tile) {
@@ -960,12 +965,15 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
 constexpr int GM_MAX_ITEMS = 1 << 16;
 // upper bound of the work items: sum over active experts of ceil(cnt / GM_TOK) <= ceil(P / GM_TOK) + active
 static int max_items(int n_pairs, int max_active) { return (n_pairs + GM_TOK - 1) / GM_TOK + max_active; }
-// item slots per row tile: enough blocks for about `per_cu` resident blocks on every CU
-static int item_slots(int row_tiles, int n_pairs, int max_active, int per_cu) {
-    // the current device's CU count (an attribute query: cheap, thread-safe, and right for each device)
+// the current device's CU count (an attribute query: cheap, thread-safe, and right for each device)
+static int cu_count() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    const int want = cus * per_cu / row_tiles;   // every block resident at once
+    return cus;
+}
+// item slots per row tile: enough blocks for about `per_cu` resident blocks on every CU
+static int item_slots(int row_tiles, int n_pairs, int max_active, int per_cu) {
+    const int want = cu_count() * per_cu / row_tiles;   // every block resident at once
     const int n = std::max(1, std::min(max_items(n_pairs, max_active), want));
     const int P = 8 / xcd_gcd8(row_tiles);       // k_gemm places consecutive items P slots apart: a multiple of P
     return n >= P ? n / P * P : n;
@@ -983,6 +991,15 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
     if ((size_t) n_pairs * (m.n / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_gate_up: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
     if (k <= 0 || (uint64_t) n_pairs * (uint64_t) k >= (1ull << 32)) { set_error("hy_moe_gemm_gate_up: k out of range for the pair count"); return HY_EBAD_SHAPE; }
     if (max_items(n_pairs, max_active) >= GM_MAX_ITEMS) { set_error("hy_moe_gemm_gate_up: %d pairs make more than %d work items", n_pairs, GM_MAX_ITEMS - 1); return HY_EBAD_SHAPE; }
+    // Q5_K: 16-wave blocks (256 weight rows, so every item's activations are read by half as many row blocks, and
+    // four waves a SIMD) while that grid still has a block for every CU; fewer items (a shared expert's) keep 8 waves
+    // and twice the blocks.  ff is a multiple of 256, so either size tiles it.
+    if (m.tg == Q5_K && max_items(n_pairs, max_active) * (m.ff / 128) >= cu_count()) {
+        const int rb = m.ff / 128;
+        dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
+        hipLaunchKernelGGL((k_gemm<Q5_K, true, 16, 1>), grid, dim3(1024), 0, s, m, (const uint8_t *) xq, div_mul_of(k), order, order_n, egrp, nullptr, h);
+        return check_launch("hy_moe_gemm_gate_up");
+    }
     HY_GEMM_SWITCH(m.tg, {
         constexpr int W = 8, B = g5_blocks<TT, true>();
         const int rb = m.ff / (8 * W);   // 8 W output rows a block

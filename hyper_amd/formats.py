@@ -136,6 +136,7 @@ class Workload:
     zipf: Optional[float] = None     # routing skew (logit bias log p_zipf + Gumbel noise), None: plain router
     shared: Optional[tuple] = None   # shared expert types (tg, td), same shape as the routed experts
     norm_lognormal: Optional[float] = None   # per-token L2 norms log-normal(0, sigma)
+    chunk: Optional[int] = None      # rows per layer call (a long prompt in chunks, routing drawn per chunk); None: all rows
     notes: str = ""
     extra: dict = field(default_factory=dict)
 
@@ -160,6 +161,10 @@ WORKLOADS = {
     "q5k_q6k_chunk2048": Workload("q5k_q6k_chunk2048", 2048, 512, 10, 512, GType.Q5_K, GType.Q6_K, 2048, zipf=1.1,
                                   shared=(GType.Q5_K, GType.Q6_K), norm_lognormal=0.5,
                                   notes="one 2048-token chunk of a 16384-token prompt, 512 experts, top-10, ff 512"),
+    "q5k_q6k_prompt16384": Workload("q5k_q6k_prompt16384", 2048, 512, 10, 512, GType.Q5_K, GType.Q6_K, 16384, zipf=1.1,
+                                    shared=(GType.Q5_K, GType.Q6_K), norm_lognormal=0.5, chunk=2048,
+                                    notes="the whole 16384-token prompt as 8 chunks of 2048, Zipf routing drawn per chunk, "
+                                          "each chunk's output added into the residual rows"),
 }
 
 

@@ -201,6 +201,7 @@ GEMM_CASES = [
     (GType.Q4_K, GType.Q6_K, 2048, 768, 8, 40),
     (GType.Q4_K, GType.Q4_K, 2048, 768, 8, 70),
     (GType.Q5_K, GType.Q6_K, 2048, 512, 10, 33),
+    (GType.Q5_K, GType.Q6_K, 2048, 768, 10, 600),   # enough items for the 16-wave Q5_K gate/up (6 row blocks)
     (GType.IQ4_XS, GType.IQ4_XS, 4096, 1536, 8, 4),
     (GType.IQ2_XS, GType.IQ2_XS, 7168, 2048, 6, 8),
     (GType.IQ4_NL, GType.IQ4_NL, 4096, 1536, 8, 4),

@@ -33,9 +33,12 @@ def test_workload_full_size(cuda, name):
     g.manual_seed(seed + 2)
     W_r = torch.randn(w.E, w.d, generator=g, device=cuda) * 0.02
     x = activations(w.rows, w.d, g, cuda, lognormal=w.norm_lognormal)
-    bias = zipf_logit_bias(w.rows, w.E, w.zipf, g, cuda) if w.zipf else None
+    bias = zipf_logit_bias(w.rows, w.E, w.zipf, g, cuda) if w.zipf and not w.chunk else None
     dev = moe.MoeDev(L, torch.arange(w.E, dtype=torch.int32, device=cuda))
     sdev = moe.MoeDev(S, torch.zeros(1, dtype=torch.int32, device=cuda)) if S is not None else None
+    if w.chunk:
+        _prompt_in_chunks(w, L, S, W_r, x, g, dev, sdev, seed)
+        return
     r = moe.MoeLayerRunner(dev, W_r, w.k, max_rows=w.rows, shared=sdev)
     out = (r.decode(x, bias=bias) if w.rows <= 8 else r.prefill(x, bias=bias)).clone()
     torch.cuda.synchronize()
@@ -56,3 +59,37 @@ def test_workload_full_size(cuda, name):
     got = out.cpu().numpy()[tok]
     assert_bits_equal(got, ref, "out")
     assert rel_l2(got, ref) <= 2e-3
+
+
+def _prompt_in_chunks(w, L, S, W_r, x, g, dev, sdev, seed):
+    """A long prompt through one runner of chunk rows: each chunk draws its own routing skew and adds its output into
+    its rows of a random residual.  Checked: every chunk's logits and routing on its sampled tokens, and the residual
+    rows of all sampled tokens (the oracle's layer output plus one fp32 add to the residual they started from)."""
+    C, nch = w.chunk, w.rows // w.chunk
+    r = moe.MoeLayerRunner(dev, W_r, w.k, max_rows=C, shared=sdev)
+    resid = torch.randn(w.rows, w.d, generator=g, device=x.device)
+    resid0 = resid.cpu().numpy()
+    rng = np.random.default_rng(seed)
+    tok = np.sort(rng.choice(w.rows, SAMPLE, replace=False))
+    Wh, xs_all = W_r.cpu().numpy(), x.cpu().numpy()
+    ids_all, wts_all = np.zeros((w.rows, w.k), np.int32), np.zeros((w.rows, w.k), np.float32)
+    for j in range(nch):
+        b = zipf_logit_bias(C, w.E, w.zipf, g, x.device)
+        r.prefill(x[j * C:(j + 1) * C], bias=b, resid=resid[j * C:(j + 1) * C])
+        torch.cuda.synchronize()
+        t = tok[(tok >= j * C) & (tok < (j + 1) * C)] - j * C
+        if t.size == 0:
+            continue
+        logits = (orc.gemv_f32(Wh, xs_all[j * C + t]) + b.cpu().numpy()[t]).astype(np.float32)
+        assert_bits_equal(r.logits.cpu().numpy()[t], logits, f"chunk {j} logits")
+        ids, wts, _ = orc.route(logits, w.E, w.k)
+        assert_bits_equal(r.ids.cpu().numpy().reshape(-1, w.k)[t], ids, f"chunk {j} ids")
+        assert_bits_equal(r.wts.cpu().numpy().reshape(-1, w.k)[t], wts, f"chunk {j} wts")
+        ids_all[j * C + t], wts_all[j * C + t] = ids, wts
+    ids, wts = ids_all[tok], wts_all[tok]
+    used = np.unique(ids)
+    ids_sub = np.searchsorted(used, ids).astype(np.int32)
+    ref = orc.moe_layer(_sub_layer(L, used), xs_all[tok], ids_sub, wts, shared=orc.Layer.from_expert_layer(S) if S is not None else None)
+    got = resid.cpu().numpy()[tok]
+    assert_bits_equal(got, (resid0[tok] + ref).astype(np.float32), "residual rows")
+    assert rel_l2(got - resid0[tok], ref) <= 2e-3
