@@ -73,6 +73,8 @@ SIGNATURES = {
     "hy_gguf_tensor": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(hy_gguf_tensor_info)]),
     "hy_gguf_expert_tensors": (_I, [_P, _I, _I, ctypes.POINTER(hy_expert_tensors)]),
     "hy_gemv_f32": (_I, [_P, _I, _I, _P, _I, _P, _I, _I, _P, _I, _P]),
+    "hy_gemv_bf16w": (_I, [_P, _I, _I, _P, _I, _P, _I, _I, _P, _I, _P]),
+    "hy_bf16_to_f32": (_I, [_P, ctypes.c_size_t, _P, _P]),
     "hy_moe_route": (_I, [_P, _I, _I, _I, _P, _P, _P, _I, _P]),
     "hy_moe_route_sig": (_I, [_P, _I, _P, _I, _I, _F, _P, _P, _P, _I, _P]),
     "hy_moe_route_sqrtsp": (_I, [_P, _I, _P, _I, _I, _F, _P, _P, _I, _P]),
@@ -87,6 +89,7 @@ SIGNATURES = {
     "hy_moe_down_reduce": (_I, [_DEV, _P, _P, _P, _I, _P, _P, _P, _I, _P]),
     "hy_moe_down_reduce_residual": (_I, [_DEV, _P, _P, _P, _I, _P, _P, _P, _I, _P]),
     "hy_moe_router_q8": (_I, [_P, _I, _I, _P, _I, _P, _I, _P, _I, _I, _P, _I, _P]),
+    "hy_moe_router_q8_bf16w": (_I, [_P, _I, _I, _P, _I, _P, _I, _P, _I, _I, _P, _I, _P]),
     "hy_moe_route_gate_up": (_I, [_DEV, _P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
     "hy_moe_route_gate_up_q8": (_I, [_DEV, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P]),
     "hy_moe_shared_gate_up": (_I, [_DEV, _P, _P, _I, _P]),

@@ -61,6 +61,28 @@ int check_dev_decode(const hy_moe_dev *m, const hy_moe_dev *shared, const char *
     return rc;
 }
 
+// the router GEMV entries' checks, for fp32 and bf16 weights
+template <typename WT>
+static int gemv_checked(const WT *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bias_stride,
+                        hipStream_t s, const char *what) {
+    if (!W || !x || !y || rows < 0 || nt < 0) { set_error("%s: bad argument", what); return HY_EINVAL; }
+    if (kdim <= 0 || kdim % 4 || xs % 4 || !aligned16(W) || !aligned16(x)) { set_error("%s: kdim/xs must be multiples of 4, W/x 16-byte aligned", what); return HY_EBAD_SHAPE; }
+    if (rows == 0 || nt == 0) return HY_OK;
+    return launch_gemv_f32(W, rows, kdim, x, xs, y, ys, nt, bias, bias_stride, s);
+}
+template <typename WT>
+static int router_q8_checked(const WT *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride, float *logits,
+                             int ls, int vtype, void *xq, int nt, hipStream_t s, const char *what) {
+    if (!W_r || !x || !logits || !xq || rows <= 0 || nt < 0) { set_error("%s: bad argument", what); return HY_EINVAL; }
+    if (kdim <= 0 || xs % 4 || !aligned16(W_r) || !aligned16(x)) { set_error("%s: W_r / x rows must be 16-byte aligned", what); return HY_EBAD_SHAPE; }
+    if (vtype == Q8_K) {
+        if (kdim % 256 || ((uintptr_t) xq & 3)) { set_error("%s: Q8_K needs kdim %% 256 == 0", what); return HY_EBAD_SHAPE; }
+    } else if (vtype == Q8_0) {
+        if (kdim % 32 || ((uintptr_t) xq & 1)) { set_error("%s: Q8_0 needs kdim %% 32 == 0", what); return HY_EBAD_SHAPE; }
+    } else { set_error("%s: vtype %d", what, vtype); return HY_EUNSUPPORTED_TYPE; }
+    if (rows > ls) { set_error("%s: %d rows do not fit the logit stride %d", what, rows, ls); return HY_EBAD_SHAPE; }
+    return launch_router_q8(W_r, rows, kdim, x, xs, bias, bias_stride, logits, ls, vtype, xq, nt, s);
+}
 } // namespace hy
 
 using namespace hy;
@@ -147,10 +169,16 @@ int hy_free_experts(hy_moe_dev *m) {
 
 int hy_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bias_stride,
                 hipStream_t s) {
-    if (!W || !x || !y || rows < 0 || nt < 0) { set_error("hy_gemv_f32: bad argument"); return HY_EINVAL; }
-    if (kdim <= 0 || kdim % 4 || xs % 4 || !aligned16(W) || !aligned16(x)) { set_error("hy_gemv_f32: kdim/xs must be multiples of 4, W/x 16-byte aligned"); return HY_EBAD_SHAPE; }
-    if (rows == 0 || nt == 0) return HY_OK;
-    return launch_gemv_f32(W, rows, kdim, x, xs, y, ys, nt, bias, bias_stride, s);
+    return gemv_checked(W, rows, kdim, x, xs, y, ys, nt, bias, bias_stride, s, "hy_gemv_f32");
+}
+int hy_gemv_bf16w(const uint16_t *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bias_stride,
+                  hipStream_t s) {
+    return gemv_checked(W, rows, kdim, x, xs, y, ys, nt, bias, bias_stride, s, "hy_gemv_bf16w");
+}
+int hy_bf16_to_f32(const uint16_t *W, size_t n, float *out, hipStream_t s) {
+    if ((!W || !out) && n) { set_error("hy_bf16_to_f32: bad argument"); return HY_EINVAL; }
+    if (((uintptr_t) W & 7) || !aligned16(out)) { set_error("hy_bf16_to_f32: W must be 8-byte and out 16-byte aligned"); return HY_EBAD_SHAPE; }
+    return launch_bf16_to_f32(W, n, out, s);
 }
 
 int hy_moe_route(const float *logits, int ls, int n_expert, int k, int32_t *ids, float *wts, float *sg, int nt, hipStream_t s) {
@@ -270,15 +298,11 @@ int hy_moe_down_reduce_residual(const hy_moe_dev *m, const float *h, const int32
 
 int hy_moe_router_q8(const float *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride, float *logits,
                      int ls, int vtype, void *xq, int nt, hipStream_t s) {
-    if (!W_r || !x || !logits || !xq || rows <= 0 || nt < 0) { set_error("hy_moe_router_q8: bad argument"); return HY_EINVAL; }
-    if (kdim <= 0 || xs % 4 || !aligned16(W_r) || !aligned16(x)) { set_error("hy_moe_router_q8: W_r / x rows must be 16-byte aligned"); return HY_EBAD_SHAPE; }
-    if (vtype == Q8_K) {
-        if (kdim % 256 || ((uintptr_t) xq & 3)) { set_error("hy_moe_router_q8: Q8_K needs kdim %% 256 == 0"); return HY_EBAD_SHAPE; }
-    } else if (vtype == Q8_0) {
-        if (kdim % 32 || ((uintptr_t) xq & 1)) { set_error("hy_moe_router_q8: Q8_0 needs kdim %% 32 == 0"); return HY_EBAD_SHAPE; }
-    } else { set_error("hy_moe_router_q8: vtype %d", vtype); return HY_EUNSUPPORTED_TYPE; }
-    if (rows > ls) { set_error("hy_moe_router_q8: %d rows do not fit the logit stride %d", rows, ls); return HY_EBAD_SHAPE; }
-    return launch_router_q8(W_r, rows, kdim, x, xs, bias, bias_stride, logits, ls, vtype, xq, nt, s);
+    return router_q8_checked(W_r, rows, kdim, x, xs, bias, bias_stride, logits, ls, vtype, xq, nt, s, "hy_moe_router_q8");
+}
+int hy_moe_router_q8_bf16w(const uint16_t *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride, float *logits,
+                           int ls, int vtype, void *xq, int nt, hipStream_t s) {
+    return router_q8_checked(W_r, rows, kdim, x, xs, bias, bias_stride, logits, ls, vtype, xq, nt, s, "hy_moe_router_q8_bf16w");
 }
 
 int hy_moe_route_gate_up(const hy_moe_dev *m, const float *logits, int ls, int n_expert, int k, const void *xq, int32_t *ids, float *wts,

@@ -35,6 +35,14 @@ __host__ __device__ constexpr int vec_dot_type(int t) { return t == IQ4_NL ? Q8_
 
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+// four router weights at p as fp32: fp32 rows as they are; bf16 rows (uint16 bit patterns, p 8-byte aligned) widened,
+// which is exact (a bf16 value is the fp32 value with the low 16 bits zero), so both give the same products and sums
+__device__ __forceinline__ float4 ld_w4(const float *p) { return *(const float4 *) p; }
+__device__ __forceinline__ float4 ld_w4(const uint16_t *p) {
+    const uint2 v = *(const uint2 *) p;
+    return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+                       __uint_as_float(v.y & 0xffff0000u));
+}
 
 // exp(x) of the contract: x = n ln2 + r (ln2 = 0.693359375 - 2.12194440e-4, the first part exact in
 // 9 bits), exp(r) by the Cephes expf polynomial (S. L. Moshier), 2^n applied as two exact scalings.

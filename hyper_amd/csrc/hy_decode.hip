@@ -56,8 +56,8 @@ struct Cursor {
 
 // ---------------------------------------------------------------- k_router
 
-template <int VT>
-__global__ __launch_bounds__(256) void k_router_q8(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+template <int VT, typename WT>
+__global__ __launch_bounds__(256) void k_router_q8(const WT *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
                                                    const float *__restrict__ bias, int bs, float *__restrict__ logits, int ls,
                                                    uint8_t *__restrict__ xq, int nt) {
     HY_STAMP_VARS(3);
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void k_router_q8(const float *__restrict__ W, 
     // logits of row r for every token: lane L sums elements 256 i + 4 L + j with fmaf, then the butterfly.  The
     // row's loads go out RB float4 at a time (one memory round trip per 256 RB values), then the fma chains.
     constexpr int RB = 8;
-    const float *wr = W + (size_t) r * kdim;
+    const WT *wr = W + (size_t) r * kdim;
     const float bv = bias && lane < nt ? bias[(size_t) lane * bs + r] : 0.0f;   // token lane's bias, added after the butterfly
     float acc[DEC_ROUTE_NT];
 #pragma unroll
@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void k_router_q8(const float *__restrict__ W, 
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
             const int e = e0 + 256 * i + 4 * lane;
-            w[i] = e < kdim ? *(const float4 *) (wr + e) : make_float4(0, 0, 0, 0);
+            w[i] = e < kdim ? ld_w4(wr + e) : make_float4(0, 0, 0, 0);
             xv[i] = e < kdim ? *(const float4 *) (x + e) : make_float4(0, 0, 0, 0);
         }
 #pragma unroll
@@ -582,17 +582,26 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE;   \
     }
 
-int launch_router_q8(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
-                     int vtype, void *xq, int nt, hipStream_t s) {
+template <typename WT>
+static int router_q8_any(const WT *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
+                         int vtype, void *xq, int nt, hipStream_t s) {
     if (nt == 0) return HY_OK;
     if (nt > DEC_ROUTE_NT) return launch_router_pre(W, rows, kdim, x, xs, bias, bs, logits, ls, vtype, xq, nt, s);   // batched rows
     const int qwaves = vtype == Q8_K ? nt * (kdim / 256) : nt * ((kdim / 32 + 1) / 2);
     const int blocks = (rows + qwaves + 3) / 4;
     if (vtype == Q8_K)
-        hipLaunchKernelGGL((k_router_q8<Q8_K>), dim3(blocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, (uint8_t *) xq, nt);
+        hipLaunchKernelGGL((k_router_q8<Q8_K, WT>), dim3(blocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, (uint8_t *) xq, nt);
     else
-        hipLaunchKernelGGL((k_router_q8<Q8_0>), dim3(blocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, (uint8_t *) xq, nt);
+        hipLaunchKernelGGL((k_router_q8<Q8_0, WT>), dim3(blocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, (uint8_t *) xq, nt);
     return check_launch("hy_moe_router_q8");
+}
+int launch_router_q8(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
+                     int vtype, void *xq, int nt, hipStream_t s) {
+    return router_q8_any(W, rows, kdim, x, xs, bias, bs, logits, ls, vtype, xq, nt, s);
+}
+int launch_router_q8(const uint16_t *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
+                     int vtype, void *xq, int nt, hipStream_t s) {
+    return router_q8_any(W, rows, kdim, x, xs, bias, bs, logits, ls, vtype, xq, nt, s);
 }
 
 int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int ne, int k, const void *xq, int *ids, float *wts, float *sg,

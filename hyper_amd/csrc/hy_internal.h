@@ -11,14 +11,20 @@ int check_launch(const char *what);
 // checks of the layer descriptors a whole decode step reads (gate/up and down of the layer and of the shared expert)
 int check_dev_decode(const hy_moe_dev *m, const hy_moe_dev *shared, const char *what);
 
+// router GEMVs: W fp32, or bf16 bit patterns (uint16) widened on load -- the same products and sums
 int launch_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bs,
                     hipStream_t s);
+int launch_gemv_f32(const uint16_t *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bs,
+                    hipStream_t s);
+int launch_bf16_to_f32(const uint16_t *W, size_t n, float *out, hipStream_t s);
 int launch_route(const float *logits, int ls, int ne, int k, int *ids, float *wts, float *sg, int nt, hipStream_t s);
 int launch_route_bias(int mode, const float *logits, int ls, const float *bias, int ne, int k, float scale, int *ids, float *wts,
                       float *sg, int nt, hipStream_t s);
 int launch_order(const int *slot, const int *ids, int P, int ne, int *order, int *order_n, int *egrp, hipStream_t s);
 int launch_q8(int vtype, const float *x, int xs, int n, int nt, void *q, hipStream_t s);
 int launch_router_pre(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
+                      int vtype, void *xq, int nt, hipStream_t s);
+int launch_router_pre(const uint16_t *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
                       int vtype, void *xq, int nt, hipStream_t s);
 int launch_gate_up(const hy_moe_dev &m, const float *x, int xs, const int *ids, int k, float *h, int nt, hipStream_t s, const int *order,
                    const int *order_n);
@@ -33,6 +39,8 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
 int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int *order, const int *order_n, const int *egrp, int max_active,
                      const float *wts, float *y, hipStream_t s);
 int launch_router_q8(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
+                     int vtype, void *xq, int nt, hipStream_t s);
+int launch_router_q8(const uint16_t *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
                      int vtype, void *xq, int nt, hipStream_t s);
 // hq: also write the Q8_0 rows of h (down types whose partner is Q8_0); HY_EUNSUPPORTED_TYPE where that does not apply
 int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int ne, int k, const void *xq, int *ids, float *wts, float *sg,

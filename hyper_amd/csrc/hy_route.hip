@@ -5,13 +5,14 @@
 namespace hy {
 
 // ---------------------------------------------------------------- router logits (A1)
-// y[t][r] = W[r] . x[t] (+ bias[t][r]): src/kernels4.cu:163-180 (gemv_f32).  Summation order of the contract:
+// y[t][r] = W[r] . x[t] (+ bias[t][r]): src/kernels4.cu:163-180 (gemv_f32), and with bf16 weights (WT = uint16_t,
+// widened on load) src/kernels4.cu:181-197 (gemv_bf16w): the same products and sums.  Summation order of the contract:
 // lane L of a wave accumulates elements 256 i + 4 L + j (j = 0..3) with fmaf in index order, then the
 // 64 partial sums meet in an xor butterfly (1, 2, ..., 32).  A wave computes RW rows x TW tokens; its loads for
 // step i + 1 are in flight while step i's fmas run (two register sets, a uniform trip count: past the row's end a
 // lane re-reads its first element and skips the fmas).
-template <int RW, int TW>
-__device__ __forceinline__ void gemv_tile(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+template <int RW, int TW, typename WT>
+__device__ __forceinline__ void gemv_tile(const WT *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
                                           float *__restrict__ y, int ys, int nt, const float *__restrict__ bias, int bs, int r0, int t0) {
     const int lane = threadIdx.x & 63;
     if (r0 >= rows) return;
@@ -20,7 +21,8 @@ __device__ __forceinline__ void gemv_tile(const float *__restrict__ W, int rows,
     for (int a = 0; a < RW; ++a)
 #pragma unroll
         for (int b = 0; b < TW; ++b) acc[a][b] = 0.0f;
-    const float *wr[RW], *xr[TW];
+    const WT *wr[RW];
+    const float *xr[TW];
 #pragma unroll
     for (int a = 0; a < RW; ++a) wr[a] = W + (size_t) (r0 + a < rows ? r0 + a : r0) * kdim;
 #pragma unroll
@@ -34,7 +36,7 @@ __device__ __forceinline__ void gemv_tile(const float *__restrict__ W, int rows,
     auto ld = [&](int i, float4 (&wd)[RW], float4 (&xd)[TW]) {
         const int e = 256 * i + 4 * lane < kdim ? 256 * i + 4 * lane : 4 * lane < kdim ? 4 * lane : 0;
 #pragma unroll
-        for (int a = 0; a < RW; ++a) wd[a] = *(const float4 *) (wr[a] + e);
+        for (int a = 0; a < RW; ++a) wd[a] = ld_w4(wr[a] + e);
 #pragma unroll
         for (int b = 0; b < TW; ++b) xd[b] = *(const float4 *) (xr[b] + e);
     };
@@ -83,25 +85,50 @@ __device__ __forceinline__ void gemv_tile_of(int bid, int gx, int gy, int &bx, i
     }
 }
 
-template <int RW, int TW>
-__global__ __launch_bounds__(256) void k_gemv_f32(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
-                                                  float *__restrict__ y, int ys, int nt, const float *__restrict__ bias, int bs, int gx,
-                                                  int gy) {
+template <int RW, int TW, typename WT>
+__global__ __launch_bounds__(256) void k_gemv(const WT *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+                                              float *__restrict__ y, int ys, int nt, const float *__restrict__ bias, int bs, int gx,
+                                              int gy) {
     int bx, by;
     gemv_tile_of(blockIdx.x, gx, gy, bx, by);
     gemv_tile<RW, TW>(W, rows, kdim, x, xs, y, ys, nt, bias, bs, (bx * 4 + (threadIdx.x >> 6)) * RW, by * TW);
 }
 
-int launch_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bs,
-                    hipStream_t s) {
+template <typename WT>
+static int gemv_any(const WT *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bs,
+                    hipStream_t s, const char *what) {
     if (nt <= 4) {
         const int gx = (rows + 3) / 4, gy = nt;
-        hipLaunchKernelGGL((k_gemv_f32<1, 1>), dim3(gx * gy), dim3(256), 0, s, W, rows, kdim, x, xs, y, ys, nt, bias, bs, gx, gy);
+        hipLaunchKernelGGL((k_gemv<1, 1, WT>), dim3(gx * gy), dim3(256), 0, s, W, rows, kdim, x, xs, y, ys, nt, bias, bs, gx, gy);
     } else {
         const int gx = (rows + 15) / 16, gy = (nt + 7) / 8;
-        hipLaunchKernelGGL((k_gemv_f32<4, 8>), dim3(gx * gy), dim3(256), 0, s, W, rows, kdim, x, xs, y, ys, nt, bias, bs, gx, gy);
+        hipLaunchKernelGGL((k_gemv<4, 8, WT>), dim3(gx * gy), dim3(256), 0, s, W, rows, kdim, x, xs, y, ys, nt, bias, bs, gx, gy);
     }
-    return check_launch("hy_gemv_f32");
+    return check_launch(what);
+}
+int launch_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bs,
+                    hipStream_t s) {
+    return gemv_any(W, rows, kdim, x, xs, y, ys, nt, bias, bs, s, "hy_gemv_f32");
+}
+int launch_gemv_f32(const uint16_t *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt, const float *bias, int bs,
+                    hipStream_t s) {
+    return gemv_any(W, rows, kdim, x, xs, y, ys, nt, bias, bs, s, "hy_gemv_bf16w");
+}
+
+// bf16 bit patterns -> fp32 (exact), four a thread: src/kernels4.cu:198-201 (bf16_to_f32)
+__global__ __launch_bounds__(256) void k_bf16_to_f32(const uint16_t *__restrict__ W, size_t n, float *__restrict__ out) {
+    const size_t i = 4 * ((size_t) blockIdx.x * 256 + threadIdx.x);
+    if (i + 4 <= n) {
+        *(float4 *) (out + i) = ld_w4(W + i);
+    } else {
+        for (size_t j = i; j < n; ++j) out[j] = __uint_as_float((uint32_t) W[j] << 16);
+    }
+}
+int launch_bf16_to_f32(const uint16_t *W, size_t n, float *out, hipStream_t s) {
+    if (n == 0) return HY_OK;
+    const size_t blocks = (n + 1023) / 1024;
+    hipLaunchKernelGGL(k_bf16_to_f32, dim3((unsigned) blocks), dim3(256), 0, s, W, n, out);
+    return check_launch("hy_bf16_to_f32");
 }
 
 // The same contract for a block tile of 16 rows x 16 tokens (kdim a multiple of 256), 8 waves: each 256-value step
@@ -113,22 +140,30 @@ constexpr int GL_R = 16, GL_THREADS = 512;
 typedef float f4v __attribute__((ext_vector_type(4)));
 // GT tokens a block (16, or 8 when 16-token tiles would leave CUs with fewer than two blocks); the waves are 4 row
 // groups x 2 token groups whatever GT, and lane l always takes columns 4 l .. 4 l + 3 of each 256-column step
-template <int GT>
-__device__ __forceinline__ void gemv_block_lds(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+template <int GT, typename WT>
+__device__ __forceinline__ void gemv_block_lds(const WT *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
                                                float *__restrict__ y, int ys, int nt, const float *__restrict__ bias, int bs, int r0,
                                                int t0, f4v *st) {   // st: LDS, (GL_R + GT) rows of 64 float4
     constexpr int RW = 4, TW = GT / 2, NS = (GL_R + GT) * 64 / GL_THREADS;   // float4 staged by each thread per step
     static_assert((GL_R + GT) * 64 % GL_THREADS == 0, "whole float4 per thread");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr0 = r0 + RW * (wave & 3), wt0 = t0 + TW * (wave >> 2);   // this wave's rows and tokens
-    // the NS float4 this thread stages per step: tile row (tid + 512 k) / 64 (W rows, then x rows), column tid % 64
-    const float *src[NS];
+    // the NS float4 this thread stages per step: tile row (tid + 512 k) / 64 (W rows, then x rows), column tid % 64;
+    // the first NW are W rows
+    constexpr int NW = GL_R * 64 / GL_THREADS;
+    static_assert(NW * GL_THREADS == GL_R * 64 && NW < NS, "whole W rows per thread index");
+    const WT *wsrc[NW];
+    const float *xsrc[NS - NW];
 #pragma clang loop unroll(full)
     for (int k = 0; k < NS; ++k) {
         const int row = (tid >> 6) + (GL_THREADS / 64) * k;
-        if (row < GL_R) { const int r = r0 + row; src[k] = W + (size_t) (r < rows ? r : rows - 1) * kdim + 4 * lane; }
-        else { const int t = t0 + row - GL_R; src[k] = x + (size_t) (t < nt ? t : nt - 1) * xs + 4 * lane; }
+        if (k < NW) { const int r = r0 + row; wsrc[k] = W + (size_t) (r < rows ? r : rows - 1) * kdim + 4 * lane; }
+        else { const int t = t0 + row - GL_R; xsrc[k - NW] = x + (size_t) (t < nt ? t : nt - 1) * xs + 4 * lane; }
     }
+    auto ld = [&](int k, int e) -> f4v {
+        if (k < NW) { const float4 v = ld_w4(wsrc[k] + e); return f4v{v.x, v.y, v.z, v.w}; }
+        return *(const f4v *) (xsrc[k - NW] + e);
+    };
     float acc[RW][TW];
 #pragma unroll
     for (int a = 0; a < RW; ++a)
@@ -136,7 +171,7 @@ __device__ __forceinline__ void gemv_block_lds(const float *__restrict__ W, int 
         for (int b = 0; b < TW; ++b) acc[a][b] = 0.0f;
     f4v pre[NS];
 #pragma clang loop unroll(full)
-    for (int k = 0; k < NS; ++k) pre[k] = *(const f4v *) src[k];
+    for (int k = 0; k < NS; ++k) pre[k] = ld(k, 0);
     const int niter = kdim / 256;
     for (int i = 0; i < niter; ++i) {
         __syncthreads();   // the previous step's reads of st are done
@@ -145,7 +180,7 @@ __device__ __forceinline__ void gemv_block_lds(const float *__restrict__ W, int 
         __syncthreads();
         if (i + 1 < niter) {
 #pragma clang loop unroll(full)
-            for (int k = 0; k < NS; ++k) pre[k] = *(const f4v *) (src[k] + 256 * (i + 1));
+            for (int k = 0; k < NS; ++k) pre[k] = ld(k, 256 * (i + 1));
         }
         f4v xv[TW];
 #pragma unroll
@@ -206,8 +241,8 @@ __device__ __forceinline__ void gemv_block_lds(const float *__restrict__ W, int 
 // blocks of 16 rows per GT tokens through gemv_block_lds when kdim % 256 == 0 (GT 8 or 16), else per 8 tokens
 // through gemv_tile (GT 0)), the rest quantize x -- Q8_K: 32 blocks of 256 values per block, 16 lanes each; Q8_0: 8
 // pairs of 32-value blocks per block, a wave each.  The LDS variants fit two blocks a CU.
-template <int VT, int GT>
-__global__ __launch_bounds__(GL_THREADS, GT ? 4 : 2) void k_router_pre(const float *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+template <int VT, int GT, typename WT>
+__global__ __launch_bounds__(GL_THREADS, GT ? 4 : 2) void k_router_pre(const WT *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
                                                     const float *__restrict__ bias, int bs, float *__restrict__ y, int ys, int nt,
                                                     uint8_t *__restrict__ xq, int gx, int gemv_blocks) {
     __shared__ f4v st[GT ? (GL_R + GT) * 64 : 1];
@@ -233,8 +268,9 @@ __global__ __launch_bounds__(GL_THREADS, GT ? 4 : 2) void k_router_pre(const flo
     }
 }
 
-int launch_router_pre(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
-                      int vtype, void *xq, int nt, hipStream_t s) {
+template <typename WT>
+static int router_pre_any(const WT *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
+                          int vtype, void *xq, int nt, hipStream_t s) {
     if (nt == 0) return HY_OK;
     // kdim % 256 == 0: 16 x GT tiles through LDS (gemv_block_lds), GT = 16, or 8 when 16-token tiles number fewer
     // than two per CU (more blocks to hide the steps' barriers); else 16 rows x 8 tokens a block (gemv_tile, GT 0)
@@ -243,7 +279,7 @@ int launch_router_pre(const float *W, int rows, int kdim, const float *x, int xs
     const int gx = (rows + 15) / 16;
     const int gt = kdim % 256 != 0 ? 0 : gx * ((nt + 15) / 16) < 2 * cus ? 8 : 16;
     const int gemv_blocks = gx * ((nt + (gt ? gt : 8) - 1) / (gt ? gt : 8));
-#define HY_RP(VV, GG) hipLaunchKernelGGL((k_router_pre<VV, GG>), dim3(gemv_blocks + qblocks), dim3(GL_THREADS), 0, s, W, rows, kdim, x, xs, bias, bs, \
+#define HY_RP(VV, GG) hipLaunchKernelGGL((k_router_pre<VV, GG, WT>), dim3(gemv_blocks + qblocks), dim3(GL_THREADS), 0, s, W, rows, kdim, x, xs, bias, bs, \
                                          logits, ls, nt, (uint8_t *) xq, gx, gemv_blocks)
     if (vtype == Q8_K) {
         const int qblocks = (nt * (kdim / 256) + GL_THREADS / 16 - 1) / (GL_THREADS / 16);
@@ -254,6 +290,14 @@ int launch_router_pre(const float *W, int rows, int kdim, const float *x, int xs
     }
 #undef HY_RP
     return check_launch("hy_moe_router_q8");
+}
+int launch_router_pre(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
+                      int vtype, void *xq, int nt, hipStream_t s) {
+    return router_pre_any(W, rows, kdim, x, xs, bias, bs, logits, ls, vtype, xq, nt, s);
+}
+int launch_router_pre(const uint16_t *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
+                      int vtype, void *xq, int nt, hipStream_t s) {
+    return router_pre_any(W, rows, kdim, x, xs, bias, bs, logits, ls, vtype, xq, nt, s);
 }
 
 // ---------------------------------------------------------------- routing (A2)

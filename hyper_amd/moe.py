@@ -102,8 +102,24 @@ def free_experts(m: hy_moe_dev) -> None:
 
 # ------------------------------------------------------------------ the reference API
 
+def _bf16w(W) -> bool:
+    """router weights held as bf16 (torch.bfloat16, whose storage is the uint16 bit patterns the bf16 entries take)"""
+    return isinstance(W, torch.Tensor) and W.dtype == torch.bfloat16
+
+
 def gemv_f32(W, rows, kdim, x, xs, y, ys, nt, stream=None, bias=None, bias_stride=0):
+    """Router logits; a torch.bfloat16 W goes to gemv_bf16w (the same products and sums on the widened weights)."""
+    if _bf16w(W):
+        return gemv_bf16w(W, rows, kdim, x, xs, y, ys, nt, stream, bias, bias_stride)
     check(lib().hy_gemv_f32(_p(W), rows, kdim, _p(x), xs, _p(y), ys, nt, _p(bias), bias_stride, _s(stream)))
+
+
+def gemv_bf16w(W, rows, kdim, x, xs, y, ys, nt, stream=None, bias=None, bias_stride=0):
+    check(lib().hy_gemv_bf16w(_p(W), rows, kdim, _p(x), xs, _p(y), ys, nt, _p(bias), bias_stride, _s(stream)))
+
+
+def bf16_to_f32(W, n, out, stream=None):
+    check(lib().hy_bf16_to_f32(_p(W), n, _p(out), _s(stream)))
 
 
 def moe_route(logits, ls, n_expert, k, ids, wts, sg, nt, stream=None):
@@ -162,9 +178,9 @@ def moe_down_reduce_residual(m: MoeDev, h, ids, wts, k, shexp, sg, resid, nt, st
 
 
 def moe_router_q8(W_r, rows, kdim, x, xs, logits, ls, vtype, xq, nt, stream=None, bias=None, bias_stride=0):
-    """gemv_f32 and the Q8 rows of x in one launch."""
-    check(lib().hy_moe_router_q8(_p(W_r), rows, kdim, _p(x), xs, _p(bias), bias_stride, _p(logits), ls, int(vtype), _p(xq), nt,
-                                 _s(stream)))
+    """gemv_f32 and the Q8 rows of x in one launch (a torch.bfloat16 W_r: the bf16-weight router)."""
+    fn = lib().hy_moe_router_q8_bf16w if _bf16w(W_r) else lib().hy_moe_router_q8
+    check(fn(_p(W_r), rows, kdim, _p(x), xs, _p(bias), bias_stride, _p(logits), ls, int(vtype), _p(xq), nt, _s(stream)))
 
 
 def moe_route_gate_up(m: MoeDev, logits, ls, n_expert, k, xq, ids, wts, sg, h, nt, stream=None):
@@ -204,7 +220,8 @@ class MoeLayerRunner:
 
     decode(x): rows <= decode_rows use gate/up GEMV -> fused down+combine (src/engine4.cu:880-888);
     prefill(x): bucketing + grouped int8-MFMA GEMMs (src/engine4.cu:851-854, :887).
-    The router is fp32 W_r [E, d] (src/engine4.cu:807); `bias` adds per-token logits (skewed routing).
+    The router is W_r [E, d], fp32 (src/engine4.cu:807) or bf16 (the router16 path, src/engine4.cu:808: the same
+    logits as the widened fp32 matrix, half the bytes); `bias` adds per-token logits (skewed routing).
     `router` picks the routing on the logits: "softmax" (moe_route, src/kernels4.cu:297-344), or, with `router_bias`
     (E floats, selection only) and `router_scale`: "sigmoid" (moe_route_sig, src/kernels5.cu:1090-1122; sg = 1) or
     "sqrt_softplus" (route7, src/kernels7.cu:816-865).
@@ -219,6 +236,8 @@ class MoeLayerRunner:
             raise ValueError(f"the {router} router takes router_bias and no shared-gate logit")
         self.router, self.router_bias, self.router_scale = router, router_bias, float(router_scale)
         L = dev.layer
+        if W_r.dtype not in (torch.float32, torch.bfloat16) or W_r.dim() != 2 or W_r.shape[1] != L.n or not W_r.is_contiguous():
+            raise ValueError(f"W_r must be a contiguous fp32 or bf16 [rows, {L.n}] matrix, got {W_r.dtype} {tuple(W_r.shape)}")
         self.dev, self.W_r, self.k, self.E, self.d, self.ff = dev, W_r, k, dev.slot.numel(), L.n, L.ff
         self.shared = shared
         self.sg_logit = sg_logit

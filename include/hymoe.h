@@ -122,6 +122,14 @@ int hy_free_experts(hy_moe_dev *m);
    (replaces gemv_f32, src/kernels4.cuh:35 / src/kernels4.cu:1910-1913).  kdim % 4 == 0, xs % 4 == 0. */
 int hy_gemv_f32(const float *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt,
                 const float *bias, int bias_stride, hipStream_t s);
+/* The same with bf16 router weights (uint16 bit patterns holding the fp32 values' high halves), widened on load:
+   identical products and sums to hy_gemv_f32 on the widened matrix, half the bytes (replaces gemv_bf16w,
+   src/kernels4.cuh:38 / src/kernels4.cu:1914-1917).  W 16-byte aligned, kdim % 4 == 0, xs % 4 == 0. */
+int hy_gemv_bf16w(const uint16_t *W, int rows, int kdim, const float *x, int xs, float *y, int ys, int nt,
+                  const float *bias, int bias_stride, hipStream_t s);
+/* out[i] = the fp32 value of bf16 W[i], i < n (exact; replaces bf16_to_f32, src/kernels4.cuh:39 /
+   src/kernels4.cu:1918-1920).  W 8-byte and out 16-byte aligned. */
+int hy_bf16_to_f32(const uint16_t *W, size_t n, float *out, hipStream_t s);
 
 /* Softmax over logits[t][0..n_expert), top-k (ties to the lower index), weights renormalised over the selected;
    sg[t] = sigmoid(logits[t][n_expert]) when sg is not NULL (needs ls > n_expert)
@@ -194,9 +202,14 @@ int hy_moe_down_reduce_residual(const hy_moe_dev *m, const float *h, const int32
 
 /* Router logits and the Q8 rows of x in one launch: logits as hy_gemv_f32 (rows of W_r, stride ls >= rows) and xq as
    hy_q8_quantize(vtype, x, xs, kdim, nt) -- fuses gemv_f32 (src/kernels4.cu:1910-1913) with the activation
-   quantization of the expert kernels.  nt > 8 runs the two steps as separate launches. */
+   quantization of the expert kernels.  Up to 8 tokens a wave per logit row; more, the batched router (16 rows by 16
+   or 8 tokens a block through LDS), still one launch with the quantization. */
 int hy_moe_router_q8(const float *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride, float *logits,
                      int ls, int vtype, void *xq, int nt, hipStream_t s);
+/* The same with bf16 router weights, widened on load as in hy_gemv_bf16w (the router16 path of src/engine4.cu:808:
+   gemv_bf16w, then the expert kernels' quantization of x): logits identical to hy_moe_router_q8 on the widened W_r. */
+int hy_moe_router_q8_bf16w(const uint16_t *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride,
+                           float *logits, int ls, int vtype, void *xq, int nt, hipStream_t s);
 
 /* Routing + decode gate/up in one launch: each token's softmax / top-k / weights / sg exactly as hy_moe_route
    (written to ids, wts, sg), then h[t*k + j] as hy_moe_gate_up, from the Q8 rows xq (partner type of the gate

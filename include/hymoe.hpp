@@ -99,6 +99,13 @@ inline void gemv_f32(const float *W, int rows, int k, const float *x, int xs, fl
                      const float *bias = nullptr, int bias_stride = 0) {
     check(hy_gemv_f32(W, rows, k, x, xs, y, ys, nt, bias, bias_stride, s));
 }
+// src/kernels4.cuh:38 (bf16 router weights; the reference's ys is the output stride here too)
+inline void gemv_bf16w(const uint16_t *W, int rows, int k, const float *x, int xs, float *y, int ys, int nt, hipStream_t s,
+                       const float *bias = nullptr, int bias_stride = 0) {
+    check(hy_gemv_bf16w(W, rows, k, x, xs, y, ys, nt, bias, bias_stride, s));
+}
+// src/kernels4.cuh:39
+inline void bf16_to_f32(const uint16_t *W, size_t n, float *out, hipStream_t s) { check(hy_bf16_to_f32(W, n, out, s)); }
 // src/kernels4.cuh:48
 inline void moe_route(const float *logits, int ls, int n_expert, int k, int *ids, float *wts, float *sg, int nt, hipStream_t s) {
     check(hy_moe_route(logits, ls, n_expert, k, ids, wts, sg, nt, s));
@@ -162,6 +169,11 @@ inline void moe_down_reduce(const MoeDev &m, const float *h, const int *ids, con
 inline void moe_router_q8(const float *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride, float *logits,
                           int ls, int vtype, void *xq, int nt, hipStream_t s) {
     check(hy_moe_router_q8(W_r, rows, kdim, x, xs, bias, bias_stride, logits, ls, vtype, xq, nt, s));
+}
+// the same with bf16 router weights (gemv_bf16w, src/kernels4.cuh:38, + the activation quantizer)
+inline void moe_router_q8(const uint16_t *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride, float *logits,
+                          int ls, int vtype, void *xq, int nt, hipStream_t s) {
+    check(hy_moe_router_q8_bf16w(W_r, rows, kdim, x, xs, bias, bias_stride, logits, ls, vtype, xq, nt, s));
 }
 // decode: moe_route and moe_gate_up (on the Q8 rows) in one launch
 inline void moe_route_gate_up(const MoeDev &m, const float *logits, int ls, int n_expert, int k, const void *xq, int *ids, float *wts,
