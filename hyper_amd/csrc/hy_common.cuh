@@ -193,6 +193,31 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// Direct global -> LDS loads (global_load_lds_dword / _dwordx4) from inline asm: a wave-uniform base address in SGPRs,
+// a per-lane 32-bit byte offset, and the LDS address of the instruction's first lane in M0 (saved and restored around
+// it); lane l's bytes land at M0 + 4 l (dword) or M0 + 16 l (dwordx4).  The compiler does not count them: a kernel that
+// issues them waits for them itself (wait_vm; vector memory loads of a wave complete in issue order).
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t) (uintptr_t) p; }
+// The same with a wave-uniform base address in SGPRs and a per-lane 32-bit byte offset (no 64-bit address math per lane)
+__device__ __forceinline__ uint64_t sgpr_ptr(const void *p) {   // p is uniform; this makes the compiler keep it in SGPRs
+    const uint64_t v = (uint64_t) p;
+    // readfirstlane returns int: each half goes through uint32_t so that the low half does not sign-extend
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (v >> 32));
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) v);
+    return ((uint64_t) hi << 32) | lo;
+}
+__device__ __forceinline__ void dma_s32(const void *base, uint32_t voff, uint32_t lds) {
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(voff), "s"(sgpr_ptr(base)), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+__device__ __forceinline__ void dma_s128(const void *base, uint32_t voff, uint32_t lds) {
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(voff), "s"(sgpr_ptr(base)), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
 template <int W> __device__ __forceinline__ int group_isum(int v) {   // sum over aligned groups of W lanes
 #pragma unroll
     for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);

@@ -249,7 +249,6 @@ template <class R> __device__ __forceinline__ void touch_regs(const R &r) {
 // stores as possibly completing out of order and would then wait for all of them at every step.)  Vector memory
 // operations of a wave complete in issue order, so waiting for a step's weight registers also covers every DMA
 // issued before them.  M0 holds the LDS address of a DMA; it is saved and restored around it.
-__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t) (uintptr_t) p; }
 __device__ __forceinline__ void dma_lds_b32(const void *g, uint32_t lds) {
     uint32_t keep;
     asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
@@ -259,24 +258,6 @@ __device__ __forceinline__ void dma_lds_b128(const void *g, uint32_t lds) {
     uint32_t keep;
     asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
                  : "=&s"(keep) : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
-}
-// The same with a wave-uniform base address in SGPRs and a per-lane 32-bit byte offset (no 64-bit address math per lane)
-__device__ __forceinline__ uint64_t sgpr_ptr(const void *p) {   // p is uniform; this makes the compiler keep it in SGPRs
-    const uint64_t v = (uint64_t) p;
-    // readfirstlane returns int: each half goes through uint32_t so that the low half does not sign-extend
-    const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (v >> 32));
-    const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) v);
-    return ((uint64_t) hi << 32) | lo;
-}
-__device__ __forceinline__ void dma_s32(const void *base, uint32_t voff, uint32_t lds) {
-    uint32_t keep;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
-                 : "=&s"(keep) : "v"(voff), "s"(sgpr_ptr(base)), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
-}
-__device__ __forceinline__ void dma_s128(const void *base, uint32_t voff, uint32_t lds) {
-    uint32_t keep;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
-                 : "=&s"(keep) : "v"(voff), "s"(sgpr_ptr(base)), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
 __device__ __forceinline__ void store_f32(float *g, float v) { asm volatile("global_store_dword %0, %1, off" ::"v"(g), "v"(v) : "memory"); }
 
@@ -346,8 +327,14 @@ __device__ __forceinline__ int lane_id_here() {
     asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
     return l;
 }
-template <int NT, int T0>
+template <int NT, int T0, bool FIRST>
 __device__ __forceinline__ void step_q4k(const uint8_t *wl0, const int8_t *as, const float *yd, float (&acc)[GM_TILES][4]) {
+    // the tiles past NT hold nothing this item reads (a tile count is fixed for an item, and an item's first span
+    // writes its tiles without reading them): marking them redefined frees their registers in this step
+#pragma unroll
+    for (int t = T0 + NT; t < GM_TILES; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) asm volatile("" : "=v"(acc[t][v]));
     const int lid = lane_id_here(), q = lid >> 4, rr = lid & 15;
     const uint8_t *wl = wl0 + rr * block_bytes(Q4_K);
     const uint4 hd = *(const uint4 *) wl;   // d | dmin, scales[12]
@@ -387,7 +374,7 @@ __device__ __forceinline__ void step_q4k(const uint8_t *wl0, const int8_t *as, c
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int si = (d1[t][v] << 3) + d2[t][v];
-            acc[T0 + t][v] = __builtin_fmaf(yd[(T0 + t) * 16 + 4 * q + v], __builtin_fmaf(d, (float) si, -(dmin * (float) dm[t][v])), acc[T0 + t][v]);
+            acc[T0 + t][v] = __builtin_fmaf(yd[(T0 + t) * 16 + 4 * q + v], __builtin_fmaf(d, (float) si, -(dmin * (float) dm[t][v])), FIRST ? 0.0f : acc[T0 + t][v]);
         }
     }
 }
@@ -408,8 +395,14 @@ typedef short v2i16 __attribute__((ext_vector_type(2)));
 // [-64, 64], L = B & 63): D_H = X.H and D_L = X.L give sum_g sc_g dot_g = 64 D_H + D_L exactly.  The lane's values sit
 // in ql[64 (j / 2) + 16 q ..] (nibble j % 2) and qh[32 (j / 2) + 16 (q % 2) ..] (bits 4 (j % 2) + 2 (q / 2)); rows of
 // the 210-byte blocks are 2-byte aligned in LDS, so 16-byte reads go through ld16_u2.
-template <int NT, int T0>
+template <int NT, int T0, bool FIRST>
 __device__ __forceinline__ void step_q6k(const uint8_t *wt0, const int8_t *as, const float *yd, float (&acc)[GM_TILES][4]) {
+    // the tiles past NT hold nothing this item reads (a tile count is fixed for an item, and an item's first span
+    // writes its tiles without reading them): marking them redefined frees their registers in this step
+#pragma unroll
+    for (int t = T0 + NT; t < GM_TILES; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) asm volatile("" : "=v"(acc[t][v]));
     const int lid = lane_id_here(), q = lid >> 4, rr = lid & 15;
     const uint8_t *blk = wt0 + rr * block_bytes(Q6_K);
     const uint32_t sb = 2u * (uint32_t) (rr & 1);   // the tile starts dword-aligned; a 210-byte row shifts by 2
@@ -460,7 +453,7 @@ __device__ __forceinline__ void step_q6k(const uint8_t *wt0, const int8_t *as, c
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int si = (dh[t][v] << 6) + dl[t][v];
-            acc[T0 + t][v] = __builtin_fmaf(yd[(T0 + t) * 16 + 4 * q + v], d * (float) si, acc[T0 + t][v]);
+            acc[T0 + t][v] = __builtin_fmaf(yd[(T0 + t) * 16 + 4 * q + v], d * (float) si, FIRST ? 0.0f : acc[T0 + t][v]);
         }
     }
     asm volatile("");   // keeps the tile-count variants from being merged (which moved the accumulators to memory)
@@ -468,7 +461,6 @@ __device__ __forceinline__ void step_q6k(const uint8_t *wt0, const int8_t *as, c
 
 __host__ __device__ constexpr int xcd_gcd8(int n) { return (n & 7) == 0 ? 8 : (n & 3) == 0 ? 4 : (n & 1) == 0 ? 2 : 1; }
 
-template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
 // floor(p / a) as a multiply-high, with a_mul = ceil(2^32 / a): exact while p * (a_mul * a - 2^32) < 2^32, which
 // p * a < 2^32 guarantees (the launchers check it)
@@ -640,19 +632,39 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
                 // straight-line code per tile count
                 const uint8_t *wt = stage_w(stage) + wave * C::TB;
                 static_assert(GM_TILES == 4, "one case per tile count");
-                switch (ntile) {
-                case 1: step_q4k<1, 0>(wt, as, yd, acc); break;
-                case 2: step_q4k<2, 0>(wt, as, yd, acc); break;
-                case 3: step_q4k<3, 0>(wt, as, yd, acc); break;
-                default: step_q4k<4, 0>(wt, as, yd, acc); break;
+                // an item's first span starts its accumulators (fmaf with +0, the bits of a sum begun at 0): no reset
+                // after the epilogue, so the accumulators stay in the same registers on every path through the loop
+                if (b == 0) {
+                    switch (ntile) {
+                    case 1: step_q4k<1, 0, true>(wt, as, yd, acc); break;
+                    case 2: step_q4k<2, 0, true>(wt, as, yd, acc); break;
+                    case 3: step_q4k<3, 0, true>(wt, as, yd, acc); break;
+                    default: step_q4k<4, 0, true>(wt, as, yd, acc); break;
+                    }
+                } else {
+                    switch (ntile) {
+                    case 1: step_q4k<1, 0, false>(wt, as, yd, acc); break;
+                    case 2: step_q4k<2, 0, false>(wt, as, yd, acc); break;
+                    case 3: step_q4k<3, 0, false>(wt, as, yd, acc); break;
+                    default: step_q4k<4, 0, false>(wt, as, yd, acc); break;
+                    }
                 }
             } else if constexpr (T == Q6_K) {
                 const uint8_t *wt = stage_w(stage) + wave * C::TB;
-                switch (ntile) {
-                case 1: step_q6k<1, 0>(wt, as, yd, acc); break;
-                case 2: step_q6k<2, 0>(wt, as, yd, acc); break;
-                case 3: step_q6k<3, 0>(wt, as, yd, acc); break;
-                default: step_q6k<4, 0>(wt, as, yd, acc); break;
+                if (b == 0) {
+                    switch (ntile) {
+                    case 1: step_q6k<1, 0, true>(wt, as, yd, acc); break;
+                    case 2: step_q6k<2, 0, true>(wt, as, yd, acc); break;
+                    case 3: step_q6k<3, 0, true>(wt, as, yd, acc); break;
+                    default: step_q6k<4, 0, true>(wt, as, yd, acc); break;
+                    }
+                } else {
+                    switch (ntile) {
+                    case 1: step_q6k<1, 0, false>(wt, as, yd, acc); break;
+                    case 2: step_q6k<2, 0, false>(wt, as, yd, acc); break;
+                    case 3: step_q6k<3, 0, false>(wt, as, yd, acc); break;
+                    default: step_q6k<4, 0, false>(wt, as, yd, acc); break;
+                    }
                 }
             } else {
             Raw<T> wr;
@@ -729,10 +741,12 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
                     for (int r = lane; r < OR; r += 64) store_f32(o + r, GU ? hy_swiglu(so[r], su[r], m.clamp) : wt * so[r]);
                 }
             }
+            if constexpr (T != Q4_K && T != Q6_K) {   // (the Q4_K / Q6_K steps start the next item's sums themselves)
 #pragma unroll
-            for (int tile = 0; tile < GM_TILES; ++tile)
+                for (int tile = 0; tile < GM_TILES; ++tile)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) acc[tile][v] = 0.0f;
+                    for (int v = 0; v < 4; ++v) acc[tile][v] = 0.0f;
+            }
         };
 
         // the stream: steps 0 .. D - 2 issued ahead; past the end, the last step is issued again (into the stage

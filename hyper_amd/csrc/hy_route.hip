@@ -268,10 +268,153 @@ __global__ __launch_bounds__(GL_THREADS, GT ? 4 : 2) void k_router_pre(const WT 
     }
 }
 
+// Router logits of many tokens with the weight rows held in registers (kdim = 256 NI, NI 4 or 8): a block of 8 waves
+// owns 32 rows (wave w: rows 4 w .. 4 w + 3, each lane its float4 at 256 i + 4 L of every row, loaded once) and a range
+// of tokens, which reach LDS 8 at a time by DMA (two buffers: chunk c + 1 lands while chunk c's fmas run; wave w
+// fetches token w of a chunk).  Every x value read from LDS feeds 4 rows x 4 fmas, half the LDS bytes per fma of the
+// tile kernel above, and the weights are read from memory once per block.  The lane partial sums of each chunk meet in
+// the same tree as gemv_block_lds (the butterfly's bits).  The Q8 rows of x come from the staged chunk too: every
+// row-group block of a range stages the same chunks, and block bx quantizes the chunk's units u with u % gx == bx.
+constexpr int RR_ROWS = 4, RR_WAVES = 8, RR_THREADS = 64 * RR_WAVES, RR_TC = 8;
+template <int VT, int NI, typename WT>
+__global__ __launch_bounds__(RR_THREADS, 2) void k_router_rows(const WT *__restrict__ W, int rows, const float *__restrict__ x, int xs,
+                                                             const float *__restrict__ bias, int bs, float *__restrict__ y, int ys, int nt,
+                                                             uint8_t *__restrict__ xq, int gx, int tpr) {
+    static_assert(RR_TC == RR_WAVES, "a wave fetches one token row of a chunk");
+    constexpr int kdim = 256 * NI, ROWF4 = 64 * NI;   // float4 per token row
+    __shared__ f4v st[2][RR_TC * ROWF4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int bx = blockIdx.x % gx, by = blockIdx.x / gx;
+    const int t_beg = by * tpr, t_end = min(nt, t_beg + tpr);
+    const int r0 = bx * RR_ROWS * RR_WAVES + RR_ROWS * wave;
+    const bool wave_on = r0 < rows;   // wave-uniform: waves past the last row stage, quantize and synchronize only
+    const int nchunk = t_end > t_beg ? (t_end - t_beg + RR_TC - 1) / RR_TC : 0;
+    if (nchunk == 0) return;   // uniform over the block
+    // chunk c into buffer buf: wave w's NI DMAs of 1 KB bring token c0 + w (past the range's end: its last token again,
+    // whose outputs are never stored), so that every wave issues NI per chunk
+    auto dma_chunk = [&](int c, int buf) {
+        const int t = min(t_beg + RR_TC * c + wave, t_end - 1);
+        const float *src = x + (size_t) t * xs;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) dma_s128(src + 256 * i, 16u * (uint32_t) lane, lds_addr(&st[buf][wave * ROWF4 + 64 * i]));
+    };
+    dma_chunk(0, 0);
+    f4v w[RR_ROWS][NI];
+#pragma unroll
+    for (int a = 0; a < RR_ROWS; ++a) {
+        const WT *wr = W + (size_t) min(r0 + a, rows - 1) * kdim + 4 * lane;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) { const float4 v = ld_w4(wr + 256 * i); w[a][i] = f4v{v.x, v.y, v.z, v.w}; }
+    }
+    // the weights (and chunk 0) landed, by a wait the compiler sees: it then places no wait for the weight registers
+    // inside the chunk loop, where one would also wait for the next chunk's DMAs
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0), expcnt and lgkmcnt at their maxima
+    if (nchunk > 1) dma_chunk(1, 1);
+    constexpr int NOUT = RR_ROWS * RR_TC, P = 16, LPO = 64 / P, SUB = 64 / LPO;   // the tree of gemv_block_lds, 16 outputs a pass
+    static_assert(NOUT % P == 0 && RR_WAVES * 64 * P <= RR_TC * ROWF4 * 4, "the passes fit a chunk buffer");
+    for (int c = 0; c < nchunk; ++c) {
+        const int buf = c & 1, c0 = t_beg + RR_TC * c, ntok = min(RR_TC, t_end - c0);
+        if (c + 1 < nchunk) wait_vm<NI>(); else wait_vm<0>();   // this wave's DMAs of chunk c have landed
+        lds_barrier();                                           // and every wave's
+        // the chunk's Q8 rows (from LDS): Q8_K a 256-value block per 16-lane row, Q8_0 a pair of 32-value blocks a wave
+        if constexpr (VT == Q8_K) {
+            const int units = ntok * NI;
+            for (int u = bx + gx * (tid >> 4); u < units; u += gx * (RR_THREADS / 16)) {   // uniform over the 16-lane row
+                const int tk = u / NI, b = u - tk * NI;
+                const f4v *src = &st[buf][tk * ROWF4 + 64 * b + 4 * (lane & 15)];
+                float xv[16];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) { const f4v v = src[j]; xv[4 * j] = v.x; xv[4 * j + 1] = v.y; xv[4 * j + 2] = v.z; xv[4 * j + 3] = v.w; }
+                q8k_block16(xv, xq + ((size_t) (c0 + tk) * NI + b) * Q8K_BYTES);
+            }
+        } else {
+            constexpr int NP = 4 * NI;   // pairs of Q8_0 blocks a token row
+            const int units = ntok * NP;
+            for (int u = bx + gx * wave; u < units; u += gx * RR_WAVES) {   // wave-uniform
+                const int tk = u / NP, pb = u - tk * NP;
+                const float v = ((const float *) &st[buf][tk * ROWF4])[64 * pb + lane];
+                q8_0_pair_vals(v, xq + ((size_t) (c0 + tk) * (8 * NI) + 2 * pb) * Q8_0_BYTES, true, Q8_0_BYTES, 2);
+            }
+        }
+        float acc[RR_ROWS][RR_TC];
+#pragma unroll
+        for (int a = 0; a < RR_ROWS; ++a)
+#pragma unroll
+            for (int u = 0; u < RR_TC; ++u) acc[a][u] = 0.0f;
+        if (wave_on) {
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+#pragma unroll
+                for (int u = 0; u < RR_TC; ++u) {
+                    const f4v xv = st[buf][u * ROWF4 + 64 * i + lane];
+#pragma unroll
+                    for (int a = 0; a < RR_ROWS; ++a) {
+                        float s = acc[a][u];
+                        s = __builtin_fmaf(w[a][i].x, xv.x, s);
+                        s = __builtin_fmaf(w[a][i].y, xv.y, s);
+                        s = __builtin_fmaf(w[a][i].z, xv.z, s);
+                        s = __builtin_fmaf(w[a][i].w, xv.w, s);
+                        acc[a][u] = s;
+                    }
+                }
+        }
+        lds_barrier();   // every wave is past its reads of this chunk: its buffer is the reduction's scratch now
+        if (wave_on) {
+            float *red = (float *) st[buf] + wave * 64 * P;
+            const int o = lane / LPO, q = lane % LPO;
+#pragma unroll
+            for (int p0 = 0; p0 < NOUT; p0 += P) {
+#pragma unroll
+                for (int u = 0; u < P; ++u) red[u * 64 + lane] = acc[(p0 + u) / RR_TC][(p0 + u) % RR_TC];
+                wave_lds_sync();
+                float v[SUB];
+#pragma unroll
+                for (int u = 0; u < SUB; u += 4) {
+                    const f4v w4 = *(const f4v *) (red + o * 64 + q * SUB + u);
+                    v[u] = w4.x; v[u + 1] = w4.y; v[u + 2] = w4.z; v[u + 3] = w4.w;
+                }
+#pragma unroll
+                for (int h = 1; h < SUB; h <<= 1)   // pairwise tree, natural order
+#pragma unroll
+                    for (int u = 0; u < SUB; u += 2 * h) v[u] = v[u] + v[u + h];
+                float sum = v[0];
+                sum = sum + dpp_f<DPP_XOR1>(sum);
+                sum = sum + dpp_f<DPP_XOR2>(sum);
+                const int idx = p0 + o, a = idx / RR_TC, u = idx % RR_TC, r = r0 + a, t = c0 + u;
+                if (q == 0 && r < rows && u < ntok) {
+                    if (bias) sum = sum + bias[(size_t) t * bs + r];
+                    y[(size_t) t * ys + r] = sum;
+                }
+                wave_lds_sync();   // this pass's reads are done before the next pass writes
+            }
+        }
+        if (c + 2 < nchunk) {
+            lds_barrier();        // every wave's scratch reads are done: the buffer takes chunk c + 2
+            dma_chunk(c + 2, buf);
+        }
+    }
+}
+
 template <typename WT>
 static int router_pre_any(const WT *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
                           int vtype, void *xq, int nt, hipStream_t s) {
     if (nt == 0) return HY_OK;
+    {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        const int gx = (rows + RR_ROWS * RR_WAVES - 1) / (RR_ROWS * RR_WAVES);
+        if ((kdim == 1024 || kdim == 2048) && gx * ((nt + RR_TC - 1) / RR_TC) >= cus && (xs & 3) == 0 && ((uintptr_t) x & 15) == 0) {
+            // one block a CU: the token ranges (whole chunks) that give gx x gy <= cus blocks
+            const int gy0 = std::max(1, cus / gx);
+            const int tpr = (nt + gy0 * RR_TC - 1) / (gy0 * RR_TC) * RR_TC, gy = (nt + tpr - 1) / tpr;
+#define HY_RR(VV, NN) hipLaunchKernelGGL((k_router_rows<VV, NN, WT>), dim3(gx * gy), dim3(RR_THREADS), 0, s, W, rows, x, xs, bias, bs, logits, ls, nt, \
+                                         (uint8_t *) xq, gx, tpr)
+            if (vtype == Q8_K) { if (kdim == 2048) HY_RR(Q8_K, 8); else HY_RR(Q8_K, 4); }
+            else { if (kdim == 2048) HY_RR(Q8_0, 8); else HY_RR(Q8_0, 4); }
+#undef HY_RR
+            return check_launch("hy_moe_router_q8");
+        }
+    }
     // kdim % 256 == 0: 16 x GT tiles through LDS (gemv_block_lds), GT = 16, or 8 when 16-token tiles number fewer
     // than two per CU (more blocks to hide the steps' barriers); else 16 rows x 8 tokens a block (gemv_tile, GT 0)
     int dev = 0, cus = 0;

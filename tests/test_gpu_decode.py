@@ -24,7 +24,10 @@ TOL = 2e-3
     (384, 7168, 8, GType.Q8_K, True, False),
     (512, 2048, 3, GType.Q8_K, True, True),
     (64, 512, 12, GType.Q8_0, True, False),     # more than 8 rows: the separate kernels (8-token LDS tiles)
-    (512, 512, 256, GType.Q8_K, True, True),    # 33 x 16 16-token tiles: two a CU or more, 16-token LDS tiles
+    (512, 512, 256, GType.Q8_K, True, True),    # 17 row groups x 32 chunks: the register-row kernel, kdim 512
+    (128, 2048, 512, GType.Q8_K, False, True),  # 512 tokens x 128 experts: the register-row kernel, one chunk a block
+    (199, 2048, 333, GType.Q8_0, True, True),   # a partial row group, partial chunks and token ranges
+    (288, 4096, 512, GType.Q8_K, False, False), # kdim 4096: 16-token LDS tiles
     (64, 544, 40, GType.Q8_0, False, True),     # d % 256 != 0: the register-tile path, an odd Q8_0 block count
 ])
 def test_router_q8_bitexact(cuda, E, d, nt, vt, with_sg, with_bias):

@@ -40,10 +40,12 @@ def test_gemv_bf16w_bitexact(cuda, rows, kdim, nt):
     assert_bits_equal(yb.cpu().numpy(), (ref + bias.numpy()).astype(np.float32), "bf16 logits + bias")
 
 
-# nt <= 8: the decode router (a wave per row); 9 and 40 tokens: the batched router's 8-token LDS tiles, 256 tokens x
-# 513 rows its 16-token tiles (a partial 16-row tile too); kdim 992 (not a multiple of 256): its register tiles
+# nt <= 8: the decode router (a wave per row); 9 and 40 tokens: the batched router's 8-token LDS tiles; 256 tokens x
+# 513 rows and 512 x 129: the register-row kernel (a partial row group too); 512 x 288 at kdim 4096: 16-token LDS
+# tiles; kdim 992 (not a multiple of 256): the register tiles
 @pytest.mark.parametrize("rows,kdim,nt,vt", [(129, 2048, 1, GType.Q8_K), (288, 4096, 8, GType.Q8_0), (513, 2048, 9, GType.Q8_K),
-                                              (128, 2048, 40, GType.Q8_K), (513, 1024, 256, GType.Q8_0), (128, 992, 20, GType.Q8_0)])
+                                              (128, 2048, 40, GType.Q8_K), (513, 1024, 256, GType.Q8_0), (129, 2048, 512, GType.Q8_K),
+                                              (288, 4096, 512, GType.Q8_0), (128, 992, 20, GType.Q8_0)])
 def test_router_q8_bf16w_bitexact(cuda, rows, kdim, nt, vt):
     W16, W32 = _bf16_weights(rows, kdim, 151 + nt)
     g = gen(152)
