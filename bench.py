@@ -175,11 +175,21 @@ def decode_bench(args, dev, stream):
         ms_rq = graph_time(rq * 8, max(1, args.decode_reps), stream) / (8 * len(rq))
         ms_gu = graph_time(gu * 8, max(1, args.decode_reps), stream) / (8 * len(gu))
         ms_dn = graph_time(dn * 8, max(1, args.decode_reps), stream) / (8 * len(dn))
+        # the floor of a chain of three dependent launches: three elementwise kernels a step on the token's 2048
+        # floats, each reading what the one before wrote (a launch boundary and a memory round trip each), replayed
+        # in a graph like the step
+        sink = torch.zeros(64, d, device=dev)
+        def chain(i):
+            t = xs[i:i + 1] * 2.0
+            t = t + 1.0
+            sink[i:i + 1].copy_(t)
+        ms_chain = graph_time([lambda i=i: chain(i) for i in range(64)], max(1, args.decode_reps), stream) / 64
     L0 = layers[0]
     tok_bytes = k * L0.expert_bytes() + E * d * 4 + 2 * d * 4
     us = ms * 1e3
     return ({"workload": "q4k_decode", "us_per_token": us, "hbm_gbs": tok_bytes / (us / 1e6) / 1e9,
             "hbm_frac": tok_bytes / (us / 1e6) / 1e9 / HBM_PEAK_GBS, "alg_bytes_per_token": tok_bytes,
+            "chain3_floor_us": ms_chain * 1e3,
             "kernels": {"router_q8": {"us": ms_rq * 1e3, "gbs": (E * d * 4 + d * 4) / (ms_rq / 1e3) / 1e9},
                         "route_gate_up": {"us": ms_gu * 1e3, "gbs": k * 2 * L0.gate_bytes / (ms_gu / 1e3) / 1e9},
                         "down_reduce": {"us": ms_dn * 1e3, "gbs": k * L0.down_bytes / (ms_dn / 1e3) / 1e9}}}, layers)
@@ -397,7 +407,7 @@ def main():
     if not args.no_decode:
         log("decode: building layers")
         dec, dec_layers = decode_bench(args, dev, stream)
-        log(f"decode: {dec['us_per_token']:.2f} us/token")
+        log(f"decode: {dec['us_per_token']:.2f} us/token (a chain of three dependent launches: {dec['chain3_floor_us']:.2f} us)")
     wl = None
     if not args.no_workloads:
         log("workloads: the other configured shapes")

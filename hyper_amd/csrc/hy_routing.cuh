@@ -43,15 +43,12 @@ __device__ __forceinline__ void route_probs(float (&v)[V], const int (&vi)[V], i
     for (int i = 0; i < V; ++i) v[i] = vi[i] < ne ? v[i] / s : -1.0f;
 }
 
-// softmax / top-k of one token by one wave, the contract of k_route: k rounds of wave argmax over the lanes'
-// sorted candidates
+// sort each lane's V candidates best first (rt_better2), then k rounds of wave argmax over the lanes' first candidates:
+// lane j < k gets the j-th best (value selw, index seli), every lane tot = the selected values summed in selection
+// order; a lane whose candidate is taken moves its next one up (the emptied slot gets `empty`)
 template <int V>
-__device__ void route_wave(const float *l, int ne, int k, int *ids, float *wts, float *sg) {
+__device__ __forceinline__ void select_sorted(float (&v)[V], int (&vi)[V], int k, float empty, float &selw, int &seli, float &tot) {
     const int lane = threadIdx.x & 63;
-    float v[V];
-    int vi[V];
-    route_load<V>(l, ne, v, vi);
-    route_probs<V>(v, vi, ne);
 #pragma unroll
     for (int i = 1; i < V; ++i)
 #pragma unroll
@@ -60,8 +57,7 @@ __device__ void route_wave(const float *l, int ne, int k, int *ids, float *wts, 
                 const float tv = v[j]; v[j] = v[j - 1]; v[j - 1] = tv;
                 const int ti = vi[j]; vi[j] = vi[j - 1]; vi[j - 1] = ti;
             }
-    float selw = 0.0f, tot = 0.0f;
-    int seli = 0;
+    selw = 0.0f; tot = 0.0f; seli = 0;
     for (int j = 0; j < k; ++j) {
         float bv = v[0];
         int bi = vi[0];
@@ -71,9 +67,23 @@ __device__ void route_wave(const float *l, int ne, int k, int *ids, float *wts, 
         if (vi[0] == bi) {
 #pragma unroll
             for (int i = 0; i < V - 1; ++i) { v[i] = v[i + 1]; vi[i] = vi[i + 1]; }
-            v[V - 1] = -1.0f; vi[V - 1] = 0x7fffffff;
+            v[V - 1] = empty; vi[V - 1] = 0x7fffffff;
         }
     }
+}
+
+// softmax / top-k of one token by one wave, the contract of k_route: k rounds of wave argmax over the lanes'
+// sorted candidates
+template <int V>
+__device__ void route_wave(const float *l, int ne, int k, int *ids, float *wts, float *sg) {
+    const int lane = threadIdx.x & 63;
+    float v[V];
+    int vi[V];
+    route_load<V>(l, ne, v, vi);
+    route_probs<V>(v, vi, ne);
+    float selw, tot;
+    int seli;
+    select_sorted<V>(v, vi, k, -1.0f, selw, seli, tot);
     if (lane < k) { ids[lane] = seli; wts[lane] = selw / tot; }
     if (lane == 0 && sg) sg[0] = 1.0f / (1.0f + hy_expf(-l[ne]));
 }

@@ -110,12 +110,13 @@ def _tie_logits(E, seed):
     return lg
 
 
-@pytest.mark.parametrize("E,k", [(40, 8), (128, 8), (8, 8), (64, 64)])
+# up to 128 experts: the eight-wave ranks; more: one wave
+@pytest.mark.parametrize("E,k", [(40, 8), (128, 8), (8, 8), (64, 64), (288, 8), (384, 6), (512, 16), (300, 17), (129, 1)])
 def test_route_gate_up_tie_rules(cuda, E, k):
     """The fused routing (logit ranks, checked against the probabilities, else ranks of the probabilities)
     selects, orders and weights the experts exactly as the oracle's router on ties."""
     tg = td = GType.Q4_K
-    d, ff = 2048, 256
+    d, ff = (2048, 256) if E <= 128 else (256, 256)
     L = layer(tg, td, E, ff, d, seed=760 + E)
     OL = oracle_layer(L)
     dev = moe.upload_experts(L, device=cuda)
@@ -134,6 +135,33 @@ def test_route_gate_up_tie_rules(cuda, E, k):
     assert_bits_equal(wts.cpu().numpy().reshape(nt, k), wts_r, "wts")
     assert_bits_equal(h.cpu().numpy(), h_r, "h")
     assert list(ids_r[2]) == list(range(k)), "all-equal logits select the k lowest ids"
+
+
+@pytest.mark.parametrize("E,k,sg", [(288, 8, False), (384, 6, True), (512, 10, True), (200, 16, False)])
+def test_route_gate_up_many_experts(cuda, E, k, sg):
+    """Random logits over 129-512 experts (one wave routes them), four tokens: ids, weights, the shared gate and h
+    equal the oracle's."""
+    tg = td = GType.Q4_K
+    d, ff, nt = 256, 256, 4
+    L = layer(tg, td, E, ff, d, seed=780 + E)
+    OL = oracle_layer(L)
+    dev = moe.upload_experts(L, device=cuda)
+    lg = _logits(E, nt, sg, 781 + k)
+    ids_r, wts_r, sg_r = orc.route(lg, E, k, with_sg=sg)
+    x = torch.randn(nt, d, generator=gen(782))
+    _, h_r, _ = orc.moe_layer(OL, x.numpy(), ids_r, wts_r, want_hy=True)
+    xq = torch.from_numpy(orc.quantize(GType.Q8_K, x.numpy())).reshape(-1).to(cuda)
+    ids = torch.full((nt * k,), -5, dtype=torch.int32, device=cuda)
+    wts = torch.zeros(nt * k, device=cuda)
+    sgd = torch.zeros(nt, device=cuda) if sg else None
+    h = torch.full((nt * k, ff), float("nan"), device=cuda)
+    moe.moe_route_gate_up(dev, torch.from_numpy(lg).to(cuda), lg.shape[1], E, k, xq, ids, wts, sgd, h, nt)
+    torch.cuda.synchronize()
+    assert_bits_equal(ids.cpu().numpy().reshape(nt, k), ids_r, "ids")
+    assert_bits_equal(wts.cpu().numpy().reshape(nt, k), wts_r, "wts")
+    if sg:
+        assert_bits_equal(sgd.cpu().numpy(), sg_r, "sg")
+    assert_bits_equal(h.cpu().numpy(), h_r, "h")
 
 
 def test_decode_skips_non_local_experts(cuda):
