@@ -1,6 +1,6 @@
 // Per-type block decoding for the integer dot products.
 //
-// Decode GEMV mapping: a 256-value item of a weight row (one super-block, or eight IQ4_NL blocks) is
+// Decode GEMV mapping: a 256-value item of a weight row (one super-block, or eight IQ4_NL / Q8_0 blocks) is
 // handled by 8 lanes; lane L loads a 16-byte slice of the quant bytes (coalesced: the group reads the
 // item's quant bytes contiguously) and returns exact integer partial sums (sumi, summ) against the
 // matching Q8 activation bytes; the 8 partials are summed exactly in integers.  Layouts follow the
@@ -187,13 +187,43 @@ template <> struct Item<IQ4_NL> {
     // qs of block L: 2 mod 4 for even L (spans are 16-byte aligned), where the 2 bytes read past them are the next
     // block's d (L < 7)
     __device__ __forceinline__ void load(const uint8_t *b, int L) { qs = load16_a2_nb(b + 18 * L + 2); d = ld_u16(b + 18 * L); }
-    __device__ __forceinline__ void ints(const uint8_t *y, int, int &si, int &sm) const {
-        const uint32_t *ya = (const uint32_t *) (y + 4);
+    // the block's integer dot against the 32 activation values ya (4 a word)
+    __device__ __forceinline__ int dot32(const uint32_t (&ya)[8]) const {
         const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
         int s = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) { s = sdot4(kv4(q[i] & 0x0F0F0F0Fu), ya[i], s); s = sdot4(kv4((q[i] >> 4) & 0x0F0F0F0Fu), ya[4 + i], s); }
-        si = s; sm = 0;
+        return s;
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int, int &si, int &sm) const {
+        const uint32_t *yw = (const uint32_t *) (y + 4);
+        const uint32_t ya[8] = {yw[0], yw[1], yw[2], yw[3], yw[4], yw[5], yw[6], yw[7]};
+        si = dot32(ya); sm = 0;
+    }
+    __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
+};
+// Q8_0 weights (34 B: d, qs[32] int8) against Q8_0, src/kernels4.cu:421-714 (deq8: d * qs[j]): lane L takes the
+// item's block L whole.  Its qs start at 34 L + 2: 2 mod 4 for even L, where the second 16-byte load reads the 2 bytes
+// past the block (the next block's d, L < 7); aligned for odd L.
+template <> struct Item<Q8_0> {
+    uint4 q0, q1;
+    uint16_t d;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+        q0 = load16_a2_nb(b + 34 * L + 2);
+        q1 = load16_a2_nb(b + 34 * L + 18);
+        d = ld_u16(b + 34 * L);
+    }
+    __device__ __forceinline__ int dot32(const uint32_t (&ya)[8]) const {
+        const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s = sdot4(q[i], ya[i], s);
+        return s;
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int, int &si, int &sm) const {
+        const uint32_t *yw = (const uint32_t *) (y + 4);
+        const uint32_t ya[8] = {yw[0], yw[1], yw[2], yw[3], yw[4], yw[5], yw[6], yw[7]};
+        si = dot32(ya); sm = 0;
     }
     __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
 };

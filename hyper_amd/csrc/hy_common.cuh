@@ -29,7 +29,7 @@ __host__ __device__ constexpr int block_bytes(int t) {
 __host__ __device__ constexpr int block_elems(int t) {
     return (t == IQ4_NL || t == Q8_0) ? 32 : (t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == Q8_K) ? 256 : 0;
 }
-__host__ __device__ constexpr int vec_dot_type(int t) { return t == IQ4_NL ? Q8_0 : Q8_K; }
+__host__ __device__ constexpr int vec_dot_type(int t) { return t == IQ4_NL || t == Q8_0 ? Q8_0 : Q8_K; }
 
 // ------------------------------------------------------------------ scalar helpers
 

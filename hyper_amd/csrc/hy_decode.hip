@@ -143,16 +143,13 @@ __global__ __launch_bounds__(256) void k_router_q8(const WT *__restrict__ W, int
 // aligned), with the scales kept apart.
 template <int T>
 __device__ __forceinline__ float item_t(const Item<T> &it, const uint8_t *y, int gi, int L, bool valid, float *tv_out, int tv_idx) {
-    if constexpr (T == IQ4_NL) {
+    if constexpr (block_elems(T) == 32) {
         // lane L takes block 8 gi + L whole
         const uint8_t *yb = y + (size_t) (8 * gi + L) * 32;
-        int s = 0;
         if (valid) {
             const uint4 y0 = *(const uint4 *) yb, y1 = *(const uint4 *) (yb + 16);
-            const uint32_t q[4] = {it.qs.x, it.qs.y, it.qs.z, it.qs.w}, ya[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { s = sdot4(kv4(q[i] & 0x0F0F0F0Fu), ya[i], s); s = sdot4(kv4((q[i] >> 4) & 0x0F0F0F0Fu), ya[4 + i], s); }
-            tv_out[tv_idx + L] = it.tval(s, 0);
+            const uint32_t ya[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+            tv_out[tv_idx + L] = it.tval(it.dot32(ya), 0);
         }
         return 0.0f;
     } else {
@@ -304,7 +301,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
 #pragma unroll
         for (int ps = 0; ps < NP; ++ps) {
             if (base + 8 * ps >= npos) break;   // wave-uniform
-            const int r = cc.u, gi = cc.s, blk = T == IQ4_NL ? 8 * gi : gi;
+            const int r = cc.u, gi = cc.s, blk = block_elems(T) == 32 ? 8 * gi : gi;
             const bool valid = r < rw && row0 + r < ff;
             if constexpr (T == IQ2_XS) { bg[ps].grid = grid; bu[ps].grid = grid; }
             item_t<T>(bg[ps], s_y, gi, L, valid, tw, r * rs + blk);
@@ -524,7 +521,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
                 const int j = cc.u, gi = cc.s;
                 const bool valid = i < items && pair_ok(j);
                 if constexpr (T == IQ2_XS) it[ps].grid = grid;
-                item_t<T>(it[ps], hq + (size_t) j * ng * SPAN_L, gi, L, valid, tw, j * (nb | 1) + (T == IQ4_NL ? 8 * gi : gi));
+                item_t<T>(it[ps], hq + (size_t) j * ng * SPAN_L, gi, L, valid, tw, j * (nb | 1) + (block_elems(T) == 32 ? 8 * gi : gi));
                 cc.next(ng, q8, r8);
             }
         }
@@ -579,6 +576,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     case IQ4_XS: { constexpr int TT = IQ4_XS; CALL; }                                           \
     case IQ2_XS: { constexpr int TT = IQ2_XS; CALL; }                                           \
     case IQ4_NL: { constexpr int TT = IQ4_NL; CALL; }                                           \
+    case Q8_0: { constexpr int TT = Q8_0; CALL; }                                               \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE;   \
     }
 
@@ -610,15 +608,17 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
     if (2 * ng > 8 * DEC_MAXP || 2 * nb > DEC_GU_TV) { set_error("hy_moe_route_gate_up: n = %d exceeds %d", m.n, 256 * 4 * DEC_MAXP); return HY_EBAD_SHAPE; }
     if (m.gate_bytes >= ((size_t) 1 << 32)) { set_error("hy_moe_route_gate_up: an expert matrix of %zu bytes (4 GiB or more)", m.gate_bytes); return HY_EBAD_SHAPE; }
     if (hq) {   // the Q8_0 hidden as well: 32-row blocks (rw 4), items and fold inputs within the HQ instantiation's limits
-        if (m.tg != IQ4_NL || m.td != IQ4_NL || 4 * 2 * nb > 2 * DEC_GU_TV) {
-            set_error("hy_moe_route_gate_up_q8: needs IQ4_NL gate/up and down weights and n <= 4096 (types %d/%d, n %d)", m.tg, m.td, m.n);
+        if ((m.tg != IQ4_NL && m.tg != Q8_0) || vec_dot_type(m.td) != Q8_0 || 4 * 2 * nb > 2 * DEC_GU_TV) {
+            set_error("hy_moe_route_gate_up_q8: needs IQ4_NL or Q8_0 gate/up and down weights and n <= 4096 (types %d/%d, n %d)", m.tg, m.td, m.n);
             return HY_EUNSUPPORTED_TYPE;
         }
         if (nt == 0) return HY_OK;
         const int V = (ne + 63) / 64, q8 = 8 / ng, r8 = 8 % ng;
         dim3 grid(m.ff / 32, nt * k);
-#define HY_RGUQ(VV) hipLaunchKernelGGL((k_route_gate_up<IQ4_NL, VV, DEC_PIPE_NP, true, true>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, 4, q8, r8, hq)
-        if (V <= 1) HY_RGUQ(1); else if (V <= 2) HY_RGUQ(2); else if (V <= 4) HY_RGUQ(4); else if (V <= 8) HY_RGUQ(8); else HY_RGUQ(16);
+#define HY_RGUQ(TQ, VV) hipLaunchKernelGGL((k_route_gate_up<TQ, VV, DEC_PIPE_NP, true, true>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, 4, q8, r8, hq)
+#define HY_RGUQ_V(TQ) if (V <= 1) HY_RGUQ(TQ, 1); else if (V <= 2) HY_RGUQ(TQ, 2); else if (V <= 4) HY_RGUQ(TQ, 4); else if (V <= 8) HY_RGUQ(TQ, 8); else HY_RGUQ(TQ, 16);
+        if (m.tg == IQ4_NL) { HY_RGUQ_V(IQ4_NL) } else { HY_RGUQ_V(Q8_0) }
+#undef HY_RGUQ_V
 #undef HY_RGUQ
         return check_launch("hy_moe_route_gate_up_q8");
     }

@@ -195,6 +195,25 @@ template <> struct Raw<IQ4_NL> {
     __device__ __forceinline__ float cfold(int c, int d) const { return h2f((dd[c >> 1] >> (16 * (c & 1))) & 0xffff) * (float) d; }
     __device__ __forceinline__ float fold(int si, int) const { return (float) si; }
 };
+// Q8_0 weights (8 blocks of 34 B per 256 values, Q8_0 activations): chunk c = block c; lane values 8 q .. + 7 are
+// qs[8 q ..] of block c as they are (int8); block c's qs sit at 34 c + 2 (2 mod 4 for even c, where the 8-byte read
+// takes 2 bytes of block c + 1, c < 7); every block folds on its own, as IQ4_NL's.
+template <> struct Raw<Q8_0> {
+    static constexpr bool mins = false, g16 = false, per_chunk = true;
+    uint2 qv[8]; uint32_t dd[4];
+    __device__ __forceinline__ void load(const uint8_t *blk, int q) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) qv[c] = ld8_2a(blk + 34 * c + 2 + 8 * q);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dd[i] = (uint32_t) ld_u16(blk + 68 * i) | ((uint32_t) ld_u16(blk + 68 * i + 34) << 16);
+    }
+    __device__ __forceinline__ void chunk(int c, int, const uint2 *, uint32_t &b0, uint32_t &b1, int &s0, int &s1, int &mn) const {
+        b0 = qv[c].x; b1 = qv[c].y;
+        s0 = 1; s1 = 0; mn = 0;
+    }
+    __device__ __forceinline__ float cfold(int c, int d) const { return h2f((dd[c >> 1] >> (16 * (c & 1))) & 0xffff) * (float) d; }
+    __device__ __forceinline__ float fold(int si, int) const { return (float) si; }
+};
 
 constexpr int GM_TOK = 64, GM_TILES = GM_TOK / 16, GM_ROWS = 64, GM_LD = 264;   // LDS row stride of staged activations
 
@@ -471,7 +490,7 @@ template <int T, bool GU, int W, int B>
 __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const uint8_t *__restrict__ aq, uint64_t a_mul, const int *__restrict__ order,
                                                         const int *__restrict__ order_n, const int *__restrict__ egrp, const float *__restrict__ wts,
                                                         float *__restrict__ out) {
-    static_assert(T != IQ4_NL, "IQ4_NL runs k_gemm_nl");
+    static_assert(vec_dot_type(T) != Q8_0, "the Q8_0-activation types run k_gemm_nl");
     using C = G5<T, W, B>;
     constexpr int D = C::D, AQ = Q8K_BYTES;
     __shared__ __align__(16) uint8_t smem[D * C::SB];   // stage s at s * SB: weights [wave][TB], activations [64][256], d [64]
@@ -765,7 +784,7 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
     }
 }
 
-// IQ4_NL: one chunk's MFMA per tile folded straight into the fp32 accumulators (Yc: 8 block scales per token)
+// IQ4_NL / Q8_0: one chunk's MFMA per tile folded straight into the fp32 accumulators (Yc: 8 block scales per token)
 template <int T>
 __device__ __forceinline__ void chunk_fold(const Raw<T> &w, int c, int q, const int8_t *As, const float *Yc, int rr, int ntile,
                                            float (&acc)[GM_TILES][4]) {
@@ -783,7 +802,7 @@ __device__ __forceinline__ void chunk_fold(const Raw<T> &w, int c, int q, const 
     }
 }
 
-// IQ4_NL (Q8_0 activations, whose 2-byte aligned blocks the LDS DMA above cannot stage): register-staged
+// IQ4_NL and Q8_0 weights (Q8_0 activations, whose 2-byte aligned blocks the LDS DMA above cannot stage): register-staged
 // stream, one step ahead.  A block walks the work items it, it + gridDim.y, ...; the (item, block) steps form one stream in which the
 // next step's weight and activation bytes are loaded while the current step computes, across item boundaries.
 template <int T, bool GU>
@@ -791,7 +810,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
                                               const int *__restrict__ order_n, const int *__restrict__ egrp, const float *__restrict__ wts,
                                               float *__restrict__ out) {
     __shared__ __align__(16) int8_t As[2][GM_TOK * GM_LD];
-    constexpr bool NL = T == IQ4_NL;                 // Q8_0 activations, per-block fold
+    constexpr bool NL = vec_dot_type(T) == Q8_0;     // Q8_0 activations, per-block fold (IQ4_NL, Q8_0)
     __shared__ float Yd[2][GM_TOK * (NL ? 8 : 1)];
     __shared__ int s_scan[1024 + 8];
     __shared__ float s_up[GU ? 32 * GM_TOK : 1];
@@ -997,9 +1016,10 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
                         int max_active, float *h, hipStream_t s) {
     if (max_active <= 0 || n_pairs <= 0) return HY_OK;
     const int rt = (m.ff + 31) / 32;
-    if (m.tg == IQ4_NL) {
+    if (vec_dot_type(m.tg) == Q8_0) {
         dim3 grid(rt, item_slots(rt, n_pairs, max_active, 3));
-        hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
+        if (m.tg == IQ4_NL) hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
+        else hipLaunchKernelGGL((k_gemm_nl<Q8_0, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
         return check_launch("hy_moe_gemm_gate_up");
     }
     if ((size_t) n_pairs * (m.n / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_gate_up: activations of 4 GB or more"); return HY_EBAD_SHAPE; }
@@ -1026,9 +1046,10 @@ int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int
                      const float *wts, float *y, hipStream_t s) {
     if (max_active <= 0 || n_pairs <= 0) return HY_OK;
     const int rt = (m.n + GM_ROWS - 1) / GM_ROWS;
-    if (m.td == IQ4_NL) {
+    if (vec_dot_type(m.td) == Q8_0) {
         dim3 grid(rt, item_slots(rt, n_pairs, max_active, 3));
-        hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
+        if (m.td == IQ4_NL) hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
+        else hipLaunchKernelGGL((k_gemm_nl<Q8_0, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
         return check_launch("hy_moe_gemm_down");
     }
     if ((size_t) n_pairs * (m.ff / 256) * Q8K_BYTES >= (1ull << 32)) { set_error("hy_moe_gemm_down: activations of 4 GB or more"); return HY_EBAD_SHAPE; }

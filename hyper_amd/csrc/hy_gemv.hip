@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void k_gemv(hy_moe_dev m, int n_expert, const 
             const int mat = id / (nr * ng), rem = id % (nr * ng), row = rem / ng, gi = rem % ng;
             if constexpr (T == IQ2_XS) it[i].grid = grid;
             int si, sm;
-            if constexpr (T == IQ4_NL) {
+            if constexpr (block_elems(T) == 32) {
                 it[i].ints(xq + (8 * gi + L) * Q8_0_LDS, L, si, sm);
                 tv[(mat * R + row) * nb + 8 * gi + L] = it[i].tval(si, sm);
             } else {
@@ -158,6 +158,7 @@ static int launch_gemv_t(const hy_moe_dev &m, const float *src, int ss, const in
     case IQ4_XS: { constexpr int TT = IQ4_XS; CALL; }                                    \
     case IQ2_XS: { constexpr int TT = IQ2_XS; CALL; }                                    \
     case IQ4_NL: { constexpr int TT = IQ4_NL; CALL; }                                    \
+    case Q8_0: { constexpr int TT = Q8_0; CALL; }                                        \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(256) void k_down_reduce(hy_moe_dev m, int n_expert,
             const int j = id / (nr * ng), rem = id % (nr * ng), row = rem / ng, gi = rem % ng;
             if constexpr (T == IQ2_XS) it[i].grid = grid;
             int si, sm;
-            if constexpr (T == IQ4_NL) {
+            if constexpr (block_elems(T) == 32) {
                 it[i].ints(xq + j * xq_row + (8 * gi + L) * Q8_0_LDS, L, si, sm);
                 tv[(j * R + row) * nb + 8 * gi + L] = it[i].tval(si, sm);
             } else {
@@ -440,7 +441,7 @@ __global__ __launch_bounds__(256) void k_block_ints(const uint8_t *__restrict__ 
     it.load(rows + row * row_bytes + (size_t) gi * (256 / BE) * block_bytes(T), L);
     if constexpr (T == IQ2_XS) it.grid = grid;
     int si, sm;
-    if constexpr (T == IQ4_NL) {
+    if constexpr (block_elems(T) == 32) {
         it.ints(y0 + (8 * gi + L) * Q8_0_LDS, L, si, sm);
         sumi[row * nb + 8 * gi + L] = si;
         summ[row * nb + 8 * gi + L] = 0;
@@ -455,7 +456,7 @@ int launch_block_ints(int type, const uint8_t *rows, size_t row_bytes, int nrows
                       hipStream_t s) {
     const int groups = nrows * (n / 256);
     if (groups == 0) return HY_OK;
-    if (type == IQ4_NL && n / 32 > 256) { set_error("hy_block_ints: IQ4_NL rows longer than 8192"); return HY_EBAD_SHAPE; }
+    if ((type == IQ4_NL || type == Q8_0) && n / 32 > 256) { set_error("hy_block_ints: IQ4_NL / Q8_0 rows longer than 8192"); return HY_EBAD_SHAPE; }
     dim3 grid((groups + 31) / 32);
     HY_TYPE_SWITCH(type, hipLaunchKernelGGL((k_block_ints<TT>), grid, dim3(256), 0, s, rows, row_bytes, nrows, (const uint8_t *) xq, n,
                                             sumi, summ);

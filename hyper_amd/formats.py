@@ -5,7 +5,8 @@ Block sizes follow src/gguf.cpp:43-82; layouts follow the reference's deq8<T> (s
   Q5_K 176 B: d, dmin, scales[12] @4, qh[32] @16, qs[128] @48
   Q6_K 210 B: ql[128] @0, qh[64] @128, scales int8[16] @192, d f16 @208
   IQ4_NL 18 B per 32: d f16, qs[16];  IQ4_XS 136 B: d, scales_h u16 @2, scales_l[4] @4, qs[128] @8
-  IQ2_XS 74 B: d f16, qs u16[32] @2, scales[8] @66;  Q8_K 292 B: f32 d, qs[256], i16 bsums[16];  Q8_0 34 B
+  IQ2_XS 74 B: d f16, qs u16[32] @2, scales[8] @66;  Q8_K 292 B: f32 d, qs[256], i16 bsums[16];
+  Q8_0 34 B per 32: d f16, qs int8[32] (activation rows, and expert weights)
 Synthetic blocks (the workloads' generators): uniformly random quant bytes (which gives uniform nibbles,
 6-bit scales/mins, grid indices and sign bits), fp16 scale fields drawn uniformly from a stated range.
 """
@@ -44,7 +45,7 @@ def block_elems(t) -> int:
 
 def vec_dot_type(t) -> GType:
     """Activation partner type (ggml vec_dot_type; src/cpu_moe.cpp:711-715)."""
-    return GType.Q8_0 if GType(t) == GType.IQ4_NL else GType.Q8_K
+    return GType.Q8_0 if GType(t) in (GType.IQ4_NL, GType.Q8_0) else GType.Q8_K
 
 
 def row_bytes(t, n: int) -> int:

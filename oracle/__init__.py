@@ -23,7 +23,7 @@ def block_elems(t):
 
 
 def vec_dot_type(t):
-    return Q8_0 if int(t) == IQ4_NL else Q8_K
+    return Q8_0 if int(t) in (IQ4_NL, Q8_0) else Q8_K
 
 
 def row_bytes(t, n):

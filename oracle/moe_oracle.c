@@ -35,11 +35,11 @@ int or_block_elems(int type) {
     default: return 0;
     }
 }
-/* ggml's vec_dot_type: Q8_0 for IQ4_NL, Q8_K for the K-quants and the 256-block IQ types
+/* ggml's vec_dot_type: Q8_0 for IQ4_NL and Q8_0 weights, Q8_K for the K-quants and the 256-block IQ types
    (the activation quantizer is chosen per weight type: src/cpu_moe.cpp:711-715) */
 int or_vec_dot_type(int type) {
     switch (type) {
-    case OR_IQ4_NL: return OR_Q8_0;
+    case OR_IQ4_NL: case OR_Q8_0: return OR_Q8_0;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ4_XS: return OR_Q8_K;
     default: return -1;
     }
@@ -284,10 +284,11 @@ int or_dequant_row(int type, const uint8_t *row, int n, float *out) {
 /* exact integers of one weight block (type, bytes b) against activation block y (Q8_K: 292 B, Q8_0: 34 B).
    K-quants: sumi = sum_j sc_j S_j, summ = sum_j m_j (bsums[2j] + bsums[2j+1]) (ggml q4_K/q5_K x q8_K);
    Q6_K: sumi = sum_g sc_g sum_16 (q6 - 32) y; IQ4_XS: sumi = sum_ib (ls - 32) sum_32 kv y (src/iq3s_dot.h:
-   136-166); IQ2_XS: sumi = sum (2 sc + 1) sum_16 grid sign y; IQ4_NL x Q8_0: sumi = sum_32 kv q8. */
+   136-166); IQ2_XS: sumi = sum (2 sc + 1) sum_16 grid sign y; IQ4_NL x Q8_0: sumi = sum_32 kv q8; Q8_0 x Q8_0:
+   sumi = sum_32 q q8 (ggml's vec_dot_q8_0_q8_0 integer part). */
 static void block_ints_scalar(int type, const uint8_t *b, const uint8_t *y, int32_t *sumi, int32_t *summ) {
     int32_t si = 0, sm = 0;
-    const int8_t *q8 = (const int8_t *) (y + (type == OR_IQ4_NL ? 2 : 4));
+    const int8_t *q8 = (const int8_t *) (y + (or_vec_dot_type(type) == OR_Q8_0 ? 2 : 4));
     switch (type) {
     case OR_Q4_K: case OR_Q5_K: {
         int16_t bs[16]; memcpy(bs, y + 260, 32);
@@ -323,6 +324,9 @@ static void block_ints_scalar(int type, const uint8_t *b, const uint8_t *y, int3
         break;
     case OR_IQ4_NL:
         for (int l = 0; l < 32; ++l) si += iq4nl_q(b, l) * q8[l];
+        break;
+    case OR_Q8_0:
+        for (int l = 0; l < 32; ++l) si += (int8_t) b[2 + l] * q8[l];
         break;
     default: break;
     }
@@ -400,7 +404,8 @@ static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *su
 }
 
 static int dot_ok(int type) {
-    return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_IQ4_XS || type == OR_IQ2_XS || type == OR_IQ4_NL;
+    return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_IQ4_XS || type == OR_IQ2_XS || type == OR_IQ4_NL ||
+           type == OR_Q8_0;
 }
 int or_block_ints(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ) {
     if (!dot_ok(type) || n % or_block_elems(type)) return -1;
@@ -427,12 +432,12 @@ static float row_dot(int type, const uint8_t *row, const uint8_t *xq, int n) {
         int32_t si, sm;
         block_ints(type, b, y, &si, &sm);
         float xd, t;
-        if (type == OR_IQ4_NL) xd = h2f(y); else memcpy(&xd, y, 4);
+        if (or_vec_dot_type(type) == OR_Q8_0) xd = h2f(y); else memcpy(&xd, y, 4);
         switch (type) {
         case OR_Q4_K: case OR_Q5_K: t = fmaf(h2f(b), (float) si, -(h2f(b + 2) * (float) sm)); break;
         case OR_Q6_K: t = h2f(b + 208) * (float) si; break;
         case OR_IQ2_XS: t = (h2f(b) * 0.125f) * (float) si; break;
-        default: t = h2f(b) * (float) si; break;        /* IQ4_XS, IQ4_NL */
+        default: t = h2f(b) * (float) si; break;        /* IQ4_XS, IQ4_NL, Q8_0 */
         }
         acc = fmaf(xd, t, acc);
     }

@@ -73,6 +73,13 @@ def iq4nl(b):
     return dict(q=KV_IQ4NL[idx], sc=np.ones((b.shape[0], 1), np.int64), m=None, gsize=32, d=f16(b[:, 0:2]))
 
 
+def q8_0w(b):
+    """Q8_0 weights: d f16 @0, qs int8[32] @2 (deq8: d * qs[j])."""
+    b = b.reshape(-1, 34)
+    return dict(q=b[:, 2:34].view(np.int8).astype(np.int64), sc=np.ones((b.shape[0], 1), np.int64), m=None, gsize=32,
+                d=f16(b[:, 0:2]))
+
+
 def iq2xs(b, grid_rows, ksigns):
     """grid_rows: [512, 8] codebook bytes, ksigns: [128] sign bytes."""
     b = b.reshape(-1, 74)
@@ -104,6 +111,7 @@ def decode(t, b, grid_rows=None, ksigns=None):
     if t == 14: return q6k(b)
     if t == 23: return iq4xs(b)
     if t == 20: return iq4nl(b)
+    if t == 8: return q8_0w(b)
     if t == 17: return iq2xs(b, grid_rows, ksigns)
     raise ValueError(t)
 
@@ -125,6 +133,8 @@ def dequant(t, b, grid_rows=None, ksigns=None):
         return ((d * sc) * q.astype(np.float32)).astype(np.float32)
     if t == 20:
         return (q.astype(np.float32) * d).astype(np.float32)
+    if t == 8:
+        return (d * q.astype(np.float32)).astype(np.float32)
     if t == 17:
         db = (d * (np.float32(0.5) + ((sc - 1) / 2).astype(np.float32))) * np.float32(0.25)
         return ((db * np.abs(q).astype(np.float32)) * np.where(q < 0, np.float32(-1), np.float32(1))).astype(np.float32)
@@ -135,7 +145,7 @@ def block_ints(t, b, xq, grid_rows=None, ksigns=None):
     """Brute-force integers per block: sumi = sum over groups of scale * sum(q * y), summ = sum_j m_j * sum(y_j)."""
     f = decode(t, b, grid_rows, ksigns)
     q, gs = f["q"], f["gsize"]
-    if int(t) == 20:
+    if int(t) in (20, 8):
         y = q8_0(xq)["qs"]
     else:
         y = q8k(xq)["qs"]

@@ -59,6 +59,8 @@ ROUTE_GU_CASES = [
     (GType.IQ2_XS, GType.IQ2_XS, 16, 7168, 2048, 6, 2, True),
     (GType.IQ4_NL, GType.IQ4_NL, 16, 2048, 4096, 8, 2, False),   # k * ff / 32 > 512: down falls back to the R-row kernel
     (GType.Q4_K, GType.Q6_K, 64, 2560, 512, 8, 4, False),         # down: 3 rows a wave, the last block's rows past n
+    (GType.Q8_0, GType.Q8_0, 32, 2048, 768, 8, 2, True),
+    (GType.Q8_0, GType.Q4_K, 24, 1024, 512, 6, 3, False),
 ]
 
 

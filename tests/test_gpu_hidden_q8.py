@@ -28,7 +28,8 @@ CASES = [
 @pytest.mark.parametrize("E,d,ff,k,nt,absent", CASES)
 def test_hidden_q8_handover_bitexact(cuda, E, d, ff, k, nt, absent):
     print(f"hidden q8 E={E} d={d} ff={ff} k={k} nt={nt} absent={absent}", flush=True)
-    L = layer(GType.IQ4_NL, GType.IQ4_NL, E, ff, d, seed=740 + nt)
+    L = layer(GType.Q8_0 if nt == 3 else GType.IQ4_NL, GType.IQ4_NL if nt == 3 else GType.Q8_0 if nt == 8 else GType.IQ4_NL,
+              E, ff, d, seed=740 + nt)   # IQ4_NL both ways, a Q8_0 gate/up (3 rows), a Q8_0 down (8 rows)
     slot = [(-1 if e in absent else e) for e in range(E)]
     dev = moe.upload_experts(L, slot=slot, device=cuda)
     OL = oracle_layer(L)

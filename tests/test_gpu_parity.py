@@ -39,7 +39,7 @@ def test_q8_quantize_bitexact(cuda, vt):
 
 # ------------------------------------------------------------------ A11: block decoding
 
-@pytest.mark.parametrize("t", ALL_TYPES + [GType.Q8_0])
+@pytest.mark.parametrize("t", ALL_TYPES)
 def test_dequant_row_bitexact(cuda, t):
     n = 4096
     nb = n // block_elems(t)
@@ -143,6 +143,8 @@ DECODE_CASES = [
     (GType.IQ4_NL, GType.IQ4_NL, 4096, 1536, 8, 1),
     (GType.IQ4_XS, GType.IQ4_XS, 4096, 1536, 8, 4),
     (GType.IQ2_XS, GType.IQ2_XS, 7168, 2048, 6, 2),
+    (GType.Q8_0, GType.Q8_0, 2048, 768, 8, 2),
+    (GType.Q8_0, GType.Q6_K, 2048, 512, 4, 3),
 ]
 
 
@@ -206,6 +208,8 @@ GEMM_CASES = [
     (GType.IQ2_XS, GType.IQ2_XS, 7168, 2048, 6, 8),
     (GType.IQ4_NL, GType.IQ4_NL, 4096, 1536, 8, 4),
     (GType.IQ4_NL, GType.IQ4_NL, 2048, 512, 8, 50),
+    (GType.Q8_0, GType.Q8_0, 2048, 768, 8, 40),
+    (GType.Q4_K, GType.Q8_0, 1024, 512, 4, 30),     # a K-quant gate/up with a Q8_0 down (Q8_K x, Q8_0 hidden)
     (GType.Q4_K, GType.Q6_K, 2048, 768, 1, 100),    # k = 1: the pair is the token (reciprocal 2^32)
     (GType.Q4_K, GType.Q6_K, 1024, 512, 3, 90),     # odd k: the pair-to-token multiply-high
     (GType.Q4_K, GType.Q6_K, 1024, 256, 16, 12),    # k = E: every expert active, every token in each

@@ -19,7 +19,7 @@ import pytest
 import torch
 
 import oracle as orc
-from hyper_amd.formats import GType, block_bytes, block_elems, random_blocks, row_bytes
+from hyper_amd.formats import GType, block_bytes, block_elems, random_blocks, row_bytes, vec_dot_type
 from tests import np_formats as nf
 from tests.helpers import D_RANGE, gen, layer, oracle_layer, routing, x_distributions
 
@@ -214,6 +214,30 @@ def test_iq4nl_known_answer_positions():
     assert (orc.dequant_row(GType.IQ4_NL, blk.reshape(-1), 64) == want).all()
 
 
+def test_q8_0_weight_known_answers():
+    """Q8_0 weights (src/kernels4.cu:421-714, deq8: d * qs[j]): value j of a block is d * (int8) qs[j] in place, and
+    against a Q8_0 activation block the integer is sum_j qs[j] y[j] (ggml's vec_dot_q8_0_q8_0), folded as
+    x_d * (d * sumi)."""
+    q = np.array([[(5 * j + 3 * b) % 256 - 128 for j in range(32)] for b in range(2)], np.int64)   # -128 .. 127
+    blk = np.zeros((2, 34), np.uint8)
+    for b, dv in enumerate((0.5, -0.25)):
+        blk[b, 0:2] = _f16b(dv)
+        blk[b, 2:34] = q[b].astype(np.int8).view(np.uint8)
+    want = np.concatenate([q[0] * 0.5, q[1] * -0.25]).astype(np.float32)
+    assert (orc.dequant_row(GType.Q8_0, blk.reshape(-1), 64) == want).all()
+    y = np.array([(-7 * j) % 255 - 127 for j in range(64)], np.int64)   # the activation's int8 values
+    ya = np.zeros((2, 34), np.uint8)
+    for b, yd in enumerate((2.0, 0.125)):
+        ya[b, 0:2] = _f16b(yd)
+        ya[b, 2:34] = y[32 * b:32 * b + 32].astype(np.int8).view(np.uint8)
+    si, sm = orc.block_ints(GType.Q8_0, blk.reshape(-1), ya.reshape(-1), 64)
+    assert list(si) == [int(q[0] @ y[:32]), int(q[1] @ y[32:])] and not sm.any()
+    t0, t1 = np.float32(0.5) * np.float32(si[0]), np.float32(-0.25) * np.float32(si[1])
+    acc = np.float32(np.float64(2.0) * np.float64(t0))
+    want_dot = np.float32(np.float64(np.float32(0.125)) * np.float64(t1) + np.float64(acc))   # one rounding: fmaf
+    assert orc.row_dot(GType.Q8_0, blk.reshape(-1), ya.reshape(-1), 64) == want_dot
+
+
 def test_q8k_known_answers():
     x = np.zeros(512, np.float32)
     # block 0: max -127 at index 3 -> iscale = 1, q = round-half-even(x)
@@ -234,7 +258,7 @@ def test_q8k_known_answers():
 
 # ------------------------------------------------------------------ block decoding
 
-ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ4_NL]
+ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ4_NL, GType.Q8_0]
 
 
 def blocks(t, nb, seed):
@@ -310,7 +334,7 @@ def test_iq2xs_known_answer():
 @pytest.mark.parametrize("t", ALL)
 def test_block_ints_brute_force(t):
     n = 2048
-    vt = GType.Q8_0 if t == GType.IQ4_NL else GType.Q8_K
+    vt = vec_dot_type(t)
     rows = blocks(t, 6 * n // block_elems(t), 200 + int(t)).reshape(6, -1)
     for name, x in list(x_distributions(n, seed=23).items())[:4]:
         xq = orc.quantize(vt, x)
@@ -341,7 +365,7 @@ def test_vector_block_ints_equal_scalar_restatement(t):
 def test_row_dot_equals_fp64_of_dequantized_operands(t):
     """The block integers and their fp32 fold agree with sum(dequant(w) * dequant(q8(x))) in fp64 up to fp32 rounding."""
     n = 4096
-    vt = GType.Q8_0 if t == GType.IQ4_NL else GType.Q8_K
+    vt = vec_dot_type(t)
     rows = blocks(t, 8 * n // block_elems(t), 300 + int(t)).reshape(8, -1)
     x = np.random.default_rng(5).standard_normal(n).astype(np.float32)
     xq = orc.quantize(vt, x)
@@ -428,7 +452,7 @@ def test_layer_matches_fp64_recomputation(tg, td, d, ff, k):
     ids, wts = routing(nt, E, k, seed=401)
     x = torch.randn(nt, d, generator=gen(402)).numpy()
     out, h, y = orc.moe_layer(OL, x, ids, wts, want_hy=True)
-    vg, vd = (GType.Q8_0 if tg == GType.IQ4_NL else GType.Q8_K), (GType.Q8_0 if td == GType.IQ4_NL else GType.Q8_K)
+    vg, vd = vec_dot_type(tg), vec_dot_type(td)
     rows_g, ks = iq2xs_rows(), ksigns()
     ref = np.zeros((nt, d))
     for t in range(nt):
