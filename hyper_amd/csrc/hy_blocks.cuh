@@ -39,8 +39,10 @@ __device__ __forceinline__ uint32_t apply_sign(uint32_t g, uint32_t b4) {
 }
 // the same with the byte mask given (0xFF per negated byte): -g = ~g + 1 per byte, no carry (codebook bytes are not 0)
 __device__ __forceinline__ uint32_t apply_mask(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
-// LDS entries of an expanded IQ2_XS codebook: 512 rows, then 128 sign masks
+// LDS entries of an expanded IQ2_XS codebook: 512 rows, then 128 sign masks (IQ2_XXS: 256 rows, then the masks)
 constexpr int IQ2XS_LDS = 512 + 128;
+__host__ __device__ constexpr int iq2_rows(int t) { return t == IQ2_XS ? 512 : 256; }
+__host__ __device__ constexpr int iq2_lds(int t) { return iq2_type(t) ? iq2_rows(t) + 128 : 1; }   // uint2 entries
 // Q6_K: q6 bytes (0..63) -> q6 - 32 as int8: per byte (q + 96) ^ 128 = q - 32 mod 256 (q + 96 < 256: no carry)
 __device__ __forceinline__ uint32_t q6_signed(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
 
@@ -154,7 +156,7 @@ template <> struct Item<IQ4_XS> {
 };
 // IQ2_XS (74 B: d, qs u16[32], scales[8]).  Lane L = 32-group L: 8-groups l = 0..3 use qs[4 L + l]: grid row
 // q & 511, signs ksigns[q >> 9]; scale nibble l >> 1 of scales[L]; value d (2 sc + 1) / 8 grid sign.
-// `grid`: the codebook rows expanded to 8 bytes each and the sign masks (LDS, expand_iq2xs_grid).
+// `grid`: the codebook rows expanded to 8 bytes each and the sign masks (LDS, expand_iq2_grid).
 template <> struct Item<IQ2_XS> {
     uint16_t q[4];
     uint16_t d;
@@ -175,6 +177,32 @@ template <> struct Item<IQ2_XS> {
             s[l] = sdot4(apply_mask(g.y, sm.y), ya[2 * l + 1], sdot4(apply_mask(g.x, sm.x), ya[2 * l], 0));
         }
         si = (2 * (sc & 15) + 1) * (s[0] + s[1]) + (2 * (sc >> 4) + 1) * (s[2] + s[3]);
+        sm = 0;
+    }
+    __device__ __forceinline__ float tval(int si, int) const { return (h2f(d) * 0.125f) * (float) si; }
+};
+// IQ2_XXS (66 B: d, qs u16[32]), src/kernels4.cu:578-589.  Lane L = 32-group L, two words at 2 + 8 L: a0 holds the
+// four 8-groups' grid rows (byte l), a1 their 7-bit sign indices (bits 7 l ..) and the group's 4-bit scale (bits 28..);
+// value d (2 sc + 1) / 8 grid sign (ggml's vec_dot_iq2_xxs_q8_K integers: sumi = (2 sc + 1) sum grid sign y per group).
+template <> struct Item<IQ2_XXS> {
+    uint32_t a0, a1;
+    uint16_t d;
+    const uint2 *grid;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {   // b is 2-byte aligned (66-byte rows)
+        const uint8_t *p = b + 2 + 8 * L;
+        a0 = (uint32_t) ld_u16(p) | ((uint32_t) ld_u16(p + 2) << 16);
+        a1 = (uint32_t) ld_u16(p + 4) | ((uint32_t) ld_u16(p + 6) << 16);
+        d = ld_u16(b);
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
+        const uint32_t *ya = (const uint32_t *) (y + 4 + 32 * L);
+        int s = 0;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint2 g = grid[(a0 >> (8 * l)) & 255], m = grid[256 + ((a1 >> (7 * l)) & 127)];
+            s = sdot4(apply_mask(g.y, m.y), ya[2 * l + 1], sdot4(apply_mask(g.x, m.x), ya[2 * l], s));
+        }
+        si = (2 * (int) (a1 >> 28) + 1) * s;
         sm = 0;
     }
     __device__ __forceinline__ float tval(int si, int) const { return (h2f(d) * 0.125f) * (float) si; }
@@ -228,16 +256,20 @@ template <> struct Item<Q8_0> {
     __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
 };
 
-// expand the IQ2_XS codebook (base-3 codes) into 512 x 8 bytes of LDS, followed by the 128 sign patterns as byte
-// masks (entry 512 + i: byte j = 0xFF where bit j of ksign(i) is set, the parity bit giving byte 7)
-__device__ __forceinline__ void expand_iq2xs_grid(uint2 *grid) {
-    for (int i = threadIdx.x; i < IQ2XS_LDS; i += blockDim.x) {
-        if (i >= 512) {
-            const uint32_t ks = ksign((uint32_t) i - 512);
+// expand an IQ2 codebook (base-3 codes: IQ2_XS 512 rows, IQ2_XXS 256) into rows x 8 bytes of LDS, followed by the
+// 128 sign patterns as byte masks (entry rows + i: byte j = 0xFF where bit j of ksign(i) is set, the parity bit giving
+// byte 7)
+template <int T>
+__device__ __forceinline__ void expand_iq2_grid(uint2 *grid) {
+    static_assert(iq2_type(T), "an IQ2 codebook");
+    constexpr int R = iq2_rows(T);
+    for (int i = threadIdx.x; i < R + 128; i += blockDim.x) {
+        if (i >= R) {
+            const uint32_t ks = ksign((uint32_t) i - R);
             grid[i] = make_uint2(spread4(ks & 15) * 0xFFu, spread4(ks >> 4) * 0xFFu);
             continue;
         }
-        uint32_t c = c_iq2xs_code[i], lo = 0, hi = 0;
+        uint32_t c = T == IQ2_XS ? c_iq2xs_code[i] : c_iq2xxs_code[i], lo = 0, hi = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint32_t dgt = c % 3; c /= 3;

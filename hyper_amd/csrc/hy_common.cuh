@@ -17,18 +17,21 @@
 namespace hy {
 
 // GGUF type ids (src/gguf.h:13-18)
-enum GT : int { Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, IQ2_XS = 17, IQ4_NL = 20, IQ4_XS = 23 };
+enum GT : int { Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, IQ2_XXS = 16, IQ2_XS = 17, IQ4_NL = 20, IQ4_XS = 23 };
 
 constexpr int Q8K_BYTES = 292;   // float d; int8 qs[256]; int16 bsums[16]
 constexpr int Q8_0_BYTES = 34;   // fp16 d; int8 qs[32]
 
 __host__ __device__ constexpr int block_bytes(int t) {
-    return t == Q4_K ? 144 : t == Q5_K ? 176 : t == Q6_K ? 210 : t == IQ4_XS ? 136 : t == IQ2_XS ? 74
+    return t == Q4_K ? 144 : t == Q5_K ? 176 : t == Q6_K ? 210 : t == IQ4_XS ? 136 : t == IQ2_XS ? 74 : t == IQ2_XXS ? 66
          : t == IQ4_NL ? 18 : t == Q8_0 ? 34 : t == Q8_K ? 292 : 0;
 }
 __host__ __device__ constexpr int block_elems(int t) {
-    return (t == IQ4_NL || t == Q8_0) ? 32 : (t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == Q8_K) ? 256 : 0;
+    return (t == IQ4_NL || t == Q8_0) ? 32
+         : (t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ2_XXS || t == Q8_K) ? 256 : 0;
 }
+// the IQ2 types: codebook rows and sign masks in LDS (expand_iq2_grid)
+__host__ __device__ constexpr bool iq2_type(int t) { return t == IQ2_XS || t == IQ2_XXS; }
 __host__ __device__ constexpr int vec_dot_type(int t) { return t == IQ4_NL || t == Q8_0 ? Q8_0 : Q8_K; }
 
 // ------------------------------------------------------------------ scalar helpers
@@ -263,6 +266,10 @@ __device__ __constant__ const int8_t c_kv_iq4nl[16] = {-127, -104, -83, -65, -49
 // IQ2_XS codebook rows, base-3 coded (digit i = byte i: 0 -> 8, 1 -> 25, 2 -> 43)
 __device__ __constant__ const uint16_t c_iq2xs_code[512] = {
 #include "iq2xs_grid.inc"
+};
+// IQ2_XXS codebook rows, the same coding (g_iq2xxs_grid, src/iq_grids.h:14-79)
+__device__ __constant__ const uint16_t c_iq2xxs_code[256] = {
+#include "iq2xxs_grid.inc"
 };
 // the IQ2 sign table: 7 sign bits plus an 8th that makes the count even (src/iq_grids.h:4-13)
 __device__ __forceinline__ uint32_t ksign(uint32_t i) { return i | ((uint32_t) (__builtin_popcount(i) & 1) << 7); }

@@ -199,7 +199,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     __shared__ int s_ids[64];
     __shared__ float s_wts[64], s_sg;
     __shared__ int s_slot[V ? 64 * V : 1];
-    __shared__ uint2 grid[T == IQ2_XS ? IQ2XS_LDS : 1];
+    __shared__ uint2 grid[iq2_lds(T)];
     __shared__ float s_xd[DEC_GU_TV / 2];   // activation scales of the token's Q8 row, one per weight block
     __shared__ __align__(16) uint8_t s_y[DEC_Y_BYTES];   // the token's Q8 row (every item reads its 256-value span here)
     HY_STAMP_VARS(5);
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
             if (tid + 64 * DEC_GU_WAVES < ne) s_slot[tid + 64 * DEC_GU_WAVES] = sl1;
         }
         if (tid < nb) s_xd[tid] = xd;
-        if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
+        if constexpr (iq2_type(T)) expand_iq2_grid<T>(grid);
     };
     const float *lg = logits + (size_t) t * ls;
     // the token's routing: every block of the token computes the same bits
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
             if (base + 8 * ps >= npos) break;   // wave-uniform
             const int r = cc.u, gi = cc.s, blk = block_elems(T) == 32 ? 8 * gi : gi;
             const bool valid = r < rw && row0 + r < ff;
-            if constexpr (T == IQ2_XS) { bg[ps].grid = grid; bu[ps].grid = grid; }
+            if constexpr (iq2_type(T)) { bg[ps].grid = grid; bu[ps].grid = grid; }
             item_t<T>(bg[ps], s_y, gi, L, valid, tw, r * rs + blk);
             item_t<T>(bu[ps], s_y, gi, L, valid, tw, r * rs + nb + blk);
             cc.next(ng, q8, r8);
@@ -383,7 +383,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     __shared__ float tv[DEC_DN_WAVES][DEC_DN_TV + 64];   // pair j's inputs at j (nb | 1): an odd stride, distinct banks
     __shared__ int s_slot[2 * 64 * DEC_DN_WAVES];   // n_expert <= 1024
     __shared__ int s_ord[DEC_DN_WAVES][64];
-    __shared__ uint2 grid[T == IQ2_XS ? IQ2XS_LDS : 1];
+    __shared__ uint2 grid[iq2_lds(T)];
     HY_STAMP_VARS(6);
     HY_STAMP(0);
     const int t = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
@@ -505,7 +505,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
         hquant(0);
         for (int ub = UB; ub < units; ub += UB) { hload(ub); hquant(ub); }
     }
-    if constexpr (T == IQ2_XS) expand_iq2xs_grid(grid);
+    if constexpr (iq2_type(T)) expand_iq2_grid<T>(grid);
     lds_barrier();
     HY_STAMP(2);
     HY_STAMP_WAIT(3);
@@ -520,7 +520,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
                 if (base + 8 * ps >= items) break;   // wave-uniform
                 const int j = cc.u, gi = cc.s;
                 const bool valid = i < items && pair_ok(j);
-                if constexpr (T == IQ2_XS) it[ps].grid = grid;
+                if constexpr (iq2_type(T)) it[ps].grid = grid;
                 item_t<T>(it[ps], hq + (size_t) j * ng * SPAN_L, gi, L, valid, tw, j * (nb | 1) + (block_elems(T) == 32 ? 8 * gi : gi));
                 cc.next(ng, q8, r8);
             }
@@ -575,6 +575,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     case Q6_K: { constexpr int TT = Q6_K; CALL; }                                               \
     case IQ4_XS: { constexpr int TT = IQ4_XS; CALL; }                                           \
     case IQ2_XS: { constexpr int TT = IQ2_XS; CALL; }                                           \
+    case IQ2_XXS: { constexpr int TT = IQ2_XXS; CALL; }                                         \
     case IQ4_NL: { constexpr int TT = IQ4_NL; CALL; }                                           \
     case Q8_0: { constexpr int TT = Q8_0; CALL; }                                               \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE;   \

@@ -165,6 +165,32 @@ template <> struct Raw<IQ2_XS> {
     __device__ __forceinline__ float fold(int si, int) const { return (h2f(d) * 0.125f) * (float) si; }
 };
 
+// IQ2_XXS (66 B): chunk c = 32-group c, two words at 2 + 8 c (grid rows a byte each, then 4 x 7 sign bits and the
+// 4-bit scale); lane q takes 8-group q: grid row byte q of the first word, signs bits 7 q .. of the second, the chunk's
+// scale 2 sc + 1 (src/kernels4.cu:578-589; ggml's vec_dot_iq2_xxs_q8_K integers).
+template <> struct Raw<IQ2_XXS> {
+    static constexpr bool mins = false, g16 = false, per_chunk = false;
+    uint32_t gi[2], a1[8], d;   // gi: the lane's grid row of chunk c in byte c % 4 of gi[c / 4]
+    __device__ __forceinline__ void load(const uint8_t *blk, int q) {
+        gi[0] = gi[1] = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const uint8_t *p = blk + 2 + 8 * c;
+            a1[c] = (uint32_t) ld_u16(p + 4) | ((uint32_t) ld_u16(p + 6) << 16);
+            gi[c >> 2] |= (uint32_t) p[q] << (8 * (c & 3));
+        }
+        d = ld_u16(blk);
+    }
+    __device__ __forceinline__ void chunk(int c, int q, const uint2 *grid, uint32_t &b0, uint32_t &b1, int &s0, int &s1, int &mn) const {
+        const uint2 g = grid[(gi[c >> 2] >> (8 * (c & 3))) & 255], m = grid[256 + ((a1[c] >> (7 * q)) & 127)];
+        b0 = apply_mask(g.x, m.x);
+        b1 = apply_mask(g.y, m.y);
+        s0 = 2 * (int) (a1[c] >> 28) + 1;
+        s1 = 0; mn = 0;
+    }
+    __device__ __forceinline__ float fold(int si, int) const { return (h2f(d) * 0.125f) * (float) si; }
+};
+
 // IQ4_NL (8 blocks of 18 B per 256 values, Q8_0 activations): chunk c = block c; lane values 8 q .. + 7 are
 // nibbles (q >> 1) of qs[8 (q & 1) ..]; every block folds on its own: acc = fma(x_d, fp16(d_c) * D, acc).
 template <> struct Raw<IQ4_NL> {
@@ -498,7 +524,7 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
     __shared__ int s_item[C::ITEMS][3];                  // first pair in order, tokens, weight slot
     __shared__ int s_pair[C::ITEMS][GM_TOK];             // pair index of each token of the segment's items
     __shared__ float s_wt[GU ? 1 : C::ITEMS][GM_TOK];    // down: their route weights
-    __shared__ uint2 grid[T == IQ2_XS ? IQ2XS_LDS : 1];
+    __shared__ uint2 grid[iq2_lds(T)];
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, rr = lane & 15, q = lane >> 4;
     const int na = order_n[1];
     // ---- items.  Expert group g (cnt tokens) owns ceil(cnt / 64) items: full ones of 4 token tiles and a last one of
@@ -529,7 +555,7 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
         uint64_t ex = base + inc - loc;
 #pragma unroll
         for (int i = 0; i < C::PER; ++i) { s_scan[C::PER * tid + i] = ex; ex += c2[i]; }
-        if (T == IQ2_XS) expand_iq2xs_grid(grid);
+        if constexpr (iq2_type(T)) expand_iq2_grid<T>(grid);
         __syncthreads();
     }
     uint64_t tot = 0;
@@ -814,7 +840,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
     __shared__ float Yd[2][GM_TOK * (NL ? 8 : 1)];
     __shared__ int s_scan[1024 + 8];
     __shared__ float s_up[GU ? 32 * GM_TOK : 1];
-    __shared__ uint2 grid[T == IQ2_XS ? IQ2XS_LDS : 1];
+    __shared__ uint2 grid[iq2_lds(T)];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, rr = lane & 15, q = lane >> 4;
     const int na = order_n[1];
     // ---- items: expert group g owns ceil(cnt_g / GM_TOK) of them; s_scan = exclusive prefix (block-wide)
@@ -836,7 +862,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
         int ex = base + inc - loc;
 #pragma unroll
         for (int i = 0; i < 4; ++i) { s_scan[4 * tid + i] = ex; ex += c4[i]; }
-        if (T == IQ2_XS) expand_iq2xs_grid(grid);
+        if constexpr (iq2_type(T)) expand_iq2_grid<T>(grid);
         __syncthreads();
     }
     const int total = s_scan[1024] + s_scan[1025] + s_scan[1026] + s_scan[1027];
@@ -990,6 +1016,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
     case Q6_K: { constexpr int TT = Q6_K; __VA_ARGS__; }                                                 \
     case IQ4_XS: { constexpr int TT = IQ4_XS; __VA_ARGS__; }                                             \
     case IQ2_XS: { constexpr int TT = IQ2_XS; __VA_ARGS__; }                                             \
+    case IQ2_XXS: { constexpr int TT = IQ2_XXS; __VA_ARGS__; }                                           \
     default: set_error("grouped GEMM: unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 

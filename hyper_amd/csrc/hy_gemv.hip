@@ -90,14 +90,14 @@ __global__ __launch_bounds__(256) void k_gemv(hy_moe_dev m, int n_expert, const 
         }
     }
     quantize_row_lds<VT>(xin, in_dim, xq);
-    if (T == IQ2_XS) expand_iq2xs_grid(grid);
+    if constexpr (iq2_type(T)) expand_iq2_grid<T>(grid);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < GEMV_MAXI; ++i) {
         const int id = g + 32 * i;
         if (id < items) {
             const int mat = id / (nr * ng), rem = id % (nr * ng), row = rem / ng, gi = rem % ng;
-            if constexpr (T == IQ2_XS) it[i].grid = grid;
+            if constexpr (iq2_type(T)) it[i].grid = grid;
             int si, sm;
             if constexpr (block_elems(T) == 32) {
                 it[i].ints(xq + (8 * gi + L) * Q8_0_LDS, L, si, sm);
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void k_gemv(hy_moe_dev m, int n_expert, const 
 template <int T, bool GU> static size_t gemv_lds(int in_dim, int R) {
     constexpr int VT = vec_dot_type(T), BE = block_elems(T);
     const int nb = in_dim / BE, ng = in_dim / 256, nmat = GU ? 2 : 1;
-    return lds16(VT == Q8_K ? ng * Q8K_BYTES : nb * Q8_0_LDS) + lds16(4 * nmat * R * nb) + lds16(4 * 2 * R) + (T == IQ2_XS ? IQ2XS_LDS * 8 : 0);
+    return lds16(VT == Q8_K ? ng * Q8K_BYTES : nb * Q8_0_LDS) + lds16(4 * nmat * R * nb) + lds16(4 * 2 * R) + (iq2_type(T) ? iq2_lds(T) * 8 : 0);
 }
 
 template <int T, bool GU>
@@ -157,6 +157,7 @@ static int launch_gemv_t(const hy_moe_dev &m, const float *src, int ss, const in
     case Q6_K: { constexpr int TT = Q6_K; CALL; }                                        \
     case IQ4_XS: { constexpr int TT = IQ4_XS; CALL; }                                    \
     case IQ2_XS: { constexpr int TT = IQ2_XS; CALL; }                                    \
+    case IQ2_XXS: { constexpr int TT = IQ2_XXS; CALL; }                                  \
     case IQ4_NL: { constexpr int TT = IQ4_NL; CALL; }                                    \
     case Q8_0: { constexpr int TT = Q8_0; CALL; }                                        \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
@@ -289,14 +290,14 @@ __global__ __launch_bounds__(256) void k_down_reduce(hy_moe_dev m, int n_expert,
         }
     }
     for (int j = 0; j < k; ++j) quantize_row_lds<VT>(h + ((size_t) t * k + j) * in_dim, in_dim, xq + j * xq_row);
-    if (T == IQ2_XS) expand_iq2xs_grid(grid);
+    if constexpr (iq2_type(T)) expand_iq2_grid<T>(grid);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < GEMV_MAXI; ++i) {
         const int id = g + 32 * i;
         if (id < items) {
             const int j = id / (nr * ng), rem = id % (nr * ng), row = rem / ng, gi = rem % ng;
-            if constexpr (T == IQ2_XS) it[i].grid = grid;
+            if constexpr (iq2_type(T)) it[i].grid = grid;
             int si, sm;
             if constexpr (block_elems(T) == 32) {
                 it[i].ints(xq + j * xq_row + (8 * gi + L) * Q8_0_LDS, L, si, sm);
@@ -344,7 +345,7 @@ static int launch_down_reduce_t(const hy_moe_dev &m, const float *h, const int *
     if (R < 1) { set_error("hy_moe_down_reduce: k * ff / 256 = %d exceeds %d", k * ng, 32 * GEMV_MAXI); return HY_EBAD_SHAPE; }
     if (R > rows) R = rows;
     const int xq_row = VT == Q8_K ? ng * Q8K_BYTES : nb * Q8_0_LDS;
-    const size_t lds = lds16(k * xq_row) + lds16(4 * k * R * nb) + lds16(4 * k * R) + lds16(4 * k) + (T == IQ2_XS ? IQ2XS_LDS * 8 : 0);
+    const size_t lds = lds16(k * xq_row) + lds16(4 * k * R * nb) + lds16(4 * k * R) + lds16(4 * k) + (iq2_type(T) ? iq2_lds(T) * 8 : 0);
     if (lds > 64 * 1024) { set_error("hy_moe_down_reduce: %zu bytes of LDS needed", lds); return HY_EBAD_SHAPE; }
     if (nt == 0) return HY_OK;
     dim3 grid(nt, (rows + R - 1) / R);
@@ -360,7 +361,8 @@ int launch_down_reduce(const hy_moe_dev &m, const float *h, const int *ids, cons
 // one row dequantized with the deq8 expressions (src/kernels4.cu:421-714): thread per value
 __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, float *__restrict__ out) {
     __shared__ uint2 grid[IQ2XS_LDS];
-    if (type == IQ2_XS) expand_iq2xs_grid(grid);
+    if (type == IQ2_XS) expand_iq2_grid<IQ2_XS>(grid);
+    else if (type == IQ2_XXS) expand_iq2_grid<IQ2_XXS>(grid);
     __syncthreads();
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -401,6 +403,14 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, floa
         const uint2 gr = grid[q & 511];
         const float gv = (float) (((j < 4 ? gr.x : gr.y) >> (8 * (j & 3))) & 0xff);
         v = (db * gv) * ((ksign(q >> 9) >> j) & 1 ? -1.0f : 1.0f);
+    } else if (type == IQ2_XXS) {
+        const uint8_t *b = row + (size_t) (i >> 8) * 66;
+        const int e = i & 255, ib = e >> 5, l = (e >> 3) & 3, j = e & 7;
+        const uint32_t a1 = (uint32_t) ld_u16(b + 6 + 8 * ib) | ((uint32_t) ld_u16(b + 8 + 8 * ib) << 16);
+        const float db = h2f(ld_u16(b)) * (0.5f + (float) (a1 >> 28)) * 0.25f;
+        const uint2 gr = grid[b[2 + 8 * ib + l]];
+        const float gv = (float) (((j < 4 ? gr.x : gr.y) >> (8 * (j & 3))) & 0xff);
+        v = (db * gv) * ((ksign((a1 >> (7 * l)) & 127) >> j) & 1 ? -1.0f : 1.0f);
     } else if (type == Q8_0) {
         const uint8_t *b = row + (size_t) (i >> 5) * 34;
         v = h2f(ld_u16(b)) * (float) (int8_t) b[2 + (i & 31)];
@@ -425,7 +435,7 @@ __global__ __launch_bounds__(256) void k_block_ints(const uint8_t *__restrict__ 
     __shared__ __align__(16) uint8_t y0[8 * Q8_0_LDS * 32];
     constexpr int BE = block_elems(T), VT = vec_dot_type(T);
     const int ng = n / 256, nb = n / BE;
-    if (T == IQ2_XS) expand_iq2xs_grid(grid);
+    if constexpr (iq2_type(T)) expand_iq2_grid<T>(grid);
     if (VT == Q8_0)   // repack up to 256 Q8_0 blocks of the activation row into the padded layout
         for (int i = threadIdx.x; i < nb && i < 256; i += blockDim.x) {
             const uint8_t *s = xq + i * Q8_0_BYTES;
@@ -439,7 +449,7 @@ __global__ __launch_bounds__(256) void k_block_ints(const uint8_t *__restrict__ 
     const int row = g / ng, gi = g % ng;
     Item<T> it;
     it.load(rows + row * row_bytes + (size_t) gi * (256 / BE) * block_bytes(T), L);
-    if constexpr (T == IQ2_XS) it.grid = grid;
+    if constexpr (iq2_type(T)) it.grid = grid;
     int si, sm;
     if constexpr (block_elems(T) == 32) {
         it.ints(y0 + (8 * gi + L) * Q8_0_LDS, L, si, sm);

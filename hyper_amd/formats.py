@@ -5,7 +5,8 @@ Block sizes follow src/gguf.cpp:43-82; layouts follow the reference's deq8<T> (s
   Q5_K 176 B: d, dmin, scales[12] @4, qh[32] @16, qs[128] @48
   Q6_K 210 B: ql[128] @0, qh[64] @128, scales int8[16] @192, d f16 @208
   IQ4_NL 18 B per 32: d f16, qs[16];  IQ4_XS 136 B: d, scales_h u16 @2, scales_l[4] @4, qs[128] @8
-  IQ2_XS 74 B: d f16, qs u16[32] @2, scales[8] @66;  Q8_K 292 B: f32 d, qs[256], i16 bsums[16];
+  IQ2_XS 74 B: d f16, qs u16[32] @2, scales[8] @66;  IQ2_XXS 66 B: d f16, 8 x (grid rows u8[4], signs|scale u32) @2
+  Q8_K 292 B: f32 d, qs[256], i16 bsums[16];
   Q8_0 34 B per 32: d f16, qs int8[32] (activation rows, and expert weights)
 Synthetic blocks (the workloads' generators): uniformly random quant bytes (which gives uniform nibbles,
 6-bit scales/mins, grid indices and sign bits), fp16 scale fields drawn uniformly from a stated range.
@@ -25,13 +26,14 @@ class GType(IntEnum):
     Q5_K = 13
     Q6_K = 14
     Q8_K = 15
+    IQ2_XXS = 16
     IQ2_XS = 17
     IQ4_NL = 20
     IQ4_XS = 23
 
 
 _BYTES = {GType.Q8_0: 34, GType.Q4_K: 144, GType.Q5_K: 176, GType.Q6_K: 210, GType.Q8_K: 292,
-          GType.IQ2_XS: 74, GType.IQ4_NL: 18, GType.IQ4_XS: 136}
+          GType.IQ2_XXS: 66, GType.IQ2_XS: 74, GType.IQ4_NL: 18, GType.IQ4_XS: 136}
 _ELEMS = {GType.Q8_0: 32, GType.IQ4_NL: 32}
 
 
@@ -58,7 +60,7 @@ def q8_row_bytes(vt, n: int) -> int:
 
 # fp16 scale fields per type: byte offsets inside the block
 _F16_FIELDS = {GType.Q4_K: (0, 2), GType.Q5_K: (0, 2), GType.Q6_K: (208,), GType.IQ4_NL: (0,), GType.Q8_0: (0,),
-               GType.IQ4_XS: (0,), GType.IQ2_XS: (0,)}
+               GType.IQ4_XS: (0,), GType.IQ2_XS: (0,), GType.IQ2_XXS: (0,)}
 
 
 def random_blocks(t, nblocks: int, gen: torch.Generator, device, d_range=(1e-4, 4e-3)) -> torch.Tensor:

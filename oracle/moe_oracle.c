@@ -23,6 +23,7 @@ size_t or_block_bytes(int type) {
     case OR_Q6_K: return 210;
     case OR_Q8_K: return 292;
     case OR_IQ2_XS: return 74;
+    case OR_IQ2_XXS: return 66;
     case OR_IQ4_NL: return 18;
     case OR_IQ4_XS: return 136;
     default: return 0;
@@ -31,7 +32,7 @@ size_t or_block_bytes(int type) {
 int or_block_elems(int type) {
     switch (type) {
     case OR_Q8_0: case OR_IQ4_NL: return 32;
-    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_Q8_K: case OR_IQ2_XS: case OR_IQ4_XS: return 256;
+    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_Q8_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: return 256;
     default: return 0;
     }
 }
@@ -40,7 +41,7 @@ int or_block_elems(int type) {
 int or_vec_dot_type(int type) {
     switch (type) {
     case OR_IQ4_NL: case OR_Q8_0: return OR_Q8_0;
-    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ4_XS: return OR_Q8_K;
+    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: return OR_Q8_K;
     default: return -1;
     }
 }
@@ -52,14 +53,22 @@ static const int8_t kv_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1,
 static const uint16_t iq2xs_code[512] = {
 #include "../hyper_amd/csrc/iq2xs_grid.inc"
 };
-static uint8_t iq2xs_rows[512][8];
+/* IQ2_XXS codebook: 256 rows, the same coding (values of src/iq_grids.h:14-79) */
+static const uint16_t iq2xxs_code[256] = {
+#include "../hyper_amd/csrc/iq2xxs_grid.inc"
+};
+static uint8_t iq2xs_rows[512][8], iq2xxs_rows[256][8];
 static int iq2xs_ready = 0;
-static void iq2xs_init(void) {
+static void iq2xs_init(void) {   /* both IQ2 codebooks */
     if (__atomic_load_n(&iq2xs_ready, __ATOMIC_ACQUIRE)) return;
     static const uint8_t lv[3] = {8, 25, 43};
     for (int i = 0; i < 512; ++i) {
         unsigned c = iq2xs_code[i];
         for (int j = 0; j < 8; ++j) { iq2xs_rows[i][j] = lv[c % 3]; c /= 3; }
+    }
+    for (int i = 0; i < 256; ++i) {
+        unsigned c = iq2xxs_code[i];
+        for (int j = 0; j < 8; ++j) { iq2xxs_rows[i][j] = lv[c % 3]; c /= 3; }
     }
     __atomic_store_n(&iq2xs_ready, 1, __ATOMIC_RELEASE);
 }
@@ -222,6 +231,16 @@ static inline int iq2xs_q(const uint8_t *b, int e) {
     const int g = iq2xs_rows[q & 511][j];
     return (ksign(q >> 9) >> j) & 1 ? -g : g;
 }
+/* IQ2_XXS (src/kernels4.cu:578-589): 32-group ib is two words at 2 + 8 ib -- grid rows (byte l of the first) and
+   4 x 7 sign bits with the 4-bit scale in bits 28..31 (the second) */
+static inline unsigned iq2xxs_a1(const uint8_t *b, int ib) {
+    return (unsigned) b[6 + 8 * ib] | ((unsigned) b[7 + 8 * ib] << 8) | ((unsigned) b[8 + 8 * ib] << 16) | ((unsigned) b[9 + 8 * ib] << 24);
+}
+static inline int iq2xxs_q(const uint8_t *b, int e) {   /* signed grid value of element e */
+    const int ib = e >> 5, l = (e >> 3) & 3, j = e & 7;
+    const int g = iq2xxs_rows[b[2 + 8 * ib + l]][j];
+    return (ksign((iq2xxs_a1(b, ib) >> (7 * l)) & 127) >> j) & 1 ? -g : g;
+}
 static inline int iq2xs_sc(const uint8_t *b, int e) {
     const int ib = e >> 5, l = (e >> 3) & 3;
     return (b[66 + ib] >> (4 * (l >> 1))) & 0xF;
@@ -262,6 +281,13 @@ int or_dequant_row(int type, const uint8_t *row, int n, float *out) {
             for (int e = 0; e < 256; ++e) {
                 const float db = h2f(b) * (0.5f + (float) iq2xs_sc(b, e)) * 0.25f;
                 const int q = iq2xs_q(b, e);
+                o[e] = (db * (float) (q < 0 ? -q : q)) * (q < 0 ? -1.0f : 1.0f);
+            }
+            break;
+        case OR_IQ2_XXS:
+            for (int e = 0; e < 256; ++e) {
+                const float db = h2f(b) * (0.5f + (float) (iq2xxs_a1(b, e >> 5) >> 28)) * 0.25f;
+                const int q = iq2xxs_q(b, e);
                 o[e] = (db * (float) (q < 0 ? -q : q)) * (q < 0 ? -1.0f : 1.0f);
             }
             break;
@@ -327,6 +353,13 @@ static void block_ints_scalar(int type, const uint8_t *b, const uint8_t *y, int3
         break;
     case OR_Q8_0:
         for (int l = 0; l < 32; ++l) si += (int8_t) b[2 + l] * q8[l];
+        break;
+    case OR_IQ2_XXS:   /* ggml's vec_dot_iq2_xxs_q8_K: sum_ib (2 sc + 1) sum_32 grid sign y */
+        for (int ib = 0; ib < 8; ++ib) {
+            int32_t s = 0;
+            for (int l = 0; l < 32; ++l) s += iq2xxs_q(b, 32 * ib + l) * q8[32 * ib + l];
+            si += (2 * (int) (iq2xxs_a1(b, ib) >> 28) + 1) * s;
+        }
         break;
     default: break;
     }
@@ -405,7 +438,7 @@ static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *su
 
 static int dot_ok(int type) {
     return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_IQ4_XS || type == OR_IQ2_XS || type == OR_IQ4_NL ||
-           type == OR_Q8_0;
+           type == OR_Q8_0 || type == OR_IQ2_XXS;
 }
 int or_block_ints(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ) {
     if (!dot_ok(type) || n % or_block_elems(type)) return -1;
@@ -436,7 +469,7 @@ static float row_dot(int type, const uint8_t *row, const uint8_t *xq, int n) {
         switch (type) {
         case OR_Q4_K: case OR_Q5_K: t = fmaf(h2f(b), (float) si, -(h2f(b + 2) * (float) sm)); break;
         case OR_Q6_K: t = h2f(b + 208) * (float) si; break;
-        case OR_IQ2_XS: t = (h2f(b) * 0.125f) * (float) si; break;
+        case OR_IQ2_XS: case OR_IQ2_XXS: t = (h2f(b) * 0.125f) * (float) si; break;
         default: t = h2f(b) * (float) si; break;        /* IQ4_XS, IQ4_NL, Q8_0 */
         }
         acc = fmaf(xd, t, acc);

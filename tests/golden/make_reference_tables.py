@@ -1,7 +1,8 @@
 """Write tests/golden/reference_tables.json: SHA-256 digests of the codebooks the reference carries, so the
 tests can check this repository's copies without reading the reference at run time.
 
-  iq2xs_grid: src/iq_grids.h:80-209 (g_iq2xs_grid, 512 x u64, little-endian bytes)
+  iq2xs_grid:  src/iq_grids.h:80-209 (g_iq2xs_grid, 512 x u64, little-endian bytes)
+  iq2xxs_grid: src/iq_grids.h:14-79  (g_iq2xxs_grid, 256 x u64, little-endian bytes)
   ksigns:     src/iq_grids.h:4-13   (g_ksigns_iq2xs, 128 bytes)
   iq4nl:      src/kernels4.cu:546   (g_iq4nl, 16 x int8)
 
@@ -24,13 +25,15 @@ def array(text, name):
 grids = (ref / "src/iq_grids.h").read_text()
 k4 = (ref / "src/kernels4.cu").read_text()
 grid = array(grids, "g_iq2xs_grid")
+grid2 = array(grids, "g_iq2xxs_grid")
 ks = array(grids, "g_ksigns_iq2xs")
 kv = array(k4, "g_iq4nl")
 out = {
     "iq2xs_grid_sha256": hashlib.sha256(b"".join(v.to_bytes(8, "little") for v in grid)).hexdigest(),
+    "iq2xxs_grid_sha256": hashlib.sha256(b"".join(v.to_bytes(8, "little") for v in grid2)).hexdigest(),
     "ksigns_sha256": hashlib.sha256(bytes(ks)).hexdigest(),
     "iq4nl_sha256": hashlib.sha256(bytes(v & 0xFF for v in kv)).hexdigest(),
-    "sizes": {"iq2xs_grid": len(grid), "ksigns": len(ks), "iq4nl": len(kv)},
+    "sizes": {"iq2xs_grid": len(grid), "iq2xxs_grid": len(grid2), "ksigns": len(ks), "iq4nl": len(kv)},
 }
 (Path(__file__).resolve().parent / "reference_tables.json").write_text(json.dumps(out, indent=1) + "\n")
 print(out)

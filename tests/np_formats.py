@@ -93,6 +93,19 @@ def iq2xs(b, grid_rows, ksigns):
     return dict(q=q, sc=2 * sc + 1, m=None, gsize=16, d=f16(b[:, 0:2]))
 
 
+def iq2xxs(b, grid_rows, ksigns):
+    """grid_rows: [256, 8] codebook bytes, ksigns: [128] sign bytes.  32-group ib: grid rows at bytes 2 + 8 ib + l,
+    then a little-endian word with the four 7-bit sign indices (bits 7 l ..) and the 4-bit scale (bits 28 ..)."""
+    b = b.reshape(-1, 66)
+    w = b[:, 2:66].reshape(-1, 8, 8)
+    g = grid_rows[w[:, :, 0:4].astype(np.int64)].astype(np.int64)                   # [nb, 8, 4, 8]
+    a1 = np.ascontiguousarray(w[:, :, 4:8]).view(np.uint32).astype(np.int64).reshape(-1, 8)
+    sgn = ksigns[np.stack([(a1 >> (7 * l)) & 127 for l in range(4)], axis=2)].astype(np.int64)
+    bits = (sgn[..., None] >> np.arange(8)) & 1
+    q = np.where(bits == 1, -g, g).reshape(-1, 256)
+    return dict(q=q, sc=2 * (a1 >> 28) + 1, m=None, gsize=32, d=f16(b[:, 0:2]))
+
+
 def q8k(b):
     b = b.reshape(-1, 292)
     return dict(d=b[:, 0:4].copy().view(np.float32).reshape(-1), qs=b[:, 4:260].view(np.int8).astype(np.int64),
@@ -113,6 +126,7 @@ def decode(t, b, grid_rows=None, ksigns=None):
     if t == 20: return iq4nl(b)
     if t == 8: return q8_0w(b)
     if t == 17: return iq2xs(b, grid_rows, ksigns)
+    if t == 16: return iq2xxs(b, grid_rows, ksigns)
     raise ValueError(t)
 
 
@@ -135,7 +149,7 @@ def dequant(t, b, grid_rows=None, ksigns=None):
         return (q.astype(np.float32) * d).astype(np.float32)
     if t == 8:
         return (d * q.astype(np.float32)).astype(np.float32)
-    if t == 17:
+    if t in (16, 17):
         db = (d * (np.float32(0.5) + ((sc - 1) / 2).astype(np.float32))) * np.float32(0.25)
         return ((db * np.abs(q).astype(np.float32)) * np.where(q < 0, np.float32(-1), np.float32(1))).astype(np.float32)
     raise ValueError(t)

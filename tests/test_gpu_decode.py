@@ -61,6 +61,8 @@ ROUTE_GU_CASES = [
     (GType.Q4_K, GType.Q6_K, 64, 2560, 512, 8, 4, False),         # down: 3 rows a wave, the last block's rows past n
     (GType.Q8_0, GType.Q8_0, 32, 2048, 768, 8, 2, True),
     (GType.Q8_0, GType.Q4_K, 24, 1024, 512, 6, 3, False),
+    (GType.IQ2_XXS, GType.IQ2_XXS, 16, 7168, 2048, 6, 2, True),
+    (GType.IQ2_XXS, GType.IQ2_XS, 20, 2048, 768, 8, 3, False),
 ]
 
 

@@ -145,6 +145,8 @@ DECODE_CASES = [
     (GType.IQ2_XS, GType.IQ2_XS, 7168, 2048, 6, 2),
     (GType.Q8_0, GType.Q8_0, 2048, 768, 8, 2),
     (GType.Q8_0, GType.Q6_K, 2048, 512, 4, 3),
+    (GType.IQ2_XXS, GType.IQ2_XXS, 7168, 2048, 6, 2),
+    (GType.IQ2_XXS, GType.IQ2_XS, 2048, 768, 8, 3),
 ]
 
 
@@ -209,6 +211,8 @@ GEMM_CASES = [
     (GType.IQ4_NL, GType.IQ4_NL, 4096, 1536, 8, 4),
     (GType.IQ4_NL, GType.IQ4_NL, 2048, 512, 8, 50),
     (GType.Q8_0, GType.Q8_0, 2048, 768, 8, 40),
+    (GType.IQ2_XXS, GType.IQ2_XXS, 7168, 2048, 6, 8),
+    (GType.IQ2_XXS, GType.Q6_K, 2048, 768, 8, 60),
     (GType.Q4_K, GType.Q8_0, 1024, 512, 4, 30),     # a K-quant gate/up with a Q8_0 down (Q8_K x, Q8_0 hidden)
     (GType.Q4_K, GType.Q6_K, 2048, 768, 1, 100),    # k = 1: the pair is the token (reciprocal 2^32)
     (GType.Q4_K, GType.Q6_K, 1024, 512, 3, 90),     # odd k: the pair-to-token multiply-high

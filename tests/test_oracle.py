@@ -44,6 +44,25 @@ def iq2xs_rows() -> np.ndarray:
     return rows
 
 
+def iq2xxs_rows() -> np.ndarray:
+    """The IQ2_XXS codebook as the kernels and the oracle expand it from iq2xxs_grid.inc."""
+    text = (Path(__file__).resolve().parents[1] / "hyper_amd/csrc/iq2xxs_grid.inc").read_text()
+    body = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("//"))
+    codes = [int(v) for v in body.replace(",", " ").split() if v.isdigit()]
+    assert len(codes) == 256
+    lv = np.array([8, 25, 43], np.uint8)
+    rows = np.zeros((256, 8), np.uint8)
+    for i, c in enumerate(codes):
+        for j in range(8):
+            rows[i, j] = lv[c % 3]
+            c //= 3
+    return rows
+
+
+def grid_for(t):
+    return iq2xxs_rows() if GType(t) == GType.IQ2_XXS else iq2xs_rows()
+
+
 def ksigns() -> np.ndarray:
     return np.array([i | ((bin(i).count("1") & 1) << 7) for i in range(128)], np.uint8)
 
@@ -51,6 +70,7 @@ def ksigns() -> np.ndarray:
 def test_codebooks_match_reference():
     rows = iq2xs_rows()
     assert hashlib.sha256(rows.tobytes()).hexdigest() == TABLES["iq2xs_grid_sha256"]
+    assert hashlib.sha256(iq2xxs_rows().tobytes()).hexdigest() == TABLES["iq2xxs_grid_sha256"]
     assert hashlib.sha256(ksigns().tobytes()).hexdigest() == TABLES["ksigns_sha256"]
     assert hashlib.sha256(nf.KV_IQ4NL.astype(np.int8).tobytes()).hexdigest() == TABLES["iq4nl_sha256"]
     assert all(bin(int(s)).count("1") % 2 == 0 for s in ksigns())   # every sign byte has an even bit count
@@ -214,6 +234,35 @@ def test_iq4nl_known_answer_positions():
     assert (orc.dequant_row(GType.IQ4_NL, blk.reshape(-1), 64) == want).all()
 
 
+def test_iq2xxs_known_answer_positions():
+    """IQ2_XXS (src/kernels4.cu:578-589): 32-group ib's grid rows are bytes 2 + 8 ib + l, its word at 6 + 8 ib holds the
+    four 7-bit sign indices (bits 7 l ..) and the 4-bit scale (bits 28 ..); value = d (0.5 + sc) / 4 * grid * sign.
+    Rows fixed by the reference's table: row 0 is all 8s, row 1 = 0x080808080808082b (byte 0 = 43).  With d = 1:
+    group 0 takes rows 0, 1, 0, 0 and sign index 1 on 8-group 1 (ksign(1) = 0x81: elements 0 and 7 negated),
+    scale 0 (db = 1/8); group 1 takes row 0 with scale 15 (db = 3.875); the rest row 0, scale 0."""
+    rows = iq2xxs_rows()
+    assert list(rows[0]) == [8] * 8 and list(rows[1]) == [43] + [8] * 7
+    blk = np.zeros(66, np.uint8)
+    blk[0:2] = _f16b(1.0)
+    blk[2 + 1] = 1                                             # group 0, 8-group 1: grid row 1
+    blk[6:10] = np.frombuffer(np.uint32(1 << 7).tobytes(), np.uint8)     # group 0: sign index 1 on 8-group 1
+    blk[14:18] = np.frombuffer(np.uint32(15 << 28).tobytes(), np.uint8)  # group 1: scale 15
+    want = np.ones(256, np.float32)
+    want[8:16] = [-43 / 8, 1, 1, 1, 1, 1, 1, -1]
+    want[32:64] = 31.0
+    got = orc.dequant_row(GType.IQ2_XXS, blk, 256)
+    assert (got == want).all(), np.nonzero(got != want)
+    x = np.arange(256, dtype=np.float32) % 7 - 3.0            # small integers: Q8_K of x is exact up to its scale
+    xq = orc.quantize(GType.Q8_K, x)
+    q8 = xq[4:260].view(np.int8).astype(np.int64)
+    ints = (want * 8).astype(np.int64)                          # grid * sign at scale 0; group 1's rows stay 8s
+    ints[32:64] = 8
+    scale = np.array([1] + [31] + [1] * 6, np.int64)            # 2 sc + 1 per 32-group
+    si, sm = orc.block_ints(GType.IQ2_XXS, blk, xq, 256)
+    assert int(si[0]) == int(sum(scale[g] * (ints[32 * g:32 * g + 32] @ q8[32 * g:32 * g + 32]) for g in range(8)))
+    assert not sm.any()
+
+
 def test_q8_0_weight_known_answers():
     """Q8_0 weights (src/kernels4.cu:421-714, deq8: d * qs[j]): value j of a block is d * (int8) qs[j] in place, and
     against a Q8_0 activation block the integer is sum_j qs[j] y[j] (ggml's vec_dot_q8_0_q8_0), folded as
@@ -258,7 +307,7 @@ def test_q8k_known_answers():
 
 # ------------------------------------------------------------------ block decoding
 
-ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ4_NL, GType.Q8_0]
+ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.IQ4_NL, GType.Q8_0]
 
 
 def blocks(t, nb, seed):
@@ -270,7 +319,7 @@ def test_dequant_matches_numpy_decoder(t):
     b = blocks(t, 64, 100 + int(t))
     n = 64 * block_elems(t)
     got = orc.dequant_row(t, b.reshape(-1), n)
-    ref = nf.dequant(t, b, iq2xs_rows(), ksigns()).reshape(-1)
+    ref = nf.dequant(t, b, grid_for(t), ksigns()).reshape(-1)
     assert (got == ref).all(), f"{int((got != ref).sum())} values differ"
 
 
@@ -340,7 +389,7 @@ def test_block_ints_brute_force(t):
         xq = orc.quantize(vt, x)
         for r in range(rows.shape[0]):
             si, sm = orc.block_ints(t, rows[r], xq, n)
-            bsi, bsm = nf.block_ints(t, rows[r], xq, iq2xs_rows(), ksigns())
+            bsi, bsm = nf.block_ints(t, rows[r], xq, grid_for(t), ksigns())
             assert (si == bsi).all() and (sm == bsm).all(), f"{t.name} {name} row {r}"
 
 
@@ -371,7 +420,7 @@ def test_row_dot_equals_fp64_of_dequantized_operands(t):
     xq = orc.quantize(vt, x)
     xd = orc.dequant_row(vt, xq, n).astype(np.float64)
     for r in range(8):
-        w = nf.dequant(t, rows[r], iq2xs_rows(), ksigns()).reshape(-1).astype(np.float64)
+        w = nf.dequant(t, rows[r], grid_for(t), ksigns()).reshape(-1).astype(np.float64)
         ref = float(w @ xd)
         got = float(orc.row_dot(t, rows[r], xq, n))
         scale = float(np.abs(w).dot(np.abs(xd)))
