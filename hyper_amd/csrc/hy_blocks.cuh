@@ -21,16 +21,18 @@ __device__ __forceinline__ void scale_min_k4(uint32_t s0, uint32_t s1, uint32_t 
     if (j < 4) { sc = byte_of(v, j) & 63; mn = byte_of(v, j + 4) & 63; }
     else { sc = (byte_of(v, j + 4) & 0xF) | ((byte_of(v, j - 4) >> 6) << 4); mn = (byte_of(v, j + 4) >> 4) | ((byte_of(v, j) >> 6) << 4); }
 }
-// four packed nibble indices (bytes 0..15) -> the IQ4_NL codebook values as packed int8
-__device__ __forceinline__ uint32_t kv4(uint32_t idx) {
-    const uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;
-    // (bytes: -127 -104 -83 -65 | -49 -35 -22 -10 | 1 13 25 38 | 53 69 89 113)
+// four packed nibble indices (bytes 0..15) -> entries of a 16-byte int8 codebook T0..T3 as packed int8
+__device__ __forceinline__ uint32_t kv16(uint32_t idx, uint32_t T0, uint32_t T1, uint32_t T2, uint32_t T3) {
     const uint32_t sel = idx & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
     // 0xFF in the bytes whose index is 8..15: selector idx >> 1 picks a byte of 0xFFFFFFFF (4..7) or of 0 (0..3)
     const uint32_t m = __builtin_amdgcn_perm(0xFFFFFFFFu, 0u, (idx >> 1) & 0x07070707u);
     return (hi & m) | (lo & ~m);
 }
+// the IQ4_NL codebook (bytes: -127 -104 -83 -65 | -49 -35 -22 -10 | 1 13 25 38 | 53 69 89 113)
+__device__ __forceinline__ uint32_t kv4(uint32_t idx) { return kv16(idx, 0xBFAD9881u, 0xF6EADDCFu, 0x26190D01u, 0x71594535u); }
+// the MXFP4 codebook, E2M1 values doubled (src/kernels4.cu:551; bytes: 0 1 2 3 | 4 6 8 12 | 0 -1 -2 -3 | -4 -6 -8 -12)
+__device__ __forceinline__ uint32_t kvfp4(uint32_t idx) { return kv16(idx, 0x03020100u, 0x0C080604u, 0xFDFEFF00u, 0xF4F8FAFCu); }
 // IQ2 signs: 8 sign bits -> two words whose bytes are 0xFF where negated; value = (g ^ M) + (M & 1)
 __device__ __forceinline__ uint32_t spread4(uint32_t b4) { return (b4 * 0x00204081u) & 0x01010101u; }
 __device__ __forceinline__ uint32_t apply_sign(uint32_t g, uint32_t b4) {
@@ -254,6 +256,29 @@ template <> struct Item<Q8_0> {
         si = dot32(ya); sm = 0;
     }
     __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
+};
+// MXFP4 (17 B: e, qs[16]) against Q8_0, src/kernels4.cu:569-577: lane L takes the item's block L whole, value j < 16 =
+// kv[qs[j] & 15], 16 + j = kv[qs[j] >> 4], scaled by e8m0_half(e) (ggml's vec_dot_mxfp4_q8_0 integers:
+// sumi = sum_32 kv q8).  Block L's qs start at 17 L + 1, at every offset mod 4; the spans are 8-byte aligned
+// (136 bytes), so the misaligned loads end within the block or at most 3 bytes into the next (L < 7; for L = 7 the
+// qs end the span, dword-aligned).
+template <> struct Item<MXFP4> {
+    uint4 qs;
+    uint32_t e;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) { qs = load16_a2_nb(b + 17 * L + 1); e = b[17 * L]; }
+    __device__ __forceinline__ int dot32(const uint32_t (&ya)[8]) const {
+        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { s = sdot4(kvfp4(q[i] & 0x0F0F0F0Fu), ya[i], s); s = sdot4(kvfp4((q[i] >> 4) & 0x0F0F0F0Fu), ya[4 + i], s); }
+        return s;
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int, int &si, int &sm) const {
+        const uint32_t *yw = (const uint32_t *) (y + 4);
+        const uint32_t ya[8] = {yw[0], yw[1], yw[2], yw[3], yw[4], yw[5], yw[6], yw[7]};
+        si = dot32(ya); sm = 0;
+    }
+    __device__ __forceinline__ float tval(int si, int) const { return e8m0_half(e) * (float) si; }
 };
 
 // expand an IQ2 codebook (base-3 codes: IQ2_XS 512 rows, IQ2_XXS 256) into rows x 8 bytes of LDS, followed by the

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -25,7 +26,7 @@ int check_launch(const char *what) {
     return HY_OK;
 }
 
-static bool dot_type(int t) { return t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ2_XXS || t == IQ4_NL || t == Q8_0; }
+static bool dot_type(int t) { return t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ2_XXS || t == IQ4_NL || t == Q8_0 || t == MXFP4; }
 static bool gemm_type(int t) { return dot_type(t); }
 
 // the expert layer descriptor is usable: types, sizes, pointers, row sizes that the kernels assume
@@ -358,7 +359,13 @@ int hy_block_ints(int type, const uint8_t *rows, size_t row_bytes, int nrows, co
                   hipStream_t s) {
     if (!rows || !xq || !sumi || !summ || nrows < 0) { set_error("hy_block_ints: bad argument"); return HY_EINVAL; }
     if (!dot_type(type)) { set_error("hy_block_ints: type %d", type); return HY_EUNSUPPORTED_TYPE; }
-    if (n <= 0 || n % 256 || row_bytes % 2 || ((uintptr_t) rows & 15) || ((uintptr_t) xq & 3)) { set_error("hy_block_ints: n %% 256 != 0 or unaligned"); return HY_EBAD_SHAPE; }
+    // rows keep the alignment their 256-value spans have in the uploaded layout (the largest power of two dividing
+    // the span, at most 16): the item loads of the 17- and 18-byte block types count on it to end within the span
+    const int sb = span_bytes(type), ra = std::min(16, sb & -sb);
+    if (n <= 0 || n % 256 || row_bytes % ra || ((uintptr_t) rows & 15) || ((uintptr_t) xq & 3)) {
+        set_error("hy_block_ints: n %% 256 != 0, rows unaligned or row_bytes not a multiple of %d", ra);
+        return HY_EBAD_SHAPE;
+    }
     return launch_block_ints(type, rows, row_bytes, nrows, xq, n, sumi, summ, s);
 }
 

@@ -17,22 +17,22 @@
 namespace hy {
 
 // GGUF type ids (src/gguf.h:13-18)
-enum GT : int { Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, IQ2_XXS = 16, IQ2_XS = 17, IQ4_NL = 20, IQ4_XS = 23 };
+enum GT : int { Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, IQ2_XXS = 16, IQ2_XS = 17, IQ4_NL = 20, IQ4_XS = 23, MXFP4 = 39 };
 
 constexpr int Q8K_BYTES = 292;   // float d; int8 qs[256]; int16 bsums[16]
 constexpr int Q8_0_BYTES = 34;   // fp16 d; int8 qs[32]
 
 __host__ __device__ constexpr int block_bytes(int t) {
     return t == Q4_K ? 144 : t == Q5_K ? 176 : t == Q6_K ? 210 : t == IQ4_XS ? 136 : t == IQ2_XS ? 74 : t == IQ2_XXS ? 66
-         : t == IQ4_NL ? 18 : t == Q8_0 ? 34 : t == Q8_K ? 292 : 0;
+         : t == IQ4_NL ? 18 : t == Q8_0 ? 34 : t == MXFP4 ? 17 : t == Q8_K ? 292 : 0;
 }
 __host__ __device__ constexpr int block_elems(int t) {
-    return (t == IQ4_NL || t == Q8_0) ? 32
+    return (t == IQ4_NL || t == Q8_0 || t == MXFP4) ? 32
          : (t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ2_XXS || t == Q8_K) ? 256 : 0;
 }
 // the IQ2 types: codebook rows and sign masks in LDS (expand_iq2_grid)
 __host__ __device__ constexpr bool iq2_type(int t) { return t == IQ2_XS || t == IQ2_XXS; }
-__host__ __device__ constexpr int vec_dot_type(int t) { return t == IQ4_NL || t == Q8_0 ? Q8_0 : Q8_K; }
+__host__ __device__ constexpr int vec_dot_type(int t) { return t == IQ4_NL || t == Q8_0 || t == MXFP4 ? Q8_0 : Q8_K; }
 
 // ------------------------------------------------------------------ scalar helpers
 
@@ -242,9 +242,9 @@ __device__ __forceinline__ uint4 load16_a2(const uint8_t *p) {
     v.x = h0 | (d1 << 16); v.y = (d1 >> 16) | (d2 << 16); v.z = (d2 >> 16) | (d3 << 16); v.w = (d3 >> 16) | (h4 << 16);
     return v;
 }
-// the same without a branch, for lanes whose alignments differ: four dwords from p & ~3 and a fifth when p is 2 mod 4
-// (else the fourth again), joined with v_alignbyte; reads at most p + 17, so the 2 bytes after the 16 must exist
-// whenever p is 2 mod 4
+// the same without a branch, for lanes whose alignments differ: four dwords from p & ~3 and a fifth when p is not
+// dword-aligned (else the fourth again), joined with v_alignbyte; any byte offset works (MXFP4's 17-byte blocks):
+// it reads up to the end of the dword holding p + 16, i.e. at most p + 19, which the caller keeps in the buffer
 __device__ __forceinline__ uint4 load16_a2_nb(const uint8_t *p) {
     const uint32_t sb = (uint32_t) ((uintptr_t) p & 3);
     const uint32_t *w = (const uint32_t *) (p - sb);
@@ -267,6 +267,14 @@ __device__ __constant__ const int8_t c_kv_iq4nl[16] = {-127, -104, -83, -65, -49
 __device__ __constant__ const uint16_t c_iq2xs_code[512] = {
 #include "iq2xs_grid.inc"
 };
+// MXFP4 block scale: an E8M0 exponent as 2^(e - 128), the half of 2^(e - 127) that pairs with the doubled fp4
+// codebook (ggml_e8m0_to_fp32_half; src/kernels4.cu:567-568): e < 2 gives the subnormals 2^-128, 2^-127
+__host__ __device__ inline float e8m0_half(uint32_t e) {
+    const uint32_t bits = e < 2 ? 0x00200000u << e : (e - 1) << 23;
+    float f;
+    __builtin_memcpy(&f, &bits, 4);
+    return f;
+}
 // IQ2_XXS codebook rows, the same coding (g_iq2xxs_grid, src/iq_grids.h:14-79)
 __device__ __constant__ const uint16_t c_iq2xxs_code[256] = {
 #include "iq2xxs_grid.inc"

@@ -106,7 +106,7 @@ int run_decode(const hy_moe_dev &m, const float *W_r, int rows, const float *x, 
     }
     // down types with a Q8_0 partner: gate/up also writes the hidden as Q8_0 rows, which the down kernel reads (shapes
     // beyond either kernel's limits take the fp32 hidden)
-    uint8_t *hq = (m.tg == IQ4_NL || m.tg == Q8_0) && dec_down_takes_q8(m, k) ? ws + L.hq : nullptr;
+    uint8_t *hq = vec_dot_type(m.tg) == Q8_0 && dec_down_takes_q8(m, k) ? ws + L.hq : nullptr;
     rc = launch_route_gate_up(m, logits, rows, E, k, xq, ids, wts, gate_logit ? sg : nullptr, h, nt, s, hq);
     if (rc == HY_EUNSUPPORTED_TYPE && hq) {
         hq = nullptr;

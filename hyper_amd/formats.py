@@ -8,8 +8,10 @@ Block sizes follow src/gguf.cpp:43-82; layouts follow the reference's deq8<T> (s
   IQ2_XS 74 B: d f16, qs u16[32] @2, scales[8] @66;  IQ2_XXS 66 B: d f16, 8 x (grid rows u8[4], signs|scale u32) @2
   Q8_K 292 B: f32 d, qs[256], i16 bsums[16];
   Q8_0 34 B per 32: d f16, qs int8[32] (activation rows, and expert weights)
+  MXFP4 17 B per 32: e (E8M0 exponent, scale 2^(e - 128)) @0, qs[16] @1
 Synthetic blocks (the workloads' generators): uniformly random quant bytes (which gives uniform nibbles,
-6-bit scales/mins, grid indices and sign bits), fp16 scale fields drawn uniformly from a stated range.
+6-bit scales/mins, grid indices and sign bits), fp16 scale fields drawn uniformly from a stated range, E8M0
+exponents uniformly from those whose scale 2^(e - 128) lies within a power of two of that range.
 """
 from dataclasses import dataclass, field
 from enum import IntEnum
@@ -30,11 +32,12 @@ class GType(IntEnum):
     IQ2_XS = 17
     IQ4_NL = 20
     IQ4_XS = 23
+    MXFP4 = 39
 
 
 _BYTES = {GType.Q8_0: 34, GType.Q4_K: 144, GType.Q5_K: 176, GType.Q6_K: 210, GType.Q8_K: 292,
-          GType.IQ2_XXS: 66, GType.IQ2_XS: 74, GType.IQ4_NL: 18, GType.IQ4_XS: 136}
-_ELEMS = {GType.Q8_0: 32, GType.IQ4_NL: 32}
+          GType.IQ2_XXS: 66, GType.IQ2_XS: 74, GType.IQ4_NL: 18, GType.IQ4_XS: 136, GType.MXFP4: 17}
+_ELEMS = {GType.Q8_0: 32, GType.IQ4_NL: 32, GType.MXFP4: 32}
 
 
 def block_bytes(t) -> int:
@@ -47,7 +50,7 @@ def block_elems(t) -> int:
 
 def vec_dot_type(t) -> GType:
     """Activation partner type (ggml vec_dot_type; src/cpu_moe.cpp:711-715)."""
-    return GType.Q8_0 if GType(t) in (GType.IQ4_NL, GType.Q8_0) else GType.Q8_K
+    return GType.Q8_0 if GType(t) in (GType.IQ4_NL, GType.Q8_0, GType.MXFP4) else GType.Q8_K
 
 
 def row_bytes(t, n: int) -> int:
@@ -60,12 +63,15 @@ def q8_row_bytes(vt, n: int) -> int:
 
 # fp16 scale fields per type: byte offsets inside the block
 _F16_FIELDS = {GType.Q4_K: (0, 2), GType.Q5_K: (0, 2), GType.Q6_K: (208,), GType.IQ4_NL: (0,), GType.Q8_0: (0,),
-               GType.IQ4_XS: (0,), GType.IQ2_XS: (0,), GType.IQ2_XXS: (0,)}
+               GType.IQ4_XS: (0,), GType.IQ2_XS: (0,), GType.IQ2_XXS: (0,), GType.MXFP4: ()}
+# E8M0 exponent bytes per type
+_E8M0_FIELDS = {GType.MXFP4: (0,)}
 
 
 def random_blocks(t, nblocks: int, gen: torch.Generator, device, d_range=(1e-4, 4e-3)) -> torch.Tensor:
     """nblocks random blocks of type t as a uint8 tensor [nblocks, block_bytes]: uniformly random bytes,
-    then every fp16 scale field drawn uniformly from d_range."""
+    then every fp16 scale field drawn uniformly from d_range and every E8M0 exponent uniformly from
+    128 + floor(log2 lo) .. 128 + ceil(log2 hi)."""
     t = GType(t)
     bb = block_bytes(t)
     blk = torch.randint(0, 256, (nblocks, bb), dtype=torch.uint8, generator=gen, device=device)
@@ -73,6 +79,9 @@ def random_blocks(t, nblocks: int, gen: torch.Generator, device, d_range=(1e-4, 
     for off in _F16_FIELDS[t]:
         d = torch.empty(nblocks, dtype=torch.float32, device=device).uniform_(lo, hi, generator=gen).to(torch.float16)
         blk[:, off:off + 2] = d.view(torch.uint8).view(nblocks, 2)
+    for off in _E8M0_FIELDS.get(t, ()):
+        elo, ehi = 128 + int(np.floor(np.log2(lo))), 128 + int(np.ceil(np.log2(hi)))
+        blk[:, off] = torch.randint(elo, ehi + 1, (nblocks,), dtype=torch.int32, generator=gen, device=device).to(torch.uint8)
     return blk
 
 

@@ -262,7 +262,7 @@ class MoeLayerRunner:
         # decode hands the hidden over as Q8_0 rows where the down type's partner is Q8_0, within the kernels' limits
         # (n <= 4096; k * ff / 32 <= 512 blocks and k * ff / 32 * 34 bytes <= 32 KiB per token)
         nbh = self.ff // 32
-        self.dec_hq = (router == "softmax" and L.tg in (GType.IQ4_NL, GType.Q8_0) and vec_dot_type(L.td) == GType.Q8_0
+        self.dec_hq = (router == "softmax" and vec_dot_type(L.tg) == GType.Q8_0 and vec_dot_type(L.td) == GType.Q8_0
                        and self.d <= 4096 and self.k * nbh <= 512
                        and self.k * nbh * 34 <= 32768 and self.E <= 1024)
         self._side = None   # the shared expert's decode stream, made on first use

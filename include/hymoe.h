@@ -9,7 +9,7 @@
  *   - every device pointer is caller-owned (the reference's callers own theirs as well); no entry point
  *     except hy_upload_experts allocates, and all are stream-ordered and free of host synchronisation;
  *   - activations reach the expert matrices as Q8 blocks (block_q8_K, 292 B per 256 values, or block_q8_0,
- *     34 B per 32 values for IQ4_NL and Q8_0 weights), the partner types of the reference's CPU path
+ *     34 B per 32 values for IQ4_NL, Q8_0 and MXFP4 weights), the partner types of the reference's CPU path
  *     (src/cpu_moe.cpp:711-715), and every block dot product is an exact integer.
  *
  * Results are bit-identical to the CPU oracle of this repository (oracle/), which restates the reference's
@@ -35,10 +35,10 @@ enum {
 };
 
 /* GGUF type ids used by the path (src/gguf.h:13-18); expert weights: Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ2_XS, IQ4_NL,
-   IQ4_XS and Q8_0 (of src/kernels4.cu:1951-1971's list); Q8_K and Q8_0 as activation rows */
+   IQ4_XS, Q8_0 and MXFP4 (of src/kernels4.cu:1951-1971's list); Q8_K and Q8_0 as activation rows */
 enum {
     HY_Q8_0 = 8, HY_Q4_K = 12, HY_Q5_K = 13, HY_Q6_K = 14, HY_Q8_K = 15,
-    HY_IQ2_XXS = 16, HY_IQ2_XS = 17, HY_IQ4_NL = 20, HY_IQ4_XS = 23
+    HY_IQ2_XXS = 16, HY_IQ2_XS = 17, HY_IQ4_NL = 20, HY_IQ4_XS = 23, HY_MXFP4 = 39
 };
 
 /* Expert weights of one layer on the device (replaces MoeDev, src/kernels4.cuh:56-63): n_local experts,
@@ -261,7 +261,9 @@ int hy_moe_decode_noalloc(const hy_moe_dev *m, const float *W_r, int rows, const
 /* Test hooks.  One row of n weights dequantized by the kernels' block decoders (replaces deq_row_test,
    src/kernels4.cuh:181 / src/kernels4.cu:2036-2044); and the exact integers of every block of nrows weight rows
    (row stride row_bytes) against one Q8 activation row: sumi/summ [nrows][n / block_elems] (summ 0 for types
-   without mins) -- the per-block int32 dot products of the contract. */
+   without mins) -- the per-block int32 dot products of the contract.  rows is 16-byte aligned and row_bytes a
+   multiple of the alignment of the type's 256-value span (its largest power-of-two factor, at most 16: 8 for
+   MXFP4's 136 bytes, 2 for Q6_K's 210). */
 int hy_dequant_row(int type, const uint8_t *row, int n, float *out, hipStream_t s);
 int hy_block_ints(int type, const uint8_t *rows, size_t row_bytes, int nrows, const void *xq, int n, int32_t *sumi, int32_t *summ,
                   hipStream_t s);

@@ -80,6 +80,29 @@ def q8_0w(b):
                 d=f16(b[:, 0:2]))
 
 
+def e2m1_doubled(idx):
+    """Twice the value of an E2M1 (OCP MX fp4) code: sign bit 3, exponent bits 2-1 (bias 1), mantissa bit 0;
+    exponent 0 is subnormal (m / 2), else 2^(e - 1) (1 + m / 2)."""
+    idx = np.asarray(idx, np.int64)
+    s, e, m = (idx >> 3) & 1, (idx >> 1) & 3, idx & 1
+    mag = np.where(e == 0, m * 0.5, np.ldexp(1.0 + m * 0.5, (e - 1).astype(np.int32)))
+    return (np.where(s == 1, -1, 1) * 2 * mag).astype(np.int64)
+
+
+def e8m0_half(e):
+    """Half of the E8M0 (OCP MX) scale 2^(e - 127), as float32 (2^-128 and 2^-127 are fp32 subnormals)."""
+    return np.ldexp(np.float64(1.0), np.asarray(e, np.int32) - 128).astype(np.float32)
+
+
+def mxfp4(b):
+    """MXFP4 weights: E8M0 exponent @0, qs[16] @1; value j < 16 from the low nibble of qs[j], 16 + j from its high
+    nibble; scale e8m0_half(e), values the doubled E2M1 codes."""
+    b = b.reshape(-1, 17)
+    qs = b[:, 1:17].astype(np.int64)
+    idx = np.concatenate([qs & 0xF, qs >> 4], axis=1)
+    return dict(q=e2m1_doubled(idx), sc=np.ones((b.shape[0], 1), np.int64), m=None, gsize=32, d=e8m0_half(b[:, 0]))
+
+
 def iq2xs(b, grid_rows, ksigns):
     """grid_rows: [512, 8] codebook bytes, ksigns: [128] sign bytes."""
     b = b.reshape(-1, 74)
@@ -125,6 +148,7 @@ def decode(t, b, grid_rows=None, ksigns=None):
     if t == 23: return iq4xs(b)
     if t == 20: return iq4nl(b)
     if t == 8: return q8_0w(b)
+    if t == 39: return mxfp4(b)
     if t == 17: return iq2xs(b, grid_rows, ksigns)
     if t == 16: return iq2xxs(b, grid_rows, ksigns)
     raise ValueError(t)
@@ -145,7 +169,7 @@ def dequant(t, b, grid_rows=None, ksigns=None):
         return ((d * sc) * q.astype(np.float32)).astype(np.float32)
     if t == 23:
         return ((d * sc) * q.astype(np.float32)).astype(np.float32)
-    if t == 20:
+    if t in (20, 39):
         return (q.astype(np.float32) * d).astype(np.float32)
     if t == 8:
         return (d * q.astype(np.float32)).astype(np.float32)
@@ -159,7 +183,7 @@ def block_ints(t, b, xq, grid_rows=None, ksigns=None):
     """Brute-force integers per block: sumi = sum over groups of scale * sum(q * y), summ = sum_j m_j * sum(y_j)."""
     f = decode(t, b, grid_rows, ksigns)
     q, gs = f["q"], f["gsize"]
-    if int(t) in (20, 8):
+    if int(t) in (20, 8, 39):
         y = q8_0(xq)["qs"]
     else:
         y = q8k(xq)["qs"]

@@ -1,4 +1,5 @@
-"""GPU: the decode hand-over of the hidden as Q8_0 rows for IQ4_NL layers.  hy_moe_route_gate_up_q8 writes h and the
+"""GPU: the decode hand-over of the hidden as Q8_0 rows for layers whose gate/up and down both take Q8_0 activations
+(IQ4_NL, Q8_0, MXFP4).  hy_moe_route_gate_up_q8 writes h and the
 Q8_0 rows of h; hy_moe_down_reduce_q8 reads those rows in place of quantizing h in every block.  Checked bit for bit
 against the oracle: h, the rows (the oracle's Q8_0 quantizer on h, src/kernels4.cu:2007-2022 quantizes h the same way
 before the down dot), and out, plain and added into a residual; with experts that are not local (their rows stay
@@ -28,8 +29,9 @@ CASES = [
 @pytest.mark.parametrize("E,d,ff,k,nt,absent", CASES)
 def test_hidden_q8_handover_bitexact(cuda, E, d, ff, k, nt, absent):
     print(f"hidden q8 E={E} d={d} ff={ff} k={k} nt={nt} absent={absent}", flush=True)
-    L = layer(GType.Q8_0 if nt == 3 else GType.IQ4_NL, GType.IQ4_NL if nt == 3 else GType.Q8_0 if nt == 8 else GType.IQ4_NL,
-              E, ff, d, seed=740 + nt)   # IQ4_NL both ways, a Q8_0 gate/up (3 rows), a Q8_0 down (8 rows)
+    tg = {3: GType.Q8_0, 4: GType.MXFP4}.get(nt, GType.IQ4_NL)
+    td = {3: GType.IQ4_NL, 4: GType.MXFP4, 8: GType.Q8_0}.get(nt, GType.IQ4_NL)
+    L = layer(tg, td, E, ff, d, seed=740 + nt)   # IQ4_NL both ways, a Q8_0 gate/up (3 rows), MXFP4 both ways (4 rows), a Q8_0 down (8 rows)
     slot = [(-1 if e in absent else e) for e in range(E)]
     dev = moe.upload_experts(L, slot=slot, device=cuda)
     OL = oracle_layer(L)

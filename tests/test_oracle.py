@@ -287,6 +287,41 @@ def test_q8_0_weight_known_answers():
     assert orc.row_dot(GType.Q8_0, blk.reshape(-1), ya.reshape(-1), 64) == want_dot
 
 
+def test_mxfp4_known_answers():
+    """MXFP4 (src/kernels4.cu:550-577): byte 0 is an E8M0 exponent, value j < 16 = kv[qs[j] & 15] * 2^(e - 128) and
+    16 + j = kv[qs[j] >> 4] * 2^(e - 128), kv the E2M1 codes doubled (OCP MX: code 7 = 6.0 -> 12, code 9 = -0.5 -> -1,
+    code 8 = -0 -> 0).  The scale's edge exponents: 0 and 1 give the fp32 subnormals 2^-128, 2^-127; 255 gives 2^127
+    (no NaN code).  Against Q8_0 the integer is sum kv y, folded as x_d * (2^(e - 128) * sumi)."""
+    assert list(nf.e2m1_doubled(np.arange(16))) == [0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12]
+    exps = (128, 0, 1, 255, 127)
+    idx = np.array([[(5 * j + 3 * b + (j >= 16)) % 16 for j in range(32)] for b in range(len(exps))], np.int64)
+    blk = np.zeros((len(exps), 17), np.uint8)
+    for b, e in enumerate(exps):
+        blk[b, 0] = e
+        for j in range(32):
+            blk[b, 1 + (j % 16)] |= idx[b, j] << (4 if j >= 16 else 0)
+    kv = np.array([0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12], np.float64)
+    with np.errstate(over="ignore"):   # e = 255: kv 2^127 past fp32's range for |kv| >= 2 is inf, as the product is there
+        want = np.concatenate([kv[idx[b]] * np.ldexp(1.0, e - 128) for b, e in enumerate(exps)]).astype(np.float32)
+    assert np.isinf(want[96:128]).any()
+    assert np.float32(np.ldexp(1.0, -128)) != 0 and np.float32(np.ldexp(1.0, 127)) == np.float32(2.0 ** 127)
+    got = orc.dequant_row(GType.MXFP4, blk.reshape(-1), 32 * len(exps))
+    assert (got == want).all(), np.nonzero(got != want)
+    y = np.array([(11 * j) % 255 - 127 for j in range(64)], np.int64)
+    ya = np.zeros((2, 34), np.uint8)
+    for b, yd in enumerate((0.25, 3.0)):
+        ya[b, 0:2] = _f16b(yd)
+        ya[b, 2:34] = y[32 * b:32 * b + 32].astype(np.int8).view(np.uint8)
+    wb = blk[[0, 4]].reshape(-1)                                  # exponents 128 and 127: scales 1 and 1/2
+    si, sm = orc.block_ints(GType.MXFP4, wb, ya.reshape(-1), 64)
+    ints = [int(kv[idx[0]].astype(np.int64) @ y[:32]), int(kv[idx[4]].astype(np.int64) @ y[32:])]
+    assert list(si) == ints and not sm.any()
+    t0, t1 = np.float32(si[0]), np.float32(0.5) * np.float32(si[1])
+    acc = np.float32(np.float64(0.25) * np.float64(t0))
+    want_dot = np.float32(np.float64(3.0) * np.float64(t1) + np.float64(acc))    # one rounding: fmaf
+    assert orc.row_dot(GType.MXFP4, wb, ya.reshape(-1), 64) == want_dot
+
+
 def test_q8k_known_answers():
     x = np.zeros(512, np.float32)
     # block 0: max -127 at index 3 -> iscale = 1, q = round-half-even(x)
@@ -307,7 +342,7 @@ def test_q8k_known_answers():
 
 # ------------------------------------------------------------------ block decoding
 
-ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.IQ4_NL, GType.Q8_0]
+ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.IQ4_NL, GType.Q8_0, GType.MXFP4]
 
 
 def blocks(t, nb, seed):
