@@ -167,6 +167,47 @@ template <int VT> __device__ __forceinline__ float q8_scale(const uint8_t *y, in
     else return h2f(ld_u16(y + (size_t) b * Q8_0_BYTES));
 }
 
+// One lane's block-order fold: acc[c] = fmaf(xs(b), tv(c, b), acc[c]) for b = 0 .. nb - 1, NC chains sharing the
+// activation scales.  The LDS operands come in batches of 8 blocks held in two register sets that alternate, so a
+// batch's reads are in flight while the previous batch's fma chain runs; full batches carry no guards and the last
+// nb % 8 blocks go one by one.  The fmas are those of the plain loop, in its order.
+template <int NC, typename XS, typename TV>
+__device__ __forceinline__ void fold_blocks(int nb, XS xs, TV tv, float (&acc)[NC]) {
+    constexpr int B = 8;
+    const int nf = nb - nb % B;
+    float x0[B], x1[B], t0[NC][B], t1[NC][B];
+    auto ld = [&](float (&x)[B], float (&t)[NC][B], int b0) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            x[u] = xs(b0 + u);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) t[c][u] = tv(c, b0 + u);
+        }
+    };
+    auto fm = [&](const float (&x)[B], const float (&t)[NC][B]) {
+#pragma unroll
+        for (int u = 0; u < B; ++u)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc[c] = __builtin_fmaf(x[u], t[c][u], acc[c]);
+    };
+    if (nf) {
+        ld(x0, t0, 0);
+        for (int b0 = 0;; b0 += 2 * B) {   // uniform over the lanes that fold
+            if (b0 + B < nf) ld(x1, t1, b0 + B);
+            fm(x0, t0);
+            if (b0 + B >= nf) break;
+            if (b0 + 2 * B < nf) ld(x0, t0, b0 + 2 * B);
+            fm(x1, t1);
+            if (b0 + 2 * B >= nf) break;
+        }
+    }
+    for (int b = nf; b < nb; ++b) {
+        const float x = xs(b);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[c] = __builtin_fmaf(x, tv(c, b), acc[c]);
+    }
+}
+
 // ---------------------------------------------------------------- k_dec_gate_up
 
 constexpr int DEC_GU_TV = 2 * 256;   // fold inputs per wave: 2 matrices x up to 256 blocks (IQ4_NL, n <= 8192)
@@ -329,25 +370,17 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     }
     lds_barrier();
     HY_STAMP(3);
-    // the folds, in block order, by wave 0: lane l takes the block's row l (wave l / rw, its row l % rw); eight
-    // blocks' inputs per LDS round trip, then the fma chain
+    // the folds, in block order, by wave 0: lane l takes the block's row l (wave l / rw, its row l % rw), gate and
+    // up chains side by side (fold_blocks)
     if (wave != 0 || (!HQ && lane >= DEC_GU_WAVES * rw)) return;
     const int row = blockIdx.x * DEC_GU_WAVES * rw + lane;
     if (!HQ && row >= ff) return;
     float hv = 0.0f;
     if (lane < DEC_GU_WAVES * rw) {   // (HQ: lanes 32-63 stay for the quantizer's cross-lane max)
         const float *tg = tv + lane * rs;
-        float ag = 0.0f, au = 0.0f;
-        for (int b0 = 0; b0 < nb; b0 += 8) {
-            float xa[8], ga[8], ua[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (b0 + u < nb) { xa[u] = s_xd[b0 + u]; ga[u] = tg[b0 + u]; ua[u] = tg[nb + b0 + u]; }
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (b0 + u < nb) { ag = __builtin_fmaf(xa[u], ga[u], ag); au = __builtin_fmaf(xa[u], ua[u], au); }
-        }
-        hv = hy_swiglu(ag, au, m.clamp);
+        float a[2] = {0.0f, 0.0f};
+        fold_blocks(nb, [&](int b) { return s_xd[b]; }, [&](int c, int b) { return tg[c * nb + b]; }, a);
+        hv = hy_swiglu(a[0], a[1], m.clamp);
         h[(size_t) p * ff + row] = hv;
     }
     HY_STAMP(4);
@@ -529,18 +562,25 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
         HY_STAMP(4);
         // lane j folds pair j in block order
         float fo = 0.0f;
-        if (mine) {   // LDS reads four blocks at a time, then the fma chain
+        if (mine) {
             const uint8_t *yj = hq + (size_t) lane * ng * SPAN_L;
             const float *tj = tw + lane * (nb | 1);
             float acc = 0.0f;
-            for (int b0 = 0; b0 < nb; b0 += 4) {
-                float sc[4], tq[4];
+            if constexpr (block_elems(T) == 32) {   // ff / 32 blocks: batches in flight ahead of the chain
+                float a1[1] = {0.0f};
+                fold_blocks(nb, [&](int b) { return VT == Q8_K ? q8_scale<VT>(yj, b) : h2f(hdq[lane * nb + b]); },
+                            [&](int, int b) { return tj[b]; }, a1);
+                acc = a1[0];
+            } else {   // ff / 256 blocks (a few): four blocks' inputs per LDS round trip, then the fma chain
+                for (int b0 = 0; b0 < nb; b0 += 4) {
+                    float sc[4], tq[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    if (b0 + u < nb) { sc[u] = VT == Q8_K ? q8_scale<VT>(yj, b0 + u) : h2f(hdq[lane * nb + b0 + u]); tq[u] = tj[b0 + u]; }
+                    for (int u = 0; u < 4; ++u)
+                        if (b0 + u < nb) { sc[u] = q8_scale<VT>(yj, b0 + u); tq[u] = tj[b0 + u]; }
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    if (b0 + u < nb) acc = __builtin_fmaf(sc[u], tq[u], acc);
+                    for (int u = 0; u < 4; ++u)
+                        if (b0 + u < nb) acc = __builtin_fmaf(sc[u], tq[u], acc);
+                }
             }
             fo = my_w * acc;
         }
