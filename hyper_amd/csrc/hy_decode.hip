@@ -730,7 +730,9 @@ int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const f
 #define HY_DN(NN) hipLaunchKernelGGL((k_dec_down<TT, NN>), grid, dim3(64 * DEC_DN_WAVES), 0, s, m, h, ids, wts, k, shexp, sg, out, res, q8, r8, hq, rpw)
     HY_DEC_SWITCH(m.td, {
         // 8 passes a round only for IQ2_XS (same occupancy as 4); the others take more rounds at a higher occupancy
-        if (np <= 2) HY_DN(2); else if (np <= 4 || TT != IQ2_XS) HY_DN(4); else HY_DN(8);
+        if (np <= 2) HY_DN(2);
+        else if constexpr (TT != IQ2_XS) HY_DN(4);
+        else if (np <= 4) HY_DN(4); else HY_DN(8);
         return check_launch("hy_moe_down_reduce");
     });
 #undef HY_DN
