@@ -35,6 +35,11 @@ __device__ __forceinline__ uint32_t kv4(uint32_t idx) { return kv16(idx, 0xBFAD9
 __device__ __forceinline__ uint32_t kvfp4(uint32_t idx) { return kv16(idx, 0x03020100u, 0x0C080604u, 0xFDFEFF00u, 0xF4F8FAFCu); }
 // IQ2 signs: 8 sign bits -> two words whose bytes are 0xFF where negated; value = (g ^ M) + (M & 1)
 __device__ __forceinline__ uint32_t spread4(uint32_t b4) { return (b4 * 0x00204081u) & 0x01010101u; }
+// 0xF0 in the bytes whose bit is set in b4 (4 bits): OR-ed onto a nibble it makes the int8 nibble - 16
+__device__ __forceinline__ uint32_t fill_f0(uint32_t b4) {
+    const uint32_t s = spread4(b4);
+    return (s << 8) - (s << 4);
+}
 __device__ __forceinline__ uint32_t apply_sign(uint32_t g, uint32_t b4) {
     const uint32_t one = spread4(b4);
     return (g ^ (one * 0xFFu)) + one;
@@ -279,6 +284,38 @@ template <> struct Item<MXFP4> {
         si = dot32(ya); sm = 0;
     }
     __device__ __forceinline__ float tval(int si, int) const { return e8m0_half(e) * (float) si; }
+};
+// Q5_0 (22 B: d, qh u32, qs[16]) against Q8_0, src/kernels4.cu:464-478: lane L takes the item's block L whole, value
+// j = (nibble j | qh bit j << 4) - 16, nibble j the low one of qs[j] for j < 16, the high one of qs[j - 16] above; as
+// an int8 byte that is the nibble, OR 0xF0 where the qh bit is clear (ggml's vec_dot_q5_0_q8_0 integers:
+// sumi = sum_32 (x - 16) q8).  Block L sits at 22 L of the 16-byte aligned 176-byte span: its qs (22 L + 6) and qh
+// (22 L + 2) are 2 mod 4 for even L, where the 16-byte read takes 2 bytes of block L + 1 (L < 7), and dword-aligned
+// for odd L.
+template <> struct Item<Q5_0> {
+    uint4 qs;
+    uint32_t qh;
+    uint16_t d;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+        qs = load16_a2_nb(b + 22 * L + 6);
+        qh = (uint32_t) ld_u16(b + 22 * L + 2) | ((uint32_t) ld_u16(b + 22 * L + 4) << 16);
+        d = ld_u16(b + 22 * L);
+    }
+    __device__ __forceinline__ int dot32(const uint32_t (&ya)[8]) const {
+        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w}, nh = ~qh;
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s = sdot4((q[i] & 0x0F0F0F0Fu) | fill_f0((nh >> (4 * i)) & 15), ya[i], s);
+            s = sdot4(((q[i] >> 4) & 0x0F0F0F0Fu) | fill_f0((nh >> (16 + 4 * i)) & 15), ya[4 + i], s);
+        }
+        return s;
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int, int &si, int &sm) const {
+        const uint32_t *yw = (const uint32_t *) (y + 4);
+        const uint32_t ya[8] = {yw[0], yw[1], yw[2], yw[3], yw[4], yw[5], yw[6], yw[7]};
+        si = dot32(ya); sm = 0;
+    }
+    __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
 };
 
 // expand an IQ2 codebook (base-3 codes: IQ2_XS 512 rows, IQ2_XXS 256) into rows x 8 bytes of LDS, followed by the

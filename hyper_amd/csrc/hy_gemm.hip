@@ -266,6 +266,35 @@ template <> struct Raw<MXFP4> {
     __device__ __forceinline__ float cfold(int c, int d) const { return e8m0_half((ee[c >> 2] >> (8 * (c & 3))) & 255) * (float) d; }
     __device__ __forceinline__ float fold(int si, int) const { return (float) si; }
 };
+// Q5_0 (8 blocks of 22 B per 256 values, Q8_0 activations): chunk c = block c, lane values as IQ4_NL's (nibbles
+// (q >> 1) of qs[8 (q & 1) ..]) with their fifth bits in qh byte q (bits 8 q .. 8 q + 7), each byte nibble | 0xF0
+// where the bit is clear (x - 16 as int8).  Block c's qs (22 c + 6) and qh (22 c + 2) are 2 mod 4 for even c, read by
+// ld8_2a whose 12 bytes end at most at blk + 155, and dword-aligned for odd c, read as they are.
+template <> struct Raw<Q5_0> {
+    static constexpr bool mins = false, g16 = false, per_chunk = true;
+    uint2 qv[8]; uint32_t hb[2], dd[4];
+    __device__ __forceinline__ void load(const uint8_t *blk, int q) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const uint8_t *p = blk + 22 * c + 6 + 8 * (q & 1);
+            qv[c] = (c & 1) ? *(const uint2 *) p : ld8_2a(p);
+        }
+        hb[0] = hb[1] = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) hb[c >> 2] |= (uint32_t) blk[22 * c + 2 + q] << (8 * (c & 3));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dd[i] = (uint32_t) ld_u16(blk + 44 * i) | ((uint32_t) ld_u16(blk + 44 * i + 22) << 16);
+    }
+    __device__ __forceinline__ void chunk(int c, int q, const uint2 *, uint32_t &b0, uint32_t &b1, int &s0, int &s1, int &mn) const {
+        const int s = 4 * (q >> 1);
+        const uint32_t nh = ~(hb[c >> 2] >> (8 * (c & 3)));
+        b0 = ((qv[c].x >> s) & 0x0F0F0F0Fu) | fill_f0(nh & 15);
+        b1 = ((qv[c].y >> s) & 0x0F0F0F0Fu) | fill_f0((nh >> 4) & 15);
+        s0 = 1; s1 = 0; mn = 0;
+    }
+    __device__ __forceinline__ float cfold(int c, int d) const { return h2f((dd[c >> 1] >> (16 * (c & 1))) & 0xffff) * (float) d; }
+    __device__ __forceinline__ float fold(int si, int) const { return (float) si; }
+};
 
 constexpr int GM_TOK = 64, GM_TILES = GM_TOK / 16, GM_ROWS = 64, GM_LD = 264;   // LDS row stride of staged activations
 
@@ -836,7 +865,7 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
     }
 }
 
-// IQ4_NL / Q8_0 / MXFP4: one chunk's MFMA per tile folded straight into the fp32 accumulators (Yc: 8 block scales per token)
+// IQ4_NL / Q8_0 / MXFP4 / Q5_0: one chunk's MFMA per tile folded straight into the fp32 accumulators (Yc: 8 block scales per token)
 template <int T>
 __device__ __forceinline__ void chunk_fold(const Raw<T> &w, int c, int q, const int8_t *As, const float *Yc, int rr, int ntile,
                                            float (&acc)[GM_TILES][4]) {
@@ -854,7 +883,7 @@ __device__ __forceinline__ void chunk_fold(const Raw<T> &w, int c, int q, const 
     }
 }
 
-// IQ4_NL, Q8_0 and MXFP4 weights (Q8_0 activations, whose 2-byte aligned blocks the LDS DMA above cannot stage): register-staged
+// IQ4_NL, Q8_0, MXFP4 and Q5_0 weights (Q8_0 activations, whose 2-byte aligned blocks the LDS DMA above cannot stage): register-staged
 // stream, one step ahead.  A block walks the work items it, it + gridDim.y, ...; the (item, block) steps form one stream in which the
 // next step's weight and activation bytes are loaded while the current step computes, across item boundaries.
 template <int T, bool GU>
@@ -862,7 +891,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
                                               const int *__restrict__ order_n, const int *__restrict__ egrp, const float *__restrict__ wts,
                                               float *__restrict__ out) {
     __shared__ __align__(16) int8_t As[2][GM_TOK * GM_LD];
-    constexpr bool NL = vec_dot_type(T) == Q8_0;     // Q8_0 activations, per-block fold (IQ4_NL, Q8_0, MXFP4)
+    constexpr bool NL = vec_dot_type(T) == Q8_0;     // Q8_0 activations, per-block fold (IQ4_NL, Q8_0, MXFP4, Q5_0)
     __shared__ float Yd[2][GM_TOK * (NL ? 8 : 1)];
     __shared__ int s_scan[1024 + 8];
     __shared__ float s_up[GU ? 32 * GM_TOK : 1];
@@ -1073,6 +1102,7 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
         dim3 grid(rt, item_slots(rt, n_pairs, max_active, 3));
         if (m.tg == IQ4_NL) hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
         else if (m.tg == MXFP4) hipLaunchKernelGGL((k_gemm_nl<MXFP4, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
+        else if (m.tg == Q5_0) hipLaunchKernelGGL((k_gemm_nl<Q5_0, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
         else hipLaunchKernelGGL((k_gemm_nl<Q8_0, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
         return check_launch("hy_moe_gemm_gate_up");
     }
@@ -1104,6 +1134,7 @@ int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int
         dim3 grid(rt, item_slots(rt, n_pairs, max_active, 3));
         if (m.td == IQ4_NL) hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
         else if (m.td == MXFP4) hipLaunchKernelGGL((k_gemm_nl<MXFP4, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
+        else if (m.td == Q5_0) hipLaunchKernelGGL((k_gemm_nl<Q5_0, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
         else hipLaunchKernelGGL((k_gemm_nl<Q8_0, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
         return check_launch("hy_moe_gemm_down");
     }

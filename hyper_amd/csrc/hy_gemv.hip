@@ -161,6 +161,7 @@ static int launch_gemv_t(const hy_moe_dev &m, const float *src, int ss, const in
     case IQ4_NL: { constexpr int TT = IQ4_NL; CALL; }                                    \
     case Q8_0: { constexpr int TT = Q8_0; CALL; }                                        \
     case MXFP4: { constexpr int TT = MXFP4; CALL; }                                      \
+    case Q5_0: { constexpr int TT = Q5_0; CALL; }                                        \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 
@@ -416,6 +417,12 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, floa
         const uint8_t *b = row + (size_t) (i >> 5) * 17;
         const int e = i & 31;
         v = (float) (int8_t) (kvfp4((b[1 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF) & 0xff) * e8m0_half(b[0]);
+    } else if (type == Q5_0) {   // src/kernels4.cu:464-478
+        const uint8_t *b = row + (size_t) (i >> 5) * 22;
+        const int e = i & 31;
+        const uint32_t qh = (uint32_t) ld_u16(b + 2) | ((uint32_t) ld_u16(b + 4) << 16);
+        const int x = ((b[6 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF) | (((qh >> e) & 1) << 4);
+        v = (float) (x - 16) * h2f(ld_u16(b));
     } else if (type == Q8_0) {
         const uint8_t *b = row + (size_t) (i >> 5) * 34;
         v = h2f(ld_u16(b)) * (float) (int8_t) b[2 + (i & 31)];
@@ -471,7 +478,7 @@ int launch_block_ints(int type, const uint8_t *rows, size_t row_bytes, int nrows
                       hipStream_t s) {
     const int groups = nrows * (n / 256);
     if (groups == 0) return HY_OK;
-    if (vec_dot_type(type) == Q8_0 && n / 32 > 256) { set_error("hy_block_ints: IQ4_NL / Q8_0 / MXFP4 rows longer than 8192"); return HY_EBAD_SHAPE; }
+    if (vec_dot_type(type) == Q8_0 && n / 32 > 256) { set_error("hy_block_ints: rows of 32-value blocks longer than 8192"); return HY_EBAD_SHAPE; }
     dim3 grid((groups + 31) / 32);
     HY_TYPE_SWITCH(type, hipLaunchKernelGGL((k_block_ints<TT>), grid, dim3(256), 0, s, rows, row_bytes, nrows, (const uint8_t *) xq, n,
                                             sumi, summ);

@@ -9,6 +9,7 @@ Block sizes follow src/gguf.cpp:43-82; layouts follow the reference's deq8<T> (s
   Q8_K 292 B: f32 d, qs[256], i16 bsums[16];
   Q8_0 34 B per 32: d f16, qs int8[32] (activation rows, and expert weights)
   MXFP4 17 B per 32: e (E8M0 exponent, scale 2^(e - 128)) @0, qs[16] @1
+  Q5_0 22 B per 32: d f16, qh u32 (bit j: value j's fifth bit) @2, qs[16] @6; value d ((nibble | bit << 4) - 16)
 Synthetic blocks (the workloads' generators): uniformly random quant bytes (which gives uniform nibbles,
 6-bit scales/mins, grid indices and sign bits), fp16 scale fields drawn uniformly from a stated range, E8M0
 exponents uniformly from those whose scale 2^(e - 128) lies within a power of two of that range.
@@ -23,6 +24,7 @@ import torch
 
 class GType(IntEnum):
     """GGUF type ids (src/gguf.h:13-18)."""
+    Q5_0 = 6
     Q8_0 = 8
     Q4_K = 12
     Q5_K = 13
@@ -36,8 +38,8 @@ class GType(IntEnum):
 
 
 _BYTES = {GType.Q8_0: 34, GType.Q4_K: 144, GType.Q5_K: 176, GType.Q6_K: 210, GType.Q8_K: 292,
-          GType.IQ2_XXS: 66, GType.IQ2_XS: 74, GType.IQ4_NL: 18, GType.IQ4_XS: 136, GType.MXFP4: 17}
-_ELEMS = {GType.Q8_0: 32, GType.IQ4_NL: 32, GType.MXFP4: 32}
+          GType.IQ2_XXS: 66, GType.IQ2_XS: 74, GType.IQ4_NL: 18, GType.IQ4_XS: 136, GType.MXFP4: 17, GType.Q5_0: 22}
+_ELEMS = {GType.Q8_0: 32, GType.IQ4_NL: 32, GType.MXFP4: 32, GType.Q5_0: 32}
 
 
 def block_bytes(t) -> int:
@@ -50,7 +52,7 @@ def block_elems(t) -> int:
 
 def vec_dot_type(t) -> GType:
     """Activation partner type (ggml vec_dot_type; src/cpu_moe.cpp:711-715)."""
-    return GType.Q8_0 if GType(t) in (GType.IQ4_NL, GType.Q8_0, GType.MXFP4) else GType.Q8_K
+    return GType.Q8_0 if GType(t) in (GType.IQ4_NL, GType.Q8_0, GType.MXFP4, GType.Q5_0) else GType.Q8_K
 
 
 def row_bytes(t, n: int) -> int:
@@ -63,7 +65,7 @@ def q8_row_bytes(vt, n: int) -> int:
 
 # fp16 scale fields per type: byte offsets inside the block
 _F16_FIELDS = {GType.Q4_K: (0, 2), GType.Q5_K: (0, 2), GType.Q6_K: (208,), GType.IQ4_NL: (0,), GType.Q8_0: (0,),
-               GType.IQ4_XS: (0,), GType.IQ2_XS: (0,), GType.IQ2_XXS: (0,), GType.MXFP4: ()}
+               GType.IQ4_XS: (0,), GType.IQ2_XS: (0,), GType.IQ2_XXS: (0,), GType.MXFP4: (), GType.Q5_0: (0,)}
 # E8M0 exponent bytes per type
 _E8M0_FIELDS = {GType.MXFP4: (0,)}
 

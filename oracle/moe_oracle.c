@@ -27,21 +27,22 @@ size_t or_block_bytes(int type) {
     case OR_IQ4_NL: return 18;
     case OR_IQ4_XS: return 136;
     case OR_MXFP4: return 17;
+    case OR_Q5_0: return 22;
     default: return 0;
     }
 }
 int or_block_elems(int type) {
     switch (type) {
-    case OR_Q8_0: case OR_IQ4_NL: case OR_MXFP4: return 32;
+    case OR_Q8_0: case OR_IQ4_NL: case OR_MXFP4: case OR_Q5_0: return 32;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_Q8_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: return 256;
     default: return 0;
     }
 }
-/* ggml's vec_dot_type: Q8_0 for IQ4_NL, Q8_0 and MXFP4 weights, Q8_K for the K-quants and the 256-block IQ types
+/* ggml's vec_dot_type: Q8_0 for IQ4_NL, Q8_0, MXFP4 and Q5_0 weights, Q8_K for the K-quants and the 256-block IQ types
    (the activation quantizer is chosen per weight type: src/cpu_moe.cpp:711-715) */
 int or_vec_dot_type(int type) {
     switch (type) {
-    case OR_IQ4_NL: case OR_Q8_0: case OR_MXFP4: return OR_Q8_0;
+    case OR_IQ4_NL: case OR_Q8_0: case OR_MXFP4: case OR_Q5_0: return OR_Q8_0;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: return OR_Q8_K;
     default: return -1;
     }
@@ -241,6 +242,12 @@ static inline int iq4nl_q(const uint8_t *b, int e) {    /* element e (0..31) of 
 static inline int mxfp4_q(const uint8_t *b, int e) {
     return kv_mxfp4[(b[1 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF];
 }
+/* element e (0..31) of a 22-byte Q5_0 block (d, qh u32, qs[16]): (nibble | qh bit e << 4) - 16, the nibble the low
+   one of qs[e] for e < 16, else the high one of qs[e - 16] (src/kernels4.cu:464-478) */
+static inline int q5_0_q(const uint8_t *b, int e) {
+    const uint32_t qh = (uint32_t) b[2] | ((uint32_t) b[3] << 8) | ((uint32_t) b[4] << 16) | ((uint32_t) b[5] << 24);
+    return (((b[6 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF) | (((qh >> e) & 1) << 4)) - 16;
+}
 /* IQ2_XS signed grid value of element e and the 4-bit scale of its 8-group (src/kernels4.cu:592-601) */
 static inline int iq2xs_q(const uint8_t *b, int e) {
     const int ib = e >> 5, l = (e >> 3) & 3, j = e & 7;
@@ -314,6 +321,9 @@ int or_dequant_row(int type, const uint8_t *row, int n, float *out) {
         case OR_MXFP4:
             for (int e = 0; e < 32; ++e) o[e] = (float) mxfp4_q(b, e) * e8m0_half(b[0]);
             break;
+        case OR_Q5_0:
+            for (int e = 0; e < 32; ++e) o[e] = (float) q5_0_q(b, e) * h2f(b);
+            break;
         case OR_Q8_K: {
             float d; memcpy(&d, b, 4);
             for (int e = 0; e < 256; ++e) o[e] = d * (float) (int8_t) b[4 + e];
@@ -331,7 +341,7 @@ int or_dequant_row(int type, const uint8_t *row, int n, float *out) {
    K-quants: sumi = sum_j sc_j S_j, summ = sum_j m_j (bsums[2j] + bsums[2j+1]) (ggml q4_K/q5_K x q8_K);
    Q6_K: sumi = sum_g sc_g sum_16 (q6 - 32) y; IQ4_XS: sumi = sum_ib (ls - 32) sum_32 kv y (src/iq3s_dot.h:
    136-166); IQ2_XS: sumi = sum (2 sc + 1) sum_16 grid sign y; IQ4_NL x Q8_0: sumi = sum_32 kv q8; Q8_0 x Q8_0:
-   sumi = sum_32 q q8 (ggml's vec_dot_q8_0_q8_0 integer part); MXFP4 x Q8_0: sumi = sum_32 kv q8. */
+   sumi = sum_32 q q8 (ggml's vec_dot_q8_0_q8_0 integer part); MXFP4 x Q8_0: sumi = sum_32 kv q8; Q5_0 x Q8_0: sumi = sum_32 (x - 16) q8. */
 static void block_ints_scalar(int type, const uint8_t *b, const uint8_t *y, int32_t *sumi, int32_t *summ) {
     int32_t si = 0, sm = 0;
     const int8_t *q8 = (const int8_t *) (y + (or_vec_dot_type(type) == OR_Q8_0 ? 2 : 4));
@@ -376,6 +386,9 @@ static void block_ints_scalar(int type, const uint8_t *b, const uint8_t *y, int3
         break;
     case OR_MXFP4:     /* ggml's vec_dot_mxfp4_q8_0 integer part: sum_32 kv q8 */
         for (int l = 0; l < 32; ++l) si += mxfp4_q(b, l) * q8[l];
+        break;
+    case OR_Q5_0:      /* ggml's vec_dot_q5_0_q8_0 integer part: sum_32 (x - 16) q8 */
+        for (int l = 0; l < 32; ++l) si += q5_0_q(b, l) * q8[l];
         break;
     case OR_IQ2_XXS:   /* ggml's vec_dot_iq2_xxs_q8_K: sum_ib (2 sc + 1) sum_32 grid sign y */
         for (int ib = 0; ib < 8; ++ib) {
@@ -461,7 +474,7 @@ static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *su
 
 static int dot_ok(int type) {
     return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_IQ4_XS || type == OR_IQ2_XS || type == OR_IQ4_NL ||
-           type == OR_Q8_0 || type == OR_IQ2_XXS || type == OR_MXFP4;
+           type == OR_Q8_0 || type == OR_IQ2_XXS || type == OR_MXFP4 || type == OR_Q5_0;
 }
 int or_block_ints(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ) {
     if (!dot_ok(type) || n % or_block_elems(type)) return -1;
@@ -494,7 +507,7 @@ static float row_dot(int type, const uint8_t *row, const uint8_t *xq, int n) {
         case OR_Q6_K: t = h2f(b + 208) * (float) si; break;
         case OR_IQ2_XS: case OR_IQ2_XXS: t = (h2f(b) * 0.125f) * (float) si; break;
         case OR_MXFP4: t = e8m0_half(b[0]) * (float) si; break;
-        default: t = h2f(b) * (float) si; break;        /* IQ4_XS, IQ4_NL, Q8_0 */
+        default: t = h2f(b) * (float) si; break;        /* IQ4_XS, IQ4_NL, Q8_0, Q5_0 */
         }
         acc = fmaf(xd, t, acc);
     }

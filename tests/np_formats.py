@@ -103,6 +103,17 @@ def mxfp4(b):
     return dict(q=e2m1_doubled(idx), sc=np.ones((b.shape[0], 1), np.int64), m=None, gsize=32, d=e8m0_half(b[:, 0]))
 
 
+def q5_0w(b):
+    """Q5_0 weights: d f16 @0, qh little-endian u32 @2, qs[16] @6; value j = (nibble j + 16 * bit j of qh) - 16, the
+    nibbles in qs order, low halves first (values 0..15), then high halves (16..31)."""
+    b = b.reshape(-1, 22)
+    qh = np.ascontiguousarray(b[:, 2:6]).view(np.uint32).astype(np.int64).reshape(-1)
+    qs = b[:, 6:22].astype(np.int64)
+    nib = np.concatenate([qs & 0xF, qs >> 4], axis=1)
+    hi = (qh[:, None] >> np.arange(32)) & 1
+    return dict(q=nib + 16 * hi - 16, sc=np.ones((b.shape[0], 1), np.int64), m=None, gsize=32, d=f16(b[:, 0:2]))
+
+
 def iq2xs(b, grid_rows, ksigns):
     """grid_rows: [512, 8] codebook bytes, ksigns: [128] sign bytes."""
     b = b.reshape(-1, 74)
@@ -149,6 +160,7 @@ def decode(t, b, grid_rows=None, ksigns=None):
     if t == 20: return iq4nl(b)
     if t == 8: return q8_0w(b)
     if t == 39: return mxfp4(b)
+    if t == 6: return q5_0w(b)
     if t == 17: return iq2xs(b, grid_rows, ksigns)
     if t == 16: return iq2xxs(b, grid_rows, ksigns)
     raise ValueError(t)
@@ -169,7 +181,7 @@ def dequant(t, b, grid_rows=None, ksigns=None):
         return ((d * sc) * q.astype(np.float32)).astype(np.float32)
     if t == 23:
         return ((d * sc) * q.astype(np.float32)).astype(np.float32)
-    if t in (20, 39):
+    if t in (20, 39, 6):
         return (q.astype(np.float32) * d).astype(np.float32)
     if t == 8:
         return (d * q.astype(np.float32)).astype(np.float32)
@@ -183,7 +195,7 @@ def block_ints(t, b, xq, grid_rows=None, ksigns=None):
     """Brute-force integers per block: sumi = sum over groups of scale * sum(q * y), summ = sum_j m_j * sum(y_j)."""
     f = decode(t, b, grid_rows, ksigns)
     q, gs = f["q"], f["gsize"]
-    if int(t) in (20, 8, 39):
+    if int(t) in (20, 8, 39, 6):
         y = q8_0(xq)["qs"]
     else:
         y = q8k(xq)["qs"]

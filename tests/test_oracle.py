@@ -322,6 +322,35 @@ def test_mxfp4_known_answers():
     assert orc.row_dot(GType.MXFP4, wb, ya.reshape(-1), 64) == want_dot
 
 
+def test_q5_0_known_answers():
+    """Q5_0 (src/kernels4.cu:464-478): value j = (nibble j | bit j of qh << 4) - 16, nibble j the low one of qs[j] for
+    j < 16 and the high one of qs[j - 16] above; qh a little-endian u32 at byte 2.  Blocks built value by value (each
+    x in 0..31 placed by hand), so a swapped nibble half, a qh bit read from the wrong end, or a dropped -16 fails;
+    against Q8_0 the integer is sum (x - 16) y, folded as x_d * (d * sumi)."""
+    x = np.array([[(7 * j + 11 * b) % 32 for j in range(32)] for b in range(2)], np.int64)   # 0 .. 31
+    blk = np.zeros((2, 22), np.uint8)
+    for b, dv in enumerate((0.5, -2.0)):
+        blk[b, 0:2] = _f16b(dv)
+        qh = 0
+        for j in range(32):
+            blk[b, 6 + (j % 16)] |= (x[b, j] & 15) << (4 if j >= 16 else 0)
+            qh |= int(x[b, j] >> 4) << j
+        blk[b, 2:6] = np.frombuffer(np.uint32(qh).tobytes(), np.uint8)
+    want = np.concatenate([(x[0] - 16) * 0.5, (x[1] - 16) * -2.0]).astype(np.float32)
+    assert (orc.dequant_row(GType.Q5_0, blk.reshape(-1), 64) == want).all()
+    y = np.array([(13 * j) % 255 - 127 for j in range(64)], np.int64)
+    ya = np.zeros((2, 34), np.uint8)
+    for b, yd in enumerate((0.75, 0.125)):
+        ya[b, 0:2] = _f16b(yd)
+        ya[b, 2:34] = y[32 * b:32 * b + 32].astype(np.int8).view(np.uint8)
+    si, sm = orc.block_ints(GType.Q5_0, blk.reshape(-1), ya.reshape(-1), 64)
+    assert list(si) == [int((x[0] - 16) @ y[:32]), int((x[1] - 16) @ y[32:])] and not sm.any()
+    t0, t1 = np.float32(0.5) * np.float32(si[0]), np.float32(-2.0) * np.float32(si[1])
+    acc = np.float32(np.float64(0.75) * np.float64(t0))
+    want_dot = np.float32(np.float64(0.125) * np.float64(t1) + np.float64(acc))    # one rounding: fmaf
+    assert orc.row_dot(GType.Q5_0, blk.reshape(-1), ya.reshape(-1), 64) == want_dot
+
+
 def test_q8k_known_answers():
     x = np.zeros(512, np.float32)
     # block 0: max -127 at index 3 -> iscale = 1, q = round-half-even(x)
@@ -342,7 +371,8 @@ def test_q8k_known_answers():
 
 # ------------------------------------------------------------------ block decoding
 
-ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.IQ4_NL, GType.Q8_0, GType.MXFP4]
+ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.IQ4_NL, GType.Q8_0, GType.MXFP4,
+       GType.Q5_0]
 
 
 def blocks(t, nb, seed):
