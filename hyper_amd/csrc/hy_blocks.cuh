@@ -107,6 +107,38 @@ template <> struct Item<Q5_K> {
         return __builtin_fmaf(h2f(hd.x & 0xffff), (float) si, -(h2f(hd.x >> 16) * (float) sm));
     }
 };
+// Q2_K (84 B: scales[16] @0, qs[64] @16, d @80, dmin @82), src/kernels4.cu:639-647.  Value e is the 2-bit field
+// 2 ((e >> 5) & 3) of qs byte 32 (e >> 7) + (e & 31); 16-group g = e >> 4 has scale byte g (low nibble the scale, high
+// nibble the min).  Lane L = 32-group L: 32 qs bytes at 16 + 32 (L >> 2), shift 2 (L & 3), 16-groups 2 L and 2 L + 1
+// (ggml's vec_dot_q2_K_q8_K integers: sumi = sum_g sc_g sum_16 q y, summ = sum_g m_g bsum_g).  Blocks are 4-byte
+// aligned (84-byte rows).
+template <> struct Item<Q2_K> {
+    uint4 q0, q1;
+    uint32_t dm, scm;   // d | dmin << 16; the lane's two scale bytes
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+        q0 = load16_a4(b + 16 + 32 * (L >> 2));
+        q1 = load16_a4(b + 32 + 32 * (L >> 2));
+        dm = *(const uint32_t *) (b + 80);
+        scm = ld_u16(b + 2 * L);
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
+        const int sh = 2 * (L & 3);
+        const uint32_t *ya = (const uint32_t *) (y + 4 + 32 * L);
+        const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        int sa = 0, sb = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sa = sdot4((q[i] >> sh) & 0x03030303u, ya[i], sa);
+            sb = sdot4((q[4 + i] >> sh) & 0x03030303u, ya[4 + i], sb);
+        }
+        const int16_t *bs = (const int16_t *) (y + 260);
+        si = (int) (scm & 15) * sa + (int) ((scm >> 8) & 15) * sb;
+        sm = (int) ((scm >> 4) & 15) * bs[2 * L] + (int) (scm >> 12) * bs[2 * L + 1];
+    }
+    __device__ __forceinline__ float tval(int si, int sm) const {
+        return __builtin_fmaf(h2f(dm & 0xffff), (float) si, -(h2f(dm >> 16) * (float) sm));
+    }
+};
 // Q6_K (210 B: ql[128], qh[64], scales int8[16], d).  Lane L: ql bytes 64 hf + 32 qt0 + 16 hl .. (+16) with
 // hf = L >> 2, qt0 = (L >> 1) & 1, hl = L & 1: low nibbles are the 16-group g = 8 hf + 2 qt0 + hl, high nibbles
 // group g + 4; bits 2 qt of qh[32 hf + l] are bits 4-5.  (q6 - 32) . y = q6 . y - 32 bsum_g.

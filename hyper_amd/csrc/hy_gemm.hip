@@ -97,6 +97,31 @@ template <> struct Raw<Q5_K> {   // 176 B: + qh[32] @16 (bit c of qh[l] is bit 4
         return __builtin_fmaf(h2f(hd.x & 0xffff), (float) si, -(h2f(hd.x >> 16) * (float) sm));
     }
 };
+// Q2_K (84 B: scales[16], qs[64] @16, d @80, dmin @82): chunk c = values 32 c ..: 2-bit fields 2 (c & 3) of qs bytes
+// 32 (c >> 2) + 8 q ..; the chunk's 16-groups 2 c (lanes q < 2) and 2 c + 1 (q >= 2): scales s0 / s1, and the lane's
+// own group's min (the mins MFMA takes each lane quarter's bytes, so each 8-value piece carries its group's min).
+template <> struct Raw<Q2_K> {
+    static constexpr bool mins = true, g16 = true, per_chunk = false;
+    uint4 scv; uint2 qv[2]; uint32_t dm;
+    __device__ __forceinline__ void load(const uint8_t *blk, int q) {
+        scv = load16_a4(blk);
+        qv[0] = *(const uint2 *) (blk + 16 + 8 * q);
+        qv[1] = *(const uint2 *) (blk + 48 + 8 * q);
+        dm = *(const uint32_t *) (blk + 80);
+    }
+    __device__ __forceinline__ void chunk(int c, int q, const uint2 *, uint32_t &b0, uint32_t &b1, int &s0, int &s1, int &mn) const {
+        const int sh = 2 * (c & 3);
+        b0 = (qv[c >> 2].x >> sh) & 0x03030303u;
+        b1 = (qv[c >> 2].y >> sh) & 0x03030303u;
+        const uint32_t w = (c < 2 ? scv.x : c < 4 ? scv.y : c < 6 ? scv.z : scv.w) >> (16 * (c & 1));   // bytes 2 c, 2 c + 1
+        s0 = (int) (w & 15);
+        s1 = (int) ((w >> 8) & 15);
+        mn = (int) ((w >> (q < 2 ? 4 : 12)) & 15);
+    }
+    __device__ __forceinline__ float fold(int si, int sm) const {
+        return __builtin_fmaf(h2f(dm & 0xffff), (float) si, -(h2f(dm >> 16) * (float) sm));
+    }
+};
 // Q6_K (210 B): chunk c = elements 32 c ..: hf = c >> 2, qt = c & 3; lane values l = 8 q .. + 7 from
 // ql[64 hf + 32 (qt & 1) + l] (high nibble when qt >= 2) and bits 2 qt of qh[32 hf + l]; groups 2 c, 2 c + 1.
 template <> struct Raw<Q6_K> {
@@ -326,6 +351,7 @@ __device__ __forceinline__ void chunk_ints(const Raw<T> &w, int c, int q, const 
             const v4i d1 = mfma16(a, mk_long(lo ? 0u : b0, lo ? 0u : b1), z);
 #pragma unroll
             for (int v = 0; v < 4; ++v) si[tile][v] += __mul24(s0, d0[v]) + __mul24(s1, d1[v]);
+            if constexpr (Raw<T>::mins) sm[tile] = mfma16(a, mk_long(mb, mb), sm[tile]);   // mb: the lane's group's min
         } else {
             const v4i d0 = mfma16(a, mk_long(b0, b1), z);
 #pragma unroll
@@ -1072,6 +1098,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
     case IQ4_XS: { constexpr int TT = IQ4_XS; __VA_ARGS__; }                                             \
     case IQ2_XS: { constexpr int TT = IQ2_XS; __VA_ARGS__; }                                             \
     case IQ2_XXS: { constexpr int TT = IQ2_XXS; __VA_ARGS__; }                                           \
+    case Q2_K: { constexpr int TT = Q2_K; __VA_ARGS__; }                                                 \
     default: set_error("grouped GEMM: unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 

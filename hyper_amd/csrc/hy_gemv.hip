@@ -162,6 +162,7 @@ static int launch_gemv_t(const hy_moe_dev &m, const float *src, int ss, const in
     case Q8_0: { constexpr int TT = Q8_0; CALL; }                                        \
     case MXFP4: { constexpr int TT = MXFP4; CALL; }                                      \
     case Q5_0: { constexpr int TT = Q5_0; CALL; }                                        \
+    case Q2_K: { constexpr int TT = Q2_K; CALL; }                                        \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 
@@ -417,6 +418,12 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, floa
         const uint8_t *b = row + (size_t) (i >> 5) * 17;
         const int e = i & 31;
         v = (float) (int8_t) (kvfp4((b[1 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF) & 0xff) * e8m0_half(b[0]);
+    } else if (type == Q2_K) {   // src/kernels4.cu:639-647
+        const uint8_t *b = row + (size_t) (i >> 8) * 84;
+        const int e = i & 255, sc = b[e >> 4];
+        const int q = (b[16 + 32 * (e >> 7) + (e & 31)] >> (2 * ((e >> 5) & 3))) & 3;
+        const float dl = h2f(ld_u16(b + 80)) * (float) (sc & 15), ml = h2f(ld_u16(b + 82)) * (float) (sc >> 4);
+        v = dl * (float) q - ml;
     } else if (type == Q5_0) {   // src/kernels4.cu:464-478
         const uint8_t *b = row + (size_t) (i >> 5) * 22;
         const int e = i & 31;

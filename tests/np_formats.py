@@ -103,6 +103,16 @@ def mxfp4(b):
     return dict(q=e2m1_doubled(idx), sc=np.ones((b.shape[0], 1), np.int64), m=None, gsize=32, d=e8m0_half(b[:, 0]))
 
 
+def q2k(b):
+    """Q2_K: scales[16] @0 (16-group g: scale = low nibble, min = high nibble), qs[64] @16, d @80, dmin @82.  Value
+    128 h + 32 j + l (h < 2, j < 4, l < 32) is bits 2 j .. 2 j + 1 of qs byte 32 h + l."""
+    b = b.reshape(-1, 84)
+    qs = b[:, 16:80].astype(np.int64).reshape(-1, 2, 1, 32)                       # [h][.][l]
+    q = ((qs >> (2 * np.arange(4)).reshape(1, 1, 4, 1)) & 3).reshape(-1, 256)      # [h][j][l] -> value order
+    s = b[:, 0:16].astype(np.int64)
+    return dict(q=q, sc=s & 15, m=s >> 4, gsize=16, d=f16(b[:, 80:82]), dmin=f16(b[:, 82:84]))
+
+
 def q5_0w(b):
     """Q5_0 weights: d f16 @0, qh little-endian u32 @2, qs[16] @6; value j = (nibble j + 16 * bit j of qh) - 16, the
     nibbles in qs order, low halves first (values 0..15), then high halves (16..31)."""
@@ -161,6 +171,7 @@ def decode(t, b, grid_rows=None, ksigns=None):
     if t == 8: return q8_0w(b)
     if t == 39: return mxfp4(b)
     if t == 6: return q5_0w(b)
+    if t == 10: return q2k(b)
     if t == 17: return iq2xs(b, grid_rows, ksigns)
     if t == 16: return iq2xxs(b, grid_rows, ksigns)
     raise ValueError(t)
@@ -174,7 +185,7 @@ def dequant(t, b, grid_rows=None, ksigns=None):
     sc = np.repeat(f["sc"], gs, axis=1)[:, :n].astype(np.float32)
     d = f["d"][:, None]
     t = int(t)
-    if t in (12, 13):
+    if t in (12, 13, 10):
         m = np.repeat(f["m"], gs, axis=1).astype(np.float32)
         return ((d * sc) * q.astype(np.float32) - f["dmin"][:, None] * m).astype(np.float32)
     if t == 14:
@@ -202,7 +213,7 @@ def block_ints(t, b, xq, grid_rows=None, ksigns=None):
     prod = (q * y).reshape(q.shape[0], -1, gs).sum(axis=2)            # per group
     sumi = (prod * f["sc"]).sum(axis=1)
     if f["m"] is not None:
-        summ = (f["m"] * y.reshape(y.shape[0], 8, 32).sum(axis=2)).sum(axis=1)
+        summ = (f["m"] * y.reshape(y.shape[0], -1, gs).sum(axis=2)).sum(axis=1)
     else:
         summ = np.zeros_like(sumi)
     return sumi, summ

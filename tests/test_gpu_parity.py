@@ -151,6 +151,8 @@ DECODE_CASES = [
     (GType.MXFP4, GType.Q8_0, 4096, 1536, 4, 3),
     (GType.Q5_0, GType.Q5_0, 2048, 768, 8, 2),
     (GType.Q5_0, GType.Q4_K, 1024, 512, 6, 3),
+    (GType.Q2_K, GType.Q2_K, 2048, 768, 8, 2),
+    (GType.Q2_K, GType.Q6_K, 4096, 1536, 6, 3),
 ]
 
 
@@ -222,6 +224,8 @@ GEMM_CASES = [
     (GType.MXFP4, GType.Q6_K, 2048, 512, 4, 30),    # Q8_0 x for gate/up, a Q8_K hidden for the down
     (GType.Q5_0, GType.Q5_0, 2048, 768, 8, 40),
     (GType.Q4_K, GType.Q5_0, 1024, 512, 4, 30),
+    (GType.Q2_K, GType.Q2_K, 2048, 768, 8, 40),
+    (GType.Q2_K, GType.Q4_K, 2048, 1024, 6, 120),
     (GType.Q4_K, GType.Q6_K, 2048, 768, 1, 100),    # k = 1: the pair is the token (reciprocal 2^32)
     (GType.Q4_K, GType.Q6_K, 1024, 512, 3, 90),     # odd k: the pair-to-token multiply-high
     (GType.Q4_K, GType.Q6_K, 1024, 256, 16, 12),    # k = E: every expert active, every token in each

@@ -351,6 +351,34 @@ def test_q5_0_known_answers():
     assert orc.row_dot(GType.Q5_0, blk.reshape(-1), ya.reshape(-1), 64) == want_dot
 
 
+def test_q2k_known_answer_positions():
+    """Q2_K (src/kernels4.cu:639-647): value 128 h + 32 j + l is bits 2 j of qs byte 32 h + l (qs at 16), scaled by
+    d * (scale nibble) minus dmin * (min nibble) of its 16-group's scale byte (index value // 16).  Every value's
+    2-bit field is placed by hand, and each group gets its own scale and min, so a wrong byte, shift, group or nibble
+    fails; the block integers (sum sc sum q y, sum m bsum) are checked the same way."""
+    q = np.array([(3 * e + e // 37) % 4 for e in range(256)], np.int64)
+    sc = np.array([(5 * g + 1) % 16 for g in range(16)], np.int64)
+    mn = np.array([(7 * g + 3) % 16 for g in range(16)], np.int64)
+    blk = np.zeros(84, np.uint8)
+    blk[0:16] = sc | (mn << 4)
+    for e in range(256):
+        h, j, l = e // 128, (e // 32) % 4, e % 32
+        blk[16 + 32 * h + l] |= q[e] << (2 * j)
+    blk[80:82] = _f16b(0.5)
+    blk[82:84] = _f16b(0.25)
+    g = np.arange(256) // 16
+    dl = (np.float32(0.5) * sc[g].astype(np.float32)).astype(np.float32)
+    ml = (np.float32(0.25) * mn[g].astype(np.float32)).astype(np.float32)
+    want = (dl * q.astype(np.float32) - ml).astype(np.float32)
+    assert (orc.dequant_row(GType.Q2_K, blk, 256) == want).all()
+    x = np.arange(256, dtype=np.float32) % 9 - 4.0
+    xq = orc.quantize(GType.Q8_K, x)
+    q8 = xq[4:260].view(np.int8).astype(np.int64)
+    si, sm = orc.block_ints(GType.Q2_K, blk, xq, 256)
+    assert int(si[0]) == int(sum(sc[k] * (q[16 * k:16 * k + 16] @ q8[16 * k:16 * k + 16]) for k in range(16)))
+    assert int(sm[0]) == int(sum(mn[k] * q8[16 * k:16 * k + 16].sum() for k in range(16)))
+
+
 def test_q8k_known_answers():
     x = np.zeros(512, np.float32)
     # block 0: max -127 at index 3 -> iscale = 1, q = round-half-even(x)
@@ -372,7 +400,7 @@ def test_q8k_known_answers():
 # ------------------------------------------------------------------ block decoding
 
 ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.IQ4_NL, GType.Q8_0, GType.MXFP4,
-       GType.Q5_0]
+       GType.Q5_0, GType.Q2_K]
 
 
 def blocks(t, nb, seed):
