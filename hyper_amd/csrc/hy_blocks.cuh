@@ -35,6 +35,8 @@ __device__ __forceinline__ uint32_t kv4(uint32_t idx) { return kv16(idx, 0xBFAD9
 __device__ __forceinline__ uint32_t kvfp4(uint32_t idx) { return kv16(idx, 0x03020100u, 0x0C080604u, 0xFDFEFF00u, 0xF4F8FAFCu); }
 // IQ2 signs: 8 sign bits -> two words whose bytes are 0xFF where negated; value = (g ^ M) + (M & 1)
 __device__ __forceinline__ uint32_t spread4(uint32_t b4) { return (b4 * 0x00204081u) & 0x01010101u; }
+// 0xFC in the bytes holding 1 (the others 0): OR-ed onto a 2-bit value it makes the int8 value - 4
+__device__ __forceinline__ uint32_t fill_fc(uint32_t s) { return (s << 8) - (s << 2); }
 // 0xF0 in the bytes whose bit is set in b4 (4 bits): OR-ed onto a nibble it makes the int8 nibble - 16
 __device__ __forceinline__ uint32_t fill_f0(uint32_t b4) {
     const uint32_t s = spread4(b4);
@@ -138,6 +140,44 @@ template <> struct Item<Q2_K> {
     __device__ __forceinline__ float tval(int si, int sm) const {
         return __builtin_fmaf(h2f(dm & 0xffff), (float) si, -(h2f(dm >> 16) * (float) sm));
     }
+};
+// Q3_K (110 B: hmask[32] @0, qs[64] @32, scales[12] @96, d @108), src/kernels4.cu:698-707.  Value e = 128 hf + 32 j + l
+// is the 2-bit field 2 j of qs byte 32 hf + l, less 4 where bit 4 hf + j of hmask[l] is clear; 16-group is = e >> 4
+// has the signed 6-bit scale (scales[is & 7] >> 4 (is >> 3) & 15 | (scales[8 + (is & 3)] >> 2 (is >> 2) & 3) << 4) - 32.
+// Lane L = 32-group L (hf = L >> 2, j = L & 3), 16-groups 2 L and 2 L + 1: sum (q | h << 2) y less 4 bsum per group
+// (ggml's vec_dot_q3_K_q8_K integers: sumi = sum_g sc_g sum_16 (q - 4 (1 - h)) y).  Blocks are 2-byte aligned
+// (110-byte rows); every 16-byte read ends by byte 97.
+template <> struct Item<Q3_K> {
+    uint4 q0, q1, h0, h1;
+    uint32_t sl, sh;   // the two 16-groups' low-nibble bytes and high-bit bytes
+    uint16_t d;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+        const int hf = L >> 2, grp = L >> 1, k = 2 * (L & 1);
+        q0 = load16_a2_nb(b + 32 + 32 * hf);
+        q1 = load16_a2_nb(b + 48 + 32 * hf);
+        h0 = load16_a2_nb(b);
+        h1 = load16_a2_nb(b + 16);
+        sl = ld_u16(b + 96 + 4 * (grp & 1) + k);
+        sh = ld_u16(b + 104 + k);
+        d = ld_u16(b + 108);
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
+        const int hf = L >> 2, j = L & 3, grp = L >> 1, s2 = 2 * j, hb = 4 * hf + j;
+        const uint32_t *ya = (const uint32_t *) (y + 4 + 32 * L);
+        const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w}, h[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        int sa = 0, sb = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sa = sdot4(((q[i] >> s2) & 0x03030303u) | (((h[i] >> hb) & 0x01010101u) << 2), ya[i], sa);
+            sb = sdot4(((q[4 + i] >> s2) & 0x03030303u) | (((h[4 + i] >> hb) & 0x01010101u) << 2), ya[4 + i], sb);
+        }
+        const int16_t *bs = (const int16_t *) (y + 260);
+        const int sc0 = (int) (((sl >> (4 * (grp >> 1))) & 15) | (((sh >> (2 * grp)) & 3) << 4)) - 32;
+        const int sc1 = (int) (((sl >> (8 + 4 * (grp >> 1))) & 15) | (((sh >> (8 + 2 * grp)) & 3) << 4)) - 32;
+        si = sc0 * (sa - 4 * bs[2 * L]) + sc1 * (sb - 4 * bs[2 * L + 1]);
+        sm = 0;
+    }
+    __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
 };
 // Q6_K (210 B: ql[128], qh[64], scales int8[16], d).  Lane L: ql bytes 64 hf + 32 qt0 + 16 hl .. (+16) with
 // hf = L >> 2, qt0 = (L >> 1) & 1, hl = L & 1: low nibbles are the 16-group g = 8 hf + 2 qt0 + hl, high nibbles

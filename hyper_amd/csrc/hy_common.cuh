@@ -17,18 +17,18 @@
 namespace hy {
 
 // GGUF type ids (src/gguf.h:13-18)
-enum GT : int { Q5_0 = 6, Q8_0 = 8, Q2_K = 10, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, IQ2_XXS = 16, IQ2_XS = 17, IQ4_NL = 20, IQ4_XS = 23, MXFP4 = 39 };
+enum GT : int { Q5_0 = 6, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, IQ2_XXS = 16, IQ2_XS = 17, IQ4_NL = 20, IQ4_XS = 23, MXFP4 = 39 };
 
 constexpr int Q8K_BYTES = 292;   // float d; int8 qs[256]; int16 bsums[16]
 constexpr int Q8_0_BYTES = 34;   // fp16 d; int8 qs[32]
 
 __host__ __device__ constexpr int block_bytes(int t) {
     return t == Q4_K ? 144 : t == Q5_K ? 176 : t == Q6_K ? 210 : t == IQ4_XS ? 136 : t == IQ2_XS ? 74 : t == IQ2_XXS ? 66
-         : t == IQ4_NL ? 18 : t == Q8_0 ? 34 : t == MXFP4 ? 17 : t == Q5_0 ? 22 : t == Q2_K ? 84 : t == Q8_K ? 292 : 0;
+         : t == IQ4_NL ? 18 : t == Q8_0 ? 34 : t == MXFP4 ? 17 : t == Q5_0 ? 22 : t == Q2_K ? 84 : t == Q3_K ? 110 : t == Q8_K ? 292 : 0;
 }
 __host__ __device__ constexpr int block_elems(int t) {
     return (t == IQ4_NL || t == Q8_0 || t == MXFP4 || t == Q5_0) ? 32
-         : (t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ2_XXS || t == Q2_K || t == Q8_K) ? 256 : 0;
+         : (t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ2_XXS || t == Q2_K || t == Q3_K || t == Q8_K) ? 256 : 0;
 }
 // the IQ2 types: codebook rows and sign masks in LDS (expand_iq2_grid)
 __host__ __device__ constexpr bool iq2_type(int t) { return t == IQ2_XS || t == IQ2_XXS; }

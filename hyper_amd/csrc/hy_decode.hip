@@ -621,6 +621,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     case MXFP4: { constexpr int TT = MXFP4; CALL; }                                             \
     case Q5_0: { constexpr int TT = Q5_0; CALL; }                                               \
     case Q2_K: { constexpr int TT = Q2_K; CALL; }                                               \
+    case Q3_K: { constexpr int TT = Q3_K; CALL; }                                               \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE;   \
     }
 

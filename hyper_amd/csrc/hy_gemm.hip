@@ -122,6 +122,35 @@ template <> struct Raw<Q2_K> {
         return __builtin_fmaf(h2f(dm & 0xffff), (float) si, -(h2f(dm >> 16) * (float) sm));
     }
 };
+// Q3_K (110 B: hmask[32], qs[64] @32, scales[12] @96, d @108): chunk c = values 32 c .., hf = c >> 2, j = c & 3; lane
+// values l = 8 q .. + 7: 2-bit fields 2 j of qs bytes 32 + 32 hf + l, each byte OR 0xFC where bit 4 hf + j of hmask[l]
+// is clear (q - 4 as int8); 16-groups 2 c (lanes q < 2) and 2 c + 1 with their signed 6-bit scales.  Blocks are 2-byte
+// aligned: ld8_2a's 12-byte reads end by byte 99.
+__device__ __forceinline__ int q3k_scale(const uint32_t (&s)[3], int is) {
+    auto byte = [&](int i) { return (int) ((s[i >> 2] >> (8 * (i & 3))) & 255); };
+    return (((byte(is & 7) >> (4 * (is >> 3))) & 15) | (((byte(8 + (is & 3)) >> (2 * (is >> 2))) & 3) << 4)) - 32;
+}
+template <> struct Raw<Q3_K> {
+    static constexpr bool mins = false, g16 = true, per_chunk = false;
+    uint2 qv[2], hm; uint32_t sc[3], d;
+    __device__ __forceinline__ void load(const uint8_t *blk, int q) {
+        qv[0] = ld8_2a(blk + 32 + 8 * q);
+        qv[1] = ld8_2a(blk + 64 + 8 * q);
+        hm = ld8_2a(blk + 8 * q);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) sc[i] = (uint32_t) ld_u16(blk + 96 + 4 * i) | ((uint32_t) ld_u16(blk + 98 + 4 * i) << 16);
+        d = ld_u16(blk + 108);
+    }
+    __device__ __forceinline__ void chunk(int c, int, const uint2 *, uint32_t &b0, uint32_t &b1, int &s0, int &s1, int &mn) const {
+        const int s2 = 2 * (c & 3), hb = 4 * (c >> 2) + (c & 3);
+        b0 = ((qv[c >> 2].x >> s2) & 0x03030303u) | fill_fc((~hm.x >> hb) & 0x01010101u);
+        b1 = ((qv[c >> 2].y >> s2) & 0x03030303u) | fill_fc((~hm.y >> hb) & 0x01010101u);
+        s0 = q3k_scale(sc, 2 * c);
+        s1 = q3k_scale(sc, 2 * c + 1);
+        mn = 0;
+    }
+    __device__ __forceinline__ float fold(int si, int) const { return h2f(d) * (float) si; }
+};
 // Q6_K (210 B): chunk c = elements 32 c ..: hf = c >> 2, qt = c & 3; lane values l = 8 q .. + 7 from
 // ql[64 hf + 32 (qt & 1) + l] (high nibble when qt >= 2) and bits 2 qt of qh[32 hf + l]; groups 2 c, 2 c + 1.
 template <> struct Raw<Q6_K> {
@@ -1099,6 +1128,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
     case IQ2_XS: { constexpr int TT = IQ2_XS; __VA_ARGS__; }                                             \
     case IQ2_XXS: { constexpr int TT = IQ2_XXS; __VA_ARGS__; }                                           \
     case Q2_K: { constexpr int TT = Q2_K; __VA_ARGS__; }                                                 \
+    case Q3_K: { constexpr int TT = Q3_K; __VA_ARGS__; }                                                 \
     default: set_error("grouped GEMM: unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 

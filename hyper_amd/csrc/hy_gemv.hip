@@ -163,6 +163,7 @@ static int launch_gemv_t(const hy_moe_dev &m, const float *src, int ss, const in
     case MXFP4: { constexpr int TT = MXFP4; CALL; }                                      \
     case Q5_0: { constexpr int TT = Q5_0; CALL; }                                        \
     case Q2_K: { constexpr int TT = Q2_K; CALL; }                                        \
+    case Q3_K: { constexpr int TT = Q3_K; CALL; }                                        \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 
@@ -418,6 +419,12 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, floa
         const uint8_t *b = row + (size_t) (i >> 5) * 17;
         const int e = i & 31;
         v = (float) (int8_t) (kvfp4((b[1 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF) & 0xff) * e8m0_half(b[0]);
+    } else if (type == Q3_K) {   // src/kernels4.cu:698-707
+        const uint8_t *b = row + (size_t) (i >> 8) * 110;
+        const int e = i & 255, is = e >> 4, hf = e >> 7, j = (e >> 5) & 3, l = e & 31;
+        const int sc = (((b[96 + (is & 7)] >> (4 * (is >> 3))) & 15) | (((b[104 + (is & 3)] >> (2 * (is >> 2))) & 3) << 4)) - 32;
+        const float dl = h2f(ld_u16(b + 108)) * (float) sc;
+        v = dl * (float) (((b[32 + 32 * hf + l] >> (2 * j)) & 3) - (((b[l] >> (4 * hf + j)) & 1) ? 0 : 4));
     } else if (type == Q2_K) {   // src/kernels4.cu:639-647
         const uint8_t *b = row + (size_t) (i >> 8) * 84;
         const int e = i & 255, sc = b[e >> 4];

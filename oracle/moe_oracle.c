@@ -29,6 +29,7 @@ size_t or_block_bytes(int type) {
     case OR_MXFP4: return 17;
     case OR_Q5_0: return 22;
     case OR_Q2_K: return 84;
+    case OR_Q3_K: return 110;
     default: return 0;
     }
 }
@@ -36,7 +37,7 @@ int or_block_elems(int type) {
     switch (type) {
     case OR_Q8_0: case OR_IQ4_NL: case OR_MXFP4: case OR_Q5_0: return 32;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_Q8_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K:
-        return 256;
+    case OR_Q3_K: return 256;
     default: return 0;
     }
 }
@@ -45,7 +46,7 @@ int or_block_elems(int type) {
 int or_vec_dot_type(int type) {
     switch (type) {
     case OR_IQ4_NL: case OR_Q8_0: case OR_MXFP4: case OR_Q5_0: return OR_Q8_0;
-    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K: return OR_Q8_K;
+    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K: case OR_Q3_K: return OR_Q8_K;
     default: return -1;
     }
 }
@@ -247,6 +248,18 @@ static inline int mxfp4_q(const uint8_t *b, int e) {
 /* element e (0..255) of an 84-byte Q2_K block: 2-bit field 2 ((e >> 5) & 3) of qs byte 32 (e >> 7) + (e & 31) (qs at
    16); its 16-group e >> 4 has scale byte e >> 4: low nibble the scale, high nibble the min (src/kernels4.cu:639-647) */
 static inline int q2k_q(const uint8_t *b, int e) { return (b[16 + 32 * (e >> 7) + (e & 31)] >> (2 * ((e >> 5) & 3))) & 3; }
+/* element e = 128 hf + 32 j + l of a 110-byte Q3_K block (hmask[32], qs[64] @32, scales[12] @96, d @108): the 2-bit
+   field 2 j of qs byte 32 hf + l, less 4 where bit 4 hf + j of hmask[l] is clear; the signed 6-bit scale of 16-group is
+   from bytes 96 + 4 ((is >> 2) & 1) + (is & 3) (a nibble, by is >> 3) and 104 + (is & 3) (two bits, by is >> 2)
+   (src/kernels4.cu:698-707) */
+static inline int q3k_q(const uint8_t *b, int e) {
+    const int hf = e >> 7, j = (e >> 5) & 3, l = e & 31;
+    return ((b[32 + 32 * hf + l] >> (2 * j)) & 3) - ((b[l] & (1 << (4 * hf + j))) ? 0 : 4);
+}
+static inline int q3k_sc(const uint8_t *b, int is) {
+    const int grp = is >> 2, k = is & 3;
+    return (((b[96 + (grp & 1) * 4 + k] >> (4 * (grp >> 1))) & 0xF) | (((b[104 + k] >> (2 * grp)) & 3) << 4)) - 32;
+}
 /* element e (0..31) of a 22-byte Q5_0 block (d, qh u32, qs[16]): (nibble | qh bit e << 4) - 16, the nibble the low
    one of qs[e] for e < 16, else the high one of qs[e - 16] (src/kernels4.cu:464-478) */
 static inline int q5_0_q(const uint8_t *b, int e) {
@@ -329,6 +342,9 @@ int or_dequant_row(int type, const uint8_t *row, int n, float *out) {
         case OR_Q5_0:
             for (int e = 0; e < 32; ++e) o[e] = (float) q5_0_q(b, e) * h2f(b);
             break;
+        case OR_Q3_K:
+            for (int e = 0; e < 256; ++e) o[e] = (h2f(b + 108) * (float) q3k_sc(b, e >> 4)) * (float) q3k_q(b, e);
+            break;
         case OR_Q2_K:
             for (int e = 0; e < 256; ++e) {
                 const int sc = b[e >> 4];
@@ -401,6 +417,13 @@ static void block_ints_scalar(int type, const uint8_t *b, const uint8_t *y, int3
         break;
     case OR_Q5_0:      /* ggml's vec_dot_q5_0_q8_0 integer part: sum_32 (x - 16) q8 */
         for (int l = 0; l < 32; ++l) si += q5_0_q(b, l) * q8[l];
+        break;
+    case OR_Q3_K:      /* ggml's vec_dot_q3_K_q8_K: sum_g sc_g sum_16 q y */
+        for (int g = 0; g < 16; ++g) {
+            int32_t s = 0;
+            for (int l = 0; l < 16; ++l) s += q3k_q(b, 16 * g + l) * q8[16 * g + l];
+            si += q3k_sc(b, g) * s;
+        }
         break;
     case OR_Q2_K: {    /* ggml's vec_dot_q2_K_q8_K: sumi = sum_g sc_g sum_16 q q8, summ = sum_g m_g bsum_g */
         int16_t bs[16]; memcpy(bs, y + 260, 32);
@@ -496,7 +519,7 @@ static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *su
 
 static int dot_ok(int type) {
     return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_IQ4_XS || type == OR_IQ2_XS || type == OR_IQ4_NL ||
-           type == OR_Q8_0 || type == OR_IQ2_XXS || type == OR_MXFP4 || type == OR_Q5_0 || type == OR_Q2_K;
+           type == OR_Q8_0 || type == OR_IQ2_XXS || type == OR_MXFP4 || type == OR_Q5_0 || type == OR_Q2_K || type == OR_Q3_K;
 }
 int or_block_ints(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ) {
     if (!dot_ok(type) || n % or_block_elems(type)) return -1;
@@ -527,6 +550,7 @@ static float row_dot(int type, const uint8_t *row, const uint8_t *xq, int n) {
         switch (type) {
         case OR_Q4_K: case OR_Q5_K: t = fmaf(h2f(b), (float) si, -(h2f(b + 2) * (float) sm)); break;
         case OR_Q6_K: t = h2f(b + 208) * (float) si; break;
+        case OR_Q3_K: t = h2f(b + 108) * (float) si; break;
         case OR_Q2_K: t = fmaf(h2f(b + 80), (float) si, -(h2f(b + 82) * (float) sm)); break;
         case OR_IQ2_XS: case OR_IQ2_XXS: t = (h2f(b) * 0.125f) * (float) si; break;
         case OR_MXFP4: t = e8m0_half(b[0]) * (float) si; break;

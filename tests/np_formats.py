@@ -113,6 +113,24 @@ def q2k(b):
     return dict(q=q, sc=s & 15, m=s >> 4, gsize=16, d=f16(b[:, 80:82]), dmin=f16(b[:, 82:84]))
 
 
+def q3k(b):
+    """Q3_K in ggml's block_q3_K terms: hmask[32], qs[64], scales[12], d.  Sub-block s = 0..7 of 32 values uses bit s
+    of hmask[l] and bits 2 (s % 4) of qs[32 (s // 4) + l]; value = q - (4 if the hmask bit is clear); 16-group i's
+    scale is the low (i < 8) or high (i >= 8) nibble of scales[i % 8] with bits 2 (i // 4) of scales[8 + i % 4] on top,
+    less 32."""
+    b = b.reshape(-1, 110)
+    hm = b[:, 0:32].astype(np.int64)
+    qs = b[:, 32:96].astype(np.int64).reshape(-1, 2, 32)
+    vals = []
+    for s in range(8):
+        q = (qs[:, s // 4, :] >> (2 * (s % 4))) & 3
+        vals.append(q - 4 * (1 - ((hm >> s) & 1)))
+    s = b[:, 96:108].astype(np.int64)
+    sc = np.stack([((s[:, i % 8] >> (4 * (i // 8))) & 15) | (((s[:, 8 + i % 4] >> (2 * (i // 4))) & 3) << 4)
+                   for i in range(16)], axis=1) - 32
+    return dict(q=np.concatenate(vals, axis=1), sc=sc, m=None, gsize=16, d=f16(b[:, 108:110]))
+
+
 def q5_0w(b):
     """Q5_0 weights: d f16 @0, qh little-endian u32 @2, qs[16] @6; value j = (nibble j + 16 * bit j of qh) - 16, the
     nibbles in qs order, low halves first (values 0..15), then high halves (16..31)."""
@@ -172,6 +190,7 @@ def decode(t, b, grid_rows=None, ksigns=None):
     if t == 39: return mxfp4(b)
     if t == 6: return q5_0w(b)
     if t == 10: return q2k(b)
+    if t == 11: return q3k(b)
     if t == 17: return iq2xs(b, grid_rows, ksigns)
     if t == 16: return iq2xxs(b, grid_rows, ksigns)
     raise ValueError(t)
@@ -188,7 +207,7 @@ def dequant(t, b, grid_rows=None, ksigns=None):
     if t in (12, 13, 10):
         m = np.repeat(f["m"], gs, axis=1).astype(np.float32)
         return ((d * sc) * q.astype(np.float32) - f["dmin"][:, None] * m).astype(np.float32)
-    if t == 14:
+    if t in (14, 11):
         return ((d * sc) * q.astype(np.float32)).astype(np.float32)
     if t == 23:
         return ((d * sc) * q.astype(np.float32)).astype(np.float32)

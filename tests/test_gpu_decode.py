@@ -67,6 +67,7 @@ ROUTE_GU_CASES = [
     (GType.MXFP4, GType.Q4_K, 24, 1024, 512, 6, 3, False),
     (GType.Q5_0, GType.Q5_0, 32, 2048, 768, 8, 2, True),
     (GType.Q2_K, GType.Q2_K, 64, 2048, 1024, 8, 3, False),
+    (GType.Q3_K, GType.Q3_K, 48, 2048, 768, 6, 2, True),
 ]
 
 

@@ -153,6 +153,8 @@ DECODE_CASES = [
     (GType.Q5_0, GType.Q4_K, 1024, 512, 6, 3),
     (GType.Q2_K, GType.Q2_K, 2048, 768, 8, 2),
     (GType.Q2_K, GType.Q6_K, 4096, 1536, 6, 3),
+    (GType.Q3_K, GType.Q3_K, 2048, 768, 8, 2),
+    (GType.Q3_K, GType.Q4_K, 2560, 512, 4, 3),
 ]
 
 
@@ -226,6 +228,8 @@ GEMM_CASES = [
     (GType.Q4_K, GType.Q5_0, 1024, 512, 4, 30),
     (GType.Q2_K, GType.Q2_K, 2048, 768, 8, 40),
     (GType.Q2_K, GType.Q4_K, 2048, 1024, 6, 120),
+    (GType.Q3_K, GType.Q3_K, 2048, 768, 8, 40),
+    (GType.Q3_K, GType.Q6_K, 1024, 512, 4, 70),
     (GType.Q4_K, GType.Q6_K, 2048, 768, 1, 100),    # k = 1: the pair is the token (reciprocal 2^32)
     (GType.Q4_K, GType.Q6_K, 1024, 512, 3, 90),     # odd k: the pair-to-token multiply-high
     (GType.Q4_K, GType.Q6_K, 1024, 256, 16, 12),    # k = E: every expert active, every token in each

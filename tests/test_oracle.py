@@ -379,6 +379,35 @@ def test_q2k_known_answer_positions():
     assert int(sm[0]) == int(sum(mn[k] * q8[16 * k:16 * k + 16].sum() for k in range(16)))
 
 
+def test_q3k_known_answer_positions():
+    """Q3_K (src/kernels4.cu:698-707): value 128 hf + 32 j + l = (bits 2 j of qs byte 32 hf + l) - 4 unless bit 4 hf + j
+    of hmask[l] is set, times d * (scale - 32) of its 16-group; the 16 scales are 6-bit values split into a nibble and
+    two high bits.  Every 2-bit field, hmask bit and scale is placed by hand (scales 0..63 all distinct per group), so a
+    wrong byte, shift, nibble half or high-bit position fails; the block integer is checked against the hand values."""
+    q2 = np.array([(5 * e + e // 29) % 4 for e in range(256)], np.int64)
+    hb = np.array([(e * 7 + e // 11) % 3 != 0 for e in range(256)], np.int64)
+    sc6 = np.array([(11 * g + 5) % 64 for g in range(16)], np.int64)
+    blk = np.zeros(110, np.uint8)
+    for e in range(256):
+        hf, j, l = e // 128, (e // 32) % 4, e % 32
+        blk[32 + 32 * hf + l] |= q2[e] << (2 * j)
+        blk[l] |= hb[e] << (4 * hf + j)
+    for g in range(16):
+        blk[96 + g % 8] |= (sc6[g] & 15) << (4 * (g // 8))
+        blk[104 + g % 4] |= (sc6[g] >> 4) << (2 * (g // 4))
+    blk[108:110] = _f16b(0.25)
+    val = q2 - 4 * (1 - hb)
+    dl = (np.float32(0.25) * (sc6 - 32).astype(np.float32)).astype(np.float32)
+    want = (dl[np.arange(256) // 16] * val.astype(np.float32)).astype(np.float32)
+    assert (orc.dequant_row(GType.Q3_K, blk, 256) == want).all()
+    x = np.arange(256, dtype=np.float32) % 11 - 5.0
+    xq = orc.quantize(GType.Q8_K, x)
+    q8 = xq[4:260].view(np.int8).astype(np.int64)
+    si, sm = orc.block_ints(GType.Q3_K, blk, xq, 256)
+    assert int(si[0]) == int(sum((sc6[g] - 32) * (val[16 * g:16 * g + 16] @ q8[16 * g:16 * g + 16]) for g in range(16)))
+    assert not sm.any()
+
+
 def test_q8k_known_answers():
     x = np.zeros(512, np.float32)
     # block 0: max -127 at index 3 -> iscale = 1, q = round-half-even(x)
@@ -400,7 +429,7 @@ def test_q8k_known_answers():
 # ------------------------------------------------------------------ block decoding
 
 ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.IQ4_NL, GType.Q8_0, GType.MXFP4,
-       GType.Q5_0, GType.Q2_K]
+       GType.Q5_0, GType.Q2_K, GType.Q3_K]
 
 
 def blocks(t, nb, seed):
