@@ -141,6 +141,36 @@ template <> struct Item<Q2_K> {
         return __builtin_fmaf(h2f(dm & 0xffff), (float) si, -(h2f(dm >> 16) * (float) sm));
     }
 };
+// IQ3_XXS (98 B: d, qs[64] @2, scales_and_signs u32[8] @66), src/kernels4.cu:613-627.  Lane L = 32-group L: grid
+// indices qs[8 L + 2 l], qs[8 L + 2 l + 1] (4-byte rows, values 0-3 and 4-7 of 8-group l), the word at 66 + 4 L holding
+// the four 7-bit sign indices (bits 7 l ..) and the 4-bit scale (bits 28 ..); value d (2 sc + 1) / 4 grid sign
+// (ggml's vec_dot_iq3_xxs_q8_K integers: sumi = sum_ib (2 sc + 1) sum_32 grid sign y).  Blocks are 2-byte aligned.
+template <> struct Item<IQ3_XXS> {
+    uint32_t g0, g1, a;   // the lane's 8 index bytes; its scale/sign word
+    uint16_t d;
+    const uint2 *grid;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+        const uint8_t *p = b + 2 + 8 * L;
+        g0 = (uint32_t) ld_u16(p) | ((uint32_t) ld_u16(p + 2) << 16);
+        g1 = (uint32_t) ld_u16(p + 4) | ((uint32_t) ld_u16(p + 6) << 16);
+        a = (uint32_t) ld_u16(b + 66 + 4 * L) | ((uint32_t) ld_u16(b + 68 + 4 * L) << 16);
+        d = ld_u16(b);
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
+        const uint32_t *ya = (const uint32_t *) (y + 4 + 32 * L);
+        int s = 0;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t gw = l < 2 ? g0 : g1, sh = 16 * (l & 1);
+            const uint2 m = grid[256 + ((a >> (7 * l)) & 127)];
+            s = sdot4(apply_mask(grid[(gw >> sh) & 255].x, m.x), ya[2 * l], s);
+            s = sdot4(apply_mask(grid[(gw >> (sh + 8)) & 255].x, m.y), ya[2 * l + 1], s);
+        }
+        si = (2 * (int) (a >> 28) + 1) * s;
+        sm = 0;
+    }
+    __device__ __forceinline__ float tval(int si, int) const { return (h2f(d) * 0.25f) * (float) si; }
+};
 // Q3_K (110 B: hmask[32] @0, qs[64] @32, scales[12] @96, d @108), src/kernels4.cu:698-707.  Value e = 128 hf + 32 j + l
 // is the 2-bit field 2 j of qs byte 32 hf + l, less 4 where bit 4 hf + j of hmask[l] is clear; 16-group is = e >> 4
 // has the signed 6-bit scale (scales[is & 7] >> 4 (is >> 3) & 15 | (scales[8 + (is & 3)] >> 2 (is >> 2) & 3) << 4) - 32.
@@ -390,9 +420,9 @@ template <> struct Item<Q5_0> {
     __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
 };
 
-// expand an IQ2 codebook (base-3 codes: IQ2_XS 512 rows, IQ2_XXS 256) into rows x 8 bytes of LDS, followed by the
-// 128 sign patterns as byte masks (entry rows + i: byte j = 0xFF where bit j of ksign(i) is set, the parity bit giving
-// byte 7)
+// expand a grid codebook (base-3 codes: IQ2_XS 512 rows, IQ2_XXS 256; base-8 codes: IQ3_XXS 256 rows of 4 bytes, in
+// .x) into rows x 8 bytes of LDS, followed by the 128 sign patterns as byte masks (entry rows + i: byte j = 0xFF where
+// bit j of ksign(i) is set, the parity bit giving byte 7)
 template <int T>
 __device__ __forceinline__ void expand_iq2_grid(uint2 *grid) {
     static_assert(iq2_type(T), "an IQ2 codebook");
@@ -401,6 +431,13 @@ __device__ __forceinline__ void expand_iq2_grid(uint2 *grid) {
         if (i >= R) {
             const uint32_t ks = ksign((uint32_t) i - R);
             grid[i] = make_uint2(spread4(ks & 15) * 0xFFu, spread4(ks >> 4) * 0xFFu);
+            continue;
+        }
+        if constexpr (T == IQ3_XXS) {
+            uint32_t c = c_iq3xxs_code[i], lo = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j, c >>= 3) lo |= ((c & 7) == 7 ? 62u : 4u + 8u * (c & 7)) << (8 * j);
+            grid[i] = make_uint2(lo, 0u);
             continue;
         }
         uint32_t c = T == IQ2_XS ? c_iq2xs_code[i] : c_iq2xxs_code[i], lo = 0, hi = 0;

@@ -122,6 +122,30 @@ template <> struct Raw<Q2_K> {
         return __builtin_fmaf(h2f(dm & 0xffff), (float) si, -(h2f(dm >> 16) * (float) sm));
     }
 };
+// IQ3_XXS (98 B): chunk c = 32-group c; lane q takes 8-group q: grid indices qs[8 c + 2 q], qs[8 c + 2 q + 1] (a
+// halfword at 2 + 8 c + 2 q), sign index bits 7 q .. of the word at 66 + 4 c, the chunk's scale 2 sc + 1 (bits 28 ..)
+// (src/kernels4.cu:613-627; ggml's vec_dot_iq3_xxs_q8_K integers).
+template <> struct Raw<IQ3_XXS> {
+    static constexpr bool mins = false, g16 = false, per_chunk = false;
+    uint32_t gi[4], a[8], d;   // gi: the lane's index pair of chunk c in halfword c % 2 of gi[c / 2]
+    __device__ __forceinline__ void load(const uint8_t *blk, int q) {
+#pragma unroll
+        for (int c = 0; c < 8; c += 2)
+            gi[c >> 1] = (uint32_t) ld_u16(blk + 2 + 8 * c + 2 * q) | ((uint32_t) ld_u16(blk + 10 + 8 * c + 2 * q) << 16);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) a[c] = (uint32_t) ld_u16(blk + 66 + 4 * c) | ((uint32_t) ld_u16(blk + 68 + 4 * c) << 16);
+        d = ld_u16(blk);
+    }
+    __device__ __forceinline__ void chunk(int c, int q, const uint2 *grid, uint32_t &b0, uint32_t &b1, int &s0, int &s1, int &mn) const {
+        const uint32_t ip = gi[c >> 1] >> (16 * (c & 1));
+        const uint2 m = grid[256 + ((a[c] >> (7 * q)) & 127)];
+        b0 = apply_mask(grid[ip & 255].x, m.x);
+        b1 = apply_mask(grid[(ip >> 8) & 255].x, m.y);
+        s0 = 2 * (int) (a[c] >> 28) + 1;
+        s1 = 0; mn = 0;
+    }
+    __device__ __forceinline__ float fold(int si, int) const { return (h2f(d) * 0.25f) * (float) si; }
+};
 // Q3_K (110 B: hmask[32], qs[64] @32, scales[12] @96, d @108): chunk c = values 32 c .., hf = c >> 2, j = c & 3; lane
 // values l = 8 q .. + 7: 2-bit fields 2 j of qs bytes 32 + 32 hf + l, each byte OR 0xFC where bit 4 hf + j of hmask[l]
 // is clear (q - 4 as int8); 16-groups 2 c (lanes q < 2) and 2 c + 1 with their signed 6-bit scales.  Blocks are 2-byte
@@ -1129,6 +1153,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
     case IQ2_XXS: { constexpr int TT = IQ2_XXS; __VA_ARGS__; }                                           \
     case Q2_K: { constexpr int TT = Q2_K; __VA_ARGS__; }                                                 \
     case Q3_K: { constexpr int TT = Q3_K; __VA_ARGS__; }                                                 \
+    case IQ3_XXS: { constexpr int TT = IQ3_XXS; __VA_ARGS__; }                                           \
     default: set_error("grouped GEMM: unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 

@@ -164,6 +164,7 @@ static int launch_gemv_t(const hy_moe_dev &m, const float *src, int ss, const in
     case Q5_0: { constexpr int TT = Q5_0; CALL; }                                        \
     case Q2_K: { constexpr int TT = Q2_K; CALL; }                                        \
     case Q3_K: { constexpr int TT = Q3_K; CALL; }                                        \
+    case IQ3_XXS: { constexpr int TT = IQ3_XXS; CALL; }                                  \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 
@@ -367,6 +368,7 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, floa
     __shared__ uint2 grid[IQ2XS_LDS];
     if (type == IQ2_XS) expand_iq2_grid<IQ2_XS>(grid);
     else if (type == IQ2_XXS) expand_iq2_grid<IQ2_XXS>(grid);
+    else if (type == IQ3_XXS) expand_iq2_grid<IQ3_XXS>(grid);
     __syncthreads();
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -419,6 +421,14 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, floa
         const uint8_t *b = row + (size_t) (i >> 5) * 17;
         const int e = i & 31;
         v = (float) (int8_t) (kvfp4((b[1 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF) & 0xff) * e8m0_half(b[0]);
+    } else if (type == IQ3_XXS) {   // src/kernels4.cu:613-627
+        const uint8_t *b = row + (size_t) (i >> 8) * 98;
+        const int e = i & 255, ib = e >> 5, l = (e >> 3) & 3, j = e & 7;
+        const uint32_t a = (uint32_t) ld_u16(b + 66 + 4 * ib) | ((uint32_t) ld_u16(b + 68 + 4 * ib) << 16);
+        const float db = h2f(ld_u16(b)) * (0.5f + (float) (a >> 28)) * 0.5f;
+        const uint32_t gr = grid[b[2 + 8 * ib + 2 * l + (j >> 2)]].x;
+        const float gv = (float) ((gr >> (8 * (j & 3))) & 0xff);
+        v = (db * gv) * ((ksign((a >> (7 * l)) & 127) >> j) & 1 ? -1.0f : 1.0f);
     } else if (type == Q3_K) {   // src/kernels4.cu:698-707
         const uint8_t *b = row + (size_t) (i >> 8) * 110;
         const int e = i & 255, is = e >> 4, hf = e >> 7, j = (e >> 5) & 3, l = e & 31;

@@ -30,6 +30,7 @@ size_t or_block_bytes(int type) {
     case OR_Q5_0: return 22;
     case OR_Q2_K: return 84;
     case OR_Q3_K: return 110;
+    case OR_IQ3_XXS: return 98;
     default: return 0;
     }
 }
@@ -37,7 +38,7 @@ int or_block_elems(int type) {
     switch (type) {
     case OR_Q8_0: case OR_IQ4_NL: case OR_MXFP4: case OR_Q5_0: return 32;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_Q8_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K:
-    case OR_Q3_K: return 256;
+    case OR_Q3_K: case OR_IQ3_XXS: return 256;
     default: return 0;
     }
 }
@@ -46,7 +47,8 @@ int or_block_elems(int type) {
 int or_vec_dot_type(int type) {
     switch (type) {
     case OR_IQ4_NL: case OR_Q8_0: case OR_MXFP4: case OR_Q5_0: return OR_Q8_0;
-    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K: case OR_Q3_K: return OR_Q8_K;
+    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K: case OR_Q3_K: case OR_IQ3_XXS:
+        return OR_Q8_K;
     default: return -1;
     }
 }
@@ -73,9 +75,14 @@ static const uint16_t iq2xs_code[512] = {
 static const uint16_t iq2xxs_code[256] = {
 #include "../hyper_amd/csrc/iq2xxs_grid.inc"
 };
-static uint8_t iq2xs_rows[512][8], iq2xxs_rows[256][8];
+/* IQ3_XXS codebook: 256 rows of 4 bytes, base-8 coded, digit i = byte i's level 4 + 8 d (62 for d = 7) (values of
+   src/iq_grids.h:468-503) */
+static const uint16_t iq3xxs_code[256] = {
+#include "../hyper_amd/csrc/iq3xxs_grid.inc"
+};
+static uint8_t iq2xs_rows[512][8], iq2xxs_rows[256][8], iq3xxs_rows[256][4];
 static int iq2xs_ready = 0;
-static void iq2xs_init(void) {   /* both IQ2 codebooks */
+static void iq2xs_init(void) {   /* the grid codebooks */
     if (__atomic_load_n(&iq2xs_ready, __ATOMIC_ACQUIRE)) return;
     static const uint8_t lv[3] = {8, 25, 43};
     for (int i = 0; i < 512; ++i) {
@@ -85,6 +92,10 @@ static void iq2xs_init(void) {   /* both IQ2 codebooks */
     for (int i = 0; i < 256; ++i) {
         unsigned c = iq2xxs_code[i];
         for (int j = 0; j < 8; ++j) { iq2xxs_rows[i][j] = lv[c % 3]; c /= 3; }
+    }
+    for (int i = 0; i < 256; ++i) {
+        unsigned c = iq3xxs_code[i];
+        for (int j = 0; j < 4; ++j) { iq3xxs_rows[i][j] = (uint8_t) ((c & 7) == 7 ? 62 : 4 + 8 * (c & 7)); c >>= 3; }
     }
     __atomic_store_n(&iq2xs_ready, 1, __ATOMIC_RELEASE);
 }
@@ -283,6 +294,16 @@ static inline int iq2xxs_q(const uint8_t *b, int e) {   /* signed grid value of 
     const int g = iq2xxs_rows[b[2 + 8 * ib + l]][j];
     return (ksign((iq2xxs_a1(b, ib) >> (7 * l)) & 127) >> j) & 1 ? -g : g;
 }
+/* IQ3_XXS (src/kernels4.cu:613-627): 32-group ib has the grid indices qs[8 ib .. 8 ib + 7] at 2 (two 4-byte rows per
+   8-group l) and the word at 66 + 4 ib: 4 x 7 sign indices and the 4-bit scale in bits 28..31 */
+static inline unsigned iq3xxs_a(const uint8_t *b, int ib) {
+    return (unsigned) b[66 + 4 * ib] | ((unsigned) b[67 + 4 * ib] << 8) | ((unsigned) b[68 + 4 * ib] << 16) | ((unsigned) b[69 + 4 * ib] << 24);
+}
+static inline int iq3xxs_q(const uint8_t *b, int e) {   /* signed grid value of element e */
+    const int ib = e >> 5, l = (e >> 3) & 3, j = e & 7;
+    const int g = iq3xxs_rows[b[2 + 8 * ib + 2 * l + (j >> 2)]][j & 3];
+    return (ksign((iq3xxs_a(b, ib) >> (7 * l)) & 127) >> j) & 1 ? -g : g;
+}
 static inline int iq2xs_sc(const uint8_t *b, int e) {
     const int ib = e >> 5, l = (e >> 3) & 3;
     return (b[66 + ib] >> (4 * (l >> 1))) & 0xF;
@@ -335,6 +356,13 @@ int or_dequant_row(int type, const uint8_t *row, int n, float *out) {
             break;
         case OR_Q8_0:
             for (int e = 0; e < 32; ++e) o[e] = h2f(b) * (float) (int8_t) b[2 + e];
+            break;
+        case OR_IQ3_XXS:
+            for (int e = 0; e < 256; ++e) {
+                const float db = h2f(b) * (0.5f + (float) (iq3xxs_a(b, e >> 5) >> 28)) * 0.5f;
+                const int q = iq3xxs_q(b, e);
+                o[e] = (db * (float) (q < 0 ? -q : q)) * (q < 0 ? -1.0f : 1.0f);
+            }
             break;
         case OR_MXFP4:
             for (int e = 0; e < 32; ++e) o[e] = (float) mxfp4_q(b, e) * e8m0_half(b[0]);
@@ -417,6 +445,13 @@ static void block_ints_scalar(int type, const uint8_t *b, const uint8_t *y, int3
         break;
     case OR_Q5_0:      /* ggml's vec_dot_q5_0_q8_0 integer part: sum_32 (x - 16) q8 */
         for (int l = 0; l < 32; ++l) si += q5_0_q(b, l) * q8[l];
+        break;
+    case OR_IQ3_XXS:   /* ggml's vec_dot_iq3_xxs_q8_K: sum_ib (2 sc + 1) sum_32 grid sign y */
+        for (int ib = 0; ib < 8; ++ib) {
+            int32_t s = 0;
+            for (int l = 0; l < 32; ++l) s += iq3xxs_q(b, 32 * ib + l) * q8[32 * ib + l];
+            si += (2 * (int) (iq3xxs_a(b, ib) >> 28) + 1) * s;
+        }
         break;
     case OR_Q3_K:      /* ggml's vec_dot_q3_K_q8_K: sum_g sc_g sum_16 q y */
         for (int g = 0; g < 16; ++g) {
@@ -519,7 +554,8 @@ static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *su
 
 static int dot_ok(int type) {
     return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_IQ4_XS || type == OR_IQ2_XS || type == OR_IQ4_NL ||
-           type == OR_Q8_0 || type == OR_IQ2_XXS || type == OR_MXFP4 || type == OR_Q5_0 || type == OR_Q2_K || type == OR_Q3_K;
+           type == OR_Q8_0 || type == OR_IQ2_XXS || type == OR_MXFP4 || type == OR_Q5_0 || type == OR_Q2_K || type == OR_Q3_K ||
+           type == OR_IQ3_XXS;
 }
 int or_block_ints(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ) {
     if (!dot_ok(type) || n % or_block_elems(type)) return -1;
@@ -551,6 +587,7 @@ static float row_dot(int type, const uint8_t *row, const uint8_t *xq, int n) {
         case OR_Q4_K: case OR_Q5_K: t = fmaf(h2f(b), (float) si, -(h2f(b + 2) * (float) sm)); break;
         case OR_Q6_K: t = h2f(b + 208) * (float) si; break;
         case OR_Q3_K: t = h2f(b + 108) * (float) si; break;
+        case OR_IQ3_XXS: t = (h2f(b) * 0.25f) * (float) si; break;
         case OR_Q2_K: t = fmaf(h2f(b + 80), (float) si, -(h2f(b + 82) * (float) sm)); break;
         case OR_IQ2_XS: case OR_IQ2_XXS: t = (h2f(b) * 0.125f) * (float) si; break;
         case OR_MXFP4: t = e8m0_half(b[0]) * (float) si; break;

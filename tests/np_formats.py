@@ -131,6 +131,20 @@ def q3k(b):
     return dict(q=np.concatenate(vals, axis=1), sc=sc, m=None, gsize=16, d=f16(b[:, 108:110]))
 
 
+def iq3xxs(b, grid_rows, ksigns):
+    """grid_rows: [256, 4] codebook bytes, ksigns: [128] sign bytes.  32-group ib: eight grid indices at 2 + 8 ib
+    (8-group l: rows 2 l and 2 l + 1, four values each), then a little-endian word at 66 + 4 ib with the four 7-bit sign
+    indices (bits 7 l ..) and the 4-bit scale (bits 28 ..)."""
+    b = b.reshape(-1, 98)
+    idx = b[:, 2:66].astype(np.int64).reshape(-1, 8, 4, 2)                       # [ib][l][half]
+    g = grid_rows[idx].astype(np.int64).reshape(-1, 8, 4, 8)                     # [ib][l][8 values]
+    a = np.ascontiguousarray(b[:, 66:98]).view(np.uint32).astype(np.int64).reshape(-1, 8)
+    sgn = ksigns[np.stack([(a >> (7 * l)) & 127 for l in range(4)], axis=2)].astype(np.int64)
+    bits = (sgn[..., None] >> np.arange(8)) & 1
+    q = np.where(bits == 1, -g, g).reshape(-1, 256)
+    return dict(q=q, sc=2 * (a >> 28) + 1, m=None, gsize=32, d=f16(b[:, 0:2]))
+
+
 def q5_0w(b):
     """Q5_0 weights: d f16 @0, qh little-endian u32 @2, qs[16] @6; value j = (nibble j + 16 * bit j of qh) - 16, the
     nibbles in qs order, low halves first (values 0..15), then high halves (16..31)."""
@@ -191,6 +205,7 @@ def decode(t, b, grid_rows=None, ksigns=None):
     if t == 6: return q5_0w(b)
     if t == 10: return q2k(b)
     if t == 11: return q3k(b)
+    if t == 18: return iq3xxs(b, grid_rows, ksigns)
     if t == 17: return iq2xs(b, grid_rows, ksigns)
     if t == 16: return iq2xxs(b, grid_rows, ksigns)
     raise ValueError(t)
@@ -215,8 +230,8 @@ def dequant(t, b, grid_rows=None, ksigns=None):
         return (q.astype(np.float32) * d).astype(np.float32)
     if t == 8:
         return (d * q.astype(np.float32)).astype(np.float32)
-    if t in (16, 17):
-        db = (d * (np.float32(0.5) + ((sc - 1) / 2).astype(np.float32))) * np.float32(0.25)
+    if t in (16, 17, 18):
+        db = (d * (np.float32(0.5) + ((sc - 1) / 2).astype(np.float32))) * np.float32(0.5 if t == 18 else 0.25)
         return ((db * np.abs(q).astype(np.float32)) * np.where(q < 0, np.float32(-1), np.float32(1))).astype(np.float32)
     raise ValueError(t)
 

@@ -68,6 +68,8 @@ ROUTE_GU_CASES = [
     (GType.Q5_0, GType.Q5_0, 32, 2048, 768, 8, 2, True),
     (GType.Q2_K, GType.Q2_K, 64, 2048, 1024, 8, 3, False),
     (GType.Q3_K, GType.Q3_K, 48, 2048, 768, 6, 2, True),
+    (GType.IQ3_XXS, GType.IQ3_XXS, 16, 7168, 2048, 6, 2, True),
+    (GType.IQ3_XXS, GType.IQ2_XXS, 20, 2048, 768, 8, 3, False),
 ]
 
 

@@ -59,8 +59,25 @@ def iq2xxs_rows() -> np.ndarray:
     return rows
 
 
+def iq3xxs_rows() -> np.ndarray:
+    """The IQ3_XXS codebook as the kernels and the oracle expand it from iq3xxs_grid.inc (base-8 digits: byte i's
+    level 4 + 8 d, 62 for d = 7)."""
+    text = (Path(__file__).resolve().parents[1] / "hyper_amd/csrc/iq3xxs_grid.inc").read_text()
+    body = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("//"))
+    codes = [int(v) for v in body.replace(",", " ").split() if v.isdigit()]
+    assert len(codes) == 256
+    lv = np.array([4, 12, 20, 28, 36, 44, 52, 62], np.uint8)
+    rows = np.zeros((256, 4), np.uint8)
+    for i, c in enumerate(codes):
+        for j in range(4):
+            rows[i, j] = lv[c % 8]
+            c //= 8
+    return rows
+
+
 def grid_for(t):
-    return iq2xxs_rows() if GType(t) == GType.IQ2_XXS else iq2xs_rows()
+    t = GType(t)
+    return iq2xxs_rows() if t == GType.IQ2_XXS else iq3xxs_rows() if t == GType.IQ3_XXS else iq2xs_rows()
 
 
 def ksigns() -> np.ndarray:
@@ -71,6 +88,7 @@ def test_codebooks_match_reference():
     rows = iq2xs_rows()
     assert hashlib.sha256(rows.tobytes()).hexdigest() == TABLES["iq2xs_grid_sha256"]
     assert hashlib.sha256(iq2xxs_rows().tobytes()).hexdigest() == TABLES["iq2xxs_grid_sha256"]
+    assert hashlib.sha256(iq3xxs_rows().tobytes()).hexdigest() == TABLES["iq3xxs_grid_sha256"]
     assert hashlib.sha256(ksigns().tobytes()).hexdigest() == TABLES["ksigns_sha256"]
     assert hashlib.sha256(nf.KV_IQ4NL.astype(np.int8).tobytes()).hexdigest() == TABLES["iq4nl_sha256"]
     assert all(bin(int(s)).count("1") % 2 == 0 for s in ksigns())   # every sign byte has an even bit count
@@ -263,6 +281,35 @@ def test_iq2xxs_known_answer_positions():
     assert not sm.any()
 
 
+def test_iq3xxs_known_answer_positions():
+    """IQ3_XXS (src/kernels4.cu:613-627): 32-group ib's grid indices are bytes 2 + 8 ib .. (8-group l: rows 2 l, 2 l + 1
+    of 4 bytes each), its word at 66 + 4 ib holds the four 7-bit sign indices (bits 7 l ..) and the 4-bit scale (bits
+    28 ..); value = d (0.5 + sc) / 2 * grid * sign.  Rows fixed by the reference's table: row 0 is all 4s, row 1 =
+    0x04040414 (byte 0 = 20).  With d = 1: group 0's 8-group 1 takes rows 1, 0 and sign index 1 (ksign(1) = 0x81:
+    elements 0 and 7 negated), scale 0 (db = 1/4); group 1 has scale 15 (db = 7.75); the rest row 0, scale 0."""
+    rows = iq3xxs_rows()
+    assert list(rows[0]) == [4] * 4 and list(rows[1]) == [20, 4, 4, 4]
+    blk = np.zeros(98, np.uint8)
+    blk[0:2] = _f16b(1.0)
+    blk[2 + 2] = 1                                                         # group 0, 8-group 1, first row: 1
+    blk[66:70] = np.frombuffer(np.uint32(1 << 7).tobytes(), np.uint8)     # group 0: sign index 1 on 8-group 1
+    blk[70:74] = np.frombuffer(np.uint32(15 << 28).tobytes(), np.uint8)   # group 1: scale 15
+    want = np.ones(256, np.float32)
+    want[8:16] = [-5, 1, 1, 1, 1, 1, 1, -1]
+    want[32:64] = 31.0
+    got = orc.dequant_row(GType.IQ3_XXS, blk, 256)
+    assert (got == want).all(), np.nonzero(got != want)
+    x = np.arange(256, dtype=np.float32) % 7 - 3.0
+    xq = orc.quantize(GType.Q8_K, x)
+    q8 = xq[4:260].view(np.int8).astype(np.int64)
+    ints = (want * 4).astype(np.int64)                          # grid * sign at scale 0; group 1's rows stay 4s
+    ints[32:64] = 4
+    scale = np.array([1] + [31] + [1] * 6, np.int64)            # 2 sc + 1 per 32-group
+    si, sm = orc.block_ints(GType.IQ3_XXS, blk, xq, 256)
+    assert int(si[0]) == int(sum(scale[g] * (ints[32 * g:32 * g + 32] @ q8[32 * g:32 * g + 32]) for g in range(8)))
+    assert not sm.any()
+
+
 def test_q8_0_weight_known_answers():
     """Q8_0 weights (src/kernels4.cu:421-714, deq8: d * qs[j]): value j of a block is d * (int8) qs[j] in place, and
     against a Q8_0 activation block the integer is sum_j qs[j] y[j] (ggml's vec_dot_q8_0_q8_0), folded as
@@ -429,7 +476,7 @@ def test_q8k_known_answers():
 # ------------------------------------------------------------------ block decoding
 
 ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.IQ4_NL, GType.Q8_0, GType.MXFP4,
-       GType.Q5_0, GType.Q2_K, GType.Q3_K]
+       GType.Q5_0, GType.Q2_K, GType.Q3_K, GType.IQ3_XXS]
 
 
 def blocks(t, nb, seed):
