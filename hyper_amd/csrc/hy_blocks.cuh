@@ -49,9 +49,11 @@ __device__ __forceinline__ uint32_t apply_sign(uint32_t g, uint32_t b4) {
 // the same with the byte mask given (0xFF per negated byte): -g = ~g + 1 per byte, no carry (codebook bytes are not 0)
 __device__ __forceinline__ uint32_t apply_mask(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
 // LDS entries of an expanded IQ2_XS codebook: 512 rows, then 128 sign masks (IQ2_XXS: 256 rows, then the masks)
-constexpr int IQ2XS_LDS = 512 + 128;
-__host__ __device__ constexpr int iq2_rows(int t) { return t == IQ2_XS ? 512 : 256; }
-__host__ __device__ constexpr int iq2_lds(int t) { return iq2_type(t) ? iq2_rows(t) + 128 : 1; }   // uint2 entries
+__host__ __device__ constexpr int iq2_rows(int t) { return t == IQ2_XS || t == IQ3_S ? 512 : 256; }
+// sign masks after the rows: the 128 ksign patterns, or for IQ3_S (literal sign bytes) all 256 bytes
+__host__ __device__ constexpr int iq2_masks(int t) { return t == IQ3_S ? 256 : 128; }
+__host__ __device__ constexpr int iq2_lds(int t) { return iq2_type(t) ? iq2_rows(t) + iq2_masks(t) : 1; }   // uint2 entries
+constexpr int GRID_LDS = 512 + 256;   // the largest of them (IQ3_S)
 // Q6_K: q6 bytes (0..63) -> q6 - 32 as int8: per byte (q + 96) ^ 128 = q - 32 mod 256 (q + 96 < 256: no carry)
 __device__ __forceinline__ uint32_t q6_signed(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
 
@@ -170,6 +172,39 @@ template <> struct Item<IQ3_XXS> {
         sm = 0;
     }
     __device__ __forceinline__ float tval(int si, int) const { return (h2f(d) * 0.25f) * (float) si; }
+};
+// IQ3_S (110 B: d, qs[64] @2, qh[8] @66, signs[32] @74, scales[4] @106), src/kernels4.cu:682-695.  Lane L = 32-group
+// L: 8-group l takes grid rows qs[8 L + 2 l] | bit 2 l of qh[L] << 8 and qs[8 L + 2 l + 1] | bit 2 l + 1 << 8 (4-byte
+// rows of the 512-row codebook), sign byte signs[4 L + l] (bit j negates value j), scale 2 sc + 1 with sc nibble L & 1
+// of scales[L / 2] (the integers of the reference's own IQ3_S x Q8_K dot, src/iq3s_dot.h:48-76: sumi = sum_ib
+// (2 sc + 1) sum_32 grid sign y).  Blocks are 2-byte aligned (110-byte rows).
+template <> struct Item<IQ3_S> {
+    uint32_t g0, g1, sg, hs;   // the lane's 8 index bytes; its 4 sign bytes; qh byte | scale nibble << 8
+    uint16_t d;
+    const uint2 *grid;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+        const uint8_t *p = b + 2 + 8 * L;
+        g0 = (uint32_t) ld_u16(p) | ((uint32_t) ld_u16(p + 2) << 16);
+        g1 = (uint32_t) ld_u16(p + 4) | ((uint32_t) ld_u16(p + 6) << 16);
+        sg = (uint32_t) ld_u16(b + 74 + 4 * L) | ((uint32_t) ld_u16(b + 76 + 4 * L) << 16);
+        hs = (uint32_t) b[66 + L] | ((uint32_t) ((b[106 + (L >> 1)] >> (4 * (L & 1))) & 15) << 8);
+        d = ld_u16(b);
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
+        const uint32_t *ya = (const uint32_t *) (y + 4 + 32 * L);
+        int s = 0;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t gw = l < 2 ? g0 : g1, sh = 16 * (l & 1);
+            const uint32_t i1 = ((gw >> sh) & 255) | (((hs >> (2 * l)) & 1) << 8), i2 = ((gw >> (sh + 8)) & 255) | (((hs >> (2 * l + 1)) & 1) << 8);
+            const uint2 m = grid[512 + ((sg >> (8 * l)) & 255)];
+            s = sdot4(apply_mask(grid[i1].x, m.x), ya[2 * l], s);
+            s = sdot4(apply_mask(grid[i2].x, m.y), ya[2 * l + 1], s);
+        }
+        si = (2 * (int) (hs >> 8) + 1) * s;
+        sm = 0;
+    }
+    __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
 };
 // Q3_K (110 B: hmask[32] @0, qs[64] @32, scales[12] @96, d @108), src/kernels4.cu:698-707.  Value e = 128 hf + 32 j + l
 // is the 2-bit field 2 j of qs byte 32 hf + l, less 4 where bit 4 hf + j of hmask[l] is clear; 16-group is = e >> 4
@@ -420,16 +455,16 @@ template <> struct Item<Q5_0> {
     __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
 };
 
-// expand a grid codebook (base-3 codes: IQ2_XS 512 rows, IQ2_XXS 256; base-8 codes: IQ3_XXS 256 rows of 4 bytes, in
-// .x) into rows x 8 bytes of LDS, followed by the 128 sign patterns as byte masks (entry rows + i: byte j = 0xFF where
-// bit j of ksign(i) is set, the parity bit giving byte 7)
+// expand a grid codebook (base-3 codes: IQ2_XS 512 rows, IQ2_XXS 256; base-8 codes: IQ3_XXS 256 and IQ3_S 512 rows of
+// 4 bytes, in .x) into rows x 8 bytes of LDS, followed by the sign patterns as byte masks (entry rows + i: byte j = 0xFF
+// where bit j of ksign(i) is set, the parity bit giving byte 7; for IQ3_S bit j of i itself, i < 256)
 template <int T>
 __device__ __forceinline__ void expand_iq2_grid(uint2 *grid) {
     static_assert(iq2_type(T), "an IQ2 codebook");
     constexpr int R = iq2_rows(T);
-    for (int i = threadIdx.x; i < R + 128; i += blockDim.x) {
+    for (int i = threadIdx.x; i < R + iq2_masks(T); i += blockDim.x) {
         if (i >= R) {
-            const uint32_t ks = ksign((uint32_t) i - R);
+            const uint32_t ks = T == IQ3_S ? (uint32_t) i - R : ksign((uint32_t) i - R);
             grid[i] = make_uint2(spread4(ks & 15) * 0xFFu, spread4(ks >> 4) * 0xFFu);
             continue;
         }
@@ -437,6 +472,13 @@ __device__ __forceinline__ void expand_iq2_grid(uint2 *grid) {
             uint32_t c = c_iq3xxs_code[i], lo = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j, c >>= 3) lo |= ((c & 7) == 7 ? 62u : 4u + 8u * (c & 7)) << (8 * j);
+            grid[i] = make_uint2(lo, 0u);
+            continue;
+        }
+        if constexpr (T == IQ3_S) {
+            uint32_t c = c_iq3s_code[i], lo = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j, c >>= 3) lo |= (2u * (c & 7) + 1u) << (8 * j);
             grid[i] = make_uint2(lo, 0u);
             continue;
         }

@@ -146,6 +146,35 @@ template <> struct Raw<IQ3_XXS> {
     }
     __device__ __forceinline__ float fold(int si, int) const { return (h2f(d) * 0.25f) * (float) si; }
 };
+// IQ3_S (110 B): chunk c = 32-group c; lane q takes 8-group q: grid indices qs[8 c + 2 q], qs[8 c + 2 q + 1] with bits
+// 2 q, 2 q + 1 of qh[c] as their 9th bits, sign byte signs[4 c + q], the chunk's scale 2 sc + 1 (nibble c & 1 of
+// scales[c / 2]) (src/kernels4.cu:682-695; src/iq3s_dot.h:48-76 integers).
+template <> struct Raw<IQ3_S> {
+    static constexpr bool mins = false, g16 = false, per_chunk = false;
+    uint32_t gi[4], qh[2], sg[2], sc, d;   // gi: index pairs (halfword c % 2 of gi[c / 2]); qh, sg: byte c % 4 of [c / 4]
+    __device__ __forceinline__ void load(const uint8_t *blk, int q) {
+#pragma unroll
+        for (int c = 0; c < 8; c += 2)
+            gi[c >> 1] = (uint32_t) ld_u16(blk + 2 + 8 * c + 2 * q) | ((uint32_t) ld_u16(blk + 10 + 8 * c + 2 * q) << 16);
+        qh[0] = (uint32_t) ld_u16(blk + 66) | ((uint32_t) ld_u16(blk + 68) << 16);
+        qh[1] = (uint32_t) ld_u16(blk + 70) | ((uint32_t) ld_u16(blk + 72) << 16);
+        sg[0] = sg[1] = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) sg[c >> 2] |= (uint32_t) blk[74 + 4 * c + q] << (8 * (c & 3));
+        sc = (uint32_t) ld_u16(blk + 106) | ((uint32_t) ld_u16(blk + 108) << 16);
+        d = ld_u16(blk);
+    }
+    __device__ __forceinline__ void chunk(int c, int q, const uint2 *grid, uint32_t &b0, uint32_t &b1, int &s0, int &s1, int &mn) const {
+        const uint32_t ip = gi[c >> 1] >> (16 * (c & 1)), h = qh[c >> 2] >> (8 * (c & 3));
+        const uint32_t i1 = (ip & 255) | (((h >> (2 * q)) & 1) << 8), i2 = ((ip >> 8) & 255) | (((h >> (2 * q + 1)) & 1) << 8);
+        const uint2 m = grid[512 + ((sg[c >> 2] >> (8 * (c & 3))) & 255)];
+        b0 = apply_mask(grid[i1].x, m.x);
+        b1 = apply_mask(grid[i2].x, m.y);
+        s0 = 2 * (int) ((sc >> (4 * c)) & 15) + 1;
+        s1 = 0; mn = 0;
+    }
+    __device__ __forceinline__ float fold(int si, int) const { return h2f(d) * (float) si; }
+};
 // Q3_K (110 B: hmask[32], qs[64] @32, scales[12] @96, d @108): chunk c = values 32 c .., hf = c >> 2, j = c & 3; lane
 // values l = 8 q .. + 7: 2-bit fields 2 j of qs bytes 32 + 32 hf + l, each byte OR 0xFC where bit 4 hf + j of hmask[l]
 // is clear (q - 4 as int8); 16-groups 2 c (lanes q < 2) and 2 c + 1 with their signed 6-bit scales.  Blocks are 2-byte
@@ -1154,6 +1183,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
     case Q2_K: { constexpr int TT = Q2_K; __VA_ARGS__; }                                                 \
     case Q3_K: { constexpr int TT = Q3_K; __VA_ARGS__; }                                                 \
     case IQ3_XXS: { constexpr int TT = IQ3_XXS; __VA_ARGS__; }                                           \
+    case IQ3_S: { constexpr int TT = IQ3_S; __VA_ARGS__; }                                               \
     default: set_error("grouped GEMM: unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 

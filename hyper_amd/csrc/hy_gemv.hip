@@ -165,6 +165,7 @@ static int launch_gemv_t(const hy_moe_dev &m, const float *src, int ss, const in
     case Q2_K: { constexpr int TT = Q2_K; CALL; }                                        \
     case Q3_K: { constexpr int TT = Q3_K; CALL; }                                        \
     case IQ3_XXS: { constexpr int TT = IQ3_XXS; CALL; }                                  \
+    case IQ3_S: { constexpr int TT = IQ3_S; CALL; }                                      \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 
@@ -365,10 +366,11 @@ int launch_down_reduce(const hy_moe_dev &m, const float *h, const int *ids, cons
 // ---------------------------------------------------------------- test hooks
 // one row dequantized with the deq8 expressions (src/kernels4.cu:421-714): thread per value
 __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, float *__restrict__ out) {
-    __shared__ uint2 grid[IQ2XS_LDS];
+    __shared__ uint2 grid[GRID_LDS];
     if (type == IQ2_XS) expand_iq2_grid<IQ2_XS>(grid);
     else if (type == IQ2_XXS) expand_iq2_grid<IQ2_XXS>(grid);
     else if (type == IQ3_XXS) expand_iq2_grid<IQ3_XXS>(grid);
+    else if (type == IQ3_S) expand_iq2_grid<IQ3_S>(grid);
     __syncthreads();
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -421,6 +423,13 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, floa
         const uint8_t *b = row + (size_t) (i >> 5) * 17;
         const int e = i & 31;
         v = (float) (int8_t) (kvfp4((b[1 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF) & 0xff) * e8m0_half(b[0]);
+    } else if (type == IQ3_S) {   // src/kernels4.cu:682-695
+        const uint8_t *b = row + (size_t) (i >> 8) * 110;
+        const int e = i & 255, ib = e >> 5, l = (e >> 3) & 3, j = e & 7, hb = 2 * l + (j >> 2);
+        const float db = h2f(ld_u16(b)) * (float) (1 + 2 * ((b[106 + (ib >> 1)] >> (4 * (ib & 1))) & 15));
+        const uint32_t gr = grid[b[2 + 8 * ib + hb] | (((b[66 + ib] >> hb) & 1) << 8)].x;
+        const float gv = (float) ((gr >> (8 * (j & 3))) & 0xff);
+        v = (db * gv) * ((b[74 + 4 * ib + l] >> j) & 1 ? -1.0f : 1.0f);
     } else if (type == IQ3_XXS) {   // src/kernels4.cu:613-627
         const uint8_t *b = row + (size_t) (i >> 8) * 98;
         const int e = i & 255, ib = e >> 5, l = (e >> 3) & 3, j = e & 7;
@@ -467,7 +476,7 @@ int launch_dequant_row(int type, const uint8_t *row, int n, float *out, hipStrea
 template <int T>
 __global__ __launch_bounds__(256) void k_block_ints(const uint8_t *__restrict__ rows, size_t row_bytes, int nrows, const uint8_t *__restrict__ xq,
                                                     int n, int *__restrict__ sumi, int *__restrict__ summ) {
-    __shared__ uint2 grid[IQ2XS_LDS];
+    __shared__ uint2 grid[GRID_LDS];
     __shared__ __align__(16) uint8_t y0[8 * Q8_0_LDS * 32];
     constexpr int BE = block_elems(T), VT = vec_dot_type(T);
     const int ng = n / 256, nb = n / BE;

@@ -31,6 +31,7 @@ size_t or_block_bytes(int type) {
     case OR_Q2_K: return 84;
     case OR_Q3_K: return 110;
     case OR_IQ3_XXS: return 98;
+    case OR_IQ3_S: return 110;
     default: return 0;
     }
 }
@@ -38,7 +39,7 @@ int or_block_elems(int type) {
     switch (type) {
     case OR_Q8_0: case OR_IQ4_NL: case OR_MXFP4: case OR_Q5_0: return 32;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_Q8_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K:
-    case OR_Q3_K: case OR_IQ3_XXS: return 256;
+    case OR_Q3_K: case OR_IQ3_XXS: case OR_IQ3_S: return 256;
     default: return 0;
     }
 }
@@ -48,7 +49,7 @@ int or_vec_dot_type(int type) {
     switch (type) {
     case OR_IQ4_NL: case OR_Q8_0: case OR_MXFP4: case OR_Q5_0: return OR_Q8_0;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K: case OR_Q3_K: case OR_IQ3_XXS:
-        return OR_Q8_K;
+    case OR_IQ3_S: return OR_Q8_K;
     default: return -1;
     }
 }
@@ -80,7 +81,12 @@ static const uint16_t iq2xxs_code[256] = {
 static const uint16_t iq3xxs_code[256] = {
 #include "../hyper_amd/csrc/iq3xxs_grid.inc"
 };
-static uint8_t iq2xs_rows[512][8], iq2xxs_rows[256][8], iq3xxs_rows[256][4];
+/* IQ3_S codebook: 512 rows of 4 bytes, base-8 coded, digit i = byte i's level 2 d + 1 (values of
+   src/kernels4.cu:480-545) */
+static const uint16_t iq3s_code[512] = {
+#include "../hyper_amd/csrc/iq3s_grid.inc"
+};
+static uint8_t iq2xs_rows[512][8], iq2xxs_rows[256][8], iq3xxs_rows[256][4], iq3s_rows[512][4];
 static int iq2xs_ready = 0;
 static void iq2xs_init(void) {   /* the grid codebooks */
     if (__atomic_load_n(&iq2xs_ready, __ATOMIC_ACQUIRE)) return;
@@ -96,6 +102,10 @@ static void iq2xs_init(void) {   /* the grid codebooks */
     for (int i = 0; i < 256; ++i) {
         unsigned c = iq3xxs_code[i];
         for (int j = 0; j < 4; ++j) { iq3xxs_rows[i][j] = (uint8_t) ((c & 7) == 7 ? 62 : 4 + 8 * (c & 7)); c >>= 3; }
+    }
+    for (int i = 0; i < 512; ++i) {
+        unsigned c = iq3s_code[i];
+        for (int j = 0; j < 4; ++j) { iq3s_rows[i][j] = (uint8_t) (2 * (c & 7) + 1); c >>= 3; }
     }
     __atomic_store_n(&iq2xs_ready, 1, __ATOMIC_RELEASE);
 }
@@ -304,6 +314,15 @@ static inline int iq3xxs_q(const uint8_t *b, int e) {   /* signed grid value of 
     const int g = iq3xxs_rows[b[2 + 8 * ib + 2 * l + (j >> 2)]][j & 3];
     return (ksign((iq3xxs_a(b, ib) >> (7 * l)) & 127) >> j) & 1 ? -g : g;
 }
+/* IQ3_S (src/kernels4.cu:682-695): element e of 32-group ib, 8-group l, position j: grid row qs[8 ib + 2 l + j / 4]
+   (qs at 2) with bit 2 l + j / 4 of qh[ib] (at 66) as its 9th bit, byte j % 4; negated where bit j of signs[4 ib + l]
+   (at 74) is set; the group's scale is nibble ib & 1 of scales[ib / 2] (at 106) */
+static inline int iq3s_q(const uint8_t *b, int e) {
+    const int ib = e >> 5, l = (e >> 3) & 3, j = e & 7, hb = 2 * l + (j >> 2);
+    const int g = iq3s_rows[b[2 + 8 * ib + hb] | (((b[66 + ib] >> hb) & 1) << 8)][j & 3];
+    return (b[74 + 4 * ib + l] >> j) & 1 ? -g : g;
+}
+static inline int iq3s_sc(const uint8_t *b, int ib) { return (b[106 + (ib >> 1)] >> (4 * (ib & 1))) & 15; }
 static inline int iq2xs_sc(const uint8_t *b, int e) {
     const int ib = e >> 5, l = (e >> 3) & 3;
     return (b[66 + ib] >> (4 * (l >> 1))) & 0xF;
@@ -356,6 +375,13 @@ int or_dequant_row(int type, const uint8_t *row, int n, float *out) {
             break;
         case OR_Q8_0:
             for (int e = 0; e < 32; ++e) o[e] = h2f(b) * (float) (int8_t) b[2 + e];
+            break;
+        case OR_IQ3_S:
+            for (int e = 0; e < 256; ++e) {
+                const float db = h2f(b) * (float) (1 + 2 * iq3s_sc(b, e >> 5));
+                const int q = iq3s_q(b, e);
+                o[e] = (db * (float) (q < 0 ? -q : q)) * (q < 0 ? -1.0f : 1.0f);
+            }
             break;
         case OR_IQ3_XXS:
             for (int e = 0; e < 256; ++e) {
@@ -445,6 +471,13 @@ static void block_ints_scalar(int type, const uint8_t *b, const uint8_t *y, int3
         break;
     case OR_Q5_0:      /* ggml's vec_dot_q5_0_q8_0 integer part: sum_32 (x - 16) q8 */
         for (int l = 0; l < 32; ++l) si += q5_0_q(b, l) * q8[l];
+        break;
+    case OR_IQ3_S:     /* the reference's IQ3_S x Q8_K dot (src/iq3s_dot.h:48-76): sum_ib (2 sc + 1) sum_32 grid sign y */
+        for (int ib = 0; ib < 8; ++ib) {
+            int32_t s = 0;
+            for (int l = 0; l < 32; ++l) s += iq3s_q(b, 32 * ib + l) * q8[32 * ib + l];
+            si += (2 * iq3s_sc(b, ib) + 1) * s;
+        }
         break;
     case OR_IQ3_XXS:   /* ggml's vec_dot_iq3_xxs_q8_K: sum_ib (2 sc + 1) sum_32 grid sign y */
         for (int ib = 0; ib < 8; ++ib) {
@@ -555,7 +588,7 @@ static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *su
 static int dot_ok(int type) {
     return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_IQ4_XS || type == OR_IQ2_XS || type == OR_IQ4_NL ||
            type == OR_Q8_0 || type == OR_IQ2_XXS || type == OR_MXFP4 || type == OR_Q5_0 || type == OR_Q2_K || type == OR_Q3_K ||
-           type == OR_IQ3_XXS;
+           type == OR_IQ3_XXS || type == OR_IQ3_S;
 }
 int or_block_ints(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ) {
     if (!dot_ok(type) || n % or_block_elems(type)) return -1;
@@ -588,6 +621,7 @@ static float row_dot(int type, const uint8_t *row, const uint8_t *xq, int n) {
         case OR_Q6_K: t = h2f(b + 208) * (float) si; break;
         case OR_Q3_K: t = h2f(b + 108) * (float) si; break;
         case OR_IQ3_XXS: t = (h2f(b) * 0.25f) * (float) si; break;
+        case OR_IQ3_S: t = h2f(b) * (float) si; break;
         case OR_Q2_K: t = fmaf(h2f(b + 80), (float) si, -(h2f(b + 82) * (float) sm)); break;
         case OR_IQ2_XS: case OR_IQ2_XXS: t = (h2f(b) * 0.125f) * (float) si; break;
         case OR_MXFP4: t = e8m0_half(b[0]) * (float) si; break;

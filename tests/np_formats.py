@@ -145,6 +145,22 @@ def iq3xxs(b, grid_rows, ksigns):
     return dict(q=q, sc=2 * (a >> 28) + 1, m=None, gsize=32, d=f16(b[:, 0:2]))
 
 
+def iq3s(b, grid_rows):
+    """grid_rows: [512, 4] codebook bytes.  32-group ib: eight indices at 2 + 8 ib, their 9th bits in qh[ib] (@66, bit
+    k for index k), four literal sign bytes at 74 + 4 ib (bit j negates value j of the 8-group), scale nibble ib % 2 of
+    scales[ib // 2] (@106), the group's factor 2 sc + 1."""
+    b = b.reshape(-1, 110)
+    qh = b[:, 66:74].astype(np.int64)                                           # [ib]
+    idx = b[:, 2:66].astype(np.int64).reshape(-1, 8, 8) | (((qh[:, :, None] >> np.arange(8)) & 1) << 8)
+    g = grid_rows[idx].astype(np.int64).reshape(-1, 8, 4, 8)                    # [ib][l][8 values]
+    sgn = b[:, 74:106].astype(np.int64).reshape(-1, 8, 4)
+    bits = (sgn[..., None] >> np.arange(8)) & 1
+    q = np.where(bits == 1, -g, g).reshape(-1, 256)
+    s = b[:, 106:110].astype(np.int64)
+    sc = np.stack([(s[:, ib // 2] >> (4 * (ib % 2))) & 15 for ib in range(8)], axis=1)
+    return dict(q=q, sc=2 * sc + 1, m=None, gsize=32, d=f16(b[:, 0:2]))
+
+
 def q5_0w(b):
     """Q5_0 weights: d f16 @0, qh little-endian u32 @2, qs[16] @6; value j = (nibble j + 16 * bit j of qh) - 16, the
     nibbles in qs order, low halves first (values 0..15), then high halves (16..31)."""
@@ -206,6 +222,7 @@ def decode(t, b, grid_rows=None, ksigns=None):
     if t == 10: return q2k(b)
     if t == 11: return q3k(b)
     if t == 18: return iq3xxs(b, grid_rows, ksigns)
+    if t == 21: return iq3s(b, grid_rows)
     if t == 17: return iq2xs(b, grid_rows, ksigns)
     if t == 16: return iq2xxs(b, grid_rows, ksigns)
     raise ValueError(t)
@@ -230,6 +247,9 @@ def dequant(t, b, grid_rows=None, ksigns=None):
         return (q.astype(np.float32) * d).astype(np.float32)
     if t == 8:
         return (d * q.astype(np.float32)).astype(np.float32)
+    if t == 21:   # d (2 sc + 1), then times the grid byte, then the sign
+        db = (d * sc.astype(np.float32)).astype(np.float32)
+        return ((db * np.abs(q).astype(np.float32)) * np.where(q < 0, np.float32(-1), np.float32(1))).astype(np.float32)
     if t in (16, 17, 18):
         db = (d * (np.float32(0.5) + ((sc - 1) / 2).astype(np.float32))) * np.float32(0.5 if t == 18 else 0.25)
         return ((db * np.abs(q).astype(np.float32)) * np.where(q < 0, np.float32(-1), np.float32(1))).astype(np.float32)

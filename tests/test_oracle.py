@@ -75,9 +75,23 @@ def iq3xxs_rows() -> np.ndarray:
     return rows
 
 
+def iq3s_rows() -> np.ndarray:
+    """The IQ3_S codebook as the kernels and the oracle expand it from iq3s_grid.inc (base-8 digits: 2 d + 1)."""
+    text = (Path(__file__).resolve().parents[1] / "hyper_amd/csrc/iq3s_grid.inc").read_text()
+    body = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("//"))
+    codes = [int(v) for v in body.replace(",", " ").split() if v.isdigit()]
+    assert len(codes) == 512
+    rows = np.zeros((512, 4), np.uint8)
+    for i, c in enumerate(codes):
+        for j in range(4):
+            rows[i, j] = 2 * (c % 8) + 1
+            c //= 8
+    return rows
+
+
 def grid_for(t):
     t = GType(t)
-    return iq2xxs_rows() if t == GType.IQ2_XXS else iq3xxs_rows() if t == GType.IQ3_XXS else iq2xs_rows()
+    return {GType.IQ2_XXS: iq2xxs_rows, GType.IQ3_XXS: iq3xxs_rows, GType.IQ3_S: iq3s_rows}.get(t, iq2xs_rows)()
 
 
 def ksigns() -> np.ndarray:
@@ -89,6 +103,7 @@ def test_codebooks_match_reference():
     assert hashlib.sha256(rows.tobytes()).hexdigest() == TABLES["iq2xs_grid_sha256"]
     assert hashlib.sha256(iq2xxs_rows().tobytes()).hexdigest() == TABLES["iq2xxs_grid_sha256"]
     assert hashlib.sha256(iq3xxs_rows().tobytes()).hexdigest() == TABLES["iq3xxs_grid_sha256"]
+    assert hashlib.sha256(iq3s_rows().tobytes()).hexdigest() == TABLES["iq3s_grid_sha256"]
     assert hashlib.sha256(ksigns().tobytes()).hexdigest() == TABLES["ksigns_sha256"]
     assert hashlib.sha256(nf.KV_IQ4NL.astype(np.int8).tobytes()).hexdigest() == TABLES["iq4nl_sha256"]
     assert all(bin(int(s)).count("1") % 2 == 0 for s in ksigns())   # every sign byte has an even bit count
@@ -310,6 +325,38 @@ def test_iq3xxs_known_answer_positions():
     assert not sm.any()
 
 
+def test_iq3s_known_answer_positions():
+    """IQ3_S (src/kernels4.cu:682-695): 32-group ib's 8-group l takes rows qs[8 ib + 2 l] and qs[8 ib + 2 l + 1], each with
+    a 9th index bit from qh[ib] (bits 2 l, 2 l + 1); bit j of the literal byte signs[4 ib + l] negates value j; value =
+    d (1 + 2 sc) * grid.  Rows fixed by the reference's table: row 0 = 0x01010101, row 1 = 0x01010103 (byte 0 = 3),
+    row 256 (the 9th bit) = its own first entry.  Placed by hand: group 0, 8-group 1 takes row 1 then row 256 (9th
+    bit of the second index), sign byte 0x81; group 3 has scale 7 (factor 15)."""
+    rows = iq3s_rows()
+    assert list(rows[0]) == [1, 1, 1, 1] and list(rows[1]) == [3, 1, 1, 1]
+    r256 = [int(v) for v in rows[256]]
+    assert r256 != [1, 1, 1, 1]   # so a dropped 9th index bit (row 0 in its place) shows
+    blk = np.zeros(110, np.uint8)
+    blk[0:2] = _f16b(1.0)
+    blk[2 + 2] = 1                # group 0, 8-group 1, first index: row 1
+    blk[66] = 1 << 3              # group 0: 9th bit of index 3 (8-group 1's second): row 256
+    blk[74 + 1] = 0x81            # group 0, 8-group 1: values 0 and 7 negated
+    blk[106 + 1] = 7 << 4         # group 3: scale 7
+    want = np.ones(256, np.float32)
+    want[8:16] = [-3, 1, 1, 1] + [r256[0], r256[1], r256[2], -r256[3]]
+    want[96:128] = 15.0
+    got = orc.dequant_row(GType.IQ3_S, blk, 256)
+    assert (got == want).all(), np.nonzero(got != want)
+    x = np.arange(256, dtype=np.float32) % 5 - 2.0
+    xq = orc.quantize(GType.Q8_K, x)
+    q8 = xq[4:260].view(np.int8).astype(np.int64)
+    ints = want.astype(np.int64)
+    ints[96:128] = 1
+    scale = np.array([1, 1, 1, 15, 1, 1, 1, 1], np.int64)
+    si, sm = orc.block_ints(GType.IQ3_S, blk, xq, 256)
+    assert int(si[0]) == int(sum(scale[g] * (ints[32 * g:32 * g + 32] @ q8[32 * g:32 * g + 32]) for g in range(8)))
+    assert not sm.any()
+
+
 def test_q8_0_weight_known_answers():
     """Q8_0 weights (src/kernels4.cu:421-714, deq8: d * qs[j]): value j of a block is d * (int8) qs[j] in place, and
     against a Q8_0 activation block the integer is sum_j qs[j] y[j] (ggml's vec_dot_q8_0_q8_0), folded as
@@ -476,7 +523,7 @@ def test_q8k_known_answers():
 # ------------------------------------------------------------------ block decoding
 
 ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.IQ4_NL, GType.Q8_0, GType.MXFP4,
-       GType.Q5_0, GType.Q2_K, GType.Q3_K, GType.IQ3_XXS]
+       GType.Q5_0, GType.Q2_K, GType.Q3_K, GType.IQ3_XXS, GType.IQ3_S]
 
 
 def blocks(t, nb, seed):
