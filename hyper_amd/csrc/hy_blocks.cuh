@@ -49,11 +49,12 @@ __device__ __forceinline__ uint32_t apply_sign(uint32_t g, uint32_t b4) {
 // the same with the byte mask given (0xFF per negated byte): -g = ~g + 1 per byte, no carry (codebook bytes are not 0)
 __device__ __forceinline__ uint32_t apply_mask(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
 // LDS entries of an expanded IQ2_XS codebook: 512 rows, then 128 sign masks (IQ2_XXS: 256 rows, then the masks)
-__host__ __device__ constexpr int iq2_rows(int t) { return t == IQ2_XS || t == IQ3_S ? 512 : 256; }
-// sign masks after the rows: the 128 ksign patterns, or for IQ3_S (literal sign bytes) all 256 bytes
-__host__ __device__ constexpr int iq2_masks(int t) { return t == IQ3_S ? 256 : 128; }
+__host__ __device__ constexpr int iq2_rows(int t) { return t == IQ2_S ? 1024 : t == IQ2_XS || t == IQ3_S ? 512 : 256; }
+// sign masks after the rows: the 128 ksign patterns, or for IQ3_S and IQ2_S (literal sign bytes) all 256 bytes
+__host__ __device__ constexpr bool literal_signs(int t) { return t == IQ3_S || t == IQ2_S; }
+__host__ __device__ constexpr int iq2_masks(int t) { return literal_signs(t) ? 256 : 128; }
 __host__ __device__ constexpr int iq2_lds(int t) { return iq2_type(t) ? iq2_rows(t) + iq2_masks(t) : 1; }   // uint2 entries
-constexpr int GRID_LDS = 512 + 256;   // the largest of them (IQ3_S)
+constexpr int GRID_LDS = 1024 + 256;   // the largest of them (IQ2_S)
 // Q6_K: q6 bytes (0..63) -> q6 - 32 as int8: per byte (q + 96) ^ 128 = q - 32 mod 256 (q + 96 < 256: no carry)
 __device__ __forceinline__ uint32_t q6_signed(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
 
@@ -172,6 +173,33 @@ template <> struct Item<IQ3_XXS> {
         sm = 0;
     }
     __device__ __forceinline__ float tval(int si, int) const { return (h2f(d) * 0.25f) * (float) si; }
+};
+// IQ2_S (82 B: d, qs[32] @2, signs[32] @34, qh[8] @66, scales[8] @74), src/kernels4.cu:602-613.  Lane L = 32-group
+// L: 8-group l takes grid row qs[4 L + l] | bits 2 l, 2 l + 1 of qh[L] << 8 (8-byte rows of the 1024-row codebook),
+// sign byte signs[4 L + l] (bit j negates value j), the scale nibble l / 2 of scales[L] (16-groups) (ggml's
+// vec_dot_iq2_s_q8_K integers: sumi = sum over 16-groups (2 sc + 1) sum_16 grid sign y).  Blocks are 2-byte aligned.
+template <> struct Item<IQ2_S> {
+    uint32_t gq, sg, hs;   // the lane's 4 index bytes; its 4 sign bytes; qh byte | scale byte << 8
+    uint16_t d;
+    const uint2 *grid;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+        gq = (uint32_t) ld_u16(b + 2 + 4 * L) | ((uint32_t) ld_u16(b + 4 + 4 * L) << 16);
+        sg = (uint32_t) ld_u16(b + 34 + 4 * L) | ((uint32_t) ld_u16(b + 36 + 4 * L) << 16);
+        hs = (uint32_t) b[66 + L] | ((uint32_t) b[74 + L] << 8);
+        d = ld_u16(b);
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
+        const uint32_t *ya = (const uint32_t *) (y + 4 + 32 * L);
+        int s[4];
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint2 g = grid[((gq >> (8 * l)) & 255) | (((hs >> (2 * l)) & 3) << 8)], m = grid[1024 + ((sg >> (8 * l)) & 255)];
+            s[l] = sdot4(apply_mask(g.y, m.y), ya[2 * l + 1], sdot4(apply_mask(g.x, m.x), ya[2 * l], 0));
+        }
+        si = (2 * (int) ((hs >> 8) & 15) + 1) * (s[0] + s[1]) + (2 * (int) ((hs >> 12) & 15) + 1) * (s[2] + s[3]);
+        sm = 0;
+    }
+    __device__ __forceinline__ float tval(int si, int) const { return (h2f(d) * 0.125f) * (float) si; }
 };
 // IQ3_S (110 B: d, qs[64] @2, qh[8] @66, signs[32] @74, scales[4] @106), src/kernels4.cu:682-695.  Lane L = 32-group
 // L: 8-group l takes grid rows qs[8 L + 2 l] | bit 2 l of qh[L] << 8 and qs[8 L + 2 l + 1] | bit 2 l + 1 << 8 (4-byte
@@ -455,16 +483,17 @@ template <> struct Item<Q5_0> {
     __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
 };
 
-// expand a grid codebook (base-3 codes: IQ2_XS 512 rows, IQ2_XXS 256; base-8 codes: IQ3_XXS 256 and IQ3_S 512 rows of
-// 4 bytes, in .x) into rows x 8 bytes of LDS, followed by the sign patterns as byte masks (entry rows + i: byte j = 0xFF
-// where bit j of ksign(i) is set, the parity bit giving byte 7; for IQ3_S bit j of i itself, i < 256)
+// expand a grid codebook (base-3 codes: IQ2_XS 512 rows, IQ2_XXS 256, IQ2_S 1024; base-8 codes: IQ3_XXS 256 and IQ3_S
+// 512 rows of 4 bytes, in .x) into rows x 8 bytes of LDS, followed by the sign patterns as byte masks (entry rows + i:
+// byte j = 0xFF where bit j of ksign(i) is set, the parity bit giving byte 7; for the literal-sign types, IQ3_S and
+// IQ2_S, bit j of i itself, i < 256)
 template <int T>
 __device__ __forceinline__ void expand_iq2_grid(uint2 *grid) {
     static_assert(iq2_type(T), "an IQ2 codebook");
     constexpr int R = iq2_rows(T);
     for (int i = threadIdx.x; i < R + iq2_masks(T); i += blockDim.x) {
         if (i >= R) {
-            const uint32_t ks = T == IQ3_S ? (uint32_t) i - R : ksign((uint32_t) i - R);
+            const uint32_t ks = literal_signs(T) ? (uint32_t) i - R : ksign((uint32_t) i - R);
             grid[i] = make_uint2(spread4(ks & 15) * 0xFFu, spread4(ks >> 4) * 0xFFu);
             continue;
         }
@@ -482,7 +511,7 @@ __device__ __forceinline__ void expand_iq2_grid(uint2 *grid) {
             grid[i] = make_uint2(lo, 0u);
             continue;
         }
-        uint32_t c = T == IQ2_XS ? c_iq2xs_code[i] : c_iq2xxs_code[i], lo = 0, hi = 0;
+        uint32_t c = T == IQ2_XS ? c_iq2xs_code[i] : T == IQ2_S ? c_iq2s_code[i] : c_iq2xxs_code[i], lo = 0, hi = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint32_t dgt = c % 3; c /= 3;

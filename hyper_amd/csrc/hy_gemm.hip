@@ -146,6 +146,39 @@ template <> struct Raw<IQ3_XXS> {
     }
     __device__ __forceinline__ float fold(int si, int) const { return (h2f(d) * 0.25f) * (float) si; }
 };
+// IQ2_S (82 B): chunk c = 32-group c; lane q takes 8-group q: grid row qs[4 c + q] | bits 2 q, 2 q + 1 of qh[c] << 8,
+// sign byte signs[4 c + q], the chunk's 16-group scales 2 sc + 1 from the nibbles of scales[c] (s0 for lanes q < 2)
+// (src/kernels4.cu:602-613; ggml's vec_dot_iq2_s_q8_K integers).
+template <> struct Raw<IQ2_S> {
+    static constexpr bool mins = false, g16 = true, per_chunk = false;
+    uint32_t gq[2], sg[2], qh[2], sc[2], d;   // byte c % 4 of [c / 4]: the lane's index byte, its sign byte, qh[c], scales[c]
+    __device__ __forceinline__ void load(const uint8_t *blk, int q) {
+        gq[0] = gq[1] = sg[0] = sg[1] = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            gq[c >> 2] |= (uint32_t) blk[2 + 4 * c + q] << (8 * (c & 3));
+            sg[c >> 2] |= (uint32_t) blk[34 + 4 * c + q] << (8 * (c & 3));
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            qh[i] = (uint32_t) ld_u16(blk + 66 + 4 * i) | ((uint32_t) ld_u16(blk + 68 + 4 * i) << 16);
+            sc[i] = (uint32_t) ld_u16(blk + 74 + 4 * i) | ((uint32_t) ld_u16(blk + 76 + 4 * i) << 16);
+        }
+        d = ld_u16(blk);
+    }
+    __device__ __forceinline__ void chunk(int c, int q, const uint2 *grid, uint32_t &b0, uint32_t &b1, int &s0, int &s1, int &mn) const {
+        const int sh = 8 * (c & 3);
+        const uint32_t idx = ((gq[c >> 2] >> sh) & 255) | (((qh[c >> 2] >> (sh + 2 * q)) & 3) << 8);
+        const uint2 g = grid[idx], m = grid[1024 + ((sg[c >> 2] >> sh) & 255)];
+        b0 = apply_mask(g.x, m.x);
+        b1 = apply_mask(g.y, m.y);
+        const uint32_t s = (sc[c >> 2] >> sh) & 255;
+        s0 = 2 * (int) (s & 15) + 1;
+        s1 = 2 * (int) (s >> 4) + 1;
+        mn = 0;
+    }
+    __device__ __forceinline__ float fold(int si, int) const { return (h2f(d) * 0.125f) * (float) si; }
+};
 // IQ3_S (110 B): chunk c = 32-group c; lane q takes 8-group q: grid indices qs[8 c + 2 q], qs[8 c + 2 q + 1] with bits
 // 2 q, 2 q + 1 of qh[c] as their 9th bits, sign byte signs[4 c + q], the chunk's scale 2 sc + 1 (nibble c & 1 of
 // scales[c / 2]) (src/kernels4.cu:682-695; src/iq3s_dot.h:48-76 integers).
@@ -1184,6 +1217,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
     case Q3_K: { constexpr int TT = Q3_K; __VA_ARGS__; }                                                 \
     case IQ3_XXS: { constexpr int TT = IQ3_XXS; __VA_ARGS__; }                                           \
     case IQ3_S: { constexpr int TT = IQ3_S; __VA_ARGS__; }                                               \
+    case IQ2_S: { constexpr int TT = IQ2_S; __VA_ARGS__; }                                               \
     default: set_error("grouped GEMM: unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 

@@ -166,6 +166,7 @@ static int launch_gemv_t(const hy_moe_dev &m, const float *src, int ss, const in
     case Q3_K: { constexpr int TT = Q3_K; CALL; }                                        \
     case IQ3_XXS: { constexpr int TT = IQ3_XXS; CALL; }                                  \
     case IQ3_S: { constexpr int TT = IQ3_S; CALL; }                                      \
+    case IQ2_S: { constexpr int TT = IQ2_S; CALL; }                                      \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 
@@ -371,6 +372,7 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, floa
     else if (type == IQ2_XXS) expand_iq2_grid<IQ2_XXS>(grid);
     else if (type == IQ3_XXS) expand_iq2_grid<IQ3_XXS>(grid);
     else if (type == IQ3_S) expand_iq2_grid<IQ3_S>(grid);
+    else if (type == IQ2_S) expand_iq2_grid<IQ2_S>(grid);
     __syncthreads();
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -423,6 +425,13 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, floa
         const uint8_t *b = row + (size_t) (i >> 5) * 17;
         const int e = i & 31;
         v = (float) (int8_t) (kvfp4((b[1 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF) & 0xff) * e8m0_half(b[0]);
+    } else if (type == IQ2_S) {   // src/kernels4.cu:602-613
+        const uint8_t *b = row + (size_t) (i >> 8) * 82;
+        const int e = i & 255, ib = e >> 5, l = (e >> 3) & 3, j = e & 7;
+        const float db = h2f(ld_u16(b)) * (0.5f + (float) ((b[74 + ib] >> (4 * (l >> 1))) & 0xf)) * 0.25f;
+        const uint2 gr = grid[b[2 + 4 * ib + l] | (((b[66 + ib] >> (2 * l)) & 3) << 8)];
+        const float gv = (float) (((j < 4 ? gr.x : gr.y) >> (8 * (j & 3))) & 0xff);
+        v = (db * gv) * ((b[34 + 4 * ib + l] >> j) & 1 ? -1.0f : 1.0f);
     } else if (type == IQ3_S) {   // src/kernels4.cu:682-695
         const uint8_t *b = row + (size_t) (i >> 8) * 110;
         const int e = i & 255, ib = e >> 5, l = (e >> 3) & 3, j = e & 7, hb = 2 * l + (j >> 2);

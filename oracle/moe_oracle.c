@@ -32,6 +32,7 @@ size_t or_block_bytes(int type) {
     case OR_Q3_K: return 110;
     case OR_IQ3_XXS: return 98;
     case OR_IQ3_S: return 110;
+    case OR_IQ2_S: return 82;
     default: return 0;
     }
 }
@@ -39,7 +40,7 @@ int or_block_elems(int type) {
     switch (type) {
     case OR_Q8_0: case OR_IQ4_NL: case OR_MXFP4: case OR_Q5_0: return 32;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_Q8_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K:
-    case OR_Q3_K: case OR_IQ3_XXS: case OR_IQ3_S: return 256;
+    case OR_Q3_K: case OR_IQ3_XXS: case OR_IQ3_S: case OR_IQ2_S: return 256;
     default: return 0;
     }
 }
@@ -49,7 +50,7 @@ int or_vec_dot_type(int type) {
     switch (type) {
     case OR_IQ4_NL: case OR_Q8_0: case OR_MXFP4: case OR_Q5_0: return OR_Q8_0;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K: case OR_Q3_K: case OR_IQ3_XXS:
-    case OR_IQ3_S: return OR_Q8_K;
+    case OR_IQ3_S: case OR_IQ2_S: return OR_Q8_K;
     default: return -1;
     }
 }
@@ -86,7 +87,11 @@ static const uint16_t iq3xxs_code[256] = {
 static const uint16_t iq3s_code[512] = {
 #include "../hyper_amd/csrc/iq3s_grid.inc"
 };
-static uint8_t iq2xs_rows[512][8], iq2xxs_rows[256][8], iq3xxs_rows[256][4], iq3s_rows[512][4];
+/* IQ2_S codebook: 1024 rows of 8 bytes, base-3 coded as IQ2_XS's (values of src/iq_grids.h:210-467) */
+static const uint16_t iq2s_code[1024] = {
+#include "../hyper_amd/csrc/iq2s_grid.inc"
+};
+static uint8_t iq2xs_rows[512][8], iq2xxs_rows[256][8], iq2s_rows[1024][8], iq3xxs_rows[256][4], iq3s_rows[512][4];
 static int iq2xs_ready = 0;
 static void iq2xs_init(void) {   /* the grid codebooks */
     if (__atomic_load_n(&iq2xs_ready, __ATOMIC_ACQUIRE)) return;
@@ -102,6 +107,10 @@ static void iq2xs_init(void) {   /* the grid codebooks */
     for (int i = 0; i < 256; ++i) {
         unsigned c = iq3xxs_code[i];
         for (int j = 0; j < 4; ++j) { iq3xxs_rows[i][j] = (uint8_t) ((c & 7) == 7 ? 62 : 4 + 8 * (c & 7)); c >>= 3; }
+    }
+    for (int i = 0; i < 1024; ++i) {
+        unsigned c = iq2s_code[i];
+        for (int j = 0; j < 8; ++j) { iq2s_rows[i][j] = lv[c % 3]; c /= 3; }
     }
     for (int i = 0; i < 512; ++i) {
         unsigned c = iq3s_code[i];
@@ -322,6 +331,15 @@ static inline int iq3s_q(const uint8_t *b, int e) {
     const int g = iq3s_rows[b[2 + 8 * ib + hb] | (((b[66 + ib] >> hb) & 1) << 8)][j & 3];
     return (b[74 + 4 * ib + l] >> j) & 1 ? -g : g;
 }
+/* IQ2_S (src/kernels4.cu:602-613): element e of 32-group ib, 8-group l, position j: grid row qs[4 ib + l] (qs at 2)
+   with bits 2 l, 2 l + 1 of qh[ib] (at 66) as index bits 8-9, byte j; negated where bit j of signs[4 ib + l] (at 34)
+   is set; its 16-group's scale is nibble l / 2 of scales[ib] (at 74) */
+static inline int iq2s_q(const uint8_t *b, int e) {
+    const int ib = e >> 5, l = (e >> 3) & 3, j = e & 7;
+    const int g = iq2s_rows[b[2 + 4 * ib + l] | (((b[66 + ib] >> (2 * l)) & 3) << 8)][j];
+    return (b[34 + 4 * ib + l] >> j) & 1 ? -g : g;
+}
+static inline int iq2s_sc(const uint8_t *b, int e) { return (b[74 + (e >> 5)] >> (4 * ((e >> 4) & 1))) & 15; }
 static inline int iq3s_sc(const uint8_t *b, int ib) { return (b[106 + (ib >> 1)] >> (4 * (ib & 1))) & 15; }
 static inline int iq2xs_sc(const uint8_t *b, int e) {
     const int ib = e >> 5, l = (e >> 3) & 3;
@@ -375,6 +393,13 @@ int or_dequant_row(int type, const uint8_t *row, int n, float *out) {
             break;
         case OR_Q8_0:
             for (int e = 0; e < 32; ++e) o[e] = h2f(b) * (float) (int8_t) b[2 + e];
+            break;
+        case OR_IQ2_S:
+            for (int e = 0; e < 256; ++e) {
+                const float db = h2f(b) * (0.5f + (float) iq2s_sc(b, e)) * 0.25f;
+                const int q = iq2s_q(b, e);
+                o[e] = (db * (float) (q < 0 ? -q : q)) * (q < 0 ? -1.0f : 1.0f);
+            }
             break;
         case OR_IQ3_S:
             for (int e = 0; e < 256; ++e) {
@@ -471,6 +496,13 @@ static void block_ints_scalar(int type, const uint8_t *b, const uint8_t *y, int3
         break;
     case OR_Q5_0:      /* ggml's vec_dot_q5_0_q8_0 integer part: sum_32 (x - 16) q8 */
         for (int l = 0; l < 32; ++l) si += q5_0_q(b, l) * q8[l];
+        break;
+    case OR_IQ2_S:     /* ggml's vec_dot_iq2_s_q8_K: sum over 16-groups (2 sc + 1) sum_16 grid sign y */
+        for (int g = 0; g < 16; ++g) {
+            int32_t s = 0;
+            for (int l = 0; l < 16; ++l) s += iq2s_q(b, 16 * g + l) * q8[16 * g + l];
+            si += (2 * iq2s_sc(b, 16 * g) + 1) * s;
+        }
         break;
     case OR_IQ3_S:     /* the reference's IQ3_S x Q8_K dot (src/iq3s_dot.h:48-76): sum_ib (2 sc + 1) sum_32 grid sign y */
         for (int ib = 0; ib < 8; ++ib) {
@@ -588,7 +620,7 @@ static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *su
 static int dot_ok(int type) {
     return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_IQ4_XS || type == OR_IQ2_XS || type == OR_IQ4_NL ||
            type == OR_Q8_0 || type == OR_IQ2_XXS || type == OR_MXFP4 || type == OR_Q5_0 || type == OR_Q2_K || type == OR_Q3_K ||
-           type == OR_IQ3_XXS || type == OR_IQ3_S;
+           type == OR_IQ3_XXS || type == OR_IQ3_S || type == OR_IQ2_S;
 }
 int or_block_ints(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ) {
     if (!dot_ok(type) || n % or_block_elems(type)) return -1;
@@ -623,7 +655,7 @@ static float row_dot(int type, const uint8_t *row, const uint8_t *xq, int n) {
         case OR_IQ3_XXS: t = (h2f(b) * 0.25f) * (float) si; break;
         case OR_IQ3_S: t = h2f(b) * (float) si; break;
         case OR_Q2_K: t = fmaf(h2f(b + 80), (float) si, -(h2f(b + 82) * (float) sm)); break;
-        case OR_IQ2_XS: case OR_IQ2_XXS: t = (h2f(b) * 0.125f) * (float) si; break;
+        case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ2_S: t = (h2f(b) * 0.125f) * (float) si; break;
         case OR_MXFP4: t = e8m0_half(b[0]) * (float) si; break;
         default: t = h2f(b) * (float) si; break;        /* IQ4_XS, IQ4_NL, Q8_0, Q5_0 */
         }

@@ -161,6 +161,22 @@ def iq3s(b, grid_rows):
     return dict(q=q, sc=2 * sc + 1, m=None, gsize=32, d=f16(b[:, 0:2]))
 
 
+def iq2s(b, grid_rows):
+    """grid_rows: [1024, 8] codebook bytes.  32-group ib: four index bytes at 2 + 4 ib with two more bits each in
+    qh[ib] (@66, bits 2 l, 2 l + 1 for 8-group l), four literal sign bytes at 34 + 4 ib, scale nibbles of scales[ib]
+    (@74) for its two 16-groups, each 2 sc + 1."""
+    b = b.reshape(-1, 82)
+    qh = b[:, 66:74].astype(np.int64)
+    idx = b[:, 2:34].astype(np.int64).reshape(-1, 8, 4) | (((qh[:, :, None] >> (2 * np.arange(4))) & 3) << 8)
+    g = grid_rows[idx].astype(np.int64)                                           # [ib][l][8]
+    sgn = b[:, 34:66].astype(np.int64).reshape(-1, 8, 4)
+    bits = (sgn[..., None] >> np.arange(8)) & 1
+    q = np.where(bits == 1, -g, g).reshape(-1, 256)
+    s = b[:, 74:82].astype(np.int64)
+    sc = np.stack([s & 15, s >> 4], axis=2).reshape(-1, 16)
+    return dict(q=q, sc=2 * sc + 1, m=None, gsize=16, d=f16(b[:, 0:2]))
+
+
 def q5_0w(b):
     """Q5_0 weights: d f16 @0, qh little-endian u32 @2, qs[16] @6; value j = (nibble j + 16 * bit j of qh) - 16, the
     nibbles in qs order, low halves first (values 0..15), then high halves (16..31)."""
@@ -223,6 +239,7 @@ def decode(t, b, grid_rows=None, ksigns=None):
     if t == 11: return q3k(b)
     if t == 18: return iq3xxs(b, grid_rows, ksigns)
     if t == 21: return iq3s(b, grid_rows)
+    if t == 22: return iq2s(b, grid_rows)
     if t == 17: return iq2xs(b, grid_rows, ksigns)
     if t == 16: return iq2xxs(b, grid_rows, ksigns)
     raise ValueError(t)
@@ -250,7 +267,7 @@ def dequant(t, b, grid_rows=None, ksigns=None):
     if t == 21:   # d (2 sc + 1), then times the grid byte, then the sign
         db = (d * sc.astype(np.float32)).astype(np.float32)
         return ((db * np.abs(q).astype(np.float32)) * np.where(q < 0, np.float32(-1), np.float32(1))).astype(np.float32)
-    if t in (16, 17, 18):
+    if t in (16, 17, 18, 22):
         db = (d * (np.float32(0.5) + ((sc - 1) / 2).astype(np.float32))) * np.float32(0.5 if t == 18 else 0.25)
         return ((db * np.abs(q).astype(np.float32)) * np.where(q < 0, np.float32(-1), np.float32(1))).astype(np.float32)
     raise ValueError(t)

@@ -89,9 +89,25 @@ def iq3s_rows() -> np.ndarray:
     return rows
 
 
+def iq2s_rows() -> np.ndarray:
+    """The IQ2_S codebook as the kernels and the oracle expand it from iq2s_grid.inc (base-3 as IQ2_XS's)."""
+    text = (Path(__file__).resolve().parents[1] / "hyper_amd/csrc/iq2s_grid.inc").read_text()
+    body = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("//"))
+    codes = [int(v) for v in body.replace(",", " ").split() if v.isdigit()]
+    assert len(codes) == 1024
+    lv = np.array([8, 25, 43], np.uint8)
+    rows = np.zeros((1024, 8), np.uint8)
+    for i, c in enumerate(codes):
+        for j in range(8):
+            rows[i, j] = lv[c % 3]
+            c //= 3
+    return rows
+
+
 def grid_for(t):
     t = GType(t)
-    return {GType.IQ2_XXS: iq2xxs_rows, GType.IQ3_XXS: iq3xxs_rows, GType.IQ3_S: iq3s_rows}.get(t, iq2xs_rows)()
+    return {GType.IQ2_XXS: iq2xxs_rows, GType.IQ3_XXS: iq3xxs_rows, GType.IQ3_S: iq3s_rows,
+            GType.IQ2_S: iq2s_rows}.get(t, iq2xs_rows)()
 
 
 def ksigns() -> np.ndarray:
@@ -104,6 +120,7 @@ def test_codebooks_match_reference():
     assert hashlib.sha256(iq2xxs_rows().tobytes()).hexdigest() == TABLES["iq2xxs_grid_sha256"]
     assert hashlib.sha256(iq3xxs_rows().tobytes()).hexdigest() == TABLES["iq3xxs_grid_sha256"]
     assert hashlib.sha256(iq3s_rows().tobytes()).hexdigest() == TABLES["iq3s_grid_sha256"]
+    assert hashlib.sha256(iq2s_rows().tobytes()).hexdigest() == TABLES["iq2s_grid_sha256"]
     assert hashlib.sha256(ksigns().tobytes()).hexdigest() == TABLES["ksigns_sha256"]
     assert hashlib.sha256(nf.KV_IQ4NL.astype(np.int8).tobytes()).hexdigest() == TABLES["iq4nl_sha256"]
     assert all(bin(int(s)).count("1") % 2 == 0 for s in ksigns())   # every sign byte has an even bit count
@@ -357,6 +374,40 @@ def test_iq3s_known_answer_positions():
     assert not sm.any()
 
 
+def test_iq2s_known_answer_positions():
+    """IQ2_S (src/kernels4.cu:602-613): 32-group ib's 8-group l takes grid row qs[4 ib + l] with bits 2 l, 2 l + 1 of
+    qh[ib] as index bits 8-9; bit j of the literal byte signs[4 ib + l] negates value j; value = d (0.5 + sc) / 4 * grid,
+    sc the nibble l / 2 of scales[ib].  Rows fixed by the reference's table: row 0 all 8s, row 1 = byte 0 43, the rest 8;
+    row 768 (both high bits) differs from row 0.  Placed by hand: group 0's 8-group 1 takes row 1 with sign byte 0x81,
+    its 8-group 2 row 768; group 2's second 16-group has scale 15."""
+    rows = iq2s_rows()
+    assert list(rows[0]) == [8] * 8 and list(rows[1]) == [43] + [8] * 7
+    r768 = [int(v) for v in rows[768]]
+    assert r768 != [8] * 8
+    blk = np.zeros(82, np.uint8)
+    blk[0:2] = _f16b(1.0)
+    blk[2 + 1] = 1                 # group 0, 8-group 1: row 1
+    blk[34 + 1] = 0x81             # its sign byte: values 0 and 7 negated
+    blk[66] = 3 << 4               # group 0, 8-group 2: index bits 8-9 set (row 768)
+    blk[74 + 2] = 15 << 4          # group 2, second 16-group: scale 15
+    want = np.ones(256, np.float32)                                # d (0.5 + 0) / 4 * 8 = 1
+    want[8:16] = [-43 / 8, 1, 1, 1, 1, 1, 1, -1]
+    want[16:24] = np.array(r768, np.float32) / 8
+    want[80:96] = 31.0                                             # (0.5 + 15) / 4 * 8
+    got = orc.dequant_row(GType.IQ2_S, blk, 256)
+    assert (got == want).all(), np.nonzero(got != want)
+    x = np.arange(256, dtype=np.float32) % 7 - 3.0
+    xq = orc.quantize(GType.Q8_K, x)
+    q8 = xq[4:260].view(np.int8).astype(np.int64)
+    ints = (want * 8).astype(np.int64)
+    ints[80:96] = 8
+    scale = np.ones(16, np.int64)
+    scale[5] = 31                                                  # 16-group 5 = group 2's second half
+    si, sm = orc.block_ints(GType.IQ2_S, blk, xq, 256)
+    assert int(si[0]) == int(sum(scale[g] * (ints[16 * g:16 * g + 16] @ q8[16 * g:16 * g + 16]) for g in range(16)))
+    assert not sm.any()
+
+
 def test_q8_0_weight_known_answers():
     """Q8_0 weights (src/kernels4.cu:421-714, deq8: d * qs[j]): value j of a block is d * (int8) qs[j] in place, and
     against a Q8_0 activation block the integer is sum_j qs[j] y[j] (ggml's vec_dot_q8_0_q8_0), folded as
@@ -523,7 +574,7 @@ def test_q8k_known_answers():
 # ------------------------------------------------------------------ block decoding
 
 ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.IQ4_NL, GType.Q8_0, GType.MXFP4,
-       GType.Q5_0, GType.Q2_K, GType.Q3_K, GType.IQ3_XXS, GType.IQ3_S]
+       GType.Q5_0, GType.Q2_K, GType.Q3_K, GType.IQ3_XXS, GType.IQ3_S, GType.IQ2_S]
 
 
 def blocks(t, nb, seed):
