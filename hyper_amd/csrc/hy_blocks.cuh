@@ -49,12 +49,12 @@ __device__ __forceinline__ uint32_t apply_sign(uint32_t g, uint32_t b4) {
 // the same with the byte mask given (0xFF per negated byte): -g = ~g + 1 per byte, no carry (codebook bytes are not 0)
 __device__ __forceinline__ uint32_t apply_mask(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
 // LDS entries of an expanded IQ2_XS codebook: 512 rows, then 128 sign masks (IQ2_XXS: 256 rows, then the masks)
-__host__ __device__ constexpr int iq2_rows(int t) { return t == IQ2_S ? 1024 : t == IQ2_XS || t == IQ3_S ? 512 : 256; }
+__host__ __device__ constexpr int iq2_rows(int t) { return t == IQ1_S ? 2048 : t == IQ2_S ? 1024 : t == IQ2_XS || t == IQ3_S ? 512 : 256; }
 // sign masks after the rows: the 128 ksign patterns, or for IQ3_S and IQ2_S (literal sign bytes) all 256 bytes
 __host__ __device__ constexpr bool literal_signs(int t) { return t == IQ3_S || t == IQ2_S; }
-__host__ __device__ constexpr int iq2_masks(int t) { return literal_signs(t) ? 256 : 128; }
+__host__ __device__ constexpr int iq2_masks(int t) { return t == IQ1_S ? 0 : literal_signs(t) ? 256 : 128; }   // IQ1_S: no signs
 __host__ __device__ constexpr int iq2_lds(int t) { return iq2_type(t) ? iq2_rows(t) + iq2_masks(t) : 1; }   // uint2 entries
-constexpr int GRID_LDS = 1024 + 256;   // the largest of them (IQ2_S)
+constexpr int GRID_LDS = 2048;   // the largest of them (IQ1_S; IQ2_S 1024 + 256)
 // Q6_K: q6 bytes (0..63) -> q6 - 32 as int8: per byte (q + 96) ^ 128 = q - 32 mod 256 (q + 96 < 256: no carry)
 __device__ __forceinline__ uint32_t q6_signed(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
 
@@ -173,6 +173,35 @@ template <> struct Item<IQ3_XXS> {
         sm = 0;
     }
     __device__ __forceinline__ float tval(int si, int) const { return (h2f(d) * 0.25f) * (float) si; }
+};
+// IQ1_S (50 B: d, qs[32] @2, qh u16[8] @34), src/kernels4.cu:650-659.  Lane L = 32-group L: 8-group l takes grid row
+// qs[4 L + l] | 3 bits (3 l) of qh[L] << 8 (8 int8 values in {-1, 0, 1}), scale ls = 2 ((qh >> 12) & 7) + 1 and delta
+// +-1/8 by qh's top bit: value d ls (grid + delta).  The integers of the reference's own IQ1_S x Q8_K dot
+// (src/iq1s_dot.h:26-64): sumi = sum_ib ls sum_32 grid y, summ = sum_ib ls (-1 if the top bit) (bsum pair of ib);
+// folded as (d / 8) (8 sumi + summ), an exact integer times a power-of-two scaled d.  Blocks are 2-byte aligned.
+template <> struct Item<IQ1_S> {
+    uint32_t gq, qh;   // the lane's 4 index bytes; its qh halfword
+    uint16_t d;
+    const uint2 *grid;
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+        gq = (uint32_t) ld_u16(b + 2 + 4 * L) | ((uint32_t) ld_u16(b + 4 + 4 * L) << 16);
+        qh = ld_u16(b + 34 + 2 * L);
+        d = ld_u16(b);
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
+        const uint32_t *ya = (const uint32_t *) (y + 4 + 32 * L);
+        int s = 0;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint2 g = grid[((gq >> (8 * l)) & 255) | (((qh >> (3 * l)) & 7) << 8)];
+            s = sdot4(g.y, ya[2 * l + 1], sdot4(g.x, ya[2 * l], s));
+        }
+        const int ls = 2 * (int) ((qh >> 12) & 7) + 1;
+        const int16_t *bs = (const int16_t *) (y + 260);
+        si = ls * s;
+        sm = (qh & 0x8000 ? -ls : ls) * (bs[2 * L] + bs[2 * L + 1]);
+    }
+    __device__ __forceinline__ float tval(int si, int sm) const { return (h2f(d) * 0.125f) * (float) (8 * si + sm); }
 };
 // IQ2_S (82 B: d, qs[32] @2, signs[32] @34, qh[8] @66, scales[8] @74), src/kernels4.cu:602-613.  Lane L = 32-group
 // L: 8-group l takes grid row qs[4 L + l] | bits 2 l, 2 l + 1 of qh[L] << 8 (8-byte rows of the 1024-row codebook),
@@ -486,7 +515,7 @@ template <> struct Item<Q5_0> {
 // expand a grid codebook (base-3 codes: IQ2_XS 512 rows, IQ2_XXS 256, IQ2_S 1024; base-8 codes: IQ3_XXS 256 and IQ3_S
 // 512 rows of 4 bytes, in .x) into rows x 8 bytes of LDS, followed by the sign patterns as byte masks (entry rows + i:
 // byte j = 0xFF where bit j of ksign(i) is set, the parity bit giving byte 7; for the literal-sign types, IQ3_S and
-// IQ2_S, bit j of i itself, i < 256)
+// IQ2_S, bit j of i itself, i < 256; IQ1_S has no signs: its 2048 rows hold int8 -1 / 0 / 1)
 template <int T>
 __device__ __forceinline__ void expand_iq2_grid(uint2 *grid) {
     static_assert(iq2_type(T), "an IQ2 codebook");
@@ -509,6 +538,17 @@ __device__ __forceinline__ void expand_iq2_grid(uint2 *grid) {
 #pragma unroll
             for (int j = 0; j < 4; ++j, c >>= 3) lo |= (2u * (c & 7) + 1u) << (8 * j);
             grid[i] = make_uint2(lo, 0u);
+            continue;
+        }
+        if constexpr (T == IQ1_S) {
+            uint32_t c = c_iq1s_code[i], lo = 0, hi = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t v = (uint32_t) (int) ((c % 3) - 1) & 0xFFu;   // digit d -> int8 d - 1
+                c /= 3;
+                if (j < 4) lo |= v << (8 * j); else hi |= v << (8 * (j - 4));
+            }
+            grid[i] = make_uint2(lo, hi);
             continue;
         }
         uint32_t c = T == IQ2_XS ? c_iq2xs_code[i] : T == IQ2_S ? c_iq2s_code[i] : c_iq2xxs_code[i], lo = 0, hi = 0;

@@ -17,21 +17,23 @@
 namespace hy {
 
 // GGUF type ids (src/gguf.h:13-18)
-enum GT : int { Q5_0 = 6, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, IQ2_XXS = 16, IQ2_XS = 17, IQ3_XXS = 18, IQ4_NL = 20, IQ3_S = 21, IQ2_S = 22, IQ4_XS = 23, MXFP4 = 39 };
+enum GT : int { Q5_0 = 6, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, IQ2_XXS = 16, IQ2_XS = 17, IQ3_XXS = 18, IQ1_S = 19, IQ4_NL = 20, IQ3_S = 21, IQ2_S = 22, IQ4_XS = 23, MXFP4 = 39 };
 
 constexpr int Q8K_BYTES = 292;   // float d; int8 qs[256]; int16 bsums[16]
 constexpr int Q8_0_BYTES = 34;   // fp16 d; int8 qs[32]
 
 __host__ __device__ constexpr int block_bytes(int t) {
     return t == Q4_K ? 144 : t == Q5_K ? 176 : t == Q6_K ? 210 : t == IQ4_XS ? 136 : t == IQ2_XS ? 74 : t == IQ2_XXS ? 66
-         : t == IQ4_NL ? 18 : t == Q8_0 ? 34 : t == MXFP4 ? 17 : t == Q5_0 ? 22 : t == Q2_K ? 84 : t == Q3_K ? 110 : t == IQ3_XXS ? 98 : t == IQ3_S ? 110 : t == IQ2_S ? 82 : t == Q8_K ? 292 : 0;
+         : t == IQ4_NL ? 18 : t == Q8_0 ? 34 : t == MXFP4 ? 17 : t == Q5_0 ? 22 : t == Q2_K ? 84 : t == Q3_K ? 110 : t == IQ3_XXS ? 98 : t == IQ3_S ? 110 : t == IQ2_S ? 82 : t == IQ1_S ? 50 : t == Q8_K ? 292 : 0;
 }
 __host__ __device__ constexpr int block_elems(int t) {
     return (t == IQ4_NL || t == Q8_0 || t == MXFP4 || t == Q5_0) ? 32
-         : (t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ2_XXS || t == Q2_K || t == Q3_K || t == IQ3_XXS || t == IQ3_S || t == IQ2_S || t == Q8_K) ? 256 : 0;
+         : (t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ2_XXS || t == Q2_K || t == Q3_K || t == IQ3_XXS || t == IQ3_S || t == IQ2_S || t == IQ1_S || t == Q8_K) ? 256 : 0;
 }
-// the grid types (IQ2_XS, IQ2_XXS, IQ2_S, IQ3_XXS, IQ3_S): codebook rows and sign masks in LDS (expand_iq2_grid)
-__host__ __device__ constexpr bool iq2_type(int t) { return t == IQ2_XS || t == IQ2_XXS || t == IQ2_S || t == IQ3_XXS || t == IQ3_S; }
+// the grid types (IQ2_XS, IQ2_XXS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S): codebook rows and sign masks in LDS (expand_iq2_grid)
+__host__ __device__ constexpr bool iq2_type(int t) {
+    return t == IQ2_XS || t == IQ2_XXS || t == IQ2_S || t == IQ3_XXS || t == IQ3_S || t == IQ1_S;
+}
 __host__ __device__ constexpr int vec_dot_type(int t) { return t == IQ4_NL || t == Q8_0 || t == MXFP4 || t == Q5_0 ? Q8_0 : Q8_K; }
 
 // ------------------------------------------------------------------ scalar helpers
@@ -282,6 +284,11 @@ __device__ __constant__ const uint16_t c_iq2xxs_code[256] = {
 // IQ2_S codebook rows, the same coding (g_iq2s_grid, src/iq_grids.h:210-467)
 __device__ __constant__ const uint16_t c_iq2s_code[1024] = {
 #include "iq2s_grid.inc"
+};
+// IQ1_S codebook rows of 8 int8 values in {-1, 0, 1}, base-3 coded with digit = value + 1 (g_iq1s_grid,
+// src/iq_grids.h:504-1017)
+__device__ __constant__ const uint16_t c_iq1s_code[2048] = {
+#include "iq1s_grid.inc"
 };
 // IQ3_XXS codebook rows of 4 bytes, base-8 coded: digit i = byte i's level, 4 + 8 d (62 for d = 7) (g_iq3xxs_grid,
 // src/iq_grids.h:468-503)

@@ -625,6 +625,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     case IQ3_XXS: { constexpr int TT = IQ3_XXS; CALL; }                                         \
     case IQ3_S: { constexpr int TT = IQ3_S; CALL; }                                             \
     case IQ2_S: { constexpr int TT = IQ2_S; CALL; }                                             \
+    case IQ1_S: { constexpr int TT = IQ1_S; CALL; }                                             \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE;   \
     }
 

@@ -146,6 +146,30 @@ template <> struct Raw<IQ3_XXS> {
     }
     __device__ __forceinline__ float fold(int si, int) const { return (h2f(d) * 0.25f) * (float) si; }
 };
+// IQ1_S (50 B): chunk c = 32-group c; lane q takes 8-group q: grid row qs[4 c + q] | 3 bits (3 q) of qh[c] << 8 (int8
+// -1 / 0 / 1), the chunk's scale ls; the delta term rides on the mins MFMA with the chunk's ls * (+-1) as its "min", so
+// sm = sum_ib ls sign sum_32 y and the fold is (d / 8) (8 si + sm) (src/kernels4.cu:650-659; src/iq1s_dot.h:26-64).
+template <> struct Raw<IQ1_S> {
+    static constexpr bool mins = true, g16 = false, per_chunk = false;
+    uint32_t gq[2], qh[4], d;   // gq: the lane's index byte of chunk c in byte c % 4 of gq[c / 4]; qh[c] in halfwords
+    __device__ __forceinline__ void load(const uint8_t *blk, int q) {
+        gq[0] = gq[1] = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) gq[c >> 2] |= (uint32_t) blk[2 + 4 * c + q] << (8 * (c & 3));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qh[i] = (uint32_t) ld_u16(blk + 34 + 4 * i) | ((uint32_t) ld_u16(blk + 36 + 4 * i) << 16);
+        d = ld_u16(blk);
+    }
+    __device__ __forceinline__ void chunk(int c, int q, const uint2 *grid, uint32_t &b0, uint32_t &b1, int &s0, int &s1, int &mn) const {
+        const uint32_t h = (qh[c >> 1] >> (16 * (c & 1))) & 0xffff;
+        const uint2 g = grid[((gq[c >> 2] >> (8 * (c & 3))) & 255) | (((h >> (3 * q)) & 7) << 8)];
+        b0 = g.x; b1 = g.y;
+        s0 = 2 * (int) ((h >> 12) & 7) + 1;
+        s1 = 0;
+        mn = h & 0x8000 ? -s0 : s0;
+    }
+    __device__ __forceinline__ float fold(int si, int sm) const { return (h2f(d) * 0.125f) * (float) (8 * si + sm); }
+};
 // IQ2_S (82 B): chunk c = 32-group c; lane q takes 8-group q: grid row qs[4 c + q] | bits 2 q, 2 q + 1 of qh[c] << 8,
 // sign byte signs[4 c + q], the chunk's 16-group scales 2 sc + 1 from the nibbles of scales[c] (s0 for lanes q < 2)
 // (src/kernels4.cu:602-613; ggml's vec_dot_iq2_s_q8_K integers).
@@ -1218,6 +1242,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
     case IQ3_XXS: { constexpr int TT = IQ3_XXS; __VA_ARGS__; }                                           \
     case IQ3_S: { constexpr int TT = IQ3_S; __VA_ARGS__; }                                               \
     case IQ2_S: { constexpr int TT = IQ2_S; __VA_ARGS__; }                                               \
+    case IQ1_S: { constexpr int TT = IQ1_S; __VA_ARGS__; }                                               \
     default: set_error("grouped GEMM: unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 

@@ -167,6 +167,7 @@ static int launch_gemv_t(const hy_moe_dev &m, const float *src, int ss, const in
     case IQ3_XXS: { constexpr int TT = IQ3_XXS; CALL; }                                  \
     case IQ3_S: { constexpr int TT = IQ3_S; CALL; }                                      \
     case IQ2_S: { constexpr int TT = IQ2_S; CALL; }                                      \
+    case IQ1_S: { constexpr int TT = IQ1_S; CALL; }                                      \
     default: set_error("unsupported expert type %d", (int) (T)); return HY_EUNSUPPORTED_TYPE; \
     }
 
@@ -373,6 +374,7 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, floa
     else if (type == IQ3_XXS) expand_iq2_grid<IQ3_XXS>(grid);
     else if (type == IQ3_S) expand_iq2_grid<IQ3_S>(grid);
     else if (type == IQ2_S) expand_iq2_grid<IQ2_S>(grid);
+    else if (type == IQ1_S) expand_iq2_grid<IQ1_S>(grid);
     __syncthreads();
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -425,6 +427,14 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, floa
         const uint8_t *b = row + (size_t) (i >> 5) * 17;
         const int e = i & 31;
         v = (float) (int8_t) (kvfp4((b[1 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF) & 0xff) * e8m0_half(b[0]);
+    } else if (type == IQ1_S) {   // src/kernels4.cu:650-659
+        const uint8_t *b = row + (size_t) (i >> 8) * 50;
+        const int e = i & 255, ib = e >> 5, l = (e >> 3) & 3, j = e & 7;
+        const int qh = ld_u16(b + 34 + 2 * ib);
+        const float dl = h2f(ld_u16(b)) * (float) (2 * ((qh >> 12) & 7) + 1);
+        const float delta = qh & 0x8000 ? -0.125f : 0.125f;
+        const uint2 gr = grid[b[2 + 4 * ib + l] | (((qh >> (3 * l)) & 7) << 8)];
+        v = dl * ((float) (int8_t) (((j < 4 ? gr.x : gr.y) >> (8 * (j & 3))) & 0xff) + delta);
     } else if (type == IQ2_S) {   // src/kernels4.cu:602-613
         const uint8_t *b = row + (size_t) (i >> 8) * 82;
         const int e = i & 255, ib = e >> 5, l = (e >> 3) & 3, j = e & 7;

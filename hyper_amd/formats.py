@@ -11,6 +11,7 @@ Block sizes follow src/gguf.cpp:43-82; layouts follow the reference's deq8<T> (s
   MXFP4 17 B per 32: e (E8M0 exponent, scale 2^(e - 128)) @0, qs[16] @1
   Q2_K 84 B: scales[16] (scale | min << 4 per 16 values) @0, qs[64] (2-bit fields) @16, d f16 @80, dmin f16 @82
   IQ3_XXS 98 B: d f16, qs[64] (grid indices, two 4-byte rows per 8 values) @2, u32[8] (signs | scale << 28) @66
+  IQ1_S 50 B: d f16, qs[32] @2, qh u16[8] (index bits 8-10, scale bits 12-14, delta sign bit 15) @34
   IQ2_S 82 B: d f16, qs[32] @2, signs[32] @34, qh[8] (index bits 8-9) @66, scales[8] (nibbles per 16) @74
   IQ3_S 110 B: d f16, qs[64] @2, qh[8] (9th index bits) @66, signs[32] @74, scales[4] (nibbles) @106
   Q3_K 110 B: hmask[32] @0, qs[64] (2-bit fields) @32, scales[12] (16 signed 6-bit scales) @96, d f16 @108
@@ -40,6 +41,7 @@ class GType(IntEnum):
     IQ2_XXS = 16
     IQ2_XS = 17
     IQ3_XXS = 18
+    IQ1_S = 19
     IQ4_NL = 20
     IQ3_S = 21
     IQ2_S = 22
@@ -48,7 +50,7 @@ class GType(IntEnum):
 
 
 _BYTES = {GType.Q8_0: 34, GType.Q4_K: 144, GType.Q5_K: 176, GType.Q6_K: 210, GType.Q8_K: 292,
-          GType.IQ2_XXS: 66, GType.IQ2_XS: 74, GType.IQ4_NL: 18, GType.IQ4_XS: 136, GType.MXFP4: 17, GType.Q5_0: 22, GType.Q2_K: 84, GType.Q3_K: 110, GType.IQ3_XXS: 98, GType.IQ3_S: 110, GType.IQ2_S: 82}
+          GType.IQ2_XXS: 66, GType.IQ2_XS: 74, GType.IQ4_NL: 18, GType.IQ4_XS: 136, GType.MXFP4: 17, GType.Q5_0: 22, GType.Q2_K: 84, GType.Q3_K: 110, GType.IQ3_XXS: 98, GType.IQ3_S: 110, GType.IQ2_S: 82, GType.IQ1_S: 50}
 _ELEMS = {GType.Q8_0: 32, GType.IQ4_NL: 32, GType.MXFP4: 32, GType.Q5_0: 32}
 
 
@@ -75,7 +77,7 @@ def q8_row_bytes(vt, n: int) -> int:
 
 # fp16 scale fields per type: byte offsets inside the block
 _F16_FIELDS = {GType.Q4_K: (0, 2), GType.Q5_K: (0, 2), GType.Q6_K: (208,), GType.IQ4_NL: (0,), GType.Q8_0: (0,),
-               GType.IQ4_XS: (0,), GType.IQ2_XS: (0,), GType.IQ2_XXS: (0,), GType.MXFP4: (), GType.Q5_0: (0,), GType.Q2_K: (80, 82), GType.Q3_K: (108,), GType.IQ3_XXS: (0,), GType.IQ3_S: (0,), GType.IQ2_S: (0,)}
+               GType.IQ4_XS: (0,), GType.IQ2_XS: (0,), GType.IQ2_XXS: (0,), GType.MXFP4: (), GType.Q5_0: (0,), GType.Q2_K: (80, 82), GType.Q3_K: (108,), GType.IQ3_XXS: (0,), GType.IQ3_S: (0,), GType.IQ2_S: (0,), GType.IQ1_S: (0,)}
 # E8M0 exponent bytes per type
 _E8M0_FIELDS = {GType.MXFP4: (0,)}
 

@@ -34,11 +34,11 @@ enum {
     HY_EINVAL = 4               /* null pointer or out-of-range argument */
 };
 
-/* GGUF type ids used by the path (src/gguf.h:13-18); expert weights: Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ2_XS, IQ2_S,
-   IQ3_XXS, IQ3_S, IQ4_NL, IQ4_XS, Q8_0, MXFP4 and Q5_0 (of src/kernels4.cu:1951-1971's list); Q8_K and Q8_0 as activation rows */
+/* GGUF type ids used by the path (src/gguf.h:13-18); expert weights: Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ1_S, IQ2_XXS, IQ2_XS,
+   IQ2_S, IQ3_XXS, IQ3_S, IQ4_NL, IQ4_XS, Q8_0, MXFP4 and Q5_0 (of src/kernels4.cu:1951-1971's list); Q8_K and Q8_0 as activation rows */
 enum {
     HY_Q5_0 = 6, HY_Q8_0 = 8, HY_Q2_K = 10, HY_Q3_K = 11, HY_Q4_K = 12, HY_Q5_K = 13, HY_Q6_K = 14, HY_Q8_K = 15,
-    HY_IQ2_XXS = 16, HY_IQ2_XS = 17, HY_IQ3_XXS = 18, HY_IQ4_NL = 20, HY_IQ3_S = 21, HY_IQ2_S = 22, HY_IQ4_XS = 23, HY_MXFP4 = 39
+    HY_IQ2_XXS = 16, HY_IQ2_XS = 17, HY_IQ3_XXS = 18, HY_IQ1_S = 19, HY_IQ4_NL = 20, HY_IQ3_S = 21, HY_IQ2_S = 22, HY_IQ4_XS = 23, HY_MXFP4 = 39
 };
 
 /* Expert weights of one layer on the device (replaces MoeDev, src/kernels4.cuh:56-63): n_local experts,

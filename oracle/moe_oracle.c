@@ -33,6 +33,7 @@ size_t or_block_bytes(int type) {
     case OR_IQ3_XXS: return 98;
     case OR_IQ3_S: return 110;
     case OR_IQ2_S: return 82;
+    case OR_IQ1_S: return 50;
     default: return 0;
     }
 }
@@ -40,7 +41,7 @@ int or_block_elems(int type) {
     switch (type) {
     case OR_Q8_0: case OR_IQ4_NL: case OR_MXFP4: case OR_Q5_0: return 32;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_Q8_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K:
-    case OR_Q3_K: case OR_IQ3_XXS: case OR_IQ3_S: case OR_IQ2_S: return 256;
+    case OR_Q3_K: case OR_IQ3_XXS: case OR_IQ3_S: case OR_IQ2_S: case OR_IQ1_S: return 256;
     default: return 0;
     }
 }
@@ -50,7 +51,7 @@ int or_vec_dot_type(int type) {
     switch (type) {
     case OR_IQ4_NL: case OR_Q8_0: case OR_MXFP4: case OR_Q5_0: return OR_Q8_0;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K: case OR_Q3_K: case OR_IQ3_XXS:
-    case OR_IQ3_S: case OR_IQ2_S: return OR_Q8_K;
+    case OR_IQ3_S: case OR_IQ2_S: case OR_IQ1_S: return OR_Q8_K;
     default: return -1;
     }
 }
@@ -91,7 +92,13 @@ static const uint16_t iq3s_code[512] = {
 static const uint16_t iq2s_code[1024] = {
 #include "../hyper_amd/csrc/iq2s_grid.inc"
 };
+/* IQ1_S codebook: 2048 rows of 8 int8 values in {-1, 0, 1}, base-3 coded with digit = value + 1 (values of
+   src/iq_grids.h:504-1017) */
+static const uint16_t iq1s_code[2048] = {
+#include "../hyper_amd/csrc/iq1s_grid.inc"
+};
 static uint8_t iq2xs_rows[512][8], iq2xxs_rows[256][8], iq2s_rows[1024][8], iq3xxs_rows[256][4], iq3s_rows[512][4];
+static int8_t iq1s_rows[2048][8];
 static int iq2xs_ready = 0;
 static void iq2xs_init(void) {   /* the grid codebooks */
     if (__atomic_load_n(&iq2xs_ready, __ATOMIC_ACQUIRE)) return;
@@ -107,6 +114,10 @@ static void iq2xs_init(void) {   /* the grid codebooks */
     for (int i = 0; i < 256; ++i) {
         unsigned c = iq3xxs_code[i];
         for (int j = 0; j < 4; ++j) { iq3xxs_rows[i][j] = (uint8_t) ((c & 7) == 7 ? 62 : 4 + 8 * (c & 7)); c >>= 3; }
+    }
+    for (int i = 0; i < 2048; ++i) {
+        unsigned c = iq1s_code[i];
+        for (int j = 0; j < 8; ++j) { iq1s_rows[i][j] = (int8_t) ((int) (c % 3) - 1); c /= 3; }
     }
     for (int i = 0; i < 1024; ++i) {
         unsigned c = iq2s_code[i];
@@ -339,6 +350,15 @@ static inline int iq2s_q(const uint8_t *b, int e) {
     const int g = iq2s_rows[b[2 + 4 * ib + l] | (((b[66 + ib] >> (2 * l)) & 3) << 8)][j];
     return (b[34 + 4 * ib + l] >> j) & 1 ? -g : g;
 }
+/* IQ1_S (src/kernels4.cu:650-659): element e of 32-group ib, 8-group l, position j: grid row qs[4 ib + l] (qs at 2)
+   with 3 bits (3 l) of qh[ib] (u16 at 34) as index bits 8-10, value j (-1, 0 or 1); the group's scale 2 ((qh >> 12) & 7)
+   + 1, its delta -1/8 if qh's top bit is set, else +1/8 */
+static inline unsigned iq1s_qh(const uint8_t *b, int ib) { return (unsigned) b[34 + 2 * ib] | ((unsigned) b[35 + 2 * ib] << 8); }
+static inline int iq1s_q(const uint8_t *b, int e) {
+    const int ib = e >> 5, l = (e >> 3) & 3;
+    return iq1s_rows[b[2 + 4 * ib + l] | (((iq1s_qh(b, ib) >> (3 * l)) & 7) << 8)][e & 7];
+}
+static inline int iq1s_ls(const uint8_t *b, int ib) { return 2 * (int) ((iq1s_qh(b, ib) >> 12) & 7) + 1; }
 static inline int iq2s_sc(const uint8_t *b, int e) { return (b[74 + (e >> 5)] >> (4 * ((e >> 4) & 1))) & 15; }
 static inline int iq3s_sc(const uint8_t *b, int ib) { return (b[106 + (ib >> 1)] >> (4 * (ib & 1))) & 15; }
 static inline int iq2xs_sc(const uint8_t *b, int e) {
@@ -393,6 +413,13 @@ int or_dequant_row(int type, const uint8_t *row, int n, float *out) {
             break;
         case OR_Q8_0:
             for (int e = 0; e < 32; ++e) o[e] = h2f(b) * (float) (int8_t) b[2 + e];
+            break;
+        case OR_IQ1_S:
+            for (int e = 0; e < 256; ++e) {
+                const float dl = h2f(b) * (float) iq1s_ls(b, e >> 5);
+                const float delta = iq1s_qh(b, e >> 5) & 0x8000 ? -0.125f : 0.125f;
+                o[e] = dl * ((float) iq1s_q(b, e) + delta);
+            }
             break;
         case OR_IQ2_S:
             for (int e = 0; e < 256; ++e) {
@@ -497,6 +524,18 @@ static void block_ints_scalar(int type, const uint8_t *b, const uint8_t *y, int3
     case OR_Q5_0:      /* ggml's vec_dot_q5_0_q8_0 integer part: sum_32 (x - 16) q8 */
         for (int l = 0; l < 32; ++l) si += q5_0_q(b, l) * q8[l];
         break;
+    case OR_IQ1_S: {   /* the reference's IQ1_S x Q8_K dot (src/iq1s_dot.h:26-64): sumi = sum_ib ls sum_32 grid y,
+                          summ = sum_ib ls (-1 if qh's top bit) (sum_32 y, the bsum pair) */
+        int16_t bs[16]; memcpy(bs, y + 260, 32);
+        for (int ib = 0; ib < 8; ++ib) {
+            int32_t s = 0;
+            for (int l = 0; l < 32; ++l) s += iq1s_q(b, 32 * ib + l) * q8[32 * ib + l];
+            const int ls = iq1s_ls(b, ib);
+            si += ls * s;
+            sm += (iq1s_qh(b, ib) & 0x8000 ? -ls : ls) * (bs[2 * ib] + bs[2 * ib + 1]);
+        }
+        break;
+    }
     case OR_IQ2_S:     /* ggml's vec_dot_iq2_s_q8_K: sum over 16-groups (2 sc + 1) sum_16 grid sign y */
         for (int g = 0; g < 16; ++g) {
             int32_t s = 0;
@@ -620,7 +659,7 @@ static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *su
 static int dot_ok(int type) {
     return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_IQ4_XS || type == OR_IQ2_XS || type == OR_IQ4_NL ||
            type == OR_Q8_0 || type == OR_IQ2_XXS || type == OR_MXFP4 || type == OR_Q5_0 || type == OR_Q2_K || type == OR_Q3_K ||
-           type == OR_IQ3_XXS || type == OR_IQ3_S || type == OR_IQ2_S;
+           type == OR_IQ3_XXS || type == OR_IQ3_S || type == OR_IQ2_S || type == OR_IQ1_S;
 }
 int or_block_ints(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ) {
     if (!dot_ok(type) || n % or_block_elems(type)) return -1;
@@ -654,6 +693,7 @@ static float row_dot(int type, const uint8_t *row, const uint8_t *xq, int n) {
         case OR_Q3_K: t = h2f(b + 108) * (float) si; break;
         case OR_IQ3_XXS: t = (h2f(b) * 0.25f) * (float) si; break;
         case OR_IQ3_S: t = h2f(b) * (float) si; break;
+        case OR_IQ1_S: t = (h2f(b) * 0.125f) * (float) (8 * si + sm); break;   /* exact: |8 si + sm| < 2^24 */
         case OR_Q2_K: t = fmaf(h2f(b + 80), (float) si, -(h2f(b + 82) * (float) sm)); break;
         case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ2_S: t = (h2f(b) * 0.125f) * (float) si; break;
         case OR_MXFP4: t = e8m0_half(b[0]) * (float) si; break;

@@ -41,7 +41,7 @@ extern "C" {
 /* GGUF type ids (src/gguf.h:13-18) */
 enum {
     OR_Q5_0 = 6, OR_Q8_0 = 8, OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14, OR_Q8_K = 15,
-    OR_IQ2_XXS = 16, OR_IQ2_XS = 17, OR_IQ3_XXS = 18, OR_IQ4_NL = 20, OR_IQ3_S = 21, OR_IQ2_S = 22, OR_IQ4_XS = 23, OR_MXFP4 = 39
+    OR_IQ2_XXS = 16, OR_IQ2_XS = 17, OR_IQ3_XXS = 18, OR_IQ1_S = 19, OR_IQ4_NL = 20, OR_IQ3_S = 21, OR_IQ2_S = 22, OR_IQ4_XS = 23, OR_MXFP4 = 39
 };
 
 size_t or_block_bytes(int type);      /* bytes per block (src/gguf.cpp:43-82) */

@@ -177,6 +177,19 @@ def iq2s(b, grid_rows):
     return dict(q=q, sc=2 * sc + 1, m=None, gsize=16, d=f16(b[:, 0:2]))
 
 
+def iq1s(b, grid_rows):
+    """grid_rows: [2048, 8] int8 codebook values.  32-group ib: four index bytes at 2 + 4 ib, the little-endian qh[ib]
+    at 34 + 2 ib: bits 3 l .. 3 l + 2 are index bits 8-10 of 8-group l, bits 12-14 the scale s (factor 2 s + 1), bit 15
+    the delta's sign (-1/8 if set).  m carries factor * sign, the weight of the group's activation sum."""
+    b = b.reshape(-1, 50)
+    qh = np.ascontiguousarray(b[:, 34:50]).view(np.uint16).astype(np.int64).reshape(-1, 8)
+    idx = b[:, 2:34].astype(np.int64).reshape(-1, 8, 4) | (((qh[:, :, None] >> (3 * np.arange(4))) & 7) << 8)
+    q = grid_rows[idx].astype(np.int64).reshape(-1, 256)
+    ls = 2 * ((qh >> 12) & 7) + 1
+    sgn = np.where(qh & 0x8000, -1, 1)
+    return dict(q=q, sc=ls, m=ls * sgn, gsize=32, d=f16(b[:, 0:2]), delta=np.where(qh & 0x8000, -0.125, 0.125))
+
+
 def q5_0w(b):
     """Q5_0 weights: d f16 @0, qh little-endian u32 @2, qs[16] @6; value j = (nibble j + 16 * bit j of qh) - 16, the
     nibbles in qs order, low halves first (values 0..15), then high halves (16..31)."""
@@ -240,6 +253,7 @@ def decode(t, b, grid_rows=None, ksigns=None):
     if t == 18: return iq3xxs(b, grid_rows, ksigns)
     if t == 21: return iq3s(b, grid_rows)
     if t == 22: return iq2s(b, grid_rows)
+    if t == 19: return iq1s(b, grid_rows)
     if t == 17: return iq2xs(b, grid_rows, ksigns)
     if t == 16: return iq2xxs(b, grid_rows, ksigns)
     raise ValueError(t)
@@ -264,6 +278,10 @@ def dequant(t, b, grid_rows=None, ksigns=None):
         return (q.astype(np.float32) * d).astype(np.float32)
     if t == 8:
         return (d * q.astype(np.float32)).astype(np.float32)
+    if t == 19:   # d (2 s + 1) (grid + delta)
+        dl = (d * sc).astype(np.float32)
+        delta = np.repeat(f["delta"], gs, axis=1).astype(np.float32)
+        return (dl * (q.astype(np.float32) + delta)).astype(np.float32)
     if t == 21:   # d (2 sc + 1), then times the grid byte, then the sign
         db = (d * sc.astype(np.float32)).astype(np.float32)
         return ((db * np.abs(q).astype(np.float32)) * np.where(q < 0, np.float32(-1), np.float32(1))).astype(np.float32)

@@ -74,6 +74,8 @@ ROUTE_GU_CASES = [
     (GType.IQ3_S, GType.IQ2_XS, 16, 7168, 2048, 6, 1, False),
     (GType.IQ2_S, GType.IQ2_S, 16, 7168, 2048, 6, 2, True),
     (GType.IQ2_S, GType.IQ3_S, 24, 2048, 768, 8, 3, False),
+    (GType.IQ1_S, GType.IQ1_S, 16, 7168, 2048, 6, 2, True),
+    (GType.IQ1_S, GType.IQ2_XXS, 24, 2048, 768, 8, 3, False),
 ]
 
 

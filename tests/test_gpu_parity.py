@@ -161,6 +161,8 @@ DECODE_CASES = [
     (GType.IQ3_S, GType.IQ4_XS, 2048, 768, 6, 3),
     (GType.IQ2_S, GType.IQ2_S, 7168, 2048, 6, 2),
     (GType.IQ2_S, GType.Q4_K, 2048, 768, 8, 3),
+    (GType.IQ1_S, GType.IQ1_S, 7168, 2048, 6, 2),
+    (GType.IQ1_S, GType.Q2_K, 2048, 768, 8, 3),
 ]
 
 
@@ -242,6 +244,8 @@ GEMM_CASES = [
     (GType.IQ3_S, GType.Q4_K, 2048, 512, 6, 90),
     (GType.IQ2_S, GType.IQ2_S, 7168, 2048, 6, 8),
     (GType.IQ2_S, GType.Q6_K, 2048, 768, 8, 60),
+    (GType.IQ1_S, GType.IQ1_S, 7168, 2048, 6, 8),
+    (GType.IQ1_S, GType.Q4_K, 2048, 768, 8, 60),
     (GType.Q4_K, GType.Q6_K, 2048, 768, 1, 100),    # k = 1: the pair is the token (reciprocal 2^32)
     (GType.Q4_K, GType.Q6_K, 1024, 512, 3, 90),     # odd k: the pair-to-token multiply-high
     (GType.Q4_K, GType.Q6_K, 1024, 256, 16, 12),    # k = E: every expert active, every token in each

@@ -104,10 +104,24 @@ def iq2s_rows() -> np.ndarray:
     return rows
 
 
+def iq1s_rows() -> np.ndarray:
+    """The IQ1_S codebook as the kernels and the oracle expand it from iq1s_grid.inc (base-3, digit = value + 1)."""
+    text = (Path(__file__).resolve().parents[1] / "hyper_amd/csrc/iq1s_grid.inc").read_text()
+    body = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("//"))
+    codes = [int(v) for v in body.replace(",", " ").split() if v.isdigit()]
+    assert len(codes) == 2048
+    rows = np.zeros((2048, 8), np.int8)
+    for i, c in enumerate(codes):
+        for j in range(8):
+            rows[i, j] = c % 3 - 1
+            c //= 3
+    return rows
+
+
 def grid_for(t):
     t = GType(t)
     return {GType.IQ2_XXS: iq2xxs_rows, GType.IQ3_XXS: iq3xxs_rows, GType.IQ3_S: iq3s_rows,
-            GType.IQ2_S: iq2s_rows}.get(t, iq2xs_rows)()
+            GType.IQ2_S: iq2s_rows, GType.IQ1_S: iq1s_rows}.get(t, iq2xs_rows)()
 
 
 def ksigns() -> np.ndarray:
@@ -121,6 +135,7 @@ def test_codebooks_match_reference():
     assert hashlib.sha256(iq3xxs_rows().tobytes()).hexdigest() == TABLES["iq3xxs_grid_sha256"]
     assert hashlib.sha256(iq3s_rows().tobytes()).hexdigest() == TABLES["iq3s_grid_sha256"]
     assert hashlib.sha256(iq2s_rows().tobytes()).hexdigest() == TABLES["iq2s_grid_sha256"]
+    assert hashlib.sha256(iq1s_rows().tobytes()).hexdigest() == TABLES["iq1s_grid_sha256"]
     assert hashlib.sha256(ksigns().tobytes()).hexdigest() == TABLES["ksigns_sha256"]
     assert hashlib.sha256(nf.KV_IQ4NL.astype(np.int8).tobytes()).hexdigest() == TABLES["iq4nl_sha256"]
     assert all(bin(int(s)).count("1") % 2 == 0 for s in ksigns())   # every sign byte has an even bit count
@@ -408,6 +423,40 @@ def test_iq2s_known_answer_positions():
     assert not sm.any()
 
 
+def test_iq1s_known_answer_positions():
+    """IQ1_S (src/kernels4.cu:650-659): 32-group ib's 8-group l takes grid row qs[4 ib + l] with bits 3 l .. 3 l + 2 of
+    qh[ib] as index bits 8-10; value = d (2 s + 1) (grid + delta), s = qh bits 12-14, delta = -1/8 if qh bit 15 else
+    +1/8.  Rows fixed by the reference's table: row 0 = all -1, row 1 = -1 except byte 0 = +1 (0xffffffffffffff01 read
+    little-endian); row 1792 (index bits 8-10 all set) differs from row 0.  Placed by hand: group 0's 8-group 1 takes
+    row 1, group 1's 8-group 2 row 1792 with scale 5 (factor 11) and the negative delta."""
+    rows = iq1s_rows()
+    assert list(rows[0]) == [-1] * 8
+    r1, r1792 = [int(v) for v in rows[1]], [int(v) for v in rows[1792]]
+    assert r1 == [1] + [-1] * 7 and r1792 != [-1] * 8
+    blk = np.zeros(50, np.uint8)
+    blk[0:2] = _f16b(0.5)
+    blk[2 + 1] = 1                                                        # group 0, 8-group 1: row 1
+    qh1 = (7 << 6) | (5 << 12) | 0x8000                                   # group 1: 8-group 2 high bits, scale 5, -delta
+    blk[34 + 2:34 + 4] = np.frombuffer(np.uint16(qh1).tobytes(), np.uint8)
+    grid = np.full(256, -1.0)
+    grid[8:16] = r1
+    grid[48:56] = r1792
+    dl = np.array([0.5] * 32 + [0.5 * 11] * 32 + [0.5] * 192)
+    delta = np.array([0.125] * 32 + [-0.125] * 32 + [0.125] * 192)
+    want = (dl.astype(np.float32) * (grid.astype(np.float32) + delta.astype(np.float32))).astype(np.float32)
+    got = orc.dequant_row(GType.IQ1_S, blk, 256)
+    assert (got == want).all(), np.nonzero(got != want)
+    x = np.arange(256, dtype=np.float32) % 9 - 4.0
+    xq = orc.quantize(GType.Q8_K, x)
+    q8 = xq[4:260].view(np.int8).astype(np.int64)
+    ls = np.array([1, 11, 1, 1, 1, 1, 1, 1], np.int64)
+    sg = np.array([1, -1, 1, 1, 1, 1, 1, 1], np.int64)
+    g = grid.astype(np.int64)
+    si, sm = orc.block_ints(GType.IQ1_S, blk, xq, 256)
+    assert int(si[0]) == int(sum(ls[k] * (g[32 * k:32 * k + 32] @ q8[32 * k:32 * k + 32]) for k in range(8)))
+    assert int(sm[0]) == int(sum(ls[k] * sg[k] * q8[32 * k:32 * k + 32].sum() for k in range(8)))
+
+
 def test_q8_0_weight_known_answers():
     """Q8_0 weights (src/kernels4.cu:421-714, deq8: d * qs[j]): value j of a block is d * (int8) qs[j] in place, and
     against a Q8_0 activation block the integer is sum_j qs[j] y[j] (ggml's vec_dot_q8_0_q8_0), folded as
@@ -574,7 +623,7 @@ def test_q8k_known_answers():
 # ------------------------------------------------------------------ block decoding
 
 ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.IQ4_NL, GType.Q8_0, GType.MXFP4,
-       GType.Q5_0, GType.Q2_K, GType.Q3_K, GType.IQ3_XXS, GType.IQ3_S, GType.IQ2_S]
+       GType.Q5_0, GType.Q2_K, GType.Q3_K, GType.IQ3_XXS, GType.IQ3_S, GType.IQ2_S, GType.IQ1_S]
 
 
 def blocks(t, nb, seed):
