@@ -479,6 +479,45 @@ template <> struct Item<MXFP4> {
     }
     __device__ __forceinline__ float tval(int si, int) const { return e8m0_half(e) * (float) si; }
 };
+// the integer sum of a 32-value activation block (4 values a word)
+__device__ __forceinline__ int ysum32(const uint32_t (&ya)[8]) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s = sdot4(ya[i], 0x01010101u, s);
+    return s;
+}
+// Q5_1 (24 B: d, m, qh u32 @4, qs[16] @8), src/kernels4.cu:449-462: value j = d x + m, x = nibble j | qh bit j << 4
+// (0..31; nibble j the low one of qs[j] for j < 16, the high one of qs[j - 16] above).  The reference's CPU path pairs
+// it with Q8_1 rows, whose d and q are Q8_0's and whose s is fp16(d sum q); here the partner is the Q8_0 row and the
+// min's term takes the exact integer sum q: sumi = sum_32 x q8 (ints' si), the block's activation sum (sm), folded as
+// t = fma(d, sumi, m * sum).  Block L sits at 24 L of the 16-byte aligned 192-byte span: every field is dword-aligned.
+template <> struct Item<Q5_1> {
+    uint4 qs;
+    uint32_t qh, dm;   // qh; d | m << 16
+    __device__ __forceinline__ void load(const uint8_t *b, int L) {
+        qs = load16_a4(b + 24 * L + 8);
+        qh = *(const uint32_t *) (b + 24 * L + 4);
+        dm = *(const uint32_t *) (b + 24 * L);
+    }
+    __device__ __forceinline__ int dot32(const uint32_t (&ya)[8]) const {
+        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s = sdot4((q[i] & 0x0F0F0F0Fu) | (spread4((qh >> (4 * i)) & 15) << 4), ya[i], s);
+            s = sdot4(((q[i] >> 4) & 0x0F0F0F0Fu) | (spread4((qh >> (16 + 4 * i)) & 15) << 4), ya[4 + i], s);
+        }
+        return s;
+    }
+    __device__ __forceinline__ void ints(const uint8_t *y, int, int &si, int &sm) const {
+        const uint32_t *yw = (const uint32_t *) (y + 4);
+        const uint32_t ya[8] = {yw[0], yw[1], yw[2], yw[3], yw[4], yw[5], yw[6], yw[7]};
+        si = dot32(ya); sm = ysum32(ya);
+    }
+    __device__ __forceinline__ float tval(int si, int sm) const {
+        return __builtin_fmaf(h2f(dm & 0xffff), (float) si, h2f(dm >> 16) * (float) sm);
+    }
+};
 // Q5_0 (22 B: d, qh u32, qs[16]) against Q8_0, src/kernels4.cu:464-478: lane L takes the item's block L whole, value
 // j = (nibble j | qh bit j << 4) - 16, nibble j the low one of qs[j] for j < 16, the high one of qs[j - 16] above; as
 // an int8 byte that is the nibble, OR 0xF0 where the qh bit is clear (ggml's vec_dot_q5_0_q8_0 integers:

@@ -26,7 +26,7 @@ int check_launch(const char *what) {
     return HY_OK;
 }
 
-static bool dot_type(int t) { return t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ2_XXS || t == IQ4_NL || t == Q8_0 || t == MXFP4 || t == Q5_0 || t == Q2_K || t == Q3_K || t == IQ3_XXS || t == IQ3_S || t == IQ2_S || t == IQ1_S; }
+static bool dot_type(int t) { return t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ2_XXS || t == IQ4_NL || t == Q8_0 || t == MXFP4 || t == Q5_0 || t == Q5_1 || t == Q2_K || t == Q3_K || t == IQ3_XXS || t == IQ3_S || t == IQ2_S || t == IQ1_S; }
 static bool gemm_type(int t) { return dot_type(t); }
 
 // the expert layer descriptor is usable: types, sizes, pointers, row sizes that the kernels assume

@@ -17,24 +17,26 @@
 namespace hy {
 
 // GGUF type ids (src/gguf.h:13-18)
-enum GT : int { Q5_0 = 6, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, IQ2_XXS = 16, IQ2_XS = 17, IQ3_XXS = 18, IQ1_S = 19, IQ4_NL = 20, IQ3_S = 21, IQ2_S = 22, IQ4_XS = 23, MXFP4 = 39 };
+enum GT : int { Q5_0 = 6, Q5_1 = 7, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, IQ2_XXS = 16, IQ2_XS = 17, IQ3_XXS = 18, IQ1_S = 19, IQ4_NL = 20, IQ3_S = 21, IQ2_S = 22, IQ4_XS = 23, MXFP4 = 39 };
 
 constexpr int Q8K_BYTES = 292;   // float d; int8 qs[256]; int16 bsums[16]
 constexpr int Q8_0_BYTES = 34;   // fp16 d; int8 qs[32]
 
 __host__ __device__ constexpr int block_bytes(int t) {
     return t == Q4_K ? 144 : t == Q5_K ? 176 : t == Q6_K ? 210 : t == IQ4_XS ? 136 : t == IQ2_XS ? 74 : t == IQ2_XXS ? 66
-         : t == IQ4_NL ? 18 : t == Q8_0 ? 34 : t == MXFP4 ? 17 : t == Q5_0 ? 22 : t == Q2_K ? 84 : t == Q3_K ? 110 : t == IQ3_XXS ? 98 : t == IQ3_S ? 110 : t == IQ2_S ? 82 : t == IQ1_S ? 50 : t == Q8_K ? 292 : 0;
+         : t == IQ4_NL ? 18 : t == Q8_0 ? 34 : t == MXFP4 ? 17 : t == Q5_0 ? 22 : t == Q2_K ? 84 : t == Q3_K ? 110 : t == IQ3_XXS ? 98 : t == IQ3_S ? 110 : t == IQ2_S ? 82 : t == IQ1_S ? 50 : t == Q5_1 ? 24 : t == Q8_K ? 292 : 0;
 }
 __host__ __device__ constexpr int block_elems(int t) {
-    return (t == IQ4_NL || t == Q8_0 || t == MXFP4 || t == Q5_0) ? 32
+    return (t == IQ4_NL || t == Q8_0 || t == MXFP4 || t == Q5_0 || t == Q5_1) ? 32
          : (t == Q4_K || t == Q5_K || t == Q6_K || t == IQ4_XS || t == IQ2_XS || t == IQ2_XXS || t == Q2_K || t == Q3_K || t == IQ3_XXS || t == IQ3_S || t == IQ2_S || t == IQ1_S || t == Q8_K) ? 256 : 0;
 }
 // the grid types (IQ2_XS, IQ2_XXS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S): codebook rows and sign masks in LDS (expand_iq2_grid)
 __host__ __device__ constexpr bool iq2_type(int t) {
     return t == IQ2_XS || t == IQ2_XXS || t == IQ2_S || t == IQ3_XXS || t == IQ3_S || t == IQ1_S;
 }
-__host__ __device__ constexpr int vec_dot_type(int t) { return t == IQ4_NL || t == Q8_0 || t == MXFP4 || t == Q5_0 ? Q8_0 : Q8_K; }
+__host__ __device__ constexpr int vec_dot_type(int t) { return t == IQ4_NL || t == Q8_0 || t == MXFP4 || t == Q5_0 || t == Q5_1 ? Q8_0 : Q8_K; }
+// 32-value block types whose fold also takes the activation block's integer sum (Q5_1's min: m * sum q)
+__host__ __device__ constexpr bool ysum_type(int t) { return t == Q5_1; }
 
 // ------------------------------------------------------------------ scalar helpers
 

@@ -149,7 +149,7 @@ __device__ __forceinline__ float item_t(const Item<T> &it, const uint8_t *y, int
         if (valid) {
             const uint4 y0 = *(const uint4 *) yb, y1 = *(const uint4 *) (yb + 16);
             const uint32_t ya[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
-            tv_out[tv_idx + L] = it.tval(it.dot32(ya), 0);
+            tv_out[tv_idx + L] = it.tval(it.dot32(ya), ysum_type(T) ? ysum32(ya) : 0);
         }
         return 0.0f;
     } else {
@@ -620,6 +620,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     case Q8_0: { constexpr int TT = Q8_0; CALL; }                                               \
     case MXFP4: { constexpr int TT = MXFP4; CALL; }                                             \
     case Q5_0: { constexpr int TT = Q5_0; CALL; }                                               \
+    case Q5_1: { constexpr int TT = Q5_1; CALL; }                                               \
     case Q2_K: { constexpr int TT = Q2_K; CALL; }                                               \
     case Q3_K: { constexpr int TT = Q3_K; CALL; }                                               \
     case IQ3_XXS: { constexpr int TT = IQ3_XXS; CALL; }                                         \
@@ -658,7 +659,7 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
     if (m.gate_bytes >= ((size_t) 1 << 32)) { set_error("hy_moe_route_gate_up: an expert matrix of %zu bytes (4 GiB or more)", m.gate_bytes); return HY_EBAD_SHAPE; }
     if (hq) {   // the Q8_0 hidden as well: 32-row blocks (rw 4), items and fold inputs within the HQ instantiation's limits
         if (vec_dot_type(m.tg) != Q8_0 || vec_dot_type(m.td) != Q8_0 || 4 * 2 * nb > 2 * DEC_GU_TV) {
-            set_error("hy_moe_route_gate_up_q8: needs IQ4_NL, Q8_0, MXFP4 or Q5_0 gate/up and down weights and n <= 4096 (types %d/%d, n %d)", m.tg, m.td, m.n);
+            set_error("hy_moe_route_gate_up_q8: needs IQ4_NL, Q8_0, MXFP4, Q5_0 or Q5_1 gate/up and down weights and n <= 4096 (types %d/%d, n %d)", m.tg, m.td, m.n);
             return HY_EUNSUPPORTED_TYPE;
         }
         if (nt == 0) return HY_OK;
@@ -667,6 +668,7 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
 #define HY_RGUQ(TQ, VV) hipLaunchKernelGGL((k_route_gate_up<TQ, VV, DEC_PIPE_NP, true, true>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, 4, q8, r8, hq)
 #define HY_RGUQ_V(TQ) if (V <= 1) HY_RGUQ(TQ, 1); else if (V <= 2) HY_RGUQ(TQ, 2); else if (V <= 4) HY_RGUQ(TQ, 4); else if (V <= 8) HY_RGUQ(TQ, 8); else HY_RGUQ(TQ, 16);
         if (m.tg == IQ4_NL) { HY_RGUQ_V(IQ4_NL) } else if (m.tg == MXFP4) { HY_RGUQ_V(MXFP4) } else if (m.tg == Q5_0) { HY_RGUQ_V(Q5_0) }
+        else if (m.tg == Q5_1) { HY_RGUQ_V(Q5_1) }
         else { HY_RGUQ_V(Q8_0) }
 #undef HY_RGUQ_V
 #undef HY_RGUQ

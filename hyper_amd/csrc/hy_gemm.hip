@@ -430,6 +430,36 @@ template <> struct Raw<MXFP4> {
     __device__ __forceinline__ float cfold(int c, int d) const { return e8m0_half((ee[c >> 2] >> (8 * (c & 3))) & 255) * (float) d; }
     __device__ __forceinline__ float fold(int si, int) const { return (float) si; }
 };
+// Q5_1 (8 blocks of 24 B per 256 values, Q8_0 activations): chunk c = block c, lane values as IQ4_NL's with the fifth
+// bits in qh byte q of the block (x = nibble | bit << 4, 0..31); every field dword-aligned (24-byte blocks in a 192-byte
+// span).  The min's term needs each token's block sum q: chunk_fold takes it from one more MFMA against ones
+// (ysum), and the fold is fma(d_c, D, m_c * S) (the integers of Item<Q5_1>).
+template <> struct Raw<Q5_1> {
+    static constexpr bool mins = false, g16 = false, per_chunk = true;
+    uint2 qv[8]; uint32_t hb[2], dm[8];
+    __device__ __forceinline__ void load(const uint8_t *blk, int q) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            qv[c] = *(const uint2 *) (blk + 24 * c + 8 + 8 * (q & 1));
+            dm[c] = *(const uint32_t *) (blk + 24 * c);
+        }
+        hb[0] = hb[1] = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) hb[c >> 2] |= (uint32_t) blk[24 * c + 4 + q] << (8 * (c & 3));
+    }
+    __device__ __forceinline__ void chunk(int c, int q, const uint2 *, uint32_t &b0, uint32_t &b1, int &s0, int &s1, int &mn) const {
+        const int s = 4 * (q >> 1);
+        const uint32_t h = hb[c >> 2] >> (8 * (c & 3));
+        b0 = ((qv[c].x >> s) & 0x0F0F0F0Fu) | (spread4(h & 15) << 4);
+        b1 = ((qv[c].y >> s) & 0x0F0F0F0Fu) | (spread4((h >> 4) & 15) << 4);
+        s0 = 1; s1 = 0; mn = 0;
+    }
+    __device__ __forceinline__ float cfold2(int c, int d, int ys) const {
+        return __builtin_fmaf(h2f(dm[c] & 0xffff), (float) d, h2f(dm[c] >> 16) * (float) ys);
+    }
+    __device__ __forceinline__ float cfold(int c, int d) const { return cfold2(c, d, 0); }
+    __device__ __forceinline__ float fold(int si, int) const { return (float) si; }
+};
 // Q5_0 (8 blocks of 22 B per 256 values, Q8_0 activations): chunk c = block c, lane values as IQ4_NL's (nibbles
 // (q >> 1) of qs[8 (q & 1) ..]) with their fifth bits in qh byte q (bits 8 q .. 8 q + 7), each byte nibble | 0xF0
 // where the bit is clear (x - 16 as int8).  Block c's qs (22 c + 6) and qh (22 c + 2) are 2 mod 4 for even c, read by
@@ -1030,7 +1060,7 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
     }
 }
 
-// IQ4_NL / Q8_0 / MXFP4 / Q5_0: one chunk's MFMA per tile folded straight into the fp32 accumulators (Yc: 8 block scales per token)
+// IQ4_NL / Q8_0 / MXFP4 / Q5_0 / Q5_1: one chunk's MFMA per tile folded straight into the fp32 accumulators (Yc: 8 block scales per token)
 template <int T>
 __device__ __forceinline__ void chunk_fold(const Raw<T> &w, int c, int q, const int8_t *As, const float *Yc, int rr, int ntile,
                                            float (&acc)[GM_TILES][4]) {
@@ -1043,12 +1073,18 @@ __device__ __forceinline__ void chunk_fold(const Raw<T> &w, int c, int q, const 
         if (tile >= ntile) break;
         const long a = *(const long *) (As + (tile * 16 + rr) * GM_LD + 32 * c + 8 * q);
         const v4i d0 = mfma16(a, mk_long(b0, b1), z);
+        if constexpr (ysum_type(T)) {   // each token's block sum: the same A against ones
+            const v4i d1 = mfma16(a, mk_long(0x01010101u, 0x01010101u), z);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[tile][v] = __builtin_fmaf(Yc[(tile * 16 + 4 * q + v) * 8 + c], w.cfold(c, d0[v]), acc[tile][v]);
+            for (int v = 0; v < 4; ++v) acc[tile][v] = __builtin_fmaf(Yc[(tile * 16 + 4 * q + v) * 8 + c], w.cfold2(c, d0[v], d1[v]), acc[tile][v]);
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[tile][v] = __builtin_fmaf(Yc[(tile * 16 + 4 * q + v) * 8 + c], w.cfold(c, d0[v]), acc[tile][v]);
+        }
     }
 }
 
-// IQ4_NL, Q8_0, MXFP4 and Q5_0 weights (Q8_0 activations, whose 2-byte aligned blocks the LDS DMA above cannot stage): register-staged
+// IQ4_NL, Q8_0, MXFP4, Q5_0 and Q5_1 weights (Q8_0 activations, whose 2-byte aligned blocks the LDS DMA above cannot stage): register-staged
 // stream, one step ahead.  A block walks the work items it, it + gridDim.y, ...; the (item, block) steps form one stream in which the
 // next step's weight and activation bytes are loaded while the current step computes, across item boundaries.
 template <int T, bool GU>
@@ -1056,7 +1092,7 @@ __global__ __launch_bounds__(256) void k_gemm_nl(hy_moe_dev m, const uint8_t *__
                                               const int *__restrict__ order_n, const int *__restrict__ egrp, const float *__restrict__ wts,
                                               float *__restrict__ out) {
     __shared__ __align__(16) int8_t As[2][GM_TOK * GM_LD];
-    constexpr bool NL = vec_dot_type(T) == Q8_0;     // Q8_0 activations, per-block fold (IQ4_NL, Q8_0, MXFP4, Q5_0)
+    constexpr bool NL = vec_dot_type(T) == Q8_0;     // Q8_0 activations, per-block fold (IQ4_NL, Q8_0, MXFP4, Q5_0, Q5_1)
     __shared__ float Yd[2][GM_TOK * (NL ? 8 : 1)];
     __shared__ int s_scan[1024 + 8];
     __shared__ float s_up[GU ? 32 * GM_TOK : 1];
@@ -1274,6 +1310,7 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
         if (m.tg == IQ4_NL) hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
         else if (m.tg == MXFP4) hipLaunchKernelGGL((k_gemm_nl<MXFP4, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
         else if (m.tg == Q5_0) hipLaunchKernelGGL((k_gemm_nl<Q5_0, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
+        else if (m.tg == Q5_1) hipLaunchKernelGGL((k_gemm_nl<Q5_1, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
         else hipLaunchKernelGGL((k_gemm_nl<Q8_0, true>), grid, dim3(256), 0, s, m, (const uint8_t *) xq, k, order, order_n, egrp, nullptr, h);
         return check_launch("hy_moe_gemm_gate_up");
     }
@@ -1306,6 +1343,7 @@ int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int
         if (m.td == IQ4_NL) hipLaunchKernelGGL((k_gemm_nl<IQ4_NL, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
         else if (m.td == MXFP4) hipLaunchKernelGGL((k_gemm_nl<MXFP4, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
         else if (m.td == Q5_0) hipLaunchKernelGGL((k_gemm_nl<Q5_0, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
+        else if (m.td == Q5_1) hipLaunchKernelGGL((k_gemm_nl<Q5_1, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
         else hipLaunchKernelGGL((k_gemm_nl<Q8_0, false>), grid, dim3(256), 0, s, m, (const uint8_t *) hq, 1, order, order_n, egrp, wts, y);
         return check_launch("hy_moe_gemm_down");
     }

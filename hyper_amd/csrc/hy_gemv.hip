@@ -162,6 +162,7 @@ static int launch_gemv_t(const hy_moe_dev &m, const float *src, int ss, const in
     case Q8_0: { constexpr int TT = Q8_0; CALL; }                                        \
     case MXFP4: { constexpr int TT = MXFP4; CALL; }                                      \
     case Q5_0: { constexpr int TT = Q5_0; CALL; }                                        \
+    case Q5_1: { constexpr int TT = Q5_1; CALL; }                                        \
     case Q2_K: { constexpr int TT = Q2_K; CALL; }                                        \
     case Q3_K: { constexpr int TT = Q3_K; CALL; }                                        \
     case IQ3_XXS: { constexpr int TT = IQ3_XXS; CALL; }                                  \
@@ -469,6 +470,12 @@ __global__ void k_dequant(int type, const uint8_t *__restrict__ row, int n, floa
         const int q = (b[16 + 32 * (e >> 7) + (e & 31)] >> (2 * ((e >> 5) & 3))) & 3;
         const float dl = h2f(ld_u16(b + 80)) * (float) (sc & 15), ml = h2f(ld_u16(b + 82)) * (float) (sc >> 4);
         v = dl * (float) q - ml;
+    } else if (type == Q5_1) {   // src/kernels4.cu:449-462
+        const uint8_t *b = row + (size_t) (i >> 5) * 24;
+        const int e = i & 31;
+        const uint32_t qh = (uint32_t) ld_u16(b + 4) | ((uint32_t) ld_u16(b + 6) << 16);
+        const int x = ((b[8 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF) | (((qh >> e) & 1) << 4);
+        v = (float) x * h2f(ld_u16(b)) + h2f(ld_u16(b + 2));
     } else if (type == Q5_0) {   // src/kernels4.cu:464-478
         const uint8_t *b = row + (size_t) (i >> 5) * 22;
         const int e = i & 31;
@@ -518,7 +525,7 @@ __global__ __launch_bounds__(256) void k_block_ints(const uint8_t *__restrict__ 
     if constexpr (block_elems(T) == 32) {
         it.ints(y0 + (8 * gi + L) * Q8_0_LDS, L, si, sm);
         sumi[row * nb + 8 * gi + L] = si;
-        summ[row * nb + 8 * gi + L] = 0;
+        summ[row * nb + 8 * gi + L] = sm;   // (Q5_1: the activation block's sum; the others 0)
     } else {
         it.ints(xq + gi * Q8K_BYTES, L, si, sm);
         si = group8_isum(si);

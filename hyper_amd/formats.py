@@ -15,6 +15,7 @@ Block sizes follow src/gguf.cpp:43-82; layouts follow the reference's deq8<T> (s
   IQ2_S 82 B: d f16, qs[32] @2, signs[32] @34, qh[8] (index bits 8-9) @66, scales[8] (nibbles per 16) @74
   IQ3_S 110 B: d f16, qs[64] @2, qh[8] (9th index bits) @66, signs[32] @74, scales[4] (nibbles) @106
   Q3_K 110 B: hmask[32] @0, qs[64] (2-bit fields) @32, scales[12] (16 signed 6-bit scales) @96, d f16 @108
+  Q5_1 24 B per 32: d f16, m f16, qh u32 @4, qs[16] @8; value d (nibble | bit << 4) + m
   Q5_0 22 B per 32: d f16, qh u32 (bit j: value j's fifth bit) @2, qs[16] @6; value d ((nibble | bit << 4) - 16)
 Synthetic blocks (the workloads' generators): uniformly random quant bytes (which gives uniform nibbles,
 6-bit scales/mins, grid indices and sign bits), fp16 scale fields drawn uniformly from a stated range, E8M0
@@ -31,6 +32,7 @@ import torch
 class GType(IntEnum):
     """GGUF type ids (src/gguf.h:13-18)."""
     Q5_0 = 6
+    Q5_1 = 7
     Q8_0 = 8
     Q2_K = 10
     Q3_K = 11
@@ -50,8 +52,8 @@ class GType(IntEnum):
 
 
 _BYTES = {GType.Q8_0: 34, GType.Q4_K: 144, GType.Q5_K: 176, GType.Q6_K: 210, GType.Q8_K: 292,
-          GType.IQ2_XXS: 66, GType.IQ2_XS: 74, GType.IQ4_NL: 18, GType.IQ4_XS: 136, GType.MXFP4: 17, GType.Q5_0: 22, GType.Q2_K: 84, GType.Q3_K: 110, GType.IQ3_XXS: 98, GType.IQ3_S: 110, GType.IQ2_S: 82, GType.IQ1_S: 50}
-_ELEMS = {GType.Q8_0: 32, GType.IQ4_NL: 32, GType.MXFP4: 32, GType.Q5_0: 32}
+          GType.IQ2_XXS: 66, GType.IQ2_XS: 74, GType.IQ4_NL: 18, GType.IQ4_XS: 136, GType.MXFP4: 17, GType.Q5_0: 22, GType.Q2_K: 84, GType.Q3_K: 110, GType.IQ3_XXS: 98, GType.IQ3_S: 110, GType.IQ2_S: 82, GType.IQ1_S: 50, GType.Q5_1: 24}
+_ELEMS = {GType.Q8_0: 32, GType.IQ4_NL: 32, GType.MXFP4: 32, GType.Q5_0: 32, GType.Q5_1: 32}
 
 
 def block_bytes(t) -> int:
@@ -63,8 +65,9 @@ def block_elems(t) -> int:
 
 
 def vec_dot_type(t) -> GType:
-    """Activation partner type (ggml vec_dot_type; src/cpu_moe.cpp:711-715)."""
-    return GType.Q8_0 if GType(t) in (GType.IQ4_NL, GType.Q8_0, GType.MXFP4, GType.Q5_0) else GType.Q8_K
+    """Activation partner type (ggml vec_dot_type; src/cpu_moe.cpp:711-715).  Q5_1: Q8_0 (the reference's Q8_1 has the
+    same d and q; its fp16 s = d sum q is replaced by the exact integer sum)."""
+    return GType.Q8_0 if GType(t) in (GType.IQ4_NL, GType.Q8_0, GType.MXFP4, GType.Q5_0, GType.Q5_1) else GType.Q8_K
 
 
 def row_bytes(t, n: int) -> int:
@@ -77,7 +80,7 @@ def q8_row_bytes(vt, n: int) -> int:
 
 # fp16 scale fields per type: byte offsets inside the block
 _F16_FIELDS = {GType.Q4_K: (0, 2), GType.Q5_K: (0, 2), GType.Q6_K: (208,), GType.IQ4_NL: (0,), GType.Q8_0: (0,),
-               GType.IQ4_XS: (0,), GType.IQ2_XS: (0,), GType.IQ2_XXS: (0,), GType.MXFP4: (), GType.Q5_0: (0,), GType.Q2_K: (80, 82), GType.Q3_K: (108,), GType.IQ3_XXS: (0,), GType.IQ3_S: (0,), GType.IQ2_S: (0,), GType.IQ1_S: (0,)}
+               GType.IQ4_XS: (0,), GType.IQ2_XS: (0,), GType.IQ2_XXS: (0,), GType.MXFP4: (), GType.Q5_0: (0,), GType.Q2_K: (80, 82), GType.Q3_K: (108,), GType.IQ3_XXS: (0,), GType.IQ3_S: (0,), GType.IQ2_S: (0,), GType.IQ1_S: (0,), GType.Q5_1: (0, 2)}
 # E8M0 exponent bytes per type
 _E8M0_FIELDS = {GType.MXFP4: (0,)}
 

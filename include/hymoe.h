@@ -9,7 +9,7 @@
  *   - every device pointer is caller-owned (the reference's callers own theirs as well); no entry point
  *     except hy_upload_experts allocates, and all are stream-ordered and free of host synchronisation;
  *   - activations reach the expert matrices as Q8 blocks (block_q8_K, 292 B per 256 values, or block_q8_0,
- *     34 B per 32 values for IQ4_NL, Q8_0, MXFP4 and Q5_0 weights), the partner types of the reference's CPU path
+ *     34 B per 32 values for IQ4_NL, Q8_0, MXFP4, Q5_0 and Q5_1 weights), the partner types of the reference's CPU path
  *     (src/cpu_moe.cpp:711-715), and every block dot product is an exact integer.
  *
  * Results are bit-identical to the CPU oracle of this repository (oracle/), which restates the reference's
@@ -35,9 +35,9 @@ enum {
 };
 
 /* GGUF type ids used by the path (src/gguf.h:13-18); expert weights: Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ1_S, IQ2_XXS, IQ2_XS,
-   IQ2_S, IQ3_XXS, IQ3_S, IQ4_NL, IQ4_XS, Q8_0, MXFP4 and Q5_0 (of src/kernels4.cu:1951-1971's list); Q8_K and Q8_0 as activation rows */
+   IQ2_S, IQ3_XXS, IQ3_S, IQ4_NL, IQ4_XS, Q8_0, MXFP4, Q5_0 and Q5_1 (every type of src/kernels4.cu:1951-1971's list); Q8_K and Q8_0 as activation rows */
 enum {
-    HY_Q5_0 = 6, HY_Q8_0 = 8, HY_Q2_K = 10, HY_Q3_K = 11, HY_Q4_K = 12, HY_Q5_K = 13, HY_Q6_K = 14, HY_Q8_K = 15,
+    HY_Q5_0 = 6, HY_Q5_1 = 7, HY_Q8_0 = 8, HY_Q2_K = 10, HY_Q3_K = 11, HY_Q4_K = 12, HY_Q5_K = 13, HY_Q6_K = 14, HY_Q8_K = 15,
     HY_IQ2_XXS = 16, HY_IQ2_XS = 17, HY_IQ3_XXS = 18, HY_IQ1_S = 19, HY_IQ4_NL = 20, HY_IQ3_S = 21, HY_IQ2_S = 22, HY_IQ4_XS = 23, HY_MXFP4 = 39
 };
 

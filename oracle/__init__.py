@@ -13,11 +13,11 @@ import numpy as np
 _DIR = Path(__file__).resolve().parent
 LIB_PATH = _DIR / "liboracle_moe.so"
 
-(Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS,
- MXFP4) = (6, 8, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 39)
+(Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS,
+ MXFP4) = (6, 7, 8, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 39)
 BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292, IQ2_XXS: 66, IQ2_XS: 74, IQ4_NL: 18, IQ4_XS: 136,
-               MXFP4: 17, Q5_0: 22, Q2_K: 84, Q3_K: 110, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82, IQ1_S: 50}
-BLOCK_ELEMS = {Q8_0: 32, IQ4_NL: 32, MXFP4: 32, Q5_0: 32}
+               MXFP4: 17, Q5_0: 22, Q2_K: 84, Q3_K: 110, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82, IQ1_S: 50, Q5_1: 24}
+BLOCK_ELEMS = {Q8_0: 32, IQ4_NL: 32, MXFP4: 32, Q5_0: 32, Q5_1: 32}
 
 
 def block_elems(t):
@@ -25,7 +25,7 @@ def block_elems(t):
 
 
 def vec_dot_type(t):
-    return Q8_0 if int(t) in (IQ4_NL, Q8_0, MXFP4, Q5_0) else Q8_K
+    return Q8_0 if int(t) in (IQ4_NL, Q8_0, MXFP4, Q5_0, Q5_1) else Q8_K
 
 
 def row_bytes(t, n):

@@ -34,22 +34,24 @@ size_t or_block_bytes(int type) {
     case OR_IQ3_S: return 110;
     case OR_IQ2_S: return 82;
     case OR_IQ1_S: return 50;
+    case OR_Q5_1: return 24;
     default: return 0;
     }
 }
 int or_block_elems(int type) {
     switch (type) {
-    case OR_Q8_0: case OR_IQ4_NL: case OR_MXFP4: case OR_Q5_0: return 32;
+    case OR_Q8_0: case OR_IQ4_NL: case OR_MXFP4: case OR_Q5_0: case OR_Q5_1: return 32;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_Q8_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K:
     case OR_Q3_K: case OR_IQ3_XXS: case OR_IQ3_S: case OR_IQ2_S: case OR_IQ1_S: return 256;
     default: return 0;
     }
 }
 /* ggml's vec_dot_type: Q8_0 for IQ4_NL, Q8_0, MXFP4 and Q5_0 weights, Q8_K for the K-quants and the 256-block IQ types
-   (the activation quantizer is chosen per weight type: src/cpu_moe.cpp:711-715) */
+   (the activation quantizer is chosen per weight type: src/cpu_moe.cpp:711-715).  Q5_1's partner there is Q8_1, whose d
+   and q are Q8_0's and whose s is fp16(d sum q); here Q5_1 takes the Q8_0 row and the exact integer sum q instead of s */
 int or_vec_dot_type(int type) {
     switch (type) {
-    case OR_IQ4_NL: case OR_Q8_0: case OR_MXFP4: case OR_Q5_0: return OR_Q8_0;
+    case OR_IQ4_NL: case OR_Q8_0: case OR_MXFP4: case OR_Q5_0: case OR_Q5_1: return OR_Q8_0;
     case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ4_XS: case OR_Q2_K: case OR_Q3_K: case OR_IQ3_XXS:
     case OR_IQ3_S: case OR_IQ2_S: case OR_IQ1_S: return OR_Q8_K;
     default: return -1;
@@ -301,6 +303,12 @@ static inline int q3k_sc(const uint8_t *b, int is) {
     const int grp = is >> 2, k = is & 3;
     return (((b[96 + (grp & 1) * 4 + k] >> (4 * (grp >> 1))) & 0xF) | (((b[104 + k] >> (2 * grp)) & 3) << 4)) - 32;
 }
+/* element e (0..31) of a 24-byte Q5_1 block (d, m, qh u32 @4, qs[16] @8): nibble | qh bit e << 4, 0..31, the nibble
+   the low one of qs[e] for e < 16, else the high one of qs[e - 16] (src/kernels4.cu:449-462); value x d + m */
+static inline int q5_1_q(const uint8_t *b, int e) {
+    const uint32_t qh = (uint32_t) b[4] | ((uint32_t) b[5] << 8) | ((uint32_t) b[6] << 16) | ((uint32_t) b[7] << 24);
+    return ((b[8 + (e & 15)] >> (e >= 16 ? 4 : 0)) & 0xF) | (((qh >> e) & 1) << 4);
+}
 /* element e (0..31) of a 22-byte Q5_0 block (d, qh u32, qs[16]): (nibble | qh bit e << 4) - 16, the nibble the low
    one of qs[e] for e < 16, else the high one of qs[e - 16] (src/kernels4.cu:464-478) */
 static inline int q5_0_q(const uint8_t *b, int e) {
@@ -448,6 +456,9 @@ int or_dequant_row(int type, const uint8_t *row, int n, float *out) {
         case OR_Q5_0:
             for (int e = 0; e < 32; ++e) o[e] = (float) q5_0_q(b, e) * h2f(b);
             break;
+        case OR_Q5_1:
+            for (int e = 0; e < 32; ++e) o[e] = (float) q5_1_q(b, e) * h2f(b) + h2f(b + 2);
+            break;
         case OR_Q3_K:
             for (int e = 0; e < 256; ++e) o[e] = (h2f(b + 108) * (float) q3k_sc(b, e >> 4)) * (float) q3k_q(b, e);
             break;
@@ -523,6 +534,9 @@ static void block_ints_scalar(int type, const uint8_t *b, const uint8_t *y, int3
         break;
     case OR_Q5_0:      /* ggml's vec_dot_q5_0_q8_0 integer part: sum_32 (x - 16) q8 */
         for (int l = 0; l < 32; ++l) si += q5_0_q(b, l) * q8[l];
+        break;
+    case OR_Q5_1:      /* ggml's vec_dot_q5_1_q8_1 integer part sum_32 x q8, and the activation sum sum_32 q8 */
+        for (int l = 0; l < 32; ++l) { si += q5_1_q(b, l) * q8[l]; sm += q8[l]; }
         break;
     case OR_IQ1_S: {   /* the reference's IQ1_S x Q8_K dot (src/iq1s_dot.h:26-64): sumi = sum_ib ls sum_32 grid y,
                           summ = sum_ib ls (-1 if qh's top bit) (sum_32 y, the bsum pair) */
@@ -659,7 +673,8 @@ static void block_ints(int type, const uint8_t *b, const uint8_t *y, int32_t *su
 static int dot_ok(int type) {
     return type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_IQ4_XS || type == OR_IQ2_XS || type == OR_IQ4_NL ||
            type == OR_Q8_0 || type == OR_IQ2_XXS || type == OR_MXFP4 || type == OR_Q5_0 || type == OR_Q2_K || type == OR_Q3_K ||
-           type == OR_IQ3_XXS || type == OR_IQ3_S || type == OR_IQ2_S || type == OR_IQ1_S;
+           type == OR_IQ3_XXS || type == OR_IQ3_S || type == OR_IQ2_S || type == OR_IQ1_S ||
+           type == OR_Q5_1;
 }
 int or_block_ints(int type, const uint8_t *row, const void *xq, int n, int32_t *sumi, int32_t *summ) {
     if (!dot_ok(type) || n % or_block_elems(type)) return -1;
@@ -694,6 +709,7 @@ static float row_dot(int type, const uint8_t *row, const uint8_t *xq, int n) {
         case OR_IQ3_XXS: t = (h2f(b) * 0.25f) * (float) si; break;
         case OR_IQ3_S: t = h2f(b) * (float) si; break;
         case OR_IQ1_S: t = (h2f(b) * 0.125f) * (float) (8 * si + sm); break;   /* exact: |8 si + sm| < 2^24 */
+        case OR_Q5_1: t = fmaf(h2f(b), (float) si, h2f(b + 2) * (float) sm); break;
         case OR_Q2_K: t = fmaf(h2f(b + 80), (float) si, -(h2f(b + 82) * (float) sm)); break;
         case OR_IQ2_XS: case OR_IQ2_XXS: case OR_IQ2_S: t = (h2f(b) * 0.125f) * (float) si; break;
         case OR_MXFP4: t = e8m0_half(b[0]) * (float) si; break;

@@ -12,7 +12,7 @@
  *
  *  - activations are quantized to the weight type's ggml vec_dot partner:
  *    Q8_K for the K-quants / IQ4_XS / IQ2_XS (src/cpu_moe.cpp:35-78),
- *    Q8_0 for IQ4_NL, Q8_0, MXFP4 and Q5_0 (ggml's x86 quantize_row_q8_0, see or_quantize_q8_0);
+ *    Q8_0 for IQ4_NL, Q8_0, MXFP4, Q5_0 and Q5_1 (ggml's x86 quantize_row_q8_0, see or_quantize_q8_0);
  *  - every weight block against its activation block gives exact integers
  *    (sumi, and summ for the types with mins);
  *  - a row dot product folds block b's integers with one fixed fp32 formula
@@ -40,7 +40,7 @@ extern "C" {
 
 /* GGUF type ids (src/gguf.h:13-18) */
 enum {
-    OR_Q5_0 = 6, OR_Q8_0 = 8, OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14, OR_Q8_K = 15,
+    OR_Q5_0 = 6, OR_Q5_1 = 7, OR_Q8_0 = 8, OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14, OR_Q8_K = 15,
     OR_IQ2_XXS = 16, OR_IQ2_XS = 17, OR_IQ3_XXS = 18, OR_IQ1_S = 19, OR_IQ4_NL = 20, OR_IQ3_S = 21, OR_IQ2_S = 22, OR_IQ4_XS = 23, OR_MXFP4 = 39
 };
 

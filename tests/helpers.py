@@ -6,11 +6,11 @@ import oracle as orc
 from hyper_amd.formats import GType, activations, random_layer, zipf_logit_bias
 
 TYPES_256 = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.Q2_K, GType.Q3_K, GType.IQ3_XXS, GType.IQ3_S, GType.IQ2_S, GType.IQ1_S]
-ALL_TYPES = TYPES_256 + [GType.IQ4_NL, GType.Q8_0, GType.MXFP4, GType.Q5_0]
+ALL_TYPES = TYPES_256 + [GType.IQ4_NL, GType.Q8_0, GType.MXFP4, GType.Q5_0, GType.Q5_1]
 D_RANGE = {GType.Q4_K: (1e-4, 4e-3), GType.Q5_K: (1e-4, 4e-3), GType.Q6_K: (1e-4, 4e-3),
            GType.IQ4_XS: (1e-3, 1e-2), GType.IQ2_XS: (1e-3, 1e-2), GType.IQ2_XXS: (1e-3, 1e-2), GType.IQ4_NL: (1e-3, 1e-2),
            GType.Q8_0: (1e-4, 1e-3), GType.MXFP4: (1e-2, 1e-1),
-           GType.Q5_0: (1e-3, 1e-2), GType.Q2_K: (1e-3, 1e-2), GType.Q3_K: (1e-4, 1e-3), GType.IQ3_XXS: (1e-3, 1e-2), GType.IQ3_S: (1e-3, 1e-2), GType.IQ2_S: (1e-3, 1e-2), GType.IQ1_S: (1e-2, 1e-1)}   # MXFP4: power-of-two scales, codebook values up to 12
+           GType.Q5_0: (1e-3, 1e-2), GType.Q2_K: (1e-3, 1e-2), GType.Q3_K: (1e-4, 1e-3), GType.IQ3_XXS: (1e-3, 1e-2), GType.IQ3_S: (1e-3, 1e-2), GType.IQ2_S: (1e-3, 1e-2), GType.IQ1_S: (1e-2, 1e-1), GType.Q5_1: (1e-3, 1e-2)}   # MXFP4: power-of-two scales, codebook values up to 12
 
 
 def gen(seed: int) -> torch.Generator:

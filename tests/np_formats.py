@@ -190,6 +190,16 @@ def iq1s(b, grid_rows):
     return dict(q=q, sc=ls, m=ls * sgn, gsize=32, d=f16(b[:, 0:2]), delta=np.where(qh & 0x8000, -0.125, 0.125))
 
 
+def q5_1w(b):
+    """Q5_1 weights: d f16 @0, m f16 @2, qh little-endian u32 @4, qs[16] @8; value j = d (nibble j + 16 bit j) + m."""
+    b = b.reshape(-1, 24)
+    qh = np.ascontiguousarray(b[:, 4:8]).view(np.uint32).astype(np.int64).reshape(-1)
+    qs = b[:, 8:24].astype(np.int64)
+    x = np.concatenate([qs & 0xF, qs >> 4], axis=1) + 16 * ((qh[:, None] >> np.arange(32)) & 1)
+    return dict(q=x, sc=np.ones((b.shape[0], 1), np.int64), m=np.ones((b.shape[0], 1), np.int64), gsize=32,
+                d=f16(b[:, 0:2]), dmin=f16(b[:, 2:4]))
+
+
 def q5_0w(b):
     """Q5_0 weights: d f16 @0, qh little-endian u32 @2, qs[16] @6; value j = (nibble j + 16 * bit j of qh) - 16, the
     nibbles in qs order, low halves first (values 0..15), then high halves (16..31)."""
@@ -248,6 +258,7 @@ def decode(t, b, grid_rows=None, ksigns=None):
     if t == 8: return q8_0w(b)
     if t == 39: return mxfp4(b)
     if t == 6: return q5_0w(b)
+    if t == 7: return q5_1w(b)
     if t == 10: return q2k(b)
     if t == 11: return q3k(b)
     if t == 18: return iq3xxs(b, grid_rows, ksigns)
@@ -274,6 +285,8 @@ def dequant(t, b, grid_rows=None, ksigns=None):
         return ((d * sc) * q.astype(np.float32)).astype(np.float32)
     if t == 23:
         return ((d * sc) * q.astype(np.float32)).astype(np.float32)
+    if t == 7:
+        return (q.astype(np.float32) * d + f["dmin"][:, None]).astype(np.float32)
     if t in (20, 39, 6):
         return (q.astype(np.float32) * d).astype(np.float32)
     if t == 8:
@@ -295,7 +308,7 @@ def block_ints(t, b, xq, grid_rows=None, ksigns=None):
     """Brute-force integers per block: sumi = sum over groups of scale * sum(q * y), summ = sum_j m_j * sum(y_j)."""
     f = decode(t, b, grid_rows, ksigns)
     q, gs = f["q"], f["gsize"]
-    if int(t) in (20, 8, 39, 6):
+    if int(t) in (20, 8, 39, 6, 7):
         y = q8_0(xq)["qs"]
     else:
         y = q8k(xq)["qs"]

@@ -76,6 +76,8 @@ ROUTE_GU_CASES = [
     (GType.IQ2_S, GType.IQ3_S, 24, 2048, 768, 8, 3, False),
     (GType.IQ1_S, GType.IQ1_S, 16, 7168, 2048, 6, 2, True),
     (GType.IQ1_S, GType.IQ2_XXS, 24, 2048, 768, 8, 3, False),
+    (GType.Q5_1, GType.Q5_1, 32, 2048, 768, 8, 2, True),
+    (GType.Q5_1, GType.Q4_K, 24, 1024, 512, 6, 3, False),
 ]
 
 

@@ -163,6 +163,8 @@ DECODE_CASES = [
     (GType.IQ2_S, GType.Q4_K, 2048, 768, 8, 3),
     (GType.IQ1_S, GType.IQ1_S, 7168, 2048, 6, 2),
     (GType.IQ1_S, GType.Q2_K, 2048, 768, 8, 3),
+    (GType.Q5_1, GType.Q5_1, 2048, 768, 8, 2),
+    (GType.Q5_1, GType.Q6_K, 4096, 1536, 4, 3),
 ]
 
 
@@ -246,6 +248,8 @@ GEMM_CASES = [
     (GType.IQ2_S, GType.Q6_K, 2048, 768, 8, 60),
     (GType.IQ1_S, GType.IQ1_S, 7168, 2048, 6, 8),
     (GType.IQ1_S, GType.Q4_K, 2048, 768, 8, 60),
+    (GType.Q5_1, GType.Q5_1, 2048, 768, 8, 40),
+    (GType.Q4_K, GType.Q5_1, 1024, 512, 4, 30),
     (GType.Q4_K, GType.Q6_K, 2048, 768, 1, 100),    # k = 1: the pair is the token (reciprocal 2^32)
     (GType.Q4_K, GType.Q6_K, 1024, 512, 3, 90),     # odd k: the pair-to-token multiply-high
     (GType.Q4_K, GType.Q6_K, 1024, 256, 16, 12),    # k = E: every expert active, every token in each

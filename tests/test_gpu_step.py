@@ -50,6 +50,7 @@ def decode_c(m, W_r, x, k, shared=None, out=None, residual=False, bias=None, ws=
     (GType.IQ3_S, GType.IQ3_S, 64, 2048, 768, 8, 2, True, False, True),
     (GType.IQ2_S, GType.IQ2_S, 48, 1024, 512, 6, 3, True, True, False),
     (GType.IQ1_S, GType.IQ1_S, 48, 2048, 512, 6, 2, True, False, True),
+    (GType.Q5_1, GType.Q5_1, 40, 1024, 512, 8, 3, True, True, False),      # Q5_1: the Q8_0 hand-over with the sum term
     (GType.IQ2_XS, GType.IQ2_XS, 64, 1024, 512, 6, 2, True, True, False),
     (GType.Q5_K, GType.Q6_K, 48, 512, 512, 4, 8, True, False, True),
     (GType.IQ4_XS, GType.IQ4_XS, 32, 512, 256, 4, 12, True, True, False),   # more than 8 rows: batched router

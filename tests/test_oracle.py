@@ -602,6 +602,38 @@ def test_q3k_known_answer_positions():
     assert not sm.any()
 
 
+def test_q5_1_known_answers():
+    """Q5_1 (src/kernels4.cu:449-462): value j = x d + m with x = nibble j | bit j of qh << 4 (0..31).  Blocks built value
+    by value; against a Q8_0 activation block the integers are sum x y and sum y (the min's partner: the Q8_1 row's d
+    and q are Q8_0's, and sum y stands for its s / d), folded as x_d * fma(d, sumi, m * sum y)."""
+    x = np.array([[(9 * j + 5 * b) % 32 for j in range(32)] for b in range(2)], np.int64)
+    blk = np.zeros((2, 24), np.uint8)
+    for b, (dv, mv) in enumerate(((0.5, -3.0), (-0.25, 1.5))):
+        blk[b, 0:2] = _f16b(dv)
+        blk[b, 2:4] = _f16b(mv)
+        qh = 0
+        for j in range(32):
+            blk[b, 8 + (j % 16)] |= (x[b, j] & 15) << (4 if j >= 16 else 0)
+            qh |= int(x[b, j] >> 4) << j
+        blk[b, 4:8] = np.frombuffer(np.uint32(qh).tobytes(), np.uint8)
+    want = np.concatenate([(x[0] * np.float32(0.5)).astype(np.float32) + np.float32(-3.0),
+                           (x[1] * np.float32(-0.25)).astype(np.float32) + np.float32(1.5)]).astype(np.float32)
+    assert (orc.dequant_row(GType.Q5_1, blk.reshape(-1), 64) == want).all()
+    y = np.array([(17 * j) % 255 - 127 for j in range(64)], np.int64)
+    ya = np.zeros((2, 34), np.uint8)
+    for b, yd in enumerate((0.5, 2.0)):
+        ya[b, 0:2] = _f16b(yd)
+        ya[b, 2:34] = y[32 * b:32 * b + 32].astype(np.int8).view(np.uint8)
+    si, sm = orc.block_ints(GType.Q5_1, blk.reshape(-1), ya.reshape(-1), 64)
+    assert list(si) == [int(x[0] @ y[:32]), int(x[1] @ y[32:])]
+    assert list(sm) == [int(y[:32].sum()), int(y[32:].sum())]
+    t0 = np.float32(np.float64(0.5) * np.float64(si[0]) + np.float64(np.float32(-3.0) * np.float32(sm[0])))
+    t1 = np.float32(np.float64(-0.25) * np.float64(si[1]) + np.float64(np.float32(1.5) * np.float32(sm[1])))
+    acc = np.float32(np.float64(0.5) * np.float64(t0))
+    want_dot = np.float32(np.float64(2.0) * np.float64(t1) + np.float64(acc))   # fmaf: one rounding each
+    assert orc.row_dot(GType.Q5_1, blk.reshape(-1), ya.reshape(-1), 64) == want_dot
+
+
 def test_q8k_known_answers():
     x = np.zeros(512, np.float32)
     # block 0: max -127 at index 3 -> iscale = 1, q = round-half-even(x)
@@ -623,7 +655,7 @@ def test_q8k_known_answers():
 # ------------------------------------------------------------------ block decoding
 
 ALL = [GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ2_XXS, GType.IQ4_NL, GType.Q8_0, GType.MXFP4,
-       GType.Q5_0, GType.Q2_K, GType.Q3_K, GType.IQ3_XXS, GType.IQ3_S, GType.IQ2_S, GType.IQ1_S]
+       GType.Q5_0, GType.Q2_K, GType.Q3_K, GType.IQ3_XXS, GType.IQ3_S, GType.IQ2_S, GType.IQ1_S, GType.Q5_1]
 
 
 def blocks(t, nb, seed):
