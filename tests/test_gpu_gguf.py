@@ -36,7 +36,8 @@ def _reference(L, W_r, x):
     return logits, ids, wts, orc.moe_layer(oracle_layer(L), x, ids, wts)
 
 
-@pytest.mark.parametrize("tg,td", [(GType.Q4_K, GType.Q6_K), (GType.IQ4_XS, GType.IQ4_XS)])
+@pytest.mark.parametrize("tg,td", [(GType.Q4_K, GType.Q6_K), (GType.IQ4_XS, GType.IQ4_XS), (GType.IQ1_S, GType.Q2_K),
+                                   (GType.MXFP4, GType.Q5_1), (GType.IQ3_S, GType.Q3_K)])
 def test_gguf_layer_runs_bit_exact(cuda, tmp_path, tg, td):
     print(f"gguf layer {tg.name}/{td.name}: E {E} d {D} ff {FF}", flush=True)
     L = random_layer(tg, td, E, FF, D, seed=31 + int(tg))

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import oracle as orc
-from hyper_amd import moe
+from hyper_amd import HyError, moe
 from hyper_amd.formats import GType, block_bytes, block_elems, q8_row_bytes, random_blocks, vec_dot_type
 from tests.helpers import (ALL_TYPES, D_RANGE, TYPES_256, assert_bits_equal, gen, layer, oracle_layer, rel_l2, routing,
                            x_distributions)
@@ -70,6 +70,25 @@ def test_block_ints_bitexact(cuda, t):
     _sync()
     assert_bits_equal(si.cpu().numpy().reshape(nrows, nb), ref_si, f"sumi {t.name}")
     assert_bits_equal(sm.cpu().numpy().reshape(nrows, nb), ref_sm, f"summ {t.name}")
+
+
+def test_block_ints_rejects_row_strides_that_break_span_alignment(cuda):
+    """Row strides must keep each row's 256-value spans at the alignment they have in the uploaded layout (the largest
+    power of two dividing the span, at most 16), which the 17- and 18-byte block types' reads count on: rejected
+    before any launch, with the output left untouched; a padded stride that keeps the alignment is accepted."""
+    n = 256
+    for t, bad, good in ((GType.MXFP4, 136 + 4, 136 + 8), (GType.IQ4_NL, 144 + 2, 144 + 16), (GType.Q6_K, 211, 212)):
+        rows = torch.zeros(2 * good, dtype=torch.uint8, device=cuda)
+        xq = torch.from_numpy(orc.quantize(vec_dot_type(t), np.ones(n, np.float32))).to(cuda)
+        nb = n // block_elems(t)
+        si = torch.full((2 * nb,), 7, dtype=torch.int32, device=cuda)
+        sm = torch.full((2 * nb,), 7, dtype=torch.int32, device=cuda)
+        with pytest.raises(HyError, match="row_bytes"):
+            moe.block_ints(t, rows, bad, 2, xq, n, si, sm)
+        _sync()
+        assert (si.cpu() == 7).all() and (sm.cpu() == 7).all()
+        moe.block_ints(t, rows, good, 2, xq, n, si, sm)
+        _sync()
 
 
 # ------------------------------------------------------------------ A1-A3: router and bucketing
