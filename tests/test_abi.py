@@ -30,12 +30,19 @@ def test_exports_every_declared_symbol():
     assert names == set(hyper_amd.SIGNATURES), "Python signatures out of step with the header"
 
 
+# block geometry of every expert type (src/gguf.cpp:43-82) and its activation partner (8 = Q8_0, 15 = Q8_K)
+EXPERT_TYPES = {6: (22, 32, 8), 7: (24, 32, 8), 8: (34, 32, 8), 10: (84, 256, 15), 11: (110, 256, 15), 12: (144, 256, 15),
+                13: (176, 256, 15), 14: (210, 256, 15), 16: (66, 256, 15), 17: (74, 256, 15), 18: (98, 256, 15),
+                19: (50, 256, 15), 20: (18, 32, 8), 21: (110, 256, 15), 22: (82, 256, 15), 23: (136, 256, 15),
+                39: (17, 32, 8)}
+
+
 def test_host_queries():
     L = lib()
     assert L.hy_abi_version() == 1
-    sizes = {12: (144, 256), 13: (176, 256), 14: (210, 256), 17: (74, 256), 20: (18, 32), 23: (136, 256), 8: (34, 32), 15: (292, 256)}
-    for t, (bb, be) in sizes.items():          # src/gguf.cpp:43-82
-        assert L.hy_block_bytes(t) == bb and L.hy_block_elems(t) == be
+    for t, (bb, be, vt) in EXPERT_TYPES.items():
+        assert (L.hy_block_bytes(t), L.hy_block_elems(t), L.hy_vec_dot_type(t)) == (bb, be, vt), t
+    assert L.hy_block_bytes(15) == 292 and L.hy_block_elems(15) == 256
     assert L.hy_vec_dot_type(20) == 8 and L.hy_vec_dot_type(12) == 15 and L.hy_vec_dot_type(2) == -1
     assert L.hy_q8_row_bytes(15, 2048) == 8 * 292 and L.hy_q8_row_bytes(8, 4096) == 128 * 34 and L.hy_q8_row_bytes(15, 100) == 0
 
@@ -166,3 +173,21 @@ def test_descriptor_weights_16_byte_aligned():
         setattr(m, field, 16 + 2)
         assert L.hy_moe_gate_up(ctypes.byref(m), p, 2048, p, 8, p, 1, None, None, None) == hyper_amd.HY_EBAD_SHAPE
         assert b"16-byte aligned" in L.hy_last_error()
+
+
+def test_type_ids_agree_across_header_python_and_oracle():
+    """include/hymoe.h's HY_* type ids, hyper_amd.formats.GType and the oracle's ids name the same GGUF type ids
+    (src/gguf.h:13-18), and every expert type there has the block geometry above."""
+    import oracle as orc
+    from hyper_amd.formats import GType, block_bytes, block_elems, vec_dot_type
+    text = (ROOT / "include/hymoe.h").read_text()
+    header = {m.group(1): int(m.group(2)) for m in re.finditer(r"\bHY_([A-Z0-9_]+)\s*=\s*(\d+)", text)
+              if not m.group(1).startswith("E")}
+    assert {k: v for k, v in header.items() if k not in ("OK",)} == {t.name: int(t) for t in GType}
+    for t in GType:
+        assert getattr(orc, t.name) == int(t)
+        if int(t) in EXPERT_TYPES:
+            bb, be, vt = EXPERT_TYPES[int(t)]
+            assert (block_bytes(t), block_elems(t), int(vec_dot_type(t))) == (bb, be, vt), t.name
+            assert orc.BLOCK_BYTES[int(t)] == bb and orc.block_elems(t) == be and orc.vec_dot_type(t) == vt, t.name
+    assert set(EXPERT_TYPES) == {int(t) for t in GType} - {15}
