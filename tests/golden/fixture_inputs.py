@@ -4,16 +4,20 @@ import hashlib
 import numpy as np
 import torch
 
-from hyper_amd.formats import GType, random_blocks, random_layer
+from hyper_amd.formats import GType, block_elems, random_blocks, random_layer, vec_dot_type
 
 CASES = {
     "q8k_heavy": {"kind": "quant", "vt": GType.Q8_K, "seed": 1},
     "q8_0_heavy": {"kind": "quant", "vt": GType.Q8_0, "seed": 2},
     **{f"blocks_{t.name}": {"kind": "blocks", "t": t, "n": 1024, "seed": 10 + int(t)}
-       for t in (GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ4_NL)},
+       for t in (GType.Q4_K, GType.Q5_K, GType.Q6_K, GType.IQ4_XS, GType.IQ2_XS, GType.IQ4_NL,
+                 GType.Q8_0, GType.IQ2_XXS, GType.MXFP4, GType.Q5_0, GType.Q5_1, GType.Q2_K, GType.Q3_K, GType.IQ3_XXS,
+                 GType.IQ3_S, GType.IQ2_S, GType.IQ1_S)},
     "route_288_8": {"kind": "route", "E": 288, "k": 8, "seed": 3},
     "layer_q4k_q6k": {"kind": "layer", "tg": GType.Q4_K, "td": GType.Q6_K, "E": 3, "ff": 256, "d": 512, "k": 2, "nt": 2, "seed": 4},
     "layer_iq4nl": {"kind": "layer", "tg": GType.IQ4_NL, "td": GType.IQ4_NL, "E": 3, "ff": 256, "d": 512, "k": 2, "nt": 2, "seed": 5},
+    "layer_iq3s_q3k": {"kind": "layer", "tg": GType.IQ3_S, "td": GType.Q3_K, "E": 3, "ff": 256, "d": 512, "k": 2, "nt": 2, "seed": 6},
+    "layer_mxfp4_q5_1": {"kind": "layer", "tg": GType.MXFP4, "td": GType.Q5_1, "E": 3, "ff": 256, "d": 512, "k": 2, "nt": 2, "seed": 7},
 }
 
 
@@ -32,10 +36,10 @@ def inputs(name: str) -> dict:
     if c["kind"] == "blocks":
         import oracle as orc
         t, n = c["t"], c["n"]
-        nb = n // (32 if t == GType.IQ4_NL else 256)
+        nb = n // block_elems(t)
         w = random_blocks(t, 3 * nb, g, "cpu", (1e-3, 1e-2)).numpy().reshape(3, -1)
         x = torch.randn(n, generator=g).numpy().astype(np.float32)
-        vt = GType.Q8_0 if t == GType.IQ4_NL else GType.Q8_K
+        vt = vec_dot_type(t)
         return {"w": w, "x": x, "xq": orc.quantize(vt, x)}
     if c["kind"] == "route":
         return {"logits": (torch.randn(5, c["E"] + 1, generator=g) * 2).numpy().astype(np.float32)}
