@@ -1,7 +1,7 @@
 // Decode / short-verify path in three launches per MoE layer, with no hand-off between blocks of a launch
 // (device-scope fences and contended atomics cost more than a launch boundary on MI355X):
-//   k_router_q8      router GEMV, a wave per logit row with its loads in flight together, and separate waves for the
-//                    Q8 blocks of x (gemv_f32, src/kernels4.cu:163-180);
+//   k_router_q8      router GEMV, a wave per (row, token) logit with its loads in flight together, and separate
+//                    waves for the Q8 blocks of x (gemv_f32, src/kernels4.cu:163-180);
 //   k_route_gate_up  every block routes its own token from the logits (softmax / top-k / renormalise / shared gate,
 //                    src/kernels4.cu:297-344: up to 128 experts ranked by all eight waves at once, more by one wave),
 //                    then each wave takes rw ff rows of its pair, gate and up against the Q8 x, and one wave folds
@@ -63,11 +63,11 @@ __global__ __launch_bounds__(256) void k_router_q8(const WT *__restrict__ W, int
     HY_STAMP_VARS(3);
     HY_STAMP(0);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int gw = blockIdx.x * 4 + wave, r = gw;
-    // waves [0, rows): a logit row each; waves [rows, rows + units): the Q8 of x, a Q8_K block (token q / nb) or a
-    // Q8_0 pair of blocks each -- no wave does both, so neither waits for the other
-    if (r >= rows) {
-        const int q = gw - rows;
+    const int gw = blockIdx.x * 4 + wave, lw = rows * nt;   // waves [0, lw): one (row, token) logit each
+    // waves [lw, lw + units): the Q8 of x, a Q8_K block (token q / nb) or a Q8_0 pair of blocks each -- no wave does
+    // both, so neither waits for the other
+    if (gw >= lw) {
+        const int q = gw - lw;
         if (VT == Q8_K) {
             const int nb = kdim / 256;
             if (q < nt * nb) {
@@ -86,51 +86,35 @@ __global__ __launch_bounds__(256) void k_router_q8(const WT *__restrict__ W, int
         HY_STAMP_SAVE(4 * gw, 3, lane == 0 && gw < 4094, false);
         return;
     }
-    // logits of row r for every token: lane L sums elements 256 i + 4 L + j with fmaf, then the butterfly.  The
-    // row's loads go out RB float4 at a time (one memory round trip per 256 RB values), then the fma chains.
+    // logit (row r, token t), the token waves of a row next to each other (they share its weight loads in L2): lane L
+    // sums elements 256 i + 4 L + j with fmaf, then the butterfly.  The loads go out RB float4 pairs at a time (one
+    // memory round trip per 256 RB values), then the fma chain.
+    const int r = gw / nt, t = gw - r * nt;
     constexpr int RB = 8;
     const WT *wr = W + (size_t) r * kdim;
-    const float bv = bias && lane < nt ? bias[(size_t) lane * bs + r] : 0.0f;   // token lane's bias, added after the butterfly
-    float acc[DEC_ROUTE_NT];
-#pragma unroll
-    for (int t = 0; t < DEC_ROUTE_NT; ++t) acc[t] = 0.0f;
+    const float *xt = x + (size_t) t * xs;
+    float acc = 0.0f;
     for (int e0 = 0; e0 < kdim; e0 += 256 * RB) {
         float4 w[RB], xv[RB];
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
             const int e = e0 + 256 * i + 4 * lane;
             w[i] = e < kdim ? ld_w4(wr + e) : make_float4(0, 0, 0, 0);
-            xv[i] = e < kdim ? *(const float4 *) (x + e) : make_float4(0, 0, 0, 0);
+            xv[i] = e < kdim ? *(const float4 *) (xt + e) : make_float4(0, 0, 0, 0);
         }
 #pragma unroll
-        for (int t = 0; t < DEC_ROUTE_NT; ++t) {
-            if (t >= nt) break;
-            if (t > 0) {
-#pragma unroll
-                for (int i = 0; i < RB; ++i) {
-                    const int e = e0 + 256 * i + 4 * lane;
-                    xv[i] = e < kdim ? *(const float4 *) (x + (size_t) t * xs + e) : make_float4(0, 0, 0, 0);
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < RB; ++i) {
-                if (e0 + 256 * i + 4 * lane < kdim) {
-                    acc[t] = __builtin_fmaf(w[i].x, xv[i].x, acc[t]);
-                    acc[t] = __builtin_fmaf(w[i].y, xv[i].y, acc[t]);
-                    acc[t] = __builtin_fmaf(w[i].z, xv[i].z, acc[t]);
-                    acc[t] = __builtin_fmaf(w[i].w, xv[i].w, acc[t]);
-                }
+        for (int i = 0; i < RB; ++i) {
+            if (e0 + 256 * i + 4 * lane < kdim) {
+                acc = __builtin_fmaf(w[i].x, xv[i].x, acc);
+                acc = __builtin_fmaf(w[i].y, xv[i].y, acc);
+                acc = __builtin_fmaf(w[i].z, xv[i].z, acc);
+                acc = __builtin_fmaf(w[i].w, xv[i].w, acc);
             }
         }
     }
-#pragma unroll
-    for (int t = 0; t < DEC_ROUTE_NT; ++t) {
-        if (t < nt) {
-            float v = wave_sum_xor(acc[t]);
-            if (bias) v = v + readlane_f(bv, t);
-            if (lane == 0) logits[(size_t) t * ls + r] = v;
-        }
-    }
+    float v = wave_sum_xor(acc);
+    if (bias) v = v + bias[(size_t) t * bs + r];   // the token's bias, added after the butterfly
+    if (lane == 0) logits[(size_t) t * ls + r] = v;
     HY_STAMP(1);
     HY_STAMP_SET(2, 1);
     HY_STAMP_SAVE(4 * gw, 3, lane == 0 && gw < 4094, false);
@@ -636,7 +620,7 @@ static int router_q8_any(const WT *W, int rows, int kdim, const float *x, int xs
     if (nt == 0) return HY_OK;
     if (nt > DEC_ROUTE_NT) return launch_router_pre(W, rows, kdim, x, xs, bias, bs, logits, ls, vtype, xq, nt, s);   // batched rows
     const int qwaves = vtype == Q8_K ? nt * (kdim / 256) : nt * ((kdim / 32 + 1) / 2);
-    const int blocks = (rows + qwaves + 3) / 4;
+    const int blocks = (rows * nt + qwaves + 3) / 4;   // a wave per (row, token) logit, then the Q8 waves
     if (vtype == Q8_K)
         hipLaunchKernelGGL((k_router_q8<Q8_K, WT>), dim3(blocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, (uint8_t *) xq, nt);
     else

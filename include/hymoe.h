@@ -203,7 +203,7 @@ int hy_moe_down_reduce_residual(const hy_moe_dev *m, const float *h, const int32
 
 /* Router logits and the Q8 rows of x in one launch: logits as hy_gemv_f32 (rows of W_r, stride ls >= rows) and xq as
    hy_q8_quantize(vtype, x, xs, kdim, nt) -- fuses gemv_f32 (src/kernels4.cu:1910-1913) with the activation
-   quantization of the expert kernels.  Up to 8 tokens a wave per logit row; more, the batched router (16 rows by 16
+   quantization of the expert kernels.  Up to 8 tokens a wave per (row, token) logit; more, the batched router (16 rows by 16
    or 8 tokens a block through LDS), still one launch with the quantization. */
 int hy_moe_router_q8(const float *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride, float *logits,
                      int ls, int vtype, void *xq, int nt, hipStream_t s);
