@@ -299,23 +299,61 @@ __global__ __launch_bounds__(RR_THREADS, 2) void k_router_rows(const WT *__restr
         for (int i = 0; i < NI; ++i) dma_s128(src + 256 * i, 16u * (uint32_t) lane, lds_addr(&st[buf][wave * ROWF4 + 64 * i]));
     };
     dma_chunk(0, 0);
+    // the weights in K order (the first half of every row, then the second): chunk 0's fmas over the first half run
+    // while the second half is still on its way
     f4v w[RR_ROWS][NI];
+    const WT *wr[RR_ROWS];
 #pragma unroll
-    for (int a = 0; a < RR_ROWS; ++a) {
-        const WT *wr = W + (size_t) min(r0 + a, rows - 1) * kdim + 4 * lane;
+    for (int a = 0; a < RR_ROWS; ++a) wr[a] = W + (size_t) min(r0 + a, rows - 1) * kdim + 4 * lane;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) { const float4 v = ld_w4(wr + 256 * i); w[a][i] = f4v{v.x, v.y, v.z, v.w}; }
-    }
-    // the weights (and chunk 0) landed, by a wait the compiler sees: it then places no wait for the weight registers
-    // inside the chunk loop, where one would also wait for the next chunk's DMAs
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0), expcnt and lgkmcnt at their maxima
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int a = 0; a < RR_ROWS; ++a) { const float4 v = ld_w4(wr[a] + 256 * i); w[a][i] = f4v{v.x, v.y, v.z, v.w}; }
+    float acc[RR_ROWS][RR_TC];
+    // the fmas of K half h (i in [h NI / 2, (h + 1) NI / 2)) of a chunk staged in buffer buf: each (row, token) chain
+    // runs over i in order, so the halves in turn give the same bits as one pass
+    auto fma_half = [&](int buf, int h) {
+        if (!wave_on) return;
+#pragma unroll
+        for (int ii = 0; ii < NI / 2; ++ii) {
+            const int i = h * (NI / 2) + ii;
+#pragma unroll
+            for (int u = 0; u < RR_TC; ++u) {
+                const f4v xv = st[buf][u * ROWF4 + 64 * i + lane];
+#pragma unroll
+                for (int a = 0; a < RR_ROWS; ++a) {
+                    float s = acc[a][u];
+                    s = __builtin_fmaf(w[a][i].x, xv.x, s);
+                    s = __builtin_fmaf(w[a][i].y, xv.y, s);
+                    s = __builtin_fmaf(w[a][i].z, xv.z, s);
+                    s = __builtin_fmaf(w[a][i].w, xv.w, s);
+                    acc[a][u] = s;
+                }
+            }
+        }
+    };
+    // chunk 0 and the first half of the weights landed (a wave's loads complete in issue order), by waits the compiler
+    // sees: it places no wait for the weight registers itself (inside the chunk loop one would also wait for the next
+    // chunk's DMAs)
+    constexpr int VM_HALF = RR_ROWS * NI / 2;
+    __builtin_amdgcn_s_waitcnt((VM_HALF & 15) | ((VM_HALF >> 4) << 14) | 0x0F70);   // vmcnt(VM_HALF), expcnt and lgkmcnt at their maxima
+    lds_barrier();   // every wave's DMAs of chunk 0
+#pragma unroll
+    for (int a = 0; a < RR_ROWS; ++a)
+#pragma unroll
+        for (int u = 0; u < RR_TC; ++u) acc[a][u] = 0.0f;
+    fma_half(0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the second half
     if (nchunk > 1) dma_chunk(1, 1);
     constexpr int NOUT = RR_ROWS * RR_TC, P = 16, LPO = 64 / P, SUB = 64 / LPO;   // the tree of gemv_block_lds, 16 outputs a pass
     static_assert(NOUT % P == 0 && RR_WAVES * 64 * P <= RR_TC * ROWF4 * 4, "the passes fit a chunk buffer");
+    static_assert(NI % 2 == 0 && VM_HALF < 64, "two halves; vmcnt holds 6 bits");
     for (int c = 0; c < nchunk; ++c) {
         const int buf = c & 1, c0 = t_beg + RR_TC * c, ntok = min(RR_TC, t_end - c0);
-        if (c + 1 < nchunk) wait_vm<NI>(); else wait_vm<0>();   // this wave's DMAs of chunk c have landed
-        lds_barrier();                                           // and every wave's
+        if (c > 0) {
+            if (c + 1 < nchunk) wait_vm<NI>(); else wait_vm<0>();   // this wave's DMAs of chunk c have landed
+            lds_barrier();                                           // and every wave's
+        }
         // the chunk's Q8 rows (from LDS): Q8_K a 256-value block per 16-lane row, Q8_0 a pair of 32-value blocks a wave
         if constexpr (VT == Q8_K) {
             const int units = ntok * NI;
@@ -336,28 +374,14 @@ __global__ __launch_bounds__(RR_THREADS, 2) void k_router_rows(const WT *__restr
                 q8_0_pair_vals(v, xq + ((size_t) (c0 + tk) * (8 * NI) + 2 * pb) * Q8_0_BYTES, true, Q8_0_BYTES, 2);
             }
         }
-        float acc[RR_ROWS][RR_TC];
+        if (c > 0) {
 #pragma unroll
-        for (int a = 0; a < RR_ROWS; ++a)
+            for (int a = 0; a < RR_ROWS; ++a)
 #pragma unroll
-            for (int u = 0; u < RR_TC; ++u) acc[a][u] = 0.0f;
-        if (wave_on) {
-#pragma unroll
-            for (int i = 0; i < NI; ++i)
-#pragma unroll
-                for (int u = 0; u < RR_TC; ++u) {
-                    const f4v xv = st[buf][u * ROWF4 + 64 * i + lane];
-#pragma unroll
-                    for (int a = 0; a < RR_ROWS; ++a) {
-                        float s = acc[a][u];
-                        s = __builtin_fmaf(w[a][i].x, xv.x, s);
-                        s = __builtin_fmaf(w[a][i].y, xv.y, s);
-                        s = __builtin_fmaf(w[a][i].z, xv.z, s);
-                        s = __builtin_fmaf(w[a][i].w, xv.w, s);
-                        acc[a][u] = s;
-                    }
-                }
+                for (int u = 0; u < RR_TC; ++u) acc[a][u] = 0.0f;
+            fma_half(buf, 0);
         }
+        fma_half(buf, 1);
         lds_barrier();   // every wave is past its reads of this chunk: its buffer is the reduction's scratch now
         if (wave_on) {
             float *red = (float *) st[buf] + wave * 64 * P;
@@ -546,54 +570,53 @@ int launch_route_bias(int mode, const float *logits, int ls, const float *bias, 
 }
 
 // ---------------------------------------------------------------- bucketing (A3)
-// One block of 16 waves.  Pairs p with slot[ids[p]] >= 0, grouped by expert, stable by pair index
-// (src/cpu_moe.cpp:672-687 order; the GPU reference src/kernels4.cu:1275-1295 is unordered within an
-// expert).  Wave w owns a contiguous segment of pairs: (1) per-wave histograms, (2) prefix over experts
-// and waves, egrp/order_n, (3) each wave walks its segment 64 pairs at a time: a lane finds the lanes that hold its
-// expert from ten ballots (one per bit of the id, ids < 1024), its rank is the number of those below it, and the
-// highest of them advances the wave's running counter for the expert.
-constexpr int ORD_WAVES = 16;
-constexpr int ORD_B = 8;   // 64-pair rows of a wave's segment whose ids are loaded together
-__global__ __launch_bounds__(64 * ORD_WAVES) void k_order(const int *__restrict__ slot, const int *__restrict__ ids, int P, int ne,
-                                                          int *__restrict__ order, int *__restrict__ order_n, int *__restrict__ egrp) {
-    __shared__ int c[ORD_WAVES * 1024];
-    __shared__ int tot[1024];
-    __shared__ int s_slot[1024];
-    __shared__ int wsum[2][ORD_WAVES];
+// Pairs p with slot[ids[p]] >= 0, grouped by expert, stable by pair index (src/cpu_moe.cpp:672-687 order; the GPU
+// reference src/kernels4.cu:1275-1295 is unordered within an expert).  Block i places pairs [1024 i, 1024 i + 1024),
+// a 64-pair row a wave, with no word from the other blocks: (1) every block counts all pairs per expert (tot, the
+// experts' starts) and those before its range (pre) -- the ids are re-read from L2 by each block, 4 P bytes --, and
+// its rows per expert; (2) per expert e (thread e): the exclusive scan of the totals over the experts gives e's start,
+// and start + pre[e] + the block's earlier rows the offset of each row's first e; block 0 writes egrp and order_n;
+// (3) a lane's rank among its row's lanes of the same expert comes from log2(ne) ballots (one per bit of the id).
+constexpr int ORD_T = 1024, ORD_W = ORD_T / 64;   // pairs (threads) a block; rows (waves) a block
+constexpr int ORD_B = 8;                          // ids a thread loads together in the counting pass
+__global__ __launch_bounds__(ORD_T) void k_order(const int *__restrict__ slot, const int *__restrict__ ids, int P, int ne, int nbits,
+                                                 int *__restrict__ order, int *__restrict__ order_n, int *__restrict__ egrp) {
+    __shared__ int c[ORD_W * 1024];   // the rows' counts per expert, then the offset of each row's first pair of e
+    __shared__ int tot[1024], pre[1024], s_slot[1024];
+    __shared__ int wsum[2][ORD_W];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int seg = ((P + ORD_WAVES - 1) / ORD_WAVES + 63) / 64 * 64;
-    const int p0 = w * seg, p1 = min(P, p0 + seg);
-    // the ids of a batch (ORD_B rows of 64 pairs) in flight together; the slot table goes to LDS alongside the first
-    int idv[ORD_B];
-    auto load_ids = [&](int q0) {
+    const int b0 = blockIdx.x * ORD_T, p = b0 + tid;
+    const int my_e = p < P ? ids[p] : -1;
+    const int sl = tid < ne ? slot[tid] : -1;
+    for (int i = tid; i < ORD_W * ne; i += ORD_T) c[i] = 0;
+    if (tid < ne) { s_slot[tid] = sl; tot[tid] = 0; pre[tid] = 0; }
+    __syncthreads();
+    auto valid_e = [&](int e) { return e >= 0 && e < ne && s_slot[e] >= 0; };
+    for (int q0 = 0; q0 < P; q0 += ORD_T * ORD_B) {
+        int idv[ORD_B];
 #pragma unroll
         for (int r = 0; r < ORD_B; ++r) {
-            const int p = q0 + 64 * r + lane;
-            idv[r] = p < p1 ? ids[p] : -1;
+            const int q = q0 + ORD_T * r + tid;
+            idv[r] = q < P ? ids[q] : -1;
         }
-    };
-    auto valid_e = [&](int e) { return e >= 0 && e < ne && s_slot[e] >= 0; };
-    const bool one_batch = p1 - p0 <= 64 * ORD_B;   // wave-uniform: the ids stay in registers for the second pass
-    load_ids(p0);
-    const int sl = tid < ne ? slot[tid] : -1;
-    for (int i = tid; i < ORD_WAVES * ne; i += blockDim.x) c[i] = 0;
-    if (tid < ne) s_slot[tid] = sl;
-    __syncthreads();
-    for (int q0 = p0; q0 < p1; q0 += 64 * ORD_B) {
-        if (q0 != p0) load_ids(q0);
 #pragma unroll
-        for (int r = 0; r < ORD_B; ++r)
-            if (valid_e(idv[r])) atomicAdd(&c[w * ne + idv[r]], 1);
+        for (int r = 0; r < ORD_B; ++r) {
+            if (valid_e(idv[r])) {
+                atomicAdd(&tot[idv[r]], 1);
+                if (q0 + ORD_T * r + tid < b0) atomicAdd(&pre[idv[r]], 1);
+            }
+        }
     }
+    const bool valid = valid_e(my_e);
+    if (valid) atomicAdd(&c[w * ne + my_e], 1);
     __syncthreads();
-    // per expert e (thread e): the waves' counts become offsets within the expert; then exclusive scans over the
-    // experts of the pair totals and of the active flags (ne <= 1024 = one entry per thread)
     {
+        // thread e: exclusive scans over the experts of the pair totals and of the active flags (ne <= 1024)
         const int e = tid;
-        int a = 0;
-        if (e < ne)
-            for (int ww = 0; ww < ORD_WAVES; ++ww) { const int v = c[ww * ne + e]; c[ww * ne + e] = a; a += v; }
-        const int b = a > 0;
+        int cnt[ORD_W];
+#pragma unroll
+        for (int ww = 0; ww < ORD_W; ++ww) cnt[ww] = e < ne ? c[ww * ne + e] : 0;
+        const int a = e < ne ? tot[e] : 0, b = a > 0;
         int sa = a, sb = b;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -606,47 +629,30 @@ __global__ __launch_bounds__(64 * ORD_WAVES) void k_order(const int *__restrict_
         for (int ww = 0; ww < w; ++ww) { oa += wsum[0][ww]; ob += wsum[1][ww]; }
         const int ea = oa + sa - a, eb = ob + sb - b;   // exclusive prefixes before e
         if (e < ne) {
-            tot[e] = ea;
-            if (b && egrp) { egrp[3 * eb] = e; egrp[3 * eb + 1] = ea; egrp[3 * eb + 2] = a; }
+            int base = ea + pre[e];
+#pragma unroll
+            for (int ww = 0; ww < ORD_W; ++ww) { c[ww * ne + e] = base; base += cnt[ww]; }
+            if (blockIdx.x == 0 && b && egrp) { egrp[3 * eb] = e; egrp[3 * eb + 1] = ea; egrp[3 * eb + 2] = a; }
         }
-        if (tid == blockDim.x - 1) {
+        if (blockIdx.x == 0 && tid == ORD_T - 1) {
             int ta = 0, tb = 0;
-            for (int ww = 0; ww < ORD_WAVES; ++ww) { ta += wsum[0][ww]; tb += wsum[1][ww]; }
+            for (int ww = 0; ww < ORD_W; ++ww) { ta += wsum[0][ww]; tb += wsum[1][ww]; }
             order_n[0] = ta; order_n[1] = tb;
         }
     }
     __syncthreads();
-    for (int i = tid; i < ORD_WAVES * ne; i += blockDim.x) c[i] += tot[i % ne];
-    __syncthreads();
-    int *cw = c + w * ne;
-    const unsigned long long below = (1ull << lane) - 1;
-    for (int q0 = p0; q0 < p1; q0 += 64 * ORD_B) {
-        if (!one_batch) load_ids(q0);
-#pragma unroll
-        for (int r = 0; r < ORD_B; ++r) {
-            if (q0 + 64 * r >= p1) break;   // wave-uniform
-            const int p = q0 + 64 * r + lane;
-            const int e = idv[r];
-            const bool valid = valid_e(e);
-            unsigned long long same = __ballot(valid);
-#pragma unroll
-            for (int bit = 0; bit < 10; ++bit) {
-                const unsigned long long ones = __ballot((e >> bit) & 1);
-                same &= ((e >> bit) & 1) ? ones : ~ones;
-            }
-            if (valid) {
-                const int rank = __popcll(same & below);
-                const int base = cw[e];
-                order[base + rank] = p;
-                if (rank == __popcll(same) - 1) cw[e] = base + rank + 1;   // the group's highest lane
-            }
-            __builtin_amdgcn_wave_barrier();
-        }
+    // the row: lanes of the same expert from the ballots of the id's bits (ids < ne < 2^nbits for valid lanes)
+    unsigned long long same = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+        const unsigned long long ones = __ballot((my_e >> bit) & 1);
+        same &= ((my_e >> bit) & 1) ? ones : ~ones;
     }
+    if (valid) order[c[w * ne + my_e] + __popcll(same & ((1ull << lane) - 1))] = p;
 }
 
 int launch_order(const int *slot, const int *ids, int P, int ne, int *order, int *order_n, int *egrp, hipStream_t s) {
-    hipLaunchKernelGGL(k_order, dim3(1), dim3(64 * ORD_WAVES), 0, s, slot, ids, P, ne, order, order_n, egrp);
+    const int blocks = std::max(1, (P + ORD_T - 1) / ORD_T), nbits = ne > 1 ? 32 - __builtin_clz((unsigned) (ne - 1)) : 0;
+    hipLaunchKernelGGL(k_order, dim3(blocks), dim3(ORD_T), 0, s, slot, ids, P, ne, nbits, order, order_n, egrp);
     return check_launch("hy_moe_order");
 }
 

@@ -128,13 +128,20 @@ def test_route_bitexact(cuda, E, k, nt):
     assert list(ids_r[0]) == list(range(k))
 
 
-@pytest.mark.parametrize("E,P,absent", [(128, 4096, 0), (512, 20480, 0), (288, 32, 5), (1024, 3000, 100), (16, 0, 0), (8, 333, 3)])
-def test_order_bitexact(cuda, E, P, absent):
+@pytest.mark.parametrize("E,P,absent,skew", [(128, 4096, 0, False), (512, 20480, 0, False), (288, 32, 5, False), (1024, 3000, 100, False),
+                                              (16, 0, 0, False), (8, 333, 3, False), (1, 1500, 0, False), (128, 4096, 3, True),
+                                              (128, 131072, 0, True)])
+def test_order_bitexact(cuda, E, P, absent, skew):
+    """Blocks of 1024 pairs each place their own range; ragged ends, one expert, Zipf-skewed ids (most pairs on a
+    few experts) and 128 blocks."""
     rng = np.random.default_rng(E + P)
     slot = np.arange(E, dtype=np.int32)
     if absent:
         slot[rng.choice(E, absent, replace=False)] = -1
-    ids = rng.integers(-2, E + 2, P).astype(np.int32)   # includes out-of-range ids (skipped)
+    if skew:
+        ids = np.minimum(rng.zipf(1.3, P) - 1, E + 1).astype(np.int32)
+    else:
+        ids = rng.integers(-2, E + 2, P).astype(np.int32)   # includes out-of-range ids (skipped)
     o_r, on_r, eg_r = orc.order(slot, ids, E)
     dev = moe.MoeDev.__new__(moe.MoeDev)
     from hyper_amd import hy_moe_dev
