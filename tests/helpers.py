@@ -22,7 +22,7 @@ def gen(seed: int) -> torch.Generator:
 def x_distributions(n: int, seed: int) -> dict:
     """The activation distributions of the reference's quantizer test (tools/cpumoebench.cu:53-86): normal,
     heavy-tailed x^3 * 30, values on a 1/8 grid (exact ties), sparse large outliers; plus all-zero and
-    negative-maximum blocks."""
+    negative-maximum blocks, and a block whose largest |x| occurs twice with opposite signs."""
     rng = np.random.default_rng(seed)
     z = rng.standard_normal(n).astype(np.float32)
     d = {
@@ -36,8 +36,12 @@ def x_distributions(n: int, seed: int) -> dict:
     d["zero_block"] = zero
     neg = z.copy()
     neg[37] = -50.0
-    neg[300] = 50.0     # equal magnitude later in the block: the first occurrence (negative) wins
+    neg[300] = 50.0     # equal magnitude in the next 256-value block
     d["neg_max"] = neg
+    tie = z.copy()
+    tie[20] = -60.0
+    tie[66] = 60.0      # equal magnitude later in the same 256-value block: the first occurrence (negative) wins
+    d["lane_tie"] = tie
     return d
 
 

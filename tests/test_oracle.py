@@ -206,7 +206,7 @@ def np_quantize_q8_0(x: np.ndarray) -> np.ndarray:
     return out
 
 
-@pytest.mark.parametrize("name", ["normal", "heavy", "ties", "sparse", "zero_block", "neg_max"])
+@pytest.mark.parametrize("name", ["normal", "heavy", "ties", "sparse", "zero_block", "neg_max", "lane_tie"])
 def test_q8k_matches_ggml_scalar_restatement(name):
     x = x_distributions(4096, seed=17)[name]
     got = orc.quantize(GType.Q8_K, x.reshape(2, 2048)).reshape(-1, 292)
