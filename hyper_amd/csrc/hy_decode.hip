@@ -56,7 +56,7 @@ struct Cursor {
 
 // ---------------------------------------------------------------- k_router
 
-template <int VT, typename WT>
+template <int VT, typename WT, int RB>
 __global__ __launch_bounds__(256) void k_router_q8(const WT *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
                                                    const float *__restrict__ bias, int bs, float *__restrict__ logits, int ls,
                                                    uint8_t *__restrict__ xq, int nt) {
@@ -88,9 +88,9 @@ __global__ __launch_bounds__(256) void k_router_q8(const WT *__restrict__ W, int
     }
     // logit (row r, token t), the token waves of a row next to each other (they share its weight loads in L2): lane L
     // sums elements 256 i + 4 L + j with fmaf, then the butterfly.  The loads go out RB float4 pairs at a time (one
-    // memory round trip per 256 RB values), then the fma chain.
+    // memory round trip per 256 RB values), then the fma chain.  RB 16 for one token and d > 2048 (d 4096 in one round
+    // trip, 7168 in two), else 8 (more tokens' waves need the occupancy of fewer registers).
     const int r = gw / nt, t = gw - r * nt;
-    constexpr int RB = 8;
     const WT *wr = W + (size_t) r * kdim;
     const float *xt = x + (size_t) t * xs;
     float acc = 0.0f;
@@ -621,10 +621,12 @@ static int router_q8_any(const WT *W, int rows, int kdim, const float *x, int xs
     if (nt > DEC_ROUTE_NT) return launch_router_pre(W, rows, kdim, x, xs, bias, bs, logits, ls, vtype, xq, nt, s);   // batched rows
     const int qwaves = vtype == Q8_K ? nt * (kdim / 256) : nt * ((kdim / 32 + 1) / 2);
     const int blocks = (rows * nt + qwaves + 3) / 4;   // a wave per (row, token) logit, then the Q8 waves
-    if (vtype == Q8_K)
-        hipLaunchKernelGGL((k_router_q8<Q8_K, WT>), dim3(blocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, (uint8_t *) xq, nt);
-    else
-        hipLaunchKernelGGL((k_router_q8<Q8_0, WT>), dim3(blocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, (uint8_t *) xq, nt);
+#define HY_RQ(VV, RR) hipLaunchKernelGGL((k_router_q8<VV, WT, RR>), dim3(blocks), dim3(256), 0, s, W, rows, kdim, x, xs, bias, bs, logits, ls, \
+                                         (uint8_t *) xq, nt)
+    const bool wide = nt == 1 && kdim > 2048;   // RB 8 already takes d <= 2048 in one round trip
+    if (vtype == Q8_K) { if (wide) HY_RQ(Q8_K, 16); else HY_RQ(Q8_K, 8); }
+    else { if (wide) HY_RQ(Q8_0, 16); else HY_RQ(Q8_0, 8); }
+#undef HY_RQ
     return check_launch("hy_moe_router_q8");
 }
 int launch_router_q8(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
