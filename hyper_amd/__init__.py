@@ -29,7 +29,7 @@ class hy_moe_dev(ctypes.Structure):
                 ("tg", ctypes.c_int32), ("td", ctypes.c_int32),
                 ("gate_bytes", ctypes.c_size_t), ("down_bytes", ctypes.c_size_t),
                 ("slot", ctypes.c_void_p), ("ff", ctypes.c_int32), ("n", ctypes.c_int32),
-                ("clamp", ctypes.c_float), ("n_expert", ctypes.c_int32)]
+                ("clamp", ctypes.c_float), ("n_expert", ctypes.c_int32), ("n_local", ctypes.c_int32)]
 
 
 class hy_expert_tensors(ctypes.Structure):
@@ -80,6 +80,7 @@ SIGNATURES = {
     "hy_moe_route_sqrtsp": (_I, [_P, _I, _P, _I, _I, _F, _P, _P, _I, _P]),
     "hy_moe_order": (_I, [_DEV, _P, _I, _I, _P, _P, _P, _P]),
     "hy_q8_quantize": (_I, [_I, _P, _I, _I, _I, _P, _P]),
+    "hy_q8k_quantize_host": (_I, [_P, _P, ctypes.c_int64]),
     "hy_moe_gate_up": (_I, [_DEV, _P, _I, _P, _I, _P, _I, _P, _P, _P]),
     "hy_moe_down": (_I, [_DEV, _P, _P, _P, _I, _P, _I, _P, _P, _P]),
     "hy_moe_gemm_gate_up": (_I, [_DEV, _P, _I, _I, _P, _P, _P, _I, _P, _P]),

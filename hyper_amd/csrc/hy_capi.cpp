@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -33,6 +34,7 @@ static bool gemm_type(int t) { return dot_type(t); }
 static int check_dev(const hy_moe_dev *m, const char *what, bool need_gate, bool need_down) {
     if (!m) { set_error("%s: null hy_moe_dev", what); return HY_EINVAL; }
     if (!m->slot || m->n_expert <= 0) { set_error("%s: slot table missing", what); return HY_EINVAL; }
+    if (m->n_local <= 0) { set_error("%s: n_local %d (the expert matrices behind gate/up/down) must be >= 1", what, m->n_local); return HY_EINVAL; }
     if (m->ff <= 0 || m->n <= 0) { set_error("%s: ff %d, n %d", what, m->ff, m->n); return HY_EBAD_SHAPE; }
     // every kernel's grid covers ff and n in whole 256-row / 256-value units (the tiled layout's 16-row tiles, the
     // GEMMs' 64- and 128-row blocks): both are checked whichever matrices the entry point reads
@@ -91,7 +93,7 @@ using namespace hy;
 extern "C" {
 
 const char *hy_last_error(void) { return g_err; }
-int hy_abi_version(void) { return 1; }
+int hy_abi_version(void) { return 2; }   // 2: hy_moe_dev.n_local
 
 size_t hy_block_bytes(int type) { return (size_t) block_bytes(type); }
 int hy_block_elems(int type) { return block_elems(type); }
@@ -156,7 +158,7 @@ int hy_upload_experts(const hy_expert_tensors *t, const int32_t *slot_host, int3
     m.tg = t->tg; m.td = t->td;
     m.gate_bytes = t->gb; m.down_bytes = t->db;
     m.slot = ds;
-    m.ff = ff; m.n = n; m.clamp = clamp; m.n_expert = t->E;
+    m.ff = ff; m.n = n; m.clamp = clamp; m.n_expert = t->E; m.n_local = (int32_t) n_alloc;
     *out = m;
     return HY_OK;
 }
@@ -212,8 +214,9 @@ int hy_moe_route_sqrtsp(const float *logits, int ls, const float *bias, int n_ex
 int hy_moe_order(const hy_moe_dev *m, const int32_t *ids, int n_pairs, int n_expert, int32_t *order, int32_t *order_n, hipStream_t s,
                  int32_t *egrp) {
     if (!m || !m->slot || !ids || !order || !order_n || n_pairs < 0) { set_error("hy_moe_order: bad argument"); return HY_EINVAL; }
+    if (m->n_local <= 0) { set_error("hy_moe_order: n_local %d must be >= 1", m->n_local); return HY_EINVAL; }
     if (n_expert <= 0 || n_expert > 1024 || n_expert > m->n_expert) { set_error("hy_moe_order: n_expert %d out of range", n_expert); return HY_EBAD_SHAPE; }
-    return launch_order(m->slot, ids, n_pairs, n_expert, order, order_n, egrp, s);
+    return launch_order(m->slot, m->n_local, ids, n_pairs, n_expert, order, order_n, egrp, s);
 }
 
 int hy_q8_quantize(int vtype, const float *x, int xs, int n, int nt, void *q, hipStream_t s) {
@@ -224,6 +227,52 @@ int hy_q8_quantize(int vtype, const float *x, int xs, int n, int nt, void *q, hi
         if (n <= 0 || n % 32 || ((uintptr_t) q & 1)) { set_error("hy_q8_quantize: Q8_0 needs n %% 32 == 0"); return HY_EBAD_SHAPE; }
     } else { set_error("hy_q8_quantize: vtype %d", vtype); return HY_EUNSUPPORTED_TYPE; }
     return launch_q8(vtype, x, xs, n, nt, q, s);
+}
+
+// src/cpu_moe.h:46 q8k_test_quantize on host memory: the block steps of src/cpu_moe.cpp:35-78 (the same ones the
+// device quantizer runs, hy_common.cuh q8k_block16), one 16-value group at a time.  Rounding: the product is
+// rounded to fp32 first (the build compiles with -ffp-contract=off), then 1.5 * 2^23 is added, which rounds it
+// half-to-even to an integer held in the low mantissa bits.
+int hy_q8k_quantize_host(const float *x, void *y, int64_t k) {
+    if (!x || !y || k < 0) { set_error("hy_q8k_quantize_host: bad argument"); return HY_EINVAL; }
+    if (k % 256) { set_error("hy_q8k_quantize_host: k = %lld is not a multiple of 256", (long long) k); return HY_EBAD_SHAPE; }
+    uint8_t *out = (uint8_t *) y;
+    for (int64_t b = 0; b < k / 256; ++b, x += 256, out += Q8K_BYTES) {
+        int at = -1;            // first position of the largest magnitude (NaNs never compare greater)
+        float best = 0.0f;
+        for (int j = 0; j < 256; ++j) {
+            const float a = std::fabs(x[j]);
+            if (a > best) { best = a; at = j; }
+        }
+        float d = 0.0f;
+        int8_t q[256];
+        int16_t sums[16];
+        if (at < 0) {
+            std::memset(q, 0, sizeof q);
+            std::memset(sums, 0, sizeof sums);
+        } else {
+            const float iscale = -127.0f / x[at];
+            for (int g = 0; g < 16; ++g) {
+                int s16 = 0;
+                for (int l = 0; l < 16; ++l) {
+                    const float prod = iscale * x[16 * g + l];
+                    const float biased = prod + 12582912.0f;
+                    uint32_t bits;
+                    std::memcpy(&bits, &biased, 4);
+                    int v = (int) (bits & 0x007fffffu) - 0x00400000;
+                    v = std::min(v, 127);
+                    q[16 * g + l] = (int8_t) v;
+                    s16 += v;
+                }
+                sums[g] = (int16_t) s16;
+            }
+            d = 1.0f / iscale;
+        }
+        std::memcpy(out, &d, 4);
+        std::memcpy(out + 4, q, 256);
+        std::memcpy(out + 260, sums, 32);
+    }
+    return HY_OK;
 }
 
 int hy_moe_gate_up(const hy_moe_dev *m, const float *x, int xs, const int32_t *ids, int k, float *h, int nt, hipStream_t s,

@@ -136,6 +136,8 @@ __device__ __forceinline__ uint32_t tiled_off32(int row, int span, int nspan, in
     return ((uint32_t) (row >> 4) * (uint32_t) nspan + (uint32_t) span) * (uint32_t) (HY_TILE * sb) + (uint32_t) (row & 15) * (uint32_t) sb;
 }
 __host__ __device__ constexpr int span_bytes(int t) { return block_bytes(t) * (256 / block_elems(t)); }
+// a slot-table entry as every kernel takes it: a local expert index below n_local, else -1 (absent)
+__device__ __forceinline__ int bound_slot(int raw, int n_local) { return (unsigned) raw < (unsigned) n_local ? raw : -1; }
 
 // ------------------------------------------------------------------ wave helpers
 

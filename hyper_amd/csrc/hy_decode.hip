@@ -253,8 +253,8 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
         }
     }
     constexpr int NS = 64 * V;   // slot-table entries held (n_expert <= NS)
-    const int sl0 = tid < ne ? m.slot[tid] : -1;
-    const int sl1 = NS > 64 * DEC_GU_WAVES && tid + 64 * DEC_GU_WAVES < ne ? m.slot[tid + 64 * DEC_GU_WAVES] : -1;
+    const int sl0 = tid < ne ? bound_slot(m.slot[tid], m.n_local) : -1;
+    const int sl1 = NS > 64 * DEC_GU_WAVES && tid + 64 * DEC_GU_WAVES < ne ? bound_slot(m.slot[tid + 64 * DEC_GU_WAVES], m.n_local) : -1;
     const float xd = tid < nb ? q8_scale<VT>(y, tid) : 0.0f;
     auto stage = [&] {
 #pragma unroll
@@ -415,8 +415,8 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     const int my_e = lane < k ? ids[t * k + lane] : -1;
     const float my_w = lane < k ? wts[t * k + lane] : 0.0f;
     const int tid = (int) threadIdx.x;
-    const int sl0 = tid < m.n_expert ? m.slot[tid] : -1;
-    const int sl1 = tid + 64 * DEC_DN_WAVES < m.n_expert ? m.slot[tid + 64 * DEC_DN_WAVES] : -1;
+    const int sl0 = tid < m.n_expert ? bound_slot(m.slot[tid], m.n_local) : -1;
+    const int sl1 = tid + 64 * DEC_DN_WAVES < m.n_expert ? bound_slot(m.slot[tid + 64 * DEC_DN_WAVES], m.n_local) : -1;
     float sh_x = 0.0f, sh_g = 1.0f;   // the shared expert's value and gate of this output, used at the end
     if (shexp && row_ok) {
         sh_x = shexp[(size_t) t * n + row];

@@ -56,7 +56,7 @@ __global__ __launch_bounds__(256) void k_gemv(hy_moe_dev m, int n_expert, const 
     if (order) { if ((int) blockIdx.x >= *order_n) return; p = order[blockIdx.x]; }
     else p = blockIdx.x;
     const int e = ids[p];
-    const int slot = (e >= 0 && e < n_expert) ? m.slot[e] : -1;
+    const int slot = (e >= 0 && e < n_expert) ? bound_slot(m.slot[e], m.n_local) : -1;
     const int in_dim = GU ? m.n : m.ff, rows = GU ? m.ff : m.n;
     const int r0 = blockIdx.y * R, nr = min(R, rows - r0);
     if (slot < 0) {
@@ -274,7 +274,7 @@ __global__ __launch_bounds__(256) void k_down_reduce(hy_moe_dev m, int n_expert,
         int c = 0;
         for (int j = 0; j < k; ++j) {
             const int e = ids[t * k + j];
-            if (e < 0 || e >= n_expert || m.slot[e] < 0) continue;
+            if (e < 0 || e >= n_expert || bound_slot(m.slot[e], m.n_local) < 0) continue;
             int i = c++;
             while (i > 0 && ids[t * k + ord[i - 1]] > e) { ord[i] = ord[i - 1]; --i; }
             ord[i] = j;
@@ -291,7 +291,7 @@ __global__ __launch_bounds__(256) void k_down_reduce(hy_moe_dev m, int n_expert,
         if (id < items) {
             const int j = id / (nr * ng), rem = id % (nr * ng), row = rem / ng, gi = rem % ng;
             const int e = ids[t * k + j];
-            const int sl = (e >= 0 && e < n_expert) ? m.slot[e] : -1;
+            const int sl = (e >= 0 && e < n_expert) ? bound_slot(m.slot[e], m.n_local) : -1;
             if (sl >= 0) {
                 const uint8_t *base = m.down + (size_t) sl * m.down_bytes + tiled_off(r0 + row, gi, ng, span_bytes(T));
                 it[i].load(base, L);

@@ -20,7 +20,7 @@ int launch_bf16_to_f32(const uint16_t *W, size_t n, float *out, hipStream_t s);
 int launch_route(const float *logits, int ls, int ne, int k, int *ids, float *wts, float *sg, int nt, hipStream_t s);
 int launch_route_bias(int mode, const float *logits, int ls, const float *bias, int ne, int k, float scale, int *ids, float *wts,
                       float *sg, int nt, hipStream_t s);
-int launch_order(const int *slot, const int *ids, int P, int ne, int *order, int *order_n, int *egrp, hipStream_t s);
+int launch_order(const int *slot, int n_local, const int *ids, int P, int ne, int *order, int *order_n, int *egrp, hipStream_t s);
 int launch_q8(int vtype, const float *x, int xs, int n, int nt, void *q, hipStream_t s);
 int launch_router_pre(const float *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
                       int vtype, void *xq, int nt, hipStream_t s);

@@ -579,7 +579,7 @@ int launch_route_bias(int mode, const float *logits, int ls, const float *bias, 
 // (3) a lane's rank among its row's lanes of the same expert comes from log2(ne) ballots (one per bit of the id).
 constexpr int ORD_T = 1024, ORD_W = ORD_T / 64;   // pairs (threads) a block; rows (waves) a block
 constexpr int ORD_B = 8;                          // ids a thread loads together in the counting pass
-__global__ __launch_bounds__(ORD_T) void k_order(const int *__restrict__ slot, const int *__restrict__ ids, int P, int ne, int nbits,
+__global__ __launch_bounds__(ORD_T) void k_order(const int *__restrict__ slot, int n_local, const int *__restrict__ ids, int P, int ne, int nbits,
                                                  int *__restrict__ order, int *__restrict__ order_n, int *__restrict__ egrp) {
     __shared__ int c[ORD_W * 1024];   // the rows' counts per expert, then the offset of each row's first pair of e
     __shared__ int tot[1024], pre[1024], s_slot[1024];
@@ -587,7 +587,7 @@ __global__ __launch_bounds__(ORD_T) void k_order(const int *__restrict__ slot, c
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int b0 = blockIdx.x * ORD_T, p = b0 + tid;
     const int my_e = p < P ? ids[p] : -1;
-    const int sl = tid < ne ? slot[tid] : -1;
+    const int sl = tid < ne ? bound_slot(slot[tid], n_local) : -1;
     for (int i = tid; i < ORD_W * ne; i += ORD_T) c[i] = 0;
     if (tid < ne) { s_slot[tid] = sl; tot[tid] = 0; pre[tid] = 0; }
     __syncthreads();
@@ -650,9 +650,9 @@ __global__ __launch_bounds__(ORD_T) void k_order(const int *__restrict__ slot, c
     if (valid) order[c[w * ne + my_e] + __popcll(same & ((1ull << lane) - 1))] = p;
 }
 
-int launch_order(const int *slot, const int *ids, int P, int ne, int *order, int *order_n, int *egrp, hipStream_t s) {
+int launch_order(const int *slot, int n_local, const int *ids, int P, int ne, int *order, int *order_n, int *egrp, hipStream_t s) {
     const int blocks = std::max(1, (P + ORD_T - 1) / ORD_T), nbits = ne > 1 ? 32 - __builtin_clz((unsigned) (ne - 1)) : 0;
-    hipLaunchKernelGGL(k_order, dim3(blocks), dim3(ORD_T), 0, s, slot, ids, P, ne, nbits, order, order_n, egrp);
+    hipLaunchKernelGGL(k_order, dim3(blocks), dim3(ORD_T), 0, s, slot, n_local, ids, P, ne, nbits, order, order_n, egrp);
     return check_launch("hy_moe_order");
 }
 

@@ -54,7 +54,7 @@ class MoeDev:
         c.tg, c.td = int(layer.tg), int(layer.td)
         c.gate_bytes, c.down_bytes = layer.gate_bytes, layer.down_bytes
         c.slot = slot.data_ptr()
-        c.ff, c.n, c.clamp, c.n_expert = layer.ff, layer.n, float(layer.clamp), slot.numel()
+        c.ff, c.n, c.clamp, c.n_expert, c.n_local = layer.ff, layer.n, float(layer.clamp), slot.numel(), layer.E
         self.c = c
         self.ref = ctypes.byref(c)
 

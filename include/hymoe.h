@@ -47,7 +47,9 @@ enum {
    the GGUF blocks of 256 values) of row r at byte ((r / 16) * nspan + s) * 16 * sb + (r % 16) * sb, nspan = values
    per row / 256.  The block bytes themselves are GGUF's; hy_upload_experts writes this order from GGUF rows.
    gate, up and down start 16-byte aligned (checked: HY_EBAD_SHAPE).
-   slot[e] (device, n_expert entries) = local index of expert e or -1. */
+   slot[e] (device, n_expert entries) = local index of expert e in [0, n_local), or -1; an entry outside
+   [0, n_local) is treated as -1 (absent) by every kernel, so a stale or corrupt table cannot index past the
+   allocation.  n_local: expert matrices allocated (hy_upload_experts sets it; must be >= 1). */
 typedef struct hy_moe_dev {
     const uint8_t *gate, *up, *down;
     int32_t tg, td;                 /* gate/up type, down type */
@@ -57,6 +59,7 @@ typedef struct hy_moe_dev {
     float clamp;                    /* SwiGLU limit (0: none) */
     int32_t n_expert;               /* entries of slot (not in MoeDev: ids outside [0, n_expert) are skipped, as on the CPU,
                                        src/cpu_moe.cpp:679, instead of indexing slot out of bounds) */
+    int32_t n_local;                /* expert matrices behind gate/up/down (not in MoeDev: bounds every slot entry) */
 } hy_moe_dev;
 
 /* Host view of one layer's GGUF expert tensors (replaces ExpertTensors, src/experts.h:20-26). */
@@ -159,6 +162,13 @@ int hy_moe_order(const hy_moe_dev *m, const int32_t *ids, int n_pairs, int n_exp
    (replaces to_half before the grouped GEMMs, src/kernels.cu:2235-2237, and the CPU path's quantizer,
    src/cpu_moe.cpp:35-78 for Q8_K).  vtype HY_Q8_K (n % 256 == 0) or HY_Q8_0 (n % 32 == 0). */
 int hy_q8_quantize(int vtype, const float *x, int xs, int n, int nt, void *q, hipStream_t s);
+
+/* The CPU expert path's Q8_K quantizer on host memory (replaces q8k_test_quantize, src/cpu_moe.h:46 /
+   src/cpu_moe.cpp:35-78): k values of x (host) -> k / 256 blocks of 292 bytes at y (host), synchronous, no HIP
+   call.  Per block: the first value of largest magnitude mx, iscale = -127 / mx, q = min(127, round-half-even of the
+   rounded product iscale * x), int16 sums of 16, d = 1 / iscale; an all-zero block gets d = 0, q = 0 and zero sums.
+   The blocks are bit-identical to hy_q8_quantize's.  k must be a multiple of 256 (HY_EBAD_SHAPE). */
+int hy_q8k_quantize_host(const float *x, void *y, int64_t k);
 
 /* Decode gate/up: h[p][f] = silu(gate_e[f] . x[t]) * (up_e[f] . x[t]) for pairs p = t*k + j (or the order_n[0]
    pairs in order) whose expert is local; x is quantized inside (replaces moe_gate_up, src/kernels4.cuh:67-68 /

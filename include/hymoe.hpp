@@ -207,10 +207,14 @@ inline void moe_decode_noalloc(const MoeDev &m, const float *W_r, int rows, cons
                                int k, const MoeDev *shared, float *out, bool residual, int nt, hipStream_t s) {
     check(hy_moe_decode_noalloc(&m, W_r, rows, x, xs, bias, bias_stride, k, shared, out, residual ? 1 : 0, nt, s));
 }
-// src/cpu_moe.h:46 q8k_test_quantize(x, y, k): the expert path's Q8_K activation quantizer, here on device memory
-// (the quantizer the kernels use; bit-identical to the reference's CPU quantizer, src/cpu_moe.cpp:35-78)
-inline void q8k_test_quantize(const float *x, void *y, int64_t k, hipStream_t s = nullptr) {
-    if (k % 256) throw std::runtime_error("q8k_test_quantize: k must be a multiple of 256");
+// src/cpu_moe.h:46 q8k_test_quantize(x, y, k): the CPU expert path's Q8_K quantizer, host buffers in and out,
+// synchronous (src/cpu_moe.cpp:35-78; the blocks equal the device quantizer's bit for bit)
+inline void q8k_test_quantize(const float *x, void *y, int64_t k) {
+    check(hy_q8k_quantize_host(x, y, k));
+}
+// the same quantizer on device memory, stream-ordered: one row of k values (the kernels' own quantizer)
+inline void q8k_quantize_device(const float *x, void *y, int64_t k, hipStream_t s) {
+    if (k < 0 || k % 256 || k > 0x7fffff00) throw std::runtime_error("q8k_quantize_device: k must be a multiple of 256 below 2^31");
     check(hy_q8_quantize(HY_Q8_K, x, (int) k, (int) k, 1, y, s));
 }
 // src/kernels4.cuh:181 test hook

@@ -1,12 +1,14 @@
 // A C++ caller of libhymoe through include/hymoe.hpp, as the reference's engine would call it: experts uploaded from
 // GGUF-layout bytes, one decode step (moe_decode on a workspace, then moe_decode_noalloc), and one prefill step through
 // the reference-signature sequence (gemv_f32, moe_route, moe_order, q8_quantize, moe_gemm_gate_up, q8_quantize,
-// moe_gemm_down, moe_reduce).  Reads its inputs from argv[1], writes the outputs to argv[2]; the test compares them
-// with the CPU oracle.
+// moe_gemm_down, moe_reduce); and the CPU path's host quantizer q8k_test_quantize on std::vector data (src/cpu_moe.h:46,
+// called as tools/cpumoebench.cu:68 calls it).  Reads its inputs from argv[1], writes the outputs to argv[2]; the test
+// compares them with the CPU oracle.
 //
 // input:  int32 E, d, ff, k, nt_dec, nt_pre, tg, td; uint64 gb, db; gate[E gb], up[E gb], down[E db] (GGUF rows);
 //         float W_r[E][d], x_dec[nt_dec][d], x_pre[nt_pre][d]
-// output: float out_dec[nt_dec][d], out_dec_noalloc[nt_dec][d], out_pre[nt_pre][d]; int32 ids_pre[nt_pre][k]
+// output: float out_dec[nt_dec][d], out_dec_noalloc[nt_dec][d], out_pre[nt_pre][d]; int32 ids_pre[nt_pre][k];
+//         Q8_K blocks of x_pre (nt_pre d / 256 x 292 bytes, from the host quantizer)
 #include "hymoe.hpp"
 
 #include <hip/hip_runtime.h>
@@ -72,6 +74,9 @@ int main(int argc, char **argv) {
         hymoe::moe_gemm_down(m, hq, P, order, order_n, egrp, max_active, wts, y, s);
         hymoe::moe_reduce(nullptr, nullptr, y, k, op, d, ntp, ids, s);
         HIP_OK(hipStreamSynchronize(s));
+        // the host quantizer on host vectors, as the reference's quantizer test calls it
+        std::vector<uint8_t> xq_host((size_t) ntp * d / 256 * 292);
+        hymoe::q8k_test_quantize(xp.data(), xq_host.data(), (int64_t) xp.size());
 
         FILE *o = std::fopen(argv[2], "wb");
         if (!o) { std::perror(argv[2]); return 2; }
@@ -79,6 +84,7 @@ int main(int argc, char **argv) {
         const auto i = host_copy(ids, (size_t) P);
         std::fwrite(a.data(), 4, a.size(), o); std::fwrite(b.data(), 4, b.size(), o);
         std::fwrite(c.data(), 4, c.size(), o); std::fwrite(i.data(), 4, i.size(), o);
+        std::fwrite(xq_host.data(), 1, xq_host.size(), o);
         std::fclose(o);
         hymoe::free_experts(m);
         HIP_OK(hipStreamDestroy(s));

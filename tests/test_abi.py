@@ -39,7 +39,7 @@ EXPERT_TYPES = {6: (22, 32, 8), 7: (24, 32, 8), 8: (34, 32, 8), 10: (84, 256, 15
 
 def test_host_queries():
     L = lib()
-    assert L.hy_abi_version() == 1
+    assert L.hy_abi_version() == 2
     for t, (bb, be, vt) in EXPERT_TYPES.items():
         assert (L.hy_block_bytes(t), L.hy_block_elems(t), L.hy_vec_dot_type(t)) == (bb, be, vt), t
     assert L.hy_block_bytes(15) == 292 and L.hy_block_elems(15) == 256
@@ -59,7 +59,7 @@ def test_argument_errors_need_no_gpu():
         check(L.hy_moe_route(p, 128, 128, 200, p, p, None, 1, None))
     m = hy_moe_dev()
     m.gate = m.up = m.down = m.slot = 16
-    m.tg, m.td, m.ff, m.n, m.n_expert = 2, 12, 768, 2048, 128       # Q4_0 gate: no kernels for it
+    m.tg, m.td, m.ff, m.n, m.n_expert, m.n_local = 2, 12, 768, 2048, 128, 128   # Q4_0 gate: no kernels for it
     rc = L.hy_moe_gate_up(ctypes.byref(m), p, 2048, p, 8, p, 1, None, None, None)
     assert rc == hyper_amd.HY_EUNSUPPORTED_TYPE
     m.tg, m.gate_bytes = 12, 1234                                   # wrong bytes per expert matrix
@@ -72,7 +72,7 @@ def test_cpp_header_compiles(tmp_path):
     if not gxx or not Path("/opt/rocm/include/hip/hip_runtime_api.h").exists():
         pytest.skip("g++ or the HIP headers are not installed")
     src = tmp_path / "t.cpp"
-    src.write_text('#include "hymoe.hpp"\nint main() { hymoe::MoeDev m{}; (void) m; return hy_abi_version() == 1 ? 0 : 1; }\n')
+    src.write_text('#include "hymoe.hpp"\nint main() { hymoe::MoeDev m{}; (void) m; return hy_abi_version() == 2 ? 0 : 1; }\n')
     r = subprocess.run([gxx, "-std=c++17", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}",
                         "-I/opt/rocm/include", str(src)], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
@@ -100,7 +100,7 @@ def _dev(tg=12, td=14, ff=768, n=2048, E=128):
     from hyper_amd import hy_moe_dev
     m = hy_moe_dev()
     m.gate = m.up = m.down = m.slot = 16
-    m.tg, m.td, m.ff, m.n, m.n_expert = tg, td, ff, n, E
+    m.tg, m.td, m.ff, m.n, m.n_expert, m.n_local = tg, td, ff, n, E, E
     m.gate_bytes = ff * (n // 256) * {12: 144, 13: 176, 14: 210}[tg]
     m.down_bytes = n * (ff // 256) * {12: 144, 13: 176, 14: 210}[td]
     return m
@@ -191,3 +191,35 @@ def test_type_ids_agree_across_header_python_and_oracle():
             assert (block_bytes(t), block_elems(t), int(vec_dot_type(t))) == (bb, be, vt), t.name
             assert orc.BLOCK_BYTES[int(t)] == bb and orc.block_elems(t) == be and orc.vec_dot_type(t) == vt, t.name
     assert set(EXPERT_TYPES) == {int(t) for t in GType} - {15}
+
+
+def test_moe_dev_layout_matches_c(tmp_path):
+    """The ctypes hy_moe_dev has the C struct's size and field offsets (n_local included)."""
+    from hyper_amd import hy_moe_dev
+    gxx = shutil.which("g++")
+    if not gxx or not Path("/opt/rocm/include/hip/hip_runtime_api.h").exists():
+        pytest.skip("g++ or the HIP headers are not installed")
+    fields = [f for f, _ in hy_moe_dev._fields_]
+    src = tmp_path / "lay.cpp"
+    src.write_text('#include "hymoe.h"\n#include <cstddef>\n#include <cstdio>\nint main() {\n'
+                   '  std::printf("%zu", sizeof(hy_moe_dev));\n'
+                   + "".join(f'  std::printf(" %zu", offsetof(hy_moe_dev, {f}));\n' for f in fields) + "}\n")
+    exe = tmp_path / "lay"
+    r = subprocess.run([gxx, "-std=c++17", "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}", "-I/opt/rocm/include",
+                        str(src), "-o", str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [ctypes.sizeof(hy_moe_dev)] + [getattr(hy_moe_dev, f).offset for f in fields]
+    assert got == want
+
+
+def test_n_local_is_required():
+    """A descriptor without n_local (0) is refused before any launch: every slot entry is bounded by it."""
+    m = _dev()
+    m.n_local = 0
+    p = ctypes.c_void_p(16)
+    L = lib()
+    assert L.hy_moe_gate_up(ctypes.byref(m), p, 2048, p, 8, p, 1, None, None, None) == hyper_amd.HY_EINVAL
+    assert b"n_local" in L.hy_last_error()
+    assert L.hy_moe_order(ctypes.byref(m), p, 8, 128, p, p, None, p) == hyper_amd.HY_EINVAL
+    assert L.hy_moe_down_reduce(ctypes.byref(m), p, p, p, 8, None, None, p, 1, None) == hyper_amd.HY_EINVAL

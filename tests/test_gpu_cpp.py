@@ -1,7 +1,7 @@
 """A C++ program built against include/hymoe.hpp and linked with libhymoe.so (tests/cpp/moe_step, built by
 tests/cpp/Makefile) runs one decode step -- moe_decode on a workspace and moe_decode_noalloc -- and one prefill step
-through the reference-signature calls, on experts it uploads itself from GGUF-layout bytes.  Its outputs must equal the
-CPU oracle's bit for bit."""
+through the reference-signature calls, on experts it uploads itself from GGUF-layout bytes, and calls the host quantizer
+hymoe::q8k_test_quantize on std::vector data.  Its outputs must equal the CPU oracle's bit for bit."""
 import subprocess
 from pathlib import Path
 
@@ -39,7 +39,10 @@ def test_cpp_caller_matches_oracle(cuda, tmp_path, tg, td, E, d, ff, k, ntd, ntp
     raw = out.read_bytes()
     f32 = np.frombuffer(raw[: 4 * d * (2 * ntd + ntp)], np.float32)
     dec, dec_na, pre = f32[: ntd * d].reshape(ntd, d), f32[ntd * d: 2 * ntd * d].reshape(ntd, d), f32[2 * ntd * d:].reshape(ntp, d)
-    ids_pre = np.frombuffer(raw[4 * d * (2 * ntd + ntp):], np.int32).reshape(ntp, k)
+    o_ids = 4 * d * (2 * ntd + ntp)
+    ids_pre = np.frombuffer(raw[o_ids: o_ids + 4 * ntp * k], np.int32).reshape(ntp, k)
+    xq_host = np.frombuffer(raw[o_ids + 4 * ntp * k:], np.uint8).reshape(ntp * d // 256, 292)
+    assert_bits_equal(xq_host, orc.quantize(GType.Q8_K, xp).reshape(-1, 292), "q8k_test_quantize")
     OL = oracle_layer(L)
     for x, got, what in ((xd, dec, "moe_decode"), (xd, dec_na, "moe_decode_noalloc"), (xp, pre, "prefill")):
         ids, wts, _ = orc.route(orc.gemv_f32(W, x), E, k)

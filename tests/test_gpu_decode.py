@@ -212,6 +212,64 @@ def test_decode_skips_non_local_experts(cuda):
     assert_bits_equal(out.cpu().numpy(), out_r, "out")
 
 
+def test_slot_entries_outside_n_local_are_absent(cuda):
+    """A slot-table entry outside [0, n_local) (a stale or corrupt table) makes its expert absent in every kernel
+    that reads the table -- routed gate/up, down + combine, the separate gate/up and down GEMVs, the fused GEMV down
+    + combine and the bucketing -- instead of forming a weight address past the allocation."""
+    tg = td = GType.Q4_K
+    E, d, ff, k, nt = 12, 2048, 512, 4, 3
+    L = layer(tg, td, E, ff, d, seed=740)
+    dev = moe.upload_experts(L, device=cuda)
+    assert dev.c.n_local == E
+    bad = {1: E, 4: E + 1000, 6: 1 << 30, 9: -5}
+    for e, v in bad.items():
+        dev.slot[e] = v
+    torch.cuda.synchronize()
+    lg = _logits(E, nt, False, 741)
+    ids_r, wts_r, _ = orc.route(lg, E, k)
+    local = np.array([e not in bad for e in ids_r.reshape(-1)]).reshape(ids_r.shape)
+    assert not local.all(), "the case must route some pairs to the corrupted entries"
+    ids_cpu = np.where(local, ids_r, -1).astype(np.int32)
+    x = torch.randn(nt, d, generator=gen(742))
+    out_r, h_r, _ = orc.moe_layer(oracle_layer(L), x.numpy(), ids_cpu, wts_r, want_hy=True)
+    xq = torch.from_numpy(orc.quantize(GType.Q8_K, x.numpy())).reshape(-1).to(cuda)
+    ids = torch.zeros(nt * k, dtype=torch.int32, device=cuda)
+    wts = torch.zeros(nt * k, device=cuda)
+    h = torch.full((nt * k, ff), float("nan"), device=cuda)
+    out = torch.zeros(nt, d, device=cuda)
+    moe.moe_route_gate_up(dev, torch.from_numpy(lg).to(cuda), E, E, k, xq, ids, wts, None, h, nt)
+    moe.moe_down_reduce(dev, h, ids, wts, k, None, None, out, nt)
+    torch.cuda.synchronize()
+    lv = local.reshape(-1)
+    hv = h.cpu().numpy()
+    assert_bits_equal(hv[lv], h_r[lv], "h of local pairs")
+    assert np.isnan(hv[~lv]).all()
+    assert_bits_equal(out.cpu().numpy(), out_r, "out (route + gate/up, down + combine)")
+    # the reference-signature GEMVs on the same routing
+    xd = x.to(cuda)
+    h2 = torch.full((nt * k, ff), float("nan"), device=cuda)
+    y2 = torch.full((nt * k, d), float("nan"), device=cuda)
+    moe.moe_gate_up(dev, xd, d, ids, k, h2, nt)
+    moe.moe_down(dev, h2, ids, wts, k, y2, nt)
+    torch.cuda.synchronize()
+    assert_bits_equal(h2.cpu().numpy()[lv], h_r[lv], "moe_gate_up h of local pairs")
+    assert np.isnan(h2.cpu().numpy()[~lv]).all()
+    assert (y2.cpu().numpy()[~lv] == 0).all(), "moe_down writes zeros for pairs without a local expert"
+    # bucketing drops the corrupted experts' pairs
+    P = nt * k
+    order = torch.full((P,), -7, dtype=torch.int32, device=cuda)
+    order_n = torch.zeros(2, dtype=torch.int32, device=cuda)
+    egrp = torch.zeros(3 * E, dtype=torch.int32, device=cuda)
+    moe.moe_order(dev, ids, P, E, order, order_n, egrp=egrp)
+    torch.cuda.synchronize()
+    slot_eff = np.array([-1 if e in bad else e for e in range(E)], np.int32)
+    o_r, on_r, eg_r = orc.order(slot_eff, ids_r.reshape(-1).astype(np.int32), E)
+    on = order_n.cpu().numpy()
+    assert_bits_equal(on, on_r, "order_n")
+    assert_bits_equal(order.cpu().numpy()[:on[0]], o_r, "order")
+    assert_bits_equal(egrp.cpu().numpy()[:3 * on[1]].reshape(-1, 3), eg_r, "egrp")
+
+
 RUNNER_CASES = [
     # tg, td, E, d, ff, k, nt, shared (type or None), sg_logit
     (GType.Q4_K, GType.Q4_K, 128, 2048, 768, 8, 1, None, False),

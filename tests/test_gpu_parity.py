@@ -147,7 +147,7 @@ def test_order_bitexact(cuda, E, P, absent, skew):
     from hyper_amd import hy_moe_dev
     import ctypes
     sl = torch.from_numpy(slot).to(cuda)
-    c = hy_moe_dev(); c.slot = sl.data_ptr(); c.n_expert = E
+    c = hy_moe_dev(); c.slot = sl.data_ptr(); c.n_expert = E; c.n_local = E
     dev.c, dev.ref, dev.slot = c, ctypes.byref(c), sl
     order = torch.full((max(P, 1),), -7, dtype=torch.int32, device=cuda)
     order_n = torch.zeros(2, dtype=torch.int32, device=cuda)
