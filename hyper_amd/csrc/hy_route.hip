@@ -468,8 +468,8 @@ int launch_router_pre(const uint16_t *W, int rows, int kdim, const float *x, int
 }
 
 // ---------------------------------------------------------------- routing (A2)
-// A token per block: up to 128 experts by eight waves (route_rank8), more by one wave (route_wave); both give the
-// bits of src/kernels4.cu:297-344's contract (hy_routing.cuh).
+// A token per block: up to 128 experts by eight waves (route_rank8), more by one wave (route_wave: wave_topk);
+// both give the bits of src/kernels4.cu:297-344's contract (hy_routing.cuh).
 template <int V>
 __global__ __launch_bounds__(512) void k_route8(const float *__restrict__ logits, int ls, int ne, int k, int *__restrict__ ids,
                                                 float *__restrict__ wts, float *__restrict__ sg) {
@@ -503,57 +503,34 @@ int launch_route(const float *logits, int ls, int ne, int k, int *ids, float *wt
 
 // Routers with a selection bias (one wave per token): score s_e from the logit -- MODE 0: sigmoid, the contract of
 // k_moe_route_sig (src/kernels5.cu:1090-1122); MODE 1: sqrt(softplus), the contract of k_route7 (src/kernels7.cu:
-// 816-865) -- then the top k of s_e + bias[e] (ties to the lower index) by k rounds of wave argmax over each lane's
-// sorted candidates, as route_wave; the weights use the scores alone, summed in selection order:
-// MODE 0: s scale / max(sum, 2^-14) (and sg = 1); MODE 1: s / (sum + 1e-20) scale.
+// 816-865) -- then the top k of s_e + bias[e] (ties to the lower index) by wave_topk, the scores riding along; the
+// weights use the scores alone, summed in selection order: MODE 0: s scale / max(sum, 2^-14) (and sg = 1);
+// MODE 1: s / (sum + 1e-20) scale.
 template <int V, int MODE>
 __global__ __launch_bounds__(64) void k_route_bias(const float *__restrict__ logits, int ls, const float *__restrict__ bias, int ne, int k,
                                                    float scale, int *__restrict__ ids, float *__restrict__ wts, float *__restrict__ sg) {
     const int t = blockIdx.x, lane = threadIdx.x;
     const float *l = logits + (size_t) t * ls;
-    float key[V], val[V];
-    int vi[V];
+    float key[V], score[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) {
         const int e = lane + 64 * i;
+        score[i] = 0.0f;
+        key[i] = 0.0f;
         if (e < ne) {
             const float x = l[e];
-            val[i] = MODE == 0 ? hy_sigmoid(x) : hy_sqrt_softplus(x);
-            key[i] = val[i] + bias[e];
-            vi[i] = e;
-        } else {
-            key[i] = -__builtin_huge_valf();
-            val[i] = 0.0f;
-            vi[i] = 0x7fffffff;
+            score[i] = MODE == 0 ? hy_sigmoid(x) : hy_sqrt_softplus(x);
+            key[i] = score[i] + bias[e];
         }
     }
-#pragma unroll
-    for (int i = 1; i < V; ++i)
-#pragma unroll
-        for (int j = i; j > 0; --j)
-            if (rt_better2(key[j], vi[j], key[j - 1], vi[j - 1])) {
-                const float tk = key[j]; key[j] = key[j - 1]; key[j - 1] = tk;
-                const float tv = val[j]; val[j] = val[j - 1]; val[j - 1] = tv;
-                const int ti = vi[j]; vi[j] = vi[j - 1]; vi[j - 1] = ti;
-            }
-    float tot = 0.0f, selv = 0.0f;
-    int seli = 0;
-    for (int j = 0; j < k; ++j) {
-        float bk = key[0];
-        int bi = vi[0];
-        wave_best(bk, bi, rt_better2);
-        const float bv = readlane_f(val[0], bi & 63);   // the winner heads its lane's (sorted) list
-        tot = tot + bv;
-        if (lane == j) { selv = bv; seli = bi; }
-        if (vi[0] == bi) {
-#pragma unroll
-            for (int i = 0; i < V - 1; ++i) { key[i] = key[i + 1]; val[i] = val[i + 1]; vi[i] = vi[i + 1]; }
-            key[V - 1] = -__builtin_huge_valf(); val[V - 1] = 0.0f; vi[V - 1] = 0x7fffffff;
-        }
-    }
+    int e_r;
+    float s_r;
+    wave_topk<V>(key, score, ne, k, e_r, s_r);
+    float tot = 0.0f;
+    for (int r = 0; r < k; ++r) tot = tot + readlane_f(s_r, r);
     if (lane < k) {
-        ids[(size_t) t * k + lane] = seli;
-        wts[(size_t) t * k + lane] = MODE == 0 ? selv * (scale / fmaxf(tot, 6.103515625e-5f)) : selv / (tot + 1e-20f) * scale;
+        ids[(size_t) t * k + lane] = e_r;
+        wts[(size_t) t * k + lane] = MODE == 0 ? s_r * (scale / fmaxf(tot, 6.103515625e-5f)) : s_r / (tot + 1e-20f) * scale;
     }
     if (MODE == 0 && sg && lane == 0) sg[t] = 1.0f;
 }
