@@ -94,6 +94,7 @@ SIGNATURES = {
     "hy_moe_route_gate_up": (_I, [_DEV, _P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
     "hy_moe_route_gate_up_q8": (_I, [_DEV, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P]),
     "hy_moe_shared_gate_up": (_I, [_DEV, _P, _P, _I, _P]),
+    "hy_moe_shared_down": (_I, [_DEV, _P, _P, _I, _P]),
     "hy_moe_down_reduce_q8": (_I, [_DEV, _P, _P, _P, _I, _P, _P, _P, _I, _I, _P]),
     "hy_moe_decode_ws_bytes": (ctypes.c_size_t, [_DEV, _I, _I, _DEV, _I]),
     "hy_moe_decode": (_I, [_DEV, _P, _I, _P, _I, _P, _I, _I, _DEV, _P, _I, _I, _P, ctypes.c_size_t, _P]),

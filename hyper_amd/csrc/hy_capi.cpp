@@ -372,7 +372,8 @@ int hy_moe_shared_gate_up(const hy_moe_dev *m, const void *xq, float *h, int nt,
     if (rc) return rc;
     if (!xq || !h || nt < 0) { set_error("hy_moe_shared_gate_up: bad argument"); return HY_EINVAL; }
     if ((uintptr_t) xq & 3) { set_error("hy_moe_shared_gate_up: xq must be 4-byte aligned"); return HY_EBAD_SHAPE; }
-    return launch_fixed_gate_up(*m, xq, h, nt, s);
+    rc = launch_shared_gate_up(*m, xq, h, nt, s);   // 2..8 tokens: a pass over the weights for every 4
+    return rc == HY_EUNSUPPORTED_TYPE ? launch_fixed_gate_up(*m, xq, h, nt, s) : rc;
 }
 
 int hy_moe_route_gate_up_q8(const hy_moe_dev *m, const float *logits, int ls, int n_expert, int k, const void *xq, int32_t *ids,

@@ -386,7 +386,9 @@ constexpr int DEC_DN_HQ = 32768;      // LDS bytes for the token's k quantized h
 #endif
 constexpr int DEC_DN_BLOCKS = HY_DEC_DN_BLOCKS;   // grid size the rows per wave aim below
 
-template <int T, int NP>
+// SEP: one expert's rows for several tokens (the shared expert; pair j = token j, ids 0, weights 1): each pair's value
+// is written as its own output row, with no combine.
+template <int T, int NP, bool SEP = false>
 __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, const float *__restrict__ h, const int *__restrict__ ids,
                                                                const float *__restrict__ wts, int k, const float *__restrict__ shexp,
                                                                const float *__restrict__ sg, float *__restrict__ out, int res, int q8, int r8,
@@ -568,6 +570,15 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
             }
             fo = my_w * acc;
         }
+        if constexpr (SEP) {   // pair j's value is output row j
+            if (mine) out[(size_t) lane * n + row] = fo;
+            if (++rr == rpw || ++row >= n) break;   // wave-uniform
+            lc.start(g, ng);
+            cc.start(g, ng);
+            wave_lds_sync();
+            load_round(0);
+            continue;
+        }
         // the combine in rank order, each value read from the lane that holds it
         const int nv = __builtin_popcountll(okm);
         float acc = 0.0f;
@@ -588,6 +599,108 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     }
     HY_STAMP(5);
     HY_STAMP_SAVE(32768 + 8 * (int) (blockIdx.y * gridDim.x + blockIdx.x), 6, wave == 0 && lane == 0 && blockIdx.y * gridDim.x + blockIdx.x < 4095, true);
+}
+
+// ---------------------------------------------------------------- shared expert, several tokens
+
+// The always-on expert (the descriptor's local expert 0) for 2..SH_MAX tokens: a block takes up to SH_NT of them,
+// stages their Q8 rows in LDS, and each wave loads its rows' gate and up items once and takes their integers against
+// every staged row; one lane a (row, token) folds the blocks in order -- the expressions of k_route_gate_up with
+// V = 0 (the one-token form), so the bits are those.  SH_NT rows keep the block's LDS small enough for two blocks a
+// CU next to the routed experts' kernels (the shared expert runs beside them on a second stream).
+constexpr int SH_NT = 4;          // tokens a block takes (grid.y: token groups)
+constexpr int SH_MAX = 8;         // tokens a launch takes
+constexpr int SH_TV = 4096;       // fold inputs a block holds: tokens x rows x (2 nb + 1)
+constexpr int SH_LD = 16;         // staging loads in flight a thread
+
+template <int T, int NP>
+__global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_shared_gate_up(hy_moe_dev m, const uint8_t *__restrict__ xq, float *__restrict__ h,
+                                                                    int nt, int rw, int q8, int r8) {
+    constexpr int VT = vec_dot_type(T), BE = block_elems(T);
+    constexpr int SPAN_W = 256 / BE * block_bytes(T);
+    constexpr int SPAN_Y = VT == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
+    __shared__ __align__(16) uint8_t s_y[SH_NT * DEC_Y_BYTES];   // token t's row at t * ybytes, laid out as k_route_gate_up's
+    __shared__ float s_xd[SH_NT * (DEC_GU_TV / 2)];             // token t's activation scales at t * nb
+    __shared__ float tv[SH_TV];
+    __shared__ uint2 grid[iq2_lds(T)];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7, tid = threadIdx.x;
+    const int ff = m.ff, ng = m.n / 256, nb = m.n / BE, RB = DEC_GU_WAVES * rw, rs = 2 * nb + 1;
+    const int ny = VT == Q8_K ? ng * (Q8K_BYTES / 4) : nb * 8, ybytes = 4 * ny;
+    const int t0 = blockIdx.y * SH_NT, ntb = min(SH_NT, nt - t0);   // this block's tokens
+    xq += (size_t) t0 * ng * SPAN_Y;
+    h += (size_t) t0 * ff;
+    // the tokens' rows into LDS, SH_LD dwords a thread in flight at once
+    for (int i0 = tid; i0 < ntb * ny; i0 += SH_LD * 64 * DEC_GU_WAVES) {
+        uint32_t v[SH_LD];
+#pragma unroll
+        for (int u = 0; u < SH_LD; ++u) {
+            const int i = i0 + u * 64 * DEC_GU_WAVES, t = i / ny, w = i - t * ny;
+            v[u] = 0;
+            if (i < ntb * ny) {
+                const uint8_t *y = xq + (size_t) t * ng * SPAN_Y;
+                if constexpr (VT == Q8_K) v[u] = ((const uint32_t *) y)[w];
+                else {   // qs dword w & 7 of block w >> 3: 2-byte aligned in the row
+                    const uint8_t *q = y + (size_t) (w >> 3) * Q8_0_BYTES + 2 + 4 * (w & 7);
+                    v[u] = (uint32_t) ld_u16(q) | ((uint32_t) ld_u16(q + 2) << 16);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SH_LD; ++u) {
+            const int i = i0 + u * 64 * DEC_GU_WAVES, t = i / ny;
+            if (i < ntb * ny) ((uint32_t *) (s_y + (size_t) t * ybytes))[i - t * ny] = v[u];
+        }
+    }
+    for (int i = tid; i < ntb * nb; i += 64 * DEC_GU_WAVES) {
+        const int t = i / nb;
+        s_xd[t * nb + (i - t * nb)] = q8_scale<VT>(xq + (size_t) t * ng * SPAN_Y, i - t * nb);
+    }
+    if constexpr (iq2_type(T)) expand_iq2_grid<T>(grid);
+    const int slot = bound_slot(m.slot[0], m.n_local);
+    lds_barrier();
+    if (slot < 0) return;   // uniform: the expert is not local, h is not written
+    const int npos = rw * ng, row0 = (blockIdx.x * DEC_GU_WAVES + wave) * rw;
+    const uint8_t *Wg = m.gate + (size_t) slot * m.gate_bytes, *Wu = m.up + (size_t) slot * m.gate_bytes;
+    Cursor lc, cc;
+    lc.start(g, ng);
+    cc.start(g, ng);
+    Item<T> ig[NP], iu[NP];
+    for (int base = 0; base < npos; base += 8 * NP) {   // wave-uniform rounds of up to 8 NP positions
+#pragma unroll
+        for (int ps = 0; ps < NP; ++ps) {
+            if (lc.u < rw && row0 + lc.u < ff) {
+                const uint32_t off = tiled_off32(row0 + lc.u, lc.s, ng, SPAN_W);
+                ig[ps].load(Wg + off, L);
+                iu[ps].load(Wu + off, L);
+            }
+            lc.next(ng, q8, r8);
+        }
+#pragma unroll
+        for (int ps = 0; ps < NP; ++ps) {
+            if (base + 8 * ps >= npos) break;   // wave-uniform
+            const int r = cc.u, gi = cc.s, blk = BE == 32 ? 8 * gi : gi;
+            const bool valid = r < rw && row0 + r < ff;
+            if constexpr (iq2_type(T)) { ig[ps].grid = grid; iu[ps].grid = grid; }
+            const int rr = wave * rw + r;
+#pragma unroll
+            for (int t = 0; t < SH_NT; ++t) {
+                if (t >= ntb) break;   // uniform
+                const uint8_t *yt = s_y + (size_t) t * ybytes;
+                item_t<T>(ig[ps], yt, gi, L, valid, tv, (t * RB + rr) * rs + blk);
+                item_t<T>(iu[ps], yt, gi, L, valid, tv, (t * RB + rr) * rs + nb + blk);
+            }
+            cc.next(ng, q8, r8);
+        }
+    }
+    lds_barrier();
+    // lane (t, rr) folds row rr of the block for token t: gate and up chains side by side
+    const int t = tid / RB, rr = tid - t * RB, row = blockIdx.x * RB + rr;
+    if (t >= ntb || row >= ff) return;
+    const float *tg = tv + (t * RB + rr) * rs;
+    const float *xd = s_xd + t * nb;
+    float a[2] = {0.0f, 0.0f};
+    fold_blocks(nb, [&](int b) { return xd[b]; }, [&](int c, int b) { return tg[c * nb + b]; }, a);
+    h[(size_t) t * ff + row] = hy_swiglu(a[0], a[1], m.clamp);
 }
 
 // ---------------------------------------------------------------- launchers
@@ -699,6 +812,31 @@ int launch_fixed_gate_up(const hy_moe_dev &m, const void *xq, float *h, int nt, 
 #undef HY_FGU
 }
 
+// the shared expert's gate/up for 2..SH_MAX tokens, one pass over its weights for every SH_NT (k_shared_gate_up); HY_EUNSUPPORTED_TYPE
+// when the tokens' rows or fold inputs exceed its LDS (the caller then takes launch_fixed_gate_up)
+int launch_shared_gate_up(const hy_moe_dev &m, const void *xq, float *h, int nt, hipStream_t s) {
+    const int ng = m.n / 256, nb = m.n / block_elems(m.tg);
+    const int ybytes = vec_dot_type(m.tg) == Q8_K ? ng * Q8K_BYTES : nb * 32;
+    const int ntb = std::min(nt, SH_NT);   // tokens a block holds
+    if (nt < 2 || nt > SH_MAX || ybytes > DEC_Y_BYTES || 2 * nb > DEC_GU_TV || 2 * ng > 8 * DEC_MAXP ||
+        (long) ntb * DEC_GU_WAVES * (2 * nb + 1) > SH_TV || m.gate_bytes >= ((size_t) 1 << 32))
+        return HY_EUNSUPPORTED_TYPE;
+    // rows per wave: blocks enough for every CU (one row a wave when ff allows), within the fold inputs
+    const int groups = (nt + SH_NT - 1) / SH_NT;
+    int rw = 1;
+    while (rw < 4 && (long) ((m.ff + DEC_GU_WAVES * (rw + 1) - 1) / (DEC_GU_WAVES * (rw + 1))) * groups >= 256 &&
+           (long) ntb * DEC_GU_WAVES * (rw + 1) * (2 * nb + 1) <= SH_TV)
+        ++rw;
+    dim3 grid((m.ff + DEC_GU_WAVES * rw - 1) / (DEC_GU_WAVES * rw), groups);
+    const int np = (rw * ng + 7) / 8, q8 = 8 / ng, r8 = 8 % ng;
+#define HY_SGU(NN) hipLaunchKernelGGL((k_shared_gate_up<TT, NN>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, (const uint8_t *) xq, h, nt, rw, q8, r8)
+    HY_DEC_SWITCH(m.tg, {
+        if (np <= 1) HY_SGU(1); else if (np <= 2) HY_SGU(2); else HY_SGU(4);
+        return check_launch("hy_moe_shared_gate_up");
+    });
+#undef HY_SGU
+}
+
 static bool dec_down_fits(const hy_moe_dev &m, int k) {
     const int vt = vec_dot_type(m.td), ng = m.ff / 256, nb = m.ff / block_elems(m.td);
     const int span_y = vt == Q8_K ? Q8K_BYTES : 8 * Q8_0_BYTES;
@@ -732,6 +870,25 @@ int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const f
         return check_launch("hy_moe_down_reduce");
     });
 #undef HY_DN
+}
+
+// the shared expert's down for nt tokens in one pass over its weights: k_dec_down with the tokens as its k pairs
+// (ids all 0, weights all 1) and one output row per pair; HY_EUNSUPPORTED_TYPE beyond its LDS budget
+int launch_shared_down(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, float *out, int nt, hipStream_t s) {
+    if (nt < 2 || !dec_down_fits(m, nt)) return HY_EUNSUPPORTED_TYPE;
+    const int ng = m.ff / 256;
+    int rpw = 1;
+    while (rpw < 4 && (m.n + DEC_DN_WAVES * rpw - 1) / (DEC_DN_WAVES * rpw) > DEC_DN_BLOCKS) ++rpw;
+    dim3 grid((m.n + DEC_DN_WAVES * rpw - 1) / (DEC_DN_WAVES * rpw), 1);
+    const int np = (nt * ng + 7) / 8, q8 = 8 / ng, r8 = 8 % ng;
+#define HY_SDN(NN) hipLaunchKernelGGL((k_dec_down<TT, NN, true>), grid, dim3(64 * DEC_DN_WAVES), 0, s, m, h, ids, wts, nt, nullptr, nullptr, out, 0, q8, r8, nullptr, rpw)
+    HY_DEC_SWITCH(m.td, {
+        if (np <= 2) HY_SDN(2);
+        else if constexpr (TT != IQ2_XS) HY_SDN(4);
+        else if (np <= 4) HY_SDN(4); else HY_SDN(8);
+        return check_launch("hy_moe_shared_down");
+    });
+#undef HY_SDN
 }
 
 } // namespace hy

@@ -47,6 +47,11 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
                          float *h, int nt, hipStream_t s, uint8_t *hq = nullptr);
 // SwiGLU(gate, up) of the descriptor's local expert 0 for nt Q8 rows (a shared expert's decode gate/up, no routing)
 int launch_fixed_gate_up(const hy_moe_dev &m, const void *xq, float *h, int nt, hipStream_t s);
+// the same for 2..8 tokens in one pass over the weights; HY_EUNSUPPORTED_TYPE outside its limits (use the one above)
+int launch_shared_gate_up(const hy_moe_dev &m, const void *xq, float *h, int nt, hipStream_t s);
+// the shared expert's down for 2 or more tokens in one pass over the weights: out[t] = down . q8(h[t]) (ids all 0 and
+// wts all 1, nt entries each); HY_EUNSUPPORTED_TYPE outside its limits (use launch_dec_down with k = 1)
+int launch_shared_down(const hy_moe_dev &m, const float *h, const int *ids, const float *wts, float *out, int nt, hipStream_t s);
 // whether launch_dec_down runs its fused kernel (not HY_EUNSUPPORTED_TYPE) for this layer and k
 bool dec_down_takes_q8(const hy_moe_dev &m, int k);
 // hq: the hidden as Q8_0 rows (from launch_route_gate_up) instead of h

@@ -40,6 +40,15 @@ static int shared_tables(SharedTables &out) {
     return HY_OK;
 }
 
+// the shared expert's down for nt tokens: one pass over its weights for 2 or more tokens, else (or beyond that
+// kernel's limits) the fused down with k = 1, else the R-row kernel
+static int shared_down(const hy_moe_dev &S, const float *sh_h, const SharedTables &T, float *shexp, int nt, hipStream_t s) {
+    int rc = launch_shared_down(S, sh_h, T.ids, T.wts, shexp, nt, s);
+    if (rc == HY_EUNSUPPORTED_TYPE) rc = launch_dec_down(S, sh_h, T.ids, T.wts, 1, nullptr, nullptr, shexp, nt, s);
+    if (rc == HY_EUNSUPPORTED_TYPE) rc = launch_down_reduce(S, sh_h, T.ids, T.wts, 1, nullptr, nullptr, shexp, nt, s);
+    return rc;
+}
+
 // workspace layout: each piece 256-byte aligned
 struct DecodeLayout {
     size_t logits, ids, wts, sg, xq, h, hq, sh_h, sh_y, total;
@@ -97,11 +106,14 @@ int run_decode(const hy_moe_dev &m, const float *W_r, int rows, const float *x, 
         float *sh_h = (float *) (ws + L.sh_h);
         shexp = (float *) (ws + L.sh_y);
         // from the Q8 rows of x when the shared expert's gate type takes the same activation type, else from x
-        if (vec_dot_type(S->tg) == vec_dot_type(m.tg)) rc = launch_fixed_gate_up(*S, xq, sh_h, nt, s);
-        else rc = launch_gate_up(*S, x, xs, T.ids, 1, sh_h, nt, s, nullptr, nullptr);
+        if (vec_dot_type(S->tg) == vec_dot_type(m.tg)) {
+            rc = launch_shared_gate_up(*S, xq, sh_h, nt, s);   // several tokens: one pass over the weights
+            if (rc == HY_EUNSUPPORTED_TYPE) rc = launch_fixed_gate_up(*S, xq, sh_h, nt, s);
+        } else {
+            rc = launch_gate_up(*S, x, xs, T.ids, 1, sh_h, nt, s, nullptr, nullptr);
+        }
         if (rc) return rc;
-        rc = launch_dec_down(*S, sh_h, T.ids, T.wts, 1, nullptr, nullptr, shexp, nt, s);
-        if (rc == HY_EUNSUPPORTED_TYPE) rc = launch_down_reduce(*S, sh_h, T.ids, T.wts, 1, nullptr, nullptr, shexp, nt, s);
+        rc = shared_down(*S, sh_h, T, shexp, nt, s);
         if (rc) return rc;
     }
     // down types with a Q8_0 partner: gate/up also writes the hidden as Q8_0 rows, which the down kernel reads (shapes
@@ -151,6 +163,16 @@ static int scratch_ptr(uint8_t *&out) {
 using namespace hy;
 
 extern "C" {
+
+int hy_moe_shared_down(const hy_moe_dev *m, const float *h, float *out, int nt, hipStream_t s) {
+    int rc = check_dev_decode(m, nullptr, "hy_moe_shared_down");
+    if (rc) return rc;
+    if (!h || !out || nt < 0 || nt > DECODE_MAX_ROWS) { set_error("hy_moe_shared_down: bad argument (nt %d, at most %d)", nt, DECODE_MAX_ROWS); return HY_EINVAL; }
+    if (nt == 0) return HY_OK;
+    SharedTables T;
+    if ((rc = shared_tables(T))) return rc;
+    return shared_down(*m, h, T, out, nt, s);
+}
 
 size_t hy_moe_decode_ws_bytes(const hy_moe_dev *m, int rows, int k, const hy_moe_dev *shared, int nt) {
     if (!m || nt < 0 || k <= 0 || rows <= 0) return 0;

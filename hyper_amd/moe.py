@@ -193,6 +193,11 @@ def moe_shared_gate_up(m: MoeDev, xq, h, nt, stream=None):
     check(lib().hy_moe_shared_gate_up(m.ref, _p(xq), _p(h), nt, _s(stream)))
 
 
+def moe_shared_down(m: MoeDev, h, out, nt, stream=None):
+    """The shared expert's decode down (local expert 0, weight 1) for nt rows, each row's value alone."""
+    check(lib().hy_moe_shared_down(m.ref, _p(h), _p(out), nt, _s(stream)))
+
+
 def moe_route_gate_up_q8(m: MoeDev, logits, ls, n_expert, k, xq, ids, wts, sg, h, hq, nt, stream=None):
     """moe_route_gate_up that also writes the hidden rows as Q8_0 blocks (down types with a Q8_0 partner)."""
     check(lib().hy_moe_route_gate_up_q8(m.ref, _p(logits), ls, n_expert, k, _p(xq), _p(ids), _p(wts), _p(sg), _p(h), _p(hq), nt,
@@ -266,8 +271,10 @@ class MoeLayerRunner:
                        and self.d <= 4096 and self.k * nbh <= 512
                        and self.k * nbh * 34 <= 32768 and self.E <= 1024)
         self._side = None   # the shared expert's decode stream, made on first use
-        # decode's shared expert on a second stream: None = from 4 rows on (a one-token step is shorter in order, its
-        # launches then do not compete with the routed gate/up for CUs), True / False = always / never
+        # decode's shared expert on a second stream: None = beyond 8 rows (up to 8 rows its gate/up and down read the
+        # weights once for several rows and are shortest in order, ahead of the routed kernels: the 8-row IQ2_XS
+        # verify with a Q4_K shared expert 332 us in order against 344-347 beside them; one row runs in order as well),
+        # True / False = always / never
         self.shared_stream: Optional[bool] = None
         if shared is not None:
             S = shared.layer
@@ -304,7 +311,7 @@ class MoeLayerRunner:
             moe_shared_gate_up(S, self.xq, self.sh_h, nt, stream)
         else:
             moe_gate_up(S, x, x.stride(0), self.sh_ids, 1, self.sh_h, nt, stream)
-        moe_down_reduce(S, self.sh_h, self.sh_ids, self.sh_ones, 1, None, None, self.sh_y, nt, stream)
+        moe_shared_down(S, self.sh_h, self.sh_y, nt, stream)
 
     def _shared_decode_legacy(self, x, nt, stream):
         S = self.shared
@@ -353,7 +360,7 @@ class MoeLayerRunner:
         moe_router_q8(self.W_r, self.W_r.shape[0], self.d, x, x.stride(0), self.logits, self.ls, self.vg, self.xq, nt, stream,
                       bias=bias, bias_stride=0 if bias is None else bias.stride(0))
         shexp, joined = None, None
-        side = self.shared_stream if self.shared_stream is not None else nt >= 4
+        side = self.shared_stream if self.shared_stream is not None else nt > 8
         if self.shared is not None and not side:
             self._shared_decode(x, nt, stream)
             shexp = self.sh_y

@@ -231,7 +231,8 @@ int hy_moe_route_gate_up(const hy_moe_dev *m, const float *logits, int ls, int n
 
 /* Decode gate/up of the always-on (shared) expert: h[t] = SwiGLU(gate . x_t, up . x_t) of the descriptor's local
    expert 0 for nt tokens, from their Q8 rows xq (partner type of the gate type), as hy_moe_gate_up with every id 0
-   and k = 1 computes it from x (the reference's shared-expert call of moe_gate_up, src/engine4.cu:795-804). */
+   and k = 1 computes it from x (the reference's shared-expert call of moe_gate_up, src/engine4.cu:795-804).  From 2 to 8
+   tokens, one pass over the weights serves up to 4 tokens. */
 int hy_moe_shared_gate_up(const hy_moe_dev *m, const void *xq, float *h, int nt, hipStream_t s);
 
 /* hy_moe_route_gate_up that also writes hq: the pairs' hidden rows as Q8_0 blocks (the values and scales
@@ -246,6 +247,12 @@ int hy_moe_route_gate_up_q8(const hy_moe_dev *m, const float *logits, int ls, in
    16-byte aligned); bit-identical to them on the h the blocks came from.  HY_EUNSUPPORTED_TYPE for other down types. */
 int hy_moe_down_reduce_q8(const hy_moe_dev *m, const void *hq, const int32_t *ids, const float *wts, int k, const float *shexp,
                           const float *sg, float *out, int residual, int nt, hipStream_t s);
+
+/* The shared (always-on) expert's decode down for nt <= 64 rows: out[t][r] = down_0[r] . q8(h[t]) -- moe_down of a
+   k = 1 layer whose pairs are all its local expert 0 with weight 1 (src/engine4.cu:795-804's mm(L.sh_down)), each
+   row's value alone (no combine).  From 2 rows on one pass over the weights serves every row.  Bit-identical to
+   hy_moe_down_reduce(m, h, ids = 0, wts = 1, k = 1, NULL, NULL, out, nt). */
+int hy_moe_shared_down(const hy_moe_dev *m, const float *h, float *out, int nt, hipStream_t s);
 
 /* One MoE layer's decode step (nt <= 64 rows) in one call: the reference engine's per-layer sequence
    (src/engine4.cu:807-890 -- gemv_f32, moe_route, moe_gate_up, moe_down, moe_reduce -- and the shared expert of

@@ -378,19 +378,37 @@ def test_runner_decode_shared_graph_replays(cuda, side):
         assert_bits_equal(one.cpu().numpy(), ref(xs[1 - i][:1]), f"eager one-row step {rep}")
 
 
-@pytest.mark.parametrize("tg,d,ff,nt", [(GType.Q4_K, 7168, 2048, 1), (GType.Q5_K, 2048, 512, 5), (GType.IQ2_XS, 7168, 2048, 8),
-                                        (GType.IQ4_NL, 4096, 1536, 2)])
-def test_shared_gate_up_bitexact(cuda, tg, d, ff, nt):
-    """hy_moe_shared_gate_up: local expert 0 for every token from the Q8 rows of x, bit for bit the oracle's h with
-    every id 0 and k = 1 (the shared expert's gate/up)."""
-    L = layer(tg, GType.Q6_K if tg != GType.IQ4_NL else GType.IQ4_NL, 1, ff, d, seed=960 + int(tg))
-    x = torch.randn(nt, d, generator=gen(961))
-    ids = np.zeros((nt, 1), dtype=np.int32)
-    wts = np.ones((nt, 1), dtype=np.float32)
-    _, h_r, _ = orc.moe_layer(oracle_layer(L), x.numpy(), ids, wts, want_hy=True)
+SHARED_CASES = [
+    # tg, td, d, ff, nt: 1 row (the per-token kernels), 2..8 rows (one pass over the weights for every row), more
+    # than 8 or beyond the one-pass kernels' LDS (the per-token kernels again)
+    (GType.Q4_K, GType.Q4_K, 7168, 2048, 1), (GType.Q4_K, GType.Q4_K, 7168, 2048, 4), (GType.Q4_K, GType.Q4_K, 7168, 2048, 8),
+    (GType.Q5_K, GType.Q6_K, 2048, 512, 5), (GType.IQ2_XS, GType.IQ2_XS, 7168, 2048, 8), (GType.IQ4_NL, GType.IQ4_NL, 4096, 1536, 2),
+    (GType.IQ4_NL, GType.IQ4_NL, 4096, 1536, 8), (GType.Q4_K, GType.Q6_K, 2048, 768, 12), (GType.IQ4_XS, GType.IQ4_XS, 4096, 1536, 3),
+    (GType.Q8_0, GType.Q8_0, 2048, 768, 6), (GType.MXFP4, GType.MXFP4, 2048, 768, 7), (GType.Q5_0, GType.Q5_1, 2048, 768, 2),
+    (GType.Q5_1, GType.Q5_0, 1024, 512, 8), (GType.Q2_K, GType.Q3_K, 2048, 1024, 4), (GType.Q3_K, GType.Q2_K, 2048, 768, 3),
+    (GType.IQ1_S, GType.IQ2_S, 7168, 2048, 5), (GType.IQ2_S, GType.IQ1_S, 2048, 768, 8), (GType.IQ3_S, GType.IQ3_XXS, 4096, 1536, 4),
+    (GType.IQ3_XXS, GType.IQ2_XXS, 2048, 768, 6), (GType.IQ2_XXS, GType.IQ3_S, 2048, 768, 2), (GType.Q6_K, GType.Q4_K, 2048, 512, 8),
+]
+
+
+@pytest.mark.parametrize("tg,td,d,ff,nt", SHARED_CASES)
+def test_shared_gate_up_and_down_bitexact(cuda, tg, td, d, ff, nt):
+    """hy_moe_shared_gate_up / hy_moe_shared_down: local expert 0 for every row from the Q8 rows of x, then its
+    down for every row, bit for bit the oracle's h and output with every id 0, weight 1 and k = 1 (the shared
+    expert), twice in a row (the second call with fewer rows)."""
+    L = layer(tg, td, 1, ff, d, seed=960 + int(tg) + nt)
     dev = moe.upload_experts(L, device=cuda)
-    xq = torch.from_numpy(orc.quantize(vec_dot_type(tg), x.numpy())).reshape(-1).to(cuda)
-    h = torch.full((nt, ff), float("nan"), device=cuda)
-    moe.moe_shared_gate_up(dev, xq, h, nt)
-    torch.cuda.synchronize()
-    assert_bits_equal(h.cpu().numpy(), h_r, "h")
+    OL = oracle_layer(L)
+    for rep, rows in enumerate((nt, max(1, nt - 3))):
+        x = torch.randn(rows, d, generator=gen(961 + rep))
+        ids = np.zeros((rows, 1), dtype=np.int32)
+        wts = np.ones((rows, 1), dtype=np.float32)
+        out_r, h_r, _ = orc.moe_layer(OL, x.numpy(), ids, wts, want_hy=True)
+        xq = torch.from_numpy(orc.quantize(vec_dot_type(tg), x.numpy())).reshape(-1).to(cuda)
+        h = torch.full((rows, ff), float("nan"), device=cuda)
+        y = torch.full((rows, d), float("nan"), device=cuda)
+        moe.moe_shared_gate_up(dev, xq, h, rows)
+        moe.moe_shared_down(dev, h, y, rows)
+        torch.cuda.synchronize()
+        assert_bits_equal(h.cpu().numpy(), h_r, f"h rep {rep}")
+        assert_bits_equal(y.cpu().numpy(), out_r, f"shared down rep {rep}")
