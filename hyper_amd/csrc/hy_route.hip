@@ -419,10 +419,172 @@ __global__ __launch_bounds__(RR_THREADS, 2) void k_router_rows(const WT *__restr
     }
 }
 
+// Router logits of many tokens on the fp32 matrix cores (v_mfma_f32_16x16x4_f32), and the Q8 rows of x, in one
+// launch.  Blocks [0, gemm_blocks) take a 64-row x 64-token tile of the first 64 gm rows: K in chunks of 32, staged
+// through LDS in two buffers (rows padded to 36 floats: the operand reads are conflict-free) with the global loads of
+// the next RT_PD chunks in registers; each wave multiplies a 32 x 32 quarter of the tile (2 x 2 MFMA tiles, each 16-
+// value step {4 q + s} of lane quarter q, component s).  Blocks [gemm_blocks, + tail_blocks) take the rows past the
+// full tiles, a wave per (row, token) logit; the rest quantize x as k_router_pre.  The sums run in the matrix cores'
+// order, not gemv_f32's fmaf chain: the logits agree with it to fp32 rounding, and the routing is defined on the
+// logits it is given.
+constexpr int RT_M = 64, RT_N = 64, RT_KC = 32, RT_LD = RT_KC + 4, RT_NW = 8;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <int VT, typename WT, int NW>
+__global__ __launch_bounds__(64 * NW) void k_router_tile(const WT *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+                                                      const float *__restrict__ bias, int bs, float *__restrict__ y, int ys, int nt,
+                                                      uint8_t *__restrict__ xq, int gm, int gemm_blocks, int tail_blocks) {
+    constexpr int TH = 64 * NW, NL = RT_M * RT_KC / 4 / TH;   // threads; float4 of A (and of B) each thread moves a chunk
+    constexpr int TJ = NW == 4 ? 2 : 1;                         // 16-token MFMA tiles a wave (2 x TJ tiles)
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    constexpr int CPR = RT_KC / 4, RS = TH / CPR;   // float4 a row and chunk; rows apart of a thread's float4
+    static_assert(RT_KC % 16 == 0 && TH % CPR == 0 && RS * NL == RT_M, "whole rows a pass");
+    __shared__ __align__(16) float As[2][RT_M * RT_LD], Bs[2][RT_N * RT_LD];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int bid = blockIdx.x;
+    if (bid >= gemm_blocks + tail_blocks) {   // the Q8 rows of x
+        const int qb = bid - gemm_blocks - tail_blocks;
+        if constexpr (VT == Q8_K) {
+            const int nb = kdim / 256, u = qb * (TH / 16) + (tid >> 4);
+            if (u >= nt * nb) return;   // uniform over the 16-lane row
+            const int t = u / nb, b = u - t * nb;
+            q8k_block16_load(x + (size_t) t * xs + 256 * b, xq + ((size_t) t * nb + b) * Q8K_BYTES);
+        } else {
+            const int nb = kdim / 32, npair = (nb + 1) / 2, u = qb * NW + wave;
+            if (u >= nt * npair) return;   // wave-uniform
+            const int t = u / npair, b = 2 * (u - t * npair);
+            q8_0_pair_wave(x + (size_t) t * xs + 32 * b, xq + ((size_t) t * nb + b) * Q8_0_BYTES, b + 1 < nb, Q8_0_BYTES, 2);
+        }
+        return;
+    }
+    if (bid >= gemm_blocks) {   // rows past the full tiles: a wave per (row, token), lane L sums values 4 L + 256 i ..
+        const int rt = rows - RT_M * gm, u = (bid - gemm_blocks) * NW + wave;
+        if (u >= rt * nt) return;   // wave-uniform
+        const int r = RT_M * gm + u % rt, t = u / rt;
+        const WT *wr = W + (size_t) r * kdim;
+        const float *xt = x + (size_t) t * xs;
+        float acc = 0.0f;
+        for (int e = 4 * lane; e < kdim; e += 256) {
+            const float4 w = ld_w4(wr + e), v = *(const float4 *) (xt + e);
+            acc = __builtin_fmaf(w.x, v.x, acc); acc = __builtin_fmaf(w.y, v.y, acc);
+            acc = __builtin_fmaf(w.z, v.z, acc); acc = __builtin_fmaf(w.w, v.w, acc);
+        }
+        float sum = wave_sum_xor(acc);
+        if (bias) sum = sum + bias[(size_t) t * bs + r];
+        if (lane == 0) y[(size_t) t * ys + r] = sum;
+        return;
+    }
+    const int r0 = (bid % gm) * RT_M, t0 = (bid / gm) * RT_N;
+    const int wm = wave & 1, wn = wave >> 1, li = lane & 15, lq = lane >> 4;   // wave: rows 32 wm .., tokens 16 TJ wn ..
+    // global -> LDS: thread tid moves float4 tid % CPR of rows tid / CPR + RS h, h < NL, of the A and B chunks
+    const int lr = tid / CPR, lc = 4 * (tid % CPR);
+    const WT *ga[NL];
+    const float *gb[NL];
+#pragma unroll
+    for (int h = 0; h < NL; ++h) {
+        ga[h] = W + (size_t) (r0 + lr + RS * h) * kdim + lc;
+        gb[h] = x + (size_t) min(t0 + lr + RS * h, nt - 1) * xs + lc;
+    }
+    const int nst = kdim / RT_KC;
+    // the ring of three chunks on their way, in named slots (arrays of constant index: they stay in registers)
+    float4 sa0[NL], sb0[NL], sa1[NL], sb1[NL], sa2[NL], sb2[NL];
+#define HY_RT_LOAD(c, SA, SB)                                                                      \
+    {                                                                                            \
+        _Pragma("unroll") for (int h = 0; h < NL; ++h) {                                         \
+            SA[h] = ld_w4(ga[h] + RT_KC * (c));                                                  \
+            SB[h] = *(const float4 *) (gb[h] + RT_KC * (c));                                     \
+        }                                                                                        \
+    }
+#define HY_RT_STORE(buf, SA, SB)                                                                   \
+    {                                                                                            \
+        _Pragma("unroll") for (int h = 0; h < NL; ++h) {                                         \
+            *(float4 *) &As[buf][(lr + RS * h) * RT_LD + lc] = SA[h];                            \
+            *(float4 *) &Bs[buf][(lr + RS * h) * RT_LD + lc] = SB[h];                            \
+        }                                                                                        \
+    }
+    f32x4 acc[2][TJ];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](int buf) {
+        const float *as = As[buf] + (32 * wm + li) * RT_LD + 4 * lq, *bsm = Bs[buf] + (16 * TJ * wn + li) * RT_LD + 4 * lq;
+#pragma unroll
+        for (int kk = 0; kk < RT_KC / 16; ++kk) {
+            f32x4 a[2], b[TJ];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) a[i] = *(const f32x4 *) (as + 16 * i * RT_LD + 16 * kk);
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) b[j] = *(const f32x4 *) (bsm + 16 * j * RT_LD + 16 * kk);
+#pragma unroll
+            for (int sc = 0; sc < 4; ++sc)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][sc], b[j][sc], acc[i][j], 0, 0, 0);
+        }
+    };
+    // chunk c sits in slot c % 3; step c computes it from buffer c & 1, stores chunk c + 1 (slot (c + 1) % 3) into the
+    // other buffer (last read in step c - 1), then loads chunk c + 4 into that slot
+    if (0 < nst) HY_RT_LOAD(0, sa0, sb0);
+    if (1 < nst) HY_RT_LOAD(1, sa1, sb1);
+    if (2 < nst) HY_RT_LOAD(2, sa2, sb2);
+    HY_RT_STORE(0, sa0, sb0);
+    if (3 < nst) HY_RT_LOAD(3, sa0, sb0);
+    __syncthreads();
+#define HY_RT_STEP(SA, SB)                                                                         \
+    {                                                                                            \
+        compute(c & 1);                                                                          \
+        if (c + 1 < nst) HY_RT_STORE((c + 1) & 1, SA, SB);                                       \
+        if (c + 4 < nst) HY_RT_LOAD(c + 4, SA, SB);                                              \
+        __syncthreads();                                                                         \
+        if (++c >= nst) break;                                                                   \
+    }
+    for (int c = 0;;) {   // uniform trip count; chunk c + 1 lies in slot (c + 1) % 3
+        HY_RT_STEP(sa1, sb1)
+        HY_RT_STEP(sa2, sb2)
+        HY_RT_STEP(sa0, sb0)
+    }
+#undef HY_RT_STEP
+#undef HY_RT_LOAD
+#undef HY_RT_STORE
+    // lane holds D[4 lq + v][li] of each 16 x 16 tile: weight row r0 + 32 wm + 16 i + 4 lq + v, token t0 + 16 (TJ wn + j) + li
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int t = t0 + 16 * (TJ * wn + j) + li;
+        if (t >= nt) continue;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r = r0 + 32 * wm + 16 * i + 4 * lq + v;
+                float sum = acc[i][j][v];
+                if (bias) sum = sum + bias[(size_t) t * bs + r];
+                y[(size_t) t * ys + r] = sum;
+            }
+    }
+}
+
+template <typename WT>
+static int router_tile_any(const WT *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
+                           int vtype, void *xq, int nt, hipStream_t s) {
+    constexpr int NW = RT_NW;
+    const int gm = rows / RT_M, gn = (nt + RT_N - 1) / RT_N, gemm_blocks = gm * gn;
+    const int tail_blocks = ((rows - RT_M * gm) * nt + NW - 1) / NW;
+    const int qblocks = vtype == Q8_K ? (nt * (kdim / 256) + 4 * NW - 1) / (4 * NW) : (nt * ((kdim / 32 + 1) / 2) + NW - 1) / NW;
+#define HY_RT(VV) hipLaunchKernelGGL((k_router_tile<VV, WT, NW>), dim3(gemm_blocks + tail_blocks + qblocks), dim3(64 * NW), 0, s, W, rows, kdim, \
+                                     x, xs, bias, bs, logits, ls, nt, (uint8_t *) xq, gm, gemm_blocks, tail_blocks)
+    if (vtype == Q8_K) HY_RT(Q8_K); else HY_RT(Q8_0);
+#undef HY_RT
+    return check_launch("hy_moe_router_q8");
+}
+
 template <typename WT>
 static int router_pre_any(const WT *W, int rows, int kdim, const float *x, int xs, const float *bias, int bs, float *logits, int ls,
                           int vtype, void *xq, int nt, hipStream_t s) {
     if (nt == 0) return HY_OK;
+    // the matrix cores when the full 64 x 64 tiles alone fill every CU (their grid: at least 256 blocks)
+    if (kdim % RT_KC == 0 && (xs & 3) == 0 && ((uintptr_t) x & 15) == 0 && (long) (rows / RT_M) * ((nt + RT_N - 1) / RT_N) >= 256)
+        return router_tile_any(W, rows, kdim, x, xs, bias, bs, logits, ls, vtype, xq, nt, s);
     {
         int dev = 0, cus = 0;
         if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;

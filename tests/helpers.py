@@ -79,3 +79,25 @@ def assert_bits_equal(a, b, what=""):
 def rel_l2(a, b) -> float:
     a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def assert_logits_close(got, W, x, bias=None, what="logits"):
+    """Router logits from the matrix cores against the oracle's fmaf chain (orc.gemv_f32): any two fp32 evaluations of
+    a d-term dot product lie within 2 d u sum|w x| of each other (u = 2^-24, the worst-case bound of recursive fp32
+    summation, twice), plus half an ulp of the bias add.  A mistake in the operand layout (a transposed or shifted
+    tile) is off by O(sum|w x|) and fails it."""
+    W = np.asarray(W, np.float32)
+    x = np.asarray(x, np.float32)
+    ref = orc.gemv_f32(W, x).astype(np.float64)
+    mag = np.abs(x.astype(np.float64)) @ np.abs(W.astype(np.float64)).T
+    bound = 2 * W.shape[1] * 2.0 ** -24 * mag
+    if bias is not None:
+        b = np.asarray(bias, np.float32)
+        ref = ref + b
+        bound = bound + np.abs(ref) * 2.0 ** -23
+    err = np.abs(np.asarray(got, np.float64) - ref)
+    bad = ~(err <= bound)
+    if bad.any():
+        i = tuple(np.argwhere(bad)[0])
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside the fp32 bound; first at {i}: {got[i]!r} vs {ref[i]!r} "
+                             f"(bound {bound[i]:.3g})")

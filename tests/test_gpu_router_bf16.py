@@ -8,7 +8,7 @@ import torch
 import oracle as orc
 from hyper_amd import moe
 from hyper_amd.formats import GType, q8_row_bytes, vec_dot_type
-from tests.helpers import assert_bits_equal, gen, layer, oracle_layer
+from tests.helpers import assert_bits_equal, assert_logits_close, gen, layer, oracle_layer
 
 pytestmark = pytest.mark.gpu
 
@@ -45,7 +45,8 @@ def test_gemv_bf16w_bitexact(cuda, rows, kdim, nt):
 # tiles; kdim 992 (not a multiple of 256): the register tiles
 @pytest.mark.parametrize("rows,kdim,nt,vt", [(129, 2048, 1, GType.Q8_K), (288, 4096, 8, GType.Q8_0), (513, 2048, 9, GType.Q8_K),
                                               (128, 2048, 40, GType.Q8_K), (513, 1024, 256, GType.Q8_0), (129, 2048, 512, GType.Q8_K),
-                                              (288, 4096, 512, GType.Q8_0), (128, 992, 20, GType.Q8_0)])
+                                              (288, 4096, 512, GType.Q8_0), (128, 992, 20, GType.Q8_0),
+                                              (577, 2048, 2048, GType.Q8_K)])   # the matrix-core router, a row past the tiles
 def test_router_q8_bf16w_bitexact(cuda, rows, kdim, nt, vt):
     W16, W32 = _bf16_weights(rows, kdim, 151 + nt)
     g = gen(152)
@@ -60,7 +61,10 @@ def test_router_q8_bf16w_bitexact(cuda, rows, kdim, nt, vt):
         moe.moe_router_q8(W.to(cuda), rows, kdim, xd, kdim, lg, rows, vt, xq, nt, bias=bd, bias_stride=rows)
         outs.append((lg, xq))
     torch.cuda.synchronize()
-    assert_bits_equal(outs[0][0].cpu().numpy(), ref, "bf16 router logits vs oracle")
+    if (rows // 64) * ((nt + 63) // 64) >= 256:   # the matrix cores' sum order: within the fp32 bound of the oracle
+        assert_logits_close(outs[0][0].cpu().numpy(), W32.numpy(), x.numpy(), bias.numpy(), "bf16 router logits vs oracle")
+    else:
+        assert_bits_equal(outs[0][0].cpu().numpy(), ref, "bf16 router logits vs oracle")
     assert_bits_equal(outs[0][0].cpu().numpy(), outs[1][0].cpu().numpy(), "bf16 vs fp32 router logits")
     assert_bits_equal(outs[0][1].cpu().numpy(), orc.quantize(vt, x.numpy()).reshape(-1), "Q8 rows of x")
 

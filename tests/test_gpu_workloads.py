@@ -2,8 +2,10 @@
 and log-normal token norms) through MoeLayerRunner on the GPU: decode / verify rows through the three-launch decode,
 longer batches through the prefill path.  The layers are generated on the device at full size; the oracle checks a
 sample of the tokens on a sub-layer holding only the experts they route to (ids remapped in ascending order, so the
-combine order is unchanged).  Logits, routing and outputs are compared bit for bit; the 2e-3 relative-L2 bound on
-fp32 expert outputs is asserted as well."""
+combine order is unchanged).  Logits are checked against the oracle's fmaf chain (bit for bit on the fmaf-chain
+routers; within the fp32 summation bound where the 2048-token chunk's router runs on the matrix cores); routing and
+outputs are then compared bit for bit to the oracle's given the GPU's logits; the 2e-3 relative-L2 bound on fp32
+expert outputs is asserted as well."""
 import numpy as np
 import pytest
 import torch
@@ -11,7 +13,7 @@ import torch
 import oracle as orc
 from hyper_amd import moe
 from hyper_amd.formats import WORKLOADS, activations, random_layer, zipf_logit_bias
-from tests.helpers import assert_bits_equal, rel_l2
+from tests.helpers import assert_bits_equal, assert_logits_close, rel_l2
 
 pytestmark = pytest.mark.gpu
 SAMPLE = 24   # tokens checked against the oracle in batches longer than that
@@ -46,11 +48,12 @@ def test_workload_full_size(cuda, name):
     rng = np.random.default_rng(seed)
     tok = np.arange(w.rows) if w.rows <= SAMPLE else np.sort(rng.choice(w.rows, SAMPLE, replace=False))
     xs = x.cpu().numpy()[tok]
-    logits = orc.gemv_f32(W_r.cpu().numpy(), xs)
-    if bias is not None:
-        logits = (logits + bias.cpu().numpy()[tok]).astype(np.float32)
-    assert_bits_equal(r.logits.cpu().numpy()[tok], logits, "logits")
-    ids, wts, _ = orc.route(logits, w.E, w.k)
+    logits = r.logits.cpu().numpy()[tok, :w.E]
+    assert_logits_close(logits, W_r.cpu().numpy(), xs, bias.cpu().numpy()[tok] if bias is not None else None)
+    if (w.E // 64) * ((w.rows + 63) // 64) < 256:   # the fmaf-chain routers: the oracle's bits
+        ref_l = orc.gemv_f32(W_r.cpu().numpy(), xs)
+        assert_bits_equal(logits, (ref_l + bias.cpu().numpy()[tok]).astype(np.float32) if bias is not None else ref_l, "logits")
+    ids, wts, _ = orc.route(logits, w.E, w.k)   # routing given the GPU's logits
     assert_bits_equal(r.ids.cpu().numpy().reshape(-1, w.k)[tok], ids, "ids")
     assert_bits_equal(r.wts.cpu().numpy().reshape(-1, w.k)[tok], wts, "wts")
     used = np.unique(ids)
@@ -80,9 +83,9 @@ def _prompt_in_chunks(w, L, S, W_r, x, g, dev, sdev, seed):
         t = tok[(tok >= j * C) & (tok < (j + 1) * C)] - j * C
         if t.size == 0:
             continue
-        logits = (orc.gemv_f32(Wh, xs_all[j * C + t]) + b.cpu().numpy()[t]).astype(np.float32)
-        assert_bits_equal(r.logits.cpu().numpy()[t], logits, f"chunk {j} logits")
-        ids, wts, _ = orc.route(logits, w.E, w.k)
+        logits = r.logits.cpu().numpy()[t, :w.E]
+        assert_logits_close(logits, Wh, xs_all[j * C + t], b.cpu().numpy()[t], f"chunk {j} logits")
+        ids, wts, _ = orc.route(logits, w.E, w.k)   # routing given the GPU's logits
         assert_bits_equal(r.ids.cpu().numpy().reshape(-1, w.k)[t], ids, f"chunk {j} ids")
         assert_bits_equal(r.wts.cpu().numpy().reshape(-1, w.k)[t], wts, f"chunk {j} wts")
         ids_all[j * C + t], wts_all[j * C + t] = ids, wts
