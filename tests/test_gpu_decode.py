@@ -11,7 +11,7 @@ import torch
 import oracle as orc
 from hyper_amd import moe
 from hyper_amd.formats import GType, q8_row_bytes, vec_dot_type
-from tests.helpers import assert_bits_equal, assert_logits_close, gen, layer, oracle_layer, rel_l2
+from tests.helpers import assert_bits_equal, assert_logits_close, gen, layer, oracle_layer, rel_l2, router_on_matrix_cores
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -23,16 +23,24 @@ TOL = 2e-3
     (288, 4096, 4, GType.Q8_0, False, False),
     (384, 7168, 8, GType.Q8_K, True, False),
     (512, 2048, 3, GType.Q8_K, True, True),
-    (64, 512, 12, GType.Q8_0, True, False),     # more than 8 rows: the separate kernels (8-token LDS tiles)
-    (512, 512, 256, GType.Q8_K, True, True),    # 17 row groups x 32 chunks: the register-row kernel, kdim 512
-    (128, 2048, 512, GType.Q8_K, False, True),  # 512 tokens x 128 experts: the register-row kernel, one chunk a block
-    (199, 2048, 333, GType.Q8_0, True, True),   # a partial row group, partial chunks and token ranges
-    (288, 4096, 512, GType.Q8_K, False, False), # kdim 4096: 16-token LDS tiles
-    (64, 544, 40, GType.Q8_0, False, True),     # d % 256 != 0: the register-tile path, an odd Q8_0 block count
-    # full 64 x 64 tiles for every CU: the matrix-core router (logits within the fp32 bound, Q8 rows bit for bit)
+    # more than 8 rows: the batched routers.  The fmaf chain (logits bit for bit) where the matrix cores' 64 x 64 tiles
+    # would leave CUs idle: LDS tiles of 8 tokens (64 x 512 x 12, 48 x 4096 x 300) or 16 (256 x 768 x 1024, 288 x 4096
+    # x 512), register tiles for d % 256 != 0 (64 x 544 x 40), register rows (513 x 512 x 256 -- 17 row groups x 32
+    # chunks --, 128 x 2048 x 512, one chunk a block, 199 x 2048 x 333, partial groups, chunks and token ranges, and
+    # 16 x 2048 x 2048 below)
+    (64, 512, 12, GType.Q8_0, True, False),
+    (48, 4096, 300, GType.Q8_0, False, True),
+    (256, 768, 1024, GType.Q8_K, True, False),
+    (64, 544, 40, GType.Q8_0, False, True),     # an odd Q8_0 block count
+    (512, 512, 256, GType.Q8_K, True, True),
+    (128, 2048, 512, GType.Q8_K, False, True),  # the 512-token batch's shape
+    (199, 2048, 333, GType.Q8_0, True, True),
+    (288, 4096, 512, GType.Q8_K, False, False),
+    # the matrix cores (logits within the fp32 bound, Q8 rows bit for bit): 64 x 64 tiles when they fill every CU
     (512, 2048, 2048, GType.Q8_K, False, True),   # the 2048-token chunk's shape, no rows past the tiles
     (512, 2048, 2040, GType.Q8_K, True, True),    # a shared-gate row past the tiles, a partial last token tile
     (600, 1024, 2048, GType.Q8_0, False, False),  # 24 rows past the tiles (a wave each), Q8_0 rows of x
+    (16, 2048, 2048, GType.Q8_K, False, True),    # too few rows for either: the register-row kernel
 ])
 def test_router_q8_bitexact(cuda, E, d, nt, vt, with_sg, with_bias):
     g = gen(1000 + E + nt)
@@ -49,7 +57,7 @@ def test_router_q8_bitexact(cuda, E, d, nt, vt, with_sg, with_bias):
     moe.moe_router_q8(W.to(cuda), rows, d, x.to(cuda), d, logits, rows, vt, xq, nt,
                       bias=bias.to(cuda) if bias is not None else None, bias_stride=rows if bias is not None else 0)
     torch.cuda.synchronize()
-    if (rows // 64) * ((nt + 63) // 64) >= 256:   # the matrix cores' sum order
+    if router_on_matrix_cores(rows, d, nt):   # the matrix cores' sum order
         assert_logits_close(logits.cpu().numpy(), W.numpy(), x.numpy(), bias.numpy() if bias is not None else None)
     else:
         assert_bits_equal(logits.cpu().numpy(), ref_log, "logits")

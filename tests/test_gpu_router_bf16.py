@@ -8,7 +8,7 @@ import torch
 import oracle as orc
 from hyper_amd import moe
 from hyper_amd.formats import GType, q8_row_bytes, vec_dot_type
-from tests.helpers import assert_bits_equal, assert_logits_close, gen, layer, oracle_layer
+from tests.helpers import assert_bits_equal, assert_logits_close, gen, layer, oracle_layer, router_on_matrix_cores
 
 pytestmark = pytest.mark.gpu
 
@@ -41,12 +41,13 @@ def test_gemv_bf16w_bitexact(cuda, rows, kdim, nt):
 
 
 # nt <= 8: the decode router (a wave per row); 9 and 40 tokens: the batched router's 8-token LDS tiles; 256 tokens x
-# 513 rows and 512 x 129: the register-row kernel (a partial row group too); 512 x 288 at kdim 4096: 16-token LDS
-# tiles; kdim 992 (not a multiple of 256): the register tiles
+# 513 rows, 512 x 129 and 2048 x 16: the register-row kernel (a partial row group too); 512 x 288 at kdim 4096: 16-token
+# LDS tiles; 2048 x 577: 64 x 64 matrix-core tiles and a row past them; kdim 992 (not a multiple of 256): the register
+# tiles
 @pytest.mark.parametrize("rows,kdim,nt,vt", [(129, 2048, 1, GType.Q8_K), (288, 4096, 8, GType.Q8_0), (513, 2048, 9, GType.Q8_K),
                                               (128, 2048, 40, GType.Q8_K), (513, 1024, 256, GType.Q8_0), (129, 2048, 512, GType.Q8_K),
                                               (288, 4096, 512, GType.Q8_0), (128, 992, 20, GType.Q8_0),
-                                              (577, 2048, 2048, GType.Q8_K)])   # the matrix-core router, a row past the tiles
+                                              (577, 2048, 2048, GType.Q8_K), (16, 2048, 2048, GType.Q8_K)])
 def test_router_q8_bf16w_bitexact(cuda, rows, kdim, nt, vt):
     W16, W32 = _bf16_weights(rows, kdim, 151 + nt)
     g = gen(152)
@@ -61,7 +62,7 @@ def test_router_q8_bf16w_bitexact(cuda, rows, kdim, nt, vt):
         moe.moe_router_q8(W.to(cuda), rows, kdim, xd, kdim, lg, rows, vt, xq, nt, bias=bd, bias_stride=rows)
         outs.append((lg, xq))
     torch.cuda.synchronize()
-    if (rows // 64) * ((nt + 63) // 64) >= 256:   # the matrix cores' sum order: within the fp32 bound of the oracle
+    if router_on_matrix_cores(rows, kdim, nt):   # the matrix cores' sum order: within the fp32 bound of the oracle
         assert_logits_close(outs[0][0].cpu().numpy(), W32.numpy(), x.numpy(), bias.numpy(), "bf16 router logits vs oracle")
     else:
         assert_bits_equal(outs[0][0].cpu().numpy(), ref, "bf16 router logits vs oracle")

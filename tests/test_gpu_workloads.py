@@ -13,7 +13,7 @@ import torch
 import oracle as orc
 from hyper_amd import moe
 from hyper_amd.formats import WORKLOADS, activations, random_layer, zipf_logit_bias
-from tests.helpers import assert_bits_equal, assert_logits_close, rel_l2
+from tests.helpers import assert_bits_equal, assert_logits_close, rel_l2, router_on_matrix_cores
 
 pytestmark = pytest.mark.gpu
 SAMPLE = 24   # tokens checked against the oracle in batches longer than that
@@ -50,7 +50,7 @@ def test_workload_full_size(cuda, name):
     xs = x.cpu().numpy()[tok]
     logits = r.logits.cpu().numpy()[tok, :w.E]
     assert_logits_close(logits, W_r.cpu().numpy(), xs, bias.cpu().numpy()[tok] if bias is not None else None)
-    if (w.E // 64) * ((w.rows + 63) // 64) < 256:   # the fmaf-chain routers: the oracle's bits
+    if not router_on_matrix_cores(w.E, w.d, w.rows):   # the fmaf-chain routers: the oracle's bits
         ref_l = orc.gemv_f32(W_r.cpu().numpy(), xs)
         assert_bits_equal(logits, (ref_l + bias.cpu().numpy()[tok]).astype(np.float32) if bias is not None else ref_l, "logits")
     ids, wts, _ = orc.route(logits, w.E, w.k)   # routing given the GPU's logits
