@@ -37,12 +37,17 @@ constexpr int DEC_MAXP = 8;        // passes of 8 items per wave: up to 64 items
 constexpr int DEC_ROUTE_NT = 8;    // tokens the fused router takes (more: the separate kernels)
 constexpr int DEC_Y_BYTES = 9344;  // LDS for one Q8 activation row: 32 Q8_K blocks (n <= 8192), or 256 Q8_0 blocks (8704 B)
 
-// Position of the items g, g + 8, g + 16, ... of a wave's flat item list, a list of units (a matrix row, or a pair's
-// row) of `per` 256-value spans each, without a division per item: advancing by 8 items moves q8 = 8 / per units and
-// r8 = 8 % per spans (both from the host), plus one unit when the span wraps.
+// Position of the items g, g + 8, g + 16, ... of a wave's flat item list, a list of units of `per` items each (gate/up:
+// a 256-value span of each of the wave's rows; down: a pair's row of spans), without a division per item: advancing by
+// 8 items moves q8 = 8 / per units and r8 = 8 % per items (both from the host), plus one unit when the item index wraps.
 struct Cursor {
     int u, s;   // unit, span in the unit
-    __device__ __forceinline__ void start(int g, int per) {
+    __device__ __forceinline__ void start(int g, int per) {   // per: uniform over the wave
+        if ((per & (per - 1)) == 0) {   // a power of two (rows per wave 1, 2, 4, 8): no loop
+            const int sh = __builtin_ctz((unsigned) per);
+            u = g >> sh; s = g & (per - 1);
+            return;
+        }
         u = 0; s = g;
         while (s >= per) { s -= per; ++u; }
     }
@@ -301,37 +306,39 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     const int slot = __builtin_amdgcn_readfirstlane((e >= 0 && e < ne) ? s_slot[e] : -1);   // block-uniform
     HY_STAMP(1);
     if (slot < 0) return;   // uniform over the block: the pair's h rows are not written
-    // the wave's rows row0 .. row0 + rw - 1: position (r, s) = row r's span s, one gate item and one up item at the
-    // same offset; lane group g takes positions g, g + 8, ... (a cursor over rows and spans); rows past ff sit out
+    // the wave's rows row0 .. row0 + rw - 1: position p = (span p / rw, row p % rw), one gate item and one up item at
+    // the same offset -- span-major, so that the rw neighbouring items of one span (adjacent bytes of a 16-row tile)
+    // are fetched in one round rather than rw rounds apart, when the cache may have let their shared lines go; lane
+    // group g takes positions g, g + 8, ... (a cursor over spans and rows); rows past ff sit out
     const int npos = rw * ng, row0 = (blockIdx.x * DEC_GU_WAVES + wave) * rw;
     const uint8_t *Wg = m.gate + (size_t) slot * m.gate_bytes, *Wu = m.up + (size_t) slot * m.gate_bytes;
     const int rs = 2 * nb + 1;
     float *tw = tv + wave * rw * rs;
     Cursor lc, cc;
-    lc.start(g, ng);
-    cc.start(g, ng);
+    lc.start(g, rw);
+    cc.start(g, rw);
     // a round: up to 8 NP positions loaded into (bg, bu) (the load cursor moves on), then their dots (the dot cursor)
     auto load_r = [&](Item<T> (&bg)[NP], Item<T> (&bu)[NP]) {
 #pragma unroll
         for (int ps = 0; ps < NP; ++ps) {
-            if (lc.u < rw && row0 + lc.u < ff) {
-                const uint32_t off = tiled_off32(row0 + lc.u, lc.s, ng, SPAN_W);
+            if (lc.u < ng && row0 + lc.s < ff) {
+                const uint32_t off = tiled_off32(row0 + lc.s, lc.u, ng, SPAN_W);
                 bg[ps].load(Wg + off, L);
                 bu[ps].load(Wu + off, L);
             }
-            lc.next(ng, q8, r8);
+            lc.next(rw, q8, r8);
         }
     };
     auto dots_r = [&](Item<T> (&bg)[NP], Item<T> (&bu)[NP], int base) {
 #pragma unroll
         for (int ps = 0; ps < NP; ++ps) {
             if (base + 8 * ps >= npos) break;   // wave-uniform
-            const int r = cc.u, gi = cc.s, blk = block_elems(T) == 32 ? 8 * gi : gi;
-            const bool valid = r < rw && row0 + r < ff;
+            const int r = cc.s, gi = cc.u, blk = block_elems(T) == 32 ? 8 * gi : gi;
+            const bool valid = gi < ng && row0 + r < ff;
             if constexpr (iq2_type(T)) { bg[ps].grid = grid; bu[ps].grid = grid; }
             item_t<T>(bg[ps], s_y, gi, L, valid, tw, r * rs + blk);
             item_t<T>(bu[ps], s_y, gi, L, valid, tw, r * rs + nb + blk);
-            cc.next(ng, q8, r8);
+            cc.next(rw, q8, r8);
         }
     };
     Item<T> ig[NP], iu[NP];
@@ -408,8 +415,10 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     const int t = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
     const int n = m.n, ff = m.ff, ng = ff / 256, nb = ff / BE, items = k * ng;
     uint16_t *hdq = (uint16_t *) (hq + (VT == Q8_K ? 0 : k * nb * 32));
-    // the wave's output rows: rpw consecutive rows, one after the other (the block's hidden rows serve them all)
-    int row = (blockIdx.x * DEC_DN_WAVES + wave) * rpw;
+    // the wave's output rows, one after the other (the block's hidden rows serve them all): row w of each of the
+    // block's rpw groups of 8 consecutive rows, so that at every step the block's waves read 8 neighbouring rows
+    // (adjacent bytes of a 16-row tile, fetched together) rather than rows rpw apart
+    int row = blockIdx.x * DEC_DN_WAVES * rpw + wave;
     bool row_ok = row < n;
     const float *hp = h + (size_t) t * k * ff;
     // Everything the block reads first goes out together: lane j < k's pair (expert, weight), the slot table and
@@ -572,7 +581,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
         }
         if constexpr (SEP) {   // pair j's value is output row j
             if (mine) out[(size_t) lane * n + row] = fo;
-            if (++rr == rpw || ++row >= n) break;   // wave-uniform
+            if (++rr == rpw || (row += DEC_DN_WAVES) >= n) break;   // wave-uniform
             lc.start(g, ng);
             cc.start(g, ng);
             wave_lds_sync();
@@ -589,7 +598,7 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
             if (first) { acc = v; first = false; } else acc = acc + v;
         }
         if (lane == 0) out[(size_t) t * n + row] = res ? out[(size_t) t * n + row] + acc : acc;   // res: the residual add
-        if (++rr == rpw || ++row >= n) break;   // wave-uniform
+        if (++rr == rpw || (row += DEC_DN_WAVES) >= n) break;   // wave-uniform
         // the next row: its shared-expert value, fresh cursors, the first round of its weight bytes
         if (shexp) sh_x = shexp[(size_t) t * n + row];
         lc.start(g, ng);
@@ -661,25 +670,25 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_shared_gate_up(hy_moe_dev
     if (slot < 0) return;   // uniform: the expert is not local, h is not written
     const int npos = rw * ng, row0 = (blockIdx.x * DEC_GU_WAVES + wave) * rw;
     const uint8_t *Wg = m.gate + (size_t) slot * m.gate_bytes, *Wu = m.up + (size_t) slot * m.gate_bytes;
-    Cursor lc, cc;
-    lc.start(g, ng);
-    cc.start(g, ng);
+    Cursor lc, cc;   // positions span-major, as in k_route_gate_up
+    lc.start(g, rw);
+    cc.start(g, rw);
     Item<T> ig[NP], iu[NP];
     for (int base = 0; base < npos; base += 8 * NP) {   // wave-uniform rounds of up to 8 NP positions
 #pragma unroll
         for (int ps = 0; ps < NP; ++ps) {
-            if (lc.u < rw && row0 + lc.u < ff) {
-                const uint32_t off = tiled_off32(row0 + lc.u, lc.s, ng, SPAN_W);
+            if (lc.u < ng && row0 + lc.s < ff) {
+                const uint32_t off = tiled_off32(row0 + lc.s, lc.u, ng, SPAN_W);
                 ig[ps].load(Wg + off, L);
                 iu[ps].load(Wu + off, L);
             }
-            lc.next(ng, q8, r8);
+            lc.next(rw, q8, r8);
         }
 #pragma unroll
         for (int ps = 0; ps < NP; ++ps) {
             if (base + 8 * ps >= npos) break;   // wave-uniform
-            const int r = cc.u, gi = cc.s, blk = BE == 32 ? 8 * gi : gi;
-            const bool valid = r < rw && row0 + r < ff;
+            const int r = cc.s, gi = cc.u, blk = BE == 32 ? 8 * gi : gi;
+            const bool valid = gi < ng && row0 + r < ff;
             if constexpr (iq2_type(T)) { ig[ps].grid = grid; iu[ps].grid = grid; }
             const int rr = wave * rw + r;
 #pragma unroll
@@ -689,7 +698,7 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_shared_gate_up(hy_moe_dev
                 item_t<T>(ig[ps], yt, gi, L, valid, tv, (t * RB + rr) * rs + blk);
                 item_t<T>(iu[ps], yt, gi, L, valid, tv, (t * RB + rr) * rs + nb + blk);
             }
-            cc.next(ng, q8, r8);
+            cc.next(rw, q8, r8);
         }
     }
     lds_barrier();
@@ -762,7 +771,7 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
             return HY_EUNSUPPORTED_TYPE;
         }
         if (nt == 0) return HY_OK;
-        const int V = (ne + 63) / 64, q8 = 8 / ng, r8 = 8 % ng;
+        const int V = (ne + 63) / 64, q8 = 8 / 4, r8 = 8 % 4;   // the position cursor's step (rw 4)
         dim3 grid(m.ff / 32, nt * k);
 #define HY_RGUQ(TQ, VV) hipLaunchKernelGGL((k_route_gate_up<TQ, VV, DEC_PIPE_NP, true, true>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, 4, q8, r8, hq)
 #define HY_RGUQ_V(TQ) if (V <= 1) HY_RGUQ(TQ, 1); else if (V <= 2) HY_RGUQ(TQ, 2); else if (V <= 4) HY_RGUQ(TQ, 4); else if (V <= 8) HY_RGUQ(TQ, 8); else HY_RGUQ(TQ, 16);
@@ -782,7 +791,7 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
     dim3 grid((m.ff + DEC_GU_WAVES * rw - 1) / (DEC_GU_WAVES * rw), nt * k);
     const int V = (ne + 63) / 64;
     const int np = (rw * ng + 7) / 8;   // passes of 8 positions (a gate and an up item each)
-    const int q8 = 8 / ng, r8 = 8 % ng;   // the position cursor's step
+    const int q8 = 8 / rw, r8 = 8 % rw;   // the position cursor's step (span-major positions)
 #define HY_RGU(VV, NN, PP) hipLaunchKernelGGL((k_route_gate_up<TT, VV, NN, false, PP>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, rw, q8, r8, nullptr)
 #define HY_RGU_V(NN, PP) if (V <= 1) HY_RGU(1, NN, PP); else if (V <= 2) HY_RGU(2, NN, PP); else if (V <= 4) HY_RGU(4, NN, PP); else if (V <= 8) HY_RGU(8, NN, PP); else HY_RGU(16, NN, PP);
     HY_DEC_SWITCH(m.tg, {
@@ -803,7 +812,7 @@ int launch_fixed_gate_up(const hy_moe_dev &m, const void *xq, float *h, int nt, 
     auto nblocks = [&](int r) { return (long) ((m.ff + DEC_GU_WAVES * r - 1) / (DEC_GU_WAVES * r)) * nt; };
     while (rw < 8 && nblocks(rw) > DEC_GU_BLOCKS && (rw + 1) * 2 * nb <= DEC_GU_TV) ++rw;
     dim3 grid((m.ff + DEC_GU_WAVES * rw - 1) / (DEC_GU_WAVES * rw), nt);
-    const int np = (rw * ng + 7) / 8, q8 = 8 / ng, r8 = 8 % ng;
+    const int np = (rw * ng + 7) / 8, q8 = 8 / rw, r8 = 8 % rw;
 #define HY_FGU(NN, PP) hipLaunchKernelGGL((k_route_gate_up<TT, 0, NN, false, PP>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, nullptr, 0, 1, 1, (const uint8_t *) xq, nullptr, nullptr, nullptr, h, rw, q8, r8, nullptr)
     HY_DEC_SWITCH(m.tg, {
         if (np <= 1) { HY_FGU(1, false); } else if (np <= 2) { HY_FGU(2, false); } else if (np <= 4) { HY_FGU(4, false); } else { HY_FGU(DEC_PIPE_NP, true); }
@@ -828,7 +837,7 @@ int launch_shared_gate_up(const hy_moe_dev &m, const void *xq, float *h, int nt,
            (long) ntb * DEC_GU_WAVES * (rw + 1) * (2 * nb + 1) <= SH_TV)
         ++rw;
     dim3 grid((m.ff + DEC_GU_WAVES * rw - 1) / (DEC_GU_WAVES * rw), groups);
-    const int np = (rw * ng + 7) / 8, q8 = 8 / ng, r8 = 8 % ng;
+    const int np = (rw * ng + 7) / 8, q8 = 8 / rw, r8 = 8 % rw;
 #define HY_SGU(NN) hipLaunchKernelGGL((k_shared_gate_up<TT, NN>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, (const uint8_t *) xq, h, nt, rw, q8, r8)
     HY_DEC_SWITCH(m.tg, {
         if (np <= 1) HY_SGU(1); else if (np <= 2) HY_SGU(2); else HY_SGU(4);
