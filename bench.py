@@ -22,6 +22,10 @@ bytes each step touches; verify batches also through the grouped GEMM path.
 per launch / its average launch duration, measured on its own stream with HIP events over graph replays of
 that kernel.  `cpu_baseline` is the CPU oracle (this repository's restatement of the reference's CPU expert
 path) run on a bounded sample of the same workload on this host.
+
+`--timeline NAME ...` (a profiling mode, no headline line) replays decode steps of the named workloads on the
+stamps build of the library (`python -m hyper_amd.build --stamps`: hyper_amd/libhymoe_stamps.so, whose decode
+kernels stamp s_memrealtime at their phase boundaries) and prints each step's per-block phase times.
 """
 import argparse
 import json
@@ -35,6 +39,8 @@ import torch
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
+if "--timeline" in sys.argv:   # the stamps build of the library, loaded in place of the default one
+    os.environ.setdefault("HYMOE_LIB", str(ROOT / "hyper_amd" / "libhymoe_stamps.so"))
 
 from hyper_amd import moe  # noqa: E402
 from hyper_amd.formats import GType, WORKLOADS, activations, q8_row_bytes, random_layer, row_bytes, vec_dot_type, zipf_logit_bias  # noqa: E402
@@ -265,6 +271,88 @@ def workloads_bench(args, dev, stream):
     return res
 
 
+def _resident(start, end) -> int:
+    """most intervals [start, end) open at once"""
+    ev = sorted([(a, 1) for a in start] + [(b, -1) for b in end])
+    c = best = 0
+    for _, d in ev:
+        c += d
+        best = max(best, c)
+    return best
+
+
+def _timeline_of(ts: np.ndarray) -> dict:
+    """One step's stamp records (hy_stamps.cuh: router waves at [4 gw], gate/up blocks at [16384 + 8 b], down blocks
+    at [32768 + 8 b], s_memrealtime at 100 MHz) -> microseconds from the router's first wave.  Per-block phases
+    (medians): gate/up route = logits, slot table and Q8 row in, the token routed; wload = the first round of weight
+    bytes landed; dots; fold = block-order fold and store.  Down: slots = ids, weights and slot table in; hquant = the
+    hidden rows loaded and quantized (or copied); wload; dots; fold."""
+    tick = 0.01
+    r = ts[:16384].reshape(-1, 4)
+    r = r[r[:, 2] > 0]
+    g = ts[16384:32768].reshape(-1, 8)
+    g = g[g[:, 7] == 1]
+    d = ts[32768:].reshape(-1, 8)
+    d = d[d[:, 7] == 1]
+    t0 = r[:, 0].min()
+    at = lambda a: float((a - t0) * tick)
+    med = lambda a: float(np.median(a) * tick)
+    return {
+        "router": {"waves": len(r), "end": at(r[:, 1].max())},
+        "gate_up": {"blocks": len(g), "first_start": at(g[:, 0].min()), "end": at(g[:, 4].max()), "resident": _resident(g[:, 0], g[:, 4]),
+                    "route": med(g[:, 1] - g[:, 0]), "wload": med(g[:, 2] - g[:, 1]), "dots": med(g[:, 3] - g[:, 2]),
+                    "fold": med(g[:, 4] - g[:, 3]), "block": med(g[:, 4] - g[:, 0])},
+        "down": {"blocks": len(d), "first_start": at(d[:, 0].min()), "end": at(d[:, 5].max()), "resident": _resident(d[:, 0], d[:, 5]),
+                 "slots": med(d[:, 1] - d[:, 0]), "hquant": med(d[:, 2] - d[:, 1]), "wload": med(d[:, 3] - d[:, 2]),
+                 "dots": med(d[:, 4] - d[:, 3]), "fold": med(d[:, 5] - d[:, 4]), "block": med(d[:, 5] - d[:, 0])},
+    }
+
+
+def decode_timeline(name: str, dev, copies: int = 4, reps: int = 20) -> dict:
+    """Per-block phase times of one decode step of workload `name` (no shared expert: the phases of the three
+    routed launches), replayed as bench.py's decode measurement replays it: 64 steps over `copies` layer copies in
+    one HIP graph; the stamps of the graph's last step, medians over `reps` replays."""
+    import ctypes
+    from hyper_amd import lib
+    L = lib()
+    if not hasattr(L, "hy_stamps_read"):
+        raise RuntimeError(f"{os.environ.get('HYMOE_LIB')} has no stamps: build it with python -m hyper_amd.build --stamps")
+    L.hy_stamps_read.argtypes, L.hy_stamps_read.restype = [ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int
+    L.hy_stamps_clear.argtypes, L.hy_stamps_clear.restype = [], ctypes.c_int
+    w = WORKLOADS[name]
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    layers = [random_layer(w.tg, w.td, w.E, w.ff, w.d, seed=200 + c, device=dev, d_range=w.d_range) for c in range(copies)]
+    runners = [moe.MoeLayerRunner(moe.MoeDev(lay, torch.arange(w.E, dtype=torch.int32, device=dev)),
+                                  torch.randn(w.E, w.d, generator=g, device=dev) * 0.02, w.k, w.rows) for lay in layers]
+    xs = activations(64 * w.rows, w.d, g, dev)
+    fns = [lambda c=i % copies, i=i: runners[c].decode(xs[i * w.rows:(i + 1) * w.rows]) for i in range(64)]
+    torch.cuda.synchronize()   # the weights, slot tables and inputs come from the default stream
+    s = torch.cuda.Stream()
+    buf = np.zeros(1 << 16, dtype=np.uint64)
+    steps = []
+    with torch.cuda.stream(s):
+        for f in fns:
+            f()
+        torch.cuda.synchronize()
+        us_step = graph_time(fns, 1, s) * 1e3 / len(fns)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            for f in fns:
+                f()
+        for _ in range(reps):
+            if L.hy_stamps_clear() != 0:
+                raise RuntimeError("hy_stamps_clear failed")
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            if L.hy_stamps_read(buf.ctypes.data, buf.nbytes) != 0:
+                raise RuntimeError("hy_stamps_read failed")
+            steps.append(_timeline_of(buf.astype(np.int64)))
+    summary = {k: {f: round(float(np.median([st[k][f] for st in steps])), 2) for f in steps[0][k]} for k in steps[0]}
+    return {"workload": name, "rows": w.rows, "us_per_step_graph": round(us_step, 2), "reps": reps, "timeline_us": summary}
+
+
 def cpu_info() -> dict:
     """CPU model, physical cores and hardware threads of this host (from /proc/cpuinfo), and the CPUs this process
     may run on."""
@@ -390,11 +478,18 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-oracle work for cpu_baseline (0: skip)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain copy kernel over MIB MiB (counter calibration under rocprofv3 --pmc)")
+    ap.add_argument("--timeline", nargs="+", metavar="NAME", default=None,
+                    help="print the per-block decode timeline of these workloads from the stamps build of the library, "
+                         "then exit (python -m hyper_amd.build --stamps first)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: hyper_amd runs the expert path on one GPU and has no multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
+    if args.timeline:
+        for name in args.timeline:
+            print(json.dumps(decode_timeline(name, dev)), flush=True)
+        return
     stream = torch.cuda.Stream()
     if args.copy_probe:
         copy_probe(args.copy_probe, dev)

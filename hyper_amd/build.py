@@ -2,7 +2,7 @@
 
     python -m hyper_amd.build            # compile every source, link hyper_amd/libhymoe.so
     python -m hyper_amd.build --stamps   # the same with -DHY_STAMPS: hyper_amd/libhymoe_stamps.so, whose decode
-                                         # kernels record per-block phase times (python -m hyper_amd.stamps)
+                                         # kernels record per-block phase times (python bench.py --timeline NAME ...)
 
 Flags every HIP source is compiled with:
   -ffp-contract=off                           every fp32 product/sum is rounded on its own unless the

@@ -427,7 +427,7 @@ __global__ __launch_bounds__(RR_THREADS, 2) void k_router_rows(const WT *__restr
 // full tiles, a wave per (row, token) logit; the rest quantize x as k_router_pre.  The sums run in the matrix cores'
 // order, not gemv_f32's fmaf chain: the logits agree with it to fp32 rounding, and the routing is defined on the
 // logits it is given.
-constexpr int RT_M = 64, RT_N = 64, RT_KC = 32, RT_LD = RT_KC + 4, RT_NW = 8;
+constexpr int RT_M = 64, RT_N = 64, RT_KC = 64, RT_LD = RT_KC + 4, RT_NW = 8;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <int VT, typename WT, int NW>
 __global__ __launch_bounds__(64 * NW) void k_router_tile(const WT *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
@@ -473,7 +473,9 @@ __global__ __launch_bounds__(64 * NW) void k_router_tile(const WT *__restrict__ 
         if (lane == 0) y[(size_t) t * ys + r] = sum;
         return;
     }
-    const int r0 = (bid % gm) * RT_M, t0 = (bid / gm) * RT_N;
+    // consecutive blocks take consecutive token tiles (blocks go to the 8 XCDs in turn, each with its own L2): an XCD
+    // keeps a few token tiles of x for every row tile, fetching x once, where the other order fetched it once per XCD
+    const int gn = gemm_blocks / gm, r0 = (bid / gn) * RT_M, t0 = (bid % gn) * RT_N;
     const int wm = wave & 1, wn = wave >> 1, li = lane & 15, lq = lane >> 4;   // wave: rows 32 wm .., tokens 16 TJ wn ..
     // global -> LDS: thread tid moves float4 tid % CPR of rows tid / CPR + RS h, h < NL, of the A and B chunks
     const int lr = tid / CPR, lc = 4 * (tid % CPR);
@@ -485,20 +487,20 @@ __global__ __launch_bounds__(64 * NW) void k_router_tile(const WT *__restrict__ 
         gb[h] = x + (size_t) min(t0 + lr + RS * h, nt - 1) * xs + lc;
     }
     const int nst = kdim / RT_KC;
-    // the ring of three chunks on their way, in named slots (arrays of constant index: they stay in registers)
-    float4 sa0[NL], sb0[NL], sa1[NL], sb1[NL], sa2[NL], sb2[NL];
-#define HY_RT_LOAD(c, SA, SB)                                                                      \
+    // the ring of three chunks on their way, in named slots of up to two float4 of A and of B (named variables: they
+    // stay in registers)
+    static_assert(NL == 1 || NL == 2, "one or two float4 of each operand a thread");
+    float4 sa0, sb0, sa1, sb1, sa2, sb2, ta0, tb0, ta1, tb1, ta2, tb2;
+#define HY_RT_LOAD(c, SA, SB, TA, TB)                                                              \
     {                                                                                            \
-        _Pragma("unroll") for (int h = 0; h < NL; ++h) {                                         \
-            SA[h] = ld_w4(ga[h] + RT_KC * (c));                                                  \
-            SB[h] = *(const float4 *) (gb[h] + RT_KC * (c));                                     \
-        }                                                                                        \
+        SA = ld_w4(ga[0] + RT_KC * (c)); SB = *(const float4 *) (gb[0] + RT_KC * (c));           \
+        if constexpr (NL == 2) { TA = ld_w4(ga[NL - 1] + RT_KC * (c)); TB = *(const float4 *) (gb[NL - 1] + RT_KC * (c)); } \
     }
-#define HY_RT_STORE(buf, SA, SB)                                                                   \
+#define HY_RT_STORE(buf, SA, SB, TA, TB)                                                           \
     {                                                                                            \
-        _Pragma("unroll") for (int h = 0; h < NL; ++h) {                                         \
-            *(float4 *) &As[buf][(lr + RS * h) * RT_LD + lc] = SA[h];                            \
-            *(float4 *) &Bs[buf][(lr + RS * h) * RT_LD + lc] = SB[h];                            \
+        *(float4 *) &As[buf][lr * RT_LD + lc] = SA; *(float4 *) &Bs[buf][lr * RT_LD + lc] = SB;  \
+        if constexpr (NL == 2) {                                                                 \
+            *(float4 *) &As[buf][(lr + RS) * RT_LD + lc] = TA; *(float4 *) &Bs[buf][(lr + RS) * RT_LD + lc] = TB; \
         }                                                                                        \
     }
     f32x4 acc[2][TJ];
@@ -525,24 +527,24 @@ __global__ __launch_bounds__(64 * NW) void k_router_tile(const WT *__restrict__ 
     };
     // chunk c sits in slot c % 3; step c computes it from buffer c & 1, stores chunk c + 1 (slot (c + 1) % 3) into the
     // other buffer (last read in step c - 1), then loads chunk c + 4 into that slot
-    if (0 < nst) HY_RT_LOAD(0, sa0, sb0);
-    if (1 < nst) HY_RT_LOAD(1, sa1, sb1);
-    if (2 < nst) HY_RT_LOAD(2, sa2, sb2);
-    HY_RT_STORE(0, sa0, sb0);
-    if (3 < nst) HY_RT_LOAD(3, sa0, sb0);
+    if (0 < nst) HY_RT_LOAD(0, sa0, sb0, ta0, tb0);
+    if (1 < nst) HY_RT_LOAD(1, sa1, sb1, ta1, tb1);
+    if (2 < nst) HY_RT_LOAD(2, sa2, sb2, ta2, tb2);
+    HY_RT_STORE(0, sa0, sb0, ta0, tb0);
+    if (3 < nst) HY_RT_LOAD(3, sa0, sb0, ta0, tb0);
     __syncthreads();
-#define HY_RT_STEP(SA, SB)                                                                         \
+#define HY_RT_STEP(SA, SB, TA, TB)                                                                 \
     {                                                                                            \
         compute(c & 1);                                                                          \
-        if (c + 1 < nst) HY_RT_STORE((c + 1) & 1, SA, SB);                                       \
-        if (c + 4 < nst) HY_RT_LOAD(c + 4, SA, SB);                                              \
+        if (c + 1 < nst) HY_RT_STORE((c + 1) & 1, SA, SB, TA, TB);                               \
+        if (c + 4 < nst) HY_RT_LOAD(c + 4, SA, SB, TA, TB);                                      \
         __syncthreads();                                                                         \
         if (++c >= nst) break;                                                                   \
     }
     for (int c = 0;;) {   // uniform trip count; chunk c + 1 lies in slot (c + 1) % 3
-        HY_RT_STEP(sa1, sb1)
-        HY_RT_STEP(sa2, sb2)
-        HY_RT_STEP(sa0, sb0)
+        HY_RT_STEP(sa1, sb1, ta1, tb1)
+        HY_RT_STEP(sa2, sb2, ta2, tb2)
+        HY_RT_STEP(sa0, sb0, ta0, tb0)
     }
 #undef HY_RT_STEP
 #undef HY_RT_LOAD

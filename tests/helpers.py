@@ -107,4 +107,4 @@ def router_on_matrix_cores(rows: int, kdim: int, nt: int) -> bool:
     """Whether hy_moe_router_q8 computes these logits on the matrix cores (their own sum order) rather than the fmaf
     chain of gemv_f32: more than 8 tokens and enough full 64 x 64 tiles for every CU -- the library's dispatch
     (router_pre_any, hy_route.hip)."""
-    return nt > 8 and kdim % 32 == 0 and (rows // 64) * ((nt + 63) // 64) >= 256
+    return nt > 8 and kdim % 64 == 0 and (rows // 64) * ((nt + 63) // 64) >= 256
