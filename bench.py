@@ -10,7 +10,8 @@ several independent weight copies, so the 256 MB MALL does not serve the weights
 HIP graph (captured once, checked against an eager run first).
 
 Secondary (`decode` object): 1-token decode of the same layer shape in Q4_K/Q4_K, three launches: router GEMV +
-Q8 of x -> routing + gate/up GEMV -> down GEMV + combine, cycling 4 layer copies (1.36 GB) and fresh tokens.
+Q8 of x -> routing + gate/up GEMV -> down GEMV + combine, cycling 4 layer copies (1.36 GB) and fresh tokens.  Its
+per-kernel figures time each launch alone over the same 64 (token, copy) pairs, so they stream cold weights too.
 
 Secondary (`workloads` object): the other configured workloads at their full shapes -- IQ4_NL / IQ4_XS (d_model
 4096, 288 experts) at 1 and 4 rows, IQ2_XS (d_model 7168, 384 experts, top-6) with a shared Q4_K expert at 1 and 8
@@ -175,12 +176,20 @@ def decode_bench(args, dev, stream):
             f()
         torch.cuda.synchronize()
         ms = graph_time(fns, max(1, args.decode_reps), stream) / len(fns)
-        rq = [lambda r=r, i=i: moe.moe_router_q8(r.W_r, E, d, xs[i:i + 1], d, r.logits, E, r.vg, r.xq, 1) for i, r in enumerate(runners)]
-        gu = [lambda r=r: moe.moe_route_gate_up(r.dev, r.logits, E, E, k, r.xq, r.ids, r.wts, None, r.h, 1) for r in runners]
-        dn = [lambda r=r: moe.moe_down_reduce(r.dev, r.h, r.ids, r.wts, k, None, None, r.out, 1) for r in runners]
-        ms_rq = graph_time(rq * 8, max(1, args.decode_reps), stream) / (8 * len(rq))
-        ms_gu = graph_time(gu * 8, max(1, args.decode_reps), stream) / (8 * len(gu))
-        ms_dn = graph_time(dn * 8, max(1, args.decode_reps), stream) / (8 * len(dn))
+        # each launch alone, over the step's 64 (token, layer copy) pairs with buffers of their own: every launch
+        # routes its own token to its own copy's experts, so the weights come from HBM as in the step, not from the
+        # caches a repeated launch would leave them in
+        bufs = [{n: getattr(runners[c], n).clone() for n in ("logits", "xq", "ids", "wts", "h", "out")}
+                for c in [j % len(layers) for j in range(64)]]
+        rq = [lambda r=runners[j % len(layers)], b=b, j=j: moe.moe_router_q8(r.W_r, E, d, xs[j:j + 1], d, b["logits"], E, r.vg, b["xq"], 1)
+              for j, b in enumerate(bufs)]
+        gu = [lambda r=runners[j % len(layers)], b=b: moe.moe_route_gate_up(r.dev, b["logits"], E, E, k, b["xq"], b["ids"], b["wts"], None, b["h"], 1)
+              for j, b in enumerate(bufs)]
+        dn = [lambda r=runners[j % len(layers)], b=b: moe.moe_down_reduce(r.dev, b["h"], b["ids"], b["wts"], k, None, None, b["out"], 1)
+              for j, b in enumerate(bufs)]
+        ms_rq = graph_time(rq, max(1, args.decode_reps), stream) / len(rq)   # (the first replay fills every buffer)
+        ms_gu = graph_time(gu, max(1, args.decode_reps), stream) / len(gu)
+        ms_dn = graph_time(dn, max(1, args.decode_reps), stream) / len(dn)
         # the floor of a chain of three dependent launches: three elementwise kernels a step on the token's 2048
         # floats, each reading what the one before wrote (a launch boundary and a memory round trip each), replayed
         # in a graph like the step

@@ -812,19 +812,30 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
     for (int w = 0; w < C::WAVES; ++w) tot += s_scan[1024 + w];
     const int n4 = (int) (tot & 0xffff), n3 = (int) ((tot >> 16) & 0xffff), n2 = (int) ((tot >> 32) & 0xffff), n1 = (int) (tot >> 48);
     const int total = n4 + n3 + n2 + n1;
-    // Block (x, y) runs on XCD (x + gridDim.x y) % 8, and each XCD has its own L2.  Consecutive item positions are
-    // mostly items of one expert (the same weights), so they go to logical slots l, l + 1, ... placed P = 8 /
-    // gcd(gridDim.x, 8) physical slots apart: the same XCD for every row block, where the second reader of a weight
-    // tile finds it in L2.  (The host makes gridDim.y a multiple of P when it has P slots or more; else P = 1.)
-    const int ys = gridDim.y, P0 = 8 / xcd_gcd8((int) gridDim.x), P = ys % P0 == 0 ? P0 : 1;
-    const int y0 = ((int) blockIdx.y % P) * (ys / P) + (int) blockIdx.y / P;   // this block's logical slot
+    // Block (x, y) runs on XCD (x + gridDim.x y) % 8, and each XCD has its own L2.  This block's logical row block
+    // bx and item slot y0: with gridDim.y a multiple of 8 (the host's choice from 8 slots up), XCD c takes the slots
+    // c ys / 8 .. (c + 1) ys / 8 - 1, each with all its row blocks -- an item's activation rows are fetched into one
+    // L2 and read there by every row block, and runs of consecutive item positions (mostly one expert's items) share
+    // their weight tiles there.  Fewer slots: logical slots l, l + 1, ... sit P = 8 / gcd(gridDim.x, 8) physical
+    // slots apart (P = 1 unless gridDim.y is a multiple of it): the same XCD for every row block, the weights shared.
+    const int ys = gridDim.y;
+    int bx, y0;
+    if (ys % 8 == 0) {
+        const int b = (int) blockIdx.x + (int) gridDim.x * (int) blockIdx.y;
+        bx = (b >> 3) % (int) gridDim.x;
+        y0 = (b & 7) * (ys / 8) + (b >> 3) / (int) gridDim.x;
+    } else {
+        const int P0 = 8 / xcd_gcd8((int) gridDim.x), P = ys % P0 == 0 ? P0 : 1;
+        bx = blockIdx.x;
+        y0 = ((int) blockIdx.y % P) * (ys / P) + (int) blockIdx.y / P;
+    }
     const int rounds = total / ys, rem_items = total - rounds * ys;
     const int my_items = rounds + (((rounds & 1) ? ys - 1 - y0 : y0) < rem_items ? 1 : 0);
     if (my_items == 0) return;   // uniform over the block
     const int in_dim = GU ? m.n : m.ff, nsb = in_dim / 256;
     const size_t mbytes = GU ? m.gate_bytes : m.down_bytes;
     // this wave's 16 rows: tile index (rows / 16) in its matrix, and the output row of each lane
-    const int tile_row = GU ? blockIdx.x * C::HALF + wave % C::HALF : blockIdx.x * C::WAVES + wave;
+    const int tile_row = GU ? bx * C::HALF + wave % C::HALF : bx * C::WAVES + wave;
     const int row = 16 * tile_row + rr;
     const uint8_t *Wmat = (GU ? (wave < C::HALF ? m.gate : m.up) : m.down) + (size_t) tile_row * nsb * C::TB;
     const size_t arow = (size_t) nsb * AQ;
@@ -1013,7 +1024,7 @@ __global__ __launch_bounds__(64 * W, B * W / 4) void k_gemm(hy_moe_dev m, const 
             static_assert(NCOPY * TOKP * LD * 4 <= C::WB + C::AB, "the exchange fits in a stage");
             float *s_o = (float *) stage_w(stage);             // gate (or down) values
             float *s_u = s_o + TOKP * LD;                      // up values
-            const int row0 = blockIdx.x * OR;
+            const int row0 = bx * OR;
             for (int p0 = 0; p0 < ntok; p0 += TOKP) {
                 lds_barrier();   // the stage (or the previous pass) is no longer read
                 {
@@ -1293,11 +1304,14 @@ static int cu_count() {
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     return cus;
 }
-// item slots per row tile: enough blocks for about `per_cu` resident blocks on every CU
-static int item_slots(int row_tiles, int n_pairs, int max_active, int per_cu) {
+// item slots per row tile: enough blocks for about `per_cu` resident blocks on every CU.  k_gemm (`xcd`) groups its
+// slots by XCD when they are a multiple of 8, else places consecutive items P slots apart: from 8 slots up a
+// multiple of 8, else of P where there are that many.
+static int item_slots(int row_tiles, int n_pairs, int max_active, int per_cu, bool xcd = false) {
     const int want = cu_count() * per_cu / row_tiles;   // every block resident at once
     const int n = std::max(1, std::min(max_items(n_pairs, max_active), want));
-    const int P = 8 / xcd_gcd8(row_tiles);       // k_gemm places consecutive items P slots apart: a multiple of P
+    if (xcd && n >= 8) return n / 8 * 8;
+    const int P = 8 / xcd_gcd8(row_tiles);
     return n >= P ? n / P * P : n;
 }
 
@@ -1322,14 +1336,14 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
     // and twice the blocks.  ff is a multiple of 256, so either size tiles it.
     if (m.tg == Q5_K && max_items(n_pairs, max_active) * (m.ff / 128) >= cu_count()) {
         const int rb = m.ff / 128;
-        dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1));
+        dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1, true));
         hipLaunchKernelGGL((k_gemm<Q5_K, true, 16, 1>), grid, dim3(1024), 0, s, m, (const uint8_t *) xq, div_mul_of(k), order, order_n, egrp, nullptr, h);
         return check_launch("hy_moe_gemm_gate_up");
     }
     HY_GEMM_SWITCH(m.tg, {
         constexpr int W = 8, B = g5_blocks<TT, true>();
         const int rb = m.ff / (8 * W);   // 8 W output rows a block
-        dim3 grid(rb, item_slots(rb, n_pairs, max_active, B));
+        dim3 grid(rb, item_slots(rb, n_pairs, max_active, B, B == 1));   // two blocks a CU: every slot counts
         hipLaunchKernelGGL((k_gemm<TT, true, W, B>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) xq, div_mul_of(k), order, order_n, egrp, nullptr, h);
         return check_launch("hy_moe_gemm_gate_up");
     });
@@ -1352,7 +1366,7 @@ int launch_gemm_down(const hy_moe_dev &m, const void *hq, int n_pairs, const int
     HY_GEMM_SWITCH(m.td, {
         constexpr int W = TT == Q6_K ? 16 : 8, B = g5_blocks<TT, false>();   // Q6_K: 16 waves (fits 128 registers)
         const int rb = m.n / (16 * W);   // 16 W output rows a block
-        dim3 grid(rb, item_slots(rb, n_pairs, max_active, B));
+        dim3 grid(rb, item_slots(rb, n_pairs, max_active, B, true));
         hipLaunchKernelGGL((k_gemm<TT, false, W, B>), grid, dim3(64 * W), 0, s, m, (const uint8_t *) hq, div_mul_of(1), order, order_n, egrp, wts, y);
         return check_launch("hy_moe_gemm_down");
     });
