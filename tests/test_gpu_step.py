@@ -54,6 +54,11 @@ def decode_c(m, W_r, x, k, shared=None, out=None, residual=False, bias=None, ws=
     (GType.IQ2_XS, GType.IQ2_XS, 64, 1024, 512, 6, 2, True, True, False),
     (GType.Q5_K, GType.Q6_K, 48, 512, 512, 4, 8, True, False, True),
     (GType.IQ4_XS, GType.IQ4_XS, 32, 512, 256, 4, 12, True, True, False),   # more than 8 rows: batched router
+    # up to the 64-row limit: the batched router on d 2048 and 7168, 256-512 pair columns of route_gate_up, the
+    # down kernel's rows per wave at 32-64 tokens, and the shared expert's fixed-expert launches at 32-64 rows
+    (GType.Q4_K, GType.Q6_K, 128, 2048, 768, 8, 32, False, False, True),
+    (GType.Q4_K, GType.Q6_K, 128, 2048, 768, 8, 64, True, True, False),
+    (GType.IQ2_XS, GType.IQ2_XS, 64, 7168, 512, 6, 64, True, True, False),
 ])
 def test_decode_step_matches_oracle_and_runner(cuda, tg, td, E, d, ff, k, nt, shared, gate, bias):
     seed = 3000 + E + nt
