@@ -77,8 +77,8 @@ template <> struct Item<Q4_K> {
 #pragma unroll
         for (int i = 0; i < 4; ++i) { sa = sdot4(q[i] & 0x0F0F0F0Fu, ya[i], sa); sb = sdot4((q[i] >> 4) & 0x0F0F0F0Fu, yb[i], sb); }
         const int16_t *bs = (const int16_t *) (y + 260);
-        si = sc0 * sa + sc1 * sb;
-        sm = m0 * bs[4 * c + hh] + m1 * bs[4 * c + 2 + hh];
+        si = __mul24(sc0, sa) + __mul24(sc1, sb);   // 24-bit products, exact here: |sa| < 2^16, scales 6-bit
+        sm = __mul24(m0, bs[4 * c + hh]) + __mul24(m1, bs[4 * c + 2 + hh]);
     }
     __device__ __forceinline__ float tval(int si, int sm) const {
         return __builtin_fmaf(h2f(hd.x & 0xffff), (float) si, -(h2f(hd.x >> 16) * (float) sm));
@@ -105,8 +105,8 @@ template <> struct Item<Q5_K> {
             sa = sdot4(lo, ya[i], sa); sb = sdot4(hi, yb[i], sb);
         }
         const int16_t *bs = (const int16_t *) (y + 260);
-        si = sc0 * sa + sc1 * sb;
-        sm = m0 * bs[4 * c + hh] + m1 * bs[4 * c + 2 + hh];
+        si = __mul24(sc0, sa) + __mul24(sc1, sb);   // 24-bit products, exact here: |sa| < 2^16, scales 6-bit
+        sm = __mul24(m0, bs[4 * c + hh]) + __mul24(m1, bs[4 * c + 2 + hh]);
     }
     __device__ __forceinline__ float tval(int si, int sm) const {
         return __builtin_fmaf(h2f(hd.x & 0xffff), (float) si, -(h2f(hd.x >> 16) * (float) sm));
@@ -296,7 +296,7 @@ template <> struct Item<Q3_K> {
         const int16_t *bs = (const int16_t *) (y + 260);
         const int sc0 = (int) (((sl >> (4 * (grp >> 1))) & 15) | (((sh >> (2 * grp)) & 3) << 4)) - 32;
         const int sc1 = (int) (((sl >> (8 + 4 * (grp >> 1))) & 15) | (((sh >> (8 + 2 * grp)) & 3) << 4)) - 32;
-        si = sc0 * (sa - 4 * bs[2 * L]) + sc1 * (sb - 4 * bs[2 * L + 1]);
+        si = __mul24(sc0, sa - 4 * bs[2 * L]) + __mul24(sc1, sb - 4 * bs[2 * L + 1]);   // exact: operands well inside 24 bits
         sm = 0;
     }
     __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }
@@ -327,7 +327,7 @@ template <> struct Item<Q6_K> {
             sa = sdot4(lo, ya[i], sa); sb = sdot4(hi, yb[i], sb);
         }
         const int16_t *bs = (const int16_t *) (y + 260);
-        si = sc_lo * (sa - 32 * bs[g]) + sc_hi * (sb - 32 * bs[g + 4]);
+        si = __mul24(sc_lo, sa - 32 * bs[g]) + __mul24(sc_hi, sb - 32 * bs[g + 4]);   // exact: |sa - 32 bs| < 2^18
         sm = 0;
     }
     __device__ __forceinline__ float tval(int si, int) const { return h2f(d) * (float) si; }

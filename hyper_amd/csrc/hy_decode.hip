@@ -150,6 +150,26 @@ __device__ __forceinline__ float item_t(const Item<T> &it, const uint8_t *y, int
         return 0.0f;
     }
 }
+// item_t without the branch on `valid`: every lane computes (an invalid lane against span 0 of the row, its result
+// unused) and only valid lanes store.  Straight-line code lets the compiler compute an item's weight side (scales,
+// unpacked quants) once for several rows y taken in turn; the arithmetic, and so the bits stored, are item_t's.
+template <int T>
+__device__ __forceinline__ void item_t_all(const Item<T> &it, const uint8_t *y, int gi, int L, bool valid, float *tv_out, int tv_idx) {
+    const int gs = valid ? gi : 0;
+    if constexpr (block_elems(T) == 32) {
+        const uint8_t *yb = y + (size_t) (8 * gs + L) * 32;
+        const uint4 y0 = *(const uint4 *) yb, y1 = *(const uint4 *) (yb + 16);
+        const uint32_t ya[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+        const float v = it.tval(it.dot32(ya), ysum_type(T) ? ysum32(ya) : 0);
+        if (valid) tv_out[tv_idx + L] = v;
+    } else {
+        int si = 0, sm = 0;
+        it.ints(y + (size_t) gs * Q8K_BYTES, L, si, sm);
+        si = group8_isum(si);
+        sm = group8_isum(sm);
+        if (valid && L == 0) tv_out[tv_idx] = it.tval(si, sm);
+    }
+}
 // activation scale of block b of a Q8 row
 template <int VT> __device__ __forceinline__ float q8_scale(const uint8_t *y, int b) {
     if constexpr (VT == Q8_K) return *(const float *) (y + (size_t) b * Q8K_BYTES);
@@ -693,10 +713,10 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_shared_gate_up(hy_moe_dev
             const int rr = wave * rw + r;
 #pragma unroll
             for (int t = 0; t < SH_NT; ++t) {
-                if (t >= ntb) break;   // uniform
+                if (t >= ntb) break;   // uniform (token 0 always runs: its weight-side work serves the others)
                 const uint8_t *yt = s_y + (size_t) t * ybytes;
-                item_t<T>(ig[ps], yt, gi, L, valid, tv, (t * RB + rr) * rs + blk);
-                item_t<T>(iu[ps], yt, gi, L, valid, tv, (t * RB + rr) * rs + nb + blk);
+                item_t_all<T>(ig[ps], yt, gi, L, valid, tv, (t * RB + rr) * rs + blk);
+                item_t_all<T>(iu[ps], yt, gi, L, valid, tv, (t * RB + rr) * rs + nb + blk);
             }
             cc.next(rw, q8, r8);
         }
