@@ -433,7 +433,9 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     HY_STAMP_VARS(6);
     HY_STAMP(0);
     const int t = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 3, L = lane & 7;
-    const int n = m.n, ff = m.ff, ng = ff / 256, nb = ff / BE, items = k * ng;
+    // items: (pair, span) positions; SEP (one expert, the k pairs its tokens): the spans of the row, each item taken
+    // against every token's hidden row in turn
+    const int n = m.n, ff = m.ff, ng = ff / 256, nb = ff / BE, items = SEP ? ng : k * ng;
     uint16_t *hdq = (uint16_t *) (hq + (VT == Q8_K ? 0 : k * nb * 32));
     // the wave's output rows, one after the other (the block's hidden rows serve them all): row w of each of the
     // block's rpw groups of 8 consecutive rows, so that at every step the block's waves read 8 neighbouring rows
@@ -515,10 +517,16 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     auto load_round = [&](int base) {
 #pragma unroll
         for (int ps = 0; ps < NP; ++ps) {
-            const int i = base + g + 8 * ps, j = lc.u, gi = lc.s;
-            const int sl = __shfl(my_slot, j < 64 ? j : 0);
-            if (i < items && row_ok && sl >= 0) it[ps].load(m.down + (size_t) sl * m.down_bytes + tiled_off(row, gi, ng, SPAN_W), L);
-            lc.next(ng, q8, r8);
+            const int i = base + g + 8 * ps;
+            if constexpr (SEP) {   // span i of the row, the expert of pair 0 (every pair's)
+                const int sl = __builtin_amdgcn_readfirstlane(my_slot);
+                if (i < items && row_ok && sl >= 0) it[ps].load(m.down + (size_t) sl * m.down_bytes + tiled_off(row, i, ng, SPAN_W), L);
+            } else {
+                const int j = lc.u, gi = lc.s;
+                const int sl = __shfl(my_slot, j < 64 ? j : 0);
+                if (i < items && row_ok && sl >= 0) it[ps].load(m.down + (size_t) sl * m.down_bytes + tiled_off(row, gi, ng, SPAN_W), L);
+                lc.next(ng, q8, r8);
+            }
         }
     };
     // the first round of weight bytes goes out before the hidden rows are quantized (wave-uniform branches below)
@@ -566,11 +574,18 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
             for (int ps = 0; ps < NP; ++ps) {
                 const int i = base + g + 8 * ps;
                 if (base + 8 * ps >= items) break;   // wave-uniform
-                const int j = cc.u, gi = cc.s;
-                const bool valid = i < items && pair_ok(j);
                 if constexpr (iq2_type(T)) it[ps].grid = grid;
-                item_t<T>(it[ps], hq + (size_t) j * ng * SPAN_L, gi, L, valid, tw, j * (nb | 1) + (block_elems(T) == 32 ? 8 * gi : gi));
-                cc.next(ng, q8, r8);
+                if constexpr (SEP) {   // span i against each token's row: the item's weight side unpacked once
+                    const int blk = block_elems(T) == 32 ? 8 * i : i;
+#pragma unroll 8
+                    for (int j = 0; j < k; ++j)
+                        item_t_all<T>(it[ps], hq + (size_t) j * ng * SPAN_L, i, L, i < items && pair_ok(j), tw, j * (nb | 1) + blk);
+                } else {
+                    const int j = cc.u, gi = cc.s;
+                    const bool valid = i < items && pair_ok(j);
+                    item_t<T>(it[ps], hq + (size_t) j * ng * SPAN_L, gi, L, valid, tw, j * (nb | 1) + (block_elems(T) == 32 ? 8 * gi : gi));
+                    cc.next(ng, q8, r8);
+                }
             }
         }
         wave_lds_sync();
@@ -909,7 +924,7 @@ int launch_shared_down(const hy_moe_dev &m, const float *h, const int *ids, cons
     int rpw = 1;
     while (rpw < 4 && (m.n + DEC_DN_WAVES * rpw - 1) / (DEC_DN_WAVES * rpw) > DEC_DN_BLOCKS) ++rpw;
     dim3 grid((m.n + DEC_DN_WAVES * rpw - 1) / (DEC_DN_WAVES * rpw), 1);
-    const int np = (nt * ng + 7) / 8, q8 = 8 / ng, r8 = 8 % ng;
+    const int np = (ng + 7) / 8, q8 = 8 / ng, r8 = 8 % ng;   // passes of 8 spans (each against every token)
 #define HY_SDN(NN) hipLaunchKernelGGL((k_dec_down<TT, NN, true>), grid, dim3(64 * DEC_DN_WAVES), 0, s, m, h, ids, wts, nt, nullptr, nullptr, out, 0, q8, r8, nullptr, rpw)
     HY_DEC_SWITCH(m.td, {
         if (np <= 2) HY_SDN(2);
