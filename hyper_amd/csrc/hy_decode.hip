@@ -278,8 +278,10 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
         }
     }
     constexpr int NS = 64 * V;   // slot-table entries held (n_expert <= NS)
-    const int sl0 = tid < ne ? bound_slot(m.slot[tid], m.n_local) : -1;
-    const int sl1 = NS > 64 * DEC_GU_WAVES && tid + 64 * DEC_GU_WAVES < ne ? bound_slot(m.slot[tid + 64 * DEC_GU_WAVES], m.n_local) : -1;
+    // the slot table as loaded; bounded where it is stored, so that no compare waits on it before the loads after
+    // it (the logits) have gone out
+    const int sl0 = tid < ne ? m.slot[tid] : -1;
+    const int sl1 = NS > 64 * DEC_GU_WAVES && tid + 64 * DEC_GU_WAVES < ne ? m.slot[tid + 64 * DEC_GU_WAVES] : -1;
     const float xd = tid < nb ? q8_scale<VT>(y, tid) : 0.0f;
     auto stage = [&] {
 #pragma unroll
@@ -287,9 +289,9 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
             const int i = tid + u * 64 * DEC_GU_WAVES;
             if (i < ny) ((uint32_t *) s_y)[i] = yv[u];
         }
-        if (tid < ne) s_slot[tid] = sl0;
+        if (tid < ne) s_slot[tid] = bound_slot(sl0, m.n_local);
         if constexpr (NS > 64 * DEC_GU_WAVES) {
-            if (tid + 64 * DEC_GU_WAVES < ne) s_slot[tid + 64 * DEC_GU_WAVES] = sl1;
+            if (tid + 64 * DEC_GU_WAVES < ne) s_slot[tid + 64 * DEC_GU_WAVES] = bound_slot(sl1, m.n_local);
         }
         if (tid < nb) s_xd[tid] = xd;
         if constexpr (iq2_type(T)) expand_iq2_grid<T>(grid);
@@ -448,8 +450,8 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     const int my_e = lane < k ? ids[t * k + lane] : -1;
     const float my_w = lane < k ? wts[t * k + lane] : 0.0f;
     const int tid = (int) threadIdx.x;
-    const int sl0 = tid < m.n_expert ? bound_slot(m.slot[tid], m.n_local) : -1;
-    const int sl1 = tid + 64 * DEC_DN_WAVES < m.n_expert ? bound_slot(m.slot[tid + 64 * DEC_DN_WAVES], m.n_local) : -1;
+    const int sl0 = tid < m.n_expert ? m.slot[tid] : -1;   // bounded where stored: the loads below go out first
+    const int sl1 = tid + 64 * DEC_DN_WAVES < m.n_expert ? m.slot[tid + 64 * DEC_DN_WAVES] : -1;
     float sh_x = 0.0f, sh_g = 1.0f;   // the shared expert's value and gate of this output, used at the end
     if (shexp && row_ok) {
         sh_x = shexp[(size_t) t * n + row];
@@ -500,8 +502,8 @@ __global__ __launch_bounds__(64 * DEC_DN_WAVES) void k_dec_down(hy_moe_dev m, co
     } else {
         hload(0);
     }
-    s_slot[tid] = sl0;
-    s_slot[tid + 64 * DEC_DN_WAVES] = sl1;
+    s_slot[tid] = bound_slot(sl0, m.n_local);
+    s_slot[tid + 64 * DEC_DN_WAVES] = bound_slot(sl1, m.n_local);
     lds_barrier();
     HY_STAMP(1);
     // lane j < k: pair j's slot (-1: skipped); `okm`: the valid pairs as a wave-uniform bit mask
