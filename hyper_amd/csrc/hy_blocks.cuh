@@ -411,13 +411,14 @@ template <> struct Item<IQ2_XXS> {
 // IQ4_NL (18 B: d, qs[16]) against Q8_0: lane L takes the item's block L (32 values) whole; `y` is that
 // block's Q8_0 data in the padded layout (d at 0, qs at 4).
 template <> struct Item<IQ4_NL> {
-    uint4 qs;
+    Raw16 qr;
     uint16_t d;
     // qs of block L: 2 mod 4 for even L (spans are 16-byte aligned), where the 2 bytes read past them are the next
     // block's d (L < 7)
-    __device__ __forceinline__ void load(const uint8_t *b, int L) { qs = load16_a2_nb(b + 18 * L + 2); d = ld_u16(b + 18 * L); }
+    __device__ __forceinline__ void load(const uint8_t *b, int L) { qr.load(b + 18 * L + 2); d = ld_u16(b + 18 * L); }
     // the block's integer dot against the 32 activation values ya (4 a word)
     __device__ __forceinline__ int dot32(const uint32_t (&ya)[8]) const {
+        const uint4 qs = qr.bytes();
         const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
         int s = 0;
 #pragma unroll

@@ -258,6 +258,22 @@ __device__ __forceinline__ uint4 load16_a2_nb(const uint8_t *p) {
     return make_uint4(__builtin_amdgcn_alignbyte(d1, d0, sb), __builtin_amdgcn_alignbyte(d2, d1, sb),
                       __builtin_amdgcn_alignbyte(d3, d2, sb), __builtin_amdgcn_alignbyte(d4, d3, sb));
 }
+// 16 bytes at an address that need not be dword-aligned, kept as the five dwords that hold them (when aligned, the
+// fifth load repeats the fourth: nothing is read past the bytes) and put together where they are used.  Putting them
+// together at the load (load16_a2_nb) makes the compiler wait for the load right there, so an item's loads land
+// before the next item's go out; kept raw, a load's wait falls at its first use, after the round's other loads.
+struct Raw16 {
+    uint32_t w0, w1, w2, w3, w4, sb;
+    __device__ __forceinline__ void load(const uint8_t *p) {
+        sb = (uint32_t) ((uintptr_t) p & 3);
+        const uint32_t *w = (const uint32_t *) (p - sb);
+        w0 = w[0]; w1 = w[1]; w2 = w[2]; w3 = w[3]; w4 = w[sb ? 4 : 3];
+    }
+    __device__ __forceinline__ uint4 bytes() const {
+        return make_uint4(__builtin_amdgcn_alignbyte(w1, w0, sb), __builtin_amdgcn_alignbyte(w2, w1, sb),
+                          __builtin_amdgcn_alignbyte(w3, w2, sb), __builtin_amdgcn_alignbyte(w4, w3, sb));
+    }
+};
 __device__ __forceinline__ uint4 load16_a4(const uint8_t *p) {   // dword-aligned 16 bytes
     const uint32_t *q = (const uint32_t *) p;
     uint4 v; v.x = q[0]; v.y = q[1]; v.z = q[2]; v.w = q[3];
