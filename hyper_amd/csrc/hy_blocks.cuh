@@ -270,15 +270,13 @@ template <> struct Item<IQ3_S> {
 // (ggml's vec_dot_q3_K_q8_K integers: sumi = sum_g sc_g sum_16 (q - 4 (1 - h)) y).  Blocks are 2-byte aligned
 // (110-byte rows); every 16-byte read ends by byte 97.
 template <> struct Item<Q3_K> {
-    uint4 q0, q1, h0, h1;
+    Raw32 qr, hr;      // the lane's 32 quant bytes and the block's 32 high-bit bytes
     uint32_t sl, sh;   // the two 16-groups' low-nibble bytes and high-bit bytes
     uint16_t d;
     __device__ __forceinline__ void load(const uint8_t *b, int L) {
         const int hf = L >> 2, grp = L >> 1, k = 2 * (L & 1);
-        q0 = load16_a2_nb(b + 32 + 32 * hf);
-        q1 = load16_a2_nb(b + 48 + 32 * hf);
-        h0 = load16_a2_nb(b);
-        h1 = load16_a2_nb(b + 16);
+        qr.load(b + 32 + 32 * hf);
+        hr.load(b);
         sl = ld_u16(b + 96 + 4 * (grp & 1) + k);
         sh = ld_u16(b + 104 + k);
         d = ld_u16(b + 108);
@@ -286,6 +284,7 @@ template <> struct Item<Q3_K> {
     __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
         const int hf = L >> 2, j = L & 3, grp = L >> 1, s2 = 2 * j, hb = 4 * hf + j;
         const uint32_t *ya = (const uint32_t *) (y + 4 + 32 * L);
+        const uint4 q0 = qr.lo(), q1 = qr.hi(), h0 = hr.lo(), h1 = hr.hi();
         const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w}, h[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
         int sa = 0, sb = 0;
 #pragma unroll
@@ -305,19 +304,20 @@ template <> struct Item<Q3_K> {
 // hf = L >> 2, qt0 = (L >> 1) & 1, hl = L & 1: low nibbles are the 16-group g = 8 hf + 2 qt0 + hl, high nibbles
 // group g + 4; bits 2 qt of qh[32 hf + l] are bits 4-5.  (q6 - 32) . y = q6 . y - 32 bsum_g.
 template <> struct Item<Q6_K> {
-    uint4 ql, qh;
+    Raw16 qlr, qhr;
     int sc_lo, sc_hi;
     uint16_t d;
     __device__ __forceinline__ void load(const uint8_t *b, int L) {
         const int hf = L >> 2, qt0 = (L >> 1) & 1, hl = L & 1, g = 8 * hf + 2 * qt0 + hl;
-        ql = load16_a2_nb(b + 64 * hf + 32 * qt0 + 16 * hl);   // (both end well inside the 210-byte block)
-        qh = load16_a2_nb(b + 128 + 32 * hf + 16 * hl);
+        qlr.load(b + 64 * hf + 32 * qt0 + 16 * hl);   // (both end well inside the 210-byte block)
+        qhr.load(b + 128 + 32 * hf + 16 * hl);
         sc_lo = (int8_t) b[192 + g]; sc_hi = (int8_t) b[192 + g + 4];
         d = ld_u16(b + 208);
     }
     __device__ __forceinline__ void ints(const uint8_t *y, int L, int &si, int &sm) const {
         const int hf = L >> 2, qt0 = (L >> 1) & 1, hl = L & 1, g = 8 * hf + 2 * qt0 + hl;
         const uint32_t *ya = (const uint32_t *) (y + 4 + 16 * g), *yb = (const uint32_t *) (y + 4 + 16 * (g + 4));
+        const uint4 ql = qlr.bytes(), qh = qhr.bytes();
         const uint32_t q[4] = {ql.x, ql.y, ql.z, ql.w}, h[4] = {qh.x, qh.y, qh.z, qh.w};
         int sa = 0, sb = 0;
 #pragma unroll
@@ -436,14 +436,14 @@ template <> struct Item<IQ4_NL> {
 // item's block L whole.  Its qs start at 34 L + 2: 2 mod 4 for even L, where the second 16-byte load reads the 2 bytes
 // past the block (the next block's d, L < 7); aligned for odd L.
 template <> struct Item<Q8_0> {
-    uint4 q0, q1;
+    Raw32 qr;
     uint16_t d;
     __device__ __forceinline__ void load(const uint8_t *b, int L) {
-        q0 = load16_a2_nb(b + 34 * L + 2);
-        q1 = load16_a2_nb(b + 34 * L + 18);
+        qr.load(b + 34 * L + 2);
         d = ld_u16(b + 34 * L);
     }
     __device__ __forceinline__ int dot32(const uint32_t (&ya)[8]) const {
+        const uint4 q0 = qr.lo(), q1 = qr.hi();
         const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
         int s = 0;
 #pragma unroll
@@ -463,10 +463,11 @@ template <> struct Item<Q8_0> {
 // (136 bytes), so the misaligned loads end within the block or at most 3 bytes into the next (L < 7; for L = 7 the
 // qs end the span, dword-aligned).
 template <> struct Item<MXFP4> {
-    uint4 qs;
+    Raw16 qr;
     uint32_t e;
-    __device__ __forceinline__ void load(const uint8_t *b, int L) { qs = load16_a2_nb(b + 17 * L + 1); e = b[17 * L]; }
+    __device__ __forceinline__ void load(const uint8_t *b, int L) { qr.load(b + 17 * L + 1); e = b[17 * L]; }
     __device__ __forceinline__ int dot32(const uint32_t (&ya)[8]) const {
+        const uint4 qs = qr.bytes();
         const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
         int s = 0;
 #pragma unroll
@@ -526,15 +527,16 @@ template <> struct Item<Q5_1> {
 // (22 L + 2) are 2 mod 4 for even L, where the 16-byte read takes 2 bytes of block L + 1 (L < 7), and dword-aligned
 // for odd L.
 template <> struct Item<Q5_0> {
-    uint4 qs;
+    Raw16 qr;
     uint32_t qh;
     uint16_t d;
     __device__ __forceinline__ void load(const uint8_t *b, int L) {
-        qs = load16_a2_nb(b + 22 * L + 6);
+        qr.load(b + 22 * L + 6);
         qh = (uint32_t) ld_u16(b + 22 * L + 2) | ((uint32_t) ld_u16(b + 22 * L + 4) << 16);
         d = ld_u16(b + 22 * L);
     }
     __device__ __forceinline__ int dot32(const uint32_t (&ya)[8]) const {
+        const uint4 qs = qr.bytes();
         const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w}, nh = ~qh;
         int s = 0;
 #pragma unroll

@@ -248,20 +248,12 @@ __device__ __forceinline__ uint4 load16_a2(const uint8_t *p) {
     v.x = h0 | (d1 << 16); v.y = (d1 >> 16) | (d2 << 16); v.z = (d2 >> 16) | (d3 << 16); v.w = (d3 >> 16) | (h4 << 16);
     return v;
 }
-// the same without a branch, for lanes whose alignments differ: four dwords from p & ~3 and a fifth when p is not
-// dword-aligned (else the fourth again), joined with v_alignbyte; any byte offset works (MXFP4's 17-byte blocks):
-// it reads up to the end of the dword holding p + 16, i.e. at most p + 19, which the caller keeps in the buffer
-__device__ __forceinline__ uint4 load16_a2_nb(const uint8_t *p) {
-    const uint32_t sb = (uint32_t) ((uintptr_t) p & 3);
-    const uint32_t *w = (const uint32_t *) (p - sb);
-    const uint32_t d0 = w[0], d1 = w[1], d2 = w[2], d3 = w[3], d4 = w[sb ? 4 : 3];
-    return make_uint4(__builtin_amdgcn_alignbyte(d1, d0, sb), __builtin_amdgcn_alignbyte(d2, d1, sb),
-                      __builtin_amdgcn_alignbyte(d3, d2, sb), __builtin_amdgcn_alignbyte(d4, d3, sb));
-}
-// 16 bytes at an address that need not be dword-aligned, kept as the five dwords that hold them (when aligned, the
-// fifth load repeats the fourth: nothing is read past the bytes) and put together where they are used.  Putting them
-// together at the load (load16_a2_nb) makes the compiler wait for the load right there, so an item's loads land
-// before the next item's go out; kept raw, a load's wait falls at its first use, after the round's other loads.
+// 16 bytes at any byte offset (MXFP4's 17-byte blocks), without a branch for lanes whose alignments differ: the four
+// dwords from p & ~3 and a fifth when p is not dword-aligned (else the fourth again), kept as loaded and joined with
+// v_alignbyte where they are used.  The reads end with the dword holding p + 15, at most 3 bytes past the 16, which
+// the callers keep inside the buffer.  Joined at the load, they would make the compiler wait for the load right
+// there, so that one item's loads land before the next item's go out; kept raw, a load's wait falls at its first
+// use, after the round's other loads.
 struct Raw16 {
     uint32_t w0, w1, w2, w3, w4, sb;
     __device__ __forceinline__ void load(const uint8_t *p) {
@@ -272,6 +264,23 @@ struct Raw16 {
     __device__ __forceinline__ uint4 bytes() const {
         return make_uint4(__builtin_amdgcn_alignbyte(w1, w0, sb), __builtin_amdgcn_alignbyte(w2, w1, sb),
                           __builtin_amdgcn_alignbyte(w3, w2, sb), __builtin_amdgcn_alignbyte(w4, w3, sb));
+    }
+};
+// 32 bytes the same way: nine dwords (eight when aligned), joined at use as two 16-byte halves
+struct Raw32 {
+    uint32_t w0, w1, w2, w3, w4, w5, w6, w7, w8, sb;
+    __device__ __forceinline__ void load(const uint8_t *p) {
+        sb = (uint32_t) ((uintptr_t) p & 3);
+        const uint32_t *w = (const uint32_t *) (p - sb);
+        w0 = w[0]; w1 = w[1]; w2 = w[2]; w3 = w[3]; w4 = w[4]; w5 = w[5]; w6 = w[6]; w7 = w[7]; w8 = w[sb ? 8 : 7];
+    }
+    __device__ __forceinline__ uint4 lo() const {
+        return make_uint4(__builtin_amdgcn_alignbyte(w1, w0, sb), __builtin_amdgcn_alignbyte(w2, w1, sb),
+                          __builtin_amdgcn_alignbyte(w3, w2, sb), __builtin_amdgcn_alignbyte(w4, w3, sb));
+    }
+    __device__ __forceinline__ uint4 hi() const {
+        return make_uint4(__builtin_amdgcn_alignbyte(w5, w4, sb), __builtin_amdgcn_alignbyte(w6, w5, sb),
+                          __builtin_amdgcn_alignbyte(w7, w6, sb), __builtin_amdgcn_alignbyte(w8, w7, sb));
     }
 };
 __device__ __forceinline__ uint4 load16_a4(const uint8_t *p) {   // dword-aligned 16 bytes
