@@ -903,7 +903,7 @@ int launch_dec_down(const hy_moe_dev &m, const float *h, const int *ids, const f
     // rows per wave: more than one when one row a wave would take more blocks than the CUs hold at once (about two
     // blocks a CU), so that the blocks run in one round and each block quantizes its hidden rows once for them all
     int rpw = 1;
-    while (rpw < 4 && (long) ((m.n + DEC_DN_WAVES * rpw - 1) / (DEC_DN_WAVES * rpw)) * nt > DEC_DN_BLOCKS) ++rpw;
+    while (rpw < 16 && (long) ((m.n + DEC_DN_WAVES * rpw - 1) / (DEC_DN_WAVES * rpw)) * nt > DEC_DN_BLOCKS) ++rpw;
     dim3 grid((m.n + DEC_DN_WAVES * rpw - 1) / (DEC_DN_WAVES * rpw), nt);
     const int np = (k * ng + 7) / 8;   // passes of 8 items (more than 8: rounds)
     const int q8 = 8 / ng, r8 = 8 % ng;   // the item cursors' step
