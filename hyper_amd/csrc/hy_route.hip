@@ -429,6 +429,44 @@ __global__ __launch_bounds__(RR_THREADS, 2) void k_router_rows(const WT *__restr
 // logits it is given.
 constexpr int RT_M = 64, RT_N = 64, RT_KC = 64, RT_LD = RT_KC + 4, RT_NW = 8;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// The parts of a matrix-core router launch (NW waves a block) beside its logit tiles.  Q8 block qb of x: Q8_K a
+// 256-value block per 16-lane row, Q8_0 a pair of blocks per wave (as k_router_pre).
+template <int VT, int NW>
+__device__ __forceinline__ void router_q8_part(const float *__restrict__ x, int xs, int kdim, int nt, uint8_t *__restrict__ xq, int qb) {
+    const int tid = threadIdx.x, wave = tid >> 6;
+    if constexpr (VT == Q8_K) {
+        const int nb = kdim / 256, u = qb * (64 * NW / 16) + (tid >> 4);
+        if (u >= nt * nb) return;   // uniform over the 16-lane row
+        const int t = u / nb, b = u - t * nb;
+        q8k_block16_load(x + (size_t) t * xs + 256 * b, xq + ((size_t) t * nb + b) * Q8K_BYTES);
+    } else {
+        const int nb = kdim / 32, npair = (nb + 1) / 2, u = qb * NW + wave;
+        if (u >= nt * npair) return;   // wave-uniform
+        const int t = u / npair, b = 2 * (u - t * npair);
+        q8_0_pair_wave(x + (size_t) t * xs + 32 * b, xq + ((size_t) t * nb + b) * Q8_0_BYTES, b + 1 < nb, Q8_0_BYTES, 2);
+    }
+}
+// Rows r_first .. rows - 1 (past the full tiles): a wave per (row, token) logit u, lane L summing values 4 L + 256 i ..
+template <typename WT>
+__device__ __forceinline__ void router_tail_part(const WT *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
+                                                 const float *__restrict__ bias, int bs, float *__restrict__ y, int ys, int nt, int r_first, int u) {
+    const int lane = threadIdx.x & 63, rt = rows - r_first;
+    if (u >= rt * nt) return;   // wave-uniform
+    const int r = r_first + u % rt, t = u / rt;
+    const WT *wr = W + (size_t) r * kdim;
+    const float *xt = x + (size_t) t * xs;
+    float acc = 0.0f;
+    for (int e = 4 * lane; e < kdim; e += 256) {
+        const float4 w = ld_w4(wr + e), v = *(const float4 *) (xt + e);
+        acc = __builtin_fmaf(w.x, v.x, acc); acc = __builtin_fmaf(w.y, v.y, acc);
+        acc = __builtin_fmaf(w.z, v.z, acc); acc = __builtin_fmaf(w.w, v.w, acc);
+    }
+    float sum = wave_sum_xor(acc);
+    if (bias) sum = sum + bias[(size_t) t * bs + r];
+    if (lane == 0) y[(size_t) t * ys + r] = sum;
+}
+
 template <int VT, typename WT, int NW>
 __global__ __launch_bounds__(64 * NW) void k_router_tile(const WT *__restrict__ W, int rows, int kdim, const float *__restrict__ x, int xs,
                                                       const float *__restrict__ bias, int bs, float *__restrict__ y, int ys, int nt,
@@ -442,35 +480,11 @@ __global__ __launch_bounds__(64 * NW) void k_router_tile(const WT *__restrict__ 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int bid = blockIdx.x;
     if (bid >= gemm_blocks + tail_blocks) {   // the Q8 rows of x
-        const int qb = bid - gemm_blocks - tail_blocks;
-        if constexpr (VT == Q8_K) {
-            const int nb = kdim / 256, u = qb * (TH / 16) + (tid >> 4);
-            if (u >= nt * nb) return;   // uniform over the 16-lane row
-            const int t = u / nb, b = u - t * nb;
-            q8k_block16_load(x + (size_t) t * xs + 256 * b, xq + ((size_t) t * nb + b) * Q8K_BYTES);
-        } else {
-            const int nb = kdim / 32, npair = (nb + 1) / 2, u = qb * NW + wave;
-            if (u >= nt * npair) return;   // wave-uniform
-            const int t = u / npair, b = 2 * (u - t * npair);
-            q8_0_pair_wave(x + (size_t) t * xs + 32 * b, xq + ((size_t) t * nb + b) * Q8_0_BYTES, b + 1 < nb, Q8_0_BYTES, 2);
-        }
+        router_q8_part<VT, NW>(x, xs, kdim, nt, xq, bid - gemm_blocks - tail_blocks);
         return;
     }
-    if (bid >= gemm_blocks) {   // rows past the full tiles: a wave per (row, token), lane L sums values 4 L + 256 i ..
-        const int rt = rows - RT_M * gm, u = (bid - gemm_blocks) * NW + wave;
-        if (u >= rt * nt) return;   // wave-uniform
-        const int r = RT_M * gm + u % rt, t = u / rt;
-        const WT *wr = W + (size_t) r * kdim;
-        const float *xt = x + (size_t) t * xs;
-        float acc = 0.0f;
-        for (int e = 4 * lane; e < kdim; e += 256) {
-            const float4 w = ld_w4(wr + e), v = *(const float4 *) (xt + e);
-            acc = __builtin_fmaf(w.x, v.x, acc); acc = __builtin_fmaf(w.y, v.y, acc);
-            acc = __builtin_fmaf(w.z, v.z, acc); acc = __builtin_fmaf(w.w, v.w, acc);
-        }
-        float sum = wave_sum_xor(acc);
-        if (bias) sum = sum + bias[(size_t) t * bs + r];
-        if (lane == 0) y[(size_t) t * ys + r] = sum;
+    if (bid >= gemm_blocks) {   // rows past the full tiles
+        router_tail_part<WT>(W, rows, kdim, x, xs, bias, bs, y, ys, nt, RT_M * gm, (bid - gemm_blocks) * NW + wave);
         return;
     }
     // consecutive blocks take consecutive token tiles (blocks go to the 8 XCDs in turn, each with its own L2): an XCD
