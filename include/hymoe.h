@@ -213,8 +213,11 @@ int hy_moe_down_reduce_residual(const hy_moe_dev *m, const float *h, const int32
 
 /* Router logits and the Q8 rows of x in one launch: logits as hy_gemv_f32 (rows of W_r, stride ls >= rows) and xq as
    hy_q8_quantize(vtype, x, xs, kdim, nt) -- fuses gemv_f32 (src/kernels4.cu:1910-1913) with the activation
-   quantization of the expert kernels.  Up to 8 tokens a wave per (row, token) logit; more, the batched router (16 rows by 16
-   or 8 tokens a block through LDS), still one launch with the quantization. */
+   quantization of the expert kernels.  Up to 8 tokens a wave per (row, token) logit; more, the batched routers, still
+   one launch with the quantization.  The logits are hy_gemv_f32's bits except for large batches whose full 64 x 64
+   logit tiles number at least 256 (kdim a multiple of 64, x 16-byte aligned, xs a multiple of 4: e.g. 2048 tokens x
+   512 experts), which run on the fp32 matrix cores in their own summation order: there the logits agree with
+   hy_gemv_f32 to fp32 rounding (within 2 kdim 2^-24 sum |w x|), and the routing is defined on the logits given. */
 int hy_moe_router_q8(const float *W_r, int rows, int kdim, const float *x, int xs, const float *bias, int bias_stride, float *logits,
                      int ls, int vtype, void *xq, int nt, hipStream_t s);
 /* The same with bf16 router weights, widened on load as in hy_gemv_bf16w (the router16 path of src/engine4.cu:808:
