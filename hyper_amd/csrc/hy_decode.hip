@@ -248,7 +248,8 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
     __shared__ float tv[DEC_GU_WAVES * TVN + 64];
     __shared__ int s_ids[64];
     __shared__ float s_wts[64], s_sg;
-    __shared__ int s_slot[V ? 64 * V : 1];
+    constexpr int VA = V < 0 ? -V : V;   // V < 0: the pairs were routed beforehand (ids given), the slot table as for -V
+    __shared__ int s_slot[VA ? 64 * VA : 1];
     __shared__ uint2 grid[iq2_lds(T)];
     __shared__ float s_xd[DEC_GU_TV / 2];   // activation scales of the token's Q8 row, one per weight block
     __shared__ __align__(16) uint8_t s_y[DEC_Y_BYTES];   // the token's Q8 row (every item reads its 256-value span here)
@@ -277,7 +278,8 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
             }
         }
     }
-    constexpr int NS = 64 * V;   // slot-table entries held (n_expert <= NS)
+    constexpr int NS = 64 * VA;   // slot-table entries held (n_expert <= NS)
+    const int e_given = V < 0 ? ids[(size_t) t * k + j] : 0;   // (loaded with the rest, used after the barrier)
     // the slot table as loaded; bounded where it is stored, so that no compare waits on it before the loads after
     // it (the logits) have gone out
     const int sl0 = tid < ne ? m.slot[tid] : -1;
@@ -303,6 +305,10 @@ __global__ __launch_bounds__(64 * DEC_GU_WAVES) void k_route_gate_up(hy_moe_dev 
         stage();
         lds_barrier();
         e_sel = 0;
+    } else if constexpr (V < 0) {   // routed beforehand (hy_moe_route's bits): pair j's expert from ids
+        stage();
+        lds_barrier();
+        e_sel = e_given;
     } else if constexpr (V <= 2) {
         static_assert(DEC_GU_WAVES == 8, "route_rank8 takes eight waves");
         int er;
@@ -810,6 +816,16 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
         if (nt == 0) return HY_OK;
         const int V = (ne + 63) / 64, q8 = 8 / 4, r8 = 8 % 4;   // the position cursor's step (rw 4)
         dim3 grid(m.ff / 32, nt * k);
+        if ((long) grid.x * grid.y > DEC_GU_BLOCKS && ne <= 1024) {   // more than one round of blocks: route once first
+            int rc = launch_route(logits, ls, ne, k, ids, wts, sg, nt, s);
+            if (rc) return rc;
+#define HY_RGUQI(TQ) hipLaunchKernelGGL((k_route_gate_up<TQ, -16, DEC_PIPE_NP, true, true>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, 4, q8, r8, hq)
+            if (m.tg == IQ4_NL) { HY_RGUQI(IQ4_NL); } else if (m.tg == MXFP4) { HY_RGUQI(MXFP4); } else if (m.tg == Q5_0) { HY_RGUQI(Q5_0); }
+            else if (m.tg == Q5_1) { HY_RGUQI(Q5_1); }
+            else { HY_RGUQI(Q8_0); }
+#undef HY_RGUQI
+            return check_launch("hy_moe_route_gate_up_q8");
+        }
 #define HY_RGUQ(TQ, VV) hipLaunchKernelGGL((k_route_gate_up<TQ, VV, DEC_PIPE_NP, true, true>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, 4, q8, r8, hq)
 #define HY_RGUQ_V(TQ) if (V <= 1) HY_RGUQ(TQ, 1); else if (V <= 2) HY_RGUQ(TQ, 2); else if (V <= 4) HY_RGUQ(TQ, 4); else if (V <= 8) HY_RGUQ(TQ, 8); else HY_RGUQ(TQ, 16);
         if (m.tg == IQ4_NL) { HY_RGUQ_V(IQ4_NL) } else if (m.tg == MXFP4) { HY_RGUQ_V(MXFP4) } else if (m.tg == Q5_0) { HY_RGUQ_V(Q5_0) }
@@ -831,8 +847,17 @@ int launch_route_gate_up(const hy_moe_dev &m, const float *logits, int ls, int n
     const int q8 = 8 / rw, r8 = 8 % rw;   // the position cursor's step (span-major positions)
 #define HY_RGU(VV, NN, PP) hipLaunchKernelGGL((k_route_gate_up<TT, VV, NN, false, PP>), grid, dim3(64 * DEC_GU_WAVES), 0, s, m, logits, ls, ne, k, (const uint8_t *) xq, ids, wts, sg, h, rw, q8, r8, nullptr)
 #define HY_RGU_V(NN, PP) if (V <= 1) HY_RGU(1, NN, PP); else if (V <= 2) HY_RGU(2, NN, PP); else if (V <= 4) HY_RGU(4, NN, PP); else if (V <= 8) HY_RGU(8, NN, PP); else HY_RGU(16, NN, PP);
+    // more than one round of blocks (every block would route its token again, the later blocks after the earlier
+    // ones): route once first (hy_moe_route's kernel, the same bits), the blocks then read their pair's expert
+    const bool pre = (long) grid.x * grid.y > DEC_GU_BLOCKS && ne <= 1024;
+    if (pre) {
+        int rc = launch_route(logits, ls, ne, k, ids, wts, sg, nt, s);
+        if (rc) return rc;
+    }
     HY_DEC_SWITCH(m.tg, {
-        if (np <= 1) { HY_RGU_V(1, false) } else if (np <= 2) { HY_RGU_V(2, false) } else if (np <= 4) { HY_RGU_V(4, false) } else { HY_RGU_V(DEC_PIPE_NP, true) }
+        if (pre) {
+            if (np <= 1) { HY_RGU(-16, 1, false); } else if (np <= 2) { HY_RGU(-16, 2, false); } else if (np <= 4) { HY_RGU(-16, 4, false); } else { HY_RGU(-16, DEC_PIPE_NP, true); }
+        } else if (np <= 1) { HY_RGU_V(1, false) } else if (np <= 2) { HY_RGU_V(2, false) } else if (np <= 4) { HY_RGU_V(4, false) } else { HY_RGU_V(DEC_PIPE_NP, true) }
         return check_launch("hy_moe_route_gate_up");
     });
 #undef HY_RGU_V
