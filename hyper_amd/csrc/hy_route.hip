@@ -420,14 +420,14 @@ __global__ __launch_bounds__(RR_THREADS, 2) void k_router_rows(const WT *__restr
 }
 
 // Router logits of many tokens on the fp32 matrix cores (v_mfma_f32_16x16x4_f32), and the Q8 rows of x, in one
-// launch.  Blocks [0, gemm_blocks) take a 64-row x 64-token tile of the first 64 gm rows: K in chunks of 32, staged
-// through LDS in two buffers (rows padded to 36 floats: the operand reads are conflict-free) with the global loads of
-// the next RT_PD chunks in registers; each wave multiplies a 32 x 32 quarter of the tile (2 x 2 MFMA tiles, each 16-
-// value step {4 q + s} of lane quarter q, component s).  Blocks [gemm_blocks, + tail_blocks) take the rows past the
-// full tiles, a wave per (row, token) logit; the rest quantize x as k_router_pre.  The sums run in the matrix cores'
-// order, not gemv_f32's fmaf chain: the logits agree with it to fp32 rounding, and the routing is defined on the
-// logits it is given.
-constexpr int RT_M = 64, RT_N = 64, RT_KC = 64, RT_LD = RT_KC + 4, RT_NW = 8;
+// launch.  Blocks [0, gemm_blocks) take a 64-row x 64-token tile of the first 64 gm rows: K in chunks of RT_KC, staged
+// through LDS in two buffers (rows padded to RT_LD floats, which spreads the operand reads over the banks) with the
+// global loads of the next three chunks in registers; each wave multiplies a 32-row x 16 TJ-token part of the tile
+// (2 x TJ MFMA tiles, each 16-value step {4 q + s} of lane quarter q, component s).  Blocks [gemm_blocks, +
+// tail_blocks) take the rows past the full tiles, a wave per (row, token) logit; the rest quantize x as k_router_pre.
+// The sums run in the matrix cores' order, not gemv_f32's fmaf chain: the logits agree with it to fp32 rounding, and
+// the routing is defined on the logits it is given.
+constexpr int RT_M = 64, RT_N = 64, RT_KC = 64, RT_LD = RT_KC + 8, RT_NW = 8;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // The parts of a matrix-core router launch (NW waves a block) beside its logit tiles.  Q8 block qb of x: Q8_K a
