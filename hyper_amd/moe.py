@@ -270,12 +270,14 @@ class MoeLayerRunner:
         self.dec_hq = (router == "softmax" and vec_dot_type(L.tg) == GType.Q8_0 and vec_dot_type(L.td) == GType.Q8_0
                        and self.d <= 4096 and self.k * nbh <= 512
                        and self.k * nbh * 34 <= 32768 and self.E <= 1024)
-        self._side = None   # the shared expert's decode stream, made on first use
+        self._side = None   # the shared expert's second stream, made on first use
         # decode's shared expert on a second stream: None = beyond 8 rows (up to 8 rows its gate/up and down read the
         # weights once for several rows and are shortest in order, ahead of the routed kernels: the 8-row IQ2_XS
         # verify with a Q4_K shared expert 332 us in order against 344-347 beside them; one row runs in order as well),
         # True / False = always / never
         self.shared_stream: Optional[bool] = None
+        # prefill's shared expert on a second stream, beside the routing and the routed GEMMs
+        self.prefill_shared_stream = True
         if shared is not None:
             S = shared.layer
             self.sh_ids = torch.zeros(T, **i32)
@@ -286,7 +288,8 @@ class MoeLayerRunner:
             # order_n = (nt, 1) and egrp = (expert 0, start 0, nt) in one buffer, so one strided fill writes both counts
             self.sh_cnt = torch.tensor([0, 1, 0, 0, 0], **i32)
             self.sh_order_n, self.sh_egrp = self.sh_cnt[0:2], self.sh_cnt[2:5]
-            self.sh_xq = torch.empty(T * q8_row_bytes(vec_dot_type(S.tg), self.d), dtype=torch.uint8, device=device)
+            self.sh_xq = (None if vec_dot_type(S.tg) == self.vg
+                          else torch.empty(T * q8_row_bytes(vec_dot_type(S.tg), self.d), dtype=torch.uint8, device=device))
             self.sh_hq = torch.empty(T * q8_row_bytes(vec_dot_type(S.td), S.ff), dtype=torch.uint8, device=device)
 
     def _route_logits(self, nt: int, stream=None):
@@ -304,6 +307,15 @@ class MoeLayerRunner:
         gemv_f32(self.W_r, rows, self.d, x, x.stride(0), self.logits, self.ls, nt, stream,
                  bias=bias, bias_stride=0 if bias is None else bias.stride(0))
         self._route_logits(nt, stream)
+
+    def _fork_side(self, stream):
+        """the shared expert's second stream (default priority), made to wait for `stream`'s work so far"""
+        if self._side is None:
+            self._side = torch.cuda.Stream(device=self.device)
+            self._fork, self._join = torch.cuda.Event(), torch.cuda.Event()
+        self._fork.record(stream if stream is not None else torch.cuda.current_stream())
+        self._side.wait_event(self._fork)
+        return self._side
 
     def _shared_decode(self, x, nt, stream):
         S = self.shared
@@ -325,8 +337,11 @@ class MoeLayerRunner:
         # different nt in between never leaves a stale count behind.
         with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
             self.sh_cnt[0::4].fill_(nt)
-        q8_quantize(vec_dot_type(S.tg), x, x.stride(0), self.d, nt, self.sh_xq, stream)
-        moe_gemm_gate_up(S, self.sh_xq, 1, nt, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_h, stream)
+        xq = self.xq   # the routed gate's Q8 rows of x, where the shared gate takes the same activation type
+        if self.sh_xq is not None:
+            q8_quantize(vec_dot_type(S.tg), x, x.stride(0), self.d, nt, self.sh_xq, stream)
+            xq = self.sh_xq
+        moe_gemm_gate_up(S, xq, 1, nt, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_h, stream)
         q8_quantize(vec_dot_type(S.td), self.sh_h, S.layer.ff, S.layer.ff, nt, self.sh_hq, stream)
         moe_gemm_down(S, self.sh_hq, nt, self.sh_order, self.sh_order_n, self.sh_egrp, 1, self.sh_ones, self.sh_y, stream)
 
@@ -367,15 +382,9 @@ class MoeLayerRunner:
         elif self.shared is not None:
             # the shared expert does not depend on the routing: its two launches run on a second stream (default
             # priority), forked after the Q8 rows of x and joined before the combine
-            main = stream if stream is not None else torch.cuda.current_stream()
-            if self._side is None:
-                self._side = torch.cuda.Stream(device=self.device)
-                self._fork, self._join = torch.cuda.Event(), torch.cuda.Event()
-            self._fork.record(main)
-            self._side.wait_event(self._fork)
-            self._shared_decode(x, nt, self._side)
+            self._shared_decode(x, nt, self._fork_side(stream))
             self._join.record(self._side)
-            shexp, joined = self.sh_y, main
+            shexp, joined = self.sh_y, (stream if stream is not None else torch.cuda.current_stream())
         if self.dec_hq:
             moe_route_gate_up_q8(self.dev, self.logits, self.ls, self.E, self.k, self.xq, self.ids, self.wts, self.sg, self.h, self.hq,
                                  nt, stream)
@@ -409,12 +418,18 @@ class MoeLayerRunner:
         moe_down_reduce(self.dev, self.h, self.ids, self.wts, self.k, shexp, self.sg, self.out, nt, stream)
         return self.out[:nt]
 
-    def prefill(self, x: torch.Tensor, bias=None, stream=None, shared_ready=False, resid: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def prefill(self, x: torch.Tensor, bias=None, stream=None, resid: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Prefill: the grouped GEMM path.  With `resid` ([nt, d] fp32) the combine is added into it in place."""
         nt, k = self._check_rows(x, bias, resid), self.k
         P = nt * k
         moe_router_q8(self.W_r, self.W_r.shape[0], self.d, x, x.stride(0), self.logits, self.ls, self.vg, self.xq, nt, stream,
                       bias=bias, bias_stride=0 if bias is None else bias.stride(0))
+        side = None
+        if self.shared is not None and self.prefill_shared_stream:
+            # the shared expert needs only the Q8 rows of x: its launches run beside the routing and the routed GEMMs
+            side = self._fork_side(stream)
+            self._shared_prefill(x, nt, side)
+            self._join.record(side)
         self._route_logits(nt, stream)
         moe_order(self.dev, self.ids, P, self.E, self.order, self.order_n, stream, self.egrp)
         max_active = min(self.E, P)
@@ -423,7 +438,10 @@ class MoeLayerRunner:
         moe_gemm_down(self.dev, self.hq, P, self.order, self.order_n, self.egrp, max_active, self.wts, self.y, stream)
         shexp = None
         if self.shared is not None:
-            self._shared_prefill(x, nt, stream)
+            if side is None:
+                self._shared_prefill(x, nt, stream)
+            else:
+                (stream if stream is not None else torch.cuda.current_stream()).wait_event(self._join)
             shexp = self.sh_y
         if resid is not None:
             moe_reduce_residual(shexp, self.sg, self.y, k, resid, self.d, nt, self.ids, stream)
