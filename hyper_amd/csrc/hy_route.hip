@@ -422,7 +422,7 @@ __global__ __launch_bounds__(RR_THREADS, 2) void k_router_rows(const WT *__restr
 // Router logits of many tokens on the fp32 matrix cores (v_mfma_f32_16x16x4_f32), and the Q8 rows of x, in one
 // launch.  Blocks [0, gemm_blocks) take a 64-row x 64-token tile of the first 64 gm rows: K in chunks of RT_KC, staged
 // through LDS in two buffers (rows padded to RT_LD floats, which spreads the operand reads over the banks) with the
-// global loads of the next three chunks in registers; each wave multiplies a 32-row x 16 TJ-token part of the tile
+// global loads of the next four chunks in registers; each wave multiplies a 32-row x 16 TJ-token part of the tile
 // (2 x TJ MFMA tiles, each 16-value step {4 q + s} of lane quarter q, component s).  Blocks [gemm_blocks, +
 // tail_blocks) take the rows past the full tiles, a wave per (row, token) logit; the rest quantize x as k_router_pre.
 // The sums run in the matrix cores' order, not gemv_f32's fmaf chain: the logits agree with it to fp32 rounding, and
@@ -501,10 +501,10 @@ __global__ __launch_bounds__(64 * NW) void k_router_tile(const WT *__restrict__ 
         gb[h] = x + (size_t) min(t0 + lr + RS * h, nt - 1) * xs + lc;
     }
     const int nst = kdim / RT_KC;
-    // the ring of three chunks on their way, in named slots of up to two float4 of A and of B (named variables: they
+    // the ring of four chunks on their way, in named slots of up to two float4 of A and of B (named variables: they
     // stay in registers)
     static_assert(NL == 1 || NL == 2, "one or two float4 of each operand a thread");
-    float4 sa0, sb0, sa1, sb1, sa2, sb2, ta0, tb0, ta1, tb1, ta2, tb2;
+    float4 sa0, sb0, ta0, tb0, sa1, sb1, ta1, tb1, sa2, sb2, ta2, tb2, sa3, sb3, ta3, tb3;
 #define HY_RT_LOAD(c, SA, SB, TA, TB)                                                              \
     {                                                                                            \
         SA = ld_w4(ga[0] + RT_KC * (c)); SB = *(const float4 *) (gb[0] + RT_KC * (c));           \
@@ -539,26 +539,28 @@ __global__ __launch_bounds__(64 * NW) void k_router_tile(const WT *__restrict__ 
                     for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][sc], b[j][sc], acc[i][j], 0, 0, 0);
         }
     };
-    // chunk c sits in slot c % 3; step c computes it from buffer c & 1, stores chunk c + 1 (slot (c + 1) % 3) into the
-    // other buffer (last read in step c - 1), then loads chunk c + 4 into that slot
-    if (0 < nst) HY_RT_LOAD(0, sa0, sb0, ta0, tb0);
-    if (1 < nst) HY_RT_LOAD(1, sa1, sb1, ta1, tb1);
-    if (2 < nst) HY_RT_LOAD(2, sa2, sb2, ta2, tb2);
-    HY_RT_STORE(0, sa0, sb0, ta0, tb0);
-    if (3 < nst) HY_RT_LOAD(3, sa0, sb0, ta0, tb0);
-    __syncthreads();
-#define HY_RT_STEP(SA, SB, TA, TB)                                                                 \
+    // chunk c sits in slot c % 4; step c computes it from buffer c & 1, stores chunk c + 1 (slot (c + 1) % 4) into the
+    // other buffer (last read in step c - 1), then loads chunk c + 5 into that slot.  Steps -4 .. -1 only load (chunks
+    // 1 .. 4) and store chunk 0, so every load of the ring is issued by the loop, in one order; the loop runs whole
+    // rounds of four steps and leaves only at its end; and every step issues its loads (past the last chunk, the last
+    // chunk again, never stored).  So the compiler counts 16 loads in flight at every store and waits for the oldest
+    // chunk only: loads under a condition, a loop left from the middle of a round, or the first chunks' loads issued
+    // before the loop (in an order of the compiler's choosing) made it wait for all of them.  (Three chunks ahead:
+    // 53.7 us on the 2048-token, 513-row router; four: 50.9; five and six lose occupancy and take 53-55.)
+    const int last = nst - 1;
+    HY_RT_LOAD(0, sa0, sb0, ta0, tb0);
+#define HY_RT_STEP(C, SA, SB, TA, TB)                                                              \
     {                                                                                            \
-        compute(c & 1);                                                                          \
-        if (c + 1 < nst) HY_RT_STORE((c + 1) & 1, SA, SB, TA, TB);                               \
-        if (c + 4 < nst) HY_RT_LOAD(c + 4, SA, SB, TA, TB);                                      \
+        if ((C) >= 0 && (C) < nst) compute((C) & 1);                                             \
+        if ((C) + 1 >= 0 && (C) + 1 < nst) HY_RT_STORE(((C) + 1) & 1, SA, SB, TA, TB);           \
+        HY_RT_LOAD(min((C) + 5, last), SA, SB, TA, TB);                                          \
         __syncthreads();                                                                         \
-        if (++c >= nst) break;                                                                   \
     }
-    for (int c = 0;;) {   // uniform trip count; chunk c + 1 lies in slot (c + 1) % 3
-        HY_RT_STEP(sa1, sb1, ta1, tb1)
-        HY_RT_STEP(sa2, sb2, ta2, tb2)
-        HY_RT_STEP(sa0, sb0, ta0, tb0)
+    for (int c = -4; c < nst; c += 4) {   // uniform trip count; chunk c + 1 lies in slot (c + 1) % 4
+        HY_RT_STEP(c + 0, sa1, sb1, ta1, tb1)
+        HY_RT_STEP(c + 1, sa2, sb2, ta2, tb2)
+        HY_RT_STEP(c + 2, sa3, sb3, ta3, tb3)
+        HY_RT_STEP(c + 3, sa0, sb0, ta0, tb0)
     }
 #undef HY_RT_STEP
 #undef HY_RT_LOAD
