@@ -284,7 +284,10 @@ __global__ __launch_bounds__(RR_THREADS, 2) void k_router_rows(const WT *__restr
     constexpr int kdim = 256 * NI, ROWF4 = 64 * NI;   // float4 per token row
     __shared__ f4v st[2][RR_TC * ROWF4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int bx = blockIdx.x % gx, by = blockIdx.x / gx;
+    // block b runs on XCD b % 8 (each XCD with its own L2): with whole token ranges on one XCD (the grid a multiple of
+    // 8 blocks), a range's x rows come into one L2 and serve its gx row-group blocks there
+    const int nb = (int) gridDim.x, l = nb % 8 == 0 ? (int) (blockIdx.x % 8) * (nb / 8) + (int) (blockIdx.x / 8) : (int) blockIdx.x;
+    const int bx = l % gx, by = l / gx;
     const int t_beg = by * tpr, t_end = min(nt, t_beg + tpr);
     const int r0 = bx * RR_ROWS * RR_WAVES + RR_ROWS * wave;
     const bool wave_on = r0 < rows;   // wave-uniform: waves past the last row stage, quantize and synchronize only
