@@ -40,6 +40,10 @@ TOL = 2e-3
     (512, 2048, 2048, GType.Q8_K, False, True),   # the 2048-token chunk's shape, no rows past the tiles
     (512, 2048, 2040, GType.Q8_K, True, True),    # a shared-gate row past the tiles, a partial last token tile
     (600, 1024, 2048, GType.Q8_0, False, False),  # 24 rows past the tiles (a wave each), Q8_0 rows of x
+    # K chunks of 64 that are no multiple of the four-chunk ring: 1 and 3 (every round partly past the end), 21
+    (512, 64, 2048, GType.Q8_0, False, True),
+    (512, 192, 2048, GType.Q8_0, True, False),
+    (512, 1344, 2048, GType.Q8_0, False, True),
     (16, 2048, 2048, GType.Q8_K, False, True),    # too few rows for either: the register-row kernel
 ])
 def test_router_q8_bitexact(cuda, E, d, nt, vt, with_sg, with_bias):
