@@ -1,8 +1,8 @@
 /*
  * CPU oracle for the quantized MoE expert-FFN path -- TEST INFRASTRUCTURE ONLY.
  *
- * This library is the checker: only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load it.  The product (hyper_amd/) never
+ * It checks the GPU results and is never what is measured: only tests/,
+ * __graft_entry__.smoke() and the cpu_baseline leg of bench.py may load it.  The product (hyper_amd/) never
  * links or calls it.
  *
  * It restates, in plain C, the semantics of hyper's CPU expert path
