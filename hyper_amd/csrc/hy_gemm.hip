@@ -1332,9 +1332,11 @@ int launch_gemm_gate_up(const hy_moe_dev &m, const void *xq, int k, int n_pairs,
     if (k <= 0 || (uint64_t) n_pairs * (uint64_t) k >= (1ull << 32)) { set_error("hy_moe_gemm_gate_up: k out of range for the pair count"); return HY_EBAD_SHAPE; }
     if (max_items(n_pairs, max_active) >= GM_MAX_ITEMS) { set_error("hy_moe_gemm_gate_up: %d pairs make more than %d work items", n_pairs, GM_MAX_ITEMS - 1); return HY_EBAD_SHAPE; }
     // Q5_K: 16-wave blocks (256 weight rows, so every item's activations are read by half as many row blocks, and
-    // four waves a SIMD) while that grid still has a block for every CU; fewer items (a shared expert's) keep 8 waves
-    // and twice the blocks.  ff is a multiple of 256, so either size tiles it.
-    if (m.tg == Q5_K && max_items(n_pairs, max_active) * (m.ff / 128) >= cu_count()) {
+    // four waves a SIMD) while that grid still has a block for every CU, and for a single expert: a shared expert's
+    // GEMM, which runs beside the routing and the routed GEMMs on a second stream, then takes half the CUs and leaves
+    // the rest to them (the 2048-token Q5_K/Q6_K chunk 690 -> 683 us; alone it takes 46 us against 32 at 8 waves and
+    // twice the blocks).  Other small grids keep 8 waves.  ff is a multiple of 256, so either size tiles it.
+    if (m.tg == Q5_K && (max_items(n_pairs, max_active) * (m.ff / 128) >= cu_count() || max_active == 1)) {
         const int rb = m.ff / 128;
         dim3 grid(rb, item_slots(rb, n_pairs, max_active, 1, true));
         hipLaunchKernelGGL((k_gemm<Q5_K, true, 16, 1>), grid, dim3(1024), 0, s, m, (const uint8_t *) xq, div_mul_of(k), order, order_n, egrp, nullptr, h);
