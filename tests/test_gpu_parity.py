@@ -317,6 +317,9 @@ def test_grouped_gemm_bitexact(cuda, tg, td, d, ff, k, nt):
 @pytest.mark.parametrize("tg,td,E,d,ff,k,nt,sh,sg_logit", [
     (GType.Q4_K, GType.Q6_K, 32, 2048, 768, 8, 40, GType.Q4_K, True),
     (GType.IQ4_XS, GType.IQ4_XS, 24, 4096, 1536, 8, 24, GType.IQ4_XS, False),
+    # a shared gate whose activation type differs from the routed gate's (Q8_K against Q8_0): the shared expert's own
+    # Q8 rows of x, quantized on its stream
+    (GType.IQ4_NL, GType.IQ4_NL, 24, 2048, 512, 4, 40, GType.Q4_K, True),
 ])
 def test_runner_prefill_shared_matches_oracle(cuda, tg, td, E, d, ff, k, nt, sh, sg_logit):
     """Prefill through the runner with an always-on shared expert (and its sigmoid gate): the combine's shared
