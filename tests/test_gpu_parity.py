@@ -320,6 +320,8 @@ def test_grouped_gemm_bitexact(cuda, tg, td, d, ff, k, nt):
     # a shared gate whose activation type differs from the routed gate's (Q8_K against Q8_0): the shared expert's own
     # Q8 rows of x, quantized on its stream
     (GType.IQ4_NL, GType.IQ4_NL, 24, 2048, 512, 4, 40, GType.Q4_K, True),
+    # a Q5_K shared expert: a single expert's gate/up in 16-wave blocks, here one item (the routed one in 8-wave blocks)
+    (GType.Q5_K, GType.Q6_K, 16, 2048, 512, 4, 40, GType.Q5_K, True),
 ])
 def test_runner_prefill_shared_matches_oracle(cuda, tg, td, E, d, ff, k, nt, sh, sg_logit):
     """Prefill through the runner with an always-on shared expert (and its sigmoid gate): the combine's shared
