@@ -44,7 +44,7 @@ if "--timeline" in sys.argv:   # the stamps build of the library, loaded in plac
     os.environ.setdefault("HYMOE_LIB", str(ROOT / "hyper_amd" / "libhymoe_stamps.so"))
 
 from hyper_amd import moe  # noqa: E402
-from hyper_amd.formats import GType, WORKLOADS, activations, q8_row_bytes, random_layer, row_bytes, vec_dot_type, zipf_logit_bias  # noqa: E402
+from hyper_amd.formats import WORKLOADS, activations, q8_row_bytes, random_layer, row_bytes, vec_dot_type, zipf_logit_bias  # noqa: E402
 
 METRIC = "MoE-layer µs/token decode (HBM GB/s) + prefill tokens/s (MFMA util), 1 GPU"
 HBM_PEAK_GBS = 8000.0
